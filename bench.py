@@ -1,0 +1,196 @@
+"""Throughput of libbnneon_hip's hot path on one MI355X; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Workloads (one "step" = one pass of the hot path over one batch of synthetic
+windows already resident in HBM):
+
+  gemm_s8_requant  (default) the int8 pointwise convolution 1152 -> 256 over
+                   24 x 64 pixels per window, int8 NCHW activations with zero
+                   point -128, per-channel Q31 requant, batch 256 windows.
+  pw_s8            libbnneon's PW_S8 op (fp32 rows, per-row dynamic int8,
+                   fp32 dequant + SiLU) at the same shape, batch 256.
+
+The timed region is bracketed by device synchronisation; the dominant
+kernel's average duration comes from HIP events recorded on the stream the
+kernels are launched on. The CPU baseline times the oracle (the scalar C
+restatement of the same computation) on the host cores on a bounded sample.
+"""
+import argparse
+import concurrent.futures
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "birdnet-neon-engine_amd"))
+
+METRIC = "windows/s at batch 256 (int8 net); int8 GEMM TOPS as % of MFMA peak"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--workload", default="gemm_s8_requant",
+                    choices=["gemm_s8_requant", "pw_s8"])
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline leg")
+    return ap.parse_args()
+
+
+def config0_inputs(rng, B, N=256, K=1152, M=1536):
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    x = np.clip(np.round(rng.normal(-40, 35, (B, K, M))), -128, 127).astype(np.int8)
+    bias = rng.integers(-2 ** 14, 2 ** 14 + 1, N).astype(np.int32)
+    mult = rng.integers(2 ** 30, 2 ** 31, N).astype(np.int32)
+    shift = rng.integers(6, 11, N).astype(np.int32)
+    return w, x, bias, mult, shift
+
+
+def time_steps(H, stream, launch, steps, warmup):
+    """(ms per step from events on `stream`, wall seconds of the timed region)."""
+    for _ in range(warmup):
+        launch()
+    H.sync(stream)
+    ev0, ev1 = H.lib().bnh_event_new(), H.lib().bnh_event_new()
+    t0 = time.perf_counter()
+    H.check(H.lib().bnh_event_record(ev0, stream))
+    for _ in range(steps):
+        launch()
+    H.check(H.lib().bnh_event_record(ev1, stream))
+    H.sync(stream)
+    wall = time.perf_counter() - t0
+    ms = H.lib().bnh_event_ms(ev0, ev1)
+    if ms < 0:
+        H.check(None, "bnh_event_ms")
+    H.lib().bnh_event_free(ev0)
+    H.lib().bnh_event_free(ev1)
+    return ms / steps, wall
+
+
+def cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_baseline_gemm_s8_requant(w, bias, mult, shift, rng):
+    """The oracle's requant GEMM, one window per thread, on a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    T = cpu_threads()
+    n_win = 2 * T
+    xs = [np.clip(np.round(rng.normal(-40, 35, (w.shape[1], 1536))), -128, 127).astype(np.int8)
+          for _ in range(T)]
+    t0 = time.perf_counter()
+    with concurrent.futures.ThreadPoolExecutor(T) as ex:
+        list(ex.map(lambda i: O.gemm_s8_requant(w, xs[i % T], bias, mult, shift, -128, -128),
+                    range(n_win)))
+    dt = time.perf_counter() - t0
+    return {"value": n_win / dt, "unit": "windows/s", "cores": T, "kind": "port",
+            "sample": f"{n_win} windows of the 1152->256 x 1536-pixel requant GEMM, "
+                      f"one window per thread ({T} threads), scalar C oracle -O2 "
+                      f"-ffp-contract=off; {dt:.2f} s wall"}
+
+
+def cpu_baseline_pw_s8(pk, rng):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    T = cpu_threads()
+    n_win = 2 * T
+    xs = [rng.standard_normal((1536, 1152)).astype(np.float32) for _ in range(T)]
+    t0 = time.perf_counter()
+    with concurrent.futures.ThreadPoolExecutor(T) as ex:
+        list(ex.map(lambda i: O.pw_s8(xs[i % T], pk, act=1), range(n_win)))
+    dt = time.perf_counter() - t0
+    return {"value": n_win / dt, "unit": "windows/s", "cores": T, "kind": "port",
+            "sample": f"{n_win} windows of PW_S8 1152->256 x 1536 pixels (quantize + GEMM + "
+                      f"dequant + SiLU), one window per thread ({T} threads), scalar C oracle; "
+                      f"{dt:.2f} s wall"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: every box here has one "
+                          "MI355X and the hot path needs no collective (windows are "
+                          "independent); run with --gpus 1"}))
+        sys.exit(2)
+    from bnneon import hip as H
+    if H.lib().bnh_device_count() < 1:
+        raise SystemExit("no HIP device visible")
+    rng = np.random.default_rng(20240601)
+    B = a.batch
+    N, K, M = 256, 1152, 1536
+    stream = H.lib().bnh_stream_new()
+    if a.workload == "gemm_s8_requant":
+        w, x, bias, mult, shift = config0_inputs(rng, B)
+        Wq = H.Q8Weights(w, bias, mult, shift, -128, -128)
+        dx = H.DeviceArray.from_host(x)
+        dout = H.DeviceArray.zeros((B, N, M), np.int8)
+        del x
+
+        def launch():
+            H.check(H.lib().bnh_gemm_s8_requant(Wq.h, dx.ptr, K * M, M, B, dout.ptr, N * M, stream))
+        bytes_per_launch = B * (K * M + N * M) + N * K + 3 * 4 * N
+        workload = ("int8 pointwise conv 1152->256 over 24x64 pixels per window, NCHW int8 "
+                    "activations (zero point -128), per-channel Q31 requant, int8 out")
+        kernel = "k_gemm_s8_requant"
+        dtype = "int8"
+    else:
+        sys.path.insert(0, os.path.join(ROOT, "birdnet-neon-engine_amd"))
+        from bnneon import s8pack
+        wf = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+        pk = s8pack.pack_s8(wf, rng.standard_normal(N).astype(np.float32))
+        _, _, Kp, Np = pk["shape"]
+        Wt = H.S8Weights(N, K, Kp, Np, pk["q"], pk["sw"], pk["cs"], pk["b"])
+        dx = H.DeviceArray.from_host(rng.standard_normal((B, M, K)).astype(np.float32))
+        dq = H.DeviceArray.zeros((B, M * Kp), np.int8)
+        dsa = H.DeviceArray.zeros((B, M), np.float32)
+        dza = H.DeviceArray.zeros((B, M), np.int32)
+        dout = H.DeviceArray.zeros((B, M, Np), np.float32)
+        e = H.epi32(dout, Np, act=1, out_ws=M * Np)
+
+        def launch():
+            H.check(H.lib().bnh_pw_s8(dx.ptr, M * K, K, M, None, 0, dq.ptr, M * Kp, dsa.ptr, dza.ptr,
+                                      M, B, Wt.h, e, stream))
+        # quantize (read fp32 rows, write q) + GEMM (read q, write fp32 out)
+        bytes_per_launch = B * M * (4 * K + 2 * Kp + 4 * Np) + Np * Kp
+        workload = ("libbnneon PW_S8 1152->256 over 24x64 pixels per window: fp32 NHWC rows, "
+                    "per-row dynamic int8, fp32 dequant + SiLU epilogue")
+        kernel = "k_s8n_gemm + k_s8n_quant"
+        dtype = "int8"
+    ms, wall = time_steps(H, stream, launch, a.steps, a.warmup)
+    ops_per_launch = 2.0 * B * M * N * K
+    value = B / (ms * 1e-3)
+    tops = ops_per_launch / (ms * 1e-3) / 1e12
+    gbs = bytes_per_launch / (ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "windows/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded; config distributions)",
+        "config": {"workload": workload, "global_batch": B, "pixels_per_window": M,
+                   "cin": K, "cout": N, "parallelism": "1 GPU, windows batched per launch",
+                   "wall_s_timed_region": round(wall, 4)},
+        "int8_tops": round(tops, 2), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": kernel, "algorithmic_bytes_per_launch": bytes_per_launch},
+    }
+    if not a.no_cpu:
+        if a.workload == "gemm_s8_requant":
+            line["cpu_baseline"] = cpu_baseline_gemm_s8_requant(w, bias, mult, shift, rng)
+        else:
+            line["cpu_baseline"] = cpu_baseline_pw_s8(pk, rng)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,28 @@
+// Internal helpers shared by the libbnneon_hip sources (host side).
+#ifndef BNH_INTERNAL_H
+#define BNH_INTERNAL_H
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "bnneon_hip.h"
+
+// thread-local message of the kernel-level API (bnh_last_error)
+int bnh_fail(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+void bnh_clear_error(void);
+
+#define BNH_HIP(call)                                                                          \
+  do {                                                                                         \
+    hipError_t e_ = (call);                                                                    \
+    if (e_ != hipSuccess) return bnh_fail("%s failed: %s", #call, hipGetErrorString(e_));      \
+  } while (0)
+#define BNH_REQ(cond)                                                                          \
+  do {                                                                                         \
+    if (!(cond)) return bnh_fail("%s: parameter check failed: %s", __func__, #cond);           \
+  } while (0)
+
+static inline hipStream_t bnh_stream(void *s) { return (hipStream_t)s; }
+static inline long long bnh_ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+static inline long long bnh_round_up(long long a, long long b) { return bnh_ceil_div(a, b) * b; }
+#endif

@@ -1,0 +1,142 @@
+// Device-side scalar numerics with the exact semantics of the AArch64 instructions libbnneon's NEON kernels use,
+// so that every output element is bit-identical to the reference's (FPCR default: round to nearest even, denormals
+// kept, FMIN/FMAX propagate NaN, float->int conversions saturate). All HIP sources are compiled with
+// -ffp-contract=off: a*b+c is two roundings unless written as __builtin_fmaf.
+#ifndef BNH_NUM_H
+#define BNH_NUM_H
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define BNH_DEV __device__ __forceinline__
+
+BNH_DEV uint32_t bnh_bits(float x) { return __float_as_uint(x); }
+BNH_DEV float bnh_float(uint32_t u) { return __uint_as_float(u); }
+BNH_DEV bool bnh_isnan(float x) { return x != x; }
+
+// FMAX / FMIN (NEON vmaxq_f32 / vminq_f32): a NaN operand gives a NaN; +0 orders above -0
+BNH_DEV float bnh_fmax(float a, float b) {
+  if (bnh_isnan(a)) return bnh_float(bnh_bits(a) | 0x400000u);
+  if (bnh_isnan(b)) return bnh_float(bnh_bits(b) | 0x400000u);
+  if (a == 0.f && b == 0.f) return bnh_float(bnh_bits(a) & bnh_bits(b));
+  return a > b ? a : b;
+}
+BNH_DEV float bnh_fmin(float a, float b) {
+  if (bnh_isnan(a)) return bnh_float(bnh_bits(a) | 0x400000u);
+  if (bnh_isnan(b)) return bnh_float(bnh_bits(b) | 0x400000u);
+  if (a == 0.f && b == 0.f) return bnh_float(bnh_bits(a) | bnh_bits(b));
+  return a < b ? a : b;
+}
+// FMAXNM / FMINNM (C fmaxf / fminf on AArch64): a NaN operand is ignored
+BNH_DEV float bnh_fmaxnm(float a, float b) {
+  if (bnh_isnan(a)) return b;
+  if (bnh_isnan(b)) return a;
+  return bnh_fmax(a, b);
+}
+BNH_DEV float bnh_fminnm(float a, float b) {
+  if (bnh_isnan(a)) return b;
+  if (bnh_isnan(b)) return a;
+  return bnh_fmin(a, b);
+}
+
+BNH_DEV int32_t bnh_sat_s32(float r) {  // r integral, or NaN / inf
+  if (bnh_isnan(r)) return 0;
+  if (r >= 2147483648.f) return INT32_MAX;
+  if (r < -2147483648.f) return INT32_MIN;
+  return (int32_t)r;
+}
+// FCVTNS (vcvtnq_s32_f32): nearest even, int32-saturating
+BNH_DEV int32_t bnh_cvtn_s32(float x) { return bnh_sat_s32(__builtin_rintf(x)); }
+// FCVTAS (vcvtaq_s32_f32): nearest, ties away from zero, int32-saturating
+BNH_DEV int32_t bnh_cvta_s32(float x) {
+  float t = __builtin_truncf(x);
+  float d = x - t;  // exact
+  if (d >= 0.5f) t += 1.f;
+  else if (d <= -0.5f) t -= 1.f;
+  return bnh_sat_s32(t);
+}
+// (int32_t)lrintf(x) on AArch64: FRINTX, FCVTZS to 64 bits (saturating), low 32 bits kept
+BNH_DEV int32_t bnh_lrintf_s32(float x) {
+  float r = __builtin_rintf(x);
+  if (bnh_isnan(r)) return 0;
+  if (r >= 9223372036854775808.f) return -1;          // INT64_MAX, low word
+  if (r < -9223372036854775808.f) return 0;           // INT64_MIN, low word
+  if (r >= 2147483648.f || r < -2147483648.f) return (int32_t)(uint32_t)(uint64_t)(int64_t)r;
+  return (int32_t)r;
+}
+
+// FRECPE for binary32 (Arm ARM FPRecipEstimate, FZ = 0, round to nearest). The 9-bit estimate
+// r = (floor(2^19 / (2a + 1)) + 1) / 2 is computed as floor(2^19 * rcp(2a + 1)): for 2a + 1 in [513, 1023] the
+// quotient is at least 1/1023 away from an integer on either side and the approximate reciprocal is off by less
+// than 3e-4 absolute, so the floor is exact.
+BNH_DEV int bnh_recip_estimate(int a) {
+  int d = 2 * a + 1;
+  int b = (int)__builtin_floorf(524288.f * __builtin_amdgcn_rcpf((float)d));
+  return (b + 1) >> 1;
+}
+BNH_DEV float bnh_frecpe(float x) {
+  uint32_t u = bnh_bits(x), sign = u & 0x80000000u, ex = (u >> 23) & 0xffu, fr = u & 0x7fffffu;
+  if (ex == 0xffu) return fr ? bnh_float(u | 0x400000u) : bnh_float(sign);
+  if (ex == 0 && fr < 0x200000u) return bnh_float(sign | 0x7f800000u);  // zero, or below 2^-128: overflow
+  int e = (int)ex;
+  uint32_t f23 = fr;
+  if (e == 0) {  // denormal: normalise by one or two places
+    if (!(f23 & 0x400000u)) { e = -1; f23 = (f23 << 2) & 0x7fffffu; }
+    else f23 = (f23 << 1) & 0x7fffffu;
+  }
+  int est = bnh_recip_estimate(256 | (int)(f23 >> 15));
+  int rexp = 253 - e;
+  uint32_t rf = (uint32_t)(est & 0xff) << 15;
+  if (rexp == 0) rf = 0x400000u | (rf >> 1);
+  else if (rexp == -1) { rf = 0x200000u | (rf >> 2); rexp = 0; }
+  return bnh_float(sign | ((uint32_t)(rexp & 0xff) << 23) | rf);
+}
+// FRECPS: 2 - a*b with one rounding; (inf, 0) -> 2
+BNH_DEV float bnh_frecps(float a, float b) {
+  if (bnh_isnan(a)) return bnh_float(bnh_bits(a) | 0x400000u);
+  if (bnh_isnan(b)) return bnh_float(bnh_bits(b) | 0x400000u);
+  bool ia = __builtin_isinf(a), ib = __builtin_isinf(b);
+  if ((ia && b == 0.f) || (a == 0.f && ib)) return 2.f;
+  if (ia || ib) return ((bnh_bits(a) ^ bnh_bits(b)) & 0x80000000u) ? __builtin_inff() : -__builtin_inff();
+  return __builtin_fmaf(-a, b, 2.f);
+}
+
+// The fp32 SiLU of libbnneon's GEMM / depthwise epilogues (src/gemm_f32.h:102-118): exp2 by the magic-number split
+// and a degree-5 polynomial, t clamped to +-60, one FRECPE + FRECPS Newton step.
+BNH_DEV float bnh_silu_f32(float x) {
+  const float magic = 12582912.0f;
+  float t = x * -1.44269504f;
+  t = bnh_fmin(bnh_fmax(t, -60.f), 60.f);
+  float tm = t + magic;
+  float f = t - (tm - magic);
+  uint32_t ni = bnh_bits(tm) << 23;
+  float p = __builtin_fmaf(1.3333558e-3f, f, 9.6181291e-3f);
+  p = __builtin_fmaf(p, f, 5.5504109e-2f);
+  p = __builtin_fmaf(p, f, 2.4022651e-1f);
+  p = __builtin_fmaf(p, f, 6.9314718e-1f);
+  p = __builtin_fmaf(p, f, 1.0f);
+  float d = 1.f + bnh_float(bnh_bits(p) + ni);
+  float r = bnh_frecpe(d);
+  r = r * bnh_frecps(d, r);
+  return x * r;
+}
+// ReLU as vmaxq_f32(y, 0): -0 -> +0, NaN stays NaN
+BNH_DEV float bnh_relu_f32(float y) { return bnh_fmax(y, 0.f); }
+
+// gemmlowp fixed point (the Q31 requant specification of the int8 GEMM / depthwise of this library)
+BNH_DEV int32_t bnh_srdhm(int32_t a, int32_t b) {
+  if (a == INT32_MIN && b == INT32_MIN) return INT32_MAX;
+  int64_t ab = (int64_t)a * (int64_t)b;
+  int64_t nudge = ab >= 0 ? (1LL << 30) : (1 - (1LL << 30));
+  return (int32_t)((ab + nudge) / (1LL << 31));
+}
+BNH_DEV int32_t bnh_rdbypot(int32_t x, int e) {
+  int32_t mask = (int32_t)((1u << e) - 1u);
+  int32_t rem = x & mask;
+  int32_t thr = (mask >> 1) + (x < 0 ? 1 : 0);
+  return (x >> e) + (rem > thr ? 1 : 0);
+}
+BNH_DEV int32_t bnh_requant(int32_t acc, int32_t mult, int shift, int zy, int lo, int hi) {
+  int64_t v = (int64_t)bnh_rdbypot(bnh_srdhm(acc, mult), shift) + zy;
+  return (int32_t)(v < lo ? lo : v > hi ? hi : v);
+}
+#endif

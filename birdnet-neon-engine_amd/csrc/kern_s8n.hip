@@ -1,0 +1,506 @@
+// int8 pointwise-convolution GEMMs on gfx950 int8 MFMA (v_mfma_i32_16x16x64_i8, exact int32 accumulation).
+//
+//  * PW_S8 (libbnneon's int8 GEMM without dotprod, src/gemm_s8n.c + src/rt_ops_s8n.c): fp32 NHWC rows quantized
+//    per row (dynamic, asymmetric into [-127, 127]), per-channel symmetric int8 weights, fp32 dequant epilogue with
+//    SiLU / ReLU / residual / zero-haloed store. Bit-identical to the reference for every input.
+//  * the Q31-requantised static int8 GEMM (NCHW, int8 out): this library's own specification (bnneon_hip.h).
+//
+// Layouts in HBM:
+//  * q rows [M][Kp] per window (K contiguous) are the MFMA A operand as they stand: lane l of a 16x16x64 MFMA
+//    takes 16 bytes of row (l & 15) at k offset 16 (l >> 4) -- the same k chunk rule for A and B, so the int32 sums
+//    are exact whatever order the matrix core adds them in.
+//  * weights are repacked at load from the package's [Np/4][Kp/16][4][16] panels into channel rows [Nt][Kp]
+//    (Nt = Np rounded up to 128, zero rows beyond Np): lane l loads channel (l & 15), the same 16-byte k chunk.
+//  * per-channel epilogue vectors (sw, colsum, b) padded to Nt with zeros.
+// Tiles: a wave computes 32 rows x 64 channels (2 x 4 MFMA tiles, 32 accumulator registers); 4 waves per block.
+#include <string.h>
+
+#include "bnh_internal.h"
+#include "bnh_num.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct bnh_s8w {
+  int N, K, Kp, Np, Nt;
+  int8_t *w;        // [Nt][Kp]
+  float *sw, *b;    // [Nt]
+  int32_t *colsum;  // [Nt]
+};
+
+struct bnh_q8w {
+  int N, K, Nt, zx, zy, lo, hi;
+  int8_t *w;          // [Nt][K]
+  int32_t *bias_eff;  // [Nt]: bias[n] - zx * sum_k w[n][k] (wrapping int32)
+  int32_t *mult, *shift;
+};
+
+struct EpiDev {  // the fp32 epilogue, by value into the kernel
+  int act;
+  float *out;
+  long long out_ws;
+  int ldo, ow, opad;
+  const float *res;
+  long long res_ws;
+  int ldr, rpad, rw;
+};
+
+BNH_DEV long long epi_orow(int m, int ow, int opad) {
+  if (!opad) return m;
+  return (long long)((m / ow) + opad) * (ow + 2 * opad) + (m % ow) + opad;
+}
+
+// ------------------------------------------------------------------ per-row quantization (s8n_quant_rows)
+// One wavefront per row. min / max over k < K & ~3 with FMIN / FMAX semantics (any order: both are exact and, for
+// the values they can return, associative), then the K % 4 tail in order with FMINNM / FMAXNM, as the reference's
+// 4-lane loop + scalar tail. Quantization: FCVTNS for k < K & ~7, (int32_t)lrintf for the K % 8 tail.
+__global__ __launch_bounds__(256) void k_s8n_quant(const float *__restrict__ x, long long x_ws, int ld, int M, int K,
+                                                   int Kp, const float *__restrict__ gate, long long g_ws,
+                                                   int8_t *__restrict__ q, long long q_ws, float *__restrict__ sa,
+                                                   int32_t *__restrict__ za, long long s_ws, long long rows) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int w = (int)(row / M), m = (int)(row % M);
+  const float *r = x + w * x_ws + (long long)m * ld;
+  const float *g = gate ? gate + w * g_ws : nullptr;
+  const int K4 = K & ~3, K8 = K & ~7;
+  float lo = __builtin_inff(), hi = -__builtin_inff();
+  for (int k = lane; k < K4; k += 64) {
+    float v = r[k];
+    if (g) v = v * g[k];
+    lo = bnh_fmin(lo, v);
+    hi = bnh_fmax(hi, v);
+  }
+  for (int off = 32; off; off >>= 1) {
+    lo = bnh_fmin(lo, __shfl_xor(lo, off));
+    hi = bnh_fmax(hi, __shfl_xor(hi, off));
+  }
+  for (int k = K4; k < K; k++) {
+    float v = r[k];
+    if (g) v = v * g[k];
+    lo = bnh_fminnm(lo, v);
+    hi = bnh_fmaxnm(hi, v);
+  }
+  float inv, s;
+  int32_t z;
+  const float range = hi - lo;
+  if (!(range > 1e-30f * bnh_fmaxnm(__builtin_fabsf(hi), __builtin_fabsf(lo))) || !(range > 0.f)) {
+    float a = bnh_fmaxnm(__builtin_fabsf(hi), 1e-30f);
+    inv = 127.f / a;
+    z = 0;
+    s = a / 127.f;
+  } else {
+    inv = 254.f / range;
+    z = (int32_t)((uint32_t)-127 - (uint32_t)bnh_lrintf_s32(lo * inv));
+    s = range / 254.f;
+  }
+  if (lane == 0) {
+    sa[w * s_ws + m] = s;
+    za[w * s_ws + m] = z;
+  }
+  int8_t *o = q + w * q_ws + (long long)m * Kp;
+  const uint32_t zb = (uint32_t)z & 0xffu;
+  for (int k0 = lane * 4; k0 < Kp; k0 += 256) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int k = k0 + j;
+      uint32_t byte;
+      if (k < K) {
+        float v = r[k];
+        if (g) v = v * g[k];
+        const float t = v * inv;
+        int32_t c = (int32_t)((uint32_t)(k < K8 ? bnh_cvtn_s32(t) : bnh_lrintf_s32(t)) + (uint32_t)z);
+        c = c < -127 ? -127 : c > 127 ? 127 : c;
+        byte = (uint32_t)c & 0xffu;
+      } else
+        byte = zb;
+      word |= byte << (8 * j);
+    }
+    *(uint32_t *)(o + k0) = word;
+  }
+}
+
+// ------------------------------------------------------------------ zero halo of a padded output (rt_zero_halo)
+__global__ void k_zero_halo_f32(float *__restrict__ out, long long ws, int H, int W, int C, int h, long long total) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int Wp = W + 2 * h;
+  const long long per = (long long)(H + 2 * h) * Wp * C;
+  const int w = (int)(i / per);
+  const long long e = i % per;
+  const long long px = e / C;
+  const int y = (int)(px / Wp), xx = (int)(px % Wp);
+  if (y >= h && y < H + h && xx >= h && xx < W + h) return;
+  out[w * ws + e] = 0.f;
+}
+
+// ------------------------------------------------------------------ int8 GEMM + fp32 dequant epilogue
+template <int WM, int WN>
+__global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, long long q_ws,
+                                                  const float *__restrict__ sa, const int32_t *__restrict__ za,
+                                                  long long s_ws, int M, long long rows,
+                                                  const int8_t *__restrict__ wt, const float *__restrict__ sw,
+                                                  const int32_t *__restrict__ cs, const float *__restrict__ bias,
+                                                  int Kp, int Np, EpiDev e) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const long long row0 = (long long)blockIdx.x * (WM * 32) + wm * 32;
+  const int n0 = blockIdx.y * (WN * 64) + wn * 64;
+  if (row0 >= rows) return;
+  const int kc = (lane >> 4) * 16;  // this lane's k chunk within a 64-wide step
+  const int8_t *ap[2];
+#pragma unroll
+  for (int t = 0; t < 2; t++) {
+    long long r = row0 + 16 * t + (lane & 15);
+    if (r >= rows) r = rows - 1;  // a valid row; its sums are discarded
+    const int w = (int)(r / M), m = (int)(r % M);
+    ap[t] = q + w * q_ws + (long long)m * Kp + kc;
+  }
+  const int8_t *bp = wt + (long long)(n0 + (lane & 15)) * Kp + kc;
+  v4i acc[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[t][j] = (v4i){0, 0, 0, 0};
+  const int kmain = Kp & ~63;
+  for (int k = 0; k < kmain; k += 64) {
+    v4i a[2], b[4];
+#pragma unroll
+    for (int t = 0; t < 2; t++) a[t] = *(const v4i *)(ap[t] + k);
+#pragma unroll
+    for (int j = 0; j < 4; j++) b[j] = *(const v4i *)(bp + (long long)16 * j * Kp + k);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[j], acc[t][j], 0, 0, 0);
+  }
+  if (kmain < Kp) {  // the last partial step: chunks at or past Kp contribute zeros
+    const bool in = kmain + kc < Kp;
+    v4i a[2], b[4];
+#pragma unroll
+    for (int t = 0; t < 2; t++) a[t] = in ? *(const v4i *)(ap[t] + kmain) : (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; j++) b[j] = in ? *(const v4i *)(bp + (long long)16 * j * Kp + kmain) : (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[j], acc[t][j], 0, 0, 0);
+  }
+  // epilogue (deq4 + activation + store_rows, src/gemm_s8n.c:105-135): acc[t][j][r] is row 16t + 4 (lane >> 4) + r,
+  // channel 16j + (lane & 15) of the wave's tile
+  float swn[4], bn[4];
+  int32_t csn[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int n = n0 + 16 * j + (lane & 15);
+    swn[j] = sw[n];
+    bn[j] = bias[n];
+    csn[j] = cs[n];
+  }
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const long long row = row0 + 16 * t + 4 * (lane >> 4) + r;
+      if (row >= rows) continue;
+      const int w = (int)(row / M), m = (int)(row % M);
+      const float s_a = sa[w * s_ws + m];
+      const uint32_t z = (uint32_t)za[w * s_ws + m];
+      float *orow = e.out + w * e.out_ws + epi_orow(m, e.ow, e.opad) * e.ldo;
+      const float *rrow = e.res ? e.res + w * e.res_ws + epi_orow(m, e.rw, e.rpad) * e.ldr : nullptr;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int n = n0 + 16 * j + (lane & 15);
+        if (n >= Np) continue;
+        const int32_t c = (int32_t)((uint32_t)acc[t][j][r] - (uint32_t)csn[j] * z);
+        const float f = (float)c;
+        const float scl = swn[j] * s_a;
+        float y = f * scl;
+        y = y + bn[j];
+        if (e.act == 1) y = bnh_silu_f32(y);
+        else if (e.act == 2) y = bnh_relu_f32(y);
+        if (rrow) y = y + rrow[n];
+        orow[n] = y;
+      }
+    }
+}
+
+// ------------------------------------------------------------------ int8 GEMM, Q31 requant, NCHW
+// A operand = x^T (pixels x K): x [K][M] has pixels contiguous, so each block stages a 64 k x 64 pixel tile through
+// LDS transposed to [pixel][k] (4 x 4 byte blocks transposed in registers with v_perm), from where lane l reads its
+// 16 k bytes of pixel (l & 15). B operand = w [Nt][K] rows straight from global (L2-resident).
+// Accumulator lane layout: 4 consecutive pixels x 1 channel -> one 32-bit store of 4 output bytes.
+BNH_DEV void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, uint32_t c[4]) {
+  // r_i = bytes of k row i for pixels 0..3; c_j = bytes of pixel j for k rows 0..3
+  const uint32_t a_lo = __builtin_amdgcn_perm(r1, r0, 0x05010400u), a_hi = __builtin_amdgcn_perm(r1, r0, 0x07030602u);
+  const uint32_t b_lo = __builtin_amdgcn_perm(r3, r2, 0x05010400u), b_hi = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+  c[0] = __builtin_amdgcn_perm(b_lo, a_lo, 0x05040100u);
+  c[1] = __builtin_amdgcn_perm(b_lo, a_lo, 0x07060302u);
+  c[2] = __builtin_amdgcn_perm(b_hi, a_hi, 0x05040100u);
+  c[3] = __builtin_amdgcn_perm(b_hi, a_hi, 0x07060302u);
+}
+
+#define RQ_LDS_STRIDE 80  // bytes per staged pixel row: 64 k + 16 pad
+__global__ __launch_bounds__(256) void k_gemm_s8_requant(const int8_t *__restrict__ x, long long x_ws, int M, int K,
+                                                         int tiles_per_window, const int8_t *__restrict__ wt,
+                                                         const int32_t *__restrict__ bias_eff,
+                                                         const int32_t *__restrict__ mult,
+                                                         const int32_t *__restrict__ shift, int N, int zy, int lo,
+                                                         int hi, int8_t *__restrict__ out, long long out_ws) {
+  __shared__ __attribute__((aligned(16))) int8_t xs[64 * RQ_LDS_STRIDE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves: 64 pixels x 128 channels
+  const int win = blockIdx.x / tiles_per_window;
+  const int p0 = (blockIdx.x % tiles_per_window) * 64;
+  const int n0 = blockIdx.y * 128 + wn * 64;
+  const int8_t *xw = x + win * x_ws;
+  // staging: thread -> pixel quad pq (16 of them), k quad kq (16 of them)
+  const int pq = tid & 15, kq = tid >> 4;
+  const int px = p0 + 4 * pq;
+  const bool pin = px < M;  // M % 4 == 0: a quad is all in or all out
+  const int kc = (lane >> 4) * 16;
+  const int8_t *bp = wt + (long long)(n0 + (lane & 15)) * K + kc;
+  v4i acc[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; t++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[t][j] = (v4i){0, 0, 0, 0};
+  uint32_t rg[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int k = 4 * kq + i;
+    rg[i] = (pin && k < K) ? *(const uint32_t *)(xw + (long long)k * M + px) : 0u;
+  }
+  for (int k0 = 0; k0 < K; k0 += 64) {
+    uint32_t c[4];
+    transpose4x4(rg[0], rg[1], rg[2], rg[3], c);
+    __syncthreads();  // the previous step's fragments are read
+#pragma unroll
+    for (int j = 0; j < 4; j++) *(uint32_t *)(xs + (4 * pq + j) * RQ_LDS_STRIDE + 4 * kq) = c[j];
+    __syncthreads();
+    if (k0 + 64 < K) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int k = k0 + 64 + 4 * kq + i;
+        rg[i] = (pin && k < K) ? *(const uint32_t *)(xw + (long long)k * M + px) : 0u;
+      }
+    }
+    const bool kin = k0 + kc < K;
+    v4i a[2], b[4];
+#pragma unroll
+    for (int t = 0; t < 2; t++) a[t] = *(const v4i *)(xs + (wm * 32 + 16 * t + (lane & 15)) * RQ_LDS_STRIDE + kc);
+#pragma unroll
+    for (int j = 0; j < 4; j++) b[j] = kin ? *(const v4i *)(bp + (long long)16 * j * K + k0) : (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[j], acc[t][j], 0, 0, 0);
+  }
+  int8_t *ow = out + win * out_ws;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int n = n0 + 16 * j + (lane & 15);
+    if (n >= N) continue;
+    const int32_t be = bias_eff[n], mu = mult[n], sh = shift[n];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int p = p0 + wm * 32 + 16 * t + 4 * (lane >> 4);
+      if (p >= M) continue;
+      uint32_t word = 0;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int32_t a32 = (int32_t)((uint32_t)acc[t][j][r] + (uint32_t)be);
+        word |= ((uint32_t)bnh_requant(a32, mu, sh, zy, lo, hi) & 0xffu) << (8 * r);
+      }
+      *(uint32_t *)(ow + (long long)n * M + p) = word;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ numerics probe
+__global__ void k_eval_f32(int f, const float *__restrict__ x, float *__restrict__ y, long long n) {
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = x[i];
+  y[i] = f == 0 ? bnh_frecpe(v) : f == 1 ? bnh_silu_f32(v) : bnh_relu_f32(v);
+}
+
+// ================================================================== host side
+extern "C" {
+
+int bnh_eval_f32(int f, const float *x, float *y, long long n, void *stream) {
+  BNH_REQ(f >= 0 && f <= 2 && n >= 0 && x && y);
+  if (!n) return 0;
+  hipLaunchKernelGGL(k_eval_f32, dim3((unsigned)bnh_ceil_div(n, 256)), dim3(256), 0, bnh_stream(stream), f, x, y, n);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+bnh_s8w *bnh_s8w_new(int N, int K, int Kp, int Np, const int8_t *w, const float *sw, const int32_t *colsum,
+                     const float *b) {
+  if (N <= 0 || K <= 0 || Np != ((N + 7) & ~7) || Kp != ((K + 15) & ~15) || !w || !sw || !colsum || !b) {
+    bnh_fail("bnh_s8w_new: int8 GEMM shape N %d K %d Kp %d Np %d: expected Np = N rounded up to 8, Kp = K rounded "
+             "up to 16, and all four tensors", N, K, Kp, Np);
+    return nullptr;
+  }
+  const int Nt = (int)bnh_round_up(Np, 128);
+  int8_t *hw = (int8_t *)calloc((size_t)Nt * Kp, 1);
+  float *hsw = (float *)calloc(Nt, 4), *hb = (float *)calloc(Nt, 4);
+  int32_t *hcs = (int32_t *)calloc(Nt, 4);
+  bnh_s8w *W = (bnh_s8w *)calloc(1, sizeof *W);
+  if (!hw || !hsw || !hb || !hcs || !W) {
+    free(hw); free(hsw); free(hb); free(hcs); free(W);
+    bnh_fail("bnh_s8w_new: out of host memory");
+    return nullptr;
+  }
+  const int kb = Kp / 16;
+  for (int n = 0; n < Np; n++)
+    for (int k = 0; k < Kp; k++)
+      hw[(size_t)n * Kp + k] = w[((size_t)(n / 4) * kb + k / 16) * 64 + (n % 4) * 16 + k % 16];
+  memcpy(hsw, sw, sizeof(float) * Np);
+  memcpy(hb, b, sizeof(float) * Np);
+  memcpy(hcs, colsum, sizeof(int32_t) * Np);
+  W->N = N; W->K = K; W->Kp = Kp; W->Np = Np; W->Nt = Nt;
+  bool ok = (W->w = (int8_t *)bnh_malloc((size_t)Nt * Kp)) && (W->sw = (float *)bnh_malloc(4 * (size_t)Nt)) &&
+            (W->b = (float *)bnh_malloc(4 * (size_t)Nt)) && (W->colsum = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
+            !bnh_memcpy_h2d(W->w, hw, (size_t)Nt * Kp) && !bnh_memcpy_h2d(W->sw, hsw, 4 * (size_t)Nt) &&
+            !bnh_memcpy_h2d(W->b, hb, 4 * (size_t)Nt) && !bnh_memcpy_h2d(W->colsum, hcs, 4 * (size_t)Nt);
+  free(hw); free(hsw); free(hb); free(hcs);
+  if (!ok) { bnh_s8w_free(W); return nullptr; }
+  return W;
+}
+
+void bnh_s8w_free(bnh_s8w *W) {
+  if (!W) return;
+  if (W->w) hipFree(W->w);
+  if (W->sw) hipFree(W->sw);
+  if (W->b) hipFree(W->b);
+  if (W->colsum) hipFree(W->colsum);
+  free(W);
+}
+
+int bnh_s8n_quant_rows(const float *x, long long x_ws, int ld, int M, int K, int Kp, const float *gate,
+                       long long gate_ws, int8_t *q, long long q_ws, float *sa, int32_t *za, long long s_ws, int B,
+                       void *stream) {
+  BNH_REQ(x && q && sa && za && M > 0 && K > 0 && B > 0);
+  BNH_REQ(Kp == ((K + 15) & ~15) && ld >= K);
+  BNH_REQ(!gate || (K % 4 == 0 && K <= 4096));
+  BNH_REQ(((uintptr_t)q & 3) == 0 && q_ws % 4 == 0 && (B == 1 || q_ws >= (long long)M * Kp));
+  BNH_REQ(B == 1 || (x_ws >= (long long)(M - 1) * ld + K && s_ws >= M));
+  const long long rows = (long long)M * B;
+  hipLaunchKernelGGL(k_s8n_quant, dim3((unsigned)bnh_ceil_div(rows, 4)), dim3(256), 0, bnh_stream(stream), x, x_ws, ld,
+                     M, K, Kp, gate, gate_ws, q, q_ws, sa, za, s_ws, rows);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+static int check_epi(const bnh_epi32 *e, int M, int Np, int B) {
+  BNH_REQ(e && e->out && e->act >= 0 && e->act <= 2 && e->ldo >= Np);
+  BNH_REQ(e->opad >= 0 && e->opad <= 3 && (!e->opad || (e->ow > 0 && M % e->ow == 0)));
+  BNH_REQ(!e->res || (e->ldr >= Np && e->rpad >= 0 && (!e->rpad || (e->rw > 0 && M % e->rw == 0))));
+  (void)B;
+  return 0;
+}
+
+int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, const int32_t *za, long long s_ws, int M, int B,
+                 const bnh_s8w *W, const bnh_epi32 *e, void *stream) {
+  BNH_REQ(q && sa && za && W && M > 0 && B > 0);
+  BNH_REQ(((uintptr_t)q & 15) == 0 && q_ws % 16 == 0);
+  if (check_epi(e, M, W->Np, B)) return -1;
+  const long long rows = (long long)M * B;
+  EpiDev d = {e->act, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->res, e->res_ws, e->ldr, e->rpad, e->rw};
+  hipStream_t s = bnh_stream(stream);
+  if (W->Np > 64) {
+    dim3 grid((unsigned)bnh_ceil_div(rows, 64), (unsigned)bnh_ceil_div(W->Np, 128));
+    hipLaunchKernelGGL((k_s8n_gemm<2, 2>), grid, dim3(256), 0, s, q, q_ws, sa, za, s_ws, M, rows, W->w, W->sw,
+                       W->colsum, W->b, W->Kp, W->Np, d);
+  } else {
+    dim3 grid((unsigned)bnh_ceil_div(rows, 128), 1);
+    hipLaunchKernelGGL((k_s8n_gemm<4, 1>), grid, dim3(256), 0, s, q, q_ws, sa, za, s_ws, M, rows, W->w, W->sw,
+                       W->colsum, W->b, W->Kp, W->Np, d);
+  }
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_pw_s8(const float *in, long long in_ws, int lda, int M, const float *gate, long long gate_ws, int8_t *q,
+              long long q_ws, float *sa, int32_t *za, long long s_ws, int B, const bnh_s8w *W, const bnh_epi32 *e,
+              void *stream) {
+  BNH_REQ(W && e && e->out);
+  if (check_epi(e, M, W->Np, B)) return -1;
+  if (e->opad) {
+    const int H = M / e->ow, Wd = e->ow, h = e->opad;
+    const long long per = (long long)(H + 2 * h) * (Wd + 2 * h) * e->ldo, total = per * B;
+    BNH_REQ(B == 1 || e->out_ws >= per);
+    hipLaunchKernelGGL(k_zero_halo_f32, dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, bnh_stream(stream),
+                       e->out, B == 1 ? per : e->out_ws, H, Wd, e->ldo, h, total);
+    BNH_HIP(hipGetLastError());
+  }
+  if (bnh_s8n_quant_rows(in, in_ws, lda, M, W->K, W->Kp, gate, gate_ws, q, q_ws, sa, za, s_ws, B, stream)) return -1;
+  return bnh_s8n_gemm(q, q_ws, sa, za, s_ws, M, B, W, e, stream);
+}
+
+bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const int32_t *mult, const int32_t *shift,
+                     int zx, int zy, int lo, int hi) {
+  if (N <= 0 || K <= 0 || !w || !bias || !mult || !shift || lo > hi || lo < -128 || hi > 127) {
+    bnh_fail("bnh_q8w_new: N %d K %d lo %d hi %d: expected N, K > 0, all four arrays and -128 <= lo <= hi <= 127", N, K,
+             lo, hi);
+    return nullptr;
+  }
+  for (int n = 0; n < N; n++)
+    if (shift[n] < 0 || shift[n] > 31) {
+      bnh_fail("bnh_q8w_new: shift[%d] = %d: expected a right shift in [0, 31]", n, shift[n]);
+      return nullptr;
+    }
+  const int Nt = (int)bnh_round_up(N, 128);
+  int8_t *hw = (int8_t *)calloc((size_t)Nt * K, 1);
+  int32_t *hb = (int32_t *)calloc(Nt, 4), *hm = (int32_t *)calloc(Nt, 4), *hs = (int32_t *)calloc(Nt, 4);
+  bnh_q8w *W = (bnh_q8w *)calloc(1, sizeof *W);
+  if (!hw || !hb || !hm || !hs || !W) {
+    free(hw); free(hb); free(hm); free(hs); free(W);
+    bnh_fail("bnh_q8w_new: out of host memory");
+    return nullptr;
+  }
+  memcpy(hw, w, (size_t)N * K);
+  for (int n = 0; n < N; n++) {
+    uint32_t cs = 0;
+    for (int k = 0; k < K; k++) cs += (uint32_t)(int32_t)w[(size_t)n * K + k];
+    hb[n] = (int32_t)((uint32_t)bias[n] - (uint32_t)zx * cs);
+    hm[n] = mult[n];
+    hs[n] = shift[n];
+  }
+  W->N = N; W->K = K; W->Nt = Nt; W->zx = zx; W->zy = zy; W->lo = lo; W->hi = hi;
+  bool ok = (W->w = (int8_t *)bnh_malloc((size_t)Nt * K)) && (W->bias_eff = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
+            (W->mult = (int32_t *)bnh_malloc(4 * (size_t)Nt)) && (W->shift = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
+            !bnh_memcpy_h2d(W->w, hw, (size_t)Nt * K) && !bnh_memcpy_h2d(W->bias_eff, hb, 4 * (size_t)Nt) &&
+            !bnh_memcpy_h2d(W->mult, hm, 4 * (size_t)Nt) && !bnh_memcpy_h2d(W->shift, hs, 4 * (size_t)Nt);
+  free(hw); free(hb); free(hm); free(hs);
+  if (!ok) { bnh_q8w_free(W); return nullptr; }
+  return W;
+}
+
+void bnh_q8w_free(bnh_q8w *W) {
+  if (!W) return;
+  if (W->w) hipFree(W->w);
+  if (W->bias_eff) hipFree(W->bias_eff);
+  if (W->mult) hipFree(W->mult);
+  if (W->shift) hipFree(W->shift);
+  free(W);
+}
+
+int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M, int B, int8_t *out,
+                        long long out_ws, void *stream) {
+  BNH_REQ(W && x && out && M > 0 && B > 0);
+  BNH_REQ(M % 4 == 0 && ((uintptr_t)x & 3) == 0 && ((uintptr_t)out & 3) == 0);
+  BNH_REQ(B == 1 || (x_ws % 4 == 0 && out_ws % 4 == 0 && x_ws >= (long long)W->K * M && out_ws >= (long long)W->N * M));
+  BNH_REQ(W->K % 16 == 0);
+  const int tpw = (int)bnh_ceil_div(M, 64);
+  dim3 grid((unsigned)((long long)tpw * B), (unsigned)bnh_ceil_div(W->N, 128));
+  hipLaunchKernelGGL(k_gemm_s8_requant, grid, dim3(256), 0, bnh_stream(stream), x, x_ws, M, W->K, tpw, W->w,
+                     W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,570 @@
+// .bnpk reader (mmap, bounds-checked tables, metadata) and the batched executor (device arena, op list).
+// Package checks and error texts follow the reference loader's contract (src/rt_pkg.c:30-102, 349-509): a package
+// the reference refuses is refused here with the same kind of message, and a package it accepts runs here.
+#include <errno.h>
+#include <fcntl.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <time.h>
+#include <unistd.h>
+
+#include "rt.h"
+
+struct rt_pkg {
+  void *map;
+  size_t size;
+  uint32_t n_meta, n_tensors, n_paths;
+  int version;
+  const uint8_t *meta;
+  size_t meta_bytes;
+  rt_tensor *tensors;
+  rt_pathdesc *paths;
+};
+
+#define FAIL(...) do { snprintf(err, errlen, __VA_ARGS__); goto fail; } while (0)
+
+rt_pkg *rt_pkg_open(const char *path, char *err, size_t errlen) {
+  rt_pkg *p = (rt_pkg *)calloc(1, sizeof *p);
+  const uint8_t *m;
+  uint32_t bom, cnt[4];
+  uint16_t ver[2];
+  uint64_t off[4];
+  if (!p) { snprintf(err, errlen, "out of memory"); return nullptr; }
+  int fd = open(path, O_RDONLY);
+  if (fd < 0) { snprintf(err, errlen, "cannot open %s (%s)", path, strerror(errno)); free(p); return nullptr; }
+  struct stat sb;
+  int no_stat = fstat(fd, &sb) != 0;
+  if (no_stat || sb.st_size < 64) {
+    close(fd);
+    snprintf(err, errlen, "%s: %lld bytes, smaller than a package header (64); hint: incomplete download or the wrong file",
+             path, no_stat ? -1LL : (long long)sb.st_size);
+    free(p);
+    return nullptr;
+  }
+  p->size = (size_t)sb.st_size;
+  p->map = mmap(nullptr, p->size, PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  if (p->map == MAP_FAILED) {
+    p->map = nullptr;
+    snprintf(err, errlen, "%s: mmap of %zu bytes failed (%s); hint: memory or a filesystem that cannot map files", path,
+             p->size, strerror(errno));
+    free(p);
+    return nullptr;
+  }
+  m = (const uint8_t *)p->map;
+  if (memcmp(m, "BNNPKG01", 8))
+    FAIL("%s: not a .bnpk package (magic '%.8s', expected BNNPKG01); hint: the file is not a compiled model package: "
+         "compile the model with bnc, or check the download (sha256)", path, (const char *)m);
+  memcpy(&bom, m + 8, 4);
+  memcpy(ver, m + 12, 4);
+  if (bom != 0x01020304u) FAIL("%s: byte-order mark 0x%08x, expected 0x01020304 (little endian); hint: corrupt file", path, bom);
+  p->version = ver[0];
+  if (ver[1] > RT_READER_VERSION)
+    FAIL("%s: the package needs reader version %u, this library reads format version %u; hint: update libbnneon_hip, or "
+         "recompile the model with the compiler that matches this library", path, ver[1], RT_READER_VERSION);
+  memcpy(cnt, m + 16, 16);
+  memcpy(off, m + 32, 32);
+  p->n_meta = cnt[0]; p->n_tensors = cnt[1]; p->n_paths = cnt[2];
+  if (off[3] != p->size)
+    FAIL("%s: package truncated (size %zu, header says %llu); hint: incomplete download or copy; compare the sha256", path,
+         p->size, (unsigned long long)off[3]);
+  if (p->n_tensors > 65536 || p->n_paths < 1 || p->n_paths > 8 || p->n_meta > 4096)
+    FAIL("%s: corrupt header (%u metadata records, %u tensors, %u paths; limits 4096 / 65536 / 1..8); hint: corrupt file or "
+         "not a package", path, p->n_meta, p->n_tensors, p->n_paths);
+  if (off[0] > p->size || off[1] > p->size || off[2] > p->size || off[1] < off[0] ||
+      off[1] + (uint64_t)p->n_tensors * sizeof(rt_tensor) > p->size ||
+      off[2] + (uint64_t)p->n_paths * sizeof(rt_pathdesc) > p->size)
+    FAIL("%s: table offsets outside the file (meta %llu, tensors %llu, paths %llu, size %zu); hint: corrupt file", path,
+         (unsigned long long)off[0], (unsigned long long)off[1], (unsigned long long)off[2], p->size);
+  p->meta = m + off[0];
+  p->meta_bytes = off[1] - off[0];
+  p->tensors = (rt_tensor *)malloc(sizeof(rt_tensor) * (p->n_tensors ? p->n_tensors : 1));
+  p->paths = (rt_pathdesc *)malloc(sizeof(rt_pathdesc) * p->n_paths);
+  if (!p->tensors || !p->paths) FAIL("out of memory");
+  memcpy(p->tensors, m + off[1], sizeof(rt_tensor) * p->n_tensors);
+  memcpy(p->paths, m + off[2], sizeof(rt_pathdesc) * p->n_paths);
+  for (uint32_t i = 0; i < p->n_tensors; i++) {
+    const rt_tensor *t = &p->tensors[i];
+    if (t->offset % 64 || t->offset > p->size || t->nbytes > p->size - t->offset || t->offset + t->nbytes + 64 > p->size)
+      FAIL("%s: tensor %u (%.48s) lies outside the file (offset %llu, %llu bytes, file %zu); hint: truncated or corrupt file",
+           path, i, t->name, (unsigned long long)t->offset, (unsigned long long)t->nbytes, p->size);
+  }
+  for (uint32_t i = 0; i < p->n_paths; i++) {
+    const rt_pathdesc *d = &p->paths[i];
+    if (d->n_buf == 0 || d->n_buf > 4096 || d->n_ops == 0 || d->n_ops > 4096 || d->buf_off % 8 || d->ops_off % 8 ||
+        d->buf_off + (uint64_t)d->n_buf * sizeof(rt_bufdesc) > p->size || d->ops_off + d->ops_bytes > p->size ||
+        d->in_buf >= d->n_buf || d->out_buf >= d->n_buf || (d->emb_buf != 0xffffffffu && d->emb_buf >= d->n_buf))
+      FAIL("%s: path %u (%.24s) has corrupt tables (%u buffers, %u ops, in %u out %u emb %u); hint: corrupt file", path, i,
+           d->name, d->n_buf, d->n_ops, d->in_buf, d->out_buf, d->emb_buf);
+  }
+  return p;
+fail:
+  rt_pkg_close(p);
+  return nullptr;
+}
+
+void rt_pkg_close(rt_pkg *p) {
+  if (!p) return;
+  if (p->map) munmap(p->map, p->size);
+  free(p->tensors);
+  free(p->paths);
+  free(p);
+}
+
+// metadata records: u16 key_len, u16 type (0 str, 1 i64, 2 f64, 3 bytes), u32 val_len, key, value, padded to 8
+static const uint8_t *meta_find(const rt_pkg *p, const char *key, uint16_t *type, uint32_t *vlen) {
+  const uint8_t *q = p->meta, *end = p->meta + p->meta_bytes;
+  size_t kl = strlen(key);
+  for (uint32_t i = 0; i < p->n_meta && q + 8 <= end; i++) {
+    uint16_t h[2];
+    uint32_t vl;
+    memcpy(h, q, 4);
+    memcpy(&vl, q + 4, 4);
+    size_t rec = (8 + (size_t)h[0] + vl + 7) & ~(size_t)7;
+    if ((size_t)(end - q) < rec) return nullptr;
+    if (h[0] == kl && !memcmp(q + 8, key, kl)) { *type = h[1]; *vlen = vl; return q + 8 + h[0]; }
+    q += rec;
+  }
+  return nullptr;
+}
+
+int rt_meta_str(const rt_pkg *p, const char *key, char *buf, size_t n) {
+  uint16_t ty;
+  uint32_t vl;
+  const uint8_t *v = meta_find(p, key, &ty, &vl);
+  if (!v) return -1;
+  char tmp[64];
+  if (ty == 1 || ty == 2) {  // numbers as decimal text
+    if (ty == 1) { int64_t x; memcpy(&x, v, 8); snprintf(tmp, sizeof tmp, "%lld", (long long)x); }
+    else { double x; memcpy(&x, v, 8); snprintf(tmp, sizeof tmp, "%.17g", x); }
+    v = (const uint8_t *)tmp;
+    vl = (uint32_t)strlen(tmp);
+  }
+  if (buf && n) {
+    size_t k = vl < n - 1 ? vl : n - 1;
+    memcpy(buf, v, k);
+    buf[k] = 0;
+  }
+  return (int)vl;
+}
+static int meta_num(const rt_pkg *p, const char *key, uint16_t type, void *x) {
+  uint16_t ty;
+  uint32_t vl;
+  const uint8_t *v = meta_find(p, key, &ty, &vl);
+  if (!v || ty != type || vl != 8) return -1;
+  memcpy(x, v, 8);
+  return 0;
+}
+int rt_meta_i64(const rt_pkg *p, const char *key, int64_t *x) { return meta_num(p, key, 1, x); }
+int rt_meta_f64(const rt_pkg *p, const char *key, double *x) { return meta_num(p, key, 2, x); }
+int rt_n_paths(const rt_pkg *p) { return (int)p->n_paths; }
+int rt_format_version(const rt_pkg *p) { return p->version; }
+const rt_pathdesc *rt_path(const rt_pkg *p, int i) { return i >= 0 && i < (int)p->n_paths ? &p->paths[i] : nullptr; }
+const rt_tensor *rt_tensor_at(const rt_pkg *p, int i, const void **data) {
+  if (i < 0 || i >= (int)p->n_tensors) return nullptr;
+  if (data) *data = (const uint8_t *)p->map + p->tensors[i].offset;
+  return &p->tensors[i];
+}
+
+// ------------------------------------------------------------------ contract helpers
+size_t rt_dsize(uint32_t dt) { return dt == RT_F16 ? 2 : dt == RT_I8 ? 1 : 4; }
+const char *rt_dtype_name(uint32_t dt) {
+  static const char *nm[] = {"f32", "f16", "i8", "i32"};
+  return dt < 4 ? nm[dt] : "?";
+}
+const void *rt_t(const rt_ctx *c, const rt_op *op, int i, size_t *nbytes) {
+  if (i >= op->nt || op->t[i] < 0) return nullptr;
+  const void *d;
+  const rt_tensor *t = rt_tensor_at(c->pkg, op->t[i], &d);
+  if (!t) return nullptr;
+  if (nbytes) *nbytes = t->nbytes;
+  return d;
+}
+const rt_bufdesc *rt_bd(const rt_ctx *c, const rt_op *op, int i) {
+  return i >= op->nb || op->b[i] < 0 ? nullptr : &c->bufd[op->b[i]];
+}
+void rt_free_state(rt_op *op) { free(op->state); }
+
+static void err_set(const rt_ctx *c, int kind, const char *msg) {
+  rt_ctx *w = (rt_ctx *)c;
+  if (!w->err || w->err_kind) return;
+  w->err_kind = kind;
+  snprintf(w->err, w->errlen, "%s", msg);
+}
+static void int_params(const rt_op *op, char *buf, size_t n) {
+  size_t k = 0;
+  buf[0] = 0;
+  for (int i = 0; i < op->ni && k + 16 < n; i++) k += (size_t)snprintf(buf + k, n - k, "%s%d", i ? " " : "", op->p[i]);
+  if (op->ni && k + 16 >= n) snprintf(buf + k, n - k, " ...");
+}
+int rt_bad(const rt_ctx *c, const rt_op *op, const char *fmt, ...) {
+  char msg[320];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(msg, sizeof msg, fmt, ap);
+  va_end(ap);
+  if (c->err && !c->err_kind) int_params(op, ((rt_ctx *)c)->err_params, sizeof c->err_params);
+  err_set(c, RT_E_PARAM, msg);
+  return RT_E_PARAM;
+}
+int rt_oom(const rt_ctx *c, const rt_op *op, size_t bytes) {
+  (void)op;
+  char msg[128];
+  snprintf(msg, sizeof msg, "out of memory allocating %zu bytes of kernel state", bytes);
+  err_set(c, RT_E_OOM, msg);
+  return RT_E_OOM;
+}
+int rt_need(const rt_ctx *c, const rt_op *op, int i, int dt, size_t elems) {
+  const rt_bufdesc *d = rt_bd(c, op, i);
+  if (!d) return rt_bad(c, op, "buffer argument %d is absent (the op record has %d buffer arguments)", i, op->nb);
+  if ((int)d->dtype == dt && d->elems >= elems) return 0;
+  return rt_bad(c, op, "buffer argument %d (buffer #%d): expected dtype %s with >= %zu elements, found dtype %s "
+                "[%ux%ux%u ld %u halo %u] with %llu elements", i, op->b[i], rt_dtype_name((uint32_t)dt), elems,
+                rt_dtype_name(d->dtype), d->H, d->W, d->C, d->ld, d->halo, (unsigned long long)d->elems);
+}
+int rt_need_haloed(const rt_ctx *c, const rt_op *op, int i, int dt, int H, int W, int ld, int h) {
+  if (rt_need(c, op, i, dt, ((size_t)H + 2 * (size_t)h) * ((size_t)W + 2 * (size_t)h) * (size_t)ld)) return RT_E_PARAM;
+  const rt_bufdesc *d = rt_bd(c, op, i);
+  if ((int)d->halo != h || (int)d->ld != ld)
+    return rt_bad(c, op, "buffer argument %d (buffer #%d): expected halo %d and channel stride %d, found halo %u and stride %u",
+                  i, op->b[i], h, ld, d->halo, d->ld);
+  return 0;
+}
+int rt_need_rows(const rt_ctx *c, const rt_op *op, int i, int dt, size_t rows, int ld) {
+  if (rt_need(c, op, i, dt, rows * (size_t)ld)) return RT_E_PARAM;
+  const rt_bufdesc *d = rt_bd(c, op, i);
+  if (d->halo || (int)d->ld != ld)
+    return rt_bad(c, op, "buffer argument %d (buffer #%d): expected unpadded rows of channel stride %d, found halo %u and "
+                  "stride %u", i, op->b[i], ld, d->halo, d->ld);
+  return 0;
+}
+int rt_need_nohalo(const rt_ctx *c, const rt_op *op, int i, int dt, size_t elems) {
+  if (rt_need(c, op, i, dt, elems)) return RT_E_PARAM;
+  const rt_bufdesc *d = rt_bd(c, op, i);
+  if (d->halo) return rt_bad(c, op, "buffer argument %d (buffer #%d, input): expected no halo, found halo %u", i, op->b[i], d->halo);
+  return 0;
+}
+int rt_need_t(const rt_ctx *c, const rt_op *op, int i, size_t nbytes, int atleast) {
+  size_t nb = 0;
+  if (!rt_t(c, op, i, &nb))
+    return rt_bad(c, op, "tensor argument %d is absent (the op record has %d tensor arguments)", i, op->nt);
+  if (atleast ? nb >= nbytes : nb == nbytes) return 0;
+  const rt_tensor *t = rt_tensor_at(c->pkg, op->t[i], nullptr);
+  return rt_bad(c, op, "tensor argument %d (tensor #%d '%.48s' %s [%u %u %u %u]): expected %s%zu bytes, found %llu bytes",
+                i, op->t[i], t->name, rt_dtype_name(t->dtype), t->dims[0], t->dims[1], t->dims[2], t->dims[3],
+                atleast ? ">= " : "", nbytes, (unsigned long long)t->nbytes);
+}
+int rt_need_args(const rt_ctx *c, const rt_op *op, int nb, int nt, int ni) {
+  if ((nb < 0 || op->nb == nb) && (nt < 0 || op->nt == nt) && (ni < 0 || op->ni == ni)) return 0;
+  return rt_bad(c, op, "op record shape: expected %d buffer, %d tensor and %d int arguments, found %d, %d and %d", nb, nt,
+                ni, op->nb, op->nt, op->ni);
+}
+
+int rt_op_src(const rt_ctx *c, int i, char *buf, size_t n) {
+  if (n) buf[0] = 0;
+  if (!c->src) return -1;
+  const char *p = c->src, *end = c->src + c->src_len;
+  for (int k = 0; k < i && p < end; k++) {
+    const char *nl = (const char *)memchr(p, '\n', (size_t)(end - p));
+    if (!nl) return -1;
+    p = nl + 1;
+  }
+  if (p >= end) return -1;
+  const char *nl = (const char *)memchr(p, '\n', (size_t)(end - p));
+  size_t l = (size_t)((nl ? nl : end) - p);
+  if (n) { if (l > n - 1) l = n - 1; memcpy(buf, p, l); buf[l] = 0; }
+  return 0;
+}
+const char *rt_op_name(const rt_ctx *c, int i) { return i >= 0 && i < c->n_ops && c->ops[i].k ? c->ops[i].k->name : "?"; }
+
+const rt_kernel *rt_kernel_for(int code) {
+  int base = code & 0xff, var = code >> 8;
+  if (base <= 0 || base >= RT_OP_N) return nullptr;
+  const rt_kernel *k = var == 0 ? rt_k_var0(base) : var == 1 ? rt_k_var1(base) : nullptr;
+  return k && k->run ? k : nullptr;
+}
+
+static const char *op_prefix(const rt_ctx *c, int i, const char *kname, char *buf, size_t n) {
+  char src[160];
+  if (rt_op_src(c, i, src, sizeof src) == 0 && src[0]) {
+    if (strlen(src) > 96) strcpy(src + 93, "...'");
+    snprintf(buf, n, "op %d %s (ONNX node %s)", i, kname ? kname : "?", src);
+  } else
+    snprintf(buf, n, "op %d %s (no source node names in the package: compile with bnc 2 or newer)", i, kname ? kname : "?");
+  return buf;
+}
+#define HINT_PKG "hint: package/library mismatch or a lowering bug: recompile with bnc; if it reproduces, report this message"
+#define KIND(k) do { if (kind) *kind = (k); } while (0)
+#define PFX(kname) op_prefix(c, (int)i, kname, pfx, sizeof pfx)
+
+// ------------------------------------------------------------------ device arena
+// Per window, every memory slot gets its largest buffer's bytes + 64 zero bytes, rounded to 64 (the reference's
+// arena rule, src/rt_pkg.c:379-391); the arena holds `bcap` copies of each slot back to back.
+static int arena_alloc(rt_ctx *c, int windows, char *err, size_t errlen) {
+  size_t per = 0;
+  for (int s = 0; s < c->n_buf; s++) per += c->slot_bytes[s];
+  size_t total = per * (size_t)windows;
+  char *a = nullptr;
+  int *wf = nullptr;
+  hipError_t e = hipMalloc(&a, total ? total : 64);
+  if (e != hipSuccess) {
+    snprintf(err, errlen, "out of device memory: %zu bytes (%.1f MB) for %d windows of activation buffers; hint: use fewer "
+             "windows per batch", total, total / 1e6, windows);
+    return RT_E_OOM;
+  }
+  e = hipMalloc(&wf, sizeof(int) * (size_t)windows);
+  if (e != hipSuccess) {
+    hipFree(a);
+    snprintf(err, errlen, "out of device memory for %d window flags", windows);
+    return RT_E_OOM;
+  }
+  if (hipMemsetAsync(a, 0, total ? total : 64, c->stream) != hipSuccess || hipStreamSynchronize(c->stream) != hipSuccess) {
+    hipFree(a); hipFree(wf);
+    snprintf(err, errlen, "device error while zeroing the activation arena");
+    return RT_E_OOM;
+  }
+  if (c->arena) hipFree(c->arena);
+  if (c->win_fail) hipFree(c->win_fail);
+  c->arena = a;
+  c->win_fail = wf;
+  c->arena_bytes = total;
+  c->bcap = windows;
+  // slot s of window w at arena + slot_off[s] * windows + w * slot_bytes[s]
+  size_t off = 0;
+  size_t *slot_off = (size_t *)calloc(c->n_buf, sizeof(size_t));
+  if (!slot_off) { snprintf(err, errlen, "out of memory"); return RT_E_OOM; }
+  for (int s = 0; s < c->n_buf; s++) { slot_off[s] = off; off += c->slot_bytes[s] * (size_t)windows; }
+  for (int i = 0; i < c->n_buf; i++) {
+    const rt_bufdesc *d = &c->bufd[i];
+    c->buf[i] = a + slot_off[d->slot];
+    c->ws[i] = (long long)(c->slot_bytes[d->slot] / rt_dsize(d->dtype));
+  }
+  free(slot_off);
+  return 0;
+}
+
+int rt_reserve(rt_ctx *c, int windows, char *err, size_t errlen) {
+  if (windows <= c->bcap) return 0;
+  return arena_alloc(c, windows, err, errlen);
+}
+
+rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
+  KIND(RT_E_PARAM);
+  const rt_pathdesc *d = rt_path(p, pi);
+  const uint8_t *m, *q, *end;
+  char pfx[256];
+  size_t total = 0;
+  if (!d) { snprintf(err, errlen, "no path %d in the package (%d paths)", pi, rt_n_paths(p)); return nullptr; }
+  rt_ctx *c = (rt_ctx *)calloc(1, sizeof *c);
+  if (!c) { KIND(RT_E_OOM); snprintf(err, errlen, "out of memory (%zu bytes for the context)", sizeof *c); return nullptr; }
+  c->pkg = p;
+  c->path = d;
+  c->fail_op = -1;
+  c->err = err;
+  c->errlen = errlen;
+  c->n_buf = (int)d->n_buf;
+  {
+    char key[64];
+    uint16_t ty;
+    uint32_t vl;
+    snprintf(key, sizeof key, "src_nodes/%.24s", d->name);
+    const uint8_t *v = meta_find(p, key, &ty, &vl);
+    if (v && (ty == 0 || ty == 3)) { c->src = (const char *)v; c->src_len = vl; }
+  }
+  m = (const uint8_t *)p->map;
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    c->stream = nullptr;
+    KIND(RT_E_OOM);
+    FAIL("cannot create a HIP stream (no usable GPU?); hint: check that an MI355X is visible (rocm-smi)");
+  }
+  c->own_stream = 1;
+  c->bufd = (rt_bufdesc *)malloc(sizeof(rt_bufdesc) * d->n_buf);
+  c->buf = (void **)calloc(d->n_buf, sizeof(void *));
+  c->ws = (long long *)calloc(d->n_buf, sizeof(long long));
+  c->slot_bytes = (size_t *)calloc(d->n_buf, sizeof(size_t));
+  if (!c->bufd || !c->buf || !c->ws || !c->slot_bytes) { KIND(RT_E_OOM); FAIL("out of memory (%u buffer descriptors)", d->n_buf); }
+  memcpy(c->bufd, m + d->buf_off, sizeof(rt_bufdesc) * d->n_buf);
+  for (uint32_t i = 0; i < d->n_buf; i++) {
+    const rt_bufdesc *b = &c->bufd[i];
+    if (b->dtype > RT_I32 || b->elems > ((uint64_t)1 << 30) || b->slot >= d->n_buf)
+      FAIL("path %.24s buffer #%u: bad descriptor (dtype %u, %llu elements, slot %u of %u); " HINT_PKG, d->name, i, b->dtype,
+           (unsigned long long)b->elems, b->slot, d->n_buf);
+    if ((i == d->in_buf) != (b->slot == c->bufd[d->in_buf].slot))
+      FAIL("path %.24s buffer #%u shares the input window's memory slot %u; " HINT_PKG, d->name, i, b->slot);
+    size_t bytes = ((size_t)b->elems * rt_dsize(b->dtype) + 64 + 63) & ~(size_t)63;
+    if (bytes > c->slot_bytes[b->slot]) c->slot_bytes[b->slot] = bytes;
+  }
+  for (uint32_t s = 0; s < d->n_buf; s++) {
+    total += c->slot_bytes[s];
+    if (total > ((size_t)1 << 30))
+      FAIL("path %.24s needs more than 1 GB of activation buffers per window; hint: the package is corrupt or the model is "
+           "far larger than this runtime is built for", d->name);
+  }
+  for (uint32_t i = 0; i < d->n_buf; i++)
+    if (i != d->out_buf && (c->bufd[i].slot == c->bufd[d->out_buf].slot ||
+                            (d->emb_buf != 0xffffffffu && i != d->emb_buf && c->bufd[i].slot == c->bufd[d->emb_buf].slot)))
+      FAIL("path %.24s buffer #%u shares memory slot %u with the output buffer (#%u / #%u); " HINT_PKG, d->name, i,
+           c->bufd[i].slot, d->out_buf, d->emb_buf);
+  {
+    int k2 = arena_alloc(c, 1, err, errlen);
+    if (k2) { KIND(k2); goto fail; }
+  }
+  c->ops = (rt_op *)calloc(d->n_ops, sizeof(rt_op));
+  if (!c->ops) { KIND(RT_E_OOM); FAIL("out of memory (%u op records)", d->n_ops); }
+  q = m + d->ops_off;
+  end = q + d->ops_bytes;
+  for (uint32_t i = 0; i < d->n_ops; i++) {
+    uint16_t h[6];
+    if (q + 12 > end) FAIL("op %u: truncated op list (%u ops declared, %u bytes); " HINT_PKG, i, d->n_ops, d->ops_bytes);
+    memcpy(h, q, 12);
+    size_t need = 12 + 4 * ((size_t)h[2] + h[3] + h[4]);
+    if (h[1] < need || q + h[1] > end || ((uintptr_t)(q - m) % 4))
+      FAIL("op %u: bad op record (%u bytes for %u buffer, %u tensor, %u int arguments); " HINT_PKG, i, h[1], h[2], h[3], h[4]);
+    rt_op *op = &c->ops[i];
+    op->code = h[0]; op->nb = h[2]; op->nt = h[3]; op->ni = h[4];
+    op->b = (const int32_t *)(q + 12);
+    op->t = op->b + op->nb;
+    op->p = op->t + op->nt;
+    for (int k = 0; k < op->nb; k++)
+      if (op->b[k] >= (int32_t)d->n_buf || op->b[k] < -1)
+        FAIL("%s: buffer argument %d names buffer #%d but the path has %u buffers; " HINT_PKG, PFX(nullptr), k, op->b[k],
+             d->n_buf);
+    for (int k = 0; k < op->nt; k++)
+      if (op->t[k] >= (int32_t)p->n_tensors)
+        FAIL("%s: tensor argument %d names tensor #%d but the package has %u tensors; " HINT_PKG, PFX(nullptr), k, op->t[k],
+             p->n_tensors);
+    int var = op->code >> 8;
+    if (var && !(d->hwcap & RT_HW_FP16))
+      FAIL("%s: fp16 kernel (opcode 0x%x) in path %.24s, which does not declare the fp16 requirement; " HINT_PKG,
+           PFX(nullptr), op->code, d->name);
+    if (var == 2 && !(d->hwcap & RT_HW_DOTPROD))
+      FAIL("%s: dotprod kernel (opcode 0x%x) in path %.24s, which does not declare the dotprod requirement; " HINT_PKG,
+           PFX(nullptr), op->code, d->name);
+    const rt_kernel *k = op->k = rt_kernel_for(op->code);
+    if (!k) {
+      char comp[48];
+      if (rt_meta_str(p, "compiler", comp, sizeof comp) < 0) snprintf(comp, sizeof comp, "unknown");
+      FAIL("%s: unknown opcode 0x%x (base %d variant %d); this library runs opcodes 1..%d of variants 0 and 1 on the GPU "
+           "(reader version %d), the package was written by compiler '%s'; hint: pick a path of the package this library "
+           "runs (mode 0), or update libbnneon_hip", PFX(nullptr), op->code, op->code & 0xff, var, RT_OP_N - 1,
+           RT_READER_VERSION, comp);
+    }
+    PFX(k->name);
+    for (int a = 0; a < op->nb; a++) {
+      if (op->b[a] < 0 && !(a < 32 && (k->optmask >> a & 1)))
+        FAIL("%s: buffer argument %d is required by the kernel but absent (-1) in the op record; " HINT_PKG, pfx, a);
+      if (op->b[a] == (int32_t)d->in_buf && a < 32 && (k->outmask >> a & 1))
+        FAIL("%s: buffer argument %d is the input window (#%u) but the kernel writes it; " HINT_PKG, pfx, a, d->in_buf);
+    }
+    for (int a = 0; a < op->nb; a++)
+      for (int b2 = 0; b2 < op->nb; b2++)
+        if (a != b2 && op->b[a] >= 0 && op->b[b2] >= 0 && a < 32 && (k->outmask >> a & 1) &&
+            (op->b[a] == op->b[b2] || c->bufd[op->b[a]].slot == c->bufd[op->b[b2]].slot))
+          FAIL("%s: buffer arguments %d (#%d, written) and %d (#%d) share memory slot %u; " HINT_PKG, pfx, a, op->b[a], b2,
+               op->b[b2], c->bufd[op->b[a]].slot);
+    c->n_ops = (int)i + 1;
+    c->err_kind = 0;
+    c->err_params[0] = 0;
+    if (k->init && k->init(c, op)) {
+      char detail[400];
+      snprintf(detail, sizeof detail, "%s", c->err_kind ? err : "init failed without a message (kernel bug)");
+      if (c->err_kind == RT_E_OOM) {
+        KIND(RT_E_OOM);
+        snprintf(err, errlen, "%s: %s; hint: free device memory or use a smaller model", pfx, detail);
+      } else {
+        int n = snprintf(err, errlen, "%s: %s; " HINT_PKG, pfx, detail);
+        if (n > 0 && (size_t)n + 24 < errlen && c->err_params[0])
+          snprintf(err + n, errlen - (size_t)n, " (int params: [%s])", c->err_params);
+      }
+      goto fail;
+    }
+    q += h[1];
+  }
+  c->err = nullptr;
+  {
+    const char *pe = getenv("BNN_PROF");
+    c->prof = pe ? atoi(pe) : 0;
+    if (c->prof) c->t_op = (double *)calloc(d->n_ops, sizeof(double));
+  }
+  return c;
+fail:
+  c->err = nullptr;
+  rt_ctx_free(c);
+  return nullptr;
+}
+#undef PFX
+
+static double now_s(void) {
+  struct timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return t.tv_sec + t.tv_nsec * 1e-9;
+}
+
+int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
+  if (B > c->bcap) { snprintf(err, errlen, "rt_run_batch: %d windows but the arena holds %d", B, c->bcap); return -1; }
+  if (hipMemsetAsync(c->win_fail, 0, sizeof(int) * (size_t)B, c->stream) != hipSuccess) {
+    snprintf(err, errlen, "device error clearing the window flags");
+    return -1;
+  }
+  double t0 = c->prof ? now_s() : 0;
+  for (int i = 0; i < c->n_ops; i++) {
+    rt_op *op = &c->ops[i];
+    c->fail_op = i;  // ops read it to tag the windows they fail
+    int r = op->k->run(c, op);
+    if (r) {
+      char src[160];
+      rt_op_src(c, i, src, sizeof src);
+      snprintf(err, errlen, "op %d %s%s%s%s: launch failed (%s)", i, op->k->name, src[0] ? " (ONNX node " : "", src,
+               src[0] ? ")" : "", hipGetErrorString(hipGetLastError()));
+      return -1;
+    }
+    if (c->prof) {
+      hipStreamSynchronize(c->stream);
+      double t = now_s();
+      c->t_op[i] += t - t0;
+      t0 = t;
+    }
+  }
+  c->fail_op = -1;
+  hipError_t e = hipMemcpyAsync(status, c->win_fail, sizeof(int) * (size_t)B, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) { snprintf(err, errlen, "device error after the op list: %s", hipGetErrorString(e)); return -1; }
+  c->nprof += B;
+  int nf = 0;
+  for (int w = 0; w < B; w++) nf += status[w] != 0;
+  return nf;
+}
+
+void rt_ctx_free(rt_ctx *c) {
+  if (!c) return;
+  if (c->stream) hipStreamSynchronize(c->stream);
+  if (c->prof && c->nprof && c->t_op) {
+    double tot = 0;
+    fprintf(stderr, "profile over %d windows (ms per window, batched), path %s:\n", c->nprof, c->path->name);
+    for (int i = 0; i < c->n_ops; i++) {
+      tot += c->t_op[i];
+      char src[120];
+      rt_op_src(c, i, src, sizeof src);
+      if (c->prof > 1) fprintf(stderr, "  %3d %-14s %10.5f  %s\n", i, c->ops[i].k->name, 1e3 * c->t_op[i] / c->nprof, src);
+    }
+    fprintf(stderr, "  %-14s      %10.5f\n", "total", 1e3 * tot / c->nprof);
+  }
+  for (int i = 0; i < c->n_ops; i++) {
+    rt_op *op = &c->ops[i];
+    if (op->k && op->k->fini) op->k->fini(op);
+  }
+  free(c->ops);
+  free(c->t_op);
+  if (c->arena) hipFree(c->arena);
+  if (c->win_fail) hipFree(c->win_fail);
+  free(c->buf);
+  free(c->ws);
+  free(c->slot_bytes);
+  free(c->bufd);
+  if (c->stream && c->own_stream) hipStreamDestroy(c->stream);
+  free(c);
+}

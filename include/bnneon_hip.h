@@ -1,0 +1,95 @@
+/* libbnneon_hip kernel-level C ABI: the quantized conv / GEMM hot path of libbnneon on MI355X (gfx950).
+ *
+ * These entry points take DEVICE pointers (HBM) and a HIP stream (NULL = the default stream) and run one kernel
+ * family over B windows at once. Every buffer argument names the first window; the window w of a buffer starts
+ * `*_ws` ELEMENTS after it (its per-window stride). Each entry point replaces the reference function cited in its
+ * comment (paths relative to the reference checkout) and computes, per window, exactly what that function computes
+ * (bit-identical for the int8 paths).
+ *
+ * Return value: 0 on success; -1 with bnh_last_error() (thread-local, <= 511 bytes) describing the failure.
+ * Shapes are checked on the host before any launch; nothing here allocates device memory except the *_new
+ * constructors and bnh_malloc.
+ */
+#ifndef BNNEON_HIP_H
+#define BNNEON_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ device plumbing (for hosts without a HIP
+ * runtime of their own: ctypes, cgo). No counterpart in the reference, which has no device memory. */
+const char *bnh_last_error(void);
+int bnh_device_count(void);
+void *bnh_malloc(size_t bytes);                                   /* NULL on failure */
+int bnh_free(void *p);
+int bnh_memcpy_h2d(void *dst, const void *src, size_t bytes);     /* synchronous */
+int bnh_memcpy_d2h(void *dst, const void *src, size_t bytes);     /* synchronous */
+int bnh_memset(void *dst, int value, size_t bytes);               /* synchronous */
+void *bnh_stream_new(void);
+int bnh_stream_free(void *stream);
+int bnh_stream_sync(void *stream);
+void *bnh_event_new(void);
+int bnh_event_free(void *ev);
+int bnh_event_record(void *ev, void *stream);
+float bnh_event_ms(void *start, void *stop);                      /* after both completed; < 0 on error */
+
+/* ------------------------------------------------------------------ scalar numerics checks
+ * y[i] = f(x[i]) on the device for n elements, f = 0: FRECPE, 1: the fp32 SiLU of the epilogues
+ * (src/gemm_f32.h:102-118), 2: ReLU (vmaxq_f32 with 0). Used to pin the device numerics against the oracle. */
+int bnh_eval_f32(int f, const float *x, float *y, long long n, void *stream);
+
+/* ------------------------------------------------------------------ int8 GEMM weights (PW_S8 / GEMV_S8)
+ * Built from the package tensors of one int8 GEMM (python/bnneon/compiler/lower.py:883-914, s8_tensors; validated
+ * by s8_view, src/rt_ops_s8n.c:13-25): host arrays w int8 [Np/4][Kp/16][4][16], sw f32 [>= Np], colsum i32 [>= Np],
+ * b f32 [>= Np]. The weights are repacked once into the MFMA operand order and kept in HBM. */
+typedef struct bnh_s8w bnh_s8w;
+bnh_s8w *bnh_s8w_new(int N, int K, int Kp, int Np, const int8_t *w, const float *sw, const int32_t *colsum,
+                     const float *b);
+void bnh_s8w_free(bnh_s8w *W);
+
+/* the fp32 epilogue of the int8 GEMM (epi32, src/gemm_f32.h:15-24), with per-window strides */
+typedef struct {
+  int act;               /* 0 none, 1 SiLU, 2 ReLU */
+  float *out;            /* pixel m at row m (opad 0) or ((m/ow)+opad)*(ow+2opad) + m%ow + opad */
+  long long out_ws;
+  int ldo, ow, opad;
+  const float *res;      /* optional residual (NULL), added after the activation */
+  long long res_ws;
+  int ldr, rpad, rw;
+} bnh_epi32;
+
+/* s8n_quant_rows / s8n_quant_rows_gate (src/gemm_s8n.c:15-63; declared src/gemm_s8n.h:15-17): rows [0, M) of
+ * each window -> q int8 [M][Kp] (pad k = the zero point), sa f32 [M], za i32 [M]. gate (or NULL): f32 [K] per
+ * window (stride gate_ws), K % 4 == 0 and K <= 4096 as the reference requires. */
+int bnh_s8n_quant_rows(const float *x, long long x_ws, int ld, int M, int K, int Kp, const float *gate,
+                       long long gate_ws, int8_t *q, long long q_ws, float *sa, int32_t *za, long long s_ws, int B,
+                       void *stream);
+/* s8n_gemm_range over every row and panel (src/gemm_s8n.c:176-190; src/gemm_s8n.h:21-22): out rows [0, M) x
+ * channels [0, Np) = act(dequant(q . W) + b) (+ residual), stored by the epi32 rules */
+int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, const int32_t *za, long long s_ws, int M, int B,
+                 const bnh_s8w *W, const bnh_epi32 *e, void *stream);
+/* the PW_S8 op run (pw8_run, src/rt_ops_s8n.c:119-134): zero the output halo when opad (H = M / ow), quantize
+ * (gated when gate != NULL) and multiply, for B windows */
+int bnh_pw_s8(const float *in, long long in_ws, int lda, int M, const float *gate, long long gate_ws, int8_t *q,
+              long long q_ws, float *sa, int32_t *za, long long s_ws, int B, const bnh_s8w *W, const bnh_epi32 *e,
+              void *stream);
+
+/* ------------------------------------------------------------------ int8 GEMM with Q31 requantisation
+ * No counterpart in the reference (whose int8 GEMM dequantises to fp32): the TFLite-style static int8 pointwise
+ * convolution, NCHW. Per window: x int8 [K][M] (pixels contiguous), out int8 [N][M];
+ *   acc = sum_k w[n][k] (x[k][m] - zx) + bias[n];
+ *   out = clamp(RoundingDivideByPOT(SaturatingRoundingDoublingHighMul(acc, mult[n]), shift[n]) + zy, lo, hi).
+ * Weights are uploaded once (host w int8 [N][K], bias / mult / shift int32 [N]). */
+typedef struct bnh_q8w bnh_q8w;
+bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const int32_t *mult, const int32_t *shift,
+                     int zx, int zy, int lo, int hi);
+void bnh_q8w_free(bnh_q8w *W);
+int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M, int B, int8_t *out,
+                        long long out_ws, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

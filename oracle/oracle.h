@@ -1,0 +1,76 @@
+/* CPU oracle for the quantized conv/GEMM hot path of libbnneon (cdw9bf/birdnet-neon-engine).
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this
+ * library, and only as the checker (or as the timed CPU baseline). The product path (libbnneon_hip.so) never links,
+ * loads or calls it.
+ *
+ * Every function restates, in scalar C, what the reference's NEON kernels compute, element by element, with the
+ * AArch64 floating-point semantics those kernels run under (FPCR default: round to nearest even, no flush to zero,
+ * NaN-propagating FMIN/FMAX, saturating float->int conversions, FRECPE/FRECPS as in the Arm ARM pseudocode). Build
+ * flags: -O2 -ffp-contract=off (the reference's Makefile:16), so every a*b+c below is two roundings unless it is an
+ * explicit fmaf. Each function names the reference file:line it follows.
+ *
+ * Where the reference has no kernel (the Q31 requantised GEMM, the int8 depthwise) the function is this project's own
+ * written specification; its header comment says so.
+ */
+#ifndef BNN_ORACLE_H
+#define BNN_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- AArch64 scalar semantics */
+float orc_frecpe(float x);                 /* FRECPE (Arm ARM FPRecipEstimate, FPCR.FZ = 0, RN) */
+float orc_frecps(float a, float b);        /* FRECPS: 2 - a*b fused, with the (inf, 0) -> 2 rule */
+float orc_fmax(float a, float b);          /* FMAX: NaN-propagating, +0 > -0 */
+float orc_fmin(float a, float b);          /* FMIN: NaN-propagating, -0 < +0 */
+int32_t orc_cvtn_s32(float x);             /* FCVTNS w: round to nearest even, saturating, NaN -> 0 */
+int32_t orc_cvta_s32(float x);             /* FCVTAS w: round to nearest ties away, saturating, NaN -> 0 */
+int32_t orc_lrintf_s32(float x);           /* (int32_t)lrintf(x) on AArch64: FRINTX + FCVTZS x, low 32 bits */
+float orc_silu_f32(float x);               /* silu_f32x4 / silu4_f32x4 lane (src/gemm_f32.h:102-145) */
+void orc_eval_f32(int f, const float *x, float *y, long long n); /* 0 FRECPE, 1 SiLU, 2 ReLU, elementwise */
+
+/* ---------------------------------------------------------------- int8 no-dotprod GEMM (PW_S8) */
+typedef struct {
+  int act;          /* 0 none, 1 SiLU, 2 ReLU (src/gemm_f32.h:14) */
+  float *out;
+  int ldo, ow, opad;
+  const float *res;
+  int ldr, rpad, rw;
+} orc_epi32;        /* src/gemm_f32.h:15-24 */
+
+/* src/gemm_s8n.c:15-51 */
+void orc_s8n_quant_rows(const float *x, int ld, int r0, int r1, int K, int Kp, int8_t *q, float *sa, int32_t *za);
+/* src/gemm_s8n.c:55-63 */
+void orc_s8n_quant_rows_gate(const float *x, int ld, int r0, int r1, int K, int Kp, const float *gate, int8_t *q,
+                             float *sa, int32_t *za);
+/* src/gemm_s8n.c:82-190: every row m < M and channel n < Np of act(dequant(q . W) + b) (+ residual), stored by the
+ * epi32 rules. w is the package layout [Np/4][Kp/16][4][16]. */
+void orc_s8n_gemm(const int8_t *q, int Kp, const float *sa, const int32_t *za, int M, int Np, const int8_t *w,
+                  const float *sw, const int32_t *colsum, const float *b, const orc_epi32 *e);
+/* the PW_S8 op of one window (src/rt_ops_s8n.c:119-134): halo zeroing of a padded output (H = M / ow rows), the
+ * quantization of rows [0, M) and the GEMM */
+void orc_pw_s8(const float *in, int lda, int M, int K, int Kp, int N, int Np, const float *gate, int8_t *q, float *sa,
+               int32_t *za, const int8_t *w, const float *sw, const int32_t *colsum, const float *b, const orc_epi32 *e);
+/* rt_zero_halo (src/rt_pkg.c:194-203) */
+void orc_zero_halo(void *xp, int H, int W, int C, int h, size_t esz);
+
+/* ---------------------------------------------------------------- Q31 requantised int8 GEMM (own specification)
+ * The reference has no such kernel. Specification (TFLite / gemmlowp fixed-point conventions):
+ *   acc[n][m]  = sum_k w[n][k] * (x[k][m] - zx) + bias[n]                       (exact, int32)
+ *   y          = RoundingDivideByPOT(SaturatingRoundingDoublingHighMul(acc, mult[n]), shift[n]) + zy
+ *   out[n][m]  = clamp(y, lo, hi)                                               (int8)
+ * w int8 [N][K] row-major; x int8 [K][M] (NCHW: pixels contiguous); out int8 [N][M]. */
+int32_t orc_srdhm(int32_t a, int32_t b);
+int32_t orc_rdbypot(int32_t x, int exponent);
+int8_t orc_requant(int32_t acc, int32_t mult, int shift, int zy, int lo, int hi);
+void orc_gemm_s8_requant(const int8_t *w, const int8_t *x, const int32_t *bias, const int32_t *mult, const int32_t *shift,
+                         int N, int K, int M, int zx, int zy, int lo, int hi, int8_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

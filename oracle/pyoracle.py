@@ -1,0 +1,157 @@
+"""ctypes loader of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: loaded by tests/ (as the checker), by
+__graft_entry__.smoke() (as the checker) and by bench.py's cpu_baseline leg
+(as the timed CPU restatement). The product path never imports it.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
+ORACLE_LIB = os.path.join(ORACLE_DIR, "liboracle.so")
+
+vp = C.c_void_p
+i32 = C.c_int
+f32 = C.c_float
+
+
+class OrcEpi32(C.Structure):
+    _fields_ = [("act", i32), ("out", vp), ("ldo", i32), ("ow", i32),
+                ("opad", i32), ("res", vp), ("ldr", i32), ("rpad", i32),
+                ("rw", i32)]
+
+
+_SIGS = {
+    "orc_frecpe": (f32, [f32]),
+    "orc_frecps": (f32, [f32, f32]),
+    "orc_fmax": (f32, [f32, f32]),
+    "orc_fmin": (f32, [f32, f32]),
+    "orc_cvtn_s32": (i32, [f32]),
+    "orc_cvta_s32": (i32, [f32]),
+    "orc_lrintf_s32": (i32, [f32]),
+    "orc_silu_f32": (f32, [f32]),
+    "orc_eval_f32": (None, [i32, vp, vp, C.c_longlong]),
+    "orc_s8n_quant_rows": (None, [vp, i32, i32, i32, i32, i32, vp, vp, vp]),
+    "orc_s8n_quant_rows_gate": (None, [vp, i32, i32, i32, i32, i32, vp, vp,
+                                       vp, vp]),
+    "orc_s8n_gemm": (None, [vp, i32, vp, vp, i32, i32, vp, vp, vp, vp,
+                            C.POINTER(OrcEpi32)]),
+    "orc_pw_s8": (None, [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp,
+                         vp, vp, vp, vp, C.POINTER(OrcEpi32)]),
+    "orc_srdhm": (i32, [i32, i32]),
+    "orc_rdbypot": (i32, [i32, i32]),
+    "orc_requant": (C.c_int8, [i32, i32, i32, i32, i32, i32]),
+    "orc_gemm_s8_requant": (None, [vp, vp, vp, vp, vp, i32, i32, i32, i32,
+                                   i32, i32, i32, vp]),
+}
+
+_lib = None
+
+
+def build():
+    """Builds liboracle.so with the committed Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", ORACLE_DIR], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_LIB):
+            build()
+        L = C.CDLL(ORACLE_LIB)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name, None)
+            if f is None:
+                continue
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def P(a):
+    """Host pointer of a numpy array (or None)."""
+    return None if a is None else a.ctypes.data
+
+
+def eval_f32(f, x):
+    """orc_eval_f32 over an array: 0 FRECPE, 1 SiLU, 2 ReLU."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_eval_f32(f, P(x), P(y), x.size)
+    return y
+
+
+def vec_frecpe(x):
+    f = lib().orc_frecpe
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32)],
+                    np.float32)
+
+
+def vec_silu(x):
+    f = lib().orc_silu_f32
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32)],
+                    np.float32)
+
+
+def quant_rows(x, K, Kp, gate=None):
+    """orc_s8n_quant_rows over all rows of x [M][ld] -> (q [M][Kp], sa, za)."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, ld = x.shape
+    q = np.zeros((M, Kp), np.int8)
+    sa = np.zeros(M, np.float32)
+    za = np.zeros(M, np.int32)
+    if gate is None:
+        lib().orc_s8n_quant_rows(P(x), ld, 0, M, K, Kp, P(q), P(sa), P(za))
+    else:
+        gate = np.ascontiguousarray(gate, np.float32)
+        lib().orc_s8n_quant_rows_gate(P(x), ld, 0, M, K, Kp, P(gate), P(q),
+                                      P(sa), P(za))
+    return q, sa, za
+
+
+def pw_s8(x, pk, act=0, out_rows=None, ldo=None, ow=0, opad=0, res=None,
+          ldr=0, rpad=0, rw=0, gate=None):
+    """The PW_S8 op of one window on the oracle.
+
+    Args:
+        x: f32 [M][lda] input rows.
+        pk: s8pack.pack_s8 dict.
+        out_rows: rows of the output buffer (M, or the padded pixel count).
+    Returns:
+        (out, q, sa, za) host arrays.
+    """
+    x = np.ascontiguousarray(x, np.float32)
+    M, lda = x.shape
+    N, K, Kp, Np = pk["shape"]
+    ldo = ldo or Np
+    M4 = (M + 3) // 4 * 4
+    if out_rows is None:
+        out_rows = M if not opad else (M // ow + 2 * opad) * (ow + 2 * opad)
+    out = np.zeros((out_rows, ldo), np.float32)
+    q = np.zeros((M4, Kp), np.int8)
+    sa = np.zeros(M4, np.float32)
+    za = np.zeros(M4, np.int32)
+    res_a = None if res is None else np.ascontiguousarray(res, np.float32)
+    e = OrcEpi32(act, out.ctypes.data, ldo, ow, opad, P(res_a), ldr, rpad, rw)
+    g = None if gate is None else np.ascontiguousarray(gate, np.float32)
+    lib().orc_pw_s8(P(x), lda, M, K, Kp, N, Np, P(g), P(q), P(sa), P(za),
+                    P(pk["q"]), P(pk["sw"]), P(pk["cs"]), P(pk["b"]), C.byref(e))
+    return out, q, sa, za
+
+
+def gemm_s8_requant(w, x, bias, mult, shift, zx, zy, lo=-128, hi=127):
+    w = np.ascontiguousarray(w, np.int8)
+    x = np.ascontiguousarray(x, np.int8)
+    N, K = w.shape
+    M = x.shape[1]
+    out = np.zeros((N, M), np.int8)
+    b = np.ascontiguousarray(bias, np.int32)
+    m = np.ascontiguousarray(mult, np.int32)
+    s = np.ascontiguousarray(shift, np.int32)
+    lib().orc_gemm_s8_requant(P(w), P(x), P(b), P(m), P(s), N, K, M, zx, zy,
+                              lo, hi, P(out))
+    return out

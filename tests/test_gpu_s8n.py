@@ -1,0 +1,240 @@
+"""GPU parity of the int8 pointwise GEMMs against the CPU oracle: bit-exact.
+
+libbnneon_hip (through its C ABI) vs oracle/s8n.c on the same seeded inputs:
+the device numerics (FRECPE, SiLU, ReLU) on exhaustive / adversarial inputs,
+per-row quantization (every K tail form, constant / zero / huge-offset / NaN
+rows, the SE gate), the whole PW_S8 op (activations, residual, zero-haloed
+output, batches of windows with padded strides) and the Q31-requantised NCHW
+GEMM at the 1152 -> 256, 24 x 64 pixel shape.
+"""
+import numpy as np
+import pytest
+
+import pyoracle as O
+from bnneon import s8pack
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def same_f32(a, b):
+    """Bit equality, any NaN equal to any NaN."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    an, bn = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(an, bn) and
+                np.array_equal(a.view(np.uint32)[~an], b.view(np.uint32)[~bn]))
+
+
+def adversarial_floats(rng, n):
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45,
+                        1.17e-38, 2.0 ** -127, 2.0 ** -128, 2.0 ** -129,
+                        3.4e38, -3.4e38, 41.6, 41.59, -41.6, 60.0, -60.0,
+                        86.5, -87.3, 1.0, -1.0, 0.5], np.float32)
+    bitsr = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32)
+    return np.concatenate([special, bitsr.view(np.float32),
+                           rng.standard_normal(n).astype(np.float32) * 8])
+
+
+def run_eval(H, f, x):
+    d = H.DeviceArray.from_host(x)
+    y = H.DeviceArray.zeros(x.shape, np.float32)
+    H.check(H.lib().bnh_eval_f32(f, d.ptr, y.ptr, x.size, None), "eval")
+    H.sync()
+    return y.numpy()
+
+
+def test_frecpe_every_significand_and_exponent(hip):
+    # all 2^23 significands of [1, 2) and a spread of exponents incl. denormals
+    sig = np.arange(2 ** 23, dtype=np.uint32) | np.uint32(127 << 23)
+    xs = [sig.view(np.float32)]
+    rng = np.random.default_rng(0)
+    for e in list(range(0, 255, 3)) + [1, 2, 253, 254]:
+        s = rng.integers(0, 2 ** 23, 4096, dtype=np.uint64).astype(np.uint32)
+        xs.append(((s | np.uint32(e << 23)) | np.uint32(rng.integers(0, 2) << 31)).view(np.float32))
+    x = np.concatenate(xs + [adversarial_floats(rng, 4096)])
+    say("frecpe", x.size)
+    assert same_f32(run_eval(hip, 0, x), O.eval_f32(0, x))
+
+
+@pytest.mark.parametrize("f", [1, 2])
+def test_silu_relu_bit_exact(hip, f):
+    rng = np.random.default_rng(1)
+    x = np.concatenate([adversarial_floats(rng, 200000),
+                        np.linspace(-100, 100, 200001).astype(np.float32)])
+    say("eval", f, x.size)
+    assert same_f32(run_eval(hip, f, x), O.eval_f32(f, x))
+
+
+def quant_case(hip, x, K, Kp, gate=None, B=1):
+    """x [B][M][ld]; returns True when q, sa, za match the oracle."""
+    H = hip
+    B, M, ld = x.shape
+    M4 = (M + 3) // 4 * 4
+    q_ws = M4 * Kp + 64          # padded per-window strides
+    s_ws = M4 + 8
+    x_ws = M * ld + 32
+    xh = np.zeros((B, x_ws), np.float32)
+    xh[:, :M * ld] = x.reshape(B, -1)
+    dx = H.DeviceArray.from_host(xh)
+    dq = H.DeviceArray.zeros((B, q_ws), np.int8)
+    dsa = H.DeviceArray.zeros((B, s_ws), np.float32)
+    dza = H.DeviceArray.zeros((B, s_ws), np.int32)
+    dg, g_ws = None, 0
+    if gate is not None:
+        g_ws = K + 4
+        gh = np.zeros((B, g_ws), np.float32)
+        gh[:, :K] = gate
+        dg = H.DeviceArray.from_host(gh)
+    H.check(H.lib().bnh_s8n_quant_rows(dx.ptr, x_ws, ld, M, K, Kp, H.ptr(dg), g_ws,
+                                       dq.ptr, q_ws, dsa.ptr, dza.ptr, s_ws, B, None), "quant")
+    H.sync()
+    q, sa, za = dq.numpy(), dsa.numpy(), dza.numpy()
+    ok = True
+    for b in range(B):
+        oq, osa, oza = O.quant_rows(x[b], K, Kp, None if gate is None else gate[b])
+        ok &= np.array_equal(q[b, :M * Kp].reshape(M, Kp), oq)
+        ok &= same_f32(sa[b, :M], osa) and np.array_equal(za[b, :M], oza)
+    return ok
+
+
+@pytest.mark.parametrize("K", [1, 3, 4, 7, 8, 13, 24, 40, 144, 816, 1152, 1392])
+def test_quant_rows_random(hip, K):
+    rng = np.random.default_rng(K)
+    Kp = s8pack.r16(K)
+    B, M = 3, 37
+    ld = K + (K % 3)
+    x = (rng.standard_normal((B, M, ld)) * rng.uniform(1e-3, 1e3, (B, M, 1))
+         + rng.uniform(-10, 10, (B, M, 1))).astype(np.float32)
+    say("quant K", K)
+    assert quant_case(hip, x, K, Kp)
+
+
+def test_quant_rows_edge_rows(hip):
+    rng = np.random.default_rng(11)
+    K, Kp, M = 21, 32, 12   # K % 4 = 1 and K % 8 = 5: both tail forms
+    x = rng.standard_normal((1, M, K)).astype(np.float32)
+    x[0, 0] = 3.25                      # constant row
+    x[0, 1] = 0.0                       # zero row
+    x[0, 2] = 1e10 + rng.uniform(0, 1e3, K)   # far offset: out-of-range conversions
+    x[0, 3, 5] = np.nan                 # NaN in the 4-lane part
+    x[0, 4, 20] = np.nan                # NaN in the scalar tail
+    x[0, 5, 2] = np.inf
+    x[0, 6] = -1e-40                    # denormal constant row
+    x[0, 7, :] = rng.standard_normal(K) * 1e-38
+    x[0, 8, 0] = -3e38
+    x[0, 8, 1] = 3e38                   # range overflows to inf
+    say("quant edge rows")
+    assert quant_case(hip, x, K, Kp)
+
+
+def test_quant_rows_gate(hip):
+    rng = np.random.default_rng(12)
+    K, Kp, M, B = 96, 96, 29, 2
+    x = rng.standard_normal((B, M, K)).astype(np.float32)
+    g = rng.uniform(0, 1, (B, K)).astype(np.float32)
+    say("quant gate")
+    assert quant_case(hip, x, K, Kp, gate=g)
+
+
+def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, gate=False):
+    H = hip
+    rng = np.random.default_rng(seed)
+    M = H_ * W_
+    lda = K + lda_extra
+    w = (rng.standard_normal((N, K)) * rng.uniform(0.01, 1, (N, 1))).astype(np.float32)
+    w[0] = 0                                  # an all-zero channel
+    b = rng.standard_normal(N).astype(np.float32)
+    pk = s8pack.pack_s8(w, b)
+    N_, K_, Kp, Np = pk["shape"]
+    x = (rng.standard_normal((B, M, lda)) * 2).astype(np.float32)
+    gt = rng.uniform(0, 1, (B, K)).astype(np.float32) if gate else None
+    ldo = Np + 8
+    out_rows = M if not opad else (H_ + 2 * opad) * (W_ + 2 * opad)
+    rs = rng.standard_normal((B, M, Np)).astype(np.float32) if res else None
+    M4 = (M + 3) // 4 * 4
+    Wt = H.S8Weights(N_, K_, Kp, Np, pk["q"], pk["sw"], pk["cs"], pk["b"])
+    dx = H.DeviceArray.from_host(x)
+    dg = H.DeviceArray.from_host(gt) if gate else None
+    dq = H.DeviceArray.zeros((B, M4 * Kp), np.int8)
+    dsa = H.DeviceArray.zeros((B, M4), np.float32)
+    dza = H.DeviceArray.zeros((B, M4), np.int32)
+    # the output starts as garbage: the halo must be zeroed by the op
+    dout = H.DeviceArray.from_host(np.full((B, out_rows * ldo), 7.0, np.float32))
+    dres = H.DeviceArray.from_host(rs) if res else None
+    e = H.epi32(dout, ldo, act=act, ow=W_ if opad else 0, opad=opad, res=dres,
+                ldr=Np if res else 0, out_ws=out_rows * ldo, res_ws=M * Np)
+    say(f"pw_s8 B{B} {H_}x{W_} K{K} N{N} act{act} opad{opad} res{res} gate{gate}")
+    H.check(H.lib().bnh_pw_s8(dx.ptr, M * lda, lda, M, H.ptr(dg), K if gate else 0, dq.ptr, M4 * Kp,
+                              dsa.ptr, dza.ptr, M4, B, Wt.h, e, None), "pw_s8")
+    H.sync()
+    out = dout.numpy().reshape(B, out_rows, ldo)
+    q = dq.numpy().reshape(B, M4, Kp)
+    ok = True
+    for bi in range(B):
+        ref_out, rq, rsa, rza = O.pw_s8(x[bi], pk, act=act, ldo=ldo, ow=W_ if opad else 0, opad=opad,
+                                        res=None if rs is None else rs[bi], ldr=Np if res else 0,
+                                        gate=None if gt is None else gt[bi])
+        got = out[bi].copy()
+        # columns [Np, ldo) are never written: the garbage stays, as in the reference
+        ok &= same_f32(got[:, :Np], ref_out[:, :Np])
+        ok &= np.array_equal(q[bi, :M], rq[:M])
+    return ok
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_pw_s8_perch_shapes(hip, act):
+    for (H_, W_, K, N) in ((25, 13, 40, 24), (13, 8, 144, 32), (8, 8, 1392, 232), (4, 4, 232, 1392)):
+        assert pw_case(hip, 2, H_, W_, K, N, act, seed=H_ * K + act)
+
+
+def test_pw_s8_config0_shape(hip):
+    assert pw_case(hip, 2, 24, 64, 1152, 256, 1, seed=5)
+
+
+def test_pw_s8_residual_halo_gate(hip):
+    assert pw_case(hip, 3, 7, 9, 48, 40, 1, opad=2, res=True, lda_extra=5, seed=9)
+    assert pw_case(hip, 2, 5, 6, 96, 136, 2, opad=1, seed=10, gate=True)
+    assert pw_case(hip, 1, 1, 1, 24, 8, 0, seed=11)   # a single row (GEMV-like)
+
+
+def test_gemm_requant_config0(hip):
+    H = hip
+    rng = np.random.default_rng(2024)
+    N, K, M, B = 256, 1152, 1536, 2
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    x = np.clip(np.round(rng.normal(-40, 35, (B, K, M))), -128, 127).astype(np.int8)
+    bias = rng.integers(-2 ** 14, 2 ** 14 + 1, N).astype(np.int32)
+    mult = rng.integers(2 ** 30, 2 ** 31, N).astype(np.int32)
+    shift = rng.integers(6, 11, N).astype(np.int32)
+    Wq = H.Q8Weights(w, bias, mult, shift, -128, -128)
+    dx = H.DeviceArray.from_host(x)
+    dout = H.DeviceArray.zeros((B, N, M), np.int8)
+    say("requant gemm config0 B2")
+    H.check(H.lib().bnh_gemm_s8_requant(Wq.h, dx.ptr, K * M, M, B, dout.ptr, N * M, None), "requant")
+    H.sync()
+    got = dout.numpy()
+    for b in range(B):
+        ref = O.gemm_s8_requant(w, x[b], bias, mult, shift, -128, -128)
+        assert np.array_equal(got[b], ref), (b, np.argwhere(got[b] != ref)[:5])
+
+
+def test_gemm_requant_small_shapes(hip):
+    H = hip
+    rng = np.random.default_rng(7)
+    for (N, K, M) in ((8, 16, 4), (24, 48, 68), (136, 144, 132), (300, 80, 256)):
+        w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+        x = rng.integers(-128, 128, (1, K, M)).astype(np.int8)
+        bias = rng.integers(-2 ** 20, 2 ** 20, N).astype(np.int32)
+        mult = rng.integers(2 ** 30, 2 ** 31, N).astype(np.int32)
+        shift = rng.integers(0, 16, N).astype(np.int32)
+        Wq = H.Q8Weights(w, bias, mult, shift, 3, -5, -100, 90)
+        dx = H.DeviceArray.from_host(x)
+        dout = H.DeviceArray.zeros((N, M), np.int8)
+        say("requant", N, K, M)
+        H.check(H.lib().bnh_gemm_s8_requant(Wq.h, dx.ptr, K * M, M, 1, dout.ptr, N * M, None), "requant")
+        H.sync()
+        assert np.array_equal(dout.numpy(), O.gemm_s8_requant(w, x[0], bias, mult, shift, 3, -5, -100, 90))
