@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=256)
     ap.add_argument("--workload", default="gemm_s8_requant",
-                    choices=["gemm_s8_requant", "pw_s8"])
+                    choices=["gemm_s8_requant", "pw_s8", "copy"])
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     return ap.parse_args()
@@ -129,6 +129,18 @@ def main():
     B = a.batch
     N, K, M = 256, 1152, 1536
     stream = H.lib().bnh_stream_new()
+    if a.workload == "copy":
+        # calibration: a plain 1 GiB device-to-device copy (the achievable HBM
+        # rate, and the reference for the FETCH_SIZE / WRITE_SIZE counters)
+        nbytes = 1 << 30
+        src = H.DeviceArray.zeros(nbytes, np.uint8)
+        dst = H.DeviceArray.zeros(nbytes, np.uint8)
+        ms, wall = time_steps(H, stream, lambda: H.check(H.lib().bnh_copy(dst.ptr, src.ptr, nbytes, stream)),
+                              a.steps, a.warmup)
+        print(json.dumps({"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
+                          "ms_per_copy": round(ms, 4), "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}),
+              flush=True)
+        return
     if a.workload == "gemm_s8_requant":
         w, x, bias, mult, shift = config0_inputs(rng, B)
         Wq = H.Q8Weights(w, bias, mult, shift, -128, -128)
@@ -158,7 +170,7 @@ def main():
         e = H.epi32(dout, Np, act=1, out_ws=M * Np)
 
         def launch():
-            H.check(H.lib().bnh_pw_s8(dx.ptr, M * K, K, M, None, 0, dq.ptr, M * Kp, dsa.ptr, dza.ptr,
+            H.check(H.lib().bnh_pw_s8(dx.ptr, M * K, K, M, None, 0, dq.ptr, M * Kp, dsa.ptr, M, dza.ptr,
                                       M, B, Wt.h, e, stream))
         # quantize (read fp32 rows, write q) + GEMM (read q, write fp32 out)
         bytes_per_launch = B * M * (4 * K + 2 * Kp + 4 * Np) + Np * Kp

@@ -43,14 +43,22 @@ _SIGS = {
     "bnh_event_record": (i32, [vp, vp]),
     "bnh_event_ms": (C.c_float, [vp, vp]),
     "bnh_eval_f32": (i32, [i32, vp, vp, i64, vp]),
+    "bnh_copy": (i32, [vp, vp, C.c_size_t, vp]),
     "bnh_s8w_new": (vp, [i32, i32, i32, i32, vp, vp, vp, vp]),
     "bnh_s8w_free": (None, [vp]),
     "bnh_s8n_quant_rows": (i32, [vp, i64, i32, i32, i32, i32, vp, i64, vp,
-                                 i64, vp, vp, i64, i32, vp]),
-    "bnh_s8n_gemm": (i32, [vp, i64, vp, vp, i64, i32, i32, vp,
+                                 i64, vp, i64, vp, i64, i32, vp]),
+    "bnh_s8n_gemm": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, vp,
                            C.POINTER(Epi32), vp]),
-    "bnh_pw_s8": (i32, [vp, i64, i32, i32, vp, i64, vp, i64, vp, vp, i64,
-                        i32, vp, C.POINTER(Epi32), vp]),
+    "bnh_pw_s8": (i32, [vp, i64, i32, i32, vp, i64, vp, i64, vp, i64, vp,
+                        i64, i32, vp, C.POINTER(Epi32), vp]),
+    "bnh_s8p_new": (vp, [i32, i32, vp, vp]),
+    "bnh_s8p_free": (None, [vp]),
+    "bnh_quant_cells": (i32, [vp, i64, i32, i32, i32, C.c_float, vp, i64, i32,
+                              vp, i64, i32, vp]),
+    "bnh_proto_colmax": (i32, [vp, i64, vp, i64, i32, vp, vp, i64, i32, vp]),
+    "bnh_proto_logits": (i32, [vp, i64, vp, vp, i32, i32, vp, i64, i32, vp,
+                               i32, vp]),
     "bnh_q8w_new": (vp, [i32, i32, vp, vp, vp, vp, i32, i32, i32, i32]),
     "bnh_q8w_free": (None, [vp]),
     "bnh_gemm_s8_requant": (i32, [vp, vp, i64, i32, i32, vp, i64, vp]),

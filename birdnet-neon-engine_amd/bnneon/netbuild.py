@@ -1,0 +1,129 @@
+"""Builds .bnpk packages of synthetic networks from int8 / fp32 / fp16 ops.
+
+The op records are the ones libbnneon's compiler emits for these layers
+(python/bnneon/compiler/lower.py: pw :787-823 with s8_tensors :883-914,
+l_dwconv :916-951; the PROTO_S8 and GEMV_S8 records of src/rt_ops_s8n.c:92-253),
+so a package built here is a valid package for the reference library too.
+Every buffer gets its own memory slot (no lifetime sharing): simple and safe.
+"""
+import hashlib
+
+import numpy as np
+
+from . import pkgfmt, s8pack
+
+F32, F16, I8, I32 = 0, 1, 2, 3
+HW_FP16 = 1
+OP = {"PW": 3, "DW3": 4, "SE": 5, "FE_LOGMEL": 8, "STEM": 9, "DWK": 10,
+      "PAD": 11, "MEAN": 12, "GEMV": 15, "PW_S8": 22, "GEMV_S8": 23,
+      "SE_GATE": 25, "PROTO_S8": 35}
+ACT = {None: 0, "none": 0, "silu": 1, "relu": 2}
+
+
+class Net:
+    """One path of a package: buffers, op records and tensors."""
+
+    def __init__(self, pkg=None, prefix=""):
+        self.pkg = pkg or pkgfmt.Package()
+        self.prefix = prefix
+        self.bufs = []   # (dtype, H, W, C, ld, halo, elems, slot)
+        self.ops = []
+        self.k = 0
+        self.last = None   # the output buffer of the last op emitted
+
+    def buf(self, dtype, H, W, C, ld=None, halo=0, elems=None):
+        ld = C if ld is None else ld
+        if elems is None:
+            elems = (H + 2 * halo) * (W + 2 * halo) * ld
+        self.bufs.append((dtype, H, W, C, ld, halo, int(elems), len(self.bufs)))
+        return len(self.bufs) - 1
+
+    def tensor(self, name, a):
+        self.k += 1
+        return self.pkg.tensor(f"{self.prefix}{name}.{self.k}", a)
+
+    def emit(self, code, b, t, p, var=0):
+        self.ops.append((code | (var << 8), list(b), list(t), [int(x) for x in p]))
+
+    # ---------------------------------------------------------------- int8 ops
+    def pw_s8(self, ib, w, b, act=None, H=None, W=None, opad=0, res=-1, gate=-1):
+        """A 1x1 conv on rows of buffer ib (NHWC, no halo): PW_S8."""
+        d = self.bufs[ib]
+        H = d[1] if H is None else H
+        W = d[2] if W is None else W
+        M, lda = H * W, d[4]
+        pk = s8pack.pack_s8(np.asarray(w, np.float32), np.asarray(b, np.float32))
+        N, K, Kp, Np = pk["shape"]
+        tl = [self.tensor("s8n/pw.q", pk["q"]), self.tensor("s8n/pw.sw", pk["sw"]),
+              self.tensor("s8n/pw.cs", pk["cs"]), self.tensor("s8n/pw.b", pk["b"])]
+        ob = self.buf(F32, H, W, N, ld=Np, halo=opad)
+        m4 = (M + 3) // 4 * 4
+        qb = self.buf(I8, m4, 1, Kp)
+        sb = self.buf(F32, m4, 1, 1)
+        zb = self.buf(I32, m4, 1, 1)
+        ldr = self.bufs[res][4] if res >= 0 else 0
+        bl = [ib, ob, res, qb, sb, zb] + ([gate] if gate >= 0 else [])
+        self.emit(OP["PW_S8"], bl, tl, [N, K, Kp, Np, M, lda, ACT[act], Np,
+                                        W if opad else W, opad, ldr])
+        self.last = ob
+        return ob
+
+    def gemv_s8(self, ib, w, b, act=None):
+        pk = s8pack.pack_s8(np.asarray(w, np.float32), np.asarray(b, np.float32))
+        N, K, Kp, Np = pk["shape"]
+        tl = [self.tensor("s8n/lin.q", pk["q"]), self.tensor("s8n/lin.sw", pk["sw"]),
+              self.tensor("s8n/lin.cs", pk["cs"]), self.tensor("s8n/lin.b", pk["b"])]
+        ob = self.buf(F32, 1, 1, N, ld=Np, elems=Np)
+        qb = self.buf(I8, 4, 1, Kp)
+        sb = self.buf(F32, 4, 1, 1)
+        zb = self.buf(I32, 4, 1, 1)
+        self.emit(OP["GEMV_S8"], [ib, ob, qb, sb, zb], tl, [N, K, Kp, Np, ACT[act]])
+        self.last = ob
+        return ob
+
+    def proto_s8(self, ib, protos, clsw, clsb, eps=1e-5, n4=None):
+        """ProtoPNet head on cells [P][C] of buffer ib: int8 prototypes."""
+        d = self.bufs[ib]
+        P, C, ld = d[1] * d[2], d[3], d[4]
+        protos = np.asarray(protos, np.float32)
+        N, K = protos.shape
+        Kp, Np = s8pack.r16(K), (N + 3) // 4 * 4
+        q, sw = s8pack.quant_rows_s8(protos)
+        qp = np.zeros((Np, Kp), np.int8)
+        qp[:N, :K] = q
+        swp = np.zeros(Np, np.float32)
+        swp[:N] = sw
+        flags = s8pack.n4_panel_flags(qp) if n4 is None else np.asarray(n4, np.int8)
+        nc = len(clsb)
+        ppc = N // nc
+        tl = [self.tensor("s8n/proto.q", s8pack.pack_panels(qp)), self.tensor("s8n/proto.sw", swp),
+              self.tensor("s8n/proto.n4", flags), self.tensor("proto.clsw", np.asarray(clsw, np.float32).reshape(nc, ppc)),
+              self.tensor("proto.clsb", np.asarray(clsb, np.float32)), self.tensor("proto.eps", np.array([eps], np.float32))]
+        ob = self.buf(F32, 1, 1, nc)
+        qb = self.buf(I8, P, 1, Kp)
+        cb = self.buf(F32, 1, 1, Np)
+        self.emit(OP["PROTO_S8"], [ib, ob, qb, cb], tl, [N, K, Kp, Np, P, C, ld, nc, ppc])
+        self.last = ob
+        return ob
+
+    def add_to(self, name="neon-int8", hwcap=0, in_buf=0, out_buf=None, emb_buf=None):
+        self.pkg.add_path(name, hwcap, self.bufs, self.ops, in_buf,
+                          self.last if out_buf is None else out_buf, emb_buf)
+
+
+def standard_meta(pkg, n_samples, n_classes, sample_rate=32000, family=120,
+                  model_id="synthetic", emb_dim=0, labels=None, post=1):
+    pkg.set("format_version", 1)
+    pkg.set("family", family)
+    pkg.set("model_id", model_id)
+    pkg.set("sample_rate", sample_rate)
+    pkg.set("n_samples", n_samples)
+    pkg.set("hop_samples", 0)
+    pkg.set("n_classes", n_classes)
+    pkg.set("post", post)
+    pkg.set("emb_dim", emb_dim)
+    pkg.set("license", "synthetic weights, no license")
+    pkg.set("compiler", "bnneon.netbuild")
+    if labels is not None:
+        pkg.set("labels", labels)
+        pkg.set("labels_sha256", hashlib.sha256(labels).digest())

@@ -19,12 +19,19 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libbnneon_hip.so")
 
 SOURCES = [
-    "device.cpp",
+    "device.hip",
     "kern_s8n.hip",
     "kern_proto.hip",
     "kern_dw.hip",
     "kern_wino.hip",
     "kern_f16.hip",
+    "rt_pkg.cpp",
+    "ops_table.cpp",
+    "ops_s8n.cpp",
+    "ops_proto.cpp",
+    "ops_f32.cpp",
+    "ops_f16.cpp",
+    "bnneon.cpp",
 ]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -1,4 +1,5 @@
-// Device plumbing of the kernel-level C ABI: errors, memory, streams, events, and the numerics probe.
+// Device plumbing of the kernel-level C ABI: errors, memory, streams, events, and a streaming copy kernel (the
+// bandwidth / counter calibration reference).
 #include <string.h>
 
 #include "bnh_internal.h"
@@ -14,9 +15,27 @@ int bnh_fail(const char *fmt, ...) {
 }
 void bnh_clear_error(void) { g_err[0] = 0; }
 
+// 16 bytes per thread per step, grid-stride: reads and writes each byte once
+__global__ void k_copy16(const uint4 *__restrict__ src, uint4 *__restrict__ dst, long long n16) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (long long)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
 extern "C" {
 
 const char *bnh_last_error(void) { return g_err; }
+
+int bnh_copy(void *dst, const void *src, size_t bytes, void *stream) {
+  BNH_REQ(dst && src && bytes % 16 == 0 && ((uintptr_t)dst & 15) == 0 && ((uintptr_t)src & 15) == 0);
+  const long long n16 = (long long)(bytes / 16);
+  long long blocks = bnh_ceil_div(n16, 256);
+  if (blocks > 256 * 64) blocks = 256 * 64;
+  if (!n16) return 0;
+  hipLaunchKernelGGL(k_copy16, dim3((unsigned)blocks), dim3(256), 0, bnh_stream(stream), (const uint4 *)src, (uint4 *)dst,
+                     n16);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
 
 int bnh_device_count(void) {
   int n = 0;

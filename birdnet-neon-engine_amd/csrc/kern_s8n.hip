@@ -56,7 +56,8 @@ BNH_DEV long long epi_orow(int m, int ow, int opad) {
 __global__ __launch_bounds__(256) void k_s8n_quant(const float *__restrict__ x, long long x_ws, int ld, int M, int K,
                                                    int Kp, const float *__restrict__ gate, long long g_ws,
                                                    int8_t *__restrict__ q, long long q_ws, float *__restrict__ sa,
-                                                   int32_t *__restrict__ za, long long s_ws, long long rows) {
+                                                   long long sa_ws, int32_t *__restrict__ za, long long za_ws,
+                                                   long long rows) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -95,8 +96,8 @@ __global__ __launch_bounds__(256) void k_s8n_quant(const float *__restrict__ x, 
     s = range / 254.f;
   }
   if (lane == 0) {
-    sa[w * s_ws + m] = s;
-    za[w * s_ws + m] = z;
+    sa[w * sa_ws + m] = s;
+    za[w * za_ws + m] = z;
   }
   int8_t *o = q + w * q_ws + (long long)m * Kp;
   const uint32_t zb = (uint32_t)z & 0xffu;
@@ -138,8 +139,8 @@ __global__ void k_zero_halo_f32(float *__restrict__ out, long long ws, int H, in
 // ------------------------------------------------------------------ int8 GEMM + fp32 dequant epilogue
 template <int WM, int WN>
 __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, long long q_ws,
-                                                  const float *__restrict__ sa, const int32_t *__restrict__ za,
-                                                  long long s_ws, int M, long long rows,
+                                                  const float *__restrict__ sa, long long sa_ws,
+                                                  const int32_t *__restrict__ za, long long za_ws, int M, long long rows,
                                                   const int8_t *__restrict__ wt, const float *__restrict__ sw,
                                                   const int32_t *__restrict__ cs, const float *__restrict__ bias,
                                                   int Kp, int Np, EpiDev e) {
@@ -205,8 +206,8 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
       const long long row = row0 + 16 * t + 4 * (lane >> 4) + r;
       if (row >= rows) continue;
       const int w = (int)(row / M), m = (int)(row % M);
-      const float s_a = sa[w * s_ws + m];
-      const uint32_t z = (uint32_t)za[w * s_ws + m];
+      const float s_a = sa[w * sa_ws + m];
+      const uint32_t z = (uint32_t)za[w * za_ws + m];
       float *orow = e.out + w * e.out_ws + epi_orow(m, e.ow, e.opad) * e.ldo;
       const float *rrow = e.res ? e.res + w * e.res_ws + epi_orow(m, e.rw, e.rpad) * e.ldr : nullptr;
 #pragma unroll
@@ -373,24 +374,24 @@ bnh_s8w *bnh_s8w_new(int N, int K, int Kp, int Np, const int8_t *w, const float 
 
 void bnh_s8w_free(bnh_s8w *W) {
   if (!W) return;
-  if (W->w) hipFree(W->w);
-  if (W->sw) hipFree(W->sw);
-  if (W->b) hipFree(W->b);
-  if (W->colsum) hipFree(W->colsum);
+  if (W->w) (void)hipFree(W->w);
+  if (W->sw) (void)hipFree(W->sw);
+  if (W->b) (void)hipFree(W->b);
+  if (W->colsum) (void)hipFree(W->colsum);
   free(W);
 }
 
 int bnh_s8n_quant_rows(const float *x, long long x_ws, int ld, int M, int K, int Kp, const float *gate,
-                       long long gate_ws, int8_t *q, long long q_ws, float *sa, int32_t *za, long long s_ws, int B,
-                       void *stream) {
+                       long long gate_ws, int8_t *q, long long q_ws, float *sa, long long sa_ws, int32_t *za,
+                       long long za_ws, int B, void *stream) {
   BNH_REQ(x && q && sa && za && M > 0 && K > 0 && B > 0);
   BNH_REQ(Kp == ((K + 15) & ~15) && ld >= K);
   BNH_REQ(!gate || (K % 4 == 0 && K <= 4096));
   BNH_REQ(((uintptr_t)q & 3) == 0 && q_ws % 4 == 0 && (B == 1 || q_ws >= (long long)M * Kp));
-  BNH_REQ(B == 1 || (x_ws >= (long long)(M - 1) * ld + K && s_ws >= M));
+  BNH_REQ(B == 1 || (x_ws >= (long long)(M - 1) * ld + K && sa_ws >= M && za_ws >= M));
   const long long rows = (long long)M * B;
   hipLaunchKernelGGL(k_s8n_quant, dim3((unsigned)bnh_ceil_div(rows, 4)), dim3(256), 0, bnh_stream(stream), x, x_ws, ld,
-                     M, K, Kp, gate, gate_ws, q, q_ws, sa, za, s_ws, rows);
+                     M, K, Kp, gate, gate_ws, q, q_ws, sa, sa_ws, za, za_ws, rows);
   BNH_HIP(hipGetLastError());
   return 0;
 }
@@ -403,8 +404,8 @@ static int check_epi(const bnh_epi32 *e, int M, int Np, int B) {
   return 0;
 }
 
-int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, const int32_t *za, long long s_ws, int M, int B,
-                 const bnh_s8w *W, const bnh_epi32 *e, void *stream) {
+int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, long long sa_ws, const int32_t *za, long long za_ws,
+                 int M, int B, const bnh_s8w *W, const bnh_epi32 *e, void *stream) {
   BNH_REQ(q && sa && za && W && M > 0 && B > 0);
   BNH_REQ(((uintptr_t)q & 15) == 0 && q_ws % 16 == 0);
   if (check_epi(e, M, W->Np, B)) return -1;
@@ -413,11 +414,11 @@ int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, const int32_t
   hipStream_t s = bnh_stream(stream);
   if (W->Np > 64) {
     dim3 grid((unsigned)bnh_ceil_div(rows, 64), (unsigned)bnh_ceil_div(W->Np, 128));
-    hipLaunchKernelGGL((k_s8n_gemm<2, 2>), grid, dim3(256), 0, s, q, q_ws, sa, za, s_ws, M, rows, W->w, W->sw,
+    hipLaunchKernelGGL((k_s8n_gemm<2, 2>), grid, dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rows, W->w, W->sw,
                        W->colsum, W->b, W->Kp, W->Np, d);
   } else {
     dim3 grid((unsigned)bnh_ceil_div(rows, 128), 1);
-    hipLaunchKernelGGL((k_s8n_gemm<4, 1>), grid, dim3(256), 0, s, q, q_ws, sa, za, s_ws, M, rows, W->w, W->sw,
+    hipLaunchKernelGGL((k_s8n_gemm<4, 1>), grid, dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rows, W->w, W->sw,
                        W->colsum, W->b, W->Kp, W->Np, d);
   }
   BNH_HIP(hipGetLastError());
@@ -425,8 +426,8 @@ int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, const int32_t
 }
 
 int bnh_pw_s8(const float *in, long long in_ws, int lda, int M, const float *gate, long long gate_ws, int8_t *q,
-              long long q_ws, float *sa, int32_t *za, long long s_ws, int B, const bnh_s8w *W, const bnh_epi32 *e,
-              void *stream) {
+              long long q_ws, float *sa, long long sa_ws, int32_t *za, long long za_ws, int B, const bnh_s8w *W,
+              const bnh_epi32 *e, void *stream) {
   BNH_REQ(W && e && e->out);
   if (check_epi(e, M, W->Np, B)) return -1;
   if (e->opad) {
@@ -437,8 +438,9 @@ int bnh_pw_s8(const float *in, long long in_ws, int lda, int M, const float *gat
                        e->out, B == 1 ? per : e->out_ws, H, Wd, e->ldo, h, total);
     BNH_HIP(hipGetLastError());
   }
-  if (bnh_s8n_quant_rows(in, in_ws, lda, M, W->K, W->Kp, gate, gate_ws, q, q_ws, sa, za, s_ws, B, stream)) return -1;
-  return bnh_s8n_gemm(q, q_ws, sa, za, s_ws, M, B, W, e, stream);
+  if (bnh_s8n_quant_rows(in, in_ws, lda, M, W->K, W->Kp, gate, gate_ws, q, q_ws, sa, sa_ws, za, za_ws, B, stream))
+    return -1;
+  return bnh_s8n_gemm(q, q_ws, sa, sa_ws, za, za_ws, M, B, W, e, stream);
 }
 
 bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const int32_t *mult, const int32_t *shift,
@@ -482,10 +484,10 @@ bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const i
 
 void bnh_q8w_free(bnh_q8w *W) {
   if (!W) return;
-  if (W->w) hipFree(W->w);
-  if (W->bias_eff) hipFree(W->bias_eff);
-  if (W->mult) hipFree(W->mult);
-  if (W->shift) hipFree(W->shift);
+  if (W->w) (void)hipFree(W->w);
+  if (W->bias_eff) (void)hipFree(W->bias_eff);
+  if (W->mult) (void)hipFree(W->mult);
+  if (W->shift) (void)hipFree(W->shift);
   free(W);
 }
 

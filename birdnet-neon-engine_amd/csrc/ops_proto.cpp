@@ -1,0 +1,119 @@
+// PROTO_S8: the int8 prototype head's op contract (src/rt_ops_s8n.c:212-253 with rt_proto_geom / rt_proto_io,
+// src/rt_ops_f32.c:525-546), run on the GPU for a batch of windows.
+//   b = [x f32 [P][ld], logits f32 [nc], qa i8 [P][Kp], colmax f32 [Np]];
+//   t = [qw i8 [Np/4][Kp/16][4][16], sw f32 [Np], n4 i8 [Np/4], cls w [nc][ppc], cls b [nc], eps [1]];
+//   p = [N K Kp Np, P C ld nc ppc]
+#include <stdlib.h>
+#include <string.h>
+
+#include "bnh_internal.h"
+#include "rt.h"
+
+
+
+typedef struct {
+  bnh_s8p *W;
+  float *clsw, *clsb;  // device copies of the class tensors
+  float eps;
+  float *sx;           // device [bcap][P] cell scales (op-private scratch)
+  int sx_cap;
+} proto_state;
+
+// the geometry of a prototype head (rt_proto_geom): P cells of C channels (row stride ld), N = nc * ppc prototypes
+// of length K = C
+static int proto_geom(rt_ctx *c, rt_op *op, int nt, int ni, int kmax) {
+  if (rt_need_args(c, op, 4, nt, ni)) return RT_E_PARAM;
+  const int *p = op->p, *q = p + ni - 5;
+  int N = p[0], K = p[1], P = q[0], C = q[1], ld = q[2], nc = q[3], ppc = q[4];
+  RT_REQ(c, op, P > 0 && P <= 65536 && nc > 0 && ppc >= 1);
+  RT_REQ(c, op, N > 0 && N <= (1 << 26) && K > 0 && K <= kmax);
+  RT_REQ(c, op, K == C);
+  RT_REQ(c, op, ld >= C);
+  RT_REQ(c, op, (size_t)nc * ppc == (size_t)N);
+  return 0;
+}
+
+// the n4 loader check (pc_proto_n4_check, src/proto_s8n.c:115-132): flagged panels must keep every lane of 4
+// weights (bytes l, l + 8 of two consecutive 16-byte steps of a prototype) at sum |w| <= 258. The GPU kernels sum in
+// int32 and never need the flags, but a package that forges them is refused here as by the reference.
+static int n4_check(const int8_t *qw, int Kp, const uint8_t *n4, int npanels) {
+  if (Kp % 32) return -1;
+  for (int pn = 0; pn < npanels; pn++) {
+    if (!n4[pn]) continue;
+    const int8_t *w = qw + (size_t)pn * Kp * 4;
+    for (int k = 0; k < Kp; k += 32, w += 128)
+      for (int ch = 0; ch < 4; ch++)
+        for (int l = 0; l < 8; l++) {
+          int s = abs(w[16 * ch + l]) + abs(w[16 * ch + l + 8]) + abs(w[64 + 16 * ch + l]) + abs(w[64 + 16 * ch + l + 8]);
+          if (s > 258) return pn;
+        }
+  }
+  return -1;
+}
+
+static float *upload_f32(const void *h, size_t n) {
+  float *d = (float *)bnh_malloc(n * 4 ? n * 4 : 4);
+  if (d && bnh_memcpy_h2d(d, h, n * 4)) { hipFree(d); return nullptr; }
+  return d;
+}
+
+int bnh_proto_s8_init(rt_ctx *c, rt_op *op) {
+  proto_state *s = (proto_state *)calloc(1, sizeof *s);
+  op->state = s;
+  if (!s) return rt_oom(c, op, sizeof *s);
+  if (proto_geom(c, op, 6, 9, 1 << 17)) return RT_E_PARAM;
+  const int *p = op->p;
+  int N = p[0], K = p[1], Kp = p[2], Np = p[3], P = p[4], C = p[5], ld = p[6], nc = p[7];
+  RT_REQ(c, op, C % 8 == 0 && Kp == ((K + 15) & ~15));
+  RT_REQ(c, op, P % 4 == 0 && Np == ((N + 3) & ~3));
+  if (rt_need_t(c, op, 0, (size_t)Np * Kp, 0) || rt_need_t(c, op, 1, (size_t)Np * 4, 1) ||
+      rt_need_t(c, op, 2, (size_t)Np / 4, 1))
+    return RT_E_PARAM;
+  if (rt_need_t(c, op, 3, (size_t)N * 4, 0) || rt_need_t(c, op, 4, (size_t)nc * 4, 0) || rt_need_t(c, op, 5, 4, 0))
+    return RT_E_PARAM;
+  if (rt_need_nohalo(c, op, 0, RT_F32, (size_t)P * ld) || rt_need(c, op, 1, RT_F32, (size_t)nc)) return RT_E_PARAM;
+  if (rt_need(c, op, 2, RT_I8, (size_t)P * Kp) || rt_need(c, op, 3, RT_F32, (size_t)Np)) return RT_E_PARAM;
+  const int8_t *qw = (const int8_t *)rt_t(c, op, 0, nullptr);
+  int bad = n4_check(qw, Kp, (const uint8_t *)rt_t(c, op, 2, nullptr), Np / 4);
+  if (bad >= 0)
+    return rt_bad(c, op, "prototype panel %d is flagged for 4 products per int16 lane, but a lane's 4 weights sum to more "
+                  "than 258 (the sums could wrap)", bad);
+  memcpy(&s->eps, rt_t(c, op, 5, nullptr), 4);
+  s->W = bnh_s8p_new(Np, Kp, qw, (const float *)rt_t(c, op, 1, nullptr));
+  s->clsw = upload_f32(rt_t(c, op, 3, nullptr), (size_t)N);
+  s->clsb = upload_f32(rt_t(c, op, 4, nullptr), (size_t)nc);
+  if (!s->W || !s->clsw || !s->clsb) return rt_oom(c, op, (size_t)Np * Kp);
+  return 0;
+}
+
+int bnh_proto_s8_run(rt_ctx *c, rt_op *op) {
+  proto_state *s = (proto_state *)op->state;
+  const int *p = op->p;
+  const int N = p[0], Kp = p[2], P = p[4], C = p[5], ld = p[6], nc = p[7], ppc = p[8], B = c->nwin;
+  (void)N;
+  if (s->sx_cap < c->bcap) {  // per-window cell scales: op-private, grown with the arena
+    if (s->sx) hipFree(s->sx);
+    s->sx = (float *)bnh_malloc(sizeof(float) * (size_t)P * c->bcap);
+    if (!s->sx) { s->sx_cap = 0; return -1; }
+    s->sx_cap = c->bcap;
+  }
+  int8_t *qa = (int8_t *)rt_b(c, op, 2);
+  float *cm = (float *)rt_b(c, op, 3);
+  if (bnh_quant_cells((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), P, C, ld, s->eps, qa, rt_ws(c, op, 2), Kp, s->sx,
+                      P, B, c->stream))
+    return -1;
+  if (bnh_proto_colmax(qa, rt_ws(c, op, 2), s->sx, P, P, s->W, cm, rt_ws(c, op, 3), B, c->stream)) return -1;
+  return bnh_proto_logits(cm, rt_ws(c, op, 3), s->clsw, s->clsb, nc, ppc, (float *)rt_b(c, op, 1), rt_ws(c, op, 1), B,
+                          c->win_fail, c->fail_op + 1, c->stream);
+}
+
+void bnh_proto_s8_fini(rt_op *op) {
+  proto_state *s = (proto_state *)op->state;
+  if (s) {
+    bnh_s8p_free(s->W);
+    if (s->clsw) hipFree(s->clsw);
+    if (s->clsb) hipFree(s->clsb);
+    if (s->sx) hipFree(s->sx);
+  }
+  free(s);
+}

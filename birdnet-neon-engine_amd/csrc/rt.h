@@ -62,6 +62,7 @@ struct rt_ctx {
   int n_ops;
   // device memory: per buffer, window 0's address and the per-window stride in elements
   int bcap;              // windows the arena holds
+  int nwin;              // windows of the current run (<= bcap): ops launch for this many
   size_t *slot_bytes;    // per slot: bytes of one window's copy (64-aligned, >= 64 bytes of zero slack)
   size_t arena_bytes;
   char *arena;           // device

@@ -510,6 +510,7 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
     snprintf(err, errlen, "device error clearing the window flags");
     return -1;
   }
+  c->nwin = B;
   double t0 = c->prof ? now_s() : 0;
   for (int i = 0; i < c->n_ops; i++) {
     rt_op *op = &c->ops[i];

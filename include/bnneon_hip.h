@@ -34,6 +34,9 @@ void *bnh_event_new(void);
 int bnh_event_free(void *ev);
 int bnh_event_record(void *ev, void *stream);
 float bnh_event_ms(void *start, void *stop);                      /* after both completed; < 0 on error */
+/* a plain streaming device-to-device copy (16-byte aligned, bytes % 16 == 0): the bandwidth and HBM-counter
+ * calibration reference of the benchmarks */
+int bnh_copy(void *dst, const void *src, size_t bytes, void *stream);
 
 /* ------------------------------------------------------------------ scalar numerics checks
  * y[i] = f(x[i]) on the device for n elements, f = 0: FRECPE, 1: the fp32 SiLU of the epilogues
@@ -64,17 +67,37 @@ typedef struct {
  * each window -> q int8 [M][Kp] (pad k = the zero point), sa f32 [M], za i32 [M]. gate (or NULL): f32 [K] per
  * window (stride gate_ws), K % 4 == 0 and K <= 4096 as the reference requires. */
 int bnh_s8n_quant_rows(const float *x, long long x_ws, int ld, int M, int K, int Kp, const float *gate,
-                       long long gate_ws, int8_t *q, long long q_ws, float *sa, int32_t *za, long long s_ws, int B,
-                       void *stream);
+                       long long gate_ws, int8_t *q, long long q_ws, float *sa, long long sa_ws, int32_t *za,
+                       long long za_ws, int B, void *stream);
 /* s8n_gemm_range over every row and panel (src/gemm_s8n.c:176-190; src/gemm_s8n.h:21-22): out rows [0, M) x
  * channels [0, Np) = act(dequant(q . W) + b) (+ residual), stored by the epi32 rules */
-int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, const int32_t *za, long long s_ws, int M, int B,
-                 const bnh_s8w *W, const bnh_epi32 *e, void *stream);
+int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, long long sa_ws, const int32_t *za, long long za_ws,
+                 int M, int B, const bnh_s8w *W, const bnh_epi32 *e, void *stream);
 /* the PW_S8 op run (pw8_run, src/rt_ops_s8n.c:119-134): zero the output halo when opad (H = M / ow), quantize
  * (gated when gate != NULL) and multiply, for B windows */
 int bnh_pw_s8(const float *in, long long in_ws, int lda, int M, const float *gate, long long gate_ws, int8_t *q,
-              long long q_ws, float *sa, int32_t *za, long long s_ws, int B, const bnh_s8w *W, const bnh_epi32 *e,
-              void *stream);
+              long long q_ws, float *sa, long long sa_ws, int32_t *za, long long za_ws, int B, const bnh_s8w *W,
+              const bnh_epi32 *e, void *stream);
+
+/* ------------------------------------------------------------------ int8 prototype head (PROTO_S8)
+ * Prototypes from the package tensors of PROTO_S8 (src/rt_ops_s8n.c:212-236): qw int8 [Np/4][Kp/16][4][16] and sw
+ * f32 [>= Np], repacked once into MFMA operand rows in HBM. */
+typedef struct bnh_s8p bnh_s8p;
+bnh_s8p *bnh_s8p_new(int Np, int Kp, const int8_t *qw, const float *sw);
+void bnh_s8p_free(bnh_s8p *W);
+/* pc_quant_cells_f32 (src/proto_s8n.c:28-51; declared src/pc_kern.h:60): cells x [P][ld] (C channels, C % 8 == 0)
+ * -> qa int8 [P][Kp] in [-127, 127] (zeros past C) and sx f32 [P], the scales of the L2-normalised cells */
+int bnh_quant_cells(const float *x, long long x_ws, int P, int C, int ld, float eps, int8_t *qa, long long qa_ws,
+                    int Kp, float *sx, long long sx_ws, int B, void *stream);
+/* pc_proto_colmax_s8n over every panel (src/proto_s8n.c:139-164; src/pc_kern.h:64-65): colmax f32 [Np] per window,
+ * the maximum over the window's P cells of (float)(qa . qw) * sx, times sw */
+int bnh_proto_colmax(const int8_t *qa, long long qa_ws, const float *sx, long long sx_ws, int P, const bnh_s8p *W,
+                     float *colmax, long long cm_ws, int B, void *stream);
+/* pc_proto_logits (src/pc_kern_f32.c:364-374; src/pc_kern.h:69): logits f32 [nc] per window from colmax and the
+ * class tensors clsw f32 [nc][ppc], clsb f32 [nc] (device). A window with a non-finite logit gets
+ * win_fail[w] = fail_code (when still 0; win_fail may be NULL) -- the reference's return value -2. */
+int bnh_proto_logits(const float *colmax, long long cm_ws, const float *clsw, const float *clsb, int nc, int ppc,
+                     float *logits, long long lg_ws, int B, int *win_fail, int fail_code, void *stream);
 
 /* ------------------------------------------------------------------ int8 GEMM with Q31 requantisation
  * No counterpart in the reference (whose int8 GEMM dequantises to fp32): the TFLite-style static int8 pointwise

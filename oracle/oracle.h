@@ -58,6 +58,21 @@ void orc_pw_s8(const float *in, int lda, int M, int K, int Kp, int N, int Np, co
 /* rt_zero_halo (src/rt_pkg.c:194-203) */
 void orc_zero_halo(void *xp, int H, int W, int C, int h, size_t esz);
 
+/* ---------------------------------------------------------------- int8 prototype head (PROTO_S8) */
+/* src/proto_s8n.c:28-51 */
+void orc_quant_cells_f32(const float *x, int P, int C, int ld, float eps, int8_t *qa, int Kp, float *sx);
+/* src/proto_s8n.c:115-132 */
+int orc_proto_n4_check(const int8_t *qw, int Kp, const uint8_t *n4, int npanels);
+/* src/proto_s8n.c:139-164, every panel: prototypes [Np/4][Kp/16][4][16] */
+void orc_proto_colmax_s8n(const int8_t *qa, int Kp, const float *sx, int P, const int8_t *qw, const float *sw, int Np,
+                          float *colmax);
+/* src/pc_kern_f32.c:364-374 */
+int orc_proto_logits(const float *colmax, const float *w, const float *b, int nc, int ppc, float *logits);
+/* the whole op of one window: quantize, column maxima, logits (src/rt_ops_s8n.c:245-253); returns 0 or -2 */
+int orc_proto_s8(const float *x, int P, int C, int ld, float eps, int8_t *qa, int Kp, float *sx, const int8_t *qw,
+                 const float *sw, int Np, float *colmax, const float *clsw, const float *clsb, int nc, int ppc,
+                 float *logits);
+
 /* ---------------------------------------------------------------- Q31 requantised int8 GEMM (own specification)
  * The reference has no such kernel. Specification (TFLite / gemmlowp fixed-point conventions):
  *   acc[n][m]  = sum_k w[n][k] * (x[k][m] - zx) + bias[n]                       (exact, int32)

@@ -1,0 +1,104 @@
+/* CPU oracle (test infrastructure only): the int8 prototype head of libbnneon (PROTO_S8). See oracle.h. */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oracle.h"
+
+static inline uint32_t fbits(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+
+/* src/proto_s8n.c:28-51. Sum of squares in two 4-lane fused accumulators over 8-channel steps (lane j of the first
+ * takes channels c + j, of the second c + 4 + j), reduced as ((t0 + t1) + (t2 + t3)) with t_j = s0_j + s1_j; max |x|
+ * with FMAX (NaN-propagating) in the same lanes; q = FCVTAS(x * (127 / mx)) narrowed with saturation to int16, int8,
+ * then floored at -127; zeros from C to Kp. */
+void orc_quant_cells_f32(const float *x, int P, int C, int ld, float eps, int8_t *qa, int Kp, float *sx) {
+  for (int p = 0; p < P; p++) {
+    const float *r = x + (size_t)p * ld;
+    float s0[4] = {0, 0, 0, 0}, s1[4] = {0, 0, 0, 0}, m0[4] = {0, 0, 0, 0}, m1[4] = {0, 0, 0, 0};
+    for (int c = 0; c < C; c += 8)
+      for (int j = 0; j < 4; j++) {
+        float u0 = r[c + j], u1 = r[c + 4 + j];
+        s0[j] = fmaf(u0, u0, s0[j]);
+        s1[j] = fmaf(u1, u1, s1[j]);
+        m0[j] = orc_fmax(m0[j], fabsf(u0));
+        m1[j] = orc_fmax(m1[j], fabsf(u1));
+      }
+    float t[4], m[4];
+    for (int j = 0; j < 4; j++) { t[j] = s0[j] + s1[j]; m[j] = orc_fmax(m0[j], m1[j]); }
+    float den = sqrtf((t[0] + t[1]) + (t[2] + t[3])) + eps;
+    float mx = orc_fmax(orc_fmax(m[0], m[1]), orc_fmax(m[2], m[3]));
+    if (!(mx > 0)) mx = 1e-30f;
+    sx[p] = mx / (127.f * den);
+    const float inv = 127.f / mx;
+    int8_t *q = qa + (size_t)p * Kp;
+    for (int c = 0; c < C; c++) {
+      int32_t v = orc_cvta_s32(r[c] * inv);
+      int32_t h = v < -32768 ? -32768 : v > 32767 ? 32767 : v;   /* SQXTN to int16 */
+      int32_t b = h < -128 ? -128 : h > 127 ? 127 : h;           /* SQXTN to int8 */
+      q[c] = (int8_t)(b < -127 ? -127 : b);                       /* SMAX with -127 */
+    }
+    memset(q + C, 0, (size_t)(Kp - C));
+  }
+}
+
+/* src/proto_s8n.c:115-132: the first n4-flagged panel with a lane of 4 weights (bytes l, l + 8 of two consecutive
+ * 16-byte steps of one prototype) summing to more than 258 in |w|, or -1; -1 also when Kp % 32 (no n4 loop) */
+int orc_proto_n4_check(const int8_t *qw, int Kp, const uint8_t *n4, int npanels) {
+  if (Kp % 32) return -1;
+  for (int pn = 0; pn < npanels; pn++) {
+    if (!n4[pn]) continue;
+    const int8_t *w = qw + (size_t)pn * Kp * 4;
+    for (int k = 0; k < Kp; k += 32, w += 128)
+      for (int ch = 0; ch < 4; ch++)
+        for (int l = 0; l < 8; l++) {
+          int s = abs(w[16 * ch + l]) + abs(w[16 * ch + l + 8]) + abs(w[64 + 16 * ch + l]) + abs(w[64 + 16 * ch + l + 8]);
+          if (s > 258) return pn;
+        }
+  }
+  return -1;
+}
+
+/* src/proto_s8n.c:139-164: colmax[j] = (max over cells p of (float)acc[p][j] * sx[p]) * sw[j] for every prototype
+ * j < Np (the max starts from -inf and propagates NaN), exact int32 sums over Kp */
+void orc_proto_colmax_s8n(const int8_t *qa, int Kp, const float *sx, int P, const int8_t *qw, const float *sw, int Np,
+                          float *colmax) {
+  const int kb = Kp / 16;
+  for (int j = 0; j < Np; j++) {
+    const int8_t *wp = qw + (size_t)(j / 4) * kb * 64 + (j % 4) * 16;
+    float mx = -INFINITY;
+    for (int p = 0; p < P; p++) {
+      const int8_t *a = qa + (size_t)p * Kp;
+      uint32_t acc = 0;
+      for (int k = 0; k < Kp; k++) acc += (uint32_t)((int32_t)a[k] * (int32_t)wp[(size_t)(k / 16) * 64 + k % 16]);
+      mx = orc_fmax(mx, (float)(int32_t)acc * sx[p]);
+    }
+    colmax[j] = mx * sw[j];
+  }
+}
+
+/* src/pc_kern_f32.c:364-374: logit c = (sum over q < ppc of colmax * w, multiply then add, in order) + b; -2 when a
+ * logit is not finite (|v| <= 3e38 fails) */
+int orc_proto_logits(const float *colmax, const float *w, const float *b, int nc, int ppc, float *logits) {
+  int bad = 0;
+  for (int c = 0; c < nc; c++) {
+    float s = 0;
+    for (int q = 0; q < ppc; q++) {
+      float t = colmax[(size_t)c * ppc + q] * w[(size_t)c * ppc + q];
+      s = s + t;
+    }
+    float v = s + b[c];
+    logits[c] = v;
+    bad |= !(fabsf(v) <= 3.0e38f);
+  }
+  (void)fbits;
+  return bad ? -2 : 0;
+}
+
+/* the PROTO_S8 op of one window (src/rt_ops_s8n.c:245-253) */
+int orc_proto_s8(const float *x, int P, int C, int ld, float eps, int8_t *qa, int Kp, float *sx, const int8_t *qw,
+                 const float *sw, int Np, float *colmax, const float *clsw, const float *clsb, int nc, int ppc,
+                 float *logits) {
+  orc_quant_cells_f32(x, P, C, ld, eps, qa, Kp, sx);
+  orc_proto_colmax_s8n(qa, Kp, sx, P, qw, sw, Np, colmax);
+  return orc_proto_logits(colmax, clsw, clsb, nc, ppc, logits);
+}

@@ -155,3 +155,47 @@ def gemm_s8_requant(w, x, bias, mult, shift, zx, zy, lo=-128, hi=127):
     lib().orc_gemm_s8_requant(P(w), P(x), P(b), P(m), P(s), N, K, M, zx, zy,
                               lo, hi, P(out))
     return out
+
+
+_SIGS.update({
+    "orc_quant_cells_f32": (None, [vp, i32, i32, i32, f32, vp, i32, vp]),
+    "orc_proto_n4_check": (i32, [vp, i32, vp, i32]),
+    "orc_proto_colmax_s8n": (None, [vp, i32, vp, i32, vp, vp, i32, vp]),
+    "orc_proto_logits": (i32, [vp, vp, vp, i32, i32, vp]),
+    "orc_proto_s8": (i32, [vp, i32, i32, i32, f32, vp, i32, vp, vp, vp, i32, vp,
+                           vp, vp, i32, i32, vp]),
+})
+
+
+def quant_cells(x, C, Kp, eps):
+    """orc_quant_cells_f32 on x [P][ld] -> (qa [P][Kp], sx [P])."""
+    x = np.ascontiguousarray(x, np.float32)
+    P, ld = x.shape
+    qa = np.zeros((P, Kp), np.int8)
+    sx = np.zeros(P, np.float32)
+    lib().orc_quant_cells_f32(x.ctypes.data, P, C, ld, eps, qa.ctypes.data, Kp, sx.ctypes.data)
+    return qa, sx
+
+
+def proto_s8(x, C, eps, qw, sw, Np, Kp, clsw, clsb, nc, ppc):
+    """The PROTO_S8 op of one window -> (rc, logits, colmax, qa)."""
+    x = np.ascontiguousarray(x, np.float32)
+    Pn, ld = x.shape
+    qa = np.zeros((Pn, Kp), np.int8)
+    sx = np.zeros(Pn, np.float32)
+    cm = np.zeros(Np, np.float32)
+    lg = np.zeros(nc, np.float32)
+    qw = np.ascontiguousarray(qw, np.int8)
+    sw = np.ascontiguousarray(sw, np.float32)
+    clsw = np.ascontiguousarray(clsw, np.float32)
+    clsb = np.ascontiguousarray(clsb, np.float32)
+    rc = lib().orc_proto_s8(x.ctypes.data, Pn, C, ld, eps, qa.ctypes.data, Kp, sx.ctypes.data,
+                            qw.ctypes.data, sw.ctypes.data, Np, cm.ctypes.data, clsw.ctypes.data,
+                            clsb.ctypes.data, nc, ppc, lg.ctypes.data)
+    return rc, lg, cm, qa
+
+
+def n4_check(qw, Kp, n4):
+    qw = np.ascontiguousarray(qw, np.int8)
+    n4 = np.ascontiguousarray(n4, np.uint8)
+    return lib().orc_proto_n4_check(qw.ctypes.data, Kp, n4.ctypes.data, n4.size)

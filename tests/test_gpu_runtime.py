@@ -1,0 +1,166 @@
+"""The drop-in boundary on the GPU: .bnpk packages through bnn_init /
+bnn_infer / bnn_infer_batch on libbnneon_hip, every output compared bit for
+bit with the oracle's op-by-op restatement of the reference library, plus the
+load-time refusals and failed-window reporting of the reference's contract."""
+import numpy as np
+import pytest
+
+import pyoracle as O
+from bnneon import binding, hip, netbuild, pkgfmt, s8pack
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+class Spec:
+    """A synthetic int8 net: rows [M][K0] -> PW_S8 (SiLU) -> PW_S8 -> PROTO_S8."""
+
+    def __init__(self, seed=0, M=64, K0=40, K1=136, K2=48, nc=100, ppc=4):
+        rng = np.random.default_rng(seed)
+        self.M, self.K0, self.nc, self.ppc = M, K0, nc, ppc
+        self.w1 = rng.standard_normal((K1, K0)).astype(np.float32) * 0.3
+        self.b1 = rng.standard_normal(K1).astype(np.float32) * 0.1
+        self.w2 = rng.standard_normal((K2, K1)).astype(np.float32) * 0.1
+        self.b2 = rng.standard_normal(K2).astype(np.float32) * 0.1
+        self.protos = rng.standard_normal((nc * ppc, K2)).astype(np.float32)
+        self.clsw = rng.uniform(0.5, 1.5, nc * ppc).astype(np.float32)
+        self.clsb = rng.standard_normal(nc).astype(np.float32)
+        self.pk1 = s8pack.pack_s8(self.w1, self.b1)
+        self.pk2 = s8pack.pack_s8(self.w2, self.b2)
+
+    def package(self, path, n4=None):
+        pkg = pkgfmt.Package()
+        net = netbuild.Net(pkg)
+        ib = net.buf(netbuild.F32, self.M, 1, self.K0)
+        h1 = net.pw_s8(ib, self.w1, self.b1, act="silu")
+        h2 = net.pw_s8(h1, self.w2, self.b2)
+        net.proto_s8(h2, self.protos, self.clsw, self.clsb, n4=n4)
+        net.add_to("neon-int8", 0, in_buf=ib)
+        netbuild.standard_meta(pkg, self.M * self.K0, self.nc, model_id="synthetic_int8_proto")
+        pkg.write(path)
+        return path
+
+    def oracle(self, pcm):
+        x = pcm.reshape(self.M, self.K0)
+        h1, *_ = O.pw_s8(x, self.pk1, act=1)
+        h2, *_ = O.pw_s8(h1, self.pk2)
+        N, K = self.protos.shape
+        Kp, Np = s8pack.r16(K), (N + 3) // 4 * 4
+        q, sw = s8pack.quant_rows_s8(self.protos)
+        qp = np.zeros((Np, Kp), np.int8)
+        qp[:N, :K] = q
+        swp = np.zeros(Np, np.float32)
+        swp[:N] = sw
+        rc, lg, _, _ = O.proto_s8(h2, K, 1e-5, s8pack.pack_panels(qp), swp, Np, Kp, self.clsw, self.clsb,
+                                  self.nc, self.ppc)
+        return rc, lg
+
+
+def same(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    an, bn = np.isnan(a), np.isnan(b)
+    return np.array_equal(an, bn) and np.array_equal(a.view(np.uint32)[~an], b.view(np.uint32)[~bn])
+
+
+def test_batch_of_windows_bit_exact(hip, tmp_path):
+    spec = Spec(1)
+    path = spec.package(str(tmp_path / "net.bnpk"))
+    rng = np.random.default_rng(2)
+    pcm = (rng.standard_normal((37, spec.M * spec.K0)) * 0.5).astype(np.float32)
+    say("runtime batch 37")
+    with binding.Model(path) as m:
+        assert m.info.path == b"neon-int8" and m.info.precision == b"int8 GEMMs, fp32 elsewhere"
+        out, _, status = m.infer_batch(pcm)
+        assert not status.any()
+        for w in range(37):
+            rc, ref = spec.oracle(pcm[w])
+            assert rc == 0 and same(out[w], ref), w
+        # one window at a time gives the same bytes; a smaller batch after a larger one too
+        single, _ = m.infer(pcm[5])
+        assert same(single, out[5])
+        out2, _, _ = m.infer_batch(pcm[:3])
+        assert same(out2, out[:3])
+
+
+def test_failed_window_is_reported(hip, tmp_path):
+    spec = Spec(3)
+    path = spec.package(str(tmp_path / "net.bnpk"))
+    rng = np.random.default_rng(4)
+    pcm = rng.standard_normal((6, spec.M * spec.K0)).astype(np.float32)
+    # an inf or NaN in the input is washed out by the next layer's quantization
+    # (a NaN row quantizes to its bias); values near fp32's limit are not:
+    # the dequantized layer-1 row overflows to +-inf, the layer-2 row to NaN,
+    # and the prototype cells and logits follow
+    pcm[4] = np.where(np.arange(pcm.shape[1]) % 2, -1.5e38, 1.5e38)
+    ref_rc = [spec.oracle(p)[0] for p in pcm]
+    assert ref_rc[4] == -2 and ref_rc.count(0) == 5
+    say("runtime failed window", ref_rc)
+    with binding.Model(path) as m:
+        out, _, status = m.infer_batch(pcm, check=False)
+        assert [int(s != 0) for s in status] == [int(r != 0) for r in ref_rc]
+        assert status[4] == 3           # 1 + the index of PROTO_S8 in the op list
+        with pytest.raises(binding.BnnError) as e:
+            m.infer_batch(pcm)
+        assert e.value.kind == "window" and "op 2 proto_s8n" in str(e.value) and "window 4 of 6" in str(e.value)
+        for w in range(6):
+            assert same(out[w], spec.oracle(pcm[w])[1])
+
+
+def test_device_resident_batch(hip, tmp_path):
+    spec = Spec(5)
+    path = spec.package(str(tmp_path / "net.bnpk"))
+    rng = np.random.default_rng(6)
+    pcm = rng.standard_normal((9, spec.M * spec.K0)).astype(np.float32)
+    say("runtime device batch")
+    with binding.Model(path) as m:
+        dp = hip.DeviceArray.from_host(pcm)
+        do = hip.DeviceArray.zeros((9, spec.nc), np.float32)
+        st = np.zeros(9, np.int32)
+        r = m.L.bnn_infer_batch_device(m.ctx, dp.ptr, 9, do.ptr, None, st.ctypes.data_as(binding._IP), None)
+        assert r == 0
+        host, _, _ = m.infer_batch(pcm)
+        assert same(do.numpy(), host)
+
+
+def test_forged_n4_flags_are_refused(hip, tmp_path):
+    spec = Spec(7, K2=64)
+    # prototype 9 gets 4 full-scale weights in one int16 lane (bytes 3, 11,
+    # 19, 27 of a 32-byte step): 4 x 127 > 258, so its panel is not n4-safe
+    for k in (3, 11, 19, 27):
+        spec.protos[9, k] = 50.0
+    q, _ = s8pack.quant_rows_s8(spec.protos)
+    true_flags = s8pack.n4_panel_flags(q)
+    assert true_flags[2] == 0
+    first_bad = int(np.argmin(true_flags))
+    path = spec.package(str(tmp_path / "forged.bnpk"), n4=np.ones_like(true_flags))
+    say("runtime forged n4")
+    with pytest.raises(binding.BnnError) as e:
+        binding.Model(path)
+    assert e.value.kind == "package" and f"prototype panel {first_bad} is flagged" in str(e.value)
+    assert "op 2 proto_s8n" in str(e.value)
+    # the compiler's own flags load
+    ok = spec.package(str(tmp_path / "honest.bnpk"))
+    binding.Model(ok).close()
+
+
+def test_contract_violations_are_refused(hip, tmp_path):
+    spec = Spec(8)
+    path = spec.package(str(tmp_path / "net.bnpk"))
+    r = pkgfmt.read(path)
+    data = bytearray(open(path, "rb").read())
+    # op 0 (PW_S8): its Np parameter (int param 3) no longer matches N rounded up to 8
+    import struct
+    poff = struct.unpack_from("<Q", data, 48)[0]
+    ops_off = struct.unpack_from("<Q", data, poff + 64)[0]
+    code, rb, nb, nt, ni, _ = struct.unpack_from("<6H", data, ops_off)
+    struct.pack_into("<i", data, ops_off + 12 + 4 * (nb + nt + 3), 1000)
+    bad = tmp_path / "bad_np.bnpk"
+    bad.write_bytes(bytes(data))
+    say("runtime bad Np")
+    with pytest.raises(binding.BnnError) as e:
+        binding.Model(str(bad))
+    assert "int8 GEMM shape" in str(e.value) and "op 0 pw_s8n" in str(e.value)
+    assert r["paths"][0]["ops"][0][0] == 22

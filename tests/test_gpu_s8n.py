@@ -90,7 +90,7 @@ def quant_case(hip, x, K, Kp, gate=None, B=1):
         gh[:, :K] = gate
         dg = H.DeviceArray.from_host(gh)
     H.check(H.lib().bnh_s8n_quant_rows(dx.ptr, x_ws, ld, M, K, Kp, H.ptr(dg), g_ws,
-                                       dq.ptr, q_ws, dsa.ptr, dza.ptr, s_ws, B, None), "quant")
+                                       dq.ptr, q_ws, dsa.ptr, s_ws, dza.ptr, s_ws, B, None), "quant")
     H.sync()
     q, sa, za = dq.numpy(), dsa.numpy(), dza.numpy()
     ok = True
@@ -169,7 +169,7 @@ def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, g
                 ldr=Np if res else 0, out_ws=out_rows * ldo, res_ws=M * Np)
     say(f"pw_s8 B{B} {H_}x{W_} K{K} N{N} act{act} opad{opad} res{res} gate{gate}")
     H.check(H.lib().bnh_pw_s8(dx.ptr, M * lda, lda, M, H.ptr(dg), K if gate else 0, dq.ptr, M4 * Kp,
-                              dsa.ptr, dza.ptr, M4, B, Wt.h, e, None), "pw_s8")
+                              dsa.ptr, M4, dza.ptr, M4, B, Wt.h, e, None), "pw_s8")
     H.sync()
     out = dout.numpy().reshape(B, out_rows, ldo)
     q = dq.numpy().reshape(B, M4, Kp)
