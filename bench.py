@@ -10,6 +10,10 @@ windows already resident in HBM):
                    point -128, per-channel Q31 requant, batch 256 windows.
   pw_s8            libbnneon's PW_S8 op (fp32 rows, per-row dynamic int8,
                    fp32 dequant + SiLU) at the same shape, batch 256.
+  dw_f16, dw_s8    the depthwise convolution, NHWC, C = 672, 24 x 64, k x k
+                   (--k 3|5) at stride --s 1|2, 'same' padding, bias + SiLU,
+                   batch 64 windows: fp16 (libbnneon's DWK fp16 kernel) or
+                   int8 with per-channel Q31 requant and a SiLU table.
 
 The timed region is bracketed by device synchronisation; the dominant
 kernel's average duration comes from HIP events recorded on the stream the
@@ -38,9 +42,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--batch", type=int, default=256)
+    ap.add_argument("--batch", type=int, default=None,
+                    help="windows per launch (256; 64 for the depthwise workloads)")
     ap.add_argument("--workload", default="gemm_s8_requant",
-                    choices=["gemm_s8_requant", "pw_s8", "copy"])
+                    choices=["gemm_s8_requant", "pw_s8", "dw_f16", "dw_s8", "copy"])
+    ap.add_argument("--k", type=int, default=5, choices=[3, 5], help="depthwise kernel size")
+    ap.add_argument("--s", type=int, default=1, choices=[1, 2], help="depthwise stride")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     return ap.parse_args()
@@ -115,6 +122,67 @@ def cpu_baseline_pw_s8(pk, rng):
                       f"{dt:.2f} s wall"}
 
 
+def same_pads(n, k, s):
+    o = (n - 1) // s + 1
+    return o, max((o - 1) * s + k - n, 0) // 2
+
+
+def silu_lut_s8(sx, zx, sy, zy):
+    """int8 -> int8 SiLU table for activations with scales / zero points."""
+    q = np.arange(-128, 128, dtype=np.float64)
+    x = (q - zx) * sx
+    y = x / (1 + np.exp(-x))
+    return np.clip(np.round(y / sy) + zy, -128, 127).astype(np.int8)
+
+
+def dw_inputs(rng, B, C, H, W, k, s, kind):
+    h = (k - 1) // 2
+    Ho, pt = same_pads(H, k, s)
+    Wo, pl = same_pads(W, k, s)
+    if kind == "f16":
+        x = rng.standard_normal((B, H, W, C)).astype(np.float32)
+        x = x / (1 + np.exp(-x))                     # activations SiLU(N(0, 1))
+        xp = np.zeros((B, H + 2 * h, W + 2 * h, C), np.float16)
+        xp[:, h:h + H, h:h + W] = x
+        w = (rng.standard_normal((k * k, C)) * np.sqrt(2.0 / (k * k))).astype(np.float16)
+        b = (rng.standard_normal(C) * 0.1).astype(np.float16)
+        return dict(x=xp, w=w, b=b, Ho=Ho, Wo=Wo, pt=pt, pl=pl)
+    x = np.clip(np.round(rng.normal(-40, 35, (B, H, W, C))), -128, 127).astype(np.int8)
+    w = rng.integers(-127, 128, (k * k, C)).astype(np.int8)
+    bias = rng.integers(-2 ** 14, 2 ** 14 + 1, C).astype(np.int32)
+    mult = rng.integers(2 ** 30, 2 ** 31, C).astype(np.int32)
+    shift = rng.integers(6, 11, C).astype(np.int32)
+    lut = silu_lut_s8(0.05, -128, 0.05, -128)
+    return dict(x=x, w=w, bias=bias, mult=mult, shift=shift, lut=lut, Ho=Ho, Wo=Wo, pt=pt, pl=pl)
+
+
+def cpu_baseline_dw(d, kind, C, H, W, k, s):
+    """The oracle's depthwise kernel, one window per thread, on a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    T = cpu_threads()
+    n_win = 2 * T
+    x = d["x"]
+    if kind == "f16":
+        f = lambda i: O.dwk_f16(x[i % x.shape[0]], H, W, C, k, s, d["pt"], d["pl"], d["w"], d["b"], 1,
+                                d["Ho"], d["Wo"])
+        what = "fp16 DWK (exact fp16 arithmetic emulated in integer C)"
+    else:
+        f = lambda i: O.dw_s8(x[i % x.shape[0]], k, s, d["pt"], d["pl"], d["w"], d["bias"], d["mult"],
+                              d["shift"], -128, -128, -128, 127, d["lut"], d["Ho"], d["Wo"])
+        what = "int8 depthwise + Q31 requant + SiLU table"
+    t0 = time.perf_counter()
+    f(0)
+    n_win = T * max(2, min(200, int(5.0 / max(time.perf_counter() - t0, 1e-3))))  # about 5 s per thread
+    t0 = time.perf_counter()
+    with concurrent.futures.ThreadPoolExecutor(T) as ex:
+        list(ex.map(f, range(n_win)))
+    dt = time.perf_counter() - t0
+    return {"value": n_win / dt, "unit": "windows/s", "cores": T, "kind": "port",
+            "sample": f"{n_win} windows of the {k}x{k} s{s} {what}, C={C}, {H}x{W}, one window per "
+                      f"thread ({T} threads), scalar C oracle; {dt:.2f} s wall"}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -126,7 +194,7 @@ def main():
     if H.lib().bnh_device_count() < 1:
         raise SystemExit("no HIP device visible")
     rng = np.random.default_rng(20240601)
-    B = a.batch
+    B = a.batch or (64 if a.workload.startswith("dw_") else 256)
     N, K, M = 256, 1152, 1536
     stream = H.lib().bnh_stream_new()
     if a.workload == "copy":
@@ -140,6 +208,9 @@ def main():
         print(json.dumps({"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes,
                           "ms_per_copy": round(ms, 4), "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}),
               flush=True)
+        return
+    if a.workload.startswith("dw_"):
+        run_dw(a, H, rng, B, stream)
         return
     if a.workload == "gemm_s8_requant":
         w, x, bias, mult, shift = config0_inputs(rng, B)
@@ -201,6 +272,61 @@ def main():
             line["cpu_baseline"] = cpu_baseline_gemm_s8_requant(w, bias, mult, shift, rng)
         else:
             line["cpu_baseline"] = cpu_baseline_pw_s8(pk, rng)
+    print(json.dumps(line), flush=True)
+
+
+def run_dw(a, H, rng, B, stream):
+    C, Hh, W, k, s = 672, 24, 64, a.k, a.s
+    kind = a.workload[3:]
+    d = dw_inputs(rng, B, C, Hh, W, k, s, kind)
+    Ho, Wo, pt, pl = d["Ho"], d["Wo"], d["pt"], d["pl"]
+    L = H.lib()
+    dx = H.DeviceArray.from_host(d["x"])
+    x_ws = d["x"][0].size
+    o_ws = Ho * Wo * C
+    dw_ = H.DeviceArray.from_host(d["w"])
+    if kind == "f16":
+        db = H.DeviceArray.from_host(d["b"])
+        dout = H.DeviceArray.zeros((B, o_ws), np.float16)
+
+        def launch():
+            H.check(L.bnh_dwk_f16(dx.ptr, x_ws, Hh, W, C, k, s, pt, pl, dw_.ptr, db.ptr, 1, dout.ptr, o_ws,
+                                  Ho, Wo, None, 0, B, stream))
+        esz = 2
+        workload = (f"fp16 depthwise {k}x{k} stride {s}, 'same', NHWC C=672 24x64, bias + SiLU (LUT), "
+                    f"libbnneon DWK fp16 arithmetic")
+        kernel = "k_dw_f16"
+        dtype = "fp16"
+    else:
+        dbias, dm = H.DeviceArray.from_host(d["bias"]), H.DeviceArray.from_host(d["mult"])
+        dsh, dl = H.DeviceArray.from_host(d["shift"]), H.DeviceArray.from_host(d["lut"])
+        dout = H.DeviceArray.zeros((B, o_ws), np.int8)
+
+        def launch():
+            H.check(L.bnh_dw_s8(dx.ptr, x_ws, Hh, W, C, k, s, pt, pl, dw_.ptr, dbias.ptr, dm.ptr, dsh.ptr,
+                                -128, -128, -128, 127, dl.ptr, dout.ptr, o_ws, Ho, Wo, B, stream))
+        esz = 1
+        workload = (f"int8 depthwise {k}x{k} stride {s}, 'same', NHWC C=672 24x64, per-channel Q31 requant "
+                    f"+ SiLU table")
+        kernel = "k_dw_s8"
+        dtype = "int8"
+    ms, wall = time_steps(H, stream, launch, a.steps, a.warmup)
+    bytes_per_launch = B * (x_ws + o_ws) * esz + k * k * C * esz
+    gbs = bytes_per_launch / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "windows/s (depthwise layer, batch 64)", "value": round(B / (ms * 1e-3), 1),
+        "unit": "windows/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": dtype, "data": "synthetic (seeded; config distributions)",
+        "config": {"workload": workload, "global_batch": B, "channels": C, "height": Hh, "width": W,
+                   "k": k, "stride": s, "parallelism": "1 GPU, windows batched per launch",
+                   "wall_s_timed_region": round(wall, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
+                     "algorithmic_bytes_per_launch": bytes_per_launch},
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_dw(d, kind, C, Hh, W, k, s)
     print(json.dumps(line), flush=True)
 
 

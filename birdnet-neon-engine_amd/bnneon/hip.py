@@ -62,6 +62,17 @@ _SIGS = {
     "bnh_q8w_new": (vp, [i32, i32, vp, vp, vp, vp, i32, i32, i32, i32]),
     "bnh_q8w_free": (None, [vp]),
     "bnh_gemm_s8_requant": (i32, [vp, vp, i64, i32, i32, vp, i64, vp]),
+    "bnh_dwk_f32": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp,
+                          i32, vp, i64, i32, i32, vp, i64, i32, vp]),
+    "bnh_dw3_f32": (i32, [vp, i64, i32, i32, i32, i32, vp, vp, vp, i64, i32,
+                          i32, vp, i64, i32, vp]),
+    "bnh_dwk_f16": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp,
+                          i32, vp, i64, i32, i32, vp, i64, i32, vp]),
+    "bnh_dw3_f16": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, vp,
+                          i64, i32, i32, vp, i64, i32, vp]),
+    "bnh_dw_s8": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp,
+                        vp, i32, i32, i32, i32, vp, vp, i64, i32, i32, i32,
+                        vp]),
 }
 
 

@@ -106,6 +106,49 @@ class Net:
         self.last = ob
         return ob
 
+    # ---------------------------------------------------------------- depthwise
+    def dwk(self, ib, w, b, k, s=1, pt=None, pl=None, act="silu", fp16=False):
+        """k x k depthwise conv (DWK) on the zero-haloed buffer ib (halo (k-1)/2,
+        ld = C), TF-'same' pads by default; returns (out, chsum) buffers.
+        w [k*k][C], b [C] (fp16 when fp16, else fp32): l_dwconv's record
+        (python/bnneon/compiler/lower.py:916-951)."""
+        d = self.bufs[ib]
+        H, W, C = d[1], d[2], d[4]
+        assert d[5] == (k - 1) // 2, "DWK input needs halo (k-1)/2"
+        Ho, Wo = (H - 1) // s + 1, (W - 1) // s + 1
+        if pt is None:
+            pt = max((Ho - 1) * s + k - H, 0) // 2
+        if pl is None:
+            pl = max((Wo - 1) * s + k - W, 0) // 2
+        dt, npdt = (F16, np.float16) if fp16 else (F32, np.float32)
+        tl = [self.tensor("dw.w", np.asarray(w, npdt).reshape(k * k, C)),
+              self.tensor("dw.b", np.asarray(b, npdt).reshape(C))]
+        ob = self.buf(dt, Ho, Wo, C)
+        cb = self.buf(F32, 1, 1, C)
+        self.emit(OP["DWK"], [ib, ob, cb], tl, [H, W, C, k, s, pt, pl, Ho, Wo, ACT[act]], var=1 if fp16 else 0)
+        self.last = ob
+        return ob, cb
+
+    def dw3(self, ib, w, b, s=1, pt=1, pl=1, fp16=False):
+        """3 x 3 depthwise + SiLU (DW3) on the halo-1 buffer ib; the fp32 form
+        has pads 1, the fp16 form takes pt, pl in {0, 1}."""
+        d = self.bufs[ib]
+        H, W, C = d[1], d[2], d[4]
+        assert d[5] == 1
+        if fp16:
+            Ho, Wo = (H - 1) // s + 1, (W - 1) // s + 1
+        else:
+            Ho, Wo = (H + 2 - 3) // s + 1, (W + 2 - 3) // s + 1
+        dt, npdt = (F16, np.float16) if fp16 else (F32, np.float32)
+        tl = [self.tensor("dw3.w", np.asarray(w, npdt).reshape(9, C)),
+              self.tensor("dw3.b", np.asarray(b, npdt).reshape(C))]
+        ob = self.buf(dt, Ho, Wo, C)
+        cb = self.buf(F32, 1, 1, C)
+        p = [H, W, C, s, Ho, Wo] + ([pt, pl] if fp16 else [])
+        self.emit(OP["DW3"], [ib, ob, cb], tl, p, var=1 if fp16 else 0)
+        self.last = ob
+        return ob, cb
+
     def add_to(self, name="neon-int8", hwcap=0, in_buf=0, out_buf=None, emb_buf=None):
         self.pkg.add_path(name, hwcap, self.bufs, self.ops, in_buf,
                           self.last if out_buf is None else out_buf, emb_buf)

@@ -1,0 +1,455 @@
+// Depthwise convolutions of libbnneon on gfx950 (no MFMA: 2 k^2 flops per output against 2-4 bytes moved, so HBM
+// bound): fp32 DWK (src/pc_kern_f32.c:163-334), fp32 DW3 (src/gemm_f32.c:213-441), fp16 DWK (src/pc_kern_f16.c:16-96)
+// and fp16 DW3 (src/kern_f16.c:83-155), each bit-identical to the reference, plus this library's int8 depthwise
+// (bnneon_hip.h states its specification). NHWC, channels across the lanes of a wavefront.
+//
+// Pass 1: a thread owns one channel of one "item" of an output row: a 4-pixel group (which the DWK forms compute
+// with two chains, even and odd taps) or a tail pixel / pixel pair (one chain), so every output takes exactly the
+// reference's chain for its position in the row. The thread loads its input window once into registers.
+// Pass 2: the per-channel sums (the SE mean's input) are one serial fp32 chain per channel over the whole image in
+// the reference's order; a thread per (window, channel) re-reads the outputs and adds them up that way.
+#include <string.h>
+
+#include "bnh_internal.h"
+#include "bnh_num.h"
+
+typedef _Float16 h16;
+
+BNH_DEV uint16_t hbits(h16 x) { return __builtin_bit_cast(uint16_t, x); }
+BNH_DEV h16 hfrom(uint16_t u) { return __builtin_bit_cast(h16, u); }
+BNH_DEV bool hnan(h16 x) { return x != x; }
+BNH_DEV h16 hfma(h16 a, h16 b, h16 c) { return __builtin_fmaf16(a, b, c); }
+// FMAX / FMIN on fp16 (NaN-propagating, +0 above -0)
+BNH_DEV h16 hmax(h16 a, h16 b) {
+  if (hnan(a) || hnan(b)) return hfrom(0x7e00);
+  if (a == (h16)0 && b == (h16)0) return hfrom((uint16_t)(hbits(a) & hbits(b)));
+  return a > b ? a : b;
+}
+BNH_DEV h16 hmin(h16 a, h16 b) {
+  if (hnan(a) || hnan(b)) return hfrom(0x7e00);
+  if (a == (h16)0 && b == (h16)0) return hfrom((uint16_t)(hbits(a) | hbits(b)));
+  return a < b ? a : b;
+}
+
+// The fp16 SiLU of the kernels (src/silu_lut.h:28-42): max(x, 0) - |x| q(|x|), q a piecewise quadratic in
+// f = u - round(u) on 16 unit segments, u = min(|x|, 15.4). Coefficients as fp16 bit patterns: the values of
+// src/silu_lut_tables_deg2.h. A NaN input gives NaN whichever segment it indexes.
+__constant__ uint16_t k_silu_c0[16] = {0x3800, 0x344e, 0x2fa1, 0x2a12, 0x249a, 0x1ed9, 0x1910, 0x1375,
+                                       0x0d7e, 0x080a, 0x02f9, 0x0118, 0x0067, 0x0026, 0x000e, 0x0005};
+__constant__ uint16_t k_silu_c1[16] = {0xb40b, 0xb242, 0xaecc, 0xa9ea, 0xa4a6, 0x9f03, 0x9935, 0x93b1,
+                                       0x8daa, 0x882c, 0x8312, 0x8121, 0x806a, 0x8027, 0x800e, 0x8005};
+__constant__ uint16_t k_silu_c2[16] = {0x23bd, 0x299d, 0x2915, 0x254c, 0x2073, 0x1ae1, 0x1528, 0x0fa3,
+                                       0x09a2, 0x0426, 0x0187, 0x0090, 0x0035, 0x0013, 0x0007, 0x0003};
+BNH_DEV h16 silu_lut_h(h16 x) {
+  const h16 magic = (h16)1536.0f;
+  const h16 u = hfrom((uint16_t)(hbits(x) & 0x7fff));
+  const h16 uc = hmin(u, hfrom(0x4bb3));  // (fp16)15.4f
+  const h16 tm = uc + magic;
+  const h16 f = uc - (tm - magic);
+  unsigned n = hbits(tm) & 0xffu;
+  if (n > 15) n = 0;
+  const h16 c0 = hfrom(k_silu_c0[n]), c1 = hfrom(k_silu_c1[n]), c2 = hfrom(k_silu_c2[n]);
+  h16 p = hfma(c2, f, c1);
+  p = hfma(p, f, c0);
+  return hfma(-u, p, hmax(x, (h16)0.0f));
+}
+
+// ------------------------------------------------------------------ the items of an output row
+// DWK forms: items [0, g4/4) are 4-pixel groups, then (fp32) one item per tail pixel, or (fp16) a pixel pair when
+// Wo % 4 >= 2 and a single pixel when Wo is odd. DW3 forms compute each pixel alike: items of up to 4 pixels.
+struct Item { int px, n, split; };
+BNH_DEV Item item_of(int it, int Wo, int form) {
+  const int g4 = Wo & ~3, ng = g4 >> 2;
+  Item r;
+  if (form == 2) {  // DW3: groups of 4 (the last one shorter)
+    r.px = it * 4;
+    r.n = Wo - r.px < 4 ? Wo - r.px : 4;
+    r.split = 0;
+    return r;
+  }
+  if (it < ng) { r.px = it * 4; r.n = 4; r.split = 1; return r; }
+  const int t = it - ng;
+  if (form == 0) { r.px = g4 + t; r.n = 1; r.split = 0; return r; }  // fp32: single tail pixels
+  const int two = (Wo - g4) & 2;                                        // fp16: a pair, then a single
+  if (t == 0 && two) { r.px = g4; r.n = 2; r.split = 0; return r; }
+  r.px = g4 + two;
+  r.n = 1;
+  r.split = 0;
+  return r;
+}
+static int items_per_row(int Wo, int form) {
+  const int g4 = Wo & ~3, ng = g4 >> 2, t = Wo - g4;
+  if (form == 2) return (Wo + 3) / 4;
+  if (form == 0) return ng + t;
+  return ng + ((t & 2) ? 1 : 0) + (t & 1);
+}
+
+// ------------------------------------------------------------------ fp32 DWK (form 0) and DW3 (form 2)
+// DWK: input row oy*s - pt + h + ky, column px*s - pl + h + kx of the halo-h input. DW3: the reference's three column
+// partial sums, rows oy*s + ky, columns px*s + kx of the halo-1 input (pads 1), SiLU always.
+template <int K, int S, int FORM>
+__global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, long long x_ws, int Wp, int C, int pt,
+                                                int pl, const float *__restrict__ w, const float *__restrict__ b,
+                                                int act, float *__restrict__ out, long long o_ws, int Ho, int Wo,
+                                                int nitems, long long total) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c = (int)(i % C);
+  long long r = i / C;
+  const int it = (int)(r % nitems);
+  r /= nitems;
+  const int oy = (int)(r % Ho);
+  const int win = (int)(r / Ho);
+  const Item item = item_of(it, Wo, FORM);
+  constexpr int H = (K - 1) / 2;
+  const int iy0 = FORM == 2 ? oy * S : oy * S - pt + H;
+  const int ix0 = FORM == 2 ? item.px * S : item.px * S - pl + H;
+  const float *x0 = xp + win * x_ws + ((long long)iy0 * Wp + ix0) * C + c;
+  float wv[K * K];
+#pragma unroll
+  for (int t = 0; t < K * K; t++) wv[t] = w[(long long)t * C + c];
+  const float bias = b[c];
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) v[q] = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    if (q >= item.n) break;
+    if (FORM == 2) {
+      const float *p0 = x0 + (long long)q * S * C;
+      const long long r1 = (long long)Wp * C, r2 = 2 * r1;
+      float acc = __builtin_fmaf(wv[0], p0[0], bias);
+      float acb = wv[1] * p0[C];
+      float acd = wv[2] * p0[2 * C];
+      acc = __builtin_fmaf(wv[3], p0[r1], acc);
+      acb = __builtin_fmaf(wv[4], p0[r1 + C], acb);
+      acd = __builtin_fmaf(wv[5], p0[r1 + 2 * C], acd);
+      acc = __builtin_fmaf(wv[6], p0[r2], acc);
+      acb = __builtin_fmaf(wv[7], p0[r2 + C], acb);
+      acd = __builtin_fmaf(wv[8], p0[r2 + 2 * C], acd);
+      v[q] = bnh_silu_f32(acc + (acb + acd));
+    } else {
+      float a = bias, e = 0.f;
+#pragma unroll
+      for (int ky = 0; ky < K; ky++)
+#pragma unroll
+        for (int kx = 0; kx < K; kx++) {
+          const int t = ky * K + kx;
+          const float xv = x0[((long long)ky * Wp + q * S + kx) * C];
+          if (item.split && (t & 1)) e = __builtin_fmaf(xv, wv[t], e);
+          else a = __builtin_fmaf(xv, wv[t], a);
+        }
+      float y = item.split ? a + e : a;
+      if (act == 1) y = bnh_silu_f32(y);
+      v[q] = y;
+    }
+  }
+  float *o = out + win * o_ws + ((long long)oy * Wo + item.px) * C + c;
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    if (q < item.n) o[(long long)q * C] = v[q];
+}
+
+// ------------------------------------------------------------------ fp16 DWK (form 1) and DW3 (form 2)
+template <int K, int S, int FORM>
+__global__ __launch_bounds__(256) void k_dw_f16(const h16 *__restrict__ xp, long long x_ws, int Wp, int C, int pt,
+                                                int pl, const h16 *__restrict__ w, const h16 *__restrict__ b, int act,
+                                                h16 *__restrict__ out, long long o_ws, int Ho, int Wo, int nitems,
+                                                long long total) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c = (int)(i % C);
+  long long r = i / C;
+  const int it = (int)(r % nitems);
+  r /= nitems;
+  const int oy = (int)(r % Ho);
+  const int win = (int)(r / Ho);
+  const Item item = item_of(it, Wo, FORM);
+  constexpr int H = (K - 1) / 2;
+  const int iy0 = FORM == 2 ? oy * S - pt + 1 : oy * S - pt + H;
+  const int ix0 = FORM == 2 ? item.px * S - pl + 1 : item.px * S - pl + H;
+  const h16 *x0 = xp + win * x_ws + ((long long)iy0 * Wp + ix0) * C + c;
+  h16 wv[K * K];
+#pragma unroll
+  for (int t = 0; t < K * K; t++) wv[t] = w[(long long)t * C + c];
+  const h16 bias = b[c];
+  h16 v[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) v[q] = (h16)0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    if (q >= item.n) break;
+    if (FORM == 2) {
+      const h16 *r0 = x0 + (long long)q * S * C, *r1 = r0 + (long long)Wp * C, *r2 = r1 + (long long)Wp * C;
+      h16 a = hfma(r0[0], wv[0], bias);
+      h16 a2 = r0[C] * wv[1];
+      a = hfma(r0[2 * C], wv[2], a);
+      a2 = hfma(r1[0], wv[3], a2);
+      a = hfma(r1[C], wv[4], a);
+      a2 = hfma(r1[2 * C], wv[5], a2);
+      a = hfma(r2[0], wv[6], a);
+      a2 = hfma(r2[C], wv[7], a2);
+      a = hfma(r2[2 * C], wv[8], a);
+      v[q] = silu_lut_h(a + a2);
+    } else {
+      h16 a = bias, e = (h16)0.0f;
+#pragma unroll
+      for (int ky = 0; ky < K; ky++)
+#pragma unroll
+        for (int kx = 0; kx < K; kx++) {
+          const int t = ky * K + kx;
+          const h16 xv = x0[((long long)ky * Wp + q * S + kx) * C];
+          if (item.split && (t & 1)) e = hfma(xv, wv[t], e);
+          else a = hfma(xv, wv[t], a);
+        }
+      h16 y = item.split ? a + e : a;
+      if (act == 1) y = silu_lut_h(y);
+      v[q] = y;
+    }
+  }
+  h16 *o = out + win * o_ws + ((long long)oy * Wo + item.px) * C + c;
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    if (q < item.n) o[(long long)q * C] = v[q];
+}
+
+// ------------------------------------------------------------------ channel sums (pass 2)
+// form 0 (fp32 DWK): per row, 4-groups add (o0 + o1) + (o2 + o3), tail pixels their value; form 2 (fp32 DW3): every
+// pixel in raster order; form 1 (fp16 DWK): fp16 group sums (pairs, singles) widened; form 3 (fp16 DW3): per row an
+// fp16 running sum, widened at the row's end.
+__global__ void k_chsum_f32(const float *__restrict__ out, long long o_ws, int C, int Ho, int Wo, int form,
+                            float *__restrict__ chsum, long long cs_ws, int B) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)B * C) return;
+  const int win = (int)(i / C), c = (int)(i % C);
+  const float *o = out + win * o_ws + c;
+  float cs = 0.f;
+  const int g4 = form == 0 ? (Wo & ~3) : 0;
+  for (int oy = 0; oy < Ho; oy++) {
+    const float *row = o + (long long)oy * Wo * C;
+    for (int ox = 0; ox < g4; ox += 4) {
+      const float s01 = row[(long long)ox * C] + row[(long long)(ox + 1) * C];
+      const float s23 = row[(long long)(ox + 2) * C] + row[(long long)(ox + 3) * C];
+      cs = cs + (s01 + s23);
+    }
+    for (int ox = g4; ox < Wo; ox++) cs = cs + row[(long long)ox * C];
+  }
+  chsum[win * cs_ws + c] = cs;
+}
+__global__ void k_chsum_f16(const h16 *__restrict__ out, long long o_ws, int C, int Ho, int Wo, int form,
+                            float *__restrict__ chsum, long long cs_ws, int B) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long long)B * C) return;
+  const int win = (int)(i / C), c = (int)(i % C);
+  const h16 *o = out + win * o_ws + c;
+  float cs = 0.f;
+  const int g4 = Wo & ~3, g2 = g4 + ((Wo - g4) & 2);
+  for (int oy = 0; oy < Ho; oy++) {
+    const h16 *row = o + (long long)oy * Wo * C;
+    if (form == 3) {
+      h16 rs = (h16)0.0f;
+      for (int ox = 0; ox < Wo; ox++) rs = rs + row[(long long)ox * C];
+      cs = cs + (float)rs;
+      continue;
+    }
+    for (int ox = 0; ox < g4; ox += 4) {
+      const h16 s = (row[(long long)ox * C] + row[(long long)(ox + 1) * C]) +
+                    (row[(long long)(ox + 2) * C] + row[(long long)(ox + 3) * C]);
+      cs = cs + (float)s;
+    }
+    if (g2 > g4) cs = cs + (float)(row[(long long)g4 * C] + row[(long long)(g4 + 1) * C]);
+    if (Wo > g2) cs = cs + (float)row[(long long)g2 * C];
+  }
+  chsum[win * cs_ws + c] = cs;
+}
+
+// ------------------------------------------------------------------ int8 depthwise (own specification)
+// a thread owns 4 channels (one 32-bit word of every pixel) of one output pixel
+template <int K, int S>
+__global__ __launch_bounds__(256) void k_dw_s8(const int8_t *__restrict__ x, long long x_ws, int H, int W, int C, int pt,
+                                               int pl, const int8_t *__restrict__ w, const int32_t *__restrict__ bias,
+                                               const int32_t *__restrict__ mult, const int32_t *__restrict__ shift,
+                                               int zx, int zy, int lo, int hi, const int8_t *__restrict__ lut,
+                                               int8_t *__restrict__ out, long long o_ws, int Ho, int Wo,
+                                               long long total) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int C4 = C >> 2;
+  const int c4 = (int)(i % C4);
+  long long r = i / C4;
+  const int ox = (int)(r % Wo);
+  r /= Wo;
+  const int oy = (int)(r % Ho);
+  const int win = (int)(r / Ho);
+  const int c = c4 * 4;
+  int32_t acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) acc[j] = bias[c + j];
+  const int8_t *xw = x + win * x_ws;
+#pragma unroll
+  for (int ky = 0; ky < K; ky++) {
+    const int iy = oy * S - pt + ky;
+    if (iy < 0 || iy >= H) continue;
+#pragma unroll
+    for (int kx = 0; kx < K; kx++) {
+      const int ix = ox * S - pl + kx;
+      if (ix < 0 || ix >= W) continue;
+      const uint32_t xv = *(const uint32_t *)(xw + ((long long)iy * W + ix) * C + c);
+      const uint32_t wv = *(const uint32_t *)(w + (long long)(ky * K + kx) * C + c);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[j] = (int32_t)((uint32_t)acc[j] + (uint32_t)((int32_t)(int8_t)(wv >> (8 * j)) *
+                                                          ((int32_t)(int8_t)(xv >> (8 * j)) - zx)));
+    }
+  }
+  uint32_t word = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    int32_t y = bnh_requant(acc[j], mult[c + j], shift[c + j], zy, lo, hi);
+    if (lut) y = lut[y + 128];
+    word |= ((uint32_t)y & 0xffu) << (8 * j);
+  }
+  *(uint32_t *)(out + win * o_ws + ((long long)oy * Wo + ox) * C + c) = word;
+}
+
+// ================================================================== host side
+template <typename T, typename L>
+static void dispatch_ks(int k, int s, L &&launch) {
+  if (k == 1 && s == 1) launch.template operator()<1, 1>();
+  else if (k == 1 && s == 2) launch.template operator()<1, 2>();
+  else if (k == 3 && s == 1) launch.template operator()<3, 1>();
+  else if (k == 3 && s == 2) launch.template operator()<3, 2>();
+  else if (k == 5 && s == 1) launch.template operator()<5, 1>();
+  else if (k == 5 && s == 2) launch.template operator()<5, 2>();
+  else if (k == 7 && s == 1) launch.template operator()<7, 1>();
+  else launch.template operator()<7, 2>();
+}
+
+static int dw_check(int H, int W, int C, int k, int s, int pt, int pl, int Ho, int Wo, int B, long long x_ws,
+                    long long o_ws, int halo) {
+  BNH_REQ(H > 0 && W > 0 && C > 0 && Ho > 0 && Wo > 0 && B > 0);
+  BNH_REQ(k == 1 || k == 3 || k == 5 || k == 7);
+  BNH_REQ(s == 1 || s == 2);
+  const int h = halo;
+  BNH_REQ(pt >= 0 && pt <= h && pl >= 0 && pl <= h);
+  BNH_REQ((Ho - 1) * s - pt + k <= H + h && (Wo - 1) * s - pl + k <= W + h);  // the last tap stays in the halo
+  BNH_REQ(B == 1 || (x_ws >= (long long)(H + 2 * h) * (W + 2 * h) * C && o_ws >= (long long)Ho * Wo * C));
+  BNH_REQ((long long)B * Ho * Wo * C / 256 < (1LL << 31));
+  return 0;
+}
+
+extern "C" {
+
+int bnh_dwk_f32(const float *xp, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl, const float *w,
+                const float *b, int act, float *out, long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws,
+                int B, void *stream) {
+  BNH_REQ(xp && w && b && out && (act == 0 || act == 1));
+  if (dw_check(H, W, C, k, s, pt, pl, Ho, Wo, B, x_ws, o_ws, (k - 1) / 2)) return -1;
+  const int nit = items_per_row(Wo, 0);
+  const long long total = (long long)B * Ho * nit * C;
+  hipStream_t st = bnh_stream(stream);
+  const int Wp = W + k - 1;
+  dispatch_ks<float>(k, s, [&]<int K, int S>() {
+    hipLaunchKernelGGL((k_dw_f32<K, S, 0>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, xp, x_ws, Wp, C,
+                       pt, pl, w, b, act, out, o_ws, Ho, Wo, nit, total);
+  });
+  BNH_HIP(hipGetLastError());
+  if (chsum) {
+    BNH_REQ(B == 1 || cs_ws >= C);
+    hipLaunchKernelGGL(k_chsum_f32, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st, out, o_ws, C,
+                       Ho, Wo, 0, chsum, cs_ws, B);
+    BNH_HIP(hipGetLastError());
+  }
+  return 0;
+}
+
+int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, const float *w, const float *b, float *out,
+                long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws, int B, void *stream) {
+  BNH_REQ(xp && w && b && out);
+  if (dw_check(H, W, C, 3, s, 1, 1, Ho, Wo, B, x_ws, o_ws, 1)) return -1;
+  const int nit = items_per_row(Wo, 2);
+  const long long total = (long long)B * Ho * nit * C;
+  hipStream_t st = bnh_stream(stream);
+  if (s == 1)
+    hipLaunchKernelGGL((k_dw_f32<3, 1, 2>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, xp, x_ws, W + 2,
+                       C, 1, 1, w, b, 1, out, o_ws, Ho, Wo, nit, total);
+  else
+    hipLaunchKernelGGL((k_dw_f32<3, 2, 2>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, xp, x_ws, W + 2,
+                       C, 1, 1, w, b, 1, out, o_ws, Ho, Wo, nit, total);
+  BNH_HIP(hipGetLastError());
+  if (chsum) {
+    BNH_REQ(B == 1 || cs_ws >= C);
+    hipLaunchKernelGGL(k_chsum_f32, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st, out, o_ws, C,
+                       Ho, Wo, 2, chsum, cs_ws, B);
+    BNH_HIP(hipGetLastError());
+  }
+  return 0;
+}
+
+int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl,
+                const uint16_t *w, const uint16_t *b, int act, uint16_t *out, long long o_ws, int Ho, int Wo,
+                float *chsum, long long cs_ws, int B, void *stream) {
+  BNH_REQ(xp && w && b && out && (act == 0 || act == 1));
+  if (dw_check(H, W, C, k, s, pt, pl, Ho, Wo, B, x_ws, o_ws, (k - 1) / 2)) return -1;
+  const int nit = items_per_row(Wo, 1);
+  const long long total = (long long)B * Ho * nit * C;
+  hipStream_t st = bnh_stream(stream);
+  const int Wp = W + k - 1;
+  dispatch_ks<h16>(k, s, [&]<int K, int S>() {
+    hipLaunchKernelGGL((k_dw_f16<K, S, 1>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st,
+                       (const h16 *)xp, x_ws, Wp, C, pt, pl, (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, Ho,
+                       Wo, nit, total);
+  });
+  BNH_HIP(hipGetLastError());
+  if (chsum) {
+    BNH_REQ(B == 1 || cs_ws >= C);
+    hipLaunchKernelGGL(k_chsum_f16, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st,
+                       (const h16 *)out, o_ws, C, Ho, Wo, 1, chsum, cs_ws, B);
+    BNH_HIP(hipGetLastError());
+  }
+  return 0;
+}
+
+int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, int pt, int pl, const uint16_t *w,
+                const uint16_t *b, uint16_t *out, long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws, int B,
+                void *stream) {
+  BNH_REQ(xp && w && b && out && pt >= 0 && pt <= 1 && pl >= 0 && pl <= 1);
+  if (dw_check(H, W, C, 3, s, pt, pl, Ho, Wo, B, x_ws, o_ws, 1)) return -1;
+  const int nit = items_per_row(Wo, 2);
+  const long long total = (long long)B * Ho * nit * C;
+  hipStream_t st = bnh_stream(stream);
+  if (s == 1)
+    hipLaunchKernelGGL((k_dw_f16<3, 1, 2>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, (const h16 *)xp,
+                       x_ws, W + 2, C, pt, pl, (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total);
+  else
+    hipLaunchKernelGGL((k_dw_f16<3, 2, 2>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, (const h16 *)xp,
+                       x_ws, W + 2, C, pt, pl, (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total);
+  BNH_HIP(hipGetLastError());
+  if (chsum) {
+    BNH_REQ(B == 1 || cs_ws >= C);
+    hipLaunchKernelGGL(k_chsum_f16, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st,
+                       (const h16 *)out, o_ws, C, Ho, Wo, 3, chsum, cs_ws, B);
+    BNH_HIP(hipGetLastError());
+  }
+  return 0;
+}
+
+int bnh_dw_s8(const int8_t *x, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl, const int8_t *w,
+              const int32_t *bias, const int32_t *mult, const int32_t *shift, int zx, int zy, int lo, int hi,
+              const int8_t *lut, int8_t *out, long long o_ws, int Ho, int Wo, int B, void *stream) {
+  BNH_REQ(x && w && bias && mult && shift && out && H > 0 && W > 0 && Ho > 0 && Wo > 0 && B > 0);
+  BNH_REQ(C > 0 && C % 4 == 0 && (k == 1 || k == 3 || k == 5 || k == 7) && (s == 1 || s == 2));
+  BNH_REQ(pt >= 0 && pl >= 0 && pt < k && pl < k && lo >= -128 && hi <= 127 && lo <= hi);
+  BNH_REQ(((uintptr_t)x & 3) == 0 && ((uintptr_t)w & 3) == 0 && ((uintptr_t)out & 3) == 0);
+  BNH_REQ(B == 1 || (x_ws % 4 == 0 && o_ws % 4 == 0 && x_ws >= (long long)H * W * C && o_ws >= (long long)Ho * Wo * C));
+  const long long total = (long long)B * Ho * Wo * (C / 4);
+  hipStream_t st = bnh_stream(stream);
+  dispatch_ks<int8_t>(k, s, [&]<int K, int S>() {
+    hipLaunchKernelGGL((k_dw_s8<K, S>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, x, x_ws, H, W, C, pt,
+                       pl, w, bias, mult, shift, zx, zy, lo, hi, lut, out, o_ws, Ho, Wo, total);
+  });
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"

@@ -319,6 +319,113 @@ __global__ __launch_bounds__(256) void k_gemm_s8_requant(const int8_t *__restric
   }
 }
 
+// Version 2: a block owns 128 pixels x 256 channels, so every activation byte is fetched from HBM once and every
+// staged k row is one whole 128-byte line. Both operands go through LDS (rows of 64 k bytes at an 80-byte stride:
+// the 16 rows a ds_read_b128 serves land on 16 disjoint 4-bank groups), prefetched into registers while the MFMAs of
+// the current step run. 4 waves as 2 (pixels) x 2 (channels), each 64 pixels x 128 channels = 4 x 8 MFMA tiles.
+#define RQ2_PIX 128
+#define RQ2_CH 256
+#define RQ2_LDS (RQ2_PIX * RQ_LDS_STRIDE + RQ2_CH * RQ_LDS_STRIDE)
+__global__ __launch_bounds__(256, 2) void k_gemm_s8_requant2(const int8_t *__restrict__ x, long long x_ws, int M, int K,
+                                                          int tiles_per_window, const int8_t *__restrict__ wt,
+                                                          const int32_t *__restrict__ bias_eff,
+                                                          const int32_t *__restrict__ mult,
+                                                          const int32_t *__restrict__ shift, int N, int zy, int lo,
+                                                          int hi, int8_t *__restrict__ out, long long out_ws) {
+  __shared__ __attribute__((aligned(16))) int8_t lds[2][RQ2_LDS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int win = blockIdx.x / tiles_per_window;
+  const int p0 = (blockIdx.x % tiles_per_window) * RQ2_PIX;
+  const int n0 = blockIdx.y * RQ2_CH;
+  const int8_t *xw = x + win * x_ws;
+  // activation staging: pixel quad pq (32 of them: one 128-byte line per k row), k quads kq and kq + 8
+  const int pq = tid & 31, kq = tid >> 5;
+  const int px = p0 + 4 * pq;
+  const bool pin = px < M;  // M % 4 == 0
+  // weight staging: channel row n0 + tid, 64 k bytes as 4 x 16
+  const int8_t *wrow = wt + (long long)(n0 + tid) * K;
+  const int kc = (lane >> 4) * 16;
+  uint32_t rx[2][4];
+  v4i rw[4];
+  auto fetch = [&](int k0) {  // K % 16 == 0: a 4-row quad, a 16-byte weight chunk is all in or all out
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int k = k0 + 4 * (kq + 8 * h);
+      const bool in = pin && k < K;
+      const int8_t *src = xw + (long long)(in ? k : 0) * M + (in ? px : 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) rx[h][i] = *(const uint32_t *)(src + (in ? (long long)i * M : 0));
+      if (!in) rx[h][0] = rx[h][1] = rx[h][2] = rx[h][3] = 0u;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const bool in = k0 + 16 * c < K;
+      rw[c] = *(const v4i *)(wrow + (in ? k0 + 16 * c : 0));
+      if (!in) rw[c] = (v4i){0, 0, 0, 0};
+    }
+  };
+  auto stage = [&](int8_t *buf) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      uint32_t c[4];
+      transpose4x4(rx[h][0], rx[h][1], rx[h][2], rx[h][3], c);
+#pragma unroll
+      for (int j = 0; j < 4; j++) *(uint32_t *)(buf + (4 * pq + j) * RQ_LDS_STRIDE + 4 * (kq + 8 * h)) = c[j];
+    }
+    int8_t *wb = buf + RQ2_PIX * RQ_LDS_STRIDE + tid * RQ_LDS_STRIDE;
+#pragma unroll
+    for (int c = 0; c < 4; c++) *(v4i *)(wb + 16 * c) = rw[c];
+  };
+  v4i acc[4][8];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[t][j] = (v4i){0, 0, 0, 0};
+  fetch(0);
+  stage(lds[0]);
+  __syncthreads();
+  int cur = 0;
+  for (int k0 = 0; k0 < K; k0 += 64) {
+    const bool more = k0 + 64 < K;
+    if (more) fetch(k0 + 64);  // in flight during this step's MFMAs
+    const int8_t *xs = lds[cur], *ws = lds[cur] + RQ2_PIX * RQ_LDS_STRIDE;
+    v4i a[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) a[t] = *(const v4i *)(xs + (wm * 64 + 16 * t + (lane & 15)) * RQ_LDS_STRIDE + kc);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const v4i b = *(const v4i *)(ws + (wn * 128 + 16 * j + (lane & 15)) * RQ_LDS_STRIDE + kc);
+#pragma unroll
+      for (int t = 0; t < 4; t++) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b, acc[t][j], 0, 0, 0);
+    }
+    if (more) {
+      stage(lds[cur ^ 1]);  // the other buffer: last read two steps ago, before the previous barrier
+      __syncthreads();
+      cur ^= 1;
+    }
+  }
+  int8_t *ow = out + win * out_ws;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int n = n0 + wn * 128 + 16 * j + (lane & 15);
+    if (n >= N) continue;
+    const int32_t be = bias_eff[n], mu = mult[n], sh = shift[n];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const int p = p0 + wm * 64 + 16 * t + 4 * (lane >> 4);
+      if (p >= M) continue;
+      uint32_t word = 0;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int32_t a32 = (int32_t)((uint32_t)acc[t][j][r] + (uint32_t)be);
+        word |= ((uint32_t)bnh_requant(a32, mu, sh, zy, lo, hi) & 0xffu) << (8 * r);
+      }
+      *(uint32_t *)(ow + (long long)n * M + p) = word;
+    }
+  }
+}
+
 // ------------------------------------------------------------------ numerics probe
 __global__ void k_eval_f32(int f, const float *__restrict__ x, float *__restrict__ y, long long n) {
   long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -455,7 +562,7 @@ bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const i
       bnh_fail("bnh_q8w_new: shift[%d] = %d: expected a right shift in [0, 31]", n, shift[n]);
       return nullptr;
     }
-  const int Nt = (int)bnh_round_up(N, 128);
+  const int Nt = (int)bnh_round_up(N, RQ2_CH);  // every staging thread of a block owns one weight row
   int8_t *hw = (int8_t *)calloc((size_t)Nt * K, 1);
   int32_t *hb = (int32_t *)calloc(Nt, 4), *hm = (int32_t *)calloc(Nt, 4), *hs = (int32_t *)calloc(Nt, 4);
   bnh_q8w *W = (bnh_q8w *)calloc(1, sizeof *W);
@@ -497,9 +604,9 @@ int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M
   BNH_REQ(M % 4 == 0 && ((uintptr_t)x & 3) == 0 && ((uintptr_t)out & 3) == 0);
   BNH_REQ(B == 1 || (x_ws % 4 == 0 && out_ws % 4 == 0 && x_ws >= (long long)W->K * M && out_ws >= (long long)W->N * M));
   BNH_REQ(W->K % 16 == 0);
-  const int tpw = (int)bnh_ceil_div(M, 64);
-  dim3 grid((unsigned)((long long)tpw * B), (unsigned)bnh_ceil_div(W->N, 128));
-  hipLaunchKernelGGL(k_gemm_s8_requant, grid, dim3(256), 0, bnh_stream(stream), x, x_ws, M, W->K, tpw, W->w,
+  const int tpw = (int)bnh_ceil_div(M, RQ2_PIX);
+  dim3 grid((unsigned)((long long)tpw * B), (unsigned)bnh_ceil_div(W->N, RQ2_CH));
+  hipLaunchKernelGGL(k_gemm_s8_requant2, grid, dim3(256), 0, bnh_stream(stream), x, x_ws, M, W->K, tpw, W->w,
                      W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
   BNH_HIP(hipGetLastError());
   return 0;

@@ -12,6 +12,7 @@
 #include <time.h>
 #include <unistd.h>
 
+#include "bnneon_hip.h"
 #include "rt.h"
 
 struct rt_pkg {
@@ -519,8 +520,9 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
     if (r) {
       char src[160];
       rt_op_src(c, i, src, sizeof src);
+      const char *why = bnh_last_error();
       snprintf(err, errlen, "op %d %s%s%s%s: launch failed (%s)", i, op->k->name, src[0] ? " (ONNX node " : "", src,
-               src[0] ? ")" : "", hipGetErrorString(hipGetLastError()));
+               src[0] ? ")" : "", why && why[0] ? why : hipGetErrorString(hipGetLastError()));
       return -1;
     }
     if (c->prof) {

@@ -112,6 +112,35 @@ void bnh_q8w_free(bnh_q8w *W);
 int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M, int B, int8_t *out,
                         long long out_ws, void *stream);
 
+/* ------------------------------------------------------------------ depthwise convolutions
+ * NHWC, weights [k*k][C] (tap-major), per-window strides in elements. xp is the zero-haloed input of the reference's
+ * buffers: [H + 2h][W + 2h][C], h = (k - 1) / 2 (1 for the DW3 forms); output pixel (oy, ox) reads the k x k taps
+ * from halo row oy*s - pt + h, column ox*s - pl + h. chsum (optional, fp32 [C] per window) receives the per-channel
+ * sum of the outputs in the reference's order (the SE block's mean input). Every result is bit-identical to the
+ * reference's NEON kernel. act: 0 none, 1 SiLU. */
+/* DWK fp32, k in {1, 3, 5, 7}, s in {1, 2}: replaces dwk_f32_run (src/pc_kern_f32.c:163-334) */
+int bnh_dwk_f32(const float *xp, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl, const float *w,
+                const float *b, int act, float *out, long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws,
+                int B, void *stream);
+/* DW3 fp32 (3x3, pads 1, SiLU): replaces dw3_f32 / dw3s2_f32 (src/gemm_f32.c:213-441) */
+int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, const float *w, const float *b, float *out,
+                long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws, int B, void *stream);
+/* DWK fp16 (values as fp16 bit patterns): replaces dwk_f16_run (src/pc_kern_f16.c:16-96) */
+int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl,
+                const uint16_t *w, const uint16_t *b, int act, uint16_t *out, long long o_ws, int Ho, int Wo,
+                float *chsum, long long cs_ws, int B, void *stream);
+/* DW3 fp16 (3x3, SiLU, pads pt / pl in {0, 1}): replaces dw3_f16 (src/kern_f16.c:83-155) */
+int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, int pt, int pl, const uint16_t *w,
+                const uint16_t *b, uint16_t *out, long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws, int B,
+                void *stream);
+/* int8 depthwise: no counterpart in the reference (its depthwise layers are fp32 / fp16); the static int8 form of
+ * the same layer. x int8 [H][W][C] unpadded (C % 4 == 0), taps outside the image skipped (a zero-point pad):
+ *   acc = bias[c] + sum_taps w[t][c] (x - zx);  y = clamp(RDBYPOT(SRDHM(acc, mult[c]), shift[c]) + zy, lo, hi);
+ *   out = lut ? lut[y + 128] : y   (lut: an int8 -> int8 activation table, e.g. SiLU) */
+int bnh_dw_s8(const int8_t *x, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl, const int8_t *w,
+              const int32_t *bias, const int32_t *mult, const int32_t *shift, int zx, int zy, int lo, int hi,
+              const int8_t *lut, int8_t *out, long long o_ws, int Ho, int Wo, int B, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,30 @@ int orc_proto_s8(const float *x, int P, int C, int ld, float eps, int8_t *qa, in
                  const float *sw, int Np, float *colmax, const float *clsw, const float *clsb, int nc, int ppc,
                  float *logits);
 
+/* ---------------------------------------------------------------- depthwise convolutions */
+/* fp16 values as bit patterns; one rounding to nearest even per operation, denormals kept */
+float orc_h2f(uint16_t h);
+uint16_t orc_h_fma(uint16_t a, uint16_t b, uint16_t c);   /* a * b + c */
+uint16_t orc_h_add(uint16_t a, uint16_t b);
+uint16_t orc_h_mul(uint16_t a, uint16_t b);
+uint16_t orc_silu_lut_h(uint16_t x);                       /* src/silu_lut.h:28-42 */
+/* src/pc_kern_f32.c:163-334 (DWK fp32) */
+void orc_dwk_f32(const float *xp, int H, int W, int C, int k, int s, int pt, int pl, const float *w, const float *b,
+                 int act, float *out, int Ho, int Wo, float *chsum);
+/* src/gemm_f32.c:213-441 (DW3 fp32: pads 1, SiLU) */
+void orc_dw3_f32(const float *xp, int H, int W, int C, int s, const float *w, const float *b, float *out, int Ho,
+                 int Wo, float *chsum);
+/* src/pc_kern_f16.c:16-96 (DWK fp16) */
+void orc_dwk_f16(const uint16_t *xp, int H, int W, int C, int k, int s, int pt, int pl, const uint16_t *w,
+                 const uint16_t *b, int act, uint16_t *out, int Ho, int Wo, float *chsum);
+/* src/kern_f16.c:83-155 (DW3 fp16: SiLU) */
+void orc_dw3_f16(const uint16_t *xp, int H, int W, int C, int s, int pt, int pl, const uint16_t *w, const uint16_t *b,
+                 uint16_t *out, int Ho, int Wo, float *chsum);
+/* int8 depthwise: this project's own specification (no reference kernel); dw.c states it */
+void orc_dw_s8(const int8_t *x, int H, int W, int C, int k, int s, int pt, int pl, const int8_t *w, const int32_t *bias,
+               const int32_t *mult, const int32_t *shift, int zx, int zy, int lo, int hi, const int8_t *lut, int8_t *out,
+               int Ho, int Wo);
+
 /* ---------------------------------------------------------------- Q31 requantised int8 GEMM (own specification)
  * The reference has no such kernel. Specification (TFLite / gemmlowp fixed-point conventions):
  *   acc[n][m]  = sum_k w[n][k] * (x[k][m] - zx) + bias[n]                       (exact, int32)

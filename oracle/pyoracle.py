@@ -199,3 +199,74 @@ def n4_check(qw, Kp, n4):
     qw = np.ascontiguousarray(qw, np.int8)
     n4 = np.ascontiguousarray(n4, np.uint8)
     return lib().orc_proto_n4_check(qw.ctypes.data, Kp, n4.ctypes.data, n4.size)
+
+
+u16 = C.c_uint16
+_SIGS.update({
+    "orc_h2f": (f32, [u16]),
+    "orc_h_fma": (u16, [u16, u16, u16]),
+    "orc_h_add": (u16, [u16, u16]),
+    "orc_h_mul": (u16, [u16, u16]),
+    "orc_silu_lut_h": (u16, [u16]),
+    "orc_dwk_f32": (None, [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, i32, vp, i32, i32, vp]),
+    "orc_dw3_f32": (None, [vp, i32, i32, i32, i32, vp, vp, vp, i32, i32, vp]),
+    "orc_dwk_f16": (None, [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, i32, vp, i32, i32, vp]),
+    "orc_dw3_f16": (None, [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp, i32, i32, vp]),
+    "orc_dw_s8": (None, [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, i32, i32, i32, vp,
+                         vp, i32, i32]),
+})
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dt)
+
+
+def dwk_f32(xp, H, W, C, k, s, pt, pl, w, b, act, Ho, Wo):
+    """orc_dwk_f32 on a haloed input xp [(H+2h)][(W+2h)][C] -> (out, chsum)."""
+    xp, w, b = _c(xp, np.float32), _c(w, np.float32), _c(b, np.float32)
+    out = np.zeros((Ho, Wo, C), np.float32)
+    cs = np.zeros(C, np.float32)
+    lib().orc_dwk_f32(xp.ctypes.data, H, W, C, k, s, pt, pl, w.ctypes.data, b.ctypes.data, act,
+                      out.ctypes.data, Ho, Wo, cs.ctypes.data)
+    return out, cs
+
+
+def dw3_f32(xp, H, W, C, s, w, b, Ho, Wo):
+    xp, w, b = _c(xp, np.float32), _c(w, np.float32), _c(b, np.float32)
+    out = np.zeros((Ho, Wo, C), np.float32)
+    cs = np.zeros(C, np.float32)
+    lib().orc_dw3_f32(xp.ctypes.data, H, W, C, s, w.ctypes.data, b.ctypes.data, out.ctypes.data, Ho, Wo,
+                      cs.ctypes.data)
+    return out, cs
+
+
+def dwk_f16(xp, H, W, C, k, s, pt, pl, w, b, act, Ho, Wo):
+    """fp16 arrays (numpy float16) in and out."""
+    xp, w, b = _c(xp, np.float16), _c(w, np.float16), _c(b, np.float16)
+    out = np.zeros((Ho, Wo, C), np.float16)
+    cs = np.zeros(C, np.float32)
+    lib().orc_dwk_f16(xp.ctypes.data, H, W, C, k, s, pt, pl, w.ctypes.data, b.ctypes.data, act,
+                      out.ctypes.data, Ho, Wo, cs.ctypes.data)
+    return out, cs
+
+
+def dw3_f16(xp, H, W, C, s, pt, pl, w, b, Ho, Wo):
+    xp, w, b = _c(xp, np.float16), _c(w, np.float16), _c(b, np.float16)
+    out = np.zeros((Ho, Wo, C), np.float16)
+    cs = np.zeros(C, np.float32)
+    lib().orc_dw3_f16(xp.ctypes.data, H, W, C, s, pt, pl, w.ctypes.data, b.ctypes.data, out.ctypes.data,
+                      Ho, Wo, cs.ctypes.data)
+    return out, cs
+
+
+def dw_s8(x, k, s, pt, pl, w, bias, mult, shift, zx, zy, lo, hi, lut, Ho, Wo):
+    x = _c(x, np.int8)
+    H, W, C = x.shape
+    w, bias = _c(w, np.int8), _c(bias, np.int32)
+    mult, shift = _c(mult, np.int32), _c(shift, np.int32)
+    lut_a = None if lut is None else _c(lut, np.int8)
+    out = np.zeros((Ho, Wo, C), np.int8)
+    lib().orc_dw_s8(x.ctypes.data, H, W, C, k, s, pt, pl, w.ctypes.data, bias.ctypes.data, mult.ctypes.data,
+                    shift.ctypes.data, zx, zy, lo, hi, None if lut_a is None else lut_a.ctypes.data,
+                    out.ctypes.data, Ho, Wo)
+    return out

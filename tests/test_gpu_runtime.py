@@ -164,3 +164,46 @@ def test_contract_violations_are_refused(hip, tmp_path):
         binding.Model(str(bad))
     assert "int8 GEMM shape" in str(e.value) and "op 0 pw_s8n" in str(e.value)
     assert r["paths"][0]["ops"][0][0] == 22
+
+
+@pytest.mark.parametrize("form,k,s", [("dwk", 5, 2), ("dwk", 3, 1), ("dwk", 7, 1), ("dw3", 3, 1), ("dw3", 3, 2)])
+def test_pw_s8_into_depthwise(hip, tmp_path, form, k, s):
+    """PW_S8 writing a zero-haloed output, then the fp32 depthwise op reading it:
+    the depthwise output and its channel sums (as the embedding) bit for bit."""
+    rng = np.random.default_rng(k * 10 + s)
+    H, W, K0, N = 10, 13, 40, 24
+    h = (k - 1) // 2
+    w1 = rng.standard_normal((N, K0)).astype(np.float32) * 0.3
+    b1 = rng.standard_normal(N).astype(np.float32) * 0.1
+    wd = (rng.standard_normal((k * k, N)) * 0.4).astype(np.float32)
+    bd = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    pkg = pkgfmt.Package()
+    net = netbuild.Net(pkg)
+    ib = net.buf(netbuild.F32, H * W, 1, K0)
+    h1 = net.pw_s8(ib, w1, b1, act="silu", H=H, W=W, opad=h)
+    if form == "dwk":
+        ob, cb = net.dwk(h1, wd, bd, k, s)
+    else:
+        ob, cb = net.dw3(h1, wd, bd, s)
+    _, Ho, Wo = net.bufs[ob][:3]
+    net.add_to("neon-int8", 0, in_buf=ib, out_buf=ob, emb_buf=cb)
+    netbuild.standard_meta(pkg, H * W * K0, Ho * Wo * N, model_id="synthetic_dw", emb_dim=N)
+    path = str(tmp_path / "dw.bnpk")
+    pkg.write(path)
+    pcm = rng.standard_normal((5, H * W * K0)).astype(np.float32)
+    say("runtime", form, k, s)
+    pk = s8pack.pack_s8(w1, b1)
+    with binding.Model(path) as m:
+        out, emb, status = m.infer_batch(pcm)
+        assert not status.any()
+    for i in range(5):
+        xp, *_ = O.pw_s8(pcm[i].reshape(H * W, K0), pk, act=1, ow=W, opad=h)
+        xp = xp.reshape(H + 2 * h, W + 2 * h, N)
+        if form == "dwk":
+            pt = max((Ho - 1) * s + k - H, 0) // 2
+            pl = max((Wo - 1) * s + k - W, 0) // 2
+            ro, rc = O.dwk_f32(xp, H, W, N, k, s, pt, pl, wd, bd, 1, Ho, Wo)
+        else:
+            ro, rc = O.dw3_f32(xp, H, W, N, s, wd, bd, Ho, Wo)
+        assert same(out[i], ro.reshape(-1)), i
+        assert same(emb[i], rc), i
