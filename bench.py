@@ -224,7 +224,7 @@ def main():
         bytes_per_launch = B * (K * M + N * M) + N * K + 3 * 4 * N
         workload = ("int8 pointwise conv 1152->256 over 24x64 pixels per window, NCHW int8 "
                     "activations (zero point -128), per-channel Q31 requant, int8 out")
-        kernel = "k_gemm_s8_requant"
+        kernel = "k_gemm_s8_requant4"
         dtype = "int8"
     else:
         sys.path.insert(0, os.path.join(ROOT, "birdnet-neon-engine_amd"))

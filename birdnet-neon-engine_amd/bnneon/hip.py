@@ -43,6 +43,7 @@ _SIGS = {
     "bnh_event_record": (i32, [vp, vp]),
     "bnh_event_ms": (C.c_float, [vp, vp]),
     "bnh_eval_f32": (i32, [i32, vp, vp, i64, vp]),
+    "bnh_eval_requant": (i32, [vp, vp, vp, i32, i32, i32, vp, i64, vp]),
     "bnh_copy": (i32, [vp, vp, C.c_size_t, vp]),
     "bnh_s8w_new": (vp, [i32, i32, i32, i32, vp, vp, vp, vp]),
     "bnh_s8w_free": (None, [vp]),

@@ -122,21 +122,19 @@ BNH_DEV float bnh_silu_f32(float x) {
 // ReLU as vmaxq_f32(y, 0): -0 -> +0, NaN stays NaN
 BNH_DEV float bnh_relu_f32(float y) { return bnh_fmax(y, 0.f); }
 
-// gemmlowp fixed point (the Q31 requant specification of the int8 GEMM / depthwise of this library)
-BNH_DEV int32_t bnh_srdhm(int32_t a, int32_t b) {
-  if (a == INT32_MIN && b == INT32_MIN) return INT32_MAX;
-  int64_t ab = (int64_t)a * (int64_t)b;
-  int64_t nudge = ab >= 0 ? (1LL << 30) : (1 - (1LL << 30));
-  return (int32_t)((ab + nudge) / (1LL << 31));
-}
-BNH_DEV int32_t bnh_rdbypot(int32_t x, int e) {
-  int32_t mask = (int32_t)((1u << e) - 1u);
-  int32_t rem = x & mask;
-  int32_t thr = (mask >> 1) + (x < 0 ? 1 : 0);
-  return (x >> e) + (rem > thr ? 1 : 0);
-}
+// gemmlowp fixed point (the Q31 requant specification of the int8 GEMM / depthwise of this library), in closed
+// forms that need one 64-bit multiply-add and no branches:
+//  * SaturatingRoundingDoublingHighMul(a, b) = (a b + nudge) / 2^31 truncated, nudge = 2^30 for a b >= 0 and
+//    1 - 2^30 below; both cases equal floor((a b + 2^30) / 2^31) (for a b < 0 the truncation of n = a b + 1 - 2^30 is
+//    floor((n + 2^31 - 1) / 2^31)); the one overflow, INT32_MIN x INT32_MIN, saturates to INT32_MAX.
+//  * RoundingDivideByPOT(x, e) (round half away from zero) = floor((x + 2^(e-1) - [x < 0]) / 2^e) for e >= 1, x for
+//    e = 0.
 BNH_DEV int32_t bnh_requant(int32_t acc, int32_t mult, int shift, int zy, int lo, int hi) {
-  int64_t v = (int64_t)bnh_rdbypot(bnh_srdhm(acc, mult), shift) + zy;
-  return (int32_t)(v < lo ? lo : v > hi ? hi : v);
+  const int64_t p = (int64_t)acc * mult + (1LL << 30);
+  int32_t r = (int32_t)(p >> 31);
+  r = (acc == INT32_MIN) & (mult == INT32_MIN) ? INT32_MAX : r;
+  const int64_t t = (int64_t)r + (shift ? (1LL << (shift - 1)) - (r < 0 ? 1 : 0) : 0);
+  const int32_t v = __builtin_elementwise_add_sat((int32_t)(t >> shift), zy);
+  return v < lo ? lo : v > hi ? hi : v;
 }
 #endif

@@ -28,8 +28,8 @@ struct bnh_s8w {
 };
 
 struct bnh_q8w {
-  int N, K, Nt, zx, zy, lo, hi;
-  int8_t *w;          // [Nt][K]
+  int N, K, Kt, Nt, zx, zy, lo, hi;
+  int8_t *w;          // [Nt][Kt], zero past K (Kt = K rounded up to 64) and past N
   int32_t *bias_eff;  // [Nt]: bias[n] - zx * sum_k w[n][k] (wrapping int32)
   int32_t *mult, *shift;
 };
@@ -243,81 +243,6 @@ BNH_DEV void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, ui
 }
 
 #define RQ_LDS_STRIDE 80  // bytes per staged pixel row: 64 k + 16 pad
-__global__ __launch_bounds__(256) void k_gemm_s8_requant(const int8_t *__restrict__ x, long long x_ws, int M, int K,
-                                                         int tiles_per_window, const int8_t *__restrict__ wt,
-                                                         const int32_t *__restrict__ bias_eff,
-                                                         const int32_t *__restrict__ mult,
-                                                         const int32_t *__restrict__ shift, int N, int zy, int lo,
-                                                         int hi, int8_t *__restrict__ out, long long out_ws) {
-  __shared__ __attribute__((aligned(16))) int8_t xs[64 * RQ_LDS_STRIDE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves: 64 pixels x 128 channels
-  const int win = blockIdx.x / tiles_per_window;
-  const int p0 = (blockIdx.x % tiles_per_window) * 64;
-  const int n0 = blockIdx.y * 128 + wn * 64;
-  const int8_t *xw = x + win * x_ws;
-  // staging: thread -> pixel quad pq (16 of them), k quad kq (16 of them)
-  const int pq = tid & 15, kq = tid >> 4;
-  const int px = p0 + 4 * pq;
-  const bool pin = px < M;  // M % 4 == 0: a quad is all in or all out
-  const int kc = (lane >> 4) * 16;
-  const int8_t *bp = wt + (long long)(n0 + (lane & 15)) * K + kc;
-  v4i acc[2][4];
-#pragma unroll
-  for (int t = 0; t < 2; t++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[t][j] = (v4i){0, 0, 0, 0};
-  uint32_t rg[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int k = 4 * kq + i;
-    rg[i] = (pin && k < K) ? *(const uint32_t *)(xw + (long long)k * M + px) : 0u;
-  }
-  for (int k0 = 0; k0 < K; k0 += 64) {
-    uint32_t c[4];
-    transpose4x4(rg[0], rg[1], rg[2], rg[3], c);
-    __syncthreads();  // the previous step's fragments are read
-#pragma unroll
-    for (int j = 0; j < 4; j++) *(uint32_t *)(xs + (4 * pq + j) * RQ_LDS_STRIDE + 4 * kq) = c[j];
-    __syncthreads();
-    if (k0 + 64 < K) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int k = k0 + 64 + 4 * kq + i;
-        rg[i] = (pin && k < K) ? *(const uint32_t *)(xw + (long long)k * M + px) : 0u;
-      }
-    }
-    const bool kin = k0 + kc < K;
-    v4i a[2], b[4];
-#pragma unroll
-    for (int t = 0; t < 2; t++) a[t] = *(const v4i *)(xs + (wm * 32 + 16 * t + (lane & 15)) * RQ_LDS_STRIDE + kc);
-#pragma unroll
-    for (int j = 0; j < 4; j++) b[j] = kin ? *(const v4i *)(bp + (long long)16 * j * K + k0) : (v4i){0, 0, 0, 0};
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[j], acc[t][j], 0, 0, 0);
-  }
-  int8_t *ow = out + win * out_ws;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int n = n0 + 16 * j + (lane & 15);
-    if (n >= N) continue;
-    const int32_t be = bias_eff[n], mu = mult[n], sh = shift[n];
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-      const int p = p0 + wm * 32 + 16 * t + 4 * (lane >> 4);
-      if (p >= M) continue;
-      uint32_t word = 0;
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int32_t a32 = (int32_t)((uint32_t)acc[t][j][r] + (uint32_t)be);
-        word |= ((uint32_t)bnh_requant(a32, mu, sh, zy, lo, hi) & 0xffu) << (8 * r);
-      }
-      *(uint32_t *)(ow + (long long)n * M + p) = word;
-    }
-  }
-}
 
 // Version 2: a block owns 128 pixels x 256 channels, so every activation byte is fetched from HBM once and every
 // staged k row is one whole 128-byte line. Both operands go through LDS (rows of 64 k bytes at an 80-byte stride:
@@ -327,7 +252,7 @@ __global__ __launch_bounds__(256) void k_gemm_s8_requant(const int8_t *__restric
 #define RQ2_CH 256
 #define RQ2_LDS (RQ2_PIX * RQ_LDS_STRIDE + RQ2_CH * RQ_LDS_STRIDE)
 __global__ __launch_bounds__(256, 2) void k_gemm_s8_requant2(const int8_t *__restrict__ x, long long x_ws, int M, int K,
-                                                          int tiles_per_window, const int8_t *__restrict__ wt,
+                                                          int tiles_per_window, const int8_t *__restrict__ wt, int ldw,
                                                           const int32_t *__restrict__ bias_eff,
                                                           const int32_t *__restrict__ mult,
                                                           const int32_t *__restrict__ shift, int N, int zy, int lo,
@@ -344,7 +269,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_s8_requant2(const int8_t *__res
   const int px = p0 + 4 * pq;
   const bool pin = px < M;  // M % 4 == 0
   // weight staging: channel row n0 + tid, 64 k bytes as 4 x 16
-  const int8_t *wrow = wt + (long long)(n0 + tid) * K;
+  const int8_t *wrow = wt + (long long)(n0 + tid) * ldw;
   const int kc = (lane >> 4) * 16;
   uint32_t rx[2][4];
   v4i rw[4];
@@ -426,6 +351,185 @@ __global__ __launch_bounds__(256, 2) void k_gemm_s8_requant2(const int8_t *__res
   }
 }
 
+// Version 4 (M % 16 == 0): persistent blocks of 8 waves, one per CU. A tile is 256 pixels x 256 channels of one
+// window (waves 4 (pixels) x 2 (channels), 64 x 128 each); a block walks its tiles t = blockIdx.x, + gridDim.x, ...,
+// and the K steps of all its tiles form one 4-stage LDS ring fed by direct global -> LDS loads
+// (global_load_lds_dwordx4: no registers, no VALU), so a tile's epilogue runs while the next tile's first steps load.
+// Each block starts its K loop at its own step (K-step s + rot modulo the step count: the int32 sums are exact in any
+// order), which spreads the blocks' weight-slice reads over L2.
+//
+// The activations stay in their k-major order in LDS; ds_read_b64_tr_b8 transposes them on the way to the MFMA
+// operand: over a 16-lane group, output lane l byte b comes from the 8-byte chunk of source lane 2b + l/8, byte l % 8.
+// Source lane j therefore points at k row 8h + j/2, pixels 8 (j % 2) .. + 7 of a 16-pixel column, and lane l receives
+// pixel l's 8 k bytes of that half. XOR-swizzled 16-byte slots keep the DMA writes (64 consecutive slots per
+// instruction) and the fragment reads free of bank conflicts:
+//   activations: k row r (256 bytes), pixel column c (16 bytes) at r * 256 + 16 (c ^ (r & 7));
+//   weights:     channel row n (64 bytes), k chunk c (16 bytes) at n * 64 + 16 (c ^ ((n >> 1) & 3)).
+// K is padded to a multiple of 64 with zero weights (activation rows past K are clamped to row K - 1: multiplied by
+// zero); pixel columns past M are clamped to the last column and their results dropped. The output tile is staged,
+// 128 channels at a time, in the stage the last K step used and written as whole 256-byte channel rows.
+#define RQ4_PIX 256
+#define RQ4_CH 256
+#define RQ4_BK 64
+#define RQ4_XB (RQ4_BK * RQ4_PIX)
+#define RQ4_STAGE (RQ4_XB + RQ4_CH * RQ4_BK)
+#define RQ4_NST 4
+#define RQ4_NLD 4  // DMA instructions per wave per K step: 2 activation + 2 weight
+typedef __attribute__((address_space(3))) int8_t lds_i8;
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+// The DMA loads are issued from inline assembly and awaited with explicit vmcnt waits: the compiler, seeing an
+// LDS-writing load, would otherwise wait for every outstanding load (vmcnt(0)) before each LDS read and serialise the
+// ring. The "memory" clobbers keep the compiler from moving LDS accesses across the waits and the barriers.
+BNH_DEV void rq_dma16(const int8_t *src, const lds_i8 *dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+#define RQ_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+#define RQ_BARRIER() asm volatile("s_barrier" ::: "memory")
+
+__global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__restrict__ x, long long x_ws, int M, int K,
+                                                          int Kt, int tpw, int nblk, int ntiles,
+                                                          const int8_t *__restrict__ wt,
+                                                          const int32_t *__restrict__ bias_eff,
+                                                          const int32_t *__restrict__ mult,
+                                                          const int32_t *__restrict__ shift, int N, int zy, int lo,
+                                                          int hi, int8_t *__restrict__ out, long long out_ws) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds_raw[RQ4_NST * RQ4_STAGE];
+  lds_i8 *lds = (lds_i8 *)lds_raw;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int steps = Kt / RQ4_BK;
+  const int rot = (int)(blockIdx.x % steps);
+  const int mytiles = ntiles > (int)blockIdx.x ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int total = mytiles * steps;
+  // tile t: channel block t % nblk, pixel tile (t / nblk) % tpw, window t / (nblk tpw)
+  // DMA sources: activation instruction q (2 per wave) fills k rows 4q .. 4q + 3, lane -> row 4q + lane / 16, slot
+  // lane % 16 = column (lane % 16) ^ (row % 8); weight instruction q (2 per wave) fills channel rows 16q .. 16q + 15,
+  // lane -> row 16q + lane / 4, slot lane % 4 = chunk (lane % 4) ^ ((lane / 8) % 4)
+  const int xr = lane >> 4, xslot = lane & 15;
+  const int wrow = lane >> 2, wchunk = (lane & 3) ^ ((lane >> 3) & 3);
+  auto issue = [&](int gs) {
+    const int t = (int)blockIdx.x + (gs / steps) * (int)gridDim.x;
+    int s = gs % steps + rot;
+    if (s >= steps) s -= steps;
+    const int cb = t % nblk, rest = t / nblk, p0 = (rest % tpw) * RQ4_PIX, win = rest / tpw;
+    const int8_t *xw = x + win * x_ws;
+    lds_i8 *st = lds + (gs % RQ4_NST) * RQ4_STAGE;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int q = 2 * wave + h, row = 4 * q + xr;
+      int k = s * RQ4_BK + row;
+      if (k > K - 1) k = K - 1;
+      int px = p0 + 16 * (xslot ^ (row & 7));
+      if (px > M - 16) px = M - 16;
+      rq_dma16(xw + (long long)k * M + px, st + q * 1024);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int q = 2 * wave + h;
+      rq_dma16(wt + (long long)(cb * RQ4_CH + 16 * q + wrow) * Kt + s * RQ4_BK + 16 * wchunk, st + RQ4_XB + q * 1024);
+    }
+  };
+  // fragment read offsets within a stage
+  const int g = lane >> 4, j = lane & 15;
+  int aoff[4][2], boff[8];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+      const int r = 16 * g + 8 * hf + (j >> 1), c = 4 * wm + t;
+      aoff[t][hf] = r * RQ4_PIX + 16 * (c ^ (j >> 1)) + 8 * (j & 1);
+    }
+#pragma unroll
+  for (int jj = 0; jj < 8; jj++) {
+    const int n = wn * 128 + 16 * jj + j;
+    boff[jj] = RQ4_XB + n * 64 + 16 * (g ^ ((n >> 1) & 3));
+  }
+  v4i acc[4][8];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) acc[t][jj] = (v4i){0, 0, 0, 0};
+  for (int gs = 0; gs < RQ4_NST - 1 && gs < total; gs++) issue(gs);
+  for (int gs = 0; gs < total; gs++) {
+    // this wave's loads of step gs have landed once at most the loads of the RQ4_NST - 2 later steps are outstanding
+    // (vector-memory loads retire in order; the epilogue's stores only make the wait longer)
+    if (gs + RQ4_NST - 2 < total) RQ_WAIT_VM(8);  // RQ4_NLD * (RQ4_NST - 2)
+    else RQ_WAIT_VM(0);
+    RQ_BARRIER();  // every wave's loads of step gs have landed; the stage step gs - 1 used is no longer read
+    if (gs + RQ4_NST - 1 < total) issue(gs + RQ4_NST - 1);
+    const lds_i8 *st = lds + (gs % RQ4_NST) * RQ4_STAGE;
+    v4i a[4], b[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const v2i lo8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(st + aoff[t][0]));
+      const v2i hi8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(st + aoff[t][1]));
+      a[t] = (v4i){lo8.x, lo8.y, hi8.x, hi8.y};
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) b[jj] = *(const __attribute__((address_space(3))) v4i *)(st + boff[jj]);
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[jj], acc[t][jj], 0, 0, 0);
+    if (gs % steps != steps - 1) continue;
+    // ---- epilogue of tile t: requantise, stage 128 channels x 256 pixels at a time, store whole rows
+    const int t = (int)blockIdx.x + (gs / steps) * (int)gridDim.x;
+    const int cb = t % nblk, rest = t / nblk, p0 = (rest % tpw) * RQ4_PIX, win = rest / tpw;
+    int8_t *ow = out + win * out_ws;
+    uint32_t wd[8][4];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int n = cb * RQ4_CH + wn * 128 + 16 * jj + j;  // < Nt: the per-channel vectors are padded to Nt
+      const int32_t be = bias_eff[n], mu = mult[n], sh = shift[n];
+#pragma unroll
+      for (int tt = 0; tt < 4; tt++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          word |= ((uint32_t)bnh_requant((int32_t)((uint32_t)acc[tt][jj][r] + (uint32_t)be), mu, sh, zy, lo, hi) &
+                   0xffu) << (8 * r);
+        wd[jj][tt] = word;
+        acc[tt][jj] = (v4i){0, 0, 0, 0};
+      }
+    }
+    // channel row ch (256 bytes) of the staging buffer holds 16-byte chunk c at ch * 256 + 16 (c ^ (ch & 15))
+    lds_i8 *ob = lds + (gs % RQ4_NST) * RQ4_STAGE;
+    RQ_BARRIER();  // every wave's MFMAs of step gs have read the stage
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+      if (wn == half) {
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++)
+#pragma unroll
+          for (int tt = 0; tt < 4; tt++) {
+            const int ch = 16 * jj + j, px = wm * 64 + 16 * tt + 4 * g;
+            *(__attribute__((address_space(3))) uint32_t *)(ob + ch * 256 + 16 * ((px >> 4) ^ (ch & 15)) + (px & 15)) =
+                wd[jj][tt];
+          }
+      }
+      RQ_BARRIER();
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int chunk = i * 512 + tid, ch = chunk >> 4, cp = chunk & 15;
+        const v4i val = *(const __attribute__((address_space(3))) v4i *)(ob + ch * 256 + 16 * cp);
+        const int n = cb * RQ4_CH + half * 128 + ch, p = p0 + 16 * (cp ^ (ch & 15));
+        if (n < N && p < M) *(v4i *)(ow + (long long)n * M + p) = val;
+      }
+      RQ_BARRIER();
+    }
+  }
+}
+
+// requant arithmetic check: y[i] = bnh_requant(acc[i], mult[i], shift[i], zy, lo, hi)
+__global__ void k_eval_requant(const int32_t *__restrict__ acc, const int32_t *__restrict__ mult,
+                               const int32_t *__restrict__ shift, int zy, int lo, int hi, int32_t *__restrict__ y,
+                               long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = bnh_requant(acc[i], mult[i], shift[i], zy, lo, hi);
+}
+
 // ------------------------------------------------------------------ numerics probe
 __global__ void k_eval_f32(int f, const float *__restrict__ x, float *__restrict__ y, long long n) {
   long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -436,6 +540,16 @@ __global__ void k_eval_f32(int f, const float *__restrict__ x, float *__restrict
 
 // ================================================================== host side
 extern "C" {
+
+int bnh_eval_requant(const int32_t *acc, const int32_t *mult, const int32_t *shift, int zy, int lo, int hi, int32_t *y,
+                     long long n, void *stream) {
+  BNH_REQ(acc && mult && shift && y && n >= 0 && lo <= hi);
+  if (!n) return 0;
+  hipLaunchKernelGGL(k_eval_requant, dim3((unsigned)bnh_ceil_div(n, 256)), dim3(256), 0, bnh_stream(stream), acc, mult,
+                     shift, zy, lo, hi, y, n);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
 
 int bnh_eval_f32(int f, const float *x, float *y, long long n, void *stream) {
   BNH_REQ(f >= 0 && f <= 2 && n >= 0 && x && y);
@@ -563,7 +677,8 @@ bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const i
       return nullptr;
     }
   const int Nt = (int)bnh_round_up(N, RQ2_CH);  // every staging thread of a block owns one weight row
-  int8_t *hw = (int8_t *)calloc((size_t)Nt * K, 1);
+  const int Kt = (int)bnh_round_up(K, RQ4_BK);
+  int8_t *hw = (int8_t *)calloc((size_t)Nt * Kt, 1);
   int32_t *hb = (int32_t *)calloc(Nt, 4), *hm = (int32_t *)calloc(Nt, 4), *hs = (int32_t *)calloc(Nt, 4);
   bnh_q8w *W = (bnh_q8w *)calloc(1, sizeof *W);
   if (!hw || !hb || !hm || !hs || !W) {
@@ -571,7 +686,7 @@ bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const i
     bnh_fail("bnh_q8w_new: out of host memory");
     return nullptr;
   }
-  memcpy(hw, w, (size_t)N * K);
+  for (int n = 0; n < N; n++) memcpy(hw + (size_t)n * Kt, w + (size_t)n * K, (size_t)K);
   for (int n = 0; n < N; n++) {
     uint32_t cs = 0;
     for (int k = 0; k < K; k++) cs += (uint32_t)(int32_t)w[(size_t)n * K + k];
@@ -579,10 +694,10 @@ bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const i
     hm[n] = mult[n];
     hs[n] = shift[n];
   }
-  W->N = N; W->K = K; W->Nt = Nt; W->zx = zx; W->zy = zy; W->lo = lo; W->hi = hi;
-  bool ok = (W->w = (int8_t *)bnh_malloc((size_t)Nt * K)) && (W->bias_eff = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
+  W->N = N; W->K = K; W->Kt = Kt; W->Nt = Nt; W->zx = zx; W->zy = zy; W->lo = lo; W->hi = hi;
+  bool ok = (W->w = (int8_t *)bnh_malloc((size_t)Nt * Kt)) && (W->bias_eff = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
             (W->mult = (int32_t *)bnh_malloc(4 * (size_t)Nt)) && (W->shift = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
-            !bnh_memcpy_h2d(W->w, hw, (size_t)Nt * K) && !bnh_memcpy_h2d(W->bias_eff, hb, 4 * (size_t)Nt) &&
+            !bnh_memcpy_h2d(W->w, hw, (size_t)Nt * Kt) && !bnh_memcpy_h2d(W->bias_eff, hb, 4 * (size_t)Nt) &&
             !bnh_memcpy_h2d(W->mult, hm, 4 * (size_t)Nt) && !bnh_memcpy_h2d(W->shift, hs, 4 * (size_t)Nt);
   free(hw); free(hb); free(hm); free(hs);
   if (!ok) { bnh_q8w_free(W); return nullptr; }
@@ -604,10 +719,26 @@ int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M
   BNH_REQ(M % 4 == 0 && ((uintptr_t)x & 3) == 0 && ((uintptr_t)out & 3) == 0);
   BNH_REQ(B == 1 || (x_ws % 4 == 0 && out_ws % 4 == 0 && x_ws >= (long long)W->K * M && out_ws >= (long long)W->N * M));
   BNH_REQ(W->K % 16 == 0);
-  const int tpw = (int)bnh_ceil_div(M, RQ2_PIX);
-  dim3 grid((unsigned)((long long)tpw * B), (unsigned)bnh_ceil_div(W->N, RQ2_CH));
-  hipLaunchKernelGGL(k_gemm_s8_requant2, grid, dim3(256), 0, bnh_stream(stream), x, x_ws, M, W->K, tpw, W->w,
-                     W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
+  hipStream_t st = bnh_stream(stream);
+  if (M % 16 == 0 && ((uintptr_t)x & 15) == 0 && (B == 1 || x_ws % 16 == 0)) {
+    static int ncu = 0;
+    if (!ncu) {
+      int dev = 0;
+      BNH_HIP(hipGetDevice(&dev));
+      BNH_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    }
+    const int tpw = (int)bnh_ceil_div(M, RQ4_PIX), nblk = W->Nt / RQ4_CH;
+    const long long nt = (long long)tpw * nblk * B;
+    BNH_REQ(nt < (1LL << 31));
+    const int grid = (int)(nt < ncu ? nt : ncu);
+    hipLaunchKernelGGL(k_gemm_s8_requant4, dim3(grid), dim3(512), 0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt,
+                       W->w, W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
+  } else {
+    const int tpw = (int)bnh_ceil_div(M, RQ2_PIX);
+    dim3 grid((unsigned)((long long)tpw * B), (unsigned)(W->Nt / RQ2_CH));
+    hipLaunchKernelGGL(k_gemm_s8_requant2, grid, dim3(256), 0, st, x, x_ws, M, W->K, tpw, W->w, W->Kt, W->bias_eff,
+                       W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
+  }
   BNH_HIP(hipGetLastError());
   return 0;
 }

@@ -42,6 +42,10 @@ int bnh_copy(void *dst, const void *src, size_t bytes, void *stream);
  * y[i] = f(x[i]) on the device for n elements, f = 0: FRECPE, 1: the fp32 SiLU of the epilogues
  * (src/gemm_f32.h:102-118), 2: ReLU (vmaxq_f32 with 0). Used to pin the device numerics against the oracle. */
 int bnh_eval_f32(int f, const float *x, float *y, long long n, void *stream);
+/* y[i] = the Q31 requantisation of the int8 GEMM / depthwise below applied to acc[i] with mult[i], shift[i] (0..31),
+ * zy, clamp [lo, hi]: pins the device fixed-point arithmetic against the oracle */
+int bnh_eval_requant(const int32_t *acc, const int32_t *mult, const int32_t *shift, int zy, int lo, int hi, int32_t *y,
+                     long long n, void *stream);
 
 /* ------------------------------------------------------------------ int8 GEMM weights (PW_S8 / GEMV_S8)
  * Built from the package tensors of one int8 GEMM (python/bnneon/compiler/lower.py:883-914, s8_tensors; validated

@@ -238,3 +238,72 @@ def test_gemm_requant_small_shapes(hip):
         H.check(H.lib().bnh_gemm_s8_requant(Wq.h, dx.ptr, K * M, M, 1, dout.ptr, N * M, None), "requant")
         H.sync()
         assert np.array_equal(dout.numpy(), O.gemm_s8_requant(w, x[0], bias, mult, shift, 3, -5, -100, 90))
+
+
+def test_gemm_requant_ring_kernel_shapes(hip):
+    """Pixel counts that are multiples of 16 (the direct-to-LDS kernel): a
+    single 16-pixel column, a partial last pixel tile, one K step, a K tail
+    inside the last step, channel counts past one 256-channel block, and
+    windows at padded (16-byte multiple) strides."""
+    H = hip
+    rng = np.random.default_rng(77)
+    for (N, K, M, B, slack) in ((8, 16, 16, 1, 0), (24, 48, 144, 3, 16), (256, 64, 272, 2, 48),
+                                (520, 208, 128, 2, 0), (40, 1152, 1536, 3, 4096)):
+        w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+        x = rng.integers(-128, 128, (B, K, M)).astype(np.int8)
+        bias = rng.integers(-2 ** 20, 2 ** 20, N).astype(np.int32)
+        mult = rng.integers(2 ** 30, 2 ** 31, N).astype(np.int32)
+        shift = rng.integers(0, 16, N).astype(np.int32)
+        Wq = H.Q8Weights(w, bias, mult, shift, -7, 4, -120, 127)
+        x_ws = K * M + slack
+        xs = np.zeros((B, x_ws), np.int8)
+        xs[:, :K * M] = x.reshape(B, -1)
+        o_ws = N * M + 32
+        dx = H.DeviceArray.from_host(xs)
+        dout = H.DeviceArray.zeros((B, o_ws), np.int8)
+        say("requant ring", N, K, M, B)
+        H.check(H.lib().bnh_gemm_s8_requant(Wq.h, dx.ptr, x_ws, M, B, dout.ptr, o_ws, None), "requant")
+        H.sync()
+        got = dout.numpy()
+        for b in range(B):
+            ref = O.gemm_s8_requant(w, x[b], bias, mult, shift, -7, 4, -120, 127)
+            assert np.array_equal(got[b, :N * M].reshape(N, M), ref), (N, K, M, b)
+            assert not got[b, N * M:].any()   # nothing written past the window's output
+
+
+def test_requant_arithmetic_edges(hip):
+    """The device's closed-form Q31 requantisation against the oracle's
+    textbook SaturatingRoundingDoublingHighMul + RoundingDivideByPOT on the
+    extremes (INT32_MIN x INT32_MIN saturation, INT32_MAX products), exact
+    rounding ties at every shift, negative multipliers and random values."""
+    H = hip
+    L = O.lib()
+    rng = np.random.default_rng(99)
+    I32 = np.iinfo(np.int32)
+    edge = np.array([I32.min, I32.min + 1, -1, 0, 1, I32.max - 1, I32.max, 1 << 30, -(1 << 30)], np.int64)
+    acc, mult, shift = [], [], []
+    for a in edge:
+        for m in edge:
+            for s in (0, 1, 5, 30, 31):
+                acc.append(a), mult.append(m), shift.append(s)
+    # ties of RoundingDivideByPOT: x = (2q + 1) 2^(s-1) exactly, through mult = 2^30 (SRDHM(a, 2^30) = a / 2 rounded)
+    for s in range(1, 32):
+        for q in (-3, -2, -1, 0, 1, 2):
+            x = (2 * q + 1) * (1 << (s - 1))
+            if I32.min <= 2 * x <= I32.max:
+                acc.append(2 * x), mult.append(1 << 30), shift.append(s)
+    n = 200000
+    acc += list(rng.integers(I32.min, I32.max, n, endpoint=True))
+    mult += list(rng.integers(I32.min, I32.max, n, endpoint=True))
+    shift += list(rng.integers(0, 32, n))
+    acc, mult, shift = (np.array(v, np.int32) for v in (acc, mult, shift))
+    for zy, lo, hi in ((0, -128, 127), (-128, -128, 127), (5, -100, 90)):
+        da, dm, ds = H.DeviceArray.from_host(acc), H.DeviceArray.from_host(mult), H.DeviceArray.from_host(shift)
+        dy = H.DeviceArray.zeros(acc.size, np.int32)
+        H.check(H.lib().bnh_eval_requant(da.ptr, dm.ptr, ds.ptr, zy, lo, hi, dy.ptr, acc.size, None), "requant")
+        H.sync()
+        got = dy.numpy()
+        want = np.array([L.orc_requant(int(a), int(m), int(s), zy, lo, hi) for a, m, s in zip(acc, mult, shift)],
+                        np.int32)
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, [(int(acc[i]), int(mult[i]), int(shift[i]), int(got[i]), int(want[i])) for i in bad[:5]]
