@@ -27,6 +27,13 @@ class Epi32(C.Structure):
                 ("ldr", i32), ("rpad", i32), ("rw", i32)]
 
 
+class Epi16(C.Structure):
+    """bnh_epi16: the fp16 GEMM epilogue (per-window strides)."""
+    _fields_ = [("act", i32), ("out", vp), ("out_ws", i64), ("ldo", i32),
+                ("ow", i32), ("opad", i32), ("res", vp), ("res_ws", i64),
+                ("ldr", i32)]
+
+
 _SIGS = {
     "bnh_last_error": (C.c_char_p, []),
     "bnh_device_count": (i32, []),
@@ -63,6 +70,9 @@ _SIGS = {
     "bnh_q8w_new": (vp, [i32, i32, vp, vp, vp, vp, i32, i32, i32, i32]),
     "bnh_q8w_free": (None, [vp]),
     "bnh_gemm_s8_requant": (i32, [vp, vp, i64, i32, i32, vp, i64, vp]),
+    "bnh_h16w_new": (vp, [i32, i32, i32, i32, vp, vp]),
+    "bnh_h16w_free": (None, [vp]),
+    "bnh_gemm_f16": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
     "bnh_dwk_f32": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp,
                           i32, vp, i64, i32, i32, vp, i64, i32, vp]),
     "bnh_dw3_f32": (i32, [vp, i64, i32, i32, i32, i32, vp, vp, vp, i64, i32,

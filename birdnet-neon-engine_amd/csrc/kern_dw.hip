@@ -13,46 +13,7 @@
 #include "bnh_internal.h"
 #include "bnh_num.h"
 
-typedef _Float16 h16;
-
-BNH_DEV uint16_t hbits(h16 x) { return __builtin_bit_cast(uint16_t, x); }
-BNH_DEV h16 hfrom(uint16_t u) { return __builtin_bit_cast(h16, u); }
-BNH_DEV bool hnan(h16 x) { return x != x; }
-BNH_DEV h16 hfma(h16 a, h16 b, h16 c) { return __builtin_fmaf16(a, b, c); }
-// FMAX / FMIN on fp16 (NaN-propagating, +0 above -0)
-BNH_DEV h16 hmax(h16 a, h16 b) {
-  if (hnan(a) || hnan(b)) return hfrom(0x7e00);
-  if (a == (h16)0 && b == (h16)0) return hfrom((uint16_t)(hbits(a) & hbits(b)));
-  return a > b ? a : b;
-}
-BNH_DEV h16 hmin(h16 a, h16 b) {
-  if (hnan(a) || hnan(b)) return hfrom(0x7e00);
-  if (a == (h16)0 && b == (h16)0) return hfrom((uint16_t)(hbits(a) | hbits(b)));
-  return a < b ? a : b;
-}
-
-// The fp16 SiLU of the kernels (src/silu_lut.h:28-42): max(x, 0) - |x| q(|x|), q a piecewise quadratic in
-// f = u - round(u) on 16 unit segments, u = min(|x|, 15.4). Coefficients as fp16 bit patterns: the values of
-// src/silu_lut_tables_deg2.h. A NaN input gives NaN whichever segment it indexes.
-__constant__ uint16_t k_silu_c0[16] = {0x3800, 0x344e, 0x2fa1, 0x2a12, 0x249a, 0x1ed9, 0x1910, 0x1375,
-                                       0x0d7e, 0x080a, 0x02f9, 0x0118, 0x0067, 0x0026, 0x000e, 0x0005};
-__constant__ uint16_t k_silu_c1[16] = {0xb40b, 0xb242, 0xaecc, 0xa9ea, 0xa4a6, 0x9f03, 0x9935, 0x93b1,
-                                       0x8daa, 0x882c, 0x8312, 0x8121, 0x806a, 0x8027, 0x800e, 0x8005};
-__constant__ uint16_t k_silu_c2[16] = {0x23bd, 0x299d, 0x2915, 0x254c, 0x2073, 0x1ae1, 0x1528, 0x0fa3,
-                                       0x09a2, 0x0426, 0x0187, 0x0090, 0x0035, 0x0013, 0x0007, 0x0003};
-BNH_DEV h16 silu_lut_h(h16 x) {
-  const h16 magic = (h16)1536.0f;
-  const h16 u = hfrom((uint16_t)(hbits(x) & 0x7fff));
-  const h16 uc = hmin(u, hfrom(0x4bb3));  // (fp16)15.4f
-  const h16 tm = uc + magic;
-  const h16 f = uc - (tm - magic);
-  unsigned n = hbits(tm) & 0xffu;
-  if (n > 15) n = 0;
-  const h16 c0 = hfrom(k_silu_c0[n]), c1 = hfrom(k_silu_c1[n]), c2 = hfrom(k_silu_c2[n]);
-  h16 p = hfma(c2, f, c1);
-  p = hfma(p, f, c0);
-  return hfma(-u, p, hmax(x, (h16)0.0f));
-}
+#include "bnh_f16.h"
 
 // ------------------------------------------------------------------ the items of an output row
 // DWK forms: items [0, g4/4) are 4-pixel groups, then (fp32) one item per tail pixel, or (fp16) a pixel pair when

@@ -1,4 +1,6 @@
 // Registry kernels with fp16 arithmetic (variant 1, the reference's rt_ops_f16.c family) on the GPU.
+#include <stdlib.h>
+
 #include "bnh_internal.h"
 #include "rt.h"
 
@@ -7,6 +9,58 @@ int rt_dw3_check(rt_ctx *c, rt_op *op, int dt, int pt, int pl);  // ops_f32.cpp
 int rt_dev_tensors(rt_ctx *c, rt_op *op, int n);
 void rt_dev_fini(rt_op *op);
 static inline const uint16_t *dev_h(const rt_op *op, int i) { return *((uint16_t *const *)op->state + i); }
+int rt_pw_out_check(rt_ctx *c, rt_op *op, int dt);             // ops_s8n.cpp
+
+// -------- PW f16: b = [in f16 [M][lda], out, res | -1]; t = [w (hpack panels), b32, b16];
+//          p = [N K Kp Np, M, lda, act, ldo, ow, opad, ldr]   (src/rt_ops_f16.c:14-27, 53-81; rt_pw_check,
+//          src/rt_ops_f32.c:129-152)
+typedef struct { bnh_h16w *W; } pw16_state;
+static void pw16_fini(rt_op *op) {
+  pw16_state *s = (pw16_state *)op->state;
+  if (s) bnh_h16w_free(s->W);
+  free(s);
+}
+static int pw16_init(rt_ctx *c, rt_op *op) {
+  pw16_state *s = (pw16_state *)calloc(1, sizeof *s);
+  op->state = s;
+  if (!s) return rt_oom(c, op, sizeof *s);
+  if (rt_need_args(c, op, 3, 3, 11)) return RT_E_PARAM;
+  const int *p = op->p;
+  const int N = p[0], K = p[1], Kp = p[2], Np = p[3];
+  if (N <= 0 || K <= 0 || Np != ((N + 7) & ~7) || Kp < K || Kp % 8)
+    return rt_bad(c, op, "GEMM shape N %d K %d Kp %d Np %d: expected Np = N rounded up to 8, Kp >= K, Kp %% 8 == 0", N,
+                  K, Kp, Np);
+  if (rt_need_t(c, op, 0, (size_t)Np * Kp * 2, 1) || rt_need_t(c, op, 1, (size_t)(Np + 16) * 4, 1) ||
+      rt_need_t(c, op, 2, (size_t)(Np + 16) * 2, 1))
+    return RT_E_PARAM;
+  const int M = p[4], lda = p[5], act = p[6], ldo = p[7], opad = p[9], ldr = p[10];
+  const size_t Mr = ((size_t)M + 7) & ~(size_t)7;
+  RT_REQ(c, op, M > 0);
+  RT_REQ(c, op, lda >= Kp);
+  RT_REQ(c, op, ldo >= Np);
+  RT_REQ(c, op, act >= 0 && act <= 2);
+  RT_REQ(c, op, opad >= 0 && opad <= 3);
+  if (rt_need(c, op, 0, RT_F16, Mr * lda) || rt_pw_out_check(c, op, RT_F16)) return RT_E_PARAM;
+  if (op->b[2] >= 0) {
+    RT_REQ(c, op, ldr >= Np);
+    const rt_bufdesc *r = rt_bd(c, op, 2);
+    if (r->halo)
+      return rt_bad(c, op, "buffer argument 2 (buffer #%d, residual): halo %u needs an fp32 buffer with ld %d and H x W = "
+                    "%d rows, found %s ld %u %ux%u", op->b[2], r->halo, ldr, M, rt_dtype_name(r->dtype), r->ld, r->H, r->W);
+    if (rt_need(c, op, 2, RT_F16, (size_t)M * ldr)) return RT_E_PARAM;
+  }
+  RT_REQ(c, op, lda % 8 == 0);  // 16-byte operand loads (every package pads rows to 8 channels)
+  s->W = bnh_h16w_new(N, K, Kp, Np, (const uint16_t *)rt_t(c, op, 0, nullptr), (const float *)rt_t(c, op, 1, nullptr));
+  if (!s->W) return rt_oom(c, op, (size_t)Np * Kp * 2);
+  return 0;
+}
+static int pw16_run(rt_ctx *c, rt_op *op) {
+  const pw16_state *s = (const pw16_state *)op->state;
+  const int *p = op->p;
+  bnh_epi16 e = {p[6], (uint16_t *)rt_b(c, op, 1), rt_ws(c, op, 1), p[7], p[8], p[9], (const uint16_t *)rt_b(c, op, 2),
+                 rt_ws(c, op, 2), p[10]};
+  return bnh_gemm_f16((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e, c->stream);
+}
 
 // -------- DWK f16: as the fp32 op, fp16 buffers and tensors (src/rt_ops_f16.c:192-203)
 static int dwk_init(rt_ctx *c, rt_op *op) {
@@ -35,11 +89,13 @@ static int dw3_run(rt_ctx *c, rt_op *op) {
                      (float *)rt_b(c, op, 2), rt_ws(c, op, 2), c->nwin, c->stream);
 }
 
+static const rt_kernel K_PW = {pw16_init, pw16_run, pw16_fini, "pw_f16", 0x2, 0x4};
 static const rt_kernel K_DW3 = {dw3_init, dw3_run, rt_dev_fini, "dw3_f16", 0x6, 0};
 static const rt_kernel K_DWK = {dwk_init, dwk_run, rt_dev_fini, "dwk_f16", 0x6, 0};
 
 const rt_kernel *rt_k_f16(int base) {
   switch (base) {
+    case RT_OP_PW: return &K_PW;
     case RT_OP_DW3: return &K_DW3;
     case RT_OP_DWK: return &K_DWK;
     default: return nullptr;

@@ -116,6 +116,30 @@ void bnh_q8w_free(bnh_q8w *W);
 int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M, int B, int8_t *out,
                         long long out_ws, void *stream);
 
+/* ------------------------------------------------------------------ fp16 GEMM (PW f16)
+ * Weights from the package tensors of an fp16 GEMM (hp_pack, src/gemm_f16.c:18-40; validated as hpack_view,
+ * src/rt_ops_f16.c:14-27): w fp16 [Np/16][Kp][16] then, if Np % 16, a tail panel [Kp][8]; b32 f32 [>= Np].
+ * Repacked once into channel rows in HBM. */
+typedef struct bnh_h16w bnh_h16w;
+bnh_h16w *bnh_h16w_new(int N, int K, int Kp, int Np, const uint16_t *w, const float *b32);
+void bnh_h16w_free(bnh_h16w *W);
+/* the fp16 epilogue (epi16, src/gemm_f16.h:19-27, without the pooled form), per-window strides in elements */
+typedef struct {
+  int act;               /* 0 none, 1 SiLU (the fp16 LUT form), 2 ReLU */
+  uint16_t *out;         /* fp16; pixel m at row m (opad 0) or ((m/ow)+opad)*(ow+2opad) + m%ow + opad */
+  long long out_ws;
+  int ldo, ow, opad;
+  const uint16_t *res;   /* optional fp16 residual [M][ldr], added after the activation */
+  long long res_ws;
+  int ldr;
+} bnh_epi16;
+/* gemm_f16 (src/gemm_f16.c:124-171; the PW f16 op run, src/rt_ops_f16.c:65-81): out rows [0, M) x channels [0, Np)
+ * of act(A . W^T + b) (+ res) for B windows of fp16 rows A [M][lda] (lda >= Kp, lda % 8 == 0; zero-haloed output
+ * zeroed when opad). fp16 MFMA with fp32 accumulation: within the fp16 accumulation error bound of the reference
+ * (which accumulates in fp16 over K blocks of <= 128 steps), not bit-identical. */
+int bnh_gemm_f16(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
+                 void *stream);
+
 /* ------------------------------------------------------------------ depthwise convolutions
  * NHWC, weights [k*k][C] (tap-major), per-window strides in elements. xp is the zero-haloed input of the reference's
  * buffers: [H + 2h][W + 2h][C], h = (k - 1) / 2 (1 for the DW3 forms); output pixel (oy, ox) reads the k x k taps

@@ -75,7 +75,7 @@ uint16_t orc_h_add(uint16_t a, uint16_t b) { return orc_h_fma(a, 0x3c00, b); }
 uint16_t orc_h_mul(uint16_t a, uint16_t b) { return orc_h_fma(a, b, 0x8000); }
 
 /* FMAX / FMIN on fp16 */
-static uint16_t h_max(uint16_t a, uint16_t b) {
+uint16_t orc_h_max(uint16_t a, uint16_t b) {
   if (h_isnan(a) || h_isnan(b)) return 0x7e00;
   float x = orc_h2f(a), y = orc_h2f(b);
   if (x == 0 && y == 0) return (uint16_t)(a & b & 0x8000);
@@ -114,7 +114,7 @@ uint16_t orc_silu_lut_h(uint16_t x) {
   uint16_t c0 = lut_coef(SILU_C0, n), c1 = lut_coef(SILU_C1, n), c2 = lut_coef(SILU_C2, n);
   uint16_t p = orc_h_fma(c2, f, c1);
   p = orc_h_fma(p, f, c0);
-  return orc_h_fma((uint16_t)(u ^ 0x8000), p, h_max(x, 0));
+  return orc_h_fma((uint16_t)(u ^ 0x8000), p, orc_h_max(x, 0));
 }
 
 /* ---------------------------------------------------------------- fp32 DWK (src/pc_kern_f32.c:163-334) */

@@ -97,6 +97,21 @@ void orc_dw_s8(const int8_t *x, int H, int W, int C, int k, int s, int pt, int p
                const int32_t *mult, const int32_t *shift, int zx, int zy, int lo, int hi, const int8_t *lut, int8_t *out,
                int Ho, int Wo);
 
+/* ---------------------------------------------------------------- fp16 GEMM (PW f16) */
+uint16_t orc_f2h(float f);                                 /* FCVT h, s: nearest even, denormals, overflow to inf */
+uint16_t orc_h_max(uint16_t a, uint16_t b);                /* FMAX on fp16 */
+typedef struct {
+  int act;          /* 0 none, 1 SiLU (LUT), 2 ReLU (src/gemm_f16.h:18) */
+  uint16_t *out;
+  int ldo, ow, opad;
+  const uint16_t *res;
+  int ldr;
+} orc_epi16;        /* src/gemm_f16.h:19-27 (without the pooled form) */
+/* src/gemm_f16.c:49-171: out rows [0, M) x channels [0, Np) of act(A . W^T + b) (+ res); W [N][Kp] channel rows, fp16
+ * accumulation in balanced K blocks of <= 128 steps, fp32 across blocks */
+void orc_gemm_f16(const uint16_t *A, int lda, int M, const uint16_t *W, int N, int Kp, const float *b32,
+                  const uint16_t *b16, const orc_epi16 *e);
+
 /* ---------------------------------------------------------------- Q31 requantised int8 GEMM (own specification)
  * The reference has no such kernel. Specification (TFLite / gemmlowp fixed-point conventions):
  *   acc[n][m]  = sum_k w[n][k] * (x[k][m] - zx) + bias[n]                       (exact, int32)

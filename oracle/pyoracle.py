@@ -270,3 +270,34 @@ def dw_s8(x, k, s, pt, pl, w, bias, mult, shift, zx, zy, lo, hi, lut, Ho, Wo):
                     shift.ctypes.data, zx, zy, lo, hi, None if lut_a is None else lut_a.ctypes.data,
                     out.ctypes.data, Ho, Wo)
     return out
+
+
+class OrcEpi16(C.Structure):
+    _fields_ = [("act", i32), ("out", vp), ("ldo", i32), ("ow", i32), ("opad", i32), ("res", vp), ("ldr", i32)]
+
+
+_SIGS.update({
+    "orc_f2h": (u16, [f32]),
+    "orc_h_max": (u16, [u16, u16]),
+    "orc_gemm_f16": (None, [vp, i32, i32, vp, i32, i32, vp, vp, C.POINTER(OrcEpi16)]),
+})
+
+
+def gemm_f16(A, W, b32, act=0, ldo=None, ow=0, opad=0, res=None, M=None):
+    """orc_gemm_f16: A fp16 [M][lda] (lda >= Kp), W fp16 [N][Kp] -> out fp16 rows [(padded) M][ldo]."""
+    A = _c(A, np.float16)
+    W = _c(W, np.float16)
+    b32 = _c(b32, np.float32)
+    b16 = b32.astype(np.float16)
+    M = A.shape[0] if M is None else M
+    lda = A.shape[1]
+    N, Kp = W.shape
+    Np = (N + 7) // 8 * 8
+    ldo = ldo or Np
+    rows = M if not opad else (M // ow + 2 * opad) * (ow + 2 * opad)
+    out = np.zeros((rows, ldo), np.float16)
+    r = None if res is None else _c(res, np.float16)
+    e = OrcEpi16(act, out.ctypes.data, ldo, ow, opad, None if r is None else r.ctypes.data,
+                 0 if r is None else r.shape[1])
+    lib().orc_gemm_f16(A.ctypes.data, lda, M, W.ctypes.data, N, Kp, b32.ctypes.data, b16.ctypes.data, C.byref(e))
+    return out

@@ -1,0 +1,133 @@
+"""GPU parity of the fp16 pointwise GEMM (libbnneon's gemm_f16 / PW f16 op).
+
+The GPU accumulates on fp16 MFMA in fp32; the reference (the oracle restates
+it) accumulates in fp16 within K blocks of <= 128 steps. Stated tolerance, per
+output before the activation: |gpu - oracle| <= (n + 2) 2^-11 S + 2^-10 |oracle|
++ 2^-24, n = the reference's K-block length, S = sum_k |a_k w_k| + |b| (the
+recursive-summation bound of the reference's fp16 chain plus one rounding of
+each result); with small-integer operands every operation of both is exact and
+the outputs are bit-identical, through every epilogue form.
+"""
+import numpy as np
+import pytest
+
+import pyoracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def hpack(W, Kp):
+    """hp_pack's panel layout (src/gemm_f16.c:18-40) of fp16 weights W [N][K]."""
+    N, K = W.shape
+    Np = (N + 7) // 8 * 8
+    n16 = Np // 16
+    out = np.zeros(Np * Kp, np.float16)
+    for o in range(N):
+        nb, j = o // 16, o % 16
+        for k in range(K):
+            idx = (nb * Kp + k) * 16 + j if nb < n16 else n16 * Kp * 16 + k * 8 + j
+            out[idx] = W[o, k]
+    return out
+
+
+def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, B=1, Kp=None):
+    """A [B][M][lda] fp16 -> out [B][rows][ldo] fp16 through bnh_gemm_f16."""
+    H = hip
+    Bw, M, lda = A.shape
+    N, K = W.shape
+    Kp = Kp or (K + 7) // 8 * 8
+    Np = (N + 7) // 8 * 8
+    Wp = np.zeros((N, Kp), np.float16)
+    Wp[:, :K] = W
+    bpad = np.zeros(Np + 16, np.float32)
+    bpad[:N] = b32
+    hp = hpack(Wp, Kp)   # kept alive across the call (a temporary's buffer could be freed before it runs)
+    hw = H.lib().bnh_h16w_new(N, K, Kp, Np, hp.ctypes.data, bpad.ctypes.data)
+    if not hw:
+        H.check(None, "bnh_h16w_new")
+    try:
+        rows = M if not opad else (M // ow + 2 * opad) * (ow + 2 * opad)
+        ldo = Np
+        a_ws = M * lda + 64
+        ah = np.zeros((Bw, a_ws), np.float16)
+        ah[:, :M * lda] = A.reshape(Bw, -1)
+        o_ws = rows * ldo + 32
+        dA = H.DeviceArray.from_host(ah)
+        dO = H.DeviceArray.from_host(np.full((Bw, o_ws), np.float16(7.0)))   # garbage that the halo zeroing clears
+        dR = None
+        r_ws = 0
+        if res is not None:
+            ldr = res.shape[2]
+            r_ws = M * ldr
+            dR = H.DeviceArray.from_host(res.reshape(Bw, -1))
+        e = H.Epi16(act, dO.ptr, o_ws, ldo, ow, opad, dR.ptr if dR else None, r_ws, res.shape[2] if res is not None else 0)
+        H.check(H.lib().bnh_gemm_f16(dA.ptr, a_ws, lda, M, Bw, hw, e, None), "gemm_f16")
+        H.sync()
+        return dO.numpy()[:, :rows * ldo].reshape(Bw, rows, ldo), Wp
+    finally:
+        H.lib().bnh_h16w_free(hw)
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_small_integers_bit_exact(hip, act):
+    rng = np.random.default_rng(act)
+    B, M, N, K = 3, 40, 24, 136      # K 136 -> Kp 136: two reference K blocks (72 + 64)
+    A = rng.integers(-3, 4, (B, M, K)).astype(np.float16)
+    W = rng.integers(-2, 3, (N, K)).astype(np.float16)
+    b = rng.integers(-9, 10, N).astype(np.float32)
+    res = rng.integers(-4, 5, (B, M, 24)).astype(np.float16)
+    say("f16 gemm ints act", act)
+    out, Wp = run_gpu(hip, A, W, b, act=act, res=res, B=B)
+    for i in range(B):
+        ref = O.gemm_f16(A[i], Wp, b, act=act, res=res[i])
+        assert np.array_equal(out[i].view(np.uint16), ref.view(np.uint16)), i
+
+
+@pytest.mark.parametrize("K,N,M", [(64, 48, 100), (200, 136, 64), (1152, 256, 256), (24, 8, 7)])
+def test_random_within_stated_tolerance(hip, K, N, M):
+    rng = np.random.default_rng(K + N)
+    B = 2
+    Kp = (K + 7) // 8 * 8
+    A = np.zeros((B, M, Kp), np.float16)
+    A[:, :, :K] = rng.standard_normal((B, M, K))
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    say("f16 gemm random", K, N, M)
+    out, Wp = run_gpu(hip, A, W, b, B=B)
+    nblk = (Kp + 127) // 128
+    n = ((Kp + nblk - 1) // nblk + 7) // 8 * 8
+    for i in range(B):
+        ref = O.gemm_f16(A[i], Wp, b).astype(np.float64)
+        g = out[i].astype(np.float64)
+        S = np.abs(A[i].astype(np.float64)) @ np.abs(Wp.astype(np.float64)).T + np.abs(np.pad(b, (0, Wp.shape[0] - N)))
+        Np = (N + 7) // 8 * 8
+        S = np.pad(S, ((0, 0), (0, Np - S.shape[1])))
+        tol = (n + 2) * 2.0 ** -11 * S + 2.0 ** -10 * np.abs(ref) + 2.0 ** -24
+        assert (np.abs(g - ref) <= tol).all(), np.max(np.abs(g - ref) / tol)
+        # and closer to the exact product than the reference's fp16 chain is allowed to be
+        exact = A[i].astype(np.float64) @ Wp.astype(np.float64).T + np.pad(b, (0, Np - N))
+        assert (np.abs(g - exact) <= 2.0 ** -10 * np.abs(exact) + 2.0 ** -24 + Kp * 2.0 ** -24 * S).all()
+
+
+def test_padded_output_and_silu(hip):
+    rng = np.random.default_rng(5)
+    B, M, N, K, ow = 2, 48, 32, 64, 8
+    A = rng.integers(-2, 3, (B, M, K)).astype(np.float16)
+    W = rng.integers(-2, 3, (N, K)).astype(np.float16)
+    b = rng.integers(-3, 4, N).astype(np.float32)
+    say("f16 gemm padded")
+    out, Wp = run_gpu(hip, A, W, b, act=1, ow=ow, opad=2, B=B)
+    for i in range(B):
+        ref = O.gemm_f16(A[i], Wp, b, act=1, ow=ow, opad=2)
+        assert np.array_equal(out[i].view(np.uint16), ref.view(np.uint16))
+
+
+def test_bad_params_refused(hip):
+    H = hip
+    w, b = np.zeros(256, np.float16), np.zeros(32, np.float32)
+    assert not H.lib().bnh_h16w_new(10, 16, 16, 10, w.ctypes.data, b.ctypes.data)
+    assert b"Np = N rounded up to 8" in H.lib().bnh_last_error()
