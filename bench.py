@@ -14,6 +14,9 @@ windows already resident in HBM):
                    (--k 3|5) at stride --s 1|2, 'same' padding, bias + SiLU,
                    batch 64 windows: fp16 (libbnneon's DWK fp16 kernel) or
                    int8 with per-channel Q31 requant and a SiLU table.
+  wino_f16         the fp16 Winograd F(2x2,3x3) convolution 64 -> 64 channels
+                   over 96 x 256, stride 1, pad 1, fp32 accumulation, bias +
+                   SiLU, batch 64 windows.
 
 The timed region is bracketed by device synchronisation; the dominant
 kernel's average duration comes from HIP events recorded on the stream the
@@ -45,7 +48,7 @@ def parse():
     ap.add_argument("--batch", type=int, default=None,
                     help="windows per launch (256; 64 for the depthwise workloads)")
     ap.add_argument("--workload", default="gemm_s8_requant",
-                    choices=["gemm_s8_requant", "pw_s8", "dw_f16", "dw_s8", "copy"])
+                    choices=["gemm_s8_requant", "pw_s8", "dw_f16", "dw_s8", "wino_f16", "copy"])
     ap.add_argument("--k", type=int, default=5, choices=[3, 5], help="depthwise kernel size")
     ap.add_argument("--s", type=int, default=1, choices=[1, 2], help="depthwise stride")
     ap.add_argument("--no-cpu", action="store_true",
@@ -194,7 +197,7 @@ def main():
     if H.lib().bnh_device_count() < 1:
         raise SystemExit("no HIP device visible")
     rng = np.random.default_rng(20240601)
-    B = a.batch or (64 if a.workload.startswith("dw_") else 256)
+    B = a.batch or (64 if a.workload.startswith(("dw_", "wino")) else 256)
     N, K, M = 256, 1152, 1536
     stream = H.lib().bnh_stream_new()
     if a.workload == "copy":
@@ -211,6 +214,9 @@ def main():
         return
     if a.workload.startswith("dw_"):
         run_dw(a, H, rng, B, stream)
+        return
+    if a.workload == "wino_f16":
+        run_wino(a, H, rng, B, stream)
         return
     if a.workload == "gemm_s8_requant":
         w, x, bias, mult, shift = config0_inputs(rng, B)
@@ -327,6 +333,65 @@ def run_dw(a, H, rng, B, stream):
     }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_dw(d, kind, C, Hh, W, k, s)
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_wino(xp, w, b):
+    """float64 direct convolution (numpy), the comparison oracle, on a bounded sample of windows."""
+    T = 1
+    t0 = time.perf_counter()
+    n = 0
+    while n == 0 or time.perf_counter() - t0 < 5.0:
+        x = xp[n % xp.shape[0]].astype(np.float64)
+        H, W = x.shape[0] - 2, x.shape[1] - 2
+        cols = np.stack([x[ky:ky + H, kx:kx + W] for ky in range(3) for kx in range(3)], axis=2)
+        y = cols.reshape(H * W, -1) @ w.reshape(w.shape[0], -1).T.astype(np.float64) + b
+        y = y / (1 + np.exp(-y))
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "windows/s", "cores": T, "kind": "port",
+            "sample": f"{n} windows of the 64->64 3x3 conv over 96x256 as a float64 im2col GEMM + SiLU "
+                      f"(numpy, BLAS threads as configured), {dt:.2f} s wall"}
+
+
+def run_wino(a, H, rng, B, stream):
+    Hh, W, C, K = 96, 256, 64, 64
+    xp = np.zeros((B, Hh + 2, W + 2, C), np.float16)
+    xp[:, 1:-1, 1:-1] = rng.standard_normal((B, Hh, W, C))
+    w = (rng.standard_normal((K, 3, 3, C)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b = (rng.standard_normal(K) * 0.1).astype(np.float32)
+    L = H.lib()
+    P = L.bnh_wino16_new(C, K, w.ctypes.data, b.ctypes.data)
+    if not P:
+        H.check(None, "bnh_wino16_new")
+    x_ws = (Hh + 2) * (W + 2) * C
+    o_ws = Hh * W * K
+    dx = H.DeviceArray.from_host(xp)
+    dout = H.DeviceArray.zeros((B, o_ws), np.float16)
+
+    def launch():
+        H.check(L.bnh_wino_f16(dx.ptr, x_ws, Hh, W, C, P, 1, dout.ptr, o_ws, K, 0, None, 0, 0, B, stream))
+    ms, wall = time_steps(H, stream, launch, a.steps, a.warmup)
+    bytes_per_launch = B * (x_ws + o_ws) * 2 + 16 * K * C * 2
+    gbs = bytes_per_launch / (ms * 1e-3) / 1e9
+    flops_direct = 2.0 * B * Hh * W * K * C * 9
+    line = {
+        "metric": "windows/s (fp16 Winograd conv, batch 64)", "value": round(B / (ms * 1e-3), 1),
+        "unit": "windows/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (seeded; config distributions)",
+        "config": {"workload": "fp16 Winograd F(2x2,3x3) conv 64->64 over 96x256, stride 1, pad 1, fp32 "
+                               "accumulation on fp16 MFMA, bias + SiLU, NHWC",
+                   "global_batch": B, "channels_in": C, "channels_out": K, "height": Hh, "width": W,
+                   "parallelism": "1 GPU, windows batched per launch", "wall_s_timed_region": round(wall, 4)},
+        "direct_equivalent_tflops": round(flops_direct / (ms * 1e-3) / 1e12, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_wino_f16",
+                     "algorithmic_bytes_per_launch": bytes_per_launch},
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_wino(xp, w, b)
+    L.bnh_wino16_free(P)
     print(json.dumps(line), flush=True)
 
 

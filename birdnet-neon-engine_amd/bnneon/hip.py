@@ -73,6 +73,9 @@ _SIGS = {
     "bnh_h16w_new": (vp, [i32, i32, i32, i32, vp, vp]),
     "bnh_h16w_free": (None, [vp]),
     "bnh_gemm_f16": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
+    "bnh_wino16_new": (vp, [i32, i32, vp, vp]),
+    "bnh_wino16_free": (None, [vp]),
+    "bnh_wino_f16": (i32, [vp, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp, i64, i32, i32, vp]),
     "bnh_dwk_f32": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp,
                           i32, vp, i64, i32, i32, vp, i64, i32, vp]),
     "bnh_dw3_f32": (i32, [vp, i64, i32, i32, i32, i32, vp, vp, vp, i64, i32,

@@ -1,0 +1,232 @@
+// fp16 Winograd F(2x2, 3x3) convolution, stride 1, 'same' (pad 1), on gfx950 fp16 MFMA (the Winograd / fp16 GEMM
+// path of libbnneon: src/wino_s0.c's transform structure, src/wino.c's tiling), one fused kernel:
+//
+//   V = B^T d B   per 4x4 input tile and input channel   (fp16 adds in wino_s0.c's order, in_tf :80-97)
+//   M_p = V_p U_p per position p = 0..15                  (fp16 MFMA, fp32 accumulation over the input channels)
+//   y = A^T M A + b, activation, + residual               (fp32, one rounding to fp16 at the end)
+//
+// with U = G g G^T computed once at load in fp32 and rounded to fp16 (wino_s0_pack, :40-64). Coefficients:
+// B^T = [[1,0,-1,0],[0,1,1,0],[0,-1,1,0],[0,1,0,-1]], G = [[1,0,0],[.5,.5,.5],[.5,-.5,.5],[0,0,1]],
+// A^T = [[1,1,1,0],[0,1,-1,-1]].
+//
+// Work split: a block owns one window's strip of 32 output columns (16 tiles across) and walks its row pairs
+// (one tile row per step). A wave owns 16 output channels and keeps their U fragments for all 16 positions and all
+// input channels in registers for the whole strip (loaded once). Per step the block transforms the 16 tiles' input
+// into LDS (V [16 positions][16 tiles][Cp]), every wave runs 16 x Cp/32 MFMAs (A = V rows of 16 tiles, B = its U),
+// and each lane, holding all 16 positions of 4 tiles for one channel, applies the output transform in registers.
+#include <string.h>
+
+#include "bnh_internal.h"
+#include "bnh_num.h"
+#include "bnh_f16.h"
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+struct bnh_wino16 {
+  int C, K, Cp, Kp;  // Cp = C rounded up to 32 (the MFMA k step), Kp = K rounded up to 16
+  uint16_t *U;       // [16][Kp][Cp] fp16, zero past C and K
+  float *b;          // [Kp]
+};
+
+#define WT_TILES 16  // tiles per step (the MFMA row dimension)
+
+template <int NCO, int NCH>  // NCO waves of 16 output channels, NCH = Cp / 32 MFMA k steps
+__global__ __launch_bounds__(64 * NCO) void k_wino_f16(const uint16_t *__restrict__ x, long long x_ws, int H, int W,
+                                                       int C, int ldx, const uint16_t *__restrict__ U,
+                                                       const float *__restrict__ bias, int K, int act,
+                                                       uint16_t *__restrict__ out, long long o_ws, int ldo, int opad,
+                                                       const uint16_t *__restrict__ res, long long r_ws, int ldr,
+                                                       int strips) {
+  constexpr int CP = 32 * NCH;
+  __shared__ __attribute__((aligned(16))) _Float16 V[16 * WT_TILES * CP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int win = blockIdx.x / strips, strip = blockIdx.x % strips;
+  const int T = W / 2, tx0 = strip * WT_TILES;  // first tile column of the strip
+  const int Wp = W + 2;
+  const h16 *xw = (const h16 *)x + win * x_ws;
+  // this wave's U fragments: position p, k step c -> lane holds channels co = 16 wave + (lane & 15), input channels
+  // 32 c + 8 (lane >> 4) .. + 7
+  const int co = 16 * wave + (lane & 15);
+  v8h u[16][NCH];
+#pragma unroll
+  for (int p = 0; p < 16; p++)
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+      u[p][c] = *(const v8h *)(U + ((long long)(p * (16 * NCO) + co)) * CP + 32 * c + 8 * (lane >> 4));
+  const float bco = bias[co];
+  // input-transform work items: (tile, group of 4 input channels)
+  const int groups = C / 4;
+  for (int ty = 0; ty < H / 2; ty++) {
+    // ---- V = B^T d B for the 16 tiles of this step (fp16, wino_s0.c in_tf order)
+    for (int it = tid; it < WT_TILES * (CP / 4); it += 64 * NCO) {
+      const int t = it % WT_TILES, g4 = it / WT_TILES;
+      v4h vv[16];
+      if (g4 < groups && tx0 + t < T) {
+        const h16 *d = xw + ((long long)(2 * ty) * Wp + 2 * (tx0 + t)) * ldx + 4 * g4;
+        v4h dd[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+          for (int cc = 0; cc < 4; cc++) dd[r][cc] = *(const v4h *)(d + ((long long)r * Wp + cc) * ldx);
+        v4h tt[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          tt[0][j] = dd[0][j] - dd[2][j];
+          tt[1][j] = dd[1][j] + dd[2][j];
+          tt[2][j] = dd[2][j] - dd[1][j];
+          tt[3][j] = dd[1][j] - dd[3][j];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          vv[4 * i + 0] = tt[i][0] - tt[i][2];
+          vv[4 * i + 1] = tt[i][1] + tt[i][2];
+          vv[4 * i + 2] = tt[i][2] - tt[i][1];
+          vv[4 * i + 3] = tt[i][1] - tt[i][3];
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < 16; p++) vv[p] = (v4h){};  // input channels past C, tiles past the image: zero rows
+      }
+#pragma unroll
+      for (int p = 0; p < 16; p++) *(v4h *)(V + (p * WT_TILES + t) * CP + 4 * g4) = vv[p];
+    }
+    __syncthreads();
+    // ---- M_p = V_p U_p: lane rows = tiles 4 (lane >> 4) + r, column = channel co
+    v4f acc[16];
+#pragma unroll
+    for (int p = 0; p < 16; p++) {
+      acc[p] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NCH; c++) {
+        const v8h a = *(const v8h *)(V + (p * WT_TILES + (lane & 15)) * CP + 32 * c + 8 * (lane >> 4));
+        acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u[p][c], acc[p], 0, 0, 0);
+      }
+    }
+    __syncthreads();  // V is rewritten by the next step
+    if (co >= K) continue;
+    // ---- y = A^T M A + b per tile; 2 x 2 outputs of channel co
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int t = 4 * (lane >> 4) + r;
+      if (tx0 + t >= T) continue;
+      float s[2][4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        s[0][j] = (acc[j][r] + acc[4 + j][r]) + acc[8 + j][r];
+        s[1][j] = (acc[4 + j][r] - acc[8 + j][r]) - acc[12 + j][r];
+      }
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int jx = 0; jx < 2; jx++) {
+          float y = jx == 0 ? (s[i][0] + s[i][1]) + s[i][2] : (s[i][1] - s[i][2]) - s[i][3];
+          y = y + bco;
+          if (act == 1) y = bnh_silu_f32(y);
+          else if (act == 2) y = bnh_relu_f32(y);
+          const int oy = 2 * ty + i, ox = 2 * (tx0 + t) + jx;
+          h16 v = (h16)y;
+          if (res) v = v + hfrom(res[win * r_ws + ((long long)oy * W + ox) * ldr + co]);
+          const long long orow = opad ? (long long)(oy + opad) * (W + 2 * opad) + ox + opad : (long long)oy * W + ox;
+          out[win * o_ws + orow * ldo + co] = hbits(v);
+        }
+    }
+  }
+}
+
+__global__ void k_zero_halo16(uint16_t *__restrict__ out, long long ws, int H, int W, int C, int h, long long total) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int Wp = W + 2 * h;
+  const long long per = (long long)(H + 2 * h) * Wp * C;
+  const int w = (int)(i / per);
+  const long long el = i % per, px = el / C;
+  const int y = (int)(px / Wp), xx = (int)(px % Wp);
+  if (y >= h && y < H + h && xx >= h && xx < W + h) return;
+  out[w * ws + el] = 0;
+}
+
+extern "C" {
+
+bnh_wino16 *bnh_wino16_new(int C, int K, const float *w, const float *bias) {
+  if (C <= 0 || K <= 0 || C % 4 || C > 64 || K > 64 || !w) {
+    bnh_fail("bnh_wino16_new: C %d K %d: expected C %% 4 == 0, C <= 64, K <= 64 and the weights", C, K);
+    return nullptr;
+  }
+  const int Cp = (int)bnh_round_up(C, 32), Kp = (int)bnh_round_up(K, 16);
+  uint16_t *hu = (uint16_t *)calloc((size_t)16 * Kp * Cp, 2);
+  float *hb = (float *)calloc(Kp, 4);
+  bnh_wino16 *P = (bnh_wino16 *)calloc(1, sizeof *P);
+  if (!hu || !hb || !P) {
+    free(hu); free(hb); free(P);
+    bnh_fail("bnh_wino16_new: out of host memory");
+    return nullptr;
+  }
+  static const float G[4][3] = {{1, 0, 0}, {.5f, .5f, .5f}, {.5f, -.5f, .5f}, {0, 0, 1}};
+  for (int o = 0; o < K; o++) {
+    hb[o] = bias ? bias[o] : 0.f;
+    for (int ci = 0; ci < C; ci++) {  // w OHWI [K][3][3][C] fp32; U = G g G^T in fp32, rounded to fp16
+      float g[3][3], t[4][3];
+      for (int ky = 0; ky < 3; ky++)
+        for (int kx = 0; kx < 3; kx++) g[ky][kx] = w[((o * 3 + ky) * 3 + kx) * C + ci];
+      for (int i = 0; i < 4; i++)
+        for (int kx = 0; kx < 3; kx++) t[i][kx] = G[i][0] * g[0][kx] + G[i][1] * g[1][kx] + G[i][2] * g[2][kx];
+      for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 4; j++) {
+          const float uv = t[i][0] * G[j][0] + t[i][1] * G[j][1] + t[i][2] * G[j][2];
+          const _Float16 hv = (_Float16)uv;
+          memcpy(&hu[((size_t)(i * 4 + j) * Kp + o) * Cp + ci], &hv, 2);
+        }
+    }
+  }
+  P->C = C; P->K = K; P->Cp = Cp; P->Kp = Kp;
+  bool ok = (P->U = (uint16_t *)bnh_malloc((size_t)16 * Kp * Cp * 2)) && (P->b = (float *)bnh_malloc(4 * (size_t)Kp)) &&
+            !bnh_memcpy_h2d(P->U, hu, (size_t)16 * Kp * Cp * 2) && !bnh_memcpy_h2d(P->b, hb, 4 * (size_t)Kp);
+  free(hu); free(hb);
+  if (!ok) { bnh_wino16_free(P); return nullptr; }
+  return P;
+}
+
+void bnh_wino16_free(bnh_wino16 *P) {
+  if (!P) return;
+  if (P->U) (void)hipFree(P->U);
+  if (P->b) (void)hipFree(P->b);
+  free(P);
+}
+
+int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const bnh_wino16 *P, int act, uint16_t *out,
+                 long long o_ws, int ldo, int opad, const uint16_t *res, long long r_ws, int ldr, int B, void *stream) {
+  BNH_REQ(x && P && out && H > 0 && W > 0 && H % 2 == 0 && W % 2 == 0 && B > 0);
+  BNH_REQ(ldx >= P->C && ldx % 4 == 0 && ldo >= P->K && (opad == 0 || opad == 1) && act >= 0 && act <= 2);
+  BNH_REQ(((uintptr_t)x & 7) == 0 && (B == 1 || x_ws % 4 == 0));
+  BNH_REQ(!res || ldr >= P->K);
+  BNH_REQ(B == 1 || (x_ws >= (long long)(H + 2) * (W + 2) * ldx && o_ws >= (long long)(H + 2 * opad) * (W + 2 * opad) * ldo));
+  hipStream_t st = bnh_stream(stream);
+  if (opad) {
+    const long long per = (long long)(H + 2) * (W + 2) * ldo, total = per * B;
+    hipLaunchKernelGGL(k_zero_halo16, dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, out,
+                       B == 1 ? per : o_ws, H, W, ldo, 1, total);
+    BNH_HIP(hipGetLastError());
+  }
+  const int strips = (int)bnh_ceil_div(W / 2, WT_TILES);
+  const dim3 grid((unsigned)((long long)strips * B));
+  const int nco = P->Kp / 16, nch = P->Cp / 32;
+#define WINO_LAUNCH(NCO, NCH)                                                                                          \
+  hipLaunchKernelGGL((k_wino_f16<NCO, NCH>), grid, dim3(64 * NCO), 0, st, x, x_ws, H, W, P->C, ldx, P->U, P->b, P->K, \
+                     act, out, o_ws, ldo, opad, res, r_ws, ldr, strips)
+  if (nch == 1) {
+    if (nco == 1) WINO_LAUNCH(1, 1); else if (nco == 2) WINO_LAUNCH(2, 1); else if (nco == 3) WINO_LAUNCH(3, 1);
+    else WINO_LAUNCH(4, 1);
+  } else if (nch == 2) {
+    if (nco == 1) WINO_LAUNCH(1, 2); else if (nco == 2) WINO_LAUNCH(2, 2); else if (nco == 3) WINO_LAUNCH(3, 2);
+    else WINO_LAUNCH(4, 2);
+  } else {
+    BNH_REQ(nch <= 2);  // C <= 64 in this kernel family
+  }
+#undef WINO_LAUNCH
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"

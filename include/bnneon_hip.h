@@ -140,6 +140,21 @@ typedef struct {
 int bnh_gemm_f16(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
                  void *stream);
 
+/* ------------------------------------------------------------------ fp16 Winograd F(2x2, 3x3) convolution
+ * The Winograd / fp16 GEMM path (src/wino_s0.c:1-165 for the transforms, src/wino.c for the tiling): a 3 x 3,
+ * stride 1, pad 1 convolution of C <= 64 input channels (C % 4 == 0) into K <= 64 output channels. Weights OHWI fp32
+ * [K][3][3][C] and bias [K] are transformed once (U = G g G^T in fp32, rounded to fp16, as wino_s0_pack). Per window:
+ * x fp16 zero-haloed [H+2][W+2][ldx] (H, W even); out fp16 [H][W][ldo] (opad 0) or zero-haloed [H+2][W+2][ldo]
+ * (opad 1); optional fp16 residual [H][W][ldr] added last. V = B^T d B in fp16 (wino_s0.c's order), the 16
+ * position GEMMs on fp16 MFMA with fp32 accumulation, y = A^T M A + b and the activation (0 none, 1 the fp32 SiLU,
+ * 2 ReLU) in fp32, one rounding to fp16. Within the fp16 Winograd error bound of a direct convolution (the
+ * parity tests state it), not bit-identical to the reference's fp16 chains. */
+typedef struct bnh_wino16 bnh_wino16;
+bnh_wino16 *bnh_wino16_new(int C, int K, const float *w, const float *bias);
+void bnh_wino16_free(bnh_wino16 *P);
+int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const bnh_wino16 *P, int act, uint16_t *out,
+                 long long o_ws, int ldo, int opad, const uint16_t *res, long long r_ws, int ldr, int B, void *stream);
+
 /* ------------------------------------------------------------------ depthwise convolutions
  * NHWC, weights [k*k][C] (tap-major), per-window strides in elements. xp is the zero-haloed input of the reference's
  * buffers: [H + 2h][W + 2h][C], h = (k - 1) / 2 (1 for the DW3 forms); output pixel (oy, ox) reads the k x k taps
