@@ -76,6 +76,10 @@ _SIGS = {
     "bnh_wino16_new": (vp, [i32, i32, vp, vp]),
     "bnh_wino16_free": (None, [vp]),
     "bnh_wino_f16": (i32, [vp, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp, i64, i32, i32, vp]),
+    "bnh_wino8_new": (vp, [i32, i32, vp, vp]),
+    "bnh_wino8_free": (None, [vp]),
+    "bnh_wino8_work_bytes": (C.c_size_t, [i32, i32, i32, i32]),
+    "bnh_wino_s8": (i32, [vp, i64, i32, i32, vp, vp, i64, i32, vp, C.c_size_t, vp]),
     "bnh_dwk_f32": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp,
                           i32, vp, i64, i32, i32, vp, i64, i32, vp]),
     "bnh_dw3_f32": (i32, [vp, i64, i32, i32, i32, i32, vp, vp, vp, i64, i32,

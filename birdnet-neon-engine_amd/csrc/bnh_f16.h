@@ -10,6 +10,13 @@ BNH_DEV uint16_t hbits(h16 x) { return __builtin_bit_cast(uint16_t, x); }
 BNH_DEV h16 hfrom(uint16_t u) { return __builtin_bit_cast(h16, u); }
 BNH_DEV bool hnan(h16 x) { return x != x; }
 BNH_DEV h16 hfma(h16 a, h16 b, h16 c) { return __builtin_fmaf16(a, b, c); }
+// fp32 -> fp16, round to nearest even, of a value that has already been rounded to fp32 (FCVT h, s after an fp32
+// operation). The empty asm pins the fp32 result in a register: without it the compiler may fold the producing
+// fp32 FMA / add and this conversion into one v_fma_mix*_f16, a single rounding straight to fp16.
+BNH_DEV h16 f2h(float y) {
+  __asm__("" : "+v"(y));
+  return (h16)y;
+}
 // FMAX / FMIN on fp16 (NaN-propagating, +0 above -0)
 BNH_DEV h16 hmax(h16 a, h16 b) {
   if (hnan(a) || hnan(b)) return hfrom(0x7e00);

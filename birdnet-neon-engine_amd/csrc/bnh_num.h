@@ -46,6 +46,8 @@ BNH_DEV int32_t bnh_sat_s32(float r) {  // r integral, or NaN / inf
 }
 // FCVTNS (vcvtnq_s32_f32): nearest even, int32-saturating
 BNH_DEV int32_t bnh_cvtn_s32(float x) { return bnh_sat_s32(__builtin_rintf(x)); }
+// FCVTZS w (the C cast float -> int32 on AArch64): toward zero, saturating, NaN -> 0
+BNH_DEV int32_t bnh_cvtz_s32(float x) { return bnh_sat_s32(__builtin_truncf(x)); }
 // FCVTAS (vcvtaq_s32_f32): nearest, ties away from zero, int32-saturating
 BNH_DEV int32_t bnh_cvta_s32(float x) {
   float t = __builtin_truncf(x);

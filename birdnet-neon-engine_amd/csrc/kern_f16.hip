@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(const uint16_t *__restrict__ A
         const long long row = row0 + 16 * t + 4 * (lane >> 4) + r;
         if (row >= rows) continue;
         const int w = (int)(row / M), m = (int)(row % M);
-        h16 v = (h16)(acc[t][j][r] + bn);  // fp32 add, one rounding to fp16 (nearest even)
+        h16 v = f2h(acc[t][j][r] + bn);  // fp32 add, then one rounding to fp16 (nearest even)
         if (e.act == 1) v = silu_lut_h(v);
         else if (e.act == 2) v = hmax(v, (h16)0.0f);
         if (e.res) v = v + hfrom(e.res[w * e.res_ws + (long long)m * e.ldr + n]);

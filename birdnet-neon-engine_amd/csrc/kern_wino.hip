@@ -14,6 +14,7 @@
 // input channels in registers for the whole strip (loaded once). Per step the block transforms the 16 tiles' input
 // into LDS (V [16 positions][16 tiles][Cp]), every wave runs 16 x Cp/32 MFMAs (A = V rows of 16 tiles, B = its U),
 // and each lane, holding all 16 positions of 4 tiles for one channel, applies the output transform in registers.
+#include <math.h>
 #include <string.h>
 
 #include "bnh_internal.h"
@@ -23,6 +24,7 @@
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct bnh_wino16 {
   int C, K, Cp, Kp;  // Cp = C rounded up to 32 (the MFMA k step), Kp = K rounded up to 16
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(64 * NCO) void k_wino_f16(const uint16_t *__restric
           if (act == 1) y = bnh_silu_f32(y);
           else if (act == 2) y = bnh_relu_f32(y);
           const int oy = 2 * ty + i, ox = 2 * (tx0 + t) + jx;
-          h16 v = (h16)y;
+          h16 v = f2h(y);
           if (res) v = v + hfrom(res[win * r_ws + ((long long)oy * W + ox) * ldr + co]);
           const long long orow = opad ? (long long)(oy + opad) * (W + 2 * opad) + ox + opad : (long long)oy * W + ox;
           out[win * o_ws + orow * ldo + co] = hbits(v);
@@ -225,6 +227,245 @@ int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const
     BNH_REQ(nch <= 2);  // C <= 64 in this kernel family
   }
 #undef WINO_LAUNCH
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"
+
+// ================================================================== int8 Winograd F(2x2, 3x3) (WINO_S8)
+// libbnneon's int8 Winograd (src/wino.c:26-227, the WINO_S8 op of src/rt_ops_dot.c:130-170), bit-identical:
+//   V = B^T d B in fp32, quantised with ONE asymmetric scale per tile (over its 16 positions x C): s = range / 255,
+//   zp = round(min / s) + 128, q = clamp(round(v / s) - zp) through the reference's magic-number FMA;
+//   U = G g G^T quantised with ONE symmetric scale per output channel (over 16 x C) at load;
+//   raw int32 position GEMMs on int8 MFMA, the integer output transform A^T M A, and per output
+//   y = fma(zw[o], s zp, fma(float(Y) sw, s, b)), fp32 -> fp16, the fp16 LUT SiLU.
+// Two kernels: k_wino8_in quantises the tiles (one wave per tile) into a scratch A8 [16][tiles][Cp] with the tile
+// scales; k_wino8_out runs, per 16 tiles x 64 output channels, the 16 position GEMMs and the output transform in
+// registers (a lane holds all 16 positions of 4 tiles for one channel).
+struct bnh_w8w {
+  int C, K, Cp, Kp;
+  int8_t *U;         // [16][Kp][Cp], zero past C and K
+  float *sw, *zw, *b;  // [Kp], [4][Kp], [Kp]
+};
+
+__global__ __launch_bounds__(256) void k_wino8_in(const float *__restrict__ x, long long x_ws, int H, int W, int C,
+                                                  int Cp, int tw, int T, int Tp, int8_t *__restrict__ a8,
+                                                  float *__restrict__ tsc, int B) {
+  const int lane = threadIdx.x & 63;
+  const long long gt = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);  // global tile index over all windows
+  if (gt >= (long long)T * B) return;
+  const int win = (int)(gt / T), t = (int)(gt % T), ti = t / tw, tj = t % tw;
+  const float *xw = x + win * x_ws;
+  auto tile_v = [&](int c, float v[16]) {
+    float d[4][4], tm[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int cc = 0; cc < 4; cc++) {
+        const int y = 2 * ti + r - 1, xx = 2 * tj + cc - 1;
+        d[r][cc] = (y >= 0 && y < H && xx >= 0 && xx < W) ? xw[((long long)y * W + xx) * C + c] : 0.f;
+      }
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) {
+      tm[0][cc] = d[0][cc] - d[2][cc]; tm[1][cc] = d[1][cc] + d[2][cc];
+      tm[2][cc] = d[2][cc] - d[1][cc]; tm[3][cc] = d[1][cc] - d[3][cc];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      v[r * 4 + 0] = tm[r][0] - tm[r][2]; v[r * 4 + 1] = tm[r][1] + tm[r][2];
+      v[r * 4 + 2] = tm[r][2] - tm[r][1]; v[r * 4 + 3] = tm[r][1] - tm[r][3];
+    }
+  };
+  // pass 1: the tile's min / max over 16 positions x C, starting from 0 (FMIN / FMAX: any order gives the same)
+  float mn = 0.f, mx = 0.f;
+  for (int c = lane; c < C; c += 64) {
+    float v[16];
+    tile_v(c, v);
+#pragma unroll
+    for (int p = 0; p < 16; p++) { mn = bnh_fmin(mn, v[p]); mx = bnh_fmax(mx, v[p]); }
+  }
+  for (int off = 32; off; off >>= 1) {
+    mn = bnh_fmin(mn, __shfl_xor(mn, off));
+    mx = bnh_fmax(mx, __shfl_xor(mx, off));
+  }
+  float s = (mx - mn) > 0 ? (mx - mn) / 255.f : 1.f;
+  if (s < 1e-30f) s = 1e-30f;
+  const float inv = 1.f / s, zp = __builtin_rintf(mn * inv) + 128.f;
+  const uint32_t zofs = 0x4B400000u + (uint32_t)bnh_cvtz_s32(zp);
+  if (lane == 0) {
+    tsc[2 * gt] = s;
+    tsc[2 * gt + 1] = s * zp;
+  }
+  // pass 2: quantise; channels past C are zero
+  int8_t *o = a8 + (long long)win * 16 * Tp * Cp + (long long)t * Cp;
+  for (int c = lane; c < Cp; c += 64) {
+    float v[16];
+    if (c < C) tile_v(c, v);
+#pragma unroll
+    for (int p = 0; p < 16; p++) {
+      int8_t q = 0;
+      if (c < C) {
+        const int32_t m = (int32_t)(__float_as_uint(__builtin_fmaf(v[p], inv, 12582912.0f)) - zofs);
+        q = (int8_t)(m < -128 ? -128 : m > 127 ? 127 : m);
+      }
+      o[(long long)p * Tp * Cp + c] = q;
+    }
+  }
+}
+
+// 4 waves, each 16 output channels; 16 tiles per block (the MFMA rows)
+__global__ __launch_bounds__(256) void k_wino8_out(const int8_t *__restrict__ a8, const float *__restrict__ tsc, int Cp,
+                                                   int tw, int T, int Tp, const int8_t *__restrict__ U, int Kp, int K,
+                                                   const float *__restrict__ sw, const float *__restrict__ zw,
+                                                   const float *__restrict__ bias, int H, int W,
+                                                   uint16_t *__restrict__ out, long long o_ws) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int win = blockIdx.z, t0 = blockIdx.x * 16, co = blockIdx.y * 64 + 16 * wave + (lane & 15);
+  const int8_t *aw = a8 + (long long)win * 16 * Tp * Cp;
+  const int ar = t0 + (lane & 15);  // this lane's A row (tile); rows past T hold zeros (Tp padding)
+  v4i acc[16];
+#pragma unroll
+  for (int p = 0; p < 16; p++) {
+    acc[p] = (v4i){0, 0, 0, 0};
+    const int8_t *ap = aw + ((long long)p * Tp + ar) * Cp + 16 * (lane >> 4);
+    const int8_t *bp = U + ((long long)p * Kp + (co < Kp ? co : Kp - 1)) * Cp + 16 * (lane >> 4);
+    for (int k = 0; k < Cp; k += 64)
+      acc[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i *)(ap + k), *(const v4i *)(bp + k), acc[p], 0, 0, 0);
+  }
+  if (co >= K) return;
+  const float swk = sw[co], bk = bias[co];
+  const float zwk[4] = {zw[co], zw[Kp + co], zw[2 * Kp + co], zw[3 * Kp + co]};
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int t = t0 + 4 * (lane >> 4) + r;
+    if (t >= T) continue;
+    const float sa = tsc[2 * ((long long)win * T + t)], zs = tsc[2 * ((long long)win * T + t) + 1];
+    uint32_t s0[4], s1[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) {
+      s0[cc] = ((uint32_t)acc[cc][r] + (uint32_t)acc[4 + cc][r]) + (uint32_t)acc[8 + cc][r];
+      s1[cc] = ((uint32_t)acc[4 + cc][r] - (uint32_t)acc[8 + cc][r]) - (uint32_t)acc[12 + cc][r];
+    }
+    const uint32_t Y[4] = {(s0[0] + s0[1]) + s0[2], (s0[1] - s0[2]) - s0[3], (s1[0] + s1[1]) + s1[2],
+                           (s1[1] - s1[2]) - s1[3]};
+    const int ti = t / tw, tj = t % tw;
+#pragma unroll
+    for (int o = 0; o < 4; o++) {
+      const int oy = 2 * ti + o / 2, ox = 2 * tj + o % 2;
+      if (oy >= H || ox >= W) continue;
+      const float inner = __builtin_fmaf((float)(int32_t)Y[o] * swk, sa, bk);
+      const float y = __builtin_fmaf(zwk[o], zs, inner);
+      out[win * o_ws + ((long long)oy * W + ox) * K + co] = hbits(silu_lut_h(f2h(y)));
+    }
+  }
+}
+
+extern "C" {
+
+bnh_w8w *bnh_wino8_new(int C, int K, const float *w, const float *bias) {
+  if (C <= 0 || K <= 0 || C % 8 || C > 2048 || K % 16 || K > 2048 || !w || !bias) {
+    bnh_fail("bnh_wino8_new: C %d K %d: expected C %% 8 == 0, C <= 2048, K %% 16 == 0, K <= 2048 and both tensors",
+             C, K);
+    return nullptr;
+  }
+  const int Cp = (int)bnh_round_up(C, 64), Kp = K;
+  float *U = (float *)malloc(sizeof(float) * 16 * (size_t)K * C);
+  int8_t *hu = (int8_t *)calloc((size_t)16 * Kp * Cp, 1);
+  float *hsw = (float *)calloc(Kp, 4), *hzw = (float *)calloc(4 * (size_t)Kp, 4);
+  int32_t *wsum = (int32_t *)calloc(16 * (size_t)K, 4);
+  bnh_w8w *P = (bnh_w8w *)calloc(1, sizeof *P);
+  if (!U || !hu || !hsw || !hzw || !wsum || !P) {
+    free(U); free(hu); free(hsw); free(hzw); free(wsum); free(P);
+    bnh_fail("bnh_wino8_new: out of host memory");
+    return nullptr;
+  }
+  // wino_pack (src/wino.c:26-88): the same fp32 operations in the same order
+  for (int k = 0; k < K; k++)
+    for (int c = 0; c < C; c++) {
+      float g[3][3], tmp[4][3];
+      for (int r = 0; r < 3; r++)
+        for (int cc = 0; cc < 3; cc++) g[r][cc] = w[(((size_t)k * 3 + r) * 3 + cc) * C + c];
+      for (int cc = 0; cc < 3; cc++) {
+        tmp[0][cc] = g[0][cc];
+        tmp[1][cc] = 0.5f * (g[0][cc] + g[1][cc] + g[2][cc]);
+        tmp[2][cc] = 0.5f * (g[0][cc] - g[1][cc] + g[2][cc]);
+        tmp[3][cc] = g[2][cc];
+      }
+      for (int r = 0; r < 4; r++) {
+        const float u[4] = {tmp[r][0], 0.5f * (tmp[r][0] + tmp[r][1] + tmp[r][2]),
+                            0.5f * (tmp[r][0] - tmp[r][1] + tmp[r][2]), tmp[r][2]};
+        for (int cc = 0; cc < 4; cc++) U[((size_t)(r * 4 + cc) * K + k) * C + c] = u[cc];
+      }
+    }
+  static const int AT[2][4] = {{1, 1, 1, 0}, {0, 1, -1, -1}};
+  for (int k = 0; k < K; k++) {
+    float mx = 0;
+    for (int xi = 0; xi < 16; xi++)
+      for (int c = 0; c < C; c++) mx = fmaxf(mx, fabsf(U[((size_t)xi * K + k) * C + c]));
+    const float s = mx > 0 ? mx / 127.f : 1.f;
+    hsw[k] = s;
+    for (int xi = 0; xi < 16; xi++) {
+      int32_t sum = 0;
+      for (int c = 0; c < C; c++) {
+        int v = (int)nearbyintf(U[((size_t)xi * K + k) * C + c] / s);
+        v = v > 127 ? 127 : (v < -127 ? -127 : v);
+        sum += v;
+        hu[((size_t)xi * Kp + k) * Cp + c] = (int8_t)v;
+      }
+      wsum[xi * K + k] = sum;
+    }
+    for (int r = 0; r < 2; r++)
+      for (int cc = 0; cc < 2; cc++) {
+        long z = 0;
+        for (int i = 0; i < 4; i++)
+          for (int j = 0; j < 4; j++) z += (long)AT[r][i] * AT[cc][j] * wsum[(i * 4 + j) * K + k];
+        hzw[(size_t)(r * 2 + cc) * Kp + k] = s * (float)z;
+      }
+  }
+  free(U); free(wsum);
+  P->C = C; P->K = K; P->Cp = Cp; P->Kp = Kp;
+  bool ok = (P->U = (int8_t *)bnh_malloc((size_t)16 * Kp * Cp)) && (P->sw = (float *)bnh_malloc(4 * (size_t)Kp)) &&
+            (P->zw = (float *)bnh_malloc(16 * (size_t)Kp)) && (P->b = (float *)bnh_malloc(4 * (size_t)Kp)) &&
+            !bnh_memcpy_h2d(P->U, hu, (size_t)16 * Kp * Cp) && !bnh_memcpy_h2d(P->sw, hsw, 4 * (size_t)Kp) &&
+            !bnh_memcpy_h2d(P->zw, hzw, 16 * (size_t)Kp) && !bnh_memcpy_h2d(P->b, bias, 4 * (size_t)K);
+  free(hu); free(hsw); free(hzw);
+  if (!ok) { bnh_wino8_free(P); return nullptr; }
+  return P;
+}
+
+void bnh_wino8_free(bnh_w8w *P) {
+  if (!P) return;
+  if (P->U) (void)hipFree(P->U);
+  if (P->sw) (void)hipFree(P->sw);
+  if (P->zw) (void)hipFree(P->zw);
+  if (P->b) (void)hipFree(P->b);
+  free(P);
+}
+
+size_t bnh_wino8_work_bytes(int H, int W, int C, int B) {
+  const long long T = (long long)((H + 1) / 2) * ((W + 1) / 2), Tp = bnh_round_up(T, 16);
+  const long long Cp = bnh_round_up(C, 64);
+  return (size_t)(B * (16 * Tp * Cp + 8 * T) + 256);
+}
+
+int bnh_wino_s8(const float *x, long long x_ws, int H, int W, const bnh_w8w *P, uint16_t *out, long long o_ws, int B,
+                void *work, size_t work_bytes, void *stream) {
+  BNH_REQ(x && P && out && work && H > 0 && W > 0 && B > 0);
+  BNH_REQ(B == 1 || (x_ws >= (long long)H * W * P->C && o_ws >= (long long)H * W * P->K));
+  BNH_REQ(work_bytes >= bnh_wino8_work_bytes(H, W, P->C, B));
+  const int tw = (W + 1) / 2, T = ((H + 1) / 2) * tw, Tp = (int)bnh_round_up(T, 16);
+  int8_t *a8 = (int8_t *)work;
+  float *tsc = (float *)(a8 + (size_t)B * 16 * Tp * P->Cp);
+  BNH_REQ(((uintptr_t)tsc & 3) == 0);
+  hipStream_t st = bnh_stream(stream);
+  // tile rows past T (up to Tp) of the scratch are read by the GEMM: zero them
+  BNH_HIP(hipMemsetAsync(a8, 0, (size_t)B * 16 * Tp * P->Cp, st));
+  hipLaunchKernelGGL(k_wino8_in, dim3((unsigned)bnh_ceil_div((long long)T * B, 4)), dim3(256), 0, st, x, x_ws, H, W,
+                     P->C, P->Cp, tw, T, Tp, a8, tsc, B);
+  BNH_HIP(hipGetLastError());
+  hipLaunchKernelGGL(k_wino8_out, dim3((unsigned)(Tp / 16), (unsigned)bnh_ceil_div(P->Kp, 64), (unsigned)B), dim3(256),
+                     0, st, a8, tsc, P->Cp, tw, T, Tp, P->U, P->Kp, P->K, P->sw, P->zw, P->b, H, W, out, o_ws);
   BNH_HIP(hipGetLastError());
   return 0;
 }

@@ -155,6 +155,19 @@ void bnh_wino16_free(bnh_wino16 *P);
 int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const bnh_wino16 *P, int act, uint16_t *out,
                  long long o_ws, int ldo, int opad, const uint16_t *res, long long r_ws, int ldr, int B, void *stream);
 
+/* ------------------------------------------------------------------ int8 Winograd F(2x2, 3x3) (WINO_S8)
+ * libbnneon's int8 Winograd for 3 x 3 stride-1 pad-1 convolutions (wino_pack / wino_f23_tiles, src/wino.c:26-227;
+ * the WINO_S8 op, src/rt_ops_dot.c:130-170), bit-identical: weights OHWI fp32 [K][3][3][C] and bias [K] are packed
+ * once (U = G g G^T quantised per output channel); per window x f32 [H][W][C] (rows, ld C) -> out fp16 [H][W][K]
+ * (ld K) = SiLU(conv + b) with per-tile asymmetric int8 activations. C % 8 == 0, K % 16 == 0, both <= 2048. work:
+ * device scratch of at least bnh_wino8_work_bytes(H, W, C, B) bytes (the quantised tiles and their scales). */
+typedef struct bnh_w8w bnh_w8w;
+bnh_w8w *bnh_wino8_new(int C, int K, const float *w, const float *bias);
+void bnh_wino8_free(bnh_w8w *P);
+size_t bnh_wino8_work_bytes(int H, int W, int C, int B);
+int bnh_wino_s8(const float *x, long long x_ws, int H, int W, const bnh_w8w *P, uint16_t *out, long long o_ws, int B,
+                void *work, size_t work_bytes, void *stream);
+
 /* ------------------------------------------------------------------ depthwise convolutions
  * NHWC, weights [k*k][C] (tap-major), per-window strides in elements. xp is the zero-haloed input of the reference's
  * buffers: [H + 2h][W + 2h][C], h = (k - 1) / 2 (1 for the DW3 forms); output pixel (oy, ox) reads the k x k taps

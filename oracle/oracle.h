@@ -112,6 +112,14 @@ typedef struct {
 void orc_gemm_f16(const uint16_t *A, int lda, int M, const uint16_t *W, int N, int Kp, const float *b32,
                   const uint16_t *b16, const orc_epi16 *e);
 
+/* ---------------------------------------------------------------- int8 Winograd F(2x2,3x3) (WINO_S8) */
+int32_t orc_cvtz_s32(float x);  /* FCVTZS w: toward zero, saturating, NaN -> 0 */
+/* src/wino.c:26-88: w OHWI fp32 [K][3][3][C] -> U8 [16][K][C], sw [K], zw [4][K] */
+void orc_wino8_pack(const float *w, int K, int C, int8_t *U8, float *sw, float *zw);
+/* src/wino.c:117-227 for one window: x f32 [H][W][C] -> out fp16 [H][W][K] (bias, LUT SiLU) */
+void orc_wino8(const float *x, int H, int W, int C, int K, const int8_t *U8, const float *sw, const float *zw,
+               const float *bias, uint16_t *out);
+
 /* ---------------------------------------------------------------- Q31 requantised int8 GEMM (own specification)
  * The reference has no such kernel. Specification (TFLite / gemmlowp fixed-point conventions):
  *   acc[n][m]  = sum_k w[n][k] * (x[k][m] - zx) + bias[n]                       (exact, int32)

@@ -301,3 +301,34 @@ def gemm_f16(A, W, b32, act=0, ldo=None, ow=0, opad=0, res=None, M=None):
                  0 if r is None else r.shape[1])
     lib().orc_gemm_f16(A.ctypes.data, lda, M, W.ctypes.data, N, Kp, b32.ctypes.data, b16.ctypes.data, C.byref(e))
     return out
+
+
+_SIGS.update({
+    "orc_cvtz_s32": (i32, [f32]),
+    "orc_wino8_pack": (None, [vp, i32, i32, vp, vp, vp]),
+    "orc_wino8": (None, [vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
+})
+
+
+def wino8_pack(w):
+    """w OHWI fp32 [K][3][3][C] -> (U8 [16][K][C], sw [K], zw [4][K])."""
+    w = _c(w, np.float32)
+    K, C = w.shape[0], w.shape[3]
+    U8 = np.zeros((16, K, C), np.int8)
+    sw = np.zeros(K, np.float32)
+    zw = np.zeros((4, K), np.float32)
+    lib().orc_wino8_pack(w.ctypes.data, K, C, U8.ctypes.data, sw.ctypes.data, zw.ctypes.data)
+    return U8, sw, zw
+
+
+def wino8(x, pk, bias):
+    """x f32 [H][W][C] -> fp16 [H][W][K] (the WINO_S8 op of one window)."""
+    x = _c(x, np.float32)
+    H, W, C = x.shape
+    U8, sw, zw = pk
+    K = U8.shape[1]
+    b = _c(bias, np.float32)
+    out = np.zeros((H, W, K), np.float16)
+    lib().orc_wino8(x.ctypes.data, H, W, C, K, U8.ctypes.data, sw.ctypes.data, zw.ctypes.data, b.ctypes.data,
+                    out.ctypes.data)
+    return out

@@ -69,6 +69,7 @@ static int32_t sat_s32(float r) { /* r integral (or NaN / inf) */
 }
 int32_t orc_cvtn_s32(float x) { return sat_s32(rintf(x)); }
 int32_t orc_cvta_s32(float x) { return sat_s32(roundf(x)); }
+int32_t orc_cvtz_s32(float x) { return sat_s32(truncf(x)); }
 int32_t orc_lrintf_s32(float x) {
   float r = rintf(x);
   int64_t v;
