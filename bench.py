@@ -370,7 +370,7 @@ def run_wino(a, H, rng, B, stream):
     dout = H.DeviceArray.zeros((B, o_ws), np.float16)
 
     def launch():
-        H.check(L.bnh_wino_f16(dx.ptr, x_ws, Hh, W, C, P, 1, dout.ptr, o_ws, K, 0, None, 0, 0, B, stream))
+        H.check(L.bnh_wino_f16(dx.ptr, x_ws, Hh, W, C, P, 1, dout.ptr, o_ws, K, 0, None, 0, 0, 0, B, stream))
     ms, wall = time_steps(H, stream, launch, a.steps, a.warmup)
     bytes_per_launch = B * (x_ws + o_ws) * 2 + 16 * K * C * 2
     gbs = bytes_per_launch / (ms * 1e-3) / 1e9

@@ -75,7 +75,7 @@ _SIGS = {
     "bnh_gemm_f16": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
     "bnh_wino16_new": (vp, [i32, i32, vp, vp]),
     "bnh_wino16_free": (None, [vp]),
-    "bnh_wino_f16": (i32, [vp, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp, i64, i32, i32, vp]),
+    "bnh_wino_f16": (i32, [vp, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp, i64, i32, i32, i32, vp]),
     "bnh_wino8_new": (vp, [i32, i32, vp, vp]),
     "bnh_wino8_free": (None, [vp]),
     "bnh_wino8_work_bytes": (C.c_size_t, [i32, i32, i32, i32]),

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(64 * NCO) void k_wino_f16(const uint16_t *__restric
                                                        const float *__restrict__ bias, int K, int act,
                                                        uint16_t *__restrict__ out, long long o_ws, int ldo, int opad,
                                                        const uint16_t *__restrict__ res, long long r_ws, int ldr,
-                                                       int strips) {
+                                                       int rpad, int strips) {
   constexpr int CP = 32 * NCH;
   __shared__ __attribute__((aligned(16))) _Float16 V[16 * WT_TILES * CP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -129,7 +129,10 @@ __global__ __launch_bounds__(64 * NCO) void k_wino_f16(const uint16_t *__restric
           else if (act == 2) y = bnh_relu_f32(y);
           const int oy = 2 * ty + i, ox = 2 * (tx0 + t) + jx;
           h16 v = f2h(y);
-          if (res) v = v + hfrom(res[win * r_ws + ((long long)oy * W + ox) * ldr + co]);
+          if (res) {
+            const long long rrow = rpad ? (long long)(oy + rpad) * (W + 2 * rpad) + ox + rpad : (long long)oy * W + ox;
+            v = v + hfrom(res[win * r_ws + rrow * ldr + co]);
+          }
           const long long orow = opad ? (long long)(oy + opad) * (W + 2 * opad) + ox + opad : (long long)oy * W + ox;
           out[win * o_ws + orow * ldo + co] = hbits(v);
         }
@@ -198,11 +201,13 @@ void bnh_wino16_free(bnh_wino16 *P) {
 }
 
 int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const bnh_wino16 *P, int act, uint16_t *out,
-                 long long o_ws, int ldo, int opad, const uint16_t *res, long long r_ws, int ldr, int B, void *stream) {
+                 long long o_ws, int ldo, int opad, const uint16_t *res, long long r_ws, int ldr, int rpad, int B,
+                 void *stream) {
   BNH_REQ(x && P && out && H > 0 && W > 0 && H % 2 == 0 && W % 2 == 0 && B > 0);
   BNH_REQ(ldx >= P->C && ldx % 4 == 0 && ldo >= P->K && (opad == 0 || opad == 1) && act >= 0 && act <= 2);
   BNH_REQ(((uintptr_t)x & 7) == 0 && (B == 1 || x_ws % 4 == 0));
-  BNH_REQ(!res || ldr >= P->K);
+  BNH_REQ(!res || (ldr >= P->K && (rpad == 0 || rpad == 1)));
+  BNH_REQ(!res || B == 1 || r_ws >= (long long)(H + 2 * rpad) * (W + 2 * rpad) * ldr);
   BNH_REQ(B == 1 || (x_ws >= (long long)(H + 2) * (W + 2) * ldx && o_ws >= (long long)(H + 2 * opad) * (W + 2 * opad) * ldo));
   hipStream_t st = bnh_stream(stream);
   if (opad) {
@@ -216,7 +221,7 @@ int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const
   const int nco = P->Kp / 16, nch = P->Cp / 32;
 #define WINO_LAUNCH(NCO, NCH)                                                                                          \
   hipLaunchKernelGGL((k_wino_f16<NCO, NCH>), grid, dim3(64 * NCO), 0, st, x, x_ws, H, W, P->C, ldx, P->U, P->b, P->K, \
-                     act, out, o_ws, ldo, opad, res, r_ws, ldr, strips)
+                     act, out, o_ws, ldo, opad, res, r_ws, ldr, rpad, strips)
   if (nch == 1) {
     if (nco == 1) WINO_LAUNCH(1, 1); else if (nco == 2) WINO_LAUNCH(2, 1); else if (nco == 3) WINO_LAUNCH(3, 1);
     else WINO_LAUNCH(4, 1);

@@ -145,7 +145,8 @@ int bnh_gemm_f16(const uint16_t *A, long long a_ws, int lda, int M, int B, const
  * stride 1, pad 1 convolution of C <= 64 input channels (C % 4 == 0) into K <= 64 output channels. Weights OHWI fp32
  * [K][3][3][C] and bias [K] are transformed once (U = G g G^T in fp32, rounded to fp16, as wino_s0_pack). Per window:
  * x fp16 zero-haloed [H+2][W+2][ldx] (H, W even); out fp16 [H][W][ldo] (opad 0) or zero-haloed [H+2][W+2][ldo]
- * (opad 1); optional fp16 residual [H][W][ldr] added last. V = B^T d B in fp16 (wino_s0.c's order), the 16
+ * (opad 1); optional fp16 residual added last, [H][W][ldr] (rpad 0) or zero-haloed [H+2][W+2][ldr] (rpad 1: the
+ * CONV3C24 form, src/rt_ops_dot.c:63-107, whose residual is its own haloed input). V = B^T d B in fp16 (wino_s0.c's order), the 16
  * position GEMMs on fp16 MFMA with fp32 accumulation, y = A^T M A + b and the activation (0 none, 1 the fp32 SiLU,
  * 2 ReLU) in fp32, one rounding to fp16. Within the fp16 Winograd error bound of a direct convolution (the
  * parity tests state it), not bit-identical to the reference's fp16 chains. */
@@ -153,7 +154,8 @@ typedef struct bnh_wino16 bnh_wino16;
 bnh_wino16 *bnh_wino16_new(int C, int K, const float *w, const float *bias);
 void bnh_wino16_free(bnh_wino16 *P);
 int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const bnh_wino16 *P, int act, uint16_t *out,
-                 long long o_ws, int ldo, int opad, const uint16_t *res, long long r_ws, int ldr, int B, void *stream);
+                 long long o_ws, int ldo, int opad, const uint16_t *res, long long r_ws, int ldr, int rpad, int B,
+                 void *stream);
 
 /* ------------------------------------------------------------------ int8 Winograd F(2x2, 3x3) (WINO_S8)
  * libbnneon's int8 Winograd for 3 x 3 stride-1 pad-1 convolutions (wino_pack / wino_f23_tiles, src/wino.c:26-227;

@@ -81,7 +81,7 @@ uint16_t orc_h_max(uint16_t a, uint16_t b) {
   if (x == 0 && y == 0) return (uint16_t)(a & b & 0x8000);
   return x > y ? a : b;
 }
-static uint16_t h_min(uint16_t a, uint16_t b) {
+uint16_t orc_h_min(uint16_t a, uint16_t b) {
   if (h_isnan(a) || h_isnan(b)) return 0x7e00;
   float x = orc_h2f(a), y = orc_h2f(b);
   if (x == 0 && y == 0) return (uint16_t)((a | b) & 0x8000);
@@ -107,7 +107,7 @@ static uint16_t lut_coef(const uint16_t *c, unsigned n) {
 uint16_t orc_silu_lut_h(uint16_t x) {
   const uint16_t magic = 0x6600, umax = 0x4bb3; /* 1536.0, (fp16)15.4f = 15.3984375 */
   uint16_t u = (uint16_t)(x & 0x7fff);
-  uint16_t uc = h_min(u, umax);
+  uint16_t uc = orc_h_min(u, umax);
   uint16_t tm = orc_h_add(uc, magic);
   uint16_t f = orc_h_add(uc, (uint16_t)(orc_h_add(tm, 0xe600 /* -1536 */) ^ 0x8000));
   unsigned n = tm & 0xff;

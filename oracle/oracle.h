@@ -120,6 +120,17 @@ void orc_wino8_pack(const float *w, int K, int C, int8_t *U8, float *sw, float *
 void orc_wino8(const float *x, int H, int W, int C, int K, const int8_t *U8, const float *sw, const float *zw,
                const float *bias, uint16_t *out);
 
+/* ---------------------------------------------------------------- fp16 Winograd, 24 channels (CONV3C24) */
+int orc_recip_estimate(int a);                    /* Arm ARM RecipEstimate on the 9-bit scaled operand */
+uint16_t orc_h_min(uint16_t a, uint16_t b);       /* FMIN on fp16 */
+uint16_t orc_frecpe_h(uint16_t x);                /* FRECPE, half precision */
+uint16_t orc_frecps_h(uint16_t a, uint16_t b);    /* FRECPS, half precision */
+uint16_t orc_silu_poly_h(uint16_t x);             /* silu4w, src/wino_s0.c:14-34 */
+/* src/wino_s0.c:40-64: w OHWI fp32 [24][3][3][24] -> U fp16 [16][24 ci][24 co], b16 [24] */
+void orc_wino_s0_pack(const float *w, const float *bias, uint16_t *U, uint16_t *b16);
+/* src/wino_s0.c:145-165 over all tile rows: x, out padded fp16 [H+2][W+2][24]; out = SiLU(conv + b) + x */
+void orc_wino_s0(const uint16_t *x, int H, int W, const uint16_t *U, const uint16_t *b16, uint16_t *out);
+
 /* ---------------------------------------------------------------- Q31 requantised int8 GEMM (own specification)
  * The reference has no such kernel. Specification (TFLite / gemmlowp fixed-point conventions):
  *   acc[n][m]  = sum_k w[n][k] * (x[k][m] - zx) + bias[n]                       (exact, int32)

@@ -332,3 +332,26 @@ def wino8(x, pk, bias):
     lib().orc_wino8(x.ctypes.data, H, W, C, K, U8.ctypes.data, sw.ctypes.data, zw.ctypes.data, b.ctypes.data,
                     out.ctypes.data)
     return out
+
+
+_SIGS.update({
+    "orc_frecpe_h": (u16, [u16]),
+    "orc_frecps_h": (u16, [u16, u16]),
+    "orc_silu_poly_h": (u16, [u16]),
+    "orc_wino_s0_pack": (None, [vp, vp, vp, vp]),
+    "orc_wino_s0": (None, [vp, i32, i32, vp, vp, vp]),
+})
+
+
+def wino_s0(xp, w, b):
+    """CONV3C24 of one window: xp fp16 [H+2][W+2][24] (zero halo) -> out fp16 [H+2][W+2][24] (zero halo)."""
+    xp = _c(xp, np.float16)
+    U = np.zeros(16 * 24 * 24, np.uint16)
+    b16 = np.zeros(24, np.uint16)
+    w = _c(w, np.float32)
+    b = _c(b, np.float32)
+    lib().orc_wino_s0_pack(w.ctypes.data, b.ctypes.data, U.ctypes.data, b16.ctypes.data)
+    out = np.zeros_like(xp)
+    lib().orc_wino_s0(xp.ctypes.data, xp.shape[0] - 2, xp.shape[1] - 2, U.ctypes.data, b16.ctypes.data,
+                      out.ctypes.data)
+    return out

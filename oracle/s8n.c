@@ -12,7 +12,7 @@ static inline float bitsf(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
 
 /* RecipEstimate of the Arm ARM (single-precision table lookup replaced by the integer formula it is defined by):
  * a in [256, 512) is 1.fraction<51:44> scaled by 2^8; returns r in [256, 512) representing r / 256. */
-static int recip_estimate(int a) {
+int orc_recip_estimate(int a) {
   a = a * 2 + 1;
   int b = (1 << 19) / a;
   return (b + 1) / 2;
@@ -33,7 +33,7 @@ float orc_frecpe(float x) {
   }
   int scaled = 256 | (int)((fraction >> 44) & 0xffu);
   int result_exp = 253 - e;
-  int est = recip_estimate(scaled);
+  int est = orc_recip_estimate(scaled);
   fraction = (uint64_t)(est & 0xff) << 44;
   if (result_exp == 0) fraction = (1ull << 51) | (fraction >> 1);
   else if (result_exp == -1) { fraction = (1ull << 50) | (fraction >> 2); result_exp = 0; }

@@ -46,7 +46,7 @@ def bound(xp, w):
     return E
 
 
-def run(hip, xp, w, b, act=0, opad=0, res=None):
+def run(hip, xp, w, b, act=0, opad=0, res=None, rpad=0):
     H_ = hip
     B, Hp, Wp, C = xp.shape
     H, W = Hp - 2, Wp - 2
@@ -65,10 +65,10 @@ def run(hip, xp, w, b, act=0, opad=0, res=None):
         do = H_.DeviceArray.from_host(np.full((B, o_ws), np.float16(3.0)))
         dr, r_ws, ldr = None, 0, 0
         if res is not None:
-            dr = H_.DeviceArray.from_host(res.reshape(B, -1))
-            r_ws, ldr = H * W * K, K
+            dr = H_.DeviceArray.from_host(np.ascontiguousarray(res).reshape(B, -1))
+            r_ws, ldr = (H + 2 * rpad) * (W + 2 * rpad) * K, K
         H_.check(H_.lib().bnh_wino_f16(dx.ptr, x_ws, H, W, C, P, act, do.ptr, o_ws, K, opad,
-                                       dr.ptr if dr else None, r_ws, ldr, B, None), "wino_f16")
+                                       dr.ptr if dr else None, r_ws, ldr, rpad, B, None), "wino_f16")
         H_.sync()
         return do.numpy()[:, :rows * K].reshape(B, H + 2 * opad, W + 2 * opad, K)
     finally:
@@ -135,6 +135,38 @@ def test_config2_full_size(hip):
         assert (err[40:48] <= tol).all()
         # everywhere: relative to the output scale
         assert err.max() <= 8 * u * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("H,W", [(8, 12), (24, 64)])
+def test_conv3c24_against_oracle(hip, H, W):
+    """The CONV3C24 form (24 -> 24 channels, SiLU, residual = the op's own zero-haloed input, zero-haloed output)
+    against the oracle's restatement of src/wino_s0.c. Both sides are held to float64 truth
+    t = SiLU(direct conv + b) + x:
+      GPU:    |gpu - t| <= 1.1 (4 u E + u |y|) + 2 u |t| + 2^-20 |y| + 2^-24
+      oracle: |orc - t| <= 1.1 (40 u E) + 2e-3 max(1, |SiLU(y)|) + 2 u |t|
+    (fp16 chain over 24 input channels, fp16 output transform and bias, the fp16 polynomial SiLU's accuracy),
+    and |gpu - orc| within the sum of the two."""
+    import pyoracle as O
+    rng = np.random.default_rng(H + W)
+    B, C = 2, 24
+    xp, w, b = make(rng, B, H, W, C, C)
+    say("wino conv3c24", H, W)
+    g = run(hip, xp, w, b, act=1, opad=1, res=xp, rpad=1).astype(np.float64)
+    u = 2.0 ** -11
+    for i in range(B):
+        assert not g[i, 0].any() and not g[i, -1].any() and not g[i, :, 0].any() and not g[i, :, -1].any()
+        o = O.wino_s0(xp[i], w, b).astype(np.float64)
+        assert np.array_equal(o[0], g[i, 0]) and np.array_equal(o[:, 0], g[i, :, 0])
+        y = direct(xp[i].astype(np.float64), w, b).reshape(H, W, C)
+        sy = silu(y)
+        t = sy + xp[i, 1:-1, 1:-1].astype(np.float64)
+        E = bound(xp[i], w)
+        tg = 1.1 * (4 * u * E + u * np.abs(y)) + 2 * u * np.abs(t) + 2.0 ** -20 * np.abs(y) + 2.0 ** -24
+        to = 1.1 * 40 * u * E + 2e-3 * np.maximum(1.0, np.abs(sy)) + 2 * u * np.abs(t)
+        gi, oi = g[i, 1:-1, 1:-1], o[1:-1, 1:-1]
+        assert (np.abs(gi - t) <= tg).all(), float(np.max(np.abs(gi - t) / tg))
+        assert (np.abs(oi - t) <= to).all(), float(np.max(np.abs(oi - t) / to))
+        assert (np.abs(gi - oi) <= tg + to).all()
 
 
 def test_bad_shapes_refused(hip):
