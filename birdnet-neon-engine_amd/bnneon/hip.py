@@ -91,6 +91,16 @@ _SIGS = {
     "bnh_dw_s8": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp,
                         vp, i32, i32, i32, i32, vp, vp, i64, i32, i32, i32,
                         vp]),
+    "bnh_logmel_new": (vp, [i32, i32, i32, i32, i32, i32, vp, vp, C.c_float, C.c_float]),
+    "bnh_logmel_free": (None, [vp]),
+    "bnh_logmel_frames": (i32, [vp]),
+    "bnh_logmel_run": (i32, [vp, vp, i64, vp, i64, i32, vp]),
+    "bnh_stem_f32": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp, i64, i32, i32, i32, vp]),
+    "bnh_se_f32": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, i64, i32, vp]),
+    "bnh_mean_f32": (i32, [vp, i64, i32, i32, i32, vp, i64, i32, vp]),
+    "bnh_pad": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, i64, i32, vp]),
+    "bnh_zero_halo": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp]),
+    "bnh_eval_expf": (i32, [vp, vp, i64, vp]),
 }
 
 

@@ -149,6 +149,83 @@ class Net:
         self.last = ob
         return ob, cb
 
+    # ---------------------------------------------------------------- fp32 ops
+    def logmel(self, ib, nsamp, frame, hop, pad, nfft, window, mel, floor_, scale):
+        """FE_LOGMEL on the pcm buffer ib (l_fe_logmel, python/bnneon/compiler/lower.py:390-413): spec
+        [nfr][nmel] as an (nfr, nmel, 1) buffer."""
+        mel = np.asarray(mel, np.float32)
+        nmel = mel.shape[0]
+        assert mel.shape[1] == nfft // 2 + 1
+        nfr = (nsamp + 2 * pad - frame) // hop + 1
+        tl = [self.tensor("fe/window", np.asarray(window, np.float32)), self.tensor("fe/mel", mel),
+              self.tensor("fe/consts", np.array([floor_, scale], np.float32))]
+        ob = self.buf(F32, nfr, nmel, 1)
+        self.emit(OP["FE_LOGMEL"], [ib, ob], tl, [nsamp, frame, hop, pad, nfft, nmel])
+        self.last = ob
+        return ob
+
+    def stem(self, ib, w, b, k, s, act="silu", opad=0, ldo=None):
+        """k x k VALID conv of stride s on the 1-channel image ib (stem, lower.py:760-785): fp32 panels
+        [Np/8][Kp][8], Kp = k*k rounded up to 4; output [Ho][Wo][ldo] with halo opad."""
+        d = self.bufs[ib]
+        H, W = d[1], d[2]
+        w = np.asarray(w, np.float32).reshape(len(b), k * k)
+        co = w.shape[0]
+        Ho, Wo = (H - k) // s + 1, (W - k) // s + 1
+        Kp, Np = (k * k + 3) // 4 * 4, (co + 7) // 8 * 8
+        wp = np.zeros((Np, Kp), np.float32)
+        wp[:co, :k * k] = w
+        panels = np.ascontiguousarray(wp.reshape(Np // 8, 8, Kp).transpose(0, 2, 1))
+        bb = np.zeros(Np + 8, np.float32)
+        bb[:co] = b
+        tl = [self.tensor("f32/stem.w", panels), self.tensor("f32/stem.b", bb)]
+        ldo = Np if ldo is None else ldo
+        ob = self.buf(F32, Ho, Wo, co, ld=ldo, halo=opad)
+        col = self.buf(F32, (Ho * Wo + 7) // 8 * 8, 1, Kp)
+        self.emit(OP["STEM"], [ib, ob, col], tl, [co, k * k, Kp, Np, H, W, Ho, Wo, k, s, ACT[act], ldo, opad])
+        self.last = ob
+        return ob
+
+    def se_gate(self, cs, P, w1, b1, w2, b2):
+        """SE_GATE from the channel sums cs of P pixels (l_se, lower.py:981-1015): w1 [rd][C], w2 [C][rd];
+        returns the gate buffer (f32 [C]) a 1x1 conv applies to its input."""
+        w1 = np.asarray(w1, np.float32)
+        rd, C = w1.shape
+        tl = [self.tensor("se.w1", w1), self.tensor("se.b1", np.asarray(b1, np.float32)),
+              self.tensor("se.w2t", np.ascontiguousarray(np.asarray(w2, np.float32).T)),
+              self.tensor("se.b2", np.asarray(b2, np.float32))]
+        gb = self.buf(F32, 1, 1, C, elems=C)
+        self.emit(OP["SE_GATE"], [cs, gb], tl, [C, rd, P])
+        return gb
+
+    def se(self, ib, cs, w1, b1, w2, b2):
+        """SE in place on the activation ib [P][C] (its channel sums cs)."""
+        w1 = np.asarray(w1, np.float32)
+        rd, C = w1.shape
+        d = self.bufs[ib]
+        tl = [self.tensor("se.w1", w1), self.tensor("se.b1", np.asarray(b1, np.float32)),
+              self.tensor("se.w2t", np.ascontiguousarray(np.asarray(w2, np.float32).T)),
+              self.tensor("se.b2", np.asarray(b2, np.float32))]
+        self.emit(OP["SE"], [ib, cs], tl, [C, rd, d[1] * d[2]])
+        return ib
+
+    def mean(self, ib):
+        """MEAN of rows ib [P][ld] -> f32 [C] (l_mean, lower.py:415-427)."""
+        d = self.bufs[ib]
+        assert not d[5]
+        ob = self.buf(F32, 1, 1, d[3])
+        self.emit(OP["MEAN"], [ib, ob], [], [d[1] * d[2], d[3], d[4]])
+        self.last = ob
+        return ob
+
+    def pad(self, ib, h):
+        """PAD of rows ib into a zero-haloed buffer with ld = C (dw_input, lower.py:967-974)."""
+        d = self.bufs[ib]
+        pb = self.buf(d[0], d[1], d[2], d[3], ld=d[3], halo=h)
+        self.emit(OP["PAD"], [ib, pb], [], [d[1], d[2], d[3], d[4], h], var=1 if d[0] == F16 else 0)
+        self.last = pb
+        return pb
+
     def add_to(self, name="neon-int8", hwcap=0, in_buf=0, out_buf=None, emb_buf=None):
         self.pkg.add_path(name, hwcap, self.bufs, self.ops, in_buf,
                           self.last if out_buf is None else out_buf, emb_buf)

@@ -25,6 +25,8 @@ SOURCES = [
     "kern_dw.hip",
     "kern_wino.hip",
     "kern_f16.hip",
+    "kern_fe.hip",
+    "kern_f32.hip",
     "rt_pkg.cpp",
     "ops_table.cpp",
     "ops_s8n.cpp",

@@ -1,0 +1,239 @@
+// fp32 registry ops around the int8 GEMMs of the int8 Perch-family plan, bit-identical to libbnneon's fp32 kernels:
+//   STEM     im2col of a 1-channel image (VALID k x k, stride s) into the fp32 GEMM (src/rt_ops_f32.c:409-425,
+//            pc_im2col1 src/pc_kern_f32.c:150-161, gemm_f32 src/gemm_f32.c:141-197): per output one FMA chain over
+//            the Kp taps from +0, + bias, SiLU / ReLU, padded store;
+//   SE_GATE  the squeeze-excitation gate from the depthwise conv's channel sums (src/rt_ops_f32.c:317-324 with
+//   / SE     v24k32_se_fc1 src/v24_f32.c:164-179 and se_gate_range src/rt_ops_f32.c:269-283), SE also gating the
+//            activation in place (v24k32_se, src/v24_f32.c:181-210);
+//   MEAN     spatial mean (pc_mean_f32, src/pc_kern_f32.c:342-348);
+//   PAD      copy into a zero-haloed buffer (src/rt_ops_f32.c:503-508), fp32 or fp16;
+// and the halo zeroing every padded output needs (rt_zero_halo, src/rt_pkg.c:194-203).
+#include <string.h>
+
+#include "bnh_internal.h"
+#include "bnh_num.h"
+#include "bnh_expf.h"
+
+// ------------------------------------------------------------------ halo zeroing, any element size (4 or 2 bytes)
+template <typename T>
+__global__ void k_zero_halo(T *__restrict__ out, long long ws, int H, int W, int C, int h, long long total) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int Wp = W + 2 * h;
+  const long long per = (long long)(H + 2 * h) * Wp * C;
+  const int w = (int)(i / per);
+  const long long e = i % per, px = e / C;
+  const int y = (int)(px / Wp), x = (int)(px % Wp);
+  if (y >= h && y < H + h && x >= h && x < W + h) return;
+  out[w * ws + e] = (T)0;
+}
+
+// ------------------------------------------------------------------ STEM
+// thread per (window, output pixel, 4 channels); w panels [Np/8][Kp][8]
+__global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img, long long i_ws, int W, int k, int s,
+                                                  int Ho, int Wo, const float *__restrict__ w,
+                                                  const float *__restrict__ bias, int Kp, int Np, int act,
+                                                  float *__restrict__ out, long long o_ws, int ldo, int opad) {
+  const int ng = Np / 4;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x, per = (long long)Ho * Wo * ng;
+  const int win = blockIdx.y;
+  if (i >= per) return;
+  const int g = (int)(i % ng), m = (int)(i / ng), oy = m / Wo, ox = m % Wo, n0 = 4 * g;
+  const float *x = img + win * i_ws + (long long)(oy * s) * W + ox * s;
+  const float *wp = w + (long long)(n0 / 8) * Kp * 8 + n0 % 8;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < Kp; q++) {
+    const float a = q < k * k ? x[(q / k) * W + q % k] : 0.f;
+    const float4 wv = *(const float4 *)(wp + (long long)q * 8);
+    acc[0] = __builtin_fmaf(wv.x, a, acc[0]);
+    acc[1] = __builtin_fmaf(wv.y, a, acc[1]);
+    acc[2] = __builtin_fmaf(wv.z, a, acc[2]);
+    acc[3] = __builtin_fmaf(wv.w, a, acc[3]);
+  }
+  float y[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    y[j] = acc[j] + bias[n0 + j];
+    if (act == 1) y[j] = bnh_silu_f32(y[j]);
+    else if (act == 2) y[j] = bnh_relu_f32(y[j]);
+  }
+  const long long orow = opad ? (long long)(oy + opad) * (Wo + 2 * opad) + ox + opad : m;
+  float *o = out + win * o_ws + orow * ldo + n0;
+  o[0] = y[0]; o[1] = y[1]; o[2] = y[2]; o[3] = y[3];
+}
+
+// ------------------------------------------------------------------ SE_GATE / SE: one block per window
+__global__ __launch_bounds__(256) void k_se_f32(const float *__restrict__ chsum, long long c_ws, int C, int rd, int P,
+                                                const float *__restrict__ w1, const float *__restrict__ b1,
+                                                const float *__restrict__ w2t, const float *__restrict__ b2,
+                                                float *__restrict__ gate, long long g_ws, float *__restrict__ D,
+                                                long long d_ws) {
+  extern __shared__ float sm[];
+  float *mean = sm, *part = sm + C, *s1 = part + 8 * rd, *g = s1 + rd;  // [C] [rd][8] [rd] [C]
+  const int win = blockIdx.x, tid = threadIdx.x;
+  const float *cs = chsum + win * c_ws;
+  const float inv = 1.f / (float)P;
+  for (int c = tid; c < C; c += 256) mean[c] = cs[c] * inv;
+  __syncthreads();
+  // fc1: the eight lane chains of the two 4-lane accumulators (lane l < 4: a0, channels 8 i + l and the 4-wide
+  // tail; l >= 4: a1, channels 8 i + l)
+  const int C8 = C / 8 * 8;
+  for (int it = tid; it < 8 * rd; it += 256) {
+    const int r = it / 8, l = it % 8;
+    const float *w = w1 + (long long)r * C;
+    float a = 0.f;
+    for (int c = l; c < C8; c += 8) a = __builtin_fmaf(w[c], mean[c], a);
+    if (l < 4 && C8 + l < C) a = __builtin_fmaf(w[C8 + l], mean[C8 + l], a);
+    part[r * 8 + l] = a;
+  }
+  __syncthreads();
+  for (int r = tid; r < rd; r += 256) {
+    const float *p = part + r * 8;
+    const float v = ((p[0] + p[4]) + (p[1] + p[5])) + ((p[2] + p[6]) + (p[3] + p[7]));
+    const float x = v + b1[r];
+    s1[r] = x / (1.f + bnh_expf(-x));  // silu_s: the C library's expf
+  }
+  __syncthreads();
+  for (int c = tid; c < C; c += 256) {
+    float a = b2[c];
+    for (int r = 0; r < rd; r++) a = __builtin_fmaf(w2t[(long long)r * C + c], s1[r], a);
+    // sigmoid_f32x4: 1 / (1 + exp2_f32x4(-a log2 e)) by FRECPE and two Newton steps
+    float t = a * -1.44269504f;
+    t = bnh_fmin(bnh_fmax(t, -126.f), 126.f);
+    const float n = __builtin_rintf(t), f = t - n;
+    float q = 1.5403530e-4f;
+    q = __builtin_fmaf(q, f, 1.3333558e-3f);
+    q = __builtin_fmaf(q, f, 9.6181291e-3f);
+    q = __builtin_fmaf(q, f, 5.5504109e-2f);
+    q = __builtin_fmaf(q, f, 2.4022651e-1f);
+    q = __builtin_fmaf(q, f, 6.9314718e-1f);
+    q = __builtin_fmaf(q, f, 1.f);
+    const float e = bnh_float(bnh_bits(q) + ((uint32_t)bnh_cvtz_s32(n) << 23));
+    const float d = 1.f + e;
+    float rr = bnh_frecpe(d);
+    rr = rr * bnh_frecps(d, rr);
+    rr = rr * bnh_frecps(d, rr);
+    g[c] = rr;
+    if (gate) gate[win * g_ws + c] = rr;
+  }
+  if (!D) return;
+  __syncthreads();
+  float *d = D + win * d_ws;
+  for (long long i = tid; i < (long long)P * C; i += 256) d[i] = d[i] * g[i % C];
+}
+
+// ------------------------------------------------------------------ MEAN
+__global__ void k_mean_f32(const float *__restrict__ x, long long x_ws, int P, int C, int ld, float *__restrict__ out,
+                           long long o_ws) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x, win = blockIdx.y;
+  if (c >= C) return;
+  const float *xw = x + win * x_ws + c;
+  float s = 0.f;
+  for (int p = 0; p < P; p++) s = s + xw[(long long)p * ld];
+  out[win * o_ws + c] = s / (float)P;
+}
+
+// the device expf on its own (for its parity test against the C library)
+__global__ void k_eval_expf(const float *__restrict__ x, float *__restrict__ y, long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = bnh_expf(x[i]);
+}
+
+// ------------------------------------------------------------------ PAD: every element of the padded buffer
+template <typename T>
+__global__ void k_pad(const T *__restrict__ x, long long x_ws, int H, int W, int C, int ld, int h, T *__restrict__ xp,
+                      long long p_ws, long long total) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int Wp = W + 2 * h;
+  const long long per = (long long)(H + 2 * h) * Wp * C;
+  const int win = (int)(i / per);
+  const long long e = i % per, px = e / C;
+  const int c = (int)(e % C), y = (int)(px / Wp) - h, xx = (int)(px % Wp) - h;
+  T v = (T)0;
+  if (y >= 0 && y < H && xx >= 0 && xx < W) v = x[win * x_ws + ((long long)y * W + xx) * ld + c];
+  xp[win * p_ws + e] = v;
+}
+
+extern "C" {
+
+int bnh_zero_halo(void *xp, long long ws, int H, int W, int C, int h, int esz, int B, void *stream) {
+  BNH_REQ(xp && H > 0 && W > 0 && C > 0 && h >= 0 && B > 0 && (esz == 4 || esz == 2));
+  const long long per = (long long)(H + 2 * h) * (W + 2 * h) * C, total = per * B;
+  BNH_REQ(B == 1 || ws >= per);
+  if (!h) return 0;
+  const dim3 grid((unsigned)bnh_ceil_div(total, 256));
+  if (esz == 4)
+    hipLaunchKernelGGL(k_zero_halo<uint32_t>, grid, dim3(256), 0, bnh_stream(stream), (uint32_t *)xp, ws, H, W, C, h,
+                       total);
+  else
+    hipLaunchKernelGGL(k_zero_halo<uint16_t>, grid, dim3(256), 0, bnh_stream(stream), (uint16_t *)xp, ws, H, W, C, h,
+                       total);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_stem_f32(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
+                 const float *bias, int Kp, int Np, int act, float *out, long long o_ws, int ldo, int opad, int B,
+                 void *stream) {
+  BNH_REQ(img && w && bias && out && B > 0 && k >= 1 && s >= 1 && Ho > 0 && Wo > 0);
+  BNH_REQ((Ho - 1) * s + k <= H && (Wo - 1) * s + k <= W && Kp >= k * k && Kp % 4 == 0 && Np % 8 == 0);
+  BNH_REQ(ldo >= Np && opad >= 0 && opad <= 3 && act >= 0 && act <= 2 && ldo % 4 == 0);
+  BNH_REQ(((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 3) == 0);
+  BNH_REQ(B == 1 || (i_ws >= (long long)H * W && o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo));
+  if (opad && bnh_zero_halo(out, o_ws, Ho, Wo, ldo, opad, 4, B, stream)) return -1;
+  const long long per = (long long)Ho * Wo * (Np / 4);
+  hipLaunchKernelGGL(k_stem_f32, dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), dim3(256), 0, bnh_stream(stream),
+                     img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, act, out, o_ws, ldo, opad);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_se_f32(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
+               const float *w2t, const float *b2, float *gate, long long g_ws, float *D, long long d_ws, int B,
+               void *stream) {
+  BNH_REQ(chsum && w1 && b1 && w2t && b2 && (gate || D) && B > 0);
+  BNH_REQ(C > 0 && C % 4 == 0 && C <= 4096 && rd > 0 && rd <= 512 && P > 0);
+  BNH_REQ(B == 1 || (c_ws >= C && (!gate || g_ws >= C) && (!D || d_ws >= (long long)P * C)));
+  const size_t lds = sizeof(float) * (2 * (size_t)C + 9 * (size_t)rd);
+  hipLaunchKernelGGL(k_se_f32, dim3((unsigned)B), dim3(256), lds, bnh_stream(stream), chsum, c_ws, C, rd, P, w1, b1,
+                     w2t, b2, gate, g_ws, D, d_ws);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
+                 void *stream) {
+  BNH_REQ(x && out && P > 0 && C > 0 && ld >= C && B > 0);
+  BNH_REQ(B == 1 || (x_ws >= (long long)P * ld && o_ws >= C));
+  hipLaunchKernelGGL(k_mean_f32, dim3((unsigned)bnh_ceil_div(C, 64), (unsigned)B), dim3(64), 0, bnh_stream(stream), x,
+                     x_ws, P, C, ld, out, o_ws);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_pad(const void *x, long long x_ws, int H, int W, int C, int ld, int h, int esz, void *xp, long long p_ws, int B,
+            void *stream) {
+  BNH_REQ(x && xp && H > 0 && W > 0 && C > 0 && ld >= C && h >= 0 && h <= 3 && B > 0 && (esz == 4 || esz == 2));
+  const long long per = (long long)(H + 2 * h) * (W + 2 * h) * C, total = per * B;
+  BNH_REQ(B == 1 || (x_ws >= (long long)H * W * ld && p_ws >= per));
+  const dim3 grid((unsigned)bnh_ceil_div(total, 256));
+  if (esz == 4)
+    hipLaunchKernelGGL(k_pad<uint32_t>, grid, dim3(256), 0, bnh_stream(stream), (const uint32_t *)x, x_ws, H, W, C, ld,
+                       h, (uint32_t *)xp, p_ws, total);
+  else
+    hipLaunchKernelGGL(k_pad<uint16_t>, grid, dim3(256), 0, bnh_stream(stream), (const uint16_t *)x, x_ws, H, W, C, ld,
+                       h, (uint16_t *)xp, p_ws, total);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_eval_expf(const float *x, float *y, long long n, void *stream) {
+  BNH_REQ(x && y && n >= 0);
+  if (!n) return 0;
+  hipLaunchKernelGGL(k_eval_expf, dim3((unsigned)bnh_ceil_div(n, 256)), dim3(256), 0, bnh_stream(stream), x, y, n);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // extern "C"

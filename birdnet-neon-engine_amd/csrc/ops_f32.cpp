@@ -90,6 +90,158 @@ static int dw3_run(rt_ctx *c, rt_op *op) {
                      rt_ws(c, op, 1), p[4], p[5], (float *)rt_b(c, op, 2), rt_ws(c, op, 2), c->nwin, c->stream);
 }
 
+// -------- FE_LOGMEL: b = [pcm, spec f32 [nfr][nmel]]; t = [window [frame], mel [nmel][nfft/2+1], consts {floor,
+//          scale}]; p = [nsamp frame hop pad nfft nmel]   (src/rt_ops_f32.c:362-385)
+static void logmel_fini(rt_op *op) { bnh_logmel_free((bnh_logmel *)op->state); }
+static int logmel_init(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, 2, 3, 6)) return RT_E_PARAM;
+  const int *p = op->p;
+  RT_REQ(c, op, p[0] > 0 && p[1] > 0 && p[2] > 0 && p[3] >= 0 && p[4] >= p[1] && p[5] > 0);
+  if (rt_need_t(c, op, 0, (size_t)p[1] * 4, 0) || rt_need_t(c, op, 1, (size_t)p[5] * (p[4] / 2 + 1) * 4, 0) ||
+      rt_need_t(c, op, 2, 8, 0))
+    return RT_E_PARAM;
+  if (rt_need(c, op, 0, RT_F32, (size_t)p[0]) || rt_need(c, op, 1, RT_F32, 1)) return RT_E_PARAM;
+  RT_REQ(c, op, (p[4] & (p[4] - 1)) == 0 && p[4] >= 16 && p[4] <= 2048);  // nfft
+  RT_REQ(c, op, p[1] <= p[4] && p[5] <= 512);                             // frame, nmel
+  const float *k = (const float *)rt_t(c, op, 2, nullptr);
+  bnh_logmel *F = bnh_logmel_new(p[0], p[1], p[2], p[3], p[4], p[5], (const float *)rt_t(c, op, 0, nullptr),
+                                 (const float *)rt_t(c, op, 1, nullptr), k[0], k[1]);
+  op->state = F;
+  if (!F) return rt_oom(c, op, (size_t)p[4] * 16);
+  return rt_need(c, op, 1, RT_F32, (size_t)bnh_logmel_frames(F) * p[5]);
+}
+static int logmel_run(rt_ctx *c, rt_op *op) {
+  return bnh_logmel_run((const bnh_logmel *)op->state, (const float *)rt_b(c, op, 0), rt_ws(c, op, 0),
+                        (float *)rt_b(c, op, 1), rt_ws(c, op, 1), c->nwin, c->stream);
+}
+
+// -------- STEM: b = [img f32 [H][W], out, col]; t = [w panels [Np/8][Kp][8], b]; p = [N K Kp Np, H W Ho Wo k s act
+//          ldo opad]   (rt_stem_f32_check, src/rt_ops_f32.c:390-415). The im2col buffer (b[2]) is not used: the
+//          kernel reads the taps from the image directly.
+static int stem_init(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, 3, 2, 13)) return RT_E_PARAM;
+  const int *p = op->p;
+  const int N = p[0], K = p[1], Kp = p[2], Np = p[3];
+  if (N <= 0 || K <= 0 || Np != ((N + 7) & ~7) || Kp < K || Kp % 4)
+    return rt_bad(c, op, "GEMM shape N %d K %d Kp %d Np %d: expected Np = N rounded up to 8, Kp >= K, Kp %% 4 == 0", N,
+                  K, Kp, Np);
+  if (rt_need_t(c, op, 0, (size_t)Np * Kp * 4, 1) || rt_need_t(c, op, 1, (size_t)Np * 4, 1)) return RT_E_PARAM;
+  const int H = p[4], W = p[5], Ho = p[6], Wo = p[7], k = p[8], s = p[9], ldo = p[11], h = p[12];
+  RT_REQ(c, op, k >= 1 && s >= 1 && Ho > 0 && Wo > 0);
+  RT_REQ(c, op, (Ho - 1) * s + k <= H && (Wo - 1) * s + k <= W);  // VALID conv
+  RT_REQ(c, op, K == k * k);
+  RT_REQ(c, op, ldo >= Np);  // the GEMM stores whole 8-channel panels
+  RT_REQ(c, op, h >= 0 && h <= 3);
+  RT_REQ(c, op, p[10] >= 0 && p[10] <= 2);
+  if (rt_need(c, op, 0, RT_F32, (size_t)H * W) || rt_need(c, op, 2, RT_F32, (size_t)((Ho * Wo + 7) & ~7) * Kp))
+    return RT_E_PARAM;
+  const rt_bufdesc *o = rt_bd(c, op, 1);
+  if (!o) return rt_bad(c, op, "buffer argument 1 (output) is absent");
+  if (o->halo != (uint32_t)h || o->ld != (uint32_t)ldo || (h && (o->W != (uint32_t)Wo || o->H != (uint32_t)Ho)))
+    return rt_bad(c, op, "buffer argument 1 (buffer #%d, output): expected %d x %d, halo %d, ld %d; found %u x %u, halo "
+                  "%u, ld %u", op->b[1], Ho, Wo, h, ldo, o->H, o->W, o->halo, o->ld);
+  if (rt_need(c, op, 1, (int)o->dtype, (size_t)(Ho + 2 * h) * (Wo + 2 * h) * ldo) || rt_need(c, op, 1, RT_F32, 1))
+    return RT_E_PARAM;
+  RT_REQ(c, op, ldo % 4 == 0);  // 4-channel output groups
+  return rt_dev_tensors(c, op, 2);
+}
+static int stem_run(rt_ctx *c, rt_op *op) {
+  const int *p = op->p;
+  return bnh_stem_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[4], p[5], p[8], p[9], p[6], p[7],
+                      (const float *)dev_tn(op, 0), (const float *)dev_tn(op, 1), p[2], p[3], p[10],
+                      (float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[11], p[12], c->nwin, c->stream);
+}
+
+// -------- SE / SE_GATE: SE b = [D [P][C], chsum]; SE_GATE b = [chsum, gate f32 [C]]; t = [w1 [rd][C], b1 [rd],
+//          w2t [rd][C], b2 [C]]; p = [C rd P]   (rt_se_check, src/rt_ops_f32.c:256-266)
+static int se_check(rt_ctx *c, rt_op *op, int gate) {
+  if (rt_need_args(c, op, 2, 4, 3)) return RT_E_PARAM;
+  const int C = op->p[0], rd = op->p[1], P = op->p[2];
+  RT_REQ(c, op, C > 0 && C % 8 == 0 && C <= 4096);
+  RT_REQ(c, op, rd > 0 && rd <= 512);
+  RT_REQ(c, op, P > 0);
+  const size_t want[4] = {(size_t)rd * C, (size_t)rd, (size_t)rd * C, (size_t)C};
+  for (int i = 0; i < 4; i++)
+    if (rt_need_t(c, op, i, want[i] * 4, 0)) return RT_E_PARAM;
+  if (rt_need(c, op, 0, RT_F32, gate ? (size_t)C : (size_t)P * C) || rt_need(c, op, 1, RT_F32, (size_t)C))
+    return RT_E_PARAM;
+  return rt_dev_tensors(c, op, 4);
+}
+static int se_init(rt_ctx *c, rt_op *op) { return se_check(c, op, 0); }
+static int seg_init(rt_ctx *c, rt_op *op) { return se_check(c, op, 1); }
+static int se_run(rt_ctx *c, rt_op *op) {
+  const int *p = op->p;
+  return bnh_se_f32((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_tn(op, 0),
+                    (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3), nullptr, 0,
+                    (float *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
+}
+static int seg_run(rt_ctx *c, rt_op *op) {
+  const int *p = op->p;
+  return bnh_se_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[0], p[1], p[2], (const float *)dev_tn(op, 0),
+                    (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3),
+                    (float *)rt_b(c, op, 1), rt_ws(c, op, 1), nullptr, 0, c->nwin, c->stream);
+}
+
+// -------- MEAN: b = [x [P][ld], out f32 [C]]; p = [P C ld]   (rt_mean_check, src/rt_ops_f32.c:510-522)
+int rt_mean_check(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, 2, -1, 3)) return RT_E_PARAM;
+  RT_REQ(c, op, op->p[0] > 0 && op->p[1] > 0);
+  RT_REQ(c, op, op->p[1] % 4 == 0);
+  RT_REQ(c, op, op->p[2] >= op->p[1]);
+  const rt_bufdesc *x = rt_bd(c, op, 0);
+  if (!x) return rt_bad(c, op, "buffer argument 0 (input) is absent");
+  if (x->halo)
+    return rt_bad(c, op, "buffer argument 0 (buffer #%d, input): expected no halo, found halo %u", op->b[0], x->halo);
+  if (rt_need(c, op, 0, (int)x->dtype, (size_t)op->p[0] * op->p[2]) || rt_need(c, op, 1, RT_F32, (size_t)op->p[1]))
+    return RT_E_PARAM;
+  return 0;
+}
+static int mean_init(rt_ctx *c, rt_op *op) {
+  return rt_mean_check(c, op) || rt_need(c, op, 0, RT_F32, 1) ? RT_E_PARAM : 0;
+}
+static int mean_run(rt_ctx *c, rt_op *op) {
+  return bnh_mean_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), op->p[0], op->p[1], op->p[2],
+                      (float *)rt_b(c, op, 1), rt_ws(c, op, 1), c->nwin, c->stream);
+}
+
+// -------- PAD: b = [x, xp (halo h)]; p = [H W C ld h]   (rt_pad_check, src/rt_ops_f32.c:480-501)
+int rt_pad_check(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, 2, -1, 5)) return RT_E_PARAM;
+  const int *p = op->p;
+  const rt_bufdesc *x = rt_bd(c, op, 0), *o = rt_bd(c, op, 1);
+  if (!x || !o) return rt_bad(c, op, "buffer argument %d is absent", x ? 1 : 0);
+  RT_REQ(c, op, p[0] > 0 && p[1] > 0 && p[2] > 0);
+  RT_REQ(c, op, p[4] >= 1 && p[4] <= 3);
+  RT_REQ(c, op, p[3] >= p[2]);
+  if (x->dtype != o->dtype)
+    return rt_bad(c, op, "buffer argument 0 (buffer #%d, input) is %s but buffer argument 1 (buffer #%d, output) is %s",
+                  op->b[0], rt_dtype_name(x->dtype), op->b[1], rt_dtype_name(o->dtype));
+  if (x->halo)
+    return rt_bad(c, op, "buffer argument 0 (buffer #%d, input): expected no halo, found halo %u", op->b[0], x->halo);
+  if (o->ld != (uint32_t)p[2] || o->halo != (uint32_t)p[4])
+    return rt_bad(c, op, "buffer argument 1 (buffer #%d, output): expected ld %d halo %d, found ld %u halo %u", op->b[1],
+                  p[2], p[4], o->ld, o->halo);
+  if (rt_need(c, op, 0, (int)x->dtype, (size_t)p[0] * p[1] * p[3]) ||
+      rt_need(c, op, 1, (int)o->dtype, (size_t)(p[0] + 2 * p[4]) * (p[1] + 2 * p[4]) * p[2]))
+    return RT_E_PARAM;
+  return 0;
+}
+static int pad_init(rt_ctx *c, rt_op *op) {
+  return rt_pad_check(c, op) || rt_need(c, op, 0, RT_F32, 1) ? RT_E_PARAM : 0;
+}
+int rt_pad_run(rt_ctx *c, rt_op *op, int esz) {
+  const int *p = op->p;
+  return bnh_pad(rt_b(c, op, 0), rt_ws(c, op, 0), p[0], p[1], p[2], p[3], p[4], esz, rt_b(c, op, 1), rt_ws(c, op, 1),
+                 c->nwin, c->stream);
+}
+static int pad_run(rt_ctx *c, rt_op *op) { return rt_pad_run(c, op, 4); }
+
+static const rt_kernel K_LOGMEL = {logmel_init, logmel_run, logmel_fini, "fe_logmel", 0x2, 0};
+static const rt_kernel K_STEM = {stem_init, stem_run, rt_dev_fini, "stem_f32", 0x6, 0};
+static const rt_kernel K_SE = {se_init, se_run, rt_dev_fini, "se_f32", 0x1, 0};
+static const rt_kernel K_SE_GATE = {seg_init, seg_run, rt_dev_fini, "se_gate_f32", 0x2, 0};
+static const rt_kernel K_MEAN = {mean_init, mean_run, nullptr, "mean_f32", 0x2, 0};
+static const rt_kernel K_PAD = {pad_init, pad_run, nullptr, "pad_f32", 0x2, 0};
 static const rt_kernel K_DW3 = {dw3_init, dw3_run, rt_dev_fini, "dw3_f32", 0x6, 0};
 static const rt_kernel K_DWK = {dwk_init, dwk_run, rt_dev_fini, "dwk_f32", 0x6, 0};
 
@@ -97,6 +249,12 @@ const rt_kernel *rt_k_f32(int base) {
   switch (base) {
     case RT_OP_DW3: return &K_DW3;
     case RT_OP_DWK: return &K_DWK;
+    case RT_OP_FE_LOGMEL: return &K_LOGMEL;
+    case RT_OP_STEM: return &K_STEM;
+    case RT_OP_SE: return &K_SE;
+    case RT_OP_SE_GATE: return &K_SE_GATE;
+    case RT_OP_MEAN: return &K_MEAN;
+    case RT_OP_PAD: return &K_PAD;
     default: return nullptr;
   }
 }

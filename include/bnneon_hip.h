@@ -199,6 +199,44 @@ int bnh_dw_s8(const int8_t *x, long long x_ws, int H, int W, int C, int k, int s
               const int32_t *bias, const int32_t *mult, const int32_t *shift, int zx, int zy, int lo, int hi,
               const int8_t *lut, int8_t *out, long long o_ws, int Ho, int Wo, int B, void *stream);
 
+/* ------------------------------------------------------------------ fp32 ops around the int8 GEMMs
+ * The fp32 registry ops of the int8 Perch-family plan, bit-identical to the reference's kernels. Per-window strides in
+ * elements; B windows per launch. */
+/* FE_LOGMEL: replaces pc_logmel_new / pc_logmel_run (src/pc_kern_f32.c:28-149): pcm [nsamp] -> spec f32
+ * [nfr][nmel], nfr = (nsamp + 2 pad - frame) / hop + 1; window [frame]; mel dense [nmel][nfft/2 + 1] (kept sparse);
+ * spec = ln(max(mel . |FFT|, floor)) * scale with the reference's radix-2 FFT and log2 polynomial. nfft a power of
+ * two in 16..2048, frame <= nfft, nmel <= 512 (the reference's limits). */
+typedef struct bnh_logmel bnh_logmel;
+bnh_logmel *bnh_logmel_new(int nsamp, int frame, int hop, int pad, int nfft, int nmel, const float *window,
+                           const float *mel, float floor_, float scale);
+void bnh_logmel_free(bnh_logmel *F);
+int bnh_logmel_frames(const bnh_logmel *F);
+int bnh_logmel_run(const bnh_logmel *F, const float *pcm, long long p_ws, float *spec, long long s_ws, int B, void *stream);
+/* STEM: replaces stem_run (src/rt_ops_f32.c:416-425; pc_im2col1 + gemm_f32): a 1-channel image [H][W], VALID k x k
+ * stride s -> out [Ho][Wo][ldo] (opad: zero-haloed [Ho+2opad][Wo+2opad][ldo]) = act(conv + b), channels < Np stored;
+ * w the package's fp32 panels [Np/8][Kp][8] (Kp >= k*k, Kp % 4 == 0; 16-byte aligned), bias [Np]. act 0/1/2. */
+int bnh_stem_f32(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
+                 const float *bias, int Kp, int Np, int act, float *out, long long o_ws, int ldo, int opad, int B,
+                 void *stream);
+/* SE_GATE / SE: replaces seg_run and se_run (src/rt_ops_f32.c:297-324; v24k32_se_fc1 / v24k32_se, src/v24_f32.c:
+ * 164-210): from the channel sums chsum [C] of P pixels, gate [C] = sigmoid(w2 silu(w1 mean + b1) + b2) (w1 [rd][C],
+ * b1 [rd], w2t [rd][C], b2 [C]; silu by the C library's expf, as the reference). gate (or NULL) receives it; D (or
+ * NULL) [P][C] is multiplied by it in place. C % 4 == 0, C <= 4096, rd <= 512. */
+int bnh_se_f32(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
+               const float *w2t, const float *b2, float *gate, long long g_ws, float *D, long long d_ws, int B,
+               void *stream);
+/* MEAN: replaces pc_mean_f32 (src/pc_kern_f32.c:342-348): out [C] = (sum over P rows of x [P][ld]) / P */
+int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
+                 void *stream);
+/* PAD: replaces pad_run (src/rt_ops_f32.c:503-508, src/rt_ops_f16.c:204-210): rows [H][W][ld] -> zero-haloed
+ * [H+2h][W+2h][C], elements of esz (4 or 2) bytes */
+int bnh_pad(const void *x, long long x_ws, int H, int W, int C, int ld, int h, int esz, void *xp, long long p_ws, int B,
+            void *stream);
+/* rt_zero_halo (src/rt_pkg.c:194-203) on every window: zeroes the halo of [H+2h][W+2h][C], elements of esz bytes */
+int bnh_zero_halo(void *xp, long long ws, int H, int W, int C, int h, int esz, int B, void *stream);
+/* test hook: y = expf(x) as the C library computes it (glibc's table method), elementwise on the device */
+int bnh_eval_expf(const float *x, float *y, long long n, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

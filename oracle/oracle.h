@@ -143,6 +143,30 @@ int8_t orc_requant(int32_t acc, int32_t mult, int shift, int zy, int lo, int hi)
 void orc_gemm_s8_requant(const int8_t *w, const int8_t *x, const int32_t *bias, const int32_t *mult, const int32_t *shift,
                          int N, int K, int M, int zx, int zy, int lo, int hi, int8_t *out);
 
+/* ---------------------------------------------------------------- fp32 ops around the int8 GEMMs (fe.c) */
+float orc_log2_acc(float x);                      /* log2_acc_f32x4 lane, src/gemm_f32.h:57-71 */
+float orc_exp2_f32(float t);                      /* exp2_f32x4 lane, src/gemm_f32.h:74-85 */
+float orc_sigmoid_f32(float x);                   /* sigmoid_f32x4 lane, src/gemm_f32.h:93-96 */
+int orc_logmel_frames(int nsamp, int frame, int hop, int pad);
+/* FE_LOGMEL of one window (src/pc_kern_f32.c:28-149): spec [nfr][nmel]; returns nfr, or -1 for refused limits */
+int orc_logmel(const float *pcm, int nsamp, int frame, int hop, int pad, int nfft, int nmel, const float *window,
+               const float *mel, float floor_, float scale, float *spec);
+/* gemm_f32 (src/gemm_f32.c:141-197), w [Np/8][Kp][8], optional input gate */
+void orc_gemm_f32(const float *A, int lda, int M, const float *w, const float *b, int Kp, int Np, const float *gate,
+                  const orc_epi32 *e);
+/* STEM (src/rt_ops_f32.c:416-425): im2col of a 1-channel image, VALID k x k stride s, then gemm_f32 */
+void orc_stem_f32(const float *img, int H, int W, int k, int s, int Ho, int Wo, const float *w, const float *b, int Kp,
+                  int Np, const orc_epi32 *e);
+/* SE_GATE (src/rt_ops_f32.c:317-324): gate [C] from the channel sums of P pixels */
+void orc_se_gate_f32(const float *chsum, int C, int rd, int P, const float *w1, const float *b1, const float *w2t,
+                     const float *b2, float *gate);
+/* SE (src/rt_ops_f32.c:297-309): D [P][C] gated in place */
+void orc_se_f32(float *D, int P, int C, const float *chsum, int rd, const float *w1, const float *b1, const float *w2t,
+                const float *b2);
+void orc_mean_f32(const float *x, int P, int C, int ld, float *out);  /* src/pc_kern_f32.c:342-348 */
+void orc_pad(const void *x, int H, int W, int C, int ld, int h, size_t esz, void *xp);  /* PAD, src/rt_ops_f32.c:503-508 */
+void orc_expf_n(const float *x, float *y, long long n);  /* the C library's expf, elementwise */
+
 #ifdef __cplusplus
 }
 #endif

@@ -355,3 +355,106 @@ def wino_s0(xp, w, b):
     lib().orc_wino_s0(xp.ctypes.data, xp.shape[0] - 2, xp.shape[1] - 2, U.ctypes.data, b16.ctypes.data,
                       out.ctypes.data)
     return out
+
+
+_SIGS.update({
+    "orc_log2_acc": (f32, [f32]),
+    "orc_exp2_f32": (f32, [f32]),
+    "orc_sigmoid_f32": (f32, [f32]),
+    "orc_logmel_frames": (i32, [i32, i32, i32, i32]),
+    "orc_logmel": (i32, [vp, i32, i32, i32, i32, i32, i32, vp, vp, f32, f32, vp]),
+    "orc_gemm_f32": (None, [vp, i32, i32, vp, vp, i32, i32, vp, C.POINTER(OrcEpi32)]),
+    "orc_stem_f32": (None, [vp, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, C.POINTER(OrcEpi32)]),
+    "orc_se_gate_f32": (None, [vp, i32, i32, i32, vp, vp, vp, vp, vp]),
+    "orc_se_f32": (None, [vp, i32, i32, vp, i32, vp, vp, vp, vp]),
+    "orc_mean_f32": (None, [vp, i32, i32, i32, vp]),
+    "orc_pad": (None, [vp, i32, i32, i32, i32, i32, C.c_size_t, vp]),
+    "orc_expf_n": (None, [vp, vp, C.c_longlong]),
+})
+
+
+def expf(x):
+    """The C library's expf (the function the reference's scalar SiLU calls)."""
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_expf_n(P(x), P(y), x.size)
+    return y
+
+
+def logmel(pcm, frame, hop, pad, nfft, window, mel, floor_, scale):
+    """FE_LOGMEL of one window: pcm [nsamp] -> spec [nfr][nmel]."""
+    pcm = _c(pcm, np.float32)
+    mel = _c(mel, np.float32)
+    nmel = mel.shape[0]
+    nfr = lib().orc_logmel_frames(pcm.size, frame, hop, pad)
+    spec = np.zeros((nfr, nmel), np.float32)
+    r = lib().orc_logmel(P(pcm), pcm.size, frame, hop, pad, nfft, nmel, P(_c(window, np.float32)), P(mel),
+                         floor_, scale, P(spec))
+    if r < 0:
+        raise ValueError("logmel limits")
+    return spec
+
+
+def fpack(w, b):
+    """fp_pack (src/gemm_f32.c:22-35): w [N][K] -> panels [Np/8][Kp][8] (Kp = K rounded to 4), bias [Np + 8]."""
+    w = np.asarray(w, np.float32)
+    N, K = w.shape
+    Np, Kp = (N + 7) // 8 * 8, (K + 3) // 4 * 4
+    wp = np.zeros((Np, Kp), np.float32)
+    wp[:N, :K] = w
+    panels = np.ascontiguousarray(wp.reshape(Np // 8, 8, Kp).transpose(0, 2, 1))
+    bb = np.zeros(Np + 8, np.float32)
+    bb[:N] = b
+    return panels, bb, (N, K, Kp, Np)
+
+
+def gemm_f32(A, panels, bb, Kp, Np, act=0, gate=None, res=None, ldr=0, rpad=0, rw=0, ow=0, opad=0, ldo=None):
+    A = _c(A, np.float32)
+    M, lda = A.shape
+    ldo = ldo or Np
+    rows = M if not opad else (M // ow + 2 * opad) * (ow + 2 * opad)
+    out = np.zeros((rows, ldo), np.float32)
+    r = None if res is None else _c(res, np.float32)
+    e = OrcEpi32(act, out.ctypes.data, ldo, ow, opad, P(r), ldr, rpad, rw)
+    g = None if gate is None else _c(gate, np.float32)
+    lib().orc_gemm_f32(P(A), lda, M, P(_c(panels, np.float32)), P(_c(bb, np.float32)), Kp, Np, P(g), C.byref(e))
+    return out
+
+
+def stem_f32(img, k, s, panels, bb, Kp, Np, act=1, opad=0, ldo=None):
+    img = _c(img, np.float32)
+    H, W = img.shape
+    Ho, Wo = (H - k) // s + 1, (W - k) // s + 1
+    ldo = ldo or Np
+    out = np.zeros(((Ho + 2 * opad) * (Wo + 2 * opad), ldo), np.float32)
+    e = OrcEpi32(act, out.ctypes.data, ldo, Wo, opad, None, 0, 0, 0)
+    lib().orc_stem_f32(P(img), H, W, k, s, Ho, Wo, P(_c(panels, np.float32)), P(_c(bb, np.float32)), Kp, Np,
+                       C.byref(e))
+    return out
+
+
+def se_gate_f32(chsum, P_, w1, b1, w2t, b2):
+    chsum = _c(chsum, np.float32)
+    w1 = _c(w1, np.float32)
+    rd, Cc = w1.shape
+    g = np.zeros(Cc, np.float32)
+    lib().orc_se_gate_f32(P(chsum), Cc, rd, P_, P(w1), P(_c(b1, np.float32)), P(_c(w2t, np.float32)),
+                          P(_c(b2, np.float32)), P(g))
+    return g
+
+
+def mean_f32(x, C_):
+    x = _c(x, np.float32)
+    Pp, ld = x.shape
+    out = np.zeros(C_, np.float32)
+    lib().orc_mean_f32(P(x), Pp, C_, ld, P(out))
+    return out
+
+
+def pad(x, H, W, C_, h):
+    """PAD of rows x [H*W][ld] -> [(H+2h)][(W+2h)][C] (dtype kept)."""
+    x = np.ascontiguousarray(x)
+    ld = x.shape[-1]
+    out = np.full(((H + 2 * h) * (W + 2 * h), C_), 7, x.dtype)
+    lib().orc_pad(P(x), H, W, C_, ld, h, x.dtype.itemsize, P(out))
+    return out

@@ -1,0 +1,196 @@
+"""GPU parity of the fp32 ops around the int8 GEMMs against the CPU oracle
+(oracle/fe.c), all bit-identical: the device expf against the C library's
+expf, the log-mel front end (Perch geometry, an odd frame length, a frame
+shorter than the FFT, a signal with a click and silence), the stem, the
+squeeze-excitation gate and in-place SE, the spatial mean and the halo copy,
+each on several windows per launch with padded per-window strides."""
+import numpy as np
+import pytest
+
+import pyoracle as O
+from bnneon import perchnet
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def same_bits(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.dtype == b.dtype and a.shape == b.shape, (a.dtype, b.dtype, a.shape, b.shape)
+    an, bn = np.isnan(a), np.isnan(b)
+    u = np.uint16 if a.dtype == np.float16 else np.uint32
+    return bool(np.array_equal(an, bn) and np.array_equal(a.view(u)[~an], b.view(u)[~bn]))
+
+
+def strided(a, slack):
+    B = a.shape[0]
+    n = a[0].size
+    out = np.zeros((B, n + slack), a.dtype)
+    out[:, :n] = a.reshape(B, n)
+    return out, n + slack
+
+
+def test_expf_matches_c_library(hip):
+    H = hip
+    rng = np.random.default_rng(0)
+    bits = np.concatenate([rng.integers(0, 2 ** 32, 1 << 22, dtype=np.uint64).astype(np.uint32),
+                           np.arange(0xc2d00000, 0xc2d80000, dtype=np.uint32),   # around -104 (underflow edge)
+                           np.arange(0x42b00000, 0x42b20000, dtype=np.uint32),   # around 88 (overflow edge)
+                           np.arange(0x3f000000, 0x3f100000, dtype=np.uint32)])  # [0.5, 0.56)
+    x = bits.view(np.float32)
+    say("expf", x.size)
+    dx = H.DeviceArray.from_host(x)
+    dy = H.DeviceArray(x.shape, np.float32)
+    H.check(H.lib().bnh_eval_expf(dx.ptr, dy.ptr, x.size, None), "eval_expf")
+    H.sync()
+    assert same_bits(dy.numpy(), O.expf(x))
+
+
+def run_logmel(H, pcm, frame, hop, pad, nfft, window, mel, floor_, scale, slack=5):
+    B, nsamp = pcm.shape
+    nmel = mel.shape[0]
+    F = H.lib().bnh_logmel_new(nsamp, frame, hop, pad, nfft, nmel, np.ascontiguousarray(window, np.float32).ctypes.data,
+                               np.ascontiguousarray(mel, np.float32).ctypes.data, floor_, scale)
+    if not F:
+        H.check(None, "bnh_logmel_new")
+    try:
+        nfr = H.lib().bnh_logmel_frames(F)
+        xs, x_ws = strided(pcm.astype(np.float32), slack)
+        dx = H.DeviceArray.from_host(xs)
+        s_ws = nfr * nmel + 3
+        do = H.DeviceArray.from_host(np.full((B, s_ws), np.nan, np.float32))
+        H.check(H.lib().bnh_logmel_run(F, dx.ptr, x_ws, do.ptr, s_ws, B, None), "logmel")
+        H.sync()
+        return do.numpy()[:, :nfr * nmel].reshape(B, nfr, nmel)
+    finally:
+        H.lib().bnh_logmel_free(F)
+
+
+def test_logmel_perch_geometry(hip):
+    rng = np.random.default_rng(1)
+    B = 3
+    pcm = np.stack([perchnet.signal(rng) for _ in range(B)])
+    pcm[1, 5000] = 1.0          # a click
+    pcm[2, 40000:80000] = 0.0   # silence: the floor
+    window = (0.5 - 0.5 * np.cos(2 * np.pi * np.arange(640) / 640)).astype(np.float32)
+    mel = perchnet.mel_bank()
+    say("logmel perch", B)
+    got = run_logmel(hip, pcm, 640, 320, 160, 1024, window, mel, 1e-3, 1.0)
+    assert got.shape == (B, 500, 128)
+    for i in range(B):
+        assert same_bits(got[i], O.logmel(pcm[i], 640, 320, 160, 1024, window, mel, 1e-3, 1.0)), i
+
+
+@pytest.mark.parametrize("nsamp,frame,hop,pad,nfft,nmel", [(2000, 201, 100, 50, 256, 8), (3000, 64, 48, 0, 64, 5),
+                                                           (1500, 400, 160, 200, 512, 40), (900, 16, 16, 7, 16, 3)])
+def test_logmel_geometries(hip, nsamp, frame, hop, pad, nfft, nmel):
+    rng = np.random.default_rng(nsamp + nfft)
+    pcm = rng.standard_normal((2, nsamp)).astype(np.float32) * 0.3
+    window = rng.uniform(-0.2, 1.0, frame).astype(np.float32)   # negative taps: -0 products in the pad
+    bins = nfft // 2 + 1
+    mel = np.where(rng.uniform(0, 1, (nmel, bins)) < 0.3, rng.uniform(0, 1, (nmel, bins)), 0).astype(np.float32)
+    mel[:, 0] = 0
+    mel[0, 0] = 0.5      # DC and Nyquist bins in use
+    mel[-1, -1] = 0.25
+    say("logmel", nsamp, frame, hop, pad, nfft, nmel)
+    got = run_logmel(hip, pcm, frame, hop, pad, nfft, window, mel, 1e-4, 0.7)
+    for i in range(2):
+        assert same_bits(got[i], O.logmel(pcm[i], frame, hop, pad, nfft, window, mel, 1e-4, 0.7)), i
+
+
+@pytest.mark.parametrize("Hh,W,k,s,co,act,opad", [(500, 128, 3, 2, 40, 1, 1), (33, 20, 5, 1, 12, 2, 0),
+                                                   (17, 19, 1, 1, 8, 0, 2), (40, 30, 7, 3, 16, 1, 0)])
+def test_stem(hip, Hh, W, k, s, co, act, opad):
+    H = hip
+    rng = np.random.default_rng(Hh + k)
+    B = 3
+    img = (rng.standard_normal((B, Hh, W)) * 3).astype(np.float32)
+    w = (rng.standard_normal((co, k * k)) * np.sqrt(2 / (k * k))).astype(np.float32)
+    b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    panels, bb, (N, K, Kp, Np) = O.fpack(w, b)
+    Ho, Wo = (Hh - k) // s + 1, (W - k) // s + 1
+    ldo = Np + 4
+    xs, x_ws = strided(img, 7)
+    dx = H.DeviceArray.from_host(xs)
+    dw = H.DeviceArray.from_host(panels)
+    db = H.DeviceArray.from_host(bb)
+    rows = (Ho + 2 * opad) * (Wo + 2 * opad)
+    o_ws = rows * ldo + 8
+    do = H.DeviceArray.from_host(np.full((B, o_ws), 5.0, np.float32))
+    say("stem", Hh, W, k, s, co)
+    H.check(H.lib().bnh_stem_f32(dx.ptr, x_ws, Hh, W, k, s, Ho, Wo, dw.ptr, db.ptr, Kp, Np, act, do.ptr, o_ws, ldo,
+                                 opad, B, None), "stem")
+    H.sync()
+    got = do.numpy()[:, :rows * ldo].reshape(B, rows, ldo)
+    for i in range(B):
+        want = O.stem_f32(img[i], k, s, panels, bb, Kp, Np, act=act, opad=opad, ldo=ldo)
+        assert same_bits(got[i][:, :Np], want[:, :Np]), i
+        if not opad:
+            assert (got[i][:, Np:] == 5.0).all()   # channels past Np untouched
+
+
+@pytest.mark.parametrize("C,rd,P,inplace", [(40, 10, 15687, False), (2304, 96, 64, False), (36, 9, 100, True),
+                                            (4096, 512, 8, False), (816, 34, 256, True)])
+def test_se(hip, C, rd, P, inplace):
+    H = hip
+    rng = np.random.default_rng(C + rd)
+    B = 3
+    chsum = (rng.standard_normal((B, C)) * np.sqrt(P) * 0.5).astype(np.float32)
+    chsum[0, :4] = [np.inf, -np.inf, 0.0, -0.0] if C > 8 else chsum[0, :4]
+    w1 = (rng.standard_normal((rd, C)) * np.sqrt(2 / C)).astype(np.float32)
+    b1 = (rng.standard_normal(rd) * 2).astype(np.float32)   # large fc1 outputs: expf far from 1
+    w2t = (rng.standard_normal((rd, C)) * np.sqrt(2 / rd)).astype(np.float32)
+    b2 = (rng.standard_normal(C) * 3).astype(np.float32)
+    cs, c_ws = strided(chsum, 3)
+    dc = H.DeviceArray.from_host(cs)
+    dt = [H.DeviceArray.from_host(a) for a in (w1, b1, w2t, b2)]
+    g_ws = C + 5
+    dg = H.DeviceArray.from_host(np.zeros((B, g_ws), np.float32))
+    D = rng.standard_normal((B, P, C)).astype(np.float32) if inplace else None
+    dD, d_ws = (None, 0)
+    if inplace:
+        Ds, d_ws = strided(D, 9)
+        dD = H.DeviceArray.from_host(Ds)
+    say("se", C, rd, P, inplace)
+    H.check(H.lib().bnh_se_f32(dc.ptr, c_ws, C, rd, P, dt[0].ptr, dt[1].ptr, dt[2].ptr, dt[3].ptr, dg.ptr, g_ws,
+                               dD.ptr if inplace else None, d_ws, B, None), "se")
+    H.sync()
+    g = dg.numpy()[:, :C]
+    for i in range(B):
+        want = O.se_gate_f32(chsum[i], P, w1, b1, w2t, b2)
+        assert same_bits(g[i], want), i
+        if inplace:
+            got = dD.numpy()[i, :P * C].reshape(P, C)
+            assert same_bits(got, (D[i] * want[None, :]).astype(np.float32)), i
+
+
+def test_mean_and_pad(hip):
+    H = hip
+    rng = np.random.default_rng(9)
+    B, P, C, ld = 3, 64, 1536, 1544
+    x = rng.standard_normal((B, P, ld)).astype(np.float32)
+    xs, x_ws = strided(x, 11)
+    dx = H.DeviceArray.from_host(xs)
+    do = H.DeviceArray.from_host(np.zeros((B, C + 4), np.float32))
+    say("mean")
+    H.check(H.lib().bnh_mean_f32(dx.ptr, x_ws, P, C, ld, do.ptr, C + 4, B, None), "mean")
+    H.sync()
+    for i in range(B):
+        assert same_bits(do.numpy()[i, :C], O.mean_f32(x[i], C))
+    for esz, dt in ((4, np.float32), (2, np.float16)):
+        Hh, W, C, ld, h = 9, 7, 24, 32, 2
+        x = rng.standard_normal((B, Hh * W, ld)).astype(dt)
+        xs, x_ws = strided(x, 3)
+        dx = H.DeviceArray.from_host(xs)
+        per = (Hh + 2 * h) * (W + 2 * h) * C
+        dp = H.DeviceArray.from_host(np.full((B, per + 6), 9, dt))
+        say("pad", esz)
+        H.check(H.lib().bnh_pad(dx.ptr, x_ws, Hh, W, C, ld, h, esz, dp.ptr, per + 6, B, None), "pad")
+        H.sync()
+        got = dp.numpy()[:, :per]
+        for i in range(B):
+            assert np.array_equal(got[i].reshape(-1), O.pad(x[i], Hh, W, C, h).reshape(-1)), (esz, i)
+        assert (dp.numpy()[:, per:] == 9).all()

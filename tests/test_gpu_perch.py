@@ -1,0 +1,56 @@
+"""The Perch-v2-shaped int8 network end to end on the GPU (bnn_init /
+bnn_infer_batch on a .bnpk built by bnneon.perchnet): FE_LOGMEL, STEM,
+DW3 / DWK, SE_GATE, PW_S8 (gated, residual), PAD, MEAN and GEMV_S8 over 26
+MBConv blocks, logits and embeddings bit-identical to the oracle's op-by-op
+run of the same package, and identical whatever the batch size."""
+import numpy as np
+import pytest
+
+from bnneon import binding, perchnet
+
+import oracle_net
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def same(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    an, bn = np.isnan(a), np.isnan(b)
+    return np.array_equal(an, bn) and np.array_equal(a.view(np.uint32)[~an], b.view(np.uint32)[~bn])
+
+
+@pytest.fixture(scope="module")
+def perch(tmp_path_factory):
+    pn = perchnet.PerchNet(seed=3)
+    path = pn.write(str(tmp_path_factory.mktemp("perch") / "perch_s8.bnpk"))
+    return pn, path
+
+
+def test_perch_batch_bit_exact(hip, perch):
+    pn, path = perch
+    rng = np.random.default_rng(4)
+    B = 6
+    pcm = np.stack([perchnet.signal(rng) for _ in range(B)])
+    pcm[1] = 0.0                 # silence: every frame at the log floor
+    pcm[2, 1000] = 0.9           # a click
+    on = oracle_net.OracleNet(pn.net, 0, pn.net.last, pn.emb_buf)
+    say("perch batch", B)
+    with binding.Model(path) as m:
+        assert m.info.n_classes == perchnet.N_CLASSES and m.info.emb_dim == perchnet.EMB
+        out, emb, status = m.infer_batch(pcm)
+        assert not status.any()
+        for w in (0, 1, 2):
+            ref, ref_emb, _ = on.run(pcm[w])
+            say("window", w)
+            assert same(out[w], ref[:perchnet.N_CLASSES]), w
+            assert same(emb[w], ref_emb[:perchnet.EMB]), w
+        # the same windows one at a time and in another batch split
+        for w in (3, 5):
+            o1, e1, s1 = m.infer_batch(pcm[w:w + 1])
+            assert not s1.any() and same(o1[0], out[w]) and same(e1[0], emb[w])
+        o2, e2, s2 = m.infer_batch(pcm[2:6])
+        assert not s2.any() and same(o2, out[2:6]) and same(e2, emb[2:6])
