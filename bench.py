@@ -5,7 +5,12 @@
 Workloads (one "step" = one pass of the hot path over one batch of synthetic
 windows already resident in HBM):
 
-  gemm_s8_requant  (default) the int8 pointwise convolution 1152 -> 256 over
+  perch_s8         (default) the Perch-v2-shaped int8 network end to end
+                   through bnn_infer_batch_device: 5 s of 32 kHz audio per
+                   window -> log-mel 500 x 128 -> stem -> 26 MBConv blocks
+                   (int8 1x1 convs, fp32 depthwise, SE) -> 1536 embedding ->
+                   14,795-class int8 linear head, batch 256 windows.
+  gemm_s8_requant  the int8 pointwise convolution 1152 -> 256 over
                    24 x 64 pixels per window, int8 NCHW activations with zero
                    point -128, per-channel Q31 requant, batch 256 windows.
   pw_s8            libbnneon's PW_S8 op (fp32 rows, per-row dynamic int8,
@@ -47,8 +52,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=None,
                     help="windows per launch (256; 64 for the depthwise workloads)")
-    ap.add_argument("--workload", default="gemm_s8_requant",
-                    choices=["gemm_s8_requant", "pw_s8", "dw_f16", "dw_s8", "wino_f16", "copy"])
+    ap.add_argument("--workload", default="perch_s8",
+                    choices=["perch_s8", "gemm_s8_requant", "pw_s8", "dw_f16", "dw_s8", "wino_f16", "copy"])
     ap.add_argument("--k", type=int, default=5, choices=[3, 5], help="depthwise kernel size")
     ap.add_argument("--s", type=int, default=1, choices=[1, 2], help="depthwise stride")
     ap.add_argument("--no-cpu", action="store_true",
@@ -217,6 +222,9 @@ def main():
         return
     if a.workload == "wino_f16":
         run_wino(a, H, rng, B, stream)
+        return
+    if a.workload == "perch_s8":
+        run_perch(a, H, rng, B, stream)
         return
     if a.workload == "gemm_s8_requant":
         w, x, bias, mult, shift = config0_inputs(rng, B)
@@ -393,6 +401,91 @@ def run_wino(a, H, rng, B, stream):
         line["cpu_baseline"] = cpu_baseline_wino(xp, w, b)
     L.bnh_wino16_free(P)
     print(json.dumps(line), flush=True)
+
+
+
+def perch_counts(net):
+    """(int8 GEMM ops per window, the largest PW_S8 op record) of a netbuild net."""
+    ops, big = 0, None
+    for code, b, t, p in net.ops:
+        if code & 0xff == 22:   # PW_S8: N K Kp Np M ...
+            ops += 2 * p[0] * p[1] * p[4]
+            if big is None or p[0] * p[1] * p[4] > big[3][0] * big[3][1] * big[3][4]:
+                big = (code, b, t, p)
+        elif code & 0xff == 23:  # GEMV_S8
+            ops += 2 * p[0] * p[1]
+    return ops, big
+
+
+def cpu_baseline_perch(pn, rng):
+    """The oracle's op-by-op run of the same package, one window per thread, on a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_net
+    from bnneon import perchnet
+    T = cpu_threads()
+    n_win = T
+    on = oracle_net.OracleNet(pn.net, 0, pn.net.last, pn.emb_buf)
+    pcms = [perchnet.signal(rng) for _ in range(n_win)]
+    t0 = time.perf_counter()
+    with concurrent.futures.ThreadPoolExecutor(T) as ex:
+        list(ex.map(lambda i: on.run(pcms[i]), range(n_win)))
+    dt = time.perf_counter() - t0
+    return {"value": round(n_win / dt, 3), "unit": "windows/s", "cores": T, "kind": "port",
+            "sample": f"{n_win} windows of the same package through the scalar C oracle's op-by-op "
+                      f"restatement (log-mel, stem, 26 blocks, head), one window per thread ({T} threads), "
+                      f"-O2 -ffp-contract=off; {dt:.2f} s wall"}
+
+
+def run_perch(a, H, rng, B, stream):
+    import tempfile
+    from bnneon import binding, perchnet
+    pn = perchnet.PerchNet(seed=7)
+    tmp = tempfile.mkdtemp(prefix="bnn_bench_")
+    path = pn.write(os.path.join(tmp, "perch_v2_shaped_s8.bnpk"))
+    L = binding.load_library()
+    m = binding.Model(path)
+    os.unlink(path)
+    os.rmdir(tmp)
+    nc, ne, ns = m.info.n_classes, m.info.emb_dim, m.info.n_samples
+    pcm = np.stack([perchnet.signal(rng) for _ in range(min(B, 16))])
+    pcm = np.concatenate([pcm] * ((B + len(pcm) - 1) // len(pcm)))[:B]
+    dx = H.DeviceArray.from_host(pcm)
+    dout = H.DeviceArray.zeros((B, nc), np.float32)
+    demb = H.DeviceArray.zeros((B, ne), np.float32)
+    status = np.zeros(B, np.int32)
+    sp = status.ctypes.data_as(binding._IP)
+
+    def launch():
+        r = L.bnn_infer_batch_device(m.ctx, dx.ptr, B, dout.ptr, demb.ptr, sp, stream)
+        if r != 0:
+            raise RuntimeError(f"bnn_infer_batch_device returned {r}: {L.bnn_last_error()}")
+    ms, wall = time_steps(H, stream, launch, a.steps, a.warmup)
+    ops_win, _ = perch_counts(pn.net)
+    value = B / (ms * 1e-3)
+    tops = ops_win * B / (ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "windows/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: -30 dBFS noise + 3 chirps 1-10 kHz per window; random weights",
+        "config": {"workload": "Perch-v2-shaped int8 net (log-mel 500x128, stem 3x3/2 -> 40, 26 MBConv blocks "
+                               "with SE, 1x1 convs on PW_S8, fp32 depthwise, 384->1536 head conv, mean, "
+                               "14,795-class GEMV_S8), 160,000 samples @ 32 kHz per window",
+                   "global_batch": B, "n_samples": ns, "n_classes": nc,
+                   "parallelism": "1 GPU, windows batched per launch",
+                   "wall_s_timed_region": round(wall, 4)},
+        "int8_tops": round(tops, 3), "mfma_frac": round(tops / INT8_PEAK_TOPS, 5),
+    }
+    line["roofline"] = perch_roofline(H, pn, B, stream, a)
+    m.close()
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_perch(pn, rng)
+    print(json.dumps(line), flush=True)
+
+
+def perch_roofline(H, pn, B, stream, a):
+    return None
 
 
 if __name__ == "__main__":

@@ -175,10 +175,129 @@ __global__ __launch_bounds__(256) void k_dw_f16(const h16 *__restrict__ xp, long
 }
 
 // ------------------------------------------------------------------ channel sums (pass 2)
-// form 0 (fp32 DWK): per row, 4-groups add (o0 + o1) + (o2 + o3), tail pixels their value; form 2 (fp32 DW3): every
-// pixel in raster order; form 1 (fp16 DWK): fp16 group sums (pairs, singles) widened; form 3 (fp16 DW3): per row an
-// fp16 running sum, widened at the row's end.
-__global__ void k_chsum_f32(const float *__restrict__ out, long long o_ws, int C, int Ho, int Wo, int form,
+// The reference adds the outputs of each channel into one fp32 sum, row after row, in terms that depend on the kernel:
+//   form 0 (fp32 DWK): per row the 4-pixel groups (o0 + o1) + (o2 + o3), then each tail pixel;
+//   form 2 (fp32 DW3): every pixel in raster order;
+//   form 1 (fp16 DWK): per row fp16 group sums (o0 + o1) + (o2 + o3), then an fp16 pair, then a single, widened;
+//   form 3 (fp16 DW3): per row an fp16 running sum over the row, widened at the row's end.
+// The sum is one dependent chain per channel. A block owns one window and a slab of <= 64 channels: all its waves
+// compute the terms of a chunk of rows into LDS (4 channels per item, vector loads), then wave 0 (one lane per
+// channel) adds them in order while the other waves compute the next chunk into the second buffer.
+template <int FORM>
+__device__ __forceinline__ int cs_terms(int Wo) {
+  if (FORM == 0) return Wo / 4 + Wo % 4;
+  if (FORM == 2) return Wo;
+  if (FORM == 1) return Wo / 4 + ((Wo % 4) >> 1) + (Wo & 1);
+  return 1;
+}
+
+struct f4 { float v[4]; };
+
+BNH_DEV f4 cs_ld(const float *p) {
+  const float4 t = *(const float4 *)p;
+  return f4{{t.x, t.y, t.z, t.w}};
+}
+BNH_DEV void cs_ld(const h16 *p, h16 (&o)[4]) {
+  const uint2 t = *(const uint2 *)p;
+  o[0] = hfrom((uint16_t)(t.x & 0xffffu)); o[1] = hfrom((uint16_t)(t.x >> 16));
+  o[2] = hfrom((uint16_t)(t.y & 0xffffu)); o[3] = hfrom((uint16_t)(t.y >> 16));
+}
+
+// term j of a row (row points at the row's first pixel, channel c0 of the 4) for 4 channels
+template <int FORM>
+BNH_DEV f4 cs_term(const float *row, int C, int Wo, int j) {
+  const int g4 = Wo / 4;
+  if (FORM == 0 && j < g4) {
+    const f4 a = cs_ld(row + (long long)(4 * j) * C), b = cs_ld(row + (long long)(4 * j + 1) * C);
+    const f4 c = cs_ld(row + (long long)(4 * j + 2) * C), d = cs_ld(row + (long long)(4 * j + 3) * C);
+    f4 r;
+#pragma unroll
+    for (int q = 0; q < 4; q++) r.v[q] = (a.v[q] + b.v[q]) + (c.v[q] + d.v[q]);
+    return r;
+  }
+  const int ox = FORM == 0 ? 4 * g4 + (j - g4) : j;
+  return cs_ld(row + (long long)ox * C);
+}
+template <int FORM>
+BNH_DEV f4 cs_term(const h16 *row, int C, int Wo, int j) {
+  f4 r;
+  h16 a[4], b[4], c[4], d[4];
+  if (FORM == 3) {
+    h16 rs[4] = {(h16)0.0f, (h16)0.0f, (h16)0.0f, (h16)0.0f};
+    for (int ox = 0; ox < Wo; ox++) {
+      cs_ld(row + (long long)ox * C, a);
+#pragma unroll
+      for (int q = 0; q < 4; q++) rs[q] = rs[q] + a[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) r.v[q] = (float)rs[q];
+    return r;
+  }
+  const int g4 = Wo / 4, np = (Wo % 4) >> 1;
+  if (j < g4) {
+    cs_ld(row + (long long)(4 * j) * C, a);
+    cs_ld(row + (long long)(4 * j + 1) * C, b);
+    cs_ld(row + (long long)(4 * j + 2) * C, c);
+    cs_ld(row + (long long)(4 * j + 3) * C, d);
+#pragma unroll
+    for (int q = 0; q < 4; q++) r.v[q] = (float)((a[q] + b[q]) + (c[q] + d[q]));
+  } else if (j < g4 + np) {
+    cs_ld(row + (long long)(4 * g4) * C, a);
+    cs_ld(row + (long long)(4 * g4 + 1) * C, b);
+#pragma unroll
+    for (int q = 0; q < 4; q++) r.v[q] = (float)(a[q] + b[q]);
+  } else {
+    cs_ld(row + (long long)(Wo - 1) * C, a);
+#pragma unroll
+    for (int q = 0; q < 4; q++) r.v[q] = (float)a[q];
+  }
+  return r;
+}
+
+template <typename T, int FORM>
+__global__ __launch_bounds__(256) void k_chsum(const T *__restrict__ out, long long o_ws, int C, int Ho, int Wo, int R,
+                                               float *__restrict__ chsum, long long cs_ws) {
+  extern __shared__ float tb[];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c0 = blockIdx.x * 64, S = C - c0 < 64 ? C - c0 : 64, S4 = S / 4, win = blockIdx.y;
+  const int Tn = cs_terms<FORM>(Wo), per = R * Tn * S, nch = (Ho + R - 1) / R;
+  const T *o = out + win * o_ws + c0;
+  auto load = [&](int ch, int t0, int nt) {
+    const int rows = Ho - ch * R < R ? Ho - ch * R : R;
+    float *buf = tb + (ch & 1) * per;
+    const int n = rows * Tn * S4;
+#pragma unroll 4
+    for (int it = t0; it < n; it += nt) {
+      const int c4 = it % S4, j = (it / S4) % Tn, r = it / (S4 * Tn);
+      const f4 v = cs_term<FORM>(o + (long long)(ch * R + r) * Wo * C + 4 * c4, C, Wo, j);
+      *(float4 *)(buf + (r * Tn + j) * S + 4 * c4) = make_float4(v.v[0], v.v[1], v.v[2], v.v[3]);
+    }
+  };
+  load(0, tid, 256);
+  __syncthreads();
+  float cs = 0.f;
+  for (int ch = 0; ch < nch; ch++) {
+    if (wave != 0) {
+      if (ch + 1 < nch) load(ch + 1, tid - 64, 192);
+    } else if (lane < S) {
+      const int rows = Ho - ch * R < R ? Ho - ch * R : R;
+      const float *buf = tb + (ch & 1) * per + lane;
+      for (int it = 0; it < rows * Tn; it++) cs = cs + buf[it * S];
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && lane < S) chsum[win * cs_ws + c0 + lane] = cs;
+}
+
+// rows per chunk: two buffers of at most 8 K floats (64 KB of LDS)
+static int chsum_rows(int Tn, int S, int Ho) {
+  int R = 8192 / (Tn * S);
+  if (R < 1) R = 1;
+  return R < Ho ? R : Ho;
+}
+
+// one thread per (window, channel) walking the whole image: for channel counts that are not a multiple of 4
+__global__ void k_chsum1_f32(const float *__restrict__ out, long long o_ws, int C, int Ho, int Wo, int form,
                             float *__restrict__ chsum, long long cs_ws, int B) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long long)B * C) return;
@@ -197,7 +316,7 @@ __global__ void k_chsum_f32(const float *__restrict__ out, long long o_ws, int C
   }
   chsum[win * cs_ws + c] = cs;
 }
-__global__ void k_chsum_f16(const h16 *__restrict__ out, long long o_ws, int C, int Ho, int Wo, int form,
+__global__ void k_chsum1_f16(const h16 *__restrict__ out, long long o_ws, int C, int Ho, int Wo, int form,
                             float *__restrict__ chsum, long long cs_ws, int B) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long long)B * C) return;
@@ -222,6 +341,29 @@ __global__ void k_chsum_f16(const h16 *__restrict__ out, long long o_ws, int C, 
     if (Wo > g2) cs = cs + (float)row[(long long)g2 * C];
   }
   chsum[win * cs_ws + c] = cs;
+}
+
+template <typename T, int FORM>
+static int chsum_launch(const T *out, long long o_ws, int C, int Ho, int Wo, float *chsum, long long cs_ws, int B,
+                        hipStream_t st) {
+  const int Tn = FORM == 0 ? Wo / 4 + Wo % 4 : FORM == 2 ? Wo : FORM == 1 ? Wo / 4 + ((Wo % 4) >> 1) + (Wo & 1) : 1;
+  const int S = C < 64 ? C : 64;
+  if (C % 4 || ((uintptr_t)out & (4 * sizeof(T) - 1)) || (B > 1 && o_ws % 4) || Tn * S > 8192) {
+    if (sizeof(T) == 4)
+      hipLaunchKernelGGL(k_chsum1_f32, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st,
+                         (const float *)out, o_ws, C, Ho, Wo, FORM, chsum, cs_ws, B);
+    else
+      hipLaunchKernelGGL(k_chsum1_f16, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st,
+                         (const h16 *)out, o_ws, C, Ho, Wo, FORM, chsum, cs_ws, B);
+    BNH_HIP(hipGetLastError());
+    return 0;
+  }
+  const int R = chsum_rows(Tn, S, Ho);
+  const size_t lds = 2 * sizeof(float) * (size_t)R * Tn * S;
+  hipLaunchKernelGGL((k_chsum<T, FORM>), dim3((unsigned)bnh_ceil_div(C, 64), (unsigned)B), dim3(256), lds, st, out,
+                     o_ws, C, Ho, Wo, R, chsum, cs_ws);
+  BNH_HIP(hipGetLastError());
+  return 0;
 }
 
 // ------------------------------------------------------------------ int8 depthwise (own specification)
@@ -317,9 +459,7 @@ int bnh_dwk_f32(const float *xp, long long x_ws, int H, int W, int C, int k, int
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);
-    hipLaunchKernelGGL(k_chsum_f32, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st, out, o_ws, C,
-                       Ho, Wo, 0, chsum, cs_ws, B);
-    BNH_HIP(hipGetLastError());
+    if (chsum_launch<float, 0>(out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st)) return -1;
   }
   return 0;
 }
@@ -340,9 +480,7 @@ int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, con
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);
-    hipLaunchKernelGGL(k_chsum_f32, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st, out, o_ws, C,
-                       Ho, Wo, 2, chsum, cs_ws, B);
-    BNH_HIP(hipGetLastError());
+    if (chsum_launch<float, 2>(out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st)) return -1;
   }
   return 0;
 }
@@ -364,9 +502,7 @@ int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, 
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);
-    hipLaunchKernelGGL(k_chsum_f16, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st,
-                       (const h16 *)out, o_ws, C, Ho, Wo, 1, chsum, cs_ws, B);
-    BNH_HIP(hipGetLastError());
+    if (chsum_launch<h16, 1>((const h16 *)out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st)) return -1;
   }
   return 0;
 }
@@ -388,9 +524,7 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);
-    hipLaunchKernelGGL(k_chsum_f16, dim3((unsigned)bnh_ceil_div((long long)B * C, 256)), dim3(256), 0, st,
-                       (const h16 *)out, o_ws, C, Ho, Wo, 3, chsum, cs_ws, B);
-    BNH_HIP(hipGetLastError());
+    if (chsum_launch<h16, 3>((const h16 *)out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st)) return -1;
   }
   return 0;
 }

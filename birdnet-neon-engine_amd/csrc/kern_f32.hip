@@ -15,17 +15,28 @@
 #include "bnh_expf.h"
 
 // ------------------------------------------------------------------ halo zeroing, any element size (4 or 2 bytes)
+// one thread per halo element: the 2h rows of Wp pixels above and below, then the 2h side pixels of each interior row
 template <typename T>
 __global__ void k_zero_halo(T *__restrict__ out, long long ws, int H, int W, int C, int h, long long total) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int Wp = W + 2 * h;
-  const long long per = (long long)(H + 2 * h) * Wp * C;
-  const int w = (int)(i / per);
-  const long long e = i % per, px = e / C;
-  const int y = (int)(px / Wp), x = (int)(px % Wp);
-  if (y >= h && y < H + h && x >= h && x < W + h) return;
-  out[w * ws + e] = (T)0;
+  const long long nh = 2LL * h * (Wp + H) * C;
+  const int win = (int)(i / nh);
+  const long long e = i % nh;
+  const int c = (int)(e % C);
+  const long long hp = e / C;
+  int y, x;
+  if (hp < 2LL * h * Wp) {
+    const int t = (int)(hp / Wp);
+    x = (int)(hp % Wp);
+    y = t < h ? t : H + t;
+  } else {
+    const int u = (int)(hp - 2LL * h * Wp), sd = u % (2 * h);
+    y = h + u / (2 * h);
+    x = sd < h ? sd : W + sd;
+  }
+  out[win * ws + ((long long)y * Wp + x) * C + c] = (T)0;
 }
 
 // ------------------------------------------------------------------ STEM
@@ -159,7 +170,7 @@ extern "C" {
 
 int bnh_zero_halo(void *xp, long long ws, int H, int W, int C, int h, int esz, int B, void *stream) {
   BNH_REQ(xp && H > 0 && W > 0 && C > 0 && h >= 0 && B > 0 && (esz == 4 || esz == 2));
-  const long long per = (long long)(H + 2 * h) * (W + 2 * h) * C, total = per * B;
+  const long long per = (long long)(H + 2 * h) * (W + 2 * h) * C, total = 2LL * h * (W + 2 * h + H) * C * B;
   BNH_REQ(B == 1 || ws >= per);
   if (!h) return 0;
   const dim3 grid((unsigned)bnh_ceil_div(total, 256));

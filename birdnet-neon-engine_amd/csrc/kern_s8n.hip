@@ -122,18 +122,99 @@ __global__ __launch_bounds__(256) void k_s8n_quant(const float *__restrict__ x, 
   }
 }
 
-// ------------------------------------------------------------------ zero halo of a padded output (rt_zero_halo)
-__global__ void k_zero_halo_f32(float *__restrict__ out, long long ws, int H, int W, int C, int h, long long total) {
-  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int Wp = W + 2 * h;
-  const long long per = (long long)(H + 2 * h) * Wp * C;
-  const int w = (int)(i / per);
-  const long long e = i % per;
-  const long long px = e / C;
-  const int y = (int)(px / Wp), xx = (int)(px % Wp);
-  if (y >= h && y < H + h && xx >= h && xx < W + h) return;
-  out[w * ws + e] = 0.f;
+// The same quantization with L lanes per row (L a power of two, 256 / L rows per block) and 16-byte loads, for rows
+// whose start is 16-byte aligned: each lane takes every L-th 4-element chunk, min / max meet in an L-lane butterfly.
+template <int L>
+__global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x, long long x_ws, int ld, int M, int K,
+                                                     int Kp, const float *__restrict__ gate, long long g_ws,
+                                                     int8_t *__restrict__ q, long long q_ws, float *__restrict__ sa,
+                                                     long long sa_ws, int32_t *__restrict__ za, long long za_ws,
+                                                     long long rows) {
+  const int sub = threadIdx.x % L;
+  const long long row0 = (long long)blockIdx.x * (256 / L) + threadIdx.x / L;
+  const bool valid = row0 < rows;
+  const long long row = valid ? row0 : rows - 1;  // every lane takes part in the butterfly
+  const int w = (int)(row / M), m = (int)(row % M);
+  const float *r = x + w * x_ws + (long long)m * ld;
+  const float *g = gate ? gate + w * g_ws : nullptr;
+  const int K4 = K & ~3, K8 = K & ~7, n4 = K4 / 4;
+  float lo = __builtin_inff(), hi = -__builtin_inff();
+  for (int c = sub; c < n4; c += L) {
+    float4 v = *(const float4 *)(r + 4 * c);
+    if (g) {
+      const float4 gv = *(const float4 *)(g + 4 * c);
+      v.x = v.x * gv.x; v.y = v.y * gv.y; v.z = v.z * gv.z; v.w = v.w * gv.w;
+    }
+    lo = bnh_fmin(bnh_fmin(lo, v.x), bnh_fmin(v.y, bnh_fmin(v.z, v.w)));
+    hi = bnh_fmax(bnh_fmax(hi, v.x), bnh_fmax(v.y, bnh_fmax(v.z, v.w)));
+  }
+#pragma unroll
+  for (int off = L / 2; off; off >>= 1) {
+    lo = bnh_fmin(lo, __shfl_xor(lo, off));
+    hi = bnh_fmax(hi, __shfl_xor(hi, off));
+  }
+  for (int k = K4; k < K; k++) {
+    float v = r[k];
+    if (g) v = v * g[k];
+    lo = bnh_fminnm(lo, v);
+    hi = bnh_fmaxnm(hi, v);
+  }
+  float inv, sc;
+  int32_t z;
+  const float range = hi - lo;
+  if (!(range > 1e-30f * bnh_fmaxnm(__builtin_fabsf(hi), __builtin_fabsf(lo))) || !(range > 0.f)) {
+    const float a = bnh_fmaxnm(__builtin_fabsf(hi), 1e-30f);
+    inv = 127.f / a;
+    z = 0;
+    sc = a / 127.f;
+  } else {
+    inv = 254.f / range;
+    z = (int32_t)((uint32_t)-127 - (uint32_t)bnh_lrintf_s32(lo * inv));
+    sc = range / 254.f;
+  }
+  if (!valid) return;
+  if (sub == 0) {
+    sa[w * sa_ws + m] = sc;
+    za[w * za_ws + m] = z;
+  }
+  int8_t *o = q + w * q_ws + (long long)m * Kp;
+  const uint32_t zb = (uint32_t)z & 0xffu;
+  for (int c = sub; c < Kp / 4; c += L) {
+    const int k0 = 4 * c;
+    float v[4];
+    if (k0 + 4 <= K4) {
+      float4 t = *(const float4 *)(r + k0);
+      if (g) {
+        const float4 gv = *(const float4 *)(g + k0);
+        t.x = t.x * gv.x; t.y = t.y * gv.y; t.z = t.z * gv.z; t.w = t.w * gv.w;
+      }
+      v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int k = k0 + j;
+        v[j] = 0.f;
+        if (k < K) {
+          v[j] = r[k];
+          if (g) v[j] = v[j] * g[k];
+        }
+      }
+    }
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int k = k0 + j;
+      uint32_t byte = zb;
+      if (k < K) {
+        const float t = v[j] * inv;
+        int32_t cq = (int32_t)((uint32_t)(k < K8 ? bnh_cvtn_s32(t) : bnh_lrintf_s32(t)) + (uint32_t)z);
+        cq = cq < -127 ? -127 : cq > 127 ? 127 : cq;
+        byte = (uint32_t)cq & 0xffu;
+      }
+      word |= byte << (8 * j);
+    }
+    *(uint32_t *)(o + k0) = word;
+  }
 }
 
 // ------------------------------------------------------------------ int8 GEMM + fp32 dequant epilogue
@@ -611,8 +692,29 @@ int bnh_s8n_quant_rows(const float *x, long long x_ws, int ld, int M, int K, int
   BNH_REQ(((uintptr_t)q & 3) == 0 && q_ws % 4 == 0 && (B == 1 || q_ws >= (long long)M * Kp));
   BNH_REQ(B == 1 || (x_ws >= (long long)(M - 1) * ld + K && sa_ws >= M && za_ws >= M));
   const long long rows = (long long)M * B;
-  hipLaunchKernelGGL(k_s8n_quant, dim3((unsigned)bnh_ceil_div(rows, 4)), dim3(256), 0, bnh_stream(stream), x, x_ws, ld,
-                     M, K, Kp, gate, gate_ws, q, q_ws, sa, sa_ws, za, za_ws, rows);
+  const bool vec = ((uintptr_t)x & 15) == 0 && ld % 4 == 0 && (B == 1 || x_ws % 4 == 0) &&
+                   (!gate || (((uintptr_t)gate & 15) == 0 && (B == 1 || gate_ws % 4 == 0)));
+  hipStream_t st = bnh_stream(stream);
+  if (!vec) {
+    hipLaunchKernelGGL(k_s8n_quant, dim3((unsigned)bnh_ceil_div(rows, 4)), dim3(256), 0, st, x, x_ws, ld, M, K, Kp,
+                       gate, gate_ws, q, q_ws, sa, sa_ws, za, za_ws, rows);
+  } else {
+    int L = 1;  // about four 16-byte chunks of a row per lane
+    while (L < 64 && 16 * L < Kp) L *= 2;
+#define QV(LL)                                                                                                         \
+  hipLaunchKernelGGL((k_s8n_quant_v<LL>), dim3((unsigned)bnh_ceil_div(rows, 256 / LL)), dim3(256), 0, st, x, x_ws, ld, \
+                     M, K, Kp, gate, gate_ws, q, q_ws, sa, sa_ws, za, za_ws, rows)
+    switch (L) {
+      case 1: QV(1); break;
+      case 2: QV(2); break;
+      case 4: QV(4); break;
+      case 8: QV(8); break;
+      case 16: QV(16); break;
+      case 32: QV(32); break;
+      default: QV(64); break;
+    }
+#undef QV
+  }
   BNH_HIP(hipGetLastError());
   return 0;
 }
@@ -653,11 +755,9 @@ int bnh_pw_s8(const float *in, long long in_ws, int lda, int M, const float *gat
   if (check_epi(e, M, W->Np, B)) return -1;
   if (e->opad) {
     const int H = M / e->ow, Wd = e->ow, h = e->opad;
-    const long long per = (long long)(H + 2 * h) * (Wd + 2 * h) * e->ldo, total = per * B;
+    const long long per = (long long)(H + 2 * h) * (Wd + 2 * h) * e->ldo;
     BNH_REQ(B == 1 || e->out_ws >= per);
-    hipLaunchKernelGGL(k_zero_halo_f32, dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, bnh_stream(stream),
-                       e->out, B == 1 ? per : e->out_ws, H, Wd, e->ldo, h, total);
-    BNH_HIP(hipGetLastError());
+    if (bnh_zero_halo(e->out, B == 1 ? per : e->out_ws, H, Wd, e->ldo, h, 4, B, stream)) return -1;
   }
   if (bnh_s8n_quant_rows(in, in_ws, lda, M, W->K, W->Kp, gate, gate_ws, q, q_ws, sa, sa_ws, za, za_ws, B, stream))
     return -1;

@@ -8,7 +8,7 @@ import pytest
 
 from bnneon import binding, perchnet
 
-import oracle_net
+import oracle_net  # oracle/oracle_net.py
 
 pytestmark = pytest.mark.gpu
 
