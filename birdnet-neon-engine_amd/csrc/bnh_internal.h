@@ -22,6 +22,11 @@ void bnh_clear_error(void);
     if (!(cond)) return bnh_fail("%s: parameter check failed: %s", __func__, #cond);           \
   } while (0)
 
+// the STEM kernel without the halo zeroing of bnh_stem_f32 (for outputs whose halo is known to be zero)
+extern "C" int bnh_stem_f32_body(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
+                      const float *bias, int Kp, int Np, int act, float *out, long long o_ws, int ldo, int opad, int B,
+                      void *stream);
+
 static inline hipStream_t bnh_stream(void *s) { return (hipStream_t)s; }
 static inline long long bnh_ceil_div(long long a, long long b) { return (a + b - 1) / b; }
 static inline long long bnh_round_up(long long a, long long b) { return bnh_ceil_div(a, b) * b; }

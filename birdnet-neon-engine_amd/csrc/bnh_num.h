@@ -103,22 +103,28 @@ BNH_DEV float bnh_frecps(float a, float b) {
 }
 
 // The fp32 SiLU of libbnneon's GEMM / depthwise epilogues (src/gemm_f32.h:102-118): exp2 by the magic-number split
-// and a degree-5 polynomial, t clamped to +-60, one FRECPE + FRECPS Newton step.
+// and a degree-5 polynomial, t clamped to +-60, one FRECPE + FRECPS Newton step. Because of the clamp, the divisor
+// d = 1 + 2^t lies in [1, 2^60 + 1] (finite, normal, positive) for every x that is not NaN, so FRECPE reduces to its
+// normal-operand case (exponent 253 - e, 8 fraction bits from the 9-bit estimate) and FRECPS to one fused
+// 2 - d r. A NaN x gives NaN through the final product x r whatever the clamp did with it (the reference's NaN
+// travels through d and r instead: the same NaN result, payloads aside).
 BNH_DEV float bnh_silu_f32(float x) {
   const float magic = 12582912.0f;
   float t = x * -1.44269504f;
-  t = bnh_fmin(bnh_fmax(t, -60.f), 60.f);
-  float tm = t + magic;
-  float f = t - (tm - magic);
-  uint32_t ni = bnh_bits(tm) << 23;
+  t = __builtin_fminf(__builtin_fmaxf(t, -60.f), 60.f);
+  const float tm = t + magic;
+  const float f = t - (tm - magic);
+  const uint32_t ni = bnh_bits(tm) << 23;
   float p = __builtin_fmaf(1.3333558e-3f, f, 9.6181291e-3f);
   p = __builtin_fmaf(p, f, 5.5504109e-2f);
   p = __builtin_fmaf(p, f, 2.4022651e-1f);
   p = __builtin_fmaf(p, f, 6.9314718e-1f);
   p = __builtin_fmaf(p, f, 1.0f);
-  float d = 1.f + bnh_float(bnh_bits(p) + ni);
-  float r = bnh_frecpe(d);
-  r = r * bnh_frecps(d, r);
+  const float d = 1.f + bnh_float(bnh_bits(p) + ni);
+  const uint32_t db = bnh_bits(d);
+  const int est = bnh_recip_estimate(256 | (int)((db >> 15) & 0xffu));
+  float r = bnh_float(((253u - (db >> 23)) << 23) | ((uint32_t)(est & 0xff) << 15));
+  r = r * __builtin_fmaf(-d, r, 2.f);
   return x * r;
 }
 // ReLU as vmaxq_f32(y, 0): -0 -> +0, NaN stays NaN

@@ -187,12 +187,20 @@ int bnh_zero_halo(void *xp, long long ws, int H, int W, int C, int h, int esz, i
 int bnh_stem_f32(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
                  const float *bias, int Kp, int Np, int act, float *out, long long o_ws, int ldo, int opad, int B,
                  void *stream) {
+  BNH_REQ(out && B > 0 && Ho > 0 && Wo > 0 && ldo > 0 && opad >= 0 && opad <= 3);
+  BNH_REQ(B == 1 || o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo);
+  if (opad && bnh_zero_halo(out, o_ws, Ho, Wo, ldo, opad, 4, B, stream)) return -1;
+  return bnh_stem_f32_body(img, i_ws, H, W, k, s, Ho, Wo, w, bias, Kp, Np, act, out, o_ws, ldo, opad, B, stream);
+}
+
+int bnh_stem_f32_body(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
+                      const float *bias, int Kp, int Np, int act, float *out, long long o_ws, int ldo, int opad, int B,
+                      void *stream) {
   BNH_REQ(img && w && bias && out && B > 0 && k >= 1 && s >= 1 && Ho > 0 && Wo > 0);
   BNH_REQ((Ho - 1) * s + k <= H && (Wo - 1) * s + k <= W && Kp >= k * k && Kp % 4 == 0 && Np % 8 == 0);
   BNH_REQ(ldo >= Np && opad >= 0 && opad <= 3 && act >= 0 && act <= 2 && ldo % 4 == 0);
   BNH_REQ(((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 3) == 0);
   BNH_REQ(B == 1 || (i_ws >= (long long)H * W && o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo));
-  if (opad && bnh_zero_halo(out, o_ws, Ho, Wo, ldo, opad, 4, B, stream)) return -1;
   const long long per = (long long)Ho * Wo * (Np / 4);
   hipLaunchKernelGGL(k_stem_f32, dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), dim3(256), 0, bnh_stream(stream),
                      img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, act, out, o_ws, ldo, opad);

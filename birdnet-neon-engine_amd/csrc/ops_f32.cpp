@@ -147,9 +147,12 @@ static int stem_init(rt_ctx *c, rt_op *op) {
 }
 static int stem_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
-  return bnh_stem_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[4], p[5], p[8], p[9], p[6], p[7],
-                      (const float *)dev_tn(op, 0), (const float *)dev_tn(op, 1), p[2], p[3], p[10],
-                      (float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[11], p[12], c->nwin, c->stream);
+  if (p[12] && !rt_halo_kept(c, op, 1) &&
+      bnh_zero_halo(rt_b(c, op, 1), rt_ws(c, op, 1), p[6], p[7], p[11], p[12], 4, c->nwin, c->stream))
+    return -1;
+  return bnh_stem_f32_body((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[4], p[5], p[8], p[9], p[6], p[7],
+                           (const float *)dev_tn(op, 0), (const float *)dev_tn(op, 1), p[2], p[3], p[10],
+                           (float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[11], p[12], c->nwin, c->stream);
 }
 
 // -------- SE / SE_GATE: SE b = [D [P][C], chsum]; SE_GATE b = [chsum, gate f32 [C]]; t = [w1 [rd][C], b1 [rd],

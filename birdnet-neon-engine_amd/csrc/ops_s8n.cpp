@@ -93,6 +93,15 @@ static int pw8_run(rt_ctx *c, rt_op *op) {
   bnh_epi32 e = {p[6], (float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[7], p[8], p[9], (const float *)rt_b(c, op, 2),
                  rt_ws(c, op, 2), p[10], r ? (int)r->halo : 0, r ? (int)r->W : 0};
   if (!e.opad) e.ow = 0;
+  if (e.opad && rt_halo_kept(c, op, 1)) {  // the halo is still zero from the arena: quantize and multiply only
+    if (bnh_s8n_quant_rows((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], p[1], p[2],
+                           gated ? (const float *)rt_b(c, op, 6) : nullptr, gated ? rt_ws(c, op, 6) : 0,
+                           (int8_t *)rt_b(c, op, 3), rt_ws(c, op, 3), (float *)rt_b(c, op, 4), rt_ws(c, op, 4),
+                           (int32_t *)rt_b(c, op, 5), rt_ws(c, op, 5), B, c->stream))
+      return -1;
+    return bnh_s8n_gemm((const int8_t *)rt_b(c, op, 3), rt_ws(c, op, 3), (const float *)rt_b(c, op, 4), rt_ws(c, op, 4),
+                        (const int32_t *)rt_b(c, op, 5), rt_ws(c, op, 5), p[4], B, s->W, &e, c->stream);
+  }
   return bnh_pw_s8((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4],
                    gated ? (const float *)rt_b(c, op, 6) : nullptr, gated ? rt_ws(c, op, 6) : 0, (int8_t *)rt_b(c, op, 3),
                    rt_ws(c, op, 3), (float *)rt_b(c, op, 4), rt_ws(c, op, 4), (int32_t *)rt_b(c, op, 5), rt_ws(c, op, 5), B,

@@ -64,6 +64,7 @@ struct rt_ctx {
   int bcap;              // windows the arena holds
   int nwin;              // windows of the current run (<= bcap): ops launch for this many
   size_t *slot_bytes;    // per slot: bytes of one window's copy (64-aligned, >= 64 bytes of zero slack)
+  int *slot_users;       // per slot: the number of buffers placed in it
   size_t arena_bytes;
   char *arena;           // device
   void **buf;            // device address of window 0 of each buffer
@@ -129,8 +130,10 @@ static inline long long rt_ws(const rt_ctx *c, const rt_op *op, int i) {
   return i >= op->nb || op->b[i] < 0 ? 0 : c->ws[op->b[i]];
 }
 void rt_free_state(rt_op *op);
-// zero the halo of a padded activation [H + 2h][W + 2h][C] of esz-byte elements, in every window
-int rt_zero_halo_dev(rt_ctx *c, void *xp, long long ws, int H, int W, int C, int h, size_t esz, int B);
+// 1 when buffer argument i has a halo that stays zero between runs: its memory slot holds no other buffer and it is
+// not the path's input (the arena is zeroed when allocated and no kernel writes a halo), so its producer need not
+// zero the halo again; 0 otherwise
+int rt_halo_kept(const rt_ctx *c, const rt_op *op, int i);
 
 // opcodes (the reference's numbering, src/rt.h:170-208; append only)
 enum {

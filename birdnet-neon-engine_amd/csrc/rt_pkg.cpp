@@ -387,7 +387,8 @@ rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
   c->buf = (void **)calloc(d->n_buf, sizeof(void *));
   c->ws = (long long *)calloc(d->n_buf, sizeof(long long));
   c->slot_bytes = (size_t *)calloc(d->n_buf, sizeof(size_t));
-  if (!c->bufd || !c->buf || !c->ws || !c->slot_bytes) { KIND(RT_E_OOM); FAIL("out of memory (%u buffer descriptors)", d->n_buf); }
+  c->slot_users = (int *)calloc(d->n_buf, sizeof(int));
+  if (!c->bufd || !c->buf || !c->ws || !c->slot_bytes || !c->slot_users) { KIND(RT_E_OOM); FAIL("out of memory (%u buffer descriptors)", d->n_buf); }
   memcpy(c->bufd, m + d->buf_off, sizeof(rt_bufdesc) * d->n_buf);
   for (uint32_t i = 0; i < d->n_buf; i++) {
     const rt_bufdesc *b = &c->bufd[i];
@@ -398,6 +399,7 @@ rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
       FAIL("path %.24s buffer #%u shares the input window's memory slot %u; " HINT_PKG, d->name, i, b->slot);
     size_t bytes = ((size_t)b->elems * rt_dsize(b->dtype) + 64 + 63) & ~(size_t)63;
     if (bytes > c->slot_bytes[b->slot]) c->slot_bytes[b->slot] = bytes;
+    c->slot_users[b->slot]++;
   }
   for (uint32_t s = 0; s < d->n_buf; s++) {
     total += c->slot_bytes[s];
@@ -542,6 +544,12 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
   return nf;
 }
 
+int rt_halo_kept(const rt_ctx *c, const rt_op *op, int i) {
+  if (i >= op->nb || op->b[i] < 0 || (uint32_t)op->b[i] == c->path->in_buf) return 0;
+  const rt_bufdesc *d = &c->bufd[op->b[i]];
+  return d->halo > 0 && d->slot < (uint32_t)c->n_buf && c->slot_users[d->slot] == 1;
+}
+
 void rt_ctx_free(rt_ctx *c) {
   if (!c) return;
   if (c->stream) hipStreamSynchronize(c->stream);
@@ -567,6 +575,7 @@ void rt_ctx_free(rt_ctx *c) {
   free(c->buf);
   free(c->ws);
   free(c->slot_bytes);
+  free(c->slot_users);
   free(c->bufd);
   if (c->stream && c->own_stream) hipStreamDestroy(c->stream);
   free(c);

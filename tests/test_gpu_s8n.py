@@ -69,6 +69,19 @@ def test_silu_relu_bit_exact(hip, f):
     assert same_f32(run_eval(hip, f, x), O.eval_f32(f, x))
 
 
+def test_silu_dense(hip):
+    """every 16th float of both signs with |x| in [2^-27, 2^34) (past +-41.6 the clamp saturates), all NaN forms
+    and infinities: the epilogue SiLU's divisor covers its whole range."""
+    e = np.arange(100, 161, dtype=np.uint32)
+    m = np.arange(0, 2 ** 23, 16, dtype=np.uint32)
+    bits = (e[:, None] << np.uint32(23)) | m[None, :]
+    bits = np.concatenate([bits.ravel(), bits.ravel() | np.uint32(0x80000000),
+                           np.array([0x7f800000, 0xff800000, 0x7fc00000, 0xffc00001, 0x7f800001], np.uint32)])
+    x = bits.view(np.float32)
+    say("silu dense", x.size)
+    assert same_f32(run_eval(hip, 1, x), O.eval_f32(1, x))
+
+
 def quant_case(hip, x, K, Kp, gate=None, B=1):
     """x [B][M][ld]; returns True when q, sa, za match the oracle."""
     H = hip
