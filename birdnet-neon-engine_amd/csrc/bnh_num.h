@@ -127,6 +127,22 @@ BNH_DEV float bnh_silu_f32(float x) {
   r = r * __builtin_fmaf(-d, r, 2.f);
   return x * r;
 }
+// n / d for 0 <= n < 2^52 and 1 <= d < 2^31, given rd = 1.0 / d: the double product is within 2^-21 of n / d, so
+// its truncation is off by at most one, which one remainder test corrects
+BNH_DEV int bnh_div(long long n, int d, double rd) {
+  int q = (int)((double)n * rd);
+  const long long r = n - (long long)q * d;
+  if (r < 0) q--;
+  else if (r >= d) q++;
+  return q;
+}
+// The logical index of hardware block b of a 1-D grid of n blocks. The hardware places block b on XCD b % 8; this
+// gives the blocks of one XCD one contiguous range of logical indices, so that work on neighbouring data (the rows a
+// stencil shares) runs under one XCD's L2.
+BNH_DEV unsigned bnh_xcd_block(unsigned b, unsigned n) {
+  const unsigned q = n / 8, r = n % 8, x = b % 8;
+  return x * q + (x < r ? x : r) + b / 8;
+}
 // ReLU as vmaxq_f32(y, 0): -0 -> +0, NaN stays NaN
 BNH_DEV float bnh_relu_f32(float y) { return bnh_fmax(y, 0.f); }
 

@@ -45,6 +45,34 @@ static int items_per_row(int Wo, int form) {
   return ng + ((t & 2) ? 1 : 0) + (t & 1);
 }
 
+// ------------------------------------------------------------------ the grid
+// A window's output row holds nitems x C (item, channel) threads in gx blocks of 256; blocks are taken in
+// (window, row, chunk) order after the XCD remap, so one XCD walks consecutive rows of a window and finds the input
+// rows they share in its L2.
+struct DwGrid { int gx; double rC, rgx, rHo; };
+struct DwPos { int c, it, oy, win; bool ok; };
+BNH_DEV DwPos dw_pos(int C, double rC, int nitems, int gx, double rgx, int Ho, double rHo) {
+  const unsigned lb = bnh_xcd_block(blockIdx.x, gridDim.x);
+  const int rowid = bnh_div(lb, gx, rgx), xch = (int)lb - rowid * gx;
+  const int i = xch * 256 + (int)threadIdx.x;
+  DwPos p;
+  p.it = bnh_div(i, C, rC);
+  p.c = i - p.it * C;
+  p.win = bnh_div(rowid, Ho, rHo);
+  p.oy = rowid - p.win * Ho;
+  p.ok = p.it < nitems;
+  return p;
+}
+static int dw_grid(int nitems, int C, int Ho, int B, unsigned *blocks, DwGrid *g) {
+  g->gx = (int)bnh_ceil_div((long long)nitems * C, 256);
+  g->rC = 1.0 / C;
+  g->rgx = 1.0 / g->gx;
+  g->rHo = 1.0 / Ho;
+  BNH_REQ((long long)B * Ho * g->gx < (1LL << 31));
+  *blocks = (unsigned)((long long)B * Ho * g->gx);
+  return 0;
+}
+
 // ------------------------------------------------------------------ fp32 DWK (form 0) and DW3 (form 2)
 // DWK: input row oy*s - pt + h + ky, column px*s - pl + h + kx of the halo-h input. DW3: the reference's three column
 // partial sums, rows oy*s + ky, columns px*s + kx of the halo-1 input (pads 1), SiLU always.
@@ -52,15 +80,10 @@ template <int K, int S, int FORM>
 __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, long long x_ws, int Wp, int C, int pt,
                                                 int pl, const float *__restrict__ w, const float *__restrict__ b,
                                                 int act, float *__restrict__ out, long long o_ws, int Ho, int Wo,
-                                                int nitems, long long total) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int c = (int)(i % C);
-  long long r = i / C;
-  const int it = (int)(r % nitems);
-  r /= nitems;
-  const int oy = (int)(r % Ho);
-  const int win = (int)(r / Ho);
+                                                int nitems, DwGrid g) {
+  const DwPos ps = dw_pos(C, g.rC, nitems, g.gx, g.rgx, Ho, g.rHo);
+  if (!ps.ok) return;
+  const int c = ps.c, it = ps.it, oy = ps.oy, win = ps.win;
   const Item item = item_of(it, Wo, FORM);
   constexpr int H = (K - 1) / 2;
   const int iy0 = FORM == 2 ? oy * S : oy * S - pt + H;
@@ -116,15 +139,10 @@ template <int K, int S, int FORM>
 __global__ __launch_bounds__(256) void k_dw_f16(const h16 *__restrict__ xp, long long x_ws, int Wp, int C, int pt,
                                                 int pl, const h16 *__restrict__ w, const h16 *__restrict__ b, int act,
                                                 h16 *__restrict__ out, long long o_ws, int Ho, int Wo, int nitems,
-                                                long long total) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int c = (int)(i % C);
-  long long r = i / C;
-  const int it = (int)(r % nitems);
-  r /= nitems;
-  const int oy = (int)(r % Ho);
-  const int win = (int)(r / Ho);
+                                                DwGrid g) {
+  const DwPos ps = dw_pos(C, g.rC, nitems, g.gx, g.rgx, Ho, g.rHo);
+  if (!ps.ok) return;
+  const int c = ps.c, it = ps.it, oy = ps.oy, win = ps.win;
   const Item item = item_of(it, Wo, FORM);
   constexpr int H = (K - 1) / 2;
   const int iy0 = FORM == 2 ? oy * S - pt + 1 : oy * S - pt + H;
@@ -449,12 +467,14 @@ int bnh_dwk_f32(const float *xp, long long x_ws, int H, int W, int C, int k, int
   BNH_REQ(xp && w && b && out && (act == 0 || act == 1));
   if (dw_check(H, W, C, k, s, pt, pl, Ho, Wo, B, x_ws, o_ws, (k - 1) / 2)) return -1;
   const int nit = items_per_row(Wo, 0);
-  const long long total = (long long)B * Ho * nit * C;
+  unsigned nb;
+  DwGrid g;
+  if (dw_grid(nit, C, Ho, B, &nb, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   const int Wp = W + k - 1;
   dispatch_ks<float>(k, s, [&]<int K, int S>() {
-    hipLaunchKernelGGL((k_dw_f32<K, S, 0>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, xp, x_ws, Wp, C,
-                       pt, pl, w, b, act, out, o_ws, Ho, Wo, nit, total);
+    hipLaunchKernelGGL((k_dw_f32<K, S, 0>), dim3(nb), dim3(256), 0, st, xp, x_ws, Wp, C, pt, pl, w, b, act, out, o_ws,
+                       Ho, Wo, nit, g);
   });
   BNH_HIP(hipGetLastError());
   if (chsum) {
@@ -469,14 +489,16 @@ int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, con
   BNH_REQ(xp && w && b && out);
   if (dw_check(H, W, C, 3, s, 1, 1, Ho, Wo, B, x_ws, o_ws, 1)) return -1;
   const int nit = items_per_row(Wo, 2);
-  const long long total = (long long)B * Ho * nit * C;
+  unsigned nb;
+  DwGrid g;
+  if (dw_grid(nit, C, Ho, B, &nb, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   if (s == 1)
-    hipLaunchKernelGGL((k_dw_f32<3, 1, 2>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, xp, x_ws, W + 2,
-                       C, 1, 1, w, b, 1, out, o_ws, Ho, Wo, nit, total);
+    hipLaunchKernelGGL((k_dw_f32<3, 1, 2>), dim3(nb), dim3(256), 0, st, xp, x_ws, W + 2, C, 1, 1, w, b, 1, out, o_ws,
+                       Ho, Wo, nit, g);
   else
-    hipLaunchKernelGGL((k_dw_f32<3, 2, 2>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, xp, x_ws, W + 2,
-                       C, 1, 1, w, b, 1, out, o_ws, Ho, Wo, nit, total);
+    hipLaunchKernelGGL((k_dw_f32<3, 2, 2>), dim3(nb), dim3(256), 0, st, xp, x_ws, W + 2, C, 1, 1, w, b, 1, out, o_ws,
+                       Ho, Wo, nit, g);
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);
@@ -491,13 +513,14 @@ int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, 
   BNH_REQ(xp && w && b && out && (act == 0 || act == 1));
   if (dw_check(H, W, C, k, s, pt, pl, Ho, Wo, B, x_ws, o_ws, (k - 1) / 2)) return -1;
   const int nit = items_per_row(Wo, 1);
-  const long long total = (long long)B * Ho * nit * C;
+  unsigned nb;
+  DwGrid g;
+  if (dw_grid(nit, C, Ho, B, &nb, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   const int Wp = W + k - 1;
   dispatch_ks<h16>(k, s, [&]<int K, int S>() {
-    hipLaunchKernelGGL((k_dw_f16<K, S, 1>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st,
-                       (const h16 *)xp, x_ws, Wp, C, pt, pl, (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, Ho,
-                       Wo, nit, total);
+    hipLaunchKernelGGL((k_dw_f16<K, S, 1>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, Wp, C, pt, pl,
+                       (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, Ho, Wo, nit, g);
   });
   BNH_HIP(hipGetLastError());
   if (chsum) {
@@ -513,14 +536,16 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
   BNH_REQ(xp && w && b && out && pt >= 0 && pt <= 1 && pl >= 0 && pl <= 1);
   if (dw_check(H, W, C, 3, s, pt, pl, Ho, Wo, B, x_ws, o_ws, 1)) return -1;
   const int nit = items_per_row(Wo, 2);
-  const long long total = (long long)B * Ho * nit * C;
+  unsigned nb;
+  DwGrid g;
+  if (dw_grid(nit, C, Ho, B, &nb, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   if (s == 1)
-    hipLaunchKernelGGL((k_dw_f16<3, 1, 2>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, (const h16 *)xp,
-                       x_ws, W + 2, C, pt, pl, (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total);
+    hipLaunchKernelGGL((k_dw_f16<3, 1, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,
+                       (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, g);
   else
-    hipLaunchKernelGGL((k_dw_f16<3, 2, 2>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, (const h16 *)xp,
-                       x_ws, W + 2, C, pt, pl, (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total);
+    hipLaunchKernelGGL((k_dw_f16<3, 2, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,
+                       (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, g);
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);

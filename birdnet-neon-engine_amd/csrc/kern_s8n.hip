@@ -42,11 +42,14 @@ struct EpiDev {  // the fp32 epilogue, by value into the kernel
   const float *res;
   long long res_ws;
   int ldr, rpad, rw;
+  double r_ow, r_rw;  // 1 / ow, 1 / rw (padded row arithmetic)
 };
 
-BNH_DEV long long epi_orow(int m, int ow, int opad) {
+// the padded row of pixel m (ow pixels per image row, halo opad)
+BNH_DEV long long epi_prow(int m, int ow, int opad, double r_ow) {
   if (!opad) return m;
-  return (long long)((m / ow) + opad) * (ow + 2 * opad) + (m % ow) + opad;
+  const int y = bnh_div(m, ow, r_ow);
+  return (long long)(y + opad) * (ow + 2 * opad) + (m - y * ow) + opad;
 }
 
 // ------------------------------------------------------------------ per-row quantization (s8n_quant_rows)
@@ -129,12 +132,12 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
                                                      int Kp, const float *__restrict__ gate, long long g_ws,
                                                      int8_t *__restrict__ q, long long q_ws, float *__restrict__ sa,
                                                      long long sa_ws, int32_t *__restrict__ za, long long za_ws,
-                                                     long long rows) {
+                                                     long long rows, double rM) {
   const int sub = threadIdx.x % L;
   const long long row0 = (long long)blockIdx.x * (256 / L) + threadIdx.x / L;
   const bool valid = row0 < rows;
   const long long row = valid ? row0 : rows - 1;  // every lane takes part in the butterfly
-  const int w = (int)(row / M), m = (int)(row % M);
+  const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
   const float *r = x + w * x_ws + (long long)m * ld;
   const float *g = gate ? gate + w * g_ws : nullptr;
   const int K4 = K & ~3, K8 = K & ~7, n4 = K4 / 4;
@@ -218,27 +221,40 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
 }
 
 // ------------------------------------------------------------------ int8 GEMM + fp32 dequant epilogue
+// A block owns WM * 32 rows (pixels of consecutive windows) x WN * 64 channels; its threads first resolve each row's
+// window, pixel, quantisation parameters and output / residual addresses into LDS (once per row), then every wave
+// runs 32 rows x 64 channels of i8 MFMAs and the reference's epilogue from those.
 template <int WM, int WN>
 __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, long long q_ws,
                                                   const float *__restrict__ sa, long long sa_ws,
-                                                  const int32_t *__restrict__ za, long long za_ws, int M, long long rows,
-                                                  const int8_t *__restrict__ wt, const float *__restrict__ sw,
-                                                  const int32_t *__restrict__ cs, const float *__restrict__ bias,
-                                                  int Kp, int Np, EpiDev e) {
+                                                  const int32_t *__restrict__ za, long long za_ws, int M, double rM,
+                                                  long long rows, const int8_t *__restrict__ wt,
+                                                  const float *__restrict__ sw, const int32_t *__restrict__ cs,
+                                                  const float *__restrict__ bias, int Kp, int Np, EpiDev e) {
+  constexpr int RB = WM * 32;
+  __shared__ long long s_q[RB], s_o[RB], s_r[RB];
+  __shared__ float s_sa[RB];
+  __shared__ uint32_t s_z[RB];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const long long row0 = (long long)blockIdx.x * (WM * 32) + wm * 32;
+  const long long rowB = (long long)blockIdx.x * RB;
+  for (int i = threadIdx.x; i < RB; i += 256) {
+    const long long row = rowB + i < rows ? rowB + i : rows - 1;  // rows past the end repeat the last row
+    const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
+    s_q[i] = w * q_ws + (long long)m * Kp;
+    s_o[i] = w * e.out_ws + epi_prow(m, e.ow, e.opad, e.r_ow) * e.ldo;
+    s_r[i] = e.res ? w * e.res_ws + epi_prow(m, e.rw, e.rpad, e.r_rw) * e.ldr : 0;
+    s_sa[i] = sa[w * sa_ws + m];
+    s_z[i] = (uint32_t)za[w * za_ws + m];
+  }
+  __syncthreads();
+  const int lr0 = wm * 32;  // the wave's first row within the block
+  if (rowB + lr0 >= rows) return;
   const int n0 = blockIdx.y * (WN * 64) + wn * 64;
-  if (row0 >= rows) return;
   const int kc = (lane >> 4) * 16;  // this lane's k chunk within a 64-wide step
   const int8_t *ap[2];
 #pragma unroll
-  for (int t = 0; t < 2; t++) {
-    long long r = row0 + 16 * t + (lane & 15);
-    if (r >= rows) r = rows - 1;  // a valid row; its sums are discarded
-    const int w = (int)(r / M), m = (int)(r % M);
-    ap[t] = q + w * q_ws + (long long)m * Kp + kc;
-  }
+  for (int t = 0; t < 2; t++) ap[t] = q + s_q[lr0 + 16 * t + (lane & 15)] + kc;
   const int8_t *bp = wt + (long long)(n0 + (lane & 15)) * Kp + kc;
   v4i acc[2][4];
 #pragma unroll
@@ -284,13 +300,12 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
   for (int t = 0; t < 2; t++)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const long long row = row0 + 16 * t + 4 * (lane >> 4) + r;
-      if (row >= rows) continue;
-      const int w = (int)(row / M), m = (int)(row % M);
-      const float s_a = sa[w * sa_ws + m];
-      const uint32_t z = (uint32_t)za[w * za_ws + m];
-      float *orow = e.out + w * e.out_ws + epi_orow(m, e.ow, e.opad) * e.ldo;
-      const float *rrow = e.res ? e.res + w * e.res_ws + epi_orow(m, e.rw, e.rpad) * e.ldr : nullptr;
+      const int lr = lr0 + 16 * t + 4 * (lane >> 4) + r;
+      if (rowB + lr >= rows) continue;
+      const float s_a = s_sa[lr];
+      const uint32_t z = s_z[lr];
+      float *orow = e.out + s_o[lr];
+      const float *rrow = e.res ? e.res + s_r[lr] : nullptr;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const int n = n0 + 16 * j + (lane & 15);
@@ -703,7 +718,7 @@ int bnh_s8n_quant_rows(const float *x, long long x_ws, int ld, int M, int K, int
     while (L < 64 && 16 * L < Kp) L *= 2;
 #define QV(LL)                                                                                                         \
   hipLaunchKernelGGL((k_s8n_quant_v<LL>), dim3((unsigned)bnh_ceil_div(rows, 256 / LL)), dim3(256), 0, st, x, x_ws, ld, \
-                     M, K, Kp, gate, gate_ws, q, q_ws, sa, sa_ws, za, za_ws, rows)
+                     M, K, Kp, gate, gate_ws, q, q_ws, sa, sa_ws, za, za_ws, rows, 1.0 / M)
     switch (L) {
       case 1: QV(1); break;
       case 2: QV(2); break;
@@ -733,16 +748,18 @@ int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, long long sa_
   BNH_REQ(((uintptr_t)q & 15) == 0 && q_ws % 16 == 0);
   if (check_epi(e, M, W->Np, B)) return -1;
   const long long rows = (long long)M * B;
-  EpiDev d = {e->act, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->res, e->res_ws, e->ldr, e->rpad, e->rw};
+  EpiDev d = {e->act, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->res, e->res_ws, e->ldr, e->rpad, e->rw,
+              e->opad ? 1.0 / e->ow : 0.0, e->rpad ? 1.0 / e->rw : 0.0};
   hipStream_t s = bnh_stream(stream);
+  const double rM = 1.0 / M;
   if (W->Np > 64) {
     dim3 grid((unsigned)bnh_ceil_div(rows, 64), (unsigned)bnh_ceil_div(W->Np, 128));
-    hipLaunchKernelGGL((k_s8n_gemm<2, 2>), grid, dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rows, W->w, W->sw,
-                       W->colsum, W->b, W->Kp, W->Np, d);
+    hipLaunchKernelGGL((k_s8n_gemm<2, 2>), grid, dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rM, rows, W->w,
+                       W->sw, W->colsum, W->b, W->Kp, W->Np, d);
   } else {
     dim3 grid((unsigned)bnh_ceil_div(rows, 128), 1);
-    hipLaunchKernelGGL((k_s8n_gemm<4, 1>), grid, dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rows, W->w, W->sw,
-                       W->colsum, W->b, W->Kp, W->Np, d);
+    hipLaunchKernelGGL((k_s8n_gemm<4, 1>), grid, dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rM, rows, W->w,
+                       W->sw, W->colsum, W->b, W->Kp, W->Np, d);
   }
   BNH_HIP(hipGetLastError());
   return 0;
