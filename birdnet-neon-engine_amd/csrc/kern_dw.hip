@@ -46,30 +46,36 @@ static int items_per_row(int Wo, int form) {
 }
 
 // ------------------------------------------------------------------ the grid
-// A window's output row holds nitems x C (item, channel) threads in gx blocks of 256; blocks are taken in
-// (window, row, chunk) order after the XCD remap, so one XCD walks consecutive rows of a window and finds the input
-// rows they share in its L2.
-struct DwGrid { int gx; double rC, rgx, rHo; };
-struct DwPos { int c, it, oy, win; bool ok; };
-BNH_DEV DwPos dw_pos(int C, double rC, int nitems, int gx, double rgx, int Ho, double rHo) {
+// A thread owns DW_NI consecutive items of one output row and one channel (weights loaded once, input columns shared
+// between neighbouring items reused from registers). Threads are numbered (window, row, strip, channel) across the
+// whole grid, and blocks are taken in that order after the XCD remap, so one XCD walks consecutive rows of a window
+// and finds the input rows they share in its L2.
+#define DW_NI 4
+struct DwGrid { int ns; double rC, rnc, rHo; };  // strips per row; 1 / C, 1 / (ns C), 1 / Ho
+struct DwPos { int c, it0, oy, win; bool ok; };
+BNH_DEV DwPos dw_pos(int C, int Ho, long long total, DwGrid g) {
   const unsigned lb = bnh_xcd_block(blockIdx.x, gridDim.x);
-  const int rowid = bnh_div(lb, gx, rgx), xch = (int)lb - rowid * gx;
-  const int i = xch * 256 + (int)threadIdx.x;
+  const long long i = (long long)lb * 256 + threadIdx.x;
   DwPos p;
-  p.it = bnh_div(i, C, rC);
-  p.c = i - p.it * C;
-  p.win = bnh_div(rowid, Ho, rHo);
+  p.ok = i < total;
+  const long long ii = p.ok ? i : 0;
+  const int nc = g.ns * C;
+  const int rowid = bnh_div(ii, nc, g.rnc), rem = (int)(ii - (long long)rowid * nc);
+  const int strip = bnh_div(rem, C, g.rC);
+  p.c = rem - strip * C;
+  p.it0 = strip * DW_NI;
+  p.win = bnh_div(rowid, Ho, g.rHo);
   p.oy = rowid - p.win * Ho;
-  p.ok = p.it < nitems;
   return p;
 }
-static int dw_grid(int nitems, int C, int Ho, int B, unsigned *blocks, DwGrid *g) {
-  g->gx = (int)bnh_ceil_div((long long)nitems * C, 256);
+static int dw_grid(int nitems, int C, int Ho, int B, unsigned *blocks, long long *total, DwGrid *g) {
+  g->ns = (nitems + DW_NI - 1) / DW_NI;
   g->rC = 1.0 / C;
-  g->rgx = 1.0 / g->gx;
+  g->rnc = 1.0 / ((double)g->ns * C);
   g->rHo = 1.0 / Ho;
-  BNH_REQ((long long)B * Ho * g->gx < (1LL << 31));
-  *blocks = (unsigned)((long long)B * Ho * g->gx);
+  *total = (long long)B * Ho * g->ns * C;
+  BNH_REQ(bnh_ceil_div(*total, 256) < (1LL << 31));
+  *blocks = (unsigned)bnh_ceil_div(*total, 256);
   return 0;
 }
 
@@ -80,58 +86,65 @@ template <int K, int S, int FORM>
 __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, long long x_ws, int Wp, int C, int pt,
                                                 int pl, const float *__restrict__ w, const float *__restrict__ b,
                                                 int act, float *__restrict__ out, long long o_ws, int Ho, int Wo,
-                                                int nitems, DwGrid g) {
-  const DwPos ps = dw_pos(C, g.rC, nitems, g.gx, g.rgx, Ho, g.rHo);
+                                                int nitems, long long total, DwGrid g) {
+  const DwPos ps = dw_pos(C, Ho, total, g);
   if (!ps.ok) return;
-  const int c = ps.c, it = ps.it, oy = ps.oy, win = ps.win;
-  const Item item = item_of(it, Wo, FORM);
+  const int c = ps.c, oy = ps.oy, win = ps.win;
   constexpr int H = (K - 1) / 2;
   const int iy0 = FORM == 2 ? oy * S : oy * S - pt + H;
-  const int ix0 = FORM == 2 ? item.px * S : item.px * S - pl + H;
-  const float *x0 = xp + win * x_ws + ((long long)iy0 * Wp + ix0) * C + c;
   float wv[K * K];
 #pragma unroll
   for (int t = 0; t < K * K; t++) wv[t] = w[(long long)t * C + c];
   const float bias = b[c];
-  float v[4];
+  const float *xw = xp + win * x_ws + (long long)iy0 * Wp * C + c;
+  float *ow = out + win * o_ws + (long long)oy * Wo * C + c;
 #pragma unroll
-  for (int q = 0; q < 4; q++) v[q] = 0.f;
+  for (int j = 0; j < DW_NI; j++) {
+    const int it = ps.it0 + j;
+    if (it >= nitems) break;
+    const Item item = item_of(it, Wo, FORM);
+    const int ix0 = FORM == 2 ? item.px * S : item.px * S - pl + H;
+    const float *x0 = xw + (long long)ix0 * C;
+    float v[4];
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    if (q >= item.n) break;
-    if (FORM == 2) {
-      const float *p0 = x0 + (long long)q * S * C;
-      const long long r1 = (long long)Wp * C, r2 = 2 * r1;
-      float acc = __builtin_fmaf(wv[0], p0[0], bias);
-      float acb = wv[1] * p0[C];
-      float acd = wv[2] * p0[2 * C];
-      acc = __builtin_fmaf(wv[3], p0[r1], acc);
-      acb = __builtin_fmaf(wv[4], p0[r1 + C], acb);
-      acd = __builtin_fmaf(wv[5], p0[r1 + 2 * C], acd);
-      acc = __builtin_fmaf(wv[6], p0[r2], acc);
-      acb = __builtin_fmaf(wv[7], p0[r2 + C], acb);
-      acd = __builtin_fmaf(wv[8], p0[r2 + 2 * C], acd);
-      v[q] = bnh_silu_f32(acc + (acb + acd));
-    } else {
-      float a = bias, e = 0.f;
+    for (int q = 0; q < 4; q++) v[q] = 0.f;
 #pragma unroll
-      for (int ky = 0; ky < K; ky++)
+    for (int q = 0; q < 4; q++) {
+      if (q >= item.n) break;
+      if (FORM == 2) {
+        const float *p0 = x0 + (long long)q * S * C;
+        const long long r1 = (long long)Wp * C, r2 = 2 * r1;
+        float acc = __builtin_fmaf(wv[0], p0[0], bias);
+        float acb = wv[1] * p0[C];
+        float acd = wv[2] * p0[2 * C];
+        acc = __builtin_fmaf(wv[3], p0[r1], acc);
+        acb = __builtin_fmaf(wv[4], p0[r1 + C], acb);
+        acd = __builtin_fmaf(wv[5], p0[r1 + 2 * C], acd);
+        acc = __builtin_fmaf(wv[6], p0[r2], acc);
+        acb = __builtin_fmaf(wv[7], p0[r2 + C], acb);
+        acd = __builtin_fmaf(wv[8], p0[r2 + 2 * C], acd);
+        v[q] = bnh_silu_f32(acc + (acb + acd));
+      } else {
+        float a = bias, e = 0.f;
 #pragma unroll
-        for (int kx = 0; kx < K; kx++) {
-          const int t = ky * K + kx;
-          const float xv = x0[((long long)ky * Wp + q * S + kx) * C];
-          if (item.split && (t & 1)) e = __builtin_fmaf(xv, wv[t], e);
-          else a = __builtin_fmaf(xv, wv[t], a);
-        }
-      float y = item.split ? a + e : a;
-      if (act == 1) y = bnh_silu_f32(y);
-      v[q] = y;
+        for (int ky = 0; ky < K; ky++)
+#pragma unroll
+          for (int kx = 0; kx < K; kx++) {
+            const int t = ky * K + kx;
+            const float xv = x0[((long long)ky * Wp + q * S + kx) * C];
+            if (item.split && (t & 1)) e = __builtin_fmaf(xv, wv[t], e);
+            else a = __builtin_fmaf(xv, wv[t], a);
+          }
+        float y = item.split ? a + e : a;
+        if (act == 1) y = bnh_silu_f32(y);
+        v[q] = y;
+      }
     }
-  }
-  float *o = out + win * o_ws + ((long long)oy * Wo + item.px) * C + c;
+    float *o = ow + (long long)item.px * C;
 #pragma unroll
-  for (int q = 0; q < 4; q++)
-    if (q < item.n) o[(long long)q * C] = v[q];
+    for (int q = 0; q < 4; q++)
+      if (q < item.n) o[(long long)q * C] = v[q];
+  }
 }
 
 // ------------------------------------------------------------------ fp16 DWK (form 1) and DW3 (form 2)
@@ -139,57 +152,64 @@ template <int K, int S, int FORM>
 __global__ __launch_bounds__(256) void k_dw_f16(const h16 *__restrict__ xp, long long x_ws, int Wp, int C, int pt,
                                                 int pl, const h16 *__restrict__ w, const h16 *__restrict__ b, int act,
                                                 h16 *__restrict__ out, long long o_ws, int Ho, int Wo, int nitems,
-                                                DwGrid g) {
-  const DwPos ps = dw_pos(C, g.rC, nitems, g.gx, g.rgx, Ho, g.rHo);
+                                                long long total, DwGrid g) {
+  const DwPos ps = dw_pos(C, Ho, total, g);
   if (!ps.ok) return;
-  const int c = ps.c, it = ps.it, oy = ps.oy, win = ps.win;
-  const Item item = item_of(it, Wo, FORM);
+  const int c = ps.c, oy = ps.oy, win = ps.win;
   constexpr int H = (K - 1) / 2;
   const int iy0 = FORM == 2 ? oy * S - pt + 1 : oy * S - pt + H;
-  const int ix0 = FORM == 2 ? item.px * S - pl + 1 : item.px * S - pl + H;
-  const h16 *x0 = xp + win * x_ws + ((long long)iy0 * Wp + ix0) * C + c;
   h16 wv[K * K];
 #pragma unroll
   for (int t = 0; t < K * K; t++) wv[t] = w[(long long)t * C + c];
   const h16 bias = b[c];
-  h16 v[4];
+  const h16 *xw = xp + win * x_ws + (long long)iy0 * Wp * C + c;
+  h16 *ow = out + win * o_ws + (long long)oy * Wo * C + c;
 #pragma unroll
-  for (int q = 0; q < 4; q++) v[q] = (h16)0.0f;
+  for (int j = 0; j < DW_NI; j++) {
+    const int it = ps.it0 + j;
+    if (it >= nitems) break;
+    const Item item = item_of(it, Wo, FORM);
+    const int ix0 = FORM == 2 ? item.px * S - pl + 1 : item.px * S - pl + H;
+    const h16 *x0 = xw + (long long)ix0 * C;
+    h16 v[4];
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    if (q >= item.n) break;
-    if (FORM == 2) {
-      const h16 *r0 = x0 + (long long)q * S * C, *r1 = r0 + (long long)Wp * C, *r2 = r1 + (long long)Wp * C;
-      h16 a = hfma(r0[0], wv[0], bias);
-      h16 a2 = r0[C] * wv[1];
-      a = hfma(r0[2 * C], wv[2], a);
-      a2 = hfma(r1[0], wv[3], a2);
-      a = hfma(r1[C], wv[4], a);
-      a2 = hfma(r1[2 * C], wv[5], a2);
-      a = hfma(r2[0], wv[6], a);
-      a2 = hfma(r2[C], wv[7], a2);
-      a = hfma(r2[2 * C], wv[8], a);
-      v[q] = silu_lut_h(a + a2);
-    } else {
-      h16 a = bias, e = (h16)0.0f;
+    for (int q = 0; q < 4; q++) v[q] = (h16)0.0f;
 #pragma unroll
-      for (int ky = 0; ky < K; ky++)
+    for (int q = 0; q < 4; q++) {
+      if (q >= item.n) break;
+      if (FORM == 2) {
+        const h16 *r0 = x0 + (long long)q * S * C, *r1 = r0 + (long long)Wp * C, *r2 = r1 + (long long)Wp * C;
+        h16 a = hfma(r0[0], wv[0], bias);
+        h16 a2 = r0[C] * wv[1];
+        a = hfma(r0[2 * C], wv[2], a);
+        a2 = hfma(r1[0], wv[3], a2);
+        a = hfma(r1[C], wv[4], a);
+        a2 = hfma(r1[2 * C], wv[5], a2);
+        a = hfma(r2[0], wv[6], a);
+        a2 = hfma(r2[C], wv[7], a2);
+        a = hfma(r2[2 * C], wv[8], a);
+        v[q] = silu_lut_h(a + a2);
+      } else {
+        h16 a = bias, e = (h16)0.0f;
 #pragma unroll
-        for (int kx = 0; kx < K; kx++) {
-          const int t = ky * K + kx;
-          const h16 xv = x0[((long long)ky * Wp + q * S + kx) * C];
-          if (item.split && (t & 1)) e = hfma(xv, wv[t], e);
-          else a = hfma(xv, wv[t], a);
-        }
-      h16 y = item.split ? a + e : a;
-      if (act == 1) y = silu_lut_h(y);
-      v[q] = y;
+        for (int ky = 0; ky < K; ky++)
+#pragma unroll
+          for (int kx = 0; kx < K; kx++) {
+            const int t = ky * K + kx;
+            const h16 xv = x0[((long long)ky * Wp + q * S + kx) * C];
+            if (item.split && (t & 1)) e = hfma(xv, wv[t], e);
+            else a = hfma(xv, wv[t], a);
+          }
+        h16 y = item.split ? a + e : a;
+        if (act == 1) y = silu_lut_h(y);
+        v[q] = y;
+      }
     }
-  }
-  h16 *o = out + win * o_ws + ((long long)oy * Wo + item.px) * C + c;
+    h16 *o = ow + (long long)item.px * C;
 #pragma unroll
-  for (int q = 0; q < 4; q++)
-    if (q < item.n) o[(long long)q * C] = v[q];
+    for (int q = 0; q < 4; q++)
+      if (q < item.n) o[(long long)q * C] = v[q];
+  }
 }
 
 // ------------------------------------------------------------------ channel sums (pass 2)
@@ -468,13 +488,14 @@ int bnh_dwk_f32(const float *xp, long long x_ws, int H, int W, int C, int k, int
   if (dw_check(H, W, C, k, s, pt, pl, Ho, Wo, B, x_ws, o_ws, (k - 1) / 2)) return -1;
   const int nit = items_per_row(Wo, 0);
   unsigned nb;
+  long long total;
   DwGrid g;
-  if (dw_grid(nit, C, Ho, B, &nb, &g)) return -1;
+  if (dw_grid(nit, C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   const int Wp = W + k - 1;
   dispatch_ks<float>(k, s, [&]<int K, int S>() {
     hipLaunchKernelGGL((k_dw_f32<K, S, 0>), dim3(nb), dim3(256), 0, st, xp, x_ws, Wp, C, pt, pl, w, b, act, out, o_ws,
-                       Ho, Wo, nit, g);
+                       Ho, Wo, nit, total, g);
   });
   BNH_HIP(hipGetLastError());
   if (chsum) {
@@ -490,15 +511,16 @@ int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, con
   if (dw_check(H, W, C, 3, s, 1, 1, Ho, Wo, B, x_ws, o_ws, 1)) return -1;
   const int nit = items_per_row(Wo, 2);
   unsigned nb;
+  long long total;
   DwGrid g;
-  if (dw_grid(nit, C, Ho, B, &nb, &g)) return -1;
+  if (dw_grid(nit, C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   if (s == 1)
     hipLaunchKernelGGL((k_dw_f32<3, 1, 2>), dim3(nb), dim3(256), 0, st, xp, x_ws, W + 2, C, 1, 1, w, b, 1, out, o_ws,
-                       Ho, Wo, nit, g);
+                       Ho, Wo, nit, total, g);
   else
     hipLaunchKernelGGL((k_dw_f32<3, 2, 2>), dim3(nb), dim3(256), 0, st, xp, x_ws, W + 2, C, 1, 1, w, b, 1, out, o_ws,
-                       Ho, Wo, nit, g);
+                       Ho, Wo, nit, total, g);
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);
@@ -514,13 +536,14 @@ int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, 
   if (dw_check(H, W, C, k, s, pt, pl, Ho, Wo, B, x_ws, o_ws, (k - 1) / 2)) return -1;
   const int nit = items_per_row(Wo, 1);
   unsigned nb;
+  long long total;
   DwGrid g;
-  if (dw_grid(nit, C, Ho, B, &nb, &g)) return -1;
+  if (dw_grid(nit, C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   const int Wp = W + k - 1;
   dispatch_ks<h16>(k, s, [&]<int K, int S>() {
     hipLaunchKernelGGL((k_dw_f16<K, S, 1>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, Wp, C, pt, pl,
-                       (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, Ho, Wo, nit, g);
+                       (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, Ho, Wo, nit, total, g);
   });
   BNH_HIP(hipGetLastError());
   if (chsum) {
@@ -537,15 +560,16 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
   if (dw_check(H, W, C, 3, s, pt, pl, Ho, Wo, B, x_ws, o_ws, 1)) return -1;
   const int nit = items_per_row(Wo, 2);
   unsigned nb;
+  long long total;
   DwGrid g;
-  if (dw_grid(nit, C, Ho, B, &nb, &g)) return -1;
+  if (dw_grid(nit, C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   if (s == 1)
     hipLaunchKernelGGL((k_dw_f16<3, 1, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,
-                       (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, g);
+                       (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total, g);
   else
     hipLaunchKernelGGL((k_dw_f16<3, 2, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,
-                       (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, g);
+                       (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total, g);
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);

@@ -73,64 +73,96 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
   o[0] = y[0]; o[1] = y[1]; o[2] = y[2]; o[3] = y[3];
 }
 
-// ------------------------------------------------------------------ SE_GATE / SE: one block per window
+// ------------------------------------------------------------------ SE_GATE / SE: one block per group of windows
+// A block computes the gates of WG windows (so each weight it streams serves WG windows), every value with the
+// reference's instructions in its order: mean = chsum * (1 / P); fc1 as eight lane chains (two 4-lane accumulators
+// over 8-channel steps) summed pairwise, + b1, SiLU by the C library's expf; fc2 from b2, one FMA per row r;
+// sigmoid_f32x4. SE also gates the activation [P][C] in place.
+template <int WG>
 __global__ __launch_bounds__(256) void k_se_f32(const float *__restrict__ chsum, long long c_ws, int C, int rd, int P,
                                                 const float *__restrict__ w1, const float *__restrict__ b1,
                                                 const float *__restrict__ w2t, const float *__restrict__ b2,
                                                 float *__restrict__ gate, long long g_ws, float *__restrict__ D,
-                                                long long d_ws) {
+                                                long long d_ws, int B) {
   extern __shared__ float sm[];
-  float *mean = sm, *part = sm + C, *s1 = part + 8 * rd, *g = s1 + rd;  // [C] [rd][8] [rd] [C]
-  const int win = blockIdx.x, tid = threadIdx.x;
-  const float *cs = chsum + win * c_ws;
+  float *mean = sm, *part = sm + WG * C, *s1 = part + WG * 8 * rd, *g = s1 + WG * rd;  // [WG][C] [WG][rd][8] [WG][rd]
+  const int win0 = blockIdx.x * WG, nw = B - win0 < WG ? B - win0 : WG, tid = threadIdx.x;
   const float inv = 1.f / (float)P;
-  for (int c = tid; c < C; c += 256) mean[c] = cs[c] * inv;
+  for (int i = tid; i < WG * C; i += 256) {
+    const int wg = i / C, c = i - wg * C;
+    mean[i] = wg < nw ? chsum[(win0 + wg) * c_ws + c] * inv : 0.f;
+  }
   __syncthreads();
-  // fc1: the eight lane chains of the two 4-lane accumulators (lane l < 4: a0, channels 8 i + l and the 4-wide
-  // tail; l >= 4: a1, channels 8 i + l)
   const int C8 = C / 8 * 8;
   for (int it = tid; it < 8 * rd; it += 256) {
     const int r = it / 8, l = it % 8;
     const float *w = w1 + (long long)r * C;
-    float a = 0.f;
-    for (int c = l; c < C8; c += 8) a = __builtin_fmaf(w[c], mean[c], a);
-    if (l < 4 && C8 + l < C) a = __builtin_fmaf(w[C8 + l], mean[C8 + l], a);
-    part[r * 8 + l] = a;
+    float a[WG];
+#pragma unroll
+    for (int wg = 0; wg < WG; wg++) a[wg] = 0.f;
+#pragma unroll 8
+    for (int c = l; c < C8; c += 8) {
+      const float wv = w[c];
+#pragma unroll
+      for (int wg = 0; wg < WG; wg++) a[wg] = __builtin_fmaf(wv, mean[wg * C + c], a[wg]);
+    }
+    if (l < 4 && C8 + l < C) {
+      const float wv = w[C8 + l];
+#pragma unroll
+      for (int wg = 0; wg < WG; wg++) a[wg] = __builtin_fmaf(wv, mean[wg * C + C8 + l], a[wg]);
+    }
+#pragma unroll
+    for (int wg = 0; wg < WG; wg++) part[(wg * rd + r) * 8 + l] = a[wg];
   }
   __syncthreads();
-  for (int r = tid; r < rd; r += 256) {
-    const float *p = part + r * 8;
-    const float v = ((p[0] + p[4]) + (p[1] + p[5])) + ((p[2] + p[6]) + (p[3] + p[7]));
+  for (int i = tid; i < WG * rd; i += 256) {
+    const int r = i % rd;
+    const float *pp = part + i * 8;
+    const float v = ((pp[0] + pp[4]) + (pp[1] + pp[5])) + ((pp[2] + pp[6]) + (pp[3] + pp[7]));
     const float x = v + b1[r];
-    s1[r] = x / (1.f + bnh_expf(-x));  // silu_s: the C library's expf
+    s1[i] = x / (1.f + bnh_expf(-x));  // silu_s: the C library's expf
   }
   __syncthreads();
   for (int c = tid; c < C; c += 256) {
-    float a = b2[c];
-    for (int r = 0; r < rd; r++) a = __builtin_fmaf(w2t[(long long)r * C + c], s1[r], a);
-    // sigmoid_f32x4: 1 / (1 + exp2_f32x4(-a log2 e)) by FRECPE and two Newton steps
-    float t = a * -1.44269504f;
-    t = bnh_fmin(bnh_fmax(t, -126.f), 126.f);
-    const float n = __builtin_rintf(t), f = t - n;
-    float q = 1.5403530e-4f;
-    q = __builtin_fmaf(q, f, 1.3333558e-3f);
-    q = __builtin_fmaf(q, f, 9.6181291e-3f);
-    q = __builtin_fmaf(q, f, 5.5504109e-2f);
-    q = __builtin_fmaf(q, f, 2.4022651e-1f);
-    q = __builtin_fmaf(q, f, 6.9314718e-1f);
-    q = __builtin_fmaf(q, f, 1.f);
-    const float e = bnh_float(bnh_bits(q) + ((uint32_t)bnh_cvtz_s32(n) << 23));
-    const float d = 1.f + e;
-    float rr = bnh_frecpe(d);
-    rr = rr * bnh_frecps(d, rr);
-    rr = rr * bnh_frecps(d, rr);
-    g[c] = rr;
-    if (gate) gate[win * g_ws + c] = rr;
+    float a[WG];
+    const float b = b2[c];
+#pragma unroll
+    for (int wg = 0; wg < WG; wg++) a[wg] = b;
+#pragma unroll 8
+    for (int r = 0; r < rd; r++) {
+      const float wv = w2t[(long long)r * C + c];
+#pragma unroll
+      for (int wg = 0; wg < WG; wg++) a[wg] = __builtin_fmaf(wv, s1[wg * rd + r], a[wg]);
+    }
+#pragma unroll
+    for (int wg = 0; wg < WG; wg++) {
+      // sigmoid_f32x4: 1 / (1 + exp2_f32x4(-a log2 e)) by FRECPE and two Newton steps
+      float t = a[wg] * -1.44269504f;
+      t = bnh_fmin(bnh_fmax(t, -126.f), 126.f);
+      const float n = __builtin_rintf(t), f = t - n;
+      float q = 1.5403530e-4f;
+      q = __builtin_fmaf(q, f, 1.3333558e-3f);
+      q = __builtin_fmaf(q, f, 9.6181291e-3f);
+      q = __builtin_fmaf(q, f, 5.5504109e-2f);
+      q = __builtin_fmaf(q, f, 2.4022651e-1f);
+      q = __builtin_fmaf(q, f, 6.9314718e-1f);
+      q = __builtin_fmaf(q, f, 1.f);
+      const float e = bnh_float(bnh_bits(q) + ((uint32_t)bnh_cvtz_s32(n) << 23));
+      const float d = 1.f + e;
+      float rr = bnh_frecpe(d);
+      rr = rr * bnh_frecps(d, rr);
+      rr = rr * bnh_frecps(d, rr);
+      g[wg * C + c] = rr;
+      if (gate && wg < nw) gate[(win0 + wg) * g_ws + c] = rr;
+    }
   }
   if (!D) return;
   __syncthreads();
-  float *d = D + win * d_ws;
-  for (long long i = tid; i < (long long)P * C; i += 256) d[i] = d[i] * g[i % C];
+  for (int wg = 0; wg < nw; wg++) {
+    float *d = D + (win0 + wg) * d_ws;
+    const float *gg = g + wg * C;
+    for (long long i = tid; i < (long long)P * C; i += 256) d[i] = d[i] * gg[i % C];
+  }
 }
 
 // ------------------------------------------------------------------ MEAN
@@ -214,9 +246,22 @@ int bnh_se_f32(const float *chsum, long long c_ws, int C, int rd, int P, const f
   BNH_REQ(chsum && w1 && b1 && w2t && b2 && (gate || D) && B > 0);
   BNH_REQ(C > 0 && C % 4 == 0 && C <= 4096 && rd > 0 && rd <= 512 && P > 0);
   BNH_REQ(B == 1 || (c_ws >= C && (!gate || g_ws >= C) && (!D || d_ws >= (long long)P * C)));
-  const size_t lds = sizeof(float) * (2 * (size_t)C + 9 * (size_t)rd);
-  hipLaunchKernelGGL(k_se_f32, dim3((unsigned)B), dim3(256), lds, bnh_stream(stream), chsum, c_ws, C, rd, P, w1, b1,
-                     w2t, b2, gate, g_ws, D, d_ws);
+  // windows per block: as many as 64 KB of LDS holds, at most 4
+  const size_t per = sizeof(float) * (2 * (size_t)C + 9 * (size_t)rd);
+  int wg = (int)((64 * 1024) / per);
+  wg = wg >= 4 ? 4 : wg >= 2 ? 2 : 1;
+  if (wg > B) wg = B >= 4 ? 4 : B >= 2 ? 2 : 1;
+  const dim3 grid((unsigned)bnh_ceil_div(B, wg));
+  hipStream_t st = bnh_stream(stream);
+#define SE_LAUNCH(W)                                                                                                   \
+  hipLaunchKernelGGL((k_se_f32<W>), grid, dim3(256), per * W, st, chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws,  \
+                     D, d_ws, B)
+  switch (wg) {
+    case 4: SE_LAUNCH(4); break;
+    case 2: SE_LAUNCH(2); break;
+    default: SE_LAUNCH(1); break;
+  }
+#undef SE_LAUNCH
   BNH_HIP(hipGetLastError());
   return 0;
 }

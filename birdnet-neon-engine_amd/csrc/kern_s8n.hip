@@ -141,24 +141,31 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
   const float *r = x + w * x_ws + (long long)m * ld;
   const float *g = gate ? gate + w * g_ws : nullptr;
   const int K4 = K & ~3, K8 = K & ~7, n4 = K4 / 4;
+  // min / max of k < K4: the reference's FMIN / FMAX give NaN when any element is NaN and otherwise the exact
+  // extremes (the sign of a zero extreme changes no later result); fminf / fmaxf plus a NaN flag give the same
   float lo = __builtin_inff(), hi = -__builtin_inff();
+  int nan = 0;
   for (int c = sub; c < n4; c += L) {
     float4 v = *(const float4 *)(r + 4 * c);
     if (g) {
       const float4 gv = *(const float4 *)(g + 4 * c);
       v.x = v.x * gv.x; v.y = v.y * gv.y; v.z = v.z * gv.z; v.w = v.w * gv.w;
     }
-    lo = bnh_fmin(bnh_fmin(lo, v.x), bnh_fmin(v.y, bnh_fmin(v.z, v.w)));
-    hi = bnh_fmax(bnh_fmax(hi, v.x), bnh_fmax(v.y, bnh_fmax(v.z, v.w)));
+    nan |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
+    lo = __builtin_fminf(__builtin_fminf(lo, v.x), __builtin_fminf(v.y, __builtin_fminf(v.z, v.w)));
+    hi = __builtin_fmaxf(__builtin_fmaxf(hi, v.x), __builtin_fmaxf(v.y, __builtin_fmaxf(v.z, v.w)));
   }
 #pragma unroll
   for (int off = L / 2; off; off >>= 1) {
-    lo = bnh_fmin(lo, __shfl_xor(lo, off));
-    hi = bnh_fmax(hi, __shfl_xor(hi, off));
+    lo = __builtin_fminf(lo, __shfl_xor(lo, off));
+    hi = __builtin_fmaxf(hi, __shfl_xor(hi, off));
+    nan |= __shfl_xor(nan, off);
   }
+  if (nan) lo = hi = __builtin_nanf("");
   for (int k = K4; k < K; k++) {
     float v = r[k];
     if (g) v = v * g[k];
+    nan |= v != v;
     lo = bnh_fminnm(lo, v);
     hi = bnh_fmaxnm(hi, v);
   }
@@ -180,6 +187,8 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
     sa[w * sa_ws + m] = sc;
     za[w * za_ws + m] = z;
   }
+  // a row of finite values whose scaled extremes stay below 2^30 needs no saturation: the roundings are plain
+  const bool fast = !nan && __builtin_fmaxf(__builtin_fabsf(lo), __builtin_fabsf(hi)) * inv < 1073741824.f;
   int8_t *o = q + w * q_ws + (long long)m * Kp;
   const uint32_t zb = (uint32_t)z & 0xffu;
   for (int c = sub; c < Kp / 4; c += L) {
@@ -210,7 +219,9 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
       uint32_t byte = zb;
       if (k < K) {
         const float t = v[j] * inv;
-        int32_t cq = (int32_t)((uint32_t)(k < K8 ? bnh_cvtn_s32(t) : bnh_lrintf_s32(t)) + (uint32_t)z);
+        int32_t cq;
+        if (fast) cq = (int32_t)__builtin_rintf(t) + z;
+        else cq = (int32_t)((uint32_t)(k < K8 ? bnh_cvtn_s32(t) : bnh_lrintf_s32(t)) + (uint32_t)z);
         cq = cq < -127 ? -127 : cq > 127 ? 127 : cq;
         byte = (uint32_t)cq & 0xffu;
       }
