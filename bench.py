@@ -405,12 +405,12 @@ def run_wino(a, H, rng, B, stream):
 
 
 def perch_counts(net):
-    """(int8 GEMM ops per window, the largest PW_S8 op record) of a netbuild net."""
+    """(int8 GEMM ops per window, the PW_S8 op record with the most output) of a netbuild net."""
     ops, big = 0, None
     for code, b, t, p in net.ops:
         if code & 0xff == 22:   # PW_S8: N K Kp Np M ...
             ops += 2 * p[0] * p[1] * p[4]
-            if big is None or p[0] * p[1] * p[4] > big[3][0] * big[3][1] * big[3][4]:
+            if big is None or p[0] * p[4] > big[3][0] * big[3][4]:
                 big = (code, b, t, p)
         elif code & 0xff == 23:  # GEMV_S8
             ops += 2 * p[0] * p[1]
@@ -485,7 +485,35 @@ def run_perch(a, H, rng, B, stream):
 
 
 def perch_roofline(H, pn, B, stream, a):
-    return None
+    """The dominant kernel of the net is the int8 pointwise GEMM with its dequant + SiLU epilogue (k_s8n_gemm, the
+    largest share of the step); its largest launch, the 24 -> 144 expansion over 249 x 63 pixels into a halo-1
+    buffer, is replayed with the net's own weights and shape on `stream` and timed with events. Algorithmic bytes
+    per launch: the int8 rows read (B x M x Kp), the fp32 outputs written (B x M x N x 4) and the weights."""
+    from bnneon import s8pack
+    _, big = perch_counts(pn.net)
+    code, b, t, p = big
+    N, K, Kp, Np, M, lda, act, ldo, ow, opad, ldr = p
+    T = [arr for (_, arr, _) in pn.pkg.tensors]
+    Wt = H.S8Weights(N, K, Kp, Np, T[t[0]], T[t[1]], T[t[2]], T[t[3]])
+    rng = np.random.default_rng(5)
+    dq = H.DeviceArray.from_host(rng.integers(-127, 128, (B, M * Kp)).astype(np.int8))
+    dsa = H.DeviceArray.from_host(rng.uniform(0.005, 0.02, (B, M)).astype(np.float32))
+    dza = H.DeviceArray.from_host(rng.integers(-20, 20, (B, M)).astype(np.int32))
+    Hh = M // ow if opad else M
+    rows = (Hh + 2 * opad) * (ow + 2 * opad) if opad else M
+    dout = H.DeviceArray.zeros((B, rows * ldo), np.float32)
+    e = H.epi32(dout, ldo, act=act, out_ws=rows * ldo, ow=ow if opad else 0, opad=opad)
+
+    def launch():
+        H.check(H.lib().bnh_s8n_gemm(dq.ptr, M * Kp, dsa.ptr, M, dza.ptr, M, M, B, Wt.h, e, stream))
+    ms, _ = time_steps(H, stream, launch, max(10, a.steps), 3)
+    nbytes = B * M * Kp + B * M * N * 4 + Np * Kp + 12 * Np
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_s8n_gemm<2, 2>",
+            "launch": f"PW_S8 GEMM {K}->{N} over {M} px x {B} windows, SiLU, halo-{opad} output",
+            "ms_per_launch": round(ms, 4), "algorithmic_bytes_per_launch": nbytes}
 
 
 if __name__ == "__main__":

@@ -105,13 +105,18 @@ BNH_DEV float bnh_frecps(float a, float b) {
 // The fp32 SiLU of libbnneon's GEMM / depthwise epilogues (src/gemm_f32.h:102-118): exp2 by the magic-number split
 // and a degree-5 polynomial, t clamped to +-60, one FRECPE + FRECPS Newton step. Because of the clamp, the divisor
 // d = 1 + 2^t lies in [1, 2^60 + 1] (finite, normal, positive) for every x that is not NaN, so FRECPE reduces to its
-// normal-operand case (exponent 253 - e, 8 fraction bits from the 9-bit estimate) and FRECPS to one fused
-// 2 - d r. A NaN x gives NaN through the final product x r whatever the clamp did with it (the reference's NaN
-// travels through d and r instead: the same NaN result, payloads aside).
-BNH_DEV float bnh_silu_f32(float x) {
+// normal-operand case (exponent 253 - e, 8 fraction bits from the 9-bit estimate of the leading 8 significand bits)
+// and FRECPS to one fused 2 - d r. A NaN x gives NaN through the final product x r whatever the clamp did with it
+// (the reference's NaN travels through d and r instead: the same NaN result, payloads aside).
+// The fraction bits of the estimate, per leading significand byte, at bits 22..15: a block puts this table in LDS
+// (bnh_silu_table, then a barrier) for bnh_silu_f32_t.
+BNH_DEV void bnh_silu_table(uint32_t *tbl) {
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = (uint32_t)(bnh_recip_estimate(256 | i) & 0xff) << 15;
+}
+BNH_DEV float bnh_silu_d(float x) {  // the divisor d = 1 + 2^t, t = clamp(-x log2 e, -60, 60)
   const float magic = 12582912.0f;
   float t = x * -1.44269504f;
-  t = __builtin_fminf(__builtin_fmaxf(t, -60.f), 60.f);
+  t = __builtin_amdgcn_fmed3f(t, -60.f, 60.f);
   const float tm = t + magic;
   const float f = t - (tm - magic);
   const uint32_t ni = bnh_bits(tm) << 23;
@@ -120,10 +125,20 @@ BNH_DEV float bnh_silu_f32(float x) {
   p = __builtin_fmaf(p, f, 2.4022651e-1f);
   p = __builtin_fmaf(p, f, 6.9314718e-1f);
   p = __builtin_fmaf(p, f, 1.0f);
-  const float d = 1.f + bnh_float(bnh_bits(p) + ni);
+  return 1.f + bnh_float(bnh_bits(p) + ni);
+}
+BNH_DEV float bnh_silu_f32_t(float x, const uint32_t *tbl) {
+  const float d = bnh_silu_d(x);
+  const uint32_t db = bnh_bits(d);
+  float r = bnh_float(((253u << 23) - (db & 0x7f800000u)) | tbl[(db >> 15) & 0xffu]);
+  r = r * __builtin_fmaf(-d, r, 2.f);
+  return x * r;
+}
+BNH_DEV float bnh_silu_f32(float x) {  // the same without the table
+  const float d = bnh_silu_d(x);
   const uint32_t db = bnh_bits(d);
   const int est = bnh_recip_estimate(256 | (int)((db >> 15) & 0xffu));
-  float r = bnh_float(((253u - (db >> 23)) << 23) | ((uint32_t)(est & 0xff) << 15));
+  float r = bnh_float(((253u << 23) - (db & 0x7f800000u)) | ((uint32_t)(est & 0xff) << 15));
   r = r * __builtin_fmaf(-d, r, 2.f);
   return x * r;
 }

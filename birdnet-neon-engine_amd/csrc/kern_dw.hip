@@ -87,10 +87,13 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
                                                 int pl, const float *__restrict__ w, const float *__restrict__ b,
                                                 int act, float *__restrict__ out, long long o_ws, int Ho, int Wo,
                                                 int nitems, long long total, DwGrid g) {
+  __shared__ uint32_t tbl[256];
+  bnh_silu_table(tbl);
+  __syncthreads();
   const DwPos ps = dw_pos(C, Ho, total, g);
   if (!ps.ok) return;
   const int c = ps.c, oy = ps.oy, win = ps.win;
-  constexpr int H = (K - 1) / 2;
+  constexpr int H = (K - 1) / 2, NC = 3 * S + K;  // input columns of a 4-pixel item
   const int iy0 = FORM == 2 ? oy * S : oy * S - pt + H;
   float wv[K * K];
 #pragma unroll
@@ -98,6 +101,7 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
   const float bias = b[c];
   const float *xw = xp + win * x_ws + (long long)iy0 * Wp * C + c;
   float *ow = out + win * o_ws + (long long)oy * Wo * C + c;
+  const long long rs = (long long)Wp * C;
 #pragma unroll
   for (int j = 0; j < DW_NI; j++) {
     const int it = ps.it0 + j;
@@ -105,25 +109,31 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
     const Item item = item_of(it, Wo, FORM);
     const int ix0 = FORM == 2 ? item.px * S : item.px * S - pl + H;
     const float *x0 = xw + (long long)ix0 * C;
+    // the item's whole input window first (columns past its last pixel's taps stay unread), so that its loads are
+    // in flight together
+    const int ncol = (item.n - 1) * S + K;
+    float xv[K][NC];
+#pragma unroll
+    for (int ky = 0; ky < K; ky++)
+#pragma unroll
+      for (int kx = 0; kx < NC; kx++) xv[ky][kx] = kx < ncol ? x0[ky * rs + (long long)kx * C] : 0.f;
     float v[4];
 #pragma unroll
-    for (int q = 0; q < 4; q++) v[q] = 0.f;
-#pragma unroll
     for (int q = 0; q < 4; q++) {
-      if (q >= item.n) break;
+      v[q] = 0.f;
+      if (q >= item.n) continue;
       if (FORM == 2) {
-        const float *p0 = x0 + (long long)q * S * C;
-        const long long r1 = (long long)Wp * C, r2 = 2 * r1;
-        float acc = __builtin_fmaf(wv[0], p0[0], bias);
-        float acb = wv[1] * p0[C];
-        float acd = wv[2] * p0[2 * C];
-        acc = __builtin_fmaf(wv[3], p0[r1], acc);
-        acb = __builtin_fmaf(wv[4], p0[r1 + C], acb);
-        acd = __builtin_fmaf(wv[5], p0[r1 + 2 * C], acd);
-        acc = __builtin_fmaf(wv[6], p0[r2], acc);
-        acb = __builtin_fmaf(wv[7], p0[r2 + C], acb);
-        acd = __builtin_fmaf(wv[8], p0[r2 + 2 * C], acd);
-        v[q] = bnh_silu_f32(acc + (acb + acd));
+        const int o = q * S;
+        float acc = __builtin_fmaf(wv[0], xv[0][o], bias);
+        float acb = wv[1] * xv[0][o + 1];
+        float acd = wv[2] * xv[0][o + 2];
+        acc = __builtin_fmaf(wv[3], xv[1][o], acc);
+        acb = __builtin_fmaf(wv[4], xv[1][o + 1], acb);
+        acd = __builtin_fmaf(wv[5], xv[1][o + 2], acd);
+        acc = __builtin_fmaf(wv[6], xv[2][o], acc);
+        acb = __builtin_fmaf(wv[7], xv[2][o + 1], acb);
+        acd = __builtin_fmaf(wv[8], xv[2][o + 2], acd);
+        v[q] = bnh_silu_f32_t(acc + (acb + acd), tbl);
       } else {
         float a = bias, e = 0.f;
 #pragma unroll
@@ -131,12 +141,12 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
 #pragma unroll
           for (int kx = 0; kx < K; kx++) {
             const int t = ky * K + kx;
-            const float xv = x0[((long long)ky * Wp + q * S + kx) * C];
-            if (item.split && (t & 1)) e = __builtin_fmaf(xv, wv[t], e);
-            else a = __builtin_fmaf(xv, wv[t], a);
+            const float x = xv[ky][q * S + kx];
+            if (item.split && (t & 1)) e = __builtin_fmaf(x, wv[t], e);
+            else a = __builtin_fmaf(x, wv[t], a);
           }
         float y = item.split ? a + e : a;
-        if (act == 1) y = bnh_silu_f32(y);
+        if (act == 1) y = bnh_silu_f32_t(y, tbl);
         v[q] = y;
       }
     }
@@ -320,7 +330,16 @@ __global__ __launch_bounds__(256) void k_chsum(const T *__restrict__ out, long l
     } else if (lane < S) {
       const int rows = Ho - ch * R < R ? Ho - ch * R : R;
       const float *buf = tb + (ch & 1) * per + lane;
-      for (int it = 0; it < rows * Tn; it++) cs = cs + buf[it * S];
+      const int n = rows * Tn;
+      int it = 0;
+      for (; it + 16 <= n; it += 16) {  // sixteen LDS reads in flight, then the sixteen dependent adds in order
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) t[u] = buf[(it + u) * S];
+#pragma unroll
+        for (int u = 0; u < 16; u++) cs = cs + t[u];
+      }
+      for (; it < n; it++) cs = cs + buf[it * S];
     }
     __syncthreads();
   }

@@ -45,6 +45,9 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
                                                   int Ho, int Wo, const float *__restrict__ w,
                                                   const float *__restrict__ bias, int Kp, int Np, int act,
                                                   float *__restrict__ out, long long o_ws, int ldo, int opad) {
+  __shared__ uint32_t tbl[256];
+  bnh_silu_table(tbl);
+  __syncthreads();
   const int ng = Np / 4;
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x, per = (long long)Ho * Wo * ng;
   const int win = blockIdx.y;
@@ -65,7 +68,7 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     y[j] = acc[j] + bias[n0 + j];
-    if (act == 1) y[j] = bnh_silu_f32(y[j]);
+    if (act == 1) y[j] = bnh_silu_f32_t(y[j], tbl);
     else if (act == 2) y[j] = bnh_relu_f32(y[j]);
   }
   const long long orow = opad ? (long long)(oy + opad) * (Wo + 2 * opad) + ox + opad : m;

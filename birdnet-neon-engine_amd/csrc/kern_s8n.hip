@@ -245,7 +245,8 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
   constexpr int RB = WM * 32;
   __shared__ long long s_q[RB], s_o[RB], s_r[RB];
   __shared__ float s_sa[RB];
-  __shared__ uint32_t s_z[RB];
+  __shared__ uint32_t s_z[RB], s_tbl[256];
+  bnh_silu_table(s_tbl);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const long long rowB = (long long)blockIdx.x * RB;
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
         const float scl = swn[j] * s_a;
         float y = f * scl;
         y = y + bn[j];
-        if (e.act == 1) y = bnh_silu_f32(y);
+        if (e.act == 1) y = bnh_silu_f32_t(y, s_tbl);
         else if (e.act == 2) y = bnh_relu_f32(y);
         if (rrow) y = y + rrow[n];
         orow[n] = y;
@@ -638,11 +639,15 @@ __global__ void k_eval_requant(const int32_t *__restrict__ acc, const int32_t *_
 }
 
 // ------------------------------------------------------------------ numerics probe
+// f: 0 FRECPE, 1 the SiLU of the epilogues (LDS-table form), 2 ReLU, 3 the SiLU without the table
 __global__ void k_eval_f32(int f, const float *__restrict__ x, float *__restrict__ y, long long n) {
+  __shared__ uint32_t tbl[256];
+  bnh_silu_table(tbl);
+  __syncthreads();
   long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const float v = x[i];
-  y[i] = f == 0 ? bnh_frecpe(v) : f == 1 ? bnh_silu_f32(v) : bnh_relu_f32(v);
+  y[i] = f == 0 ? bnh_frecpe(v) : f == 1 ? bnh_silu_f32_t(v, tbl) : f == 3 ? bnh_silu_f32(v) : bnh_relu_f32(v);
 }
 
 // ================================================================== host side
@@ -659,7 +664,7 @@ int bnh_eval_requant(const int32_t *acc, const int32_t *mult, const int32_t *shi
 }
 
 int bnh_eval_f32(int f, const float *x, float *y, long long n, void *stream) {
-  BNH_REQ(f >= 0 && f <= 2 && n >= 0 && x && y);
+  BNH_REQ(f >= 0 && f <= 3 && n >= 0 && x && y);
   if (!n) return 0;
   hipLaunchKernelGGL(k_eval_f32, dim3((unsigned)bnh_ceil_div(n, 256)), dim3(256), 0, bnh_stream(stream), f, x, y, n);
   BNH_HIP(hipGetLastError());

@@ -70,8 +70,9 @@ def test_silu_relu_bit_exact(hip, f):
 
 
 def test_silu_dense(hip):
-    """every 16th float of both signs with |x| in [2^-27, 2^34) (past +-41.6 the clamp saturates), all NaN forms
-    and infinities: the epilogue SiLU's divisor covers its whole range."""
+    """every 16th float of both signs with |x| in [2^-27, 2^34) (past +-41.6 the clamp saturates), NaNs and
+    infinities: the epilogue SiLU's divisor covers its whole range; both device forms (with and without the LDS
+    estimate table)."""
     e = np.arange(100, 161, dtype=np.uint32)
     m = np.arange(0, 2 ** 23, 16, dtype=np.uint32)
     bits = (e[:, None] << np.uint32(23)) | m[None, :]
@@ -79,7 +80,9 @@ def test_silu_dense(hip):
                            np.array([0x7f800000, 0xff800000, 0x7fc00000, 0xffc00001, 0x7f800001], np.uint32)])
     x = bits.view(np.float32)
     say("silu dense", x.size)
-    assert same_f32(run_eval(hip, 1, x), O.eval_f32(1, x))
+    want = O.eval_f32(1, x)
+    assert same_f32(run_eval(hip, 1, x), want)   # the LDS-table form the epilogues use
+    assert same_f32(run_eval(hip, 3, x), want)   # the form without the table
 
 
 def quant_case(hip, x, K, Kp, gate=None, B=1):
