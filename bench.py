@@ -484,6 +484,11 @@ def run_perch(a, H, rng, B, stream):
     print(json.dumps(line), flush=True)
 
 
+# HBM bytes per launch of that GEMM (24 -> 144 channels, 15,687 px, 256 windows): FETCH_SIZE x 2 + WRITE_SIZE from
+# rocprofv3 --pmc runs of this bench (profiles/k_s8n_gemm_pw_s8_24to144_249x63_b256.md)
+PERCH_GEMM_TRAFFIC = 2648826307
+
+
 def perch_roofline(H, pn, B, stream, a):
     """The dominant kernel of the net is the int8 pointwise GEMM with its dequant + SiLU epilogue (k_s8n_gemm, the
     largest share of the step); its largest launch, the 24 -> 144 expansion over 249 x 63 pixels into a halo-1
@@ -510,7 +515,7 @@ def perch_roofline(H, pn, B, stream, a):
     nbytes = B * M * Kp + B * M * N * 4 + Np * Kp + 12 * Np
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": PERCH_GEMM_TRAFFIC,
             "kernel": "k_s8n_gemm<2, 2>",
             "launch": f"PW_S8 GEMM {K}->{N} over {M} px x {B} windows, SiLU, halo-{opad} output",
             "ms_per_launch": round(ms, 4), "algorithmic_bytes_per_launch": nbytes}
