@@ -70,9 +70,10 @@ _SIGS = {
     "bnh_q8w_new": (vp, [i32, i32, vp, vp, vp, vp, i32, i32, i32, i32]),
     "bnh_q8w_free": (None, [vp]),
     "bnh_gemm_s8_requant": (i32, [vp, vp, i64, i32, i32, vp, i64, vp]),
-    "bnh_h16w_new": (vp, [i32, i32, i32, i32, vp, vp]),
+    "bnh_h16w_new": (vp, [i32, i32, i32, i32, vp, vp, vp]),
     "bnh_h16w_free": (None, [vp]),
     "bnh_gemm_f16": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
+    "bnh_gemm_f16_mfma": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
     "bnh_wino16_new": (vp, [i32, i32, vp, vp]),
     "bnh_wino16_free": (None, [vp]),
     "bnh_wino_f16": (i32, [vp, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp, i64, i32, i32, i32, vp]),
@@ -101,6 +102,11 @@ _SIGS = {
     "bnh_pad": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, i64, i32, vp]),
     "bnh_zero_halo": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp]),
     "bnh_eval_expf": (i32, [vp, vp, i64, vp]),
+    "bnh_stem_f32to16": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32,
+                               i32, vp]),
+    "bnh_se_f16": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, i32, vp]),
+    "bnh_mean_f16": (i32, [vp, i64, i32, i32, i32, vp, i64, i32, vp]),
+    "bnh_gemv": (i32, [vp, i32, vp, i32, i32, vp, i64, i32, vp, i64, i32, vp]),
 }
 
 

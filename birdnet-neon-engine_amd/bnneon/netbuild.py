@@ -106,6 +106,91 @@ class Net:
         self.last = ob
         return ob
 
+    # ---------------------------------------------------------------- fp16 path (variant 1)
+    @staticmethod
+    def pack_h16(w, b, k_pad):
+        """pack_h16 (python/bnneon/compiler/lower.py:99-128; hp_pack, src/gemm_f16.c:18-40): fp16 panels
+        [Np/16][Kp][16] + a tail [Kp][8] when Np % 16 == 8, the bias as fp32 and fp16 [Np + 16]."""
+        w = np.asarray(w, np.float32)
+        N, K = w.shape
+        Np = (N + 7) // 8 * 8
+        wp = np.zeros((Np, k_pad), np.float16)
+        wp[:N, :K] = w
+        n16 = Np // 16
+        main = wp[:n16 * 16].reshape(n16, 16, k_pad).transpose(0, 2, 1).reshape(-1)
+        tail = wp[n16 * 16:].T.reshape(-1) if Np % 16 else np.zeros(0, np.float16)
+        b32 = np.zeros(Np + 16, np.float32)
+        b32[:N] = b
+        return np.concatenate([main, tail]), b32, b32.astype(np.float16), (N, K, k_pad, Np)
+
+    def pw_f16(self, ib, w, b, act=None, opad=0, res=-1, ldo=None):
+        """A 1x1 conv on fp16 rows of buffer ib (the fp16 path's PW, lower.py:787-823)."""
+        d = self.bufs[ib]
+        H, W, M, lda = d[1], d[2], d[1] * d[2], d[4]
+        w = np.asarray(w, np.float32)
+        K = w.shape[1]
+        panels, b32, b16, (N, K, Kp, Np) = self.pack_h16(w, b, (K + 7) // 8 * 8)
+        tl = [self.tensor("f16/pw.w", panels), self.tensor("f16/pw.b32", b32), self.tensor("f16/pw.b16", b16)]
+        ldo = (N if opad else Np) if ldo is None else ldo
+        ob = self.buf(F16, H, W, N, ld=ldo, halo=opad)
+        ldr = self.bufs[res][4] if res >= 0 else 0
+        self.emit(OP["PW"], [ib, ob, res], tl, [N, K, Kp, Np, M, lda, ACT[act], ldo, W, opad, ldr], var=1)
+        self.last = ob
+        return ob
+
+    def stem_f16(self, ib, w, b, k, s, act="silu", opad=0, ldo=None):
+        """The fp16 path's STEM (fp32 math, fp16 output, src/rt_ops_f16.c:167-180)."""
+        d = self.bufs[ib]
+        H, W = d[1], d[2]
+        w = np.asarray(w, np.float32).reshape(len(b), k * k)
+        co = w.shape[0]
+        Ho, Wo = (H - k) // s + 1, (W - k) // s + 1
+        Kp, Np = (k * k + 3) // 4 * 4, (co + 7) // 8 * 8
+        wp = np.zeros((Np, Kp), np.float32)
+        wp[:co, :k * k] = w
+        panels = np.ascontiguousarray(wp.reshape(Np // 8, 8, Kp).transpose(0, 2, 1))
+        bb = np.zeros(Np + 8, np.float32)
+        bb[:co] = b
+        tl = [self.tensor("f32/stem.w", panels), self.tensor("f32/stem.b", bb)]
+        ldo = Np if ldo is None else ldo
+        ob = self.buf(F16, Ho, Wo, co, ld=ldo, halo=opad)
+        col = self.buf(F32, (Ho * Wo + 7) // 8 * 8, 1, Kp)
+        tmp = self.buf(F32, Ho * Wo, 1, Np)
+        self.emit(OP["STEM"], [ib, ob, col, tmp], tl, [co, k * k, Kp, Np, H, W, Ho, Wo, k, s, ACT[act], ldo, opad],
+                  var=1)
+        self.last = ob
+        return ob
+
+    def se_f16(self, ib, cs, w1, b1, w2, b2):
+        """SE in place on the fp16 activation ib [P][C] (the fp16 path's SE)."""
+        w1 = np.asarray(w1, np.float32)
+        rd, C = w1.shape
+        d = self.bufs[ib]
+        tl = [self.tensor("se.w1", w1), self.tensor("se.b1", np.asarray(b1, np.float32)),
+              self.tensor("se.w2t", np.ascontiguousarray(np.asarray(w2, np.float32).T)),
+              self.tensor("se.b2", np.asarray(b2, np.float32))]
+        self.emit(OP["SE"], [ib, cs], tl, [C, rd, d[1] * d[2]], var=1)
+        return ib
+
+    def mean_f16(self, ib):
+        d = self.bufs[ib]
+        assert not d[5]
+        ob = self.buf(F32, 1, 1, d[3])
+        self.emit(OP["MEAN"], [ib, ob], [], [d[1] * d[2], d[3], d[4]], var=1)
+        self.last = ob
+        return ob
+
+    def gemv(self, ib, w, b, act=None, fp16=False):
+        """Dense layer on a vector: GEMV (fp32 weights) or its fp16-weight form."""
+        w = np.asarray(w, np.float32)
+        N, K = w.shape
+        tl = [self.tensor("lin.w", w.astype(np.float16 if fp16 else np.float32)),
+              self.tensor("lin.b", np.asarray(b, np.float32))]
+        ob = self.buf(F32, 1, 1, N)
+        self.emit(OP["GEMV"], [ib, ob], tl, [N, K, ACT[act]], var=1 if fp16 else 0)
+        self.last = ob
+        return ob
+
     # ---------------------------------------------------------------- depthwise
     def dwk(self, ib, w, b, k, s=1, pt=None, pl=None, act="silu", fp16=False):
         """k x k depthwise conv (DWK) on the zero-haloed buffer ib (halo (k-1)/2,

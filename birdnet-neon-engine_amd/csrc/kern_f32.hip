@@ -13,6 +13,7 @@
 #include "bnh_internal.h"
 #include "bnh_num.h"
 #include "bnh_expf.h"
+#include "bnh_f16.h"
 
 // ------------------------------------------------------------------ halo zeroing, any element size (4 or 2 bytes)
 // one thread per halo element: the 2h rows of Wp pixels above and below, then the 2h side pixels of each interior row
@@ -40,11 +41,13 @@ __global__ void k_zero_halo(T *__restrict__ out, long long ws, int H, int W, int
 }
 
 // ------------------------------------------------------------------ STEM
-// thread per (window, output pixel, 4 channels); w panels [Np/8][Kp][8]
+// thread per (window, output pixel, 4 channels); w panels [Np/8][Kp][8]. H16: the fp16-path form, channels < N
+// rounded to fp16 (pc_cvt_pad_f16, src/pc_kern_f16.c:104-113) and stored as fp16
+template <bool H16>
 __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img, long long i_ws, int W, int k, int s,
                                                   int Ho, int Wo, const float *__restrict__ w,
                                                   const float *__restrict__ bias, int Kp, int Np, int act,
-                                                  float *__restrict__ out, long long o_ws, int ldo, int opad) {
+                                                  void *__restrict__ outv, long long o_ws, int ldo, int opad, int N) {
   __shared__ uint32_t tbl[256];
   bnh_silu_table(tbl);
   __syncthreads();
@@ -72,8 +75,15 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
     else if (act == 2) y[j] = bnh_relu_f32(y[j]);
   }
   const long long orow = opad ? (long long)(oy + opad) * (Wo + 2 * opad) + ox + opad : m;
-  float *o = out + win * o_ws + orow * ldo + n0;
-  o[0] = y[0]; o[1] = y[1]; o[2] = y[2]; o[3] = y[3];
+  if (H16) {
+    uint16_t *o = (uint16_t *)outv + win * o_ws + orow * ldo + n0;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (n0 + j < N) o[j] = hbits(f2h(y[j]));  // one rounding to nearest even (no fused mix forms)
+  } else {
+    float *o = (float *)outv + win * o_ws + orow * ldo + n0;
+    o[0] = y[0]; o[1] = y[1]; o[2] = y[2]; o[3] = y[3];
+  }
 }
 
 // ------------------------------------------------------------------ SE_GATE / SE: one block per group of windows
@@ -81,11 +91,13 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
 // reference's instructions in its order: mean = chsum * (1 / P); fc1 as eight lane chains (two 4-lane accumulators
 // over 8-channel steps) summed pairwise, + b1, SiLU by the C library's expf; fc2 from b2, one FMA per row r;
 // sigmoid_f32x4. SE also gates the activation [P][C] in place.
-template <int WG>
+// F16: the fp16 path's SE (v24k16_se, src/v24_fast.c:182-234): its sigmoid divides (1 / (1 + e), IEEE division),
+// the gate is rounded to fp16 and the fp16 activation is multiplied by it in fp16
+template <int WG, bool F16>
 __global__ __launch_bounds__(256) void k_se_f32(const float *__restrict__ chsum, long long c_ws, int C, int rd, int P,
                                                 const float *__restrict__ w1, const float *__restrict__ b1,
                                                 const float *__restrict__ w2t, const float *__restrict__ b2,
-                                                float *__restrict__ gate, long long g_ws, float *__restrict__ D,
+                                                float *__restrict__ gate, long long g_ws, void *__restrict__ Dv,
                                                 long long d_ws, int B) {
   extern __shared__ float sm[];
   float *mean = sm, *part = sm + WG * C, *s1 = part + WG * 8 * rd, *g = s1 + WG * rd;  // [WG][C] [WG][rd][8] [WG][rd]
@@ -152,19 +164,29 @@ __global__ __launch_bounds__(256) void k_se_f32(const float *__restrict__ chsum,
       q = __builtin_fmaf(q, f, 1.f);
       const float e = bnh_float(bnh_bits(q) + ((uint32_t)bnh_cvtz_s32(n) << 23));
       const float d = 1.f + e;
-      float rr = bnh_frecpe(d);
-      rr = rr * bnh_frecps(d, rr);
-      rr = rr * bnh_frecps(d, rr);
+      float rr;
+      if (F16) {
+        rr = 1.f / d;
+      } else {
+        rr = bnh_frecpe(d);
+        rr = rr * bnh_frecps(d, rr);
+        rr = rr * bnh_frecps(d, rr);
+      }
       g[wg * C + c] = rr;
       if (gate && wg < nw) gate[(win0 + wg) * g_ws + c] = rr;
     }
   }
-  if (!D) return;
+  if (!Dv) return;
   __syncthreads();
   for (int wg = 0; wg < nw; wg++) {
-    float *d = D + (win0 + wg) * d_ws;
     const float *gg = g + wg * C;
-    for (long long i = tid; i < (long long)P * C; i += 256) d[i] = d[i] * gg[i % C];
+    if (F16) {
+      h16 *d = (h16 *)Dv + (win0 + wg) * d_ws;
+      for (long long i = tid; i < (long long)P * C; i += 256) d[i] = d[i] * f2h(gg[i % C]);
+    } else {
+      float *d = (float *)Dv + (win0 + wg) * d_ws;
+      for (long long i = tid; i < (long long)P * C; i += 256) d[i] = d[i] * gg[i % C];
+    }
   }
 }
 
@@ -177,6 +199,71 @@ __global__ void k_mean_f32(const float *__restrict__ x, long long x_ws, int P, i
   float s = 0.f;
   for (int p = 0; p < P; p++) s = s + xw[(long long)p * ld];
   out[win * o_ws + c] = s / (float)P;
+}
+
+// MEAN of fp16 rows (pc_mean_f16, src/pc_kern_f16.c:115-121): fp32 sum of the widened values, / P
+__global__ void k_mean_f16(const uint16_t *__restrict__ x, long long x_ws, int P, int C, int ld, float *__restrict__ out,
+                           long long o_ws) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x, win = blockIdx.y;
+  if (c >= C) return;
+  const uint16_t *xw = x + win * x_ws + c;
+  float s = 0.f;
+  for (int p = 0; p < P; p++) s = s + (float)hfrom(xw[(long long)p * ld]);
+  out[win * o_ws + c] = s / (float)P;
+}
+
+// GEMV (bnn_gemv_f32 / bnn_gemv_h16, src/gemv.c:13-49) for WB windows per block: a thread owns one of the eight lane
+// chains of one output (k = 8 i + l below K & ~7, then lanes 0..3 take the K & ~3 remainder), the eight lanes of an
+// output are neighbours in a wave and meet by shuffles in the reference's pairwise order, lane 0 adds the scalar
+// tail (product and sum rounded apart), the bias and the ReLU (v < 0 ? 0 : v). The windows' inputs sit in LDS; each
+// weight read serves WB windows.
+template <bool W16, int WB>
+__global__ __launch_bounds__(256) void k_gemv(const void *__restrict__ wv, const float *__restrict__ bias, int N, int K,
+                                              const float *__restrict__ x, long long x_ws, int act,
+                                              float *__restrict__ out, long long o_ws, int B) {
+  extern __shared__ float xs[];  // [WB][K]
+  const int tid = threadIdx.x, l = tid & 7;
+  const int win0 = blockIdx.y * WB, nw = B - win0 < WB ? B - win0 : WB;
+  for (int i = tid; i < WB * K; i += 256) {
+    const int wb = i / K, k = i - wb * K;
+    xs[i] = wb < nw ? x[(win0 + wb) * x_ws + k] : 0.f;
+  }
+  __syncthreads();
+  const int n = blockIdx.x * 32 + (tid >> 3);
+  const int nn = n < N ? n : N - 1;  // lanes past N compute a valid row, store nothing
+  const int K4 = K & ~3, K8 = K & ~7;
+  auto wat = [&](int k) -> float {
+    return W16 ? (float)hfrom(((const uint16_t *)wv)[(long long)nn * K + k]) : ((const float *)wv)[(long long)nn * K + k];
+  };
+  float a[WB];
+#pragma unroll
+  for (int wb = 0; wb < WB; wb++) a[wb] = 0.f;
+#pragma unroll 4
+  for (int k = l; k < K8; k += 8) {
+    const float w = wat(k);
+#pragma unroll
+    for (int wb = 0; wb < WB; wb++) a[wb] = __builtin_fmaf(w, xs[wb * K + k], a[wb]);
+  }
+  if (l < 4 && K8 + l < K4) {
+    const float w = wat(K8 + l);
+#pragma unroll
+    for (int wb = 0; wb < WB; wb++) a[wb] = __builtin_fmaf(w, xs[wb * K + K8 + l], a[wb]);
+  }
+#pragma unroll
+  for (int wb = 0; wb < WB; wb++) {
+    // lane l holds chain l: (c0 + c4) + (c1 + c5) and (c2 + c6) + (c3 + c7), then their sum
+    const float p4 = __shfl_down(a[wb], 4, 8);       // lanes 0..3: chain l + 4
+    const float s1 = a[wb] + p4;                       // lanes 0..3: c_l + c_{l+4}
+    const float q1 = __shfl_down(s1, 1, 8);            // lane 0: c1 + c5; lane 2: c3 + c7
+    const float s2 = s1 + q1;                          // lane 0: (c0+c4)+(c1+c5); lane 2: (c2+c6)+(c3+c7)
+    const float q2 = __shfl_down(s2, 2, 8);
+    float sum = s2 + q2;                               // lane 0: the pairwise total
+    if (l == 0 && n < N && wb < nw) {
+      for (int k = K4; k < K; k++) sum = sum + wat(k) * xs[wb * K + k];
+      const float v = sum + bias[n];
+      out[(win0 + wb) * o_ws + n] = act == 2 && v < 0.f ? 0.f : v;
+    }
+  }
 }
 
 // the device expf on its own (for its parity test against the C library)
@@ -199,6 +286,33 @@ __global__ void k_pad(const T *__restrict__ x, long long x_ws, int H, int W, int
   T v = (T)0;
   if (y >= 0 && y < H && xx >= 0 && xx < W) v = x[win * x_ws + ((long long)y * W + xx) * ld + c];
   xp[win * p_ws + e] = v;
+}
+
+
+static int se_launch(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
+                     const float *w2t, const float *b2, float *gate, long long g_ws, void *D, long long d_ws, int B,
+                     bool f16, void *stream) {
+  BNH_REQ(chsum && w1 && b1 && w2t && b2 && (gate || D) && B > 0);
+  BNH_REQ(C > 0 && C % 4 == 0 && C <= 4096 && rd > 0 && rd <= 512 && P > 0);
+  BNH_REQ(B == 1 || (c_ws >= C && (!gate || g_ws >= C) && (!D || d_ws >= (long long)P * C)));
+  // windows per block: as many as 64 KB of LDS holds, at most 4
+  const size_t per = sizeof(float) * (2 * (size_t)C + 9 * (size_t)rd);
+  int wg = (int)((64 * 1024) / per);
+  wg = wg >= 4 ? 4 : wg >= 2 ? 2 : 1;
+  if (wg > B) wg = B >= 4 ? 4 : B >= 2 ? 2 : 1;
+  const dim3 grid((unsigned)bnh_ceil_div(B, wg));
+  hipStream_t st = bnh_stream(stream);
+#define SE_LAUNCH(W, F)                                                                                                \
+  hipLaunchKernelGGL((k_se_f32<W, F>), grid, dim3(256), per * W, st, chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate,    \
+                     g_ws, D, d_ws, B)
+  if (f16) {
+    if (wg == 4) SE_LAUNCH(4, true); else if (wg == 2) SE_LAUNCH(2, true); else SE_LAUNCH(1, true);
+  } else {
+    if (wg == 4) SE_LAUNCH(4, false); else if (wg == 2) SE_LAUNCH(2, false); else SE_LAUNCH(1, false);
+  }
+#undef SE_LAUNCH
+  BNH_HIP(hipGetLastError());
+  return 0;
 }
 
 extern "C" {
@@ -237,36 +351,49 @@ int bnh_stem_f32_body(const float *img, long long i_ws, int H, int W, int k, int
   BNH_REQ(((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 3) == 0);
   BNH_REQ(B == 1 || (i_ws >= (long long)H * W && o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo));
   const long long per = (long long)Ho * Wo * (Np / 4);
-  hipLaunchKernelGGL(k_stem_f32, dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), dim3(256), 0, bnh_stream(stream),
-                     img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, act, out, o_ws, ldo, opad);
+  hipLaunchKernelGGL(k_stem_f32<false>, dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), dim3(256), 0,
+                     bnh_stream(stream), img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, act, (void *)out, o_ws, ldo, opad,
+                     Np);
   BNH_HIP(hipGetLastError());
   return 0;
 }
 
+int bnh_stem_f32to16_body(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
+                          const float *bias, int Kp, int N, int Np, int act, uint16_t *out, long long o_ws, int ldo,
+                          int opad, int B, void *stream) {
+  BNH_REQ(img && w && bias && out && B > 0 && k >= 1 && s >= 1 && Ho > 0 && Wo > 0 && N > 0 && N <= Np);
+  BNH_REQ((Ho - 1) * s + k <= H && (Wo - 1) * s + k <= W && Kp >= k * k && Kp % 4 == 0 && Np % 8 == 0);
+  BNH_REQ(ldo >= N && opad >= 0 && opad <= 3 && act >= 0 && act <= 2);
+  BNH_REQ(((uintptr_t)w & 15) == 0);
+  BNH_REQ(B == 1 || (i_ws >= (long long)H * W && o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo));
+  const long long per = (long long)Ho * Wo * (Np / 4);
+  hipLaunchKernelGGL(k_stem_f32<true>, dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), dim3(256), 0,
+                     bnh_stream(stream), img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, act, (void *)out, o_ws, ldo, opad,
+                     N);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_stem_f32to16(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
+                     const float *bias, int Kp, int N, int Np, int act, uint16_t *out, long long o_ws, int ldo, int opad,
+                     int B, void *stream) {
+  BNH_REQ(out && B > 0 && Ho > 0 && Wo > 0 && ldo > 0 && opad >= 0 && opad <= 3);
+  BNH_REQ(B == 1 || o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo);
+  if (opad && bnh_zero_halo(out, o_ws, Ho, Wo, ldo, opad, 2, B, stream)) return -1;
+  return bnh_stem_f32to16_body(img, i_ws, H, W, k, s, Ho, Wo, w, bias, Kp, N, Np, act, out, o_ws, ldo, opad, B, stream);
+}
+
+
 int bnh_se_f32(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
                const float *w2t, const float *b2, float *gate, long long g_ws, float *D, long long d_ws, int B,
                void *stream) {
-  BNH_REQ(chsum && w1 && b1 && w2t && b2 && (gate || D) && B > 0);
-  BNH_REQ(C > 0 && C % 4 == 0 && C <= 4096 && rd > 0 && rd <= 512 && P > 0);
-  BNH_REQ(B == 1 || (c_ws >= C && (!gate || g_ws >= C) && (!D || d_ws >= (long long)P * C)));
-  // windows per block: as many as 64 KB of LDS holds, at most 4
-  const size_t per = sizeof(float) * (2 * (size_t)C + 9 * (size_t)rd);
-  int wg = (int)((64 * 1024) / per);
-  wg = wg >= 4 ? 4 : wg >= 2 ? 2 : 1;
-  if (wg > B) wg = B >= 4 ? 4 : B >= 2 ? 2 : 1;
-  const dim3 grid((unsigned)bnh_ceil_div(B, wg));
-  hipStream_t st = bnh_stream(stream);
-#define SE_LAUNCH(W)                                                                                                   \
-  hipLaunchKernelGGL((k_se_f32<W>), grid, dim3(256), per * W, st, chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws,  \
-                     D, d_ws, B)
-  switch (wg) {
-    case 4: SE_LAUNCH(4); break;
-    case 2: SE_LAUNCH(2); break;
-    default: SE_LAUNCH(1); break;
-  }
-#undef SE_LAUNCH
-  BNH_HIP(hipGetLastError());
-  return 0;
+  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws, D, d_ws, B, false, stream);
+}
+
+int bnh_se_f16(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
+               const float *w2t, const float *b2, uint16_t *D, long long d_ws, int B, void *stream) {
+  BNH_REQ(D);
+  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, nullptr, 0, D, d_ws, B, true, stream);
 }
 
 int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
@@ -275,6 +402,38 @@ int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *ou
   BNH_REQ(B == 1 || (x_ws >= (long long)P * ld && o_ws >= C));
   hipLaunchKernelGGL(k_mean_f32, dim3((unsigned)bnh_ceil_div(C, 64), (unsigned)B), dim3(64), 0, bnh_stream(stream), x,
                      x_ws, P, C, ld, out, o_ws);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_mean_f16(const uint16_t *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
+                 void *stream) {
+  BNH_REQ(x && out && P > 0 && C > 0 && ld >= C && B > 0);
+  BNH_REQ(B == 1 || (x_ws >= (long long)P * ld && o_ws >= C));
+  hipLaunchKernelGGL(k_mean_f16, dim3((unsigned)bnh_ceil_div(C, 64), (unsigned)B), dim3(64), 0, bnh_stream(stream), x,
+                     x_ws, P, C, ld, out, o_ws);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_gemv(const void *w, int w16, const float *bias, int N, int K, const float *x, long long x_ws, int act,
+             float *out, long long o_ws, int B, void *stream) {
+  BNH_REQ(w && bias && x && out && N > 0 && K > 0 && B > 0 && (act == 0 || act == 2));
+  BNH_REQ(B == 1 || (x_ws >= K && o_ws >= N));
+  int wb = 8;
+  while (wb > 1 && (size_t)wb * K * sizeof(float) > 64 * 1024) wb /= 2;
+  BNH_REQ((size_t)K * sizeof(float) <= 64 * 1024);
+  const dim3 grid((unsigned)bnh_ceil_div(N, 32), (unsigned)bnh_ceil_div(B, wb));
+  const size_t lds = sizeof(float) * (size_t)wb * K;
+  hipStream_t st = bnh_stream(stream);
+#define GV(W, NB)                                                                                                      \
+  hipLaunchKernelGGL((k_gemv<W, NB>), grid, dim3(256), lds, st, w, bias, N, K, x, x_ws, act, out, o_ws, B)
+  if (w16) {
+    if (wb == 8) GV(true, 8); else if (wb == 4) GV(true, 4); else if (wb == 2) GV(true, 2); else GV(true, 1);
+  } else {
+    if (wb == 8) GV(false, 8); else if (wb == 4) GV(false, 4); else if (wb == 2) GV(false, 2); else GV(false, 1);
+  }
+#undef GV
   BNH_HIP(hipGetLastError());
   return 0;
 }

@@ -10,6 +10,13 @@ int rt_dev_tensors(rt_ctx *c, rt_op *op, int n);
 void rt_dev_fini(rt_op *op);
 static inline const uint16_t *dev_h(const rt_op *op, int i) { return *((uint16_t *const *)op->state + i); }
 int rt_pw_out_check(rt_ctx *c, rt_op *op, int dt);             // ops_s8n.cpp
+int rt_stem_check(rt_ctx *c, rt_op *op);                       // ops_f32.cpp
+int rt_mean_check(rt_ctx *c, rt_op *op);
+int rt_pad_check(rt_ctx *c, rt_op *op);
+int rt_pad_run(rt_ctx *c, rt_op *op, int esz);
+int rt_gemv_check(rt_ctx *c, rt_op *op, size_t esz);
+int rt_gemv_run(rt_ctx *c, rt_op *op, int w16);
+void *rt_dev_t(const rt_op *op, int i);
 
 // -------- PW f16: b = [in f16 [M][lda], out, res | -1]; t = [w (hpack panels), b32, b16];
 //          p = [N K Kp Np, M, lda, act, ldo, ow, opad, ldr]   (src/rt_ops_f16.c:14-27, 53-81; rt_pw_check,
@@ -50,7 +57,8 @@ static int pw16_init(rt_ctx *c, rt_op *op) {
     if (rt_need(c, op, 2, RT_F16, (size_t)M * ldr)) return RT_E_PARAM;
   }
   RT_REQ(c, op, lda % 8 == 0);  // 16-byte operand loads (every package pads rows to 8 channels)
-  s->W = bnh_h16w_new(N, K, Kp, Np, (const uint16_t *)rt_t(c, op, 0, nullptr), (const float *)rt_t(c, op, 1, nullptr));
+  s->W = bnh_h16w_new(N, K, Kp, Np, (const uint16_t *)rt_t(c, op, 0, nullptr), (const float *)rt_t(c, op, 1, nullptr),
+                      (const uint16_t *)rt_t(c, op, 2, nullptr));
   if (!s->W) return rt_oom(c, op, (size_t)Np * Kp * 2);
   return 0;
 }
@@ -59,7 +67,11 @@ static int pw16_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
   bnh_epi16 e = {p[6], (uint16_t *)rt_b(c, op, 1), rt_ws(c, op, 1), p[7], p[8], p[9], (const uint16_t *)rt_b(c, op, 2),
                  rt_ws(c, op, 2), p[10]};
-  return bnh_gemm_f16((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e, c->stream);
+  if (e.opad && !rt_halo_kept(c, op, 1)) {
+    const int H = p[4] / p[8];
+    if (bnh_zero_halo(e.out, e.out_ws, H, p[8], p[7], p[9], 2, c->nwin, c->stream)) return -1;
+  }
+  return bnh_gemm_f16_body((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e, c->stream);
 }
 
 // -------- DWK f16: as the fp32 op, fp16 buffers and tensors (src/rt_ops_f16.c:192-203)
@@ -89,7 +101,66 @@ static int dw3_run(rt_ctx *c, rt_op *op) {
                      (float *)rt_b(c, op, 2), rt_ws(c, op, 2), c->nwin, c->stream);
 }
 
+// -------- STEM, fp32 math, fp16 padded output: b = [img, out f16, col f32, tmp f32 [M][Np]]
+//          (src/rt_ops_f16.c:167-180); the kernel converts as it stores (no tmp pass)
+static int stem_init(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, 4, -1, -1) || rt_stem_check(c, op) || rt_need(c, op, 1, RT_F16, 1)) return RT_E_PARAM;
+  return rt_need(c, op, 3, RT_F32, (size_t)op->p[6] * op->p[7] * op->p[3]) ? RT_E_PARAM : 0;
+}
+static int stem_run(rt_ctx *c, rt_op *op) {
+  const int *p = op->p;
+  if (p[12] && !rt_halo_kept(c, op, 1) &&
+      bnh_zero_halo(rt_b(c, op, 1), rt_ws(c, op, 1), p[6], p[7], p[11], p[12], 2, c->nwin, c->stream))
+    return -1;
+  return bnh_stem_f32to16_body((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[4], p[5], p[8], p[9], p[6], p[7],
+                               (const float *)rt_dev_t(op, 0), (const float *)rt_dev_t(op, 1), p[2], p[0], p[3], p[10],
+                               (uint16_t *)rt_b(c, op, 1), rt_ws(c, op, 1), p[11], p[12], c->nwin, c->stream);
+}
+
+// -------- SE f16: b = [D f16 (in place), chsum]; t = [se1_w, se1_b, se2t, se2_b] (fp32); p = [C rd P]
+//          (src/rt_ops_f16.c:124-137, rt_se_check src/rt_ops_f32.c:256-266)
+static int se_init(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, 2, 4, 3)) return RT_E_PARAM;
+  const int C = op->p[0], rd = op->p[1], P = op->p[2];
+  RT_REQ(c, op, C > 0 && C % 8 == 0 && C <= 4096);
+  RT_REQ(c, op, rd > 0 && rd <= 512);
+  RT_REQ(c, op, P > 0);
+  const size_t want[4] = {(size_t)rd * C, (size_t)rd, (size_t)rd * C, (size_t)C};
+  for (int i = 0; i < 4; i++)
+    if (rt_need_t(c, op, i, want[i] * 4, 0)) return RT_E_PARAM;
+  if (rt_need(c, op, 0, RT_F16, (size_t)P * C) || rt_need(c, op, 1, RT_F32, (size_t)C)) return RT_E_PARAM;
+  return rt_dev_tensors(c, op, 4);
+}
+static int se_run(rt_ctx *c, rt_op *op) {
+  const int *p = op->p;
+  return bnh_se_f16((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_h(op, 0),
+                    (const float *)dev_h(op, 1), (const float *)dev_h(op, 2), (const float *)dev_h(op, 3),
+                    (uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
+}
+
+// -------- MEAN f16, PAD f16 (src/rt_ops_f16.c:204-214)
+static int mean_init(rt_ctx *c, rt_op *op) {
+  return rt_mean_check(c, op) || rt_need(c, op, 0, RT_F16, 1) ? RT_E_PARAM : 0;
+}
+static int mean_run(rt_ctx *c, rt_op *op) {
+  return bnh_mean_f16((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), op->p[0], op->p[1], op->p[2],
+                      (float *)rt_b(c, op, 1), rt_ws(c, op, 1), c->nwin, c->stream);
+}
+static int pad_init(rt_ctx *c, rt_op *op) {
+  return rt_pad_check(c, op) || rt_need(c, op, 0, RT_F16, 1) ? RT_E_PARAM : 0;
+}
+static int pad_run(rt_ctx *c, rt_op *op) { return rt_pad_run(c, op, 2); }
+
+// -------- GEMV with fp16 weights, fp32 math (src/rt_ops_f16.c:160-166)
+static int gemv_init(rt_ctx *c, rt_op *op) { return rt_gemv_check(c, op, 2); }
+static int gemv_run(rt_ctx *c, rt_op *op) { return rt_gemv_run(c, op, 1); }
+
 static const rt_kernel K_PW = {pw16_init, pw16_run, pw16_fini, "pw_f16", 0x2, 0x4};
+static const rt_kernel K_STEM = {stem_init, stem_run, rt_dev_fini, "stem_f32to16", 0xe, 0};
+static const rt_kernel K_SE = {se_init, se_run, rt_dev_fini, "se_f16", 0x1, 0};
+static const rt_kernel K_MEAN = {mean_init, mean_run, nullptr, "mean_f16", 0x2, 0};
+static const rt_kernel K_PAD = {pad_init, pad_run, nullptr, "pad_f16", 0x2, 0};
+static const rt_kernel K_GEMV = {gemv_init, gemv_run, rt_dev_fini, "gemv_h16", 0x2, 0};
 static const rt_kernel K_DW3 = {dw3_init, dw3_run, rt_dev_fini, "dw3_f16", 0x6, 0};
 static const rt_kernel K_DWK = {dwk_init, dwk_run, rt_dev_fini, "dwk_f16", 0x6, 0};
 
@@ -98,6 +169,11 @@ const rt_kernel *rt_k_f16(int base) {
     case RT_OP_PW: return &K_PW;
     case RT_OP_DW3: return &K_DW3;
     case RT_OP_DWK: return &K_DWK;
+    case RT_OP_STEM: return &K_STEM;
+    case RT_OP_SE: return &K_SE;
+    case RT_OP_MEAN: return &K_MEAN;
+    case RT_OP_PAD: return &K_PAD;
+    case RT_OP_GEMV: return &K_GEMV;
     default: return nullptr;
   }
 }

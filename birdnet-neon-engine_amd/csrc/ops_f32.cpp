@@ -118,8 +118,9 @@ static int logmel_run(rt_ctx *c, rt_op *op) {
 // -------- STEM: b = [img f32 [H][W], out, col]; t = [w panels [Np/8][Kp][8], b]; p = [N K Kp Np, H W Ho Wo k s act
 //          ldo opad]   (rt_stem_f32_check, src/rt_ops_f32.c:390-415). The im2col buffer (b[2]) is not used: the
 //          kernel reads the taps from the image directly.
-static int stem_init(rt_ctx *c, rt_op *op) {
-  if (rt_need_args(c, op, 3, 2, 13)) return RT_E_PARAM;
+// rt_stem_f32_check (src/rt_ops_f32.c:390-408), shared with the fp16 path's STEM
+int rt_stem_check(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, -1, 2, 13)) return RT_E_PARAM;
   const int *p = op->p;
   const int N = p[0], K = p[1], Kp = p[2], Np = p[3];
   if (N <= 0 || K <= 0 || Np != ((N + 7) & ~7) || Kp < K || Kp % 4)
@@ -140,10 +141,13 @@ static int stem_init(rt_ctx *c, rt_op *op) {
   if (o->halo != (uint32_t)h || o->ld != (uint32_t)ldo || (h && (o->W != (uint32_t)Wo || o->H != (uint32_t)Ho)))
     return rt_bad(c, op, "buffer argument 1 (buffer #%d, output): expected %d x %d, halo %d, ld %d; found %u x %u, halo "
                   "%u, ld %u", op->b[1], Ho, Wo, h, ldo, o->H, o->W, o->halo, o->ld);
-  if (rt_need(c, op, 1, (int)o->dtype, (size_t)(Ho + 2 * h) * (Wo + 2 * h) * ldo) || rt_need(c, op, 1, RT_F32, 1))
-    return RT_E_PARAM;
-  RT_REQ(c, op, ldo % 4 == 0);  // 4-channel output groups
+  if (rt_need(c, op, 1, (int)o->dtype, (size_t)(Ho + 2 * h) * (Wo + 2 * h) * ldo)) return RT_E_PARAM;
   return rt_dev_tensors(c, op, 2);
+}
+static int stem_init(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, 3, -1, -1) || rt_stem_check(c, op) || rt_need(c, op, 1, RT_F32, 1)) return RT_E_PARAM;
+  RT_REQ(c, op, op->p[11] % 4 == 0);  // 4-channel output groups
+  return 0;
 }
 static int stem_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
@@ -239,6 +243,27 @@ int rt_pad_run(rt_ctx *c, rt_op *op, int esz) {
 }
 static int pad_run(rt_ctx *c, rt_op *op) { return rt_pad_run(c, op, 4); }
 
+// -------- GEMV: b = [x f32 [K], out f32 [N]]; t = [w [N][K] (fp32; fp16 in the fp16 path), b f32 [N]];
+//          p = [N K act]   (rt_gemv_check, src/rt_ops_f32.c:593-601)
+int rt_gemv_check(rt_ctx *c, rt_op *op, size_t esz) {
+  if (rt_need_args(c, op, 2, 2, 3)) return RT_E_PARAM;
+  const int N = op->p[0], K = op->p[1];
+  RT_REQ(c, op, N > 0 && K > 0);
+  RT_REQ(c, op, op->p[2] == 0 || op->p[2] == 2);
+  if (rt_need_t(c, op, 0, (size_t)N * K * esz, 0) || rt_need_t(c, op, 1, (size_t)N * 4, 0)) return RT_E_PARAM;
+  if (rt_need(c, op, 0, RT_F32, (size_t)K) || rt_need(c, op, 1, RT_F32, (size_t)N)) return RT_E_PARAM;
+  RT_REQ(c, op, (size_t)K * 4 <= 64 * 1024);  // one window's input in LDS
+  return rt_dev_tensors(c, op, 2);
+}
+static int gemv_init(rt_ctx *c, rt_op *op) { return rt_gemv_check(c, op, 4); }
+int rt_gemv_run(rt_ctx *c, rt_op *op, int w16) {
+  return bnh_gemv(dev_tn(op, 0), w16, (const float *)dev_tn(op, 1), op->p[0], op->p[1], (const float *)rt_b(c, op, 0),
+                  rt_ws(c, op, 0), op->p[2], (float *)rt_b(c, op, 1), rt_ws(c, op, 1), c->nwin, c->stream);
+}
+static int gemv_run(rt_ctx *c, rt_op *op) { return rt_gemv_run(c, op, 0); }
+void *rt_dev_t(const rt_op *op, int i) { return dev_tn(op, i); }
+
+static const rt_kernel K_GEMV = {gemv_init, gemv_run, rt_dev_fini, "gemv_f32", 0x2, 0};
 static const rt_kernel K_LOGMEL = {logmel_init, logmel_run, logmel_fini, "fe_logmel", 0x2, 0};
 static const rt_kernel K_STEM = {stem_init, stem_run, rt_dev_fini, "stem_f32", 0x6, 0};
 static const rt_kernel K_SE = {se_init, se_run, rt_dev_fini, "se_f32", 0x1, 0};
@@ -258,6 +283,7 @@ const rt_kernel *rt_k_f32(int base) {
     case RT_OP_SE_GATE: return &K_SE_GATE;
     case RT_OP_MEAN: return &K_MEAN;
     case RT_OP_PAD: return &K_PAD;
+    case RT_OP_GEMV: return &K_GEMV;
     default: return nullptr;
   }
 }

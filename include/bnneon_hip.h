@@ -40,7 +40,8 @@ int bnh_copy(void *dst, const void *src, size_t bytes, void *stream);
 
 /* ------------------------------------------------------------------ scalar numerics checks
  * y[i] = f(x[i]) on the device for n elements, f = 0: FRECPE, 1: the fp32 SiLU of the epilogues
- * (src/gemm_f32.h:102-118), 2: ReLU (vmaxq_f32 with 0). Used to pin the device numerics against the oracle. */
+ * (src/gemm_f32.h:102-118) in the form the kernels use (FRECPE's estimate from an LDS table), 2: ReLU (vmaxq_f32
+ * with 0), 3: the same SiLU without the table. Used to pin the device numerics against the oracle. */
 int bnh_eval_f32(int f, const float *x, float *y, long long n, void *stream);
 /* y[i] = the Q31 requantisation of the int8 GEMM / depthwise below applied to acc[i] with mult[i], shift[i] (0..31),
  * zy, clamp [lo, hi]: pins the device fixed-point arithmetic against the oracle */
@@ -118,10 +119,11 @@ int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M
 
 /* ------------------------------------------------------------------ fp16 GEMM (PW f16)
  * Weights from the package tensors of an fp16 GEMM (hp_pack, src/gemm_f16.c:18-40; validated as hpack_view,
- * src/rt_ops_f16.c:14-27): w fp16 [Np/16][Kp][16] then, if Np % 16, a tail panel [Kp][8]; b32 f32 [>= Np].
- * Repacked once into channel rows in HBM. */
+ * src/rt_ops_f16.c:14-27): w fp16 [Np/16][Kp][16] then, if Np % 16, a tail panel [Kp][8]; b32 f32 [>= Np];
+ * b16 fp16 [>= Np], the package's fp16 bias (NULL: b32 rounded to nearest even). Repacked once into channel rows
+ * in HBM. */
 typedef struct bnh_h16w bnh_h16w;
-bnh_h16w *bnh_h16w_new(int N, int K, int Kp, int Np, const uint16_t *w, const float *b32);
+bnh_h16w *bnh_h16w_new(int N, int K, int Kp, int Np, const uint16_t *w, const float *b32, const uint16_t *b16);
 void bnh_h16w_free(bnh_h16w *W);
 /* the fp16 epilogue (epi16, src/gemm_f16.h:19-27, without the pooled form), per-window strides in elements */
 typedef struct {
@@ -135,10 +137,14 @@ typedef struct {
 } bnh_epi16;
 /* gemm_f16 (src/gemm_f16.c:124-171; the PW f16 op run, src/rt_ops_f16.c:65-81): out rows [0, M) x channels [0, Np)
  * of act(A . W^T + b) (+ res) for B windows of fp16 rows A [M][lda] (lda >= Kp, lda % 8 == 0; zero-haloed output
- * zeroed when opad). fp16 MFMA with fp32 accumulation: within the fp16 accumulation error bound of the reference
- * (which accumulates in fp16 over K blocks of <= 128 steps), not bit-identical. */
+ * zeroed when opad). Bit-identical to the reference: fp16 FMA chains over its K blocks (packed fp16 FMAs on the
+ * VALU), fp32 sums across blocks, its bias and epilogue. */
 int bnh_gemm_f16(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
                  void *stream);
+/* the same product on fp16 MFMA with fp32 accumulation over the whole K (no reference counterpart: a faster form
+ * for callers that accept the fp16 accumulation error bound of the reference instead of its exact bits) */
+int bnh_gemm_f16_mfma(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
+                      void *stream);
 
 /* ------------------------------------------------------------------ fp16 Winograd F(2x2, 3x3) convolution
  * The Winograd / fp16 GEMM path (src/wino_s0.c:1-165 for the transforms, src/wino.c for the tiling): a 3 x 3,
@@ -225,6 +231,22 @@ int bnh_stem_f32(const float *img, long long i_ws, int H, int W, int k, int s, i
 int bnh_se_f32(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
                const float *w2t, const float *b2, float *gate, long long g_ws, float *D, long long d_ws, int B,
                void *stream);
+/* STEM of the fp16 path: replaces stem_run (src/rt_ops_f16.c:167-180): the fp32 stem above, then channels < N
+ * rounded to fp16 into out fp16 [Ho+2opad][Wo+2opad][ldo] (halo zeroed; channels N..ldo untouched) */
+int bnh_stem_f32to16(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
+                     const float *bias, int Kp, int N, int Np, int act, uint16_t *out, long long o_ws, int ldo, int opad,
+                     int B, void *stream);
+/* SE of the fp16 path: replaces se_run (src/rt_ops_f16.c:125-137; v24k16_se, src/v24_fast.c:182-234): the gate as
+ * bnh_se_f32 computes it but with a dividing sigmoid, rounded to fp16; D fp16 [P][C] multiplied by it in fp16 */
+int bnh_se_f16(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
+               const float *w2t, const float *b2, uint16_t *D, long long d_ws, int B, void *stream);
+/* MEAN of fp16 rows: replaces pc_mean_f16 (src/pc_kern_f16.c:115-121) */
+int bnh_mean_f16(const uint16_t *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
+                 void *stream);
+/* GEMV: replaces bnn_gemv_f32 / bnn_gemv_h16 (src/gemv.c:13-49): out [N] = act(b + W x), W [N][K] fp32 (w16 = 0) or
+ * fp16 (w16 = 1) weights, fp32 arithmetic in the reference's lane order; act 0 or 2 (ReLU) */
+int bnh_gemv(const void *w, int w16, const float *bias, int N, int K, const float *x, long long x_ws, int act,
+             float *out, long long o_ws, int B, void *stream);
 /* MEAN: replaces pc_mean_f32 (src/pc_kern_f32.c:342-348): out [C] = (sum over P rows of x [P][ld]) / P */
 int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
                  void *stream);

@@ -288,3 +288,81 @@ void orc_pad(const void *x, int H, int W, int C, int ld, int h, size_t esz, void
 void orc_expf_n(const float *x, float *y, long long n) {
   for (long long i = 0; i < n; i++) y[i] = expf(x[i]);
 }
+
+/* ---------------------------------------------------------------- fp16-path forms (variant 1) */
+/* STEM with fp16 output (src/rt_ops_f16.c:167-180): the fp32 stem into [M][Np] rows, then channels < N rounded to
+ * fp16 (vcvt_f16_f32, nearest even) into the padded output (pc_cvt_pad_f16, src/pc_kern_f16.c:104-113); the halo is
+ * zeroed first, channels N..ldo untouched */
+void orc_stem_f32to16(const float *img, int H, int W, int k, int s, int Ho, int Wo, const float *w, const float *b, int Kp,
+                      int N, int Np, int act, uint16_t *out, int ldo, int opad) {
+  float *tmp = calloc((size_t)Ho * Wo * Np + 8, sizeof(float));
+  orc_epi32 e = {act, tmp, Np, 0, 0, NULL, 0, 0, 0};
+  orc_stem_f32(img, H, W, k, s, Ho, Wo, w, b, Kp, Np, &e);
+  if (opad) orc_zero_halo(out, Ho, Wo, ldo, opad, 2);
+  for (int m = 0; m < Ho * Wo; m++) {
+    uint16_t *o = out + ((size_t)(m / Wo + opad) * (Wo + 2 * opad) + m % Wo + opad) * ldo;
+    for (int c = 0; c < N; c++) o[c] = orc_f2h(tmp[(size_t)m * Np + c]);
+  }
+  free(tmp);
+}
+
+/* SE fp16 (v24k16_se_gate + v24k16_se_scale, src/v24_fast.c:182-234): the fp32 gate of the fp32 SE with a sigmoid
+ * that divides (sigm4: 1 / (1 + exp2_f32x4 value), IEEE division), rounded to fp16; D (fp16) multiplied by it in
+ * fp16 */
+void orc_se_f16(uint16_t *D, int P, int C, const float *chsum, int rd, const float *w1, const float *b1, const float *w2t,
+                const float *b2) {
+  float *mean = malloc(sizeof(float) * C), *s1 = malloc(sizeof(float) * rd);
+  uint16_t *g = malloc(sizeof(uint16_t) * C);
+  const float inv = 1.f / (float)P;
+  for (int c = 0; c < C; c++) mean[c] = chsum[c] * inv;
+  for (int r = 0; r < rd; r++) {
+    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const float *w = w1 + (size_t)r * C;
+    int c = 0;
+    for (; c + 8 <= C; c += 8)
+      for (int l = 0; l < 8; l++) a[l] = fmaf(w[c + l], mean[c + l], a[l]);
+    for (; c < C; c += 4)
+      for (int l = 0; l < 4; l++) a[l] = fmaf(w[c + l], mean[c + l], a[l]);
+    const float x = (((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]))) + b1[r];
+    s1[r] = x / (1.f + expf(-x));
+  }
+  for (int c = 0; c < C; c++) {
+    float v = b2[c];
+    for (int r = 0; r < rd; r++) v = fmaf(w2t[(size_t)r * C + c], s1[r], v);
+    g[c] = orc_f2h(1.f / (1.f + orc_exp2_f32(v * -1.44269504f)));
+  }
+  for (int p = 0; p < P; p++)
+    for (int c = 0; c < C; c++) D[(size_t)p * C + c] = orc_h_mul(D[(size_t)p * C + c], g[c]);
+  free(mean); free(s1); free(g);
+}
+
+/* pc_mean_f16 (src/pc_kern_f16.c:115-121): fp32 sums of the widened values from +0 in p order, divided by P */
+void orc_mean_f16(const uint16_t *x, int P, int C, int ld, float *out) {
+  for (int c = 0; c < C; c++) {
+    float s = 0.f;
+    for (int p = 0; p < P; p++) s = s + orc_h2f(x[(size_t)p * ld + c]);
+    out[c] = s / (float)P;
+  }
+}
+
+/* bnn_gemv_f32 / bnn_gemv_h16 (src/gemv.c:13-49): eight lane chains over k < K & ~7 (two 4-lane accumulators), the
+ * K & ~3 remainder into the first, pairwise sum, then the scalar tail (product and sum rounded apart), + b, ReLU
+ * as v < 0 ? 0 : v. w16 (or NULL) holds fp16 weights, else w32. */
+void orc_gemv(const float *w32, const uint16_t *w16, const float *b, int N, int K, const float *x, int act, float *out) {
+  const int K4 = K & ~3, K8 = K & ~7;
+  for (int n = 0; n < N; n++) {
+    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < K; k++) {
+      const float wv = w16 ? orc_h2f(w16[(size_t)n * K + k]) : w32[(size_t)n * K + k];
+      if (k < K8) a[k % 8] = fmaf(wv, x[k], a[k % 8]);
+      else if (k < K4) a[k % 4] = fmaf(wv, x[k], a[k % 4]);
+    }
+    float s = ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]));
+    for (int k = K4; k < K; k++) {
+      const float wv = w16 ? orc_h2f(w16[(size_t)n * K + k]) : w32[(size_t)n * K + k];
+      s = s + wv * x[k];
+    }
+    const float v = s + b[n];
+    out[n] = act == 2 && v < 0.f ? 0.f : v;
+  }
+}

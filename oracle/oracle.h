@@ -166,6 +166,15 @@ void orc_se_f32(float *D, int P, int C, const float *chsum, int rd, const float 
 void orc_mean_f32(const float *x, int P, int C, int ld, float *out);  /* src/pc_kern_f32.c:342-348 */
 void orc_pad(const void *x, int H, int W, int C, int ld, int h, size_t esz, void *xp);  /* PAD, src/rt_ops_f32.c:503-508 */
 void orc_expf_n(const float *x, float *y, long long n);  /* the C library's expf, elementwise */
+/* STEM fp16 out (src/rt_ops_f16.c:167-180) */
+void orc_stem_f32to16(const float *img, int H, int W, int k, int s, int Ho, int Wo, const float *w, const float *b, int Kp,
+                      int N, int Np, int act, uint16_t *out, int ldo, int opad);
+/* SE fp16 in place (src/v24_fast.c:182-234) */
+void orc_se_f16(uint16_t *D, int P, int C, const float *chsum, int rd, const float *w1, const float *b1, const float *w2t,
+                const float *b2);
+void orc_mean_f16(const uint16_t *x, int P, int C, int ld, float *out);  /* src/pc_kern_f16.c:115-121 */
+/* GEMV with fp32 (w16 NULL) or fp16 weights (src/gemv.c:13-49) */
+void orc_gemv(const float *w32, const uint16_t *w16, const float *b, int N, int K, const float *x, int act, float *out);
 
 #ifdef __cplusplus
 }

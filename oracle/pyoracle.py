@@ -283,12 +283,13 @@ _SIGS.update({
 })
 
 
-def gemm_f16(A, W, b32, act=0, ldo=None, ow=0, opad=0, res=None, M=None):
-    """orc_gemm_f16: A fp16 [M][lda] (lda >= Kp), W fp16 [N][Kp] -> out fp16 rows [(padded) M][ldo]."""
+def gemm_f16(A, W, b32, act=0, ldo=None, ow=0, opad=0, res=None, M=None, b16=None):
+    """orc_gemm_f16: A fp16 [M][lda] (lda >= Kp), W fp16 [N][Kp] -> out fp16 rows [(padded) M][ldo]; b16 the
+    fp16 bias (default: b32 rounded to nearest even)."""
     A = _c(A, np.float16)
     W = _c(W, np.float16)
     b32 = _c(b32, np.float32)
-    b16 = b32.astype(np.float16)
+    b16 = b32.astype(np.float16) if b16 is None else _c(b16, np.float16)
     M = A.shape[0] if M is None else M
     lda = A.shape[1]
     N, Kp = W.shape

@@ -1,12 +1,17 @@
 """GPU parity of the fp16 pointwise GEMM (libbnneon's gemm_f16 / PW f16 op).
 
-The GPU accumulates on fp16 MFMA in fp32; the reference (the oracle restates
-it) accumulates in fp16 within K blocks of <= 128 steps. Stated tolerance, per
-output before the activation: |gpu - oracle| <= (n + 2) 2^-11 S + 2^-10 |oracle|
-+ 2^-24, n = the reference's K-block length, S = sum_k |a_k w_k| + |b| (the
-recursive-summation bound of the reference's fp16 chain plus one rounding of
-each result); with small-integer operands every operation of both is exact and
-the outputs are bit-identical, through every epilogue form.
+bnh_gemm_f16 computes in the reference's own arithmetic (fp16 FMA chains over
+its K blocks, fp32 sums across blocks, its bias and epilogue): bit-identical to
+the oracle (oracle/f16gemm.c) on random data, overflow to infinity, NaN inputs,
+every epilogue form, one and several K blocks, the 8-channel tail panel and the
+package's own fp16 bias.
+
+bnh_gemm_f16_mfma accumulates on fp16 MFMA in fp32 instead. Stated tolerance,
+per output before the activation: |gpu - oracle| <= (n + 2) 2^-11 S +
+2^-10 |oracle| + 2^-24, n = the reference's K-block length, S = sum_k |a_k w_k|
++ |b| (the recursive-summation bound of the reference's fp16 chain plus one
+rounding of each result); with small-integer operands every operation of both
+is exact and the outputs are bit-identical.
 """
 import numpy as np
 import pytest
@@ -28,14 +33,20 @@ def hpack(W, Kp):
     out = np.zeros(Np * Kp, np.float16)
     for o in range(N):
         nb, j = o // 16, o % 16
-        for k in range(K):
-            idx = (nb * Kp + k) * 16 + j if nb < n16 else n16 * Kp * 16 + k * 8 + j
-            out[idx] = W[o, k]
+        idx = (nb * Kp + np.arange(K)) * 16 + j if nb < n16 else n16 * Kp * 16 + np.arange(K) * 8 + j
+        out[idx] = W[o, :K]
     return out
 
 
-def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, B=1, Kp=None):
-    """A [B][M][lda] fp16 -> out [B][rows][ldo] fp16 through bnh_gemm_f16."""
+def same_bits(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    an, bn = np.isnan(a), np.isnan(b)
+    return bool(np.array_equal(an, bn) and np.array_equal(a.view(np.uint16)[~an], b.view(np.uint16)[~bn]))
+
+
+def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, Kp=None, b16=None, fn="bnh_gemm_f16"):
+    """A [B][M][lda] fp16 -> out [B][rows][ldo] fp16 through fn (bnh_gemm_f16 or bnh_gemm_f16_mfma)."""
     H = hip
     Bw, M, lda = A.shape
     N, K = W.shape
@@ -45,8 +56,13 @@ def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, B=1, Kp=None):
     Wp[:, :K] = W
     bpad = np.zeros(Np + 16, np.float32)
     bpad[:N] = b32
+    b16p = None
+    if b16 is not None:
+        b16p = np.zeros(Np + 16, np.float16)
+        b16p[:N] = b16
     hp = hpack(Wp, Kp)   # kept alive across the call (a temporary's buffer could be freed before it runs)
-    hw = H.lib().bnh_h16w_new(N, K, Kp, Np, hp.ctypes.data, bpad.ctypes.data)
+    hw = H.lib().bnh_h16w_new(N, K, Kp, Np, hp.ctypes.data, bpad.ctypes.data,
+                              None if b16p is None else b16p.ctypes.data)
     if not hw:
         H.check(None, "bnh_h16w_new")
     try:
@@ -65,9 +81,11 @@ def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, B=1, Kp=None):
             r_ws = M * ldr
             dR = H.DeviceArray.from_host(res.reshape(Bw, -1))
         e = H.Epi16(act, dO.ptr, o_ws, ldo, ow, opad, dR.ptr if dR else None, r_ws, res.shape[2] if res is not None else 0)
-        H.check(H.lib().bnh_gemm_f16(dA.ptr, a_ws, lda, M, Bw, hw, e, None), "gemm_f16")
+        H.check(getattr(H.lib(), fn)(dA.ptr, a_ws, lda, M, Bw, hw, e, None), fn)
         H.sync()
-        return dO.numpy()[:, :rows * ldo].reshape(Bw, rows, ldo), Wp
+        out = dO.numpy()
+        assert (out[:, rows * ldo:] == 7.0).all()   # nothing past each window's output
+        return out[:, :rows * ldo].reshape(Bw, rows, ldo), Wp
     finally:
         H.lib().bnh_h16w_free(hw)
 
@@ -80,15 +98,59 @@ def test_small_integers_bit_exact(hip, act):
     W = rng.integers(-2, 3, (N, K)).astype(np.float16)
     b = rng.integers(-9, 10, N).astype(np.float32)
     res = rng.integers(-4, 5, (B, M, 24)).astype(np.float16)
-    say("f16 gemm ints act", act)
-    out, Wp = run_gpu(hip, A, W, b, act=act, res=res, B=B)
+    for fn in ("bnh_gemm_f16", "bnh_gemm_f16_mfma"):
+        say("f16 gemm ints act", act, fn)
+        out, Wp = run_gpu(hip, A, W, b, act=act, res=res, fn=fn)
+        for i in range(B):
+            ref = O.gemm_f16(A[i], Wp, b, act=act, res=res[i])
+            assert np.array_equal(out[i].view(np.uint16), ref.view(np.uint16)), (fn, i)
+
+
+# (K, N, M, B): one K block (K <= 128), two (136: 72 + 64), three (300 -> 104 + 104 + 92), the v2.4 expansion
+# and projection shapes (36 -> 288 etc.), N with an 8-channel tail panel, M not a multiple of 64
+@pytest.mark.parametrize("K,N,M,B", [(64, 48, 100, 2), (200, 136, 64, 2), (1152, 256, 70, 2), (24, 8, 7, 3),
+                                     (300, 200, 129, 2), (36, 288, 64 * 24, 2), (864, 108, 383, 2), (128, 1024, 96, 2)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_random_bit_exact(hip, K, N, M, B, act):
+    rng = np.random.default_rng(K + N + act)
+    Kp = (K + 7) // 8 * 8
+    A = np.zeros((B, M, Kp), np.float16)
+    A[:, :, :K] = rng.standard_normal((B, M, K))
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    Np = (N + 7) // 8 * 8
+    res = rng.standard_normal((B, M, Np)).astype(np.float16) if act == 0 else None
+    say("f16 gemm random", K, N, M, B, act)
+    out, Wp = run_gpu(hip, A, W, b, act=act, res=res)
     for i in range(B):
-        ref = O.gemm_f16(A[i], Wp, b, act=act, res=res[i])
-        assert np.array_equal(out[i].view(np.uint16), ref.view(np.uint16)), i
+        ref = O.gemm_f16(A[i], Wp, b, act=act, res=None if res is None else res[i])
+        assert same_bits(out[i], ref), i
+
+
+@pytest.mark.parametrize("K", [96, 264])
+def test_package_fp16_bias_overflow_and_nan(hip, K):
+    """The package's own fp16 bias (used alone by a single K block, the fp32 one by several), fp16 overflow to
+    +-inf inside a chain, a NaN operand."""
+    rng = np.random.default_rng(K)
+    B, M, N = 2, 72, 40
+    A = rng.standard_normal((B, M, K)).astype(np.float16)
+    A[0, 3, :] = 200.0           # 200 * 100 * K overflows the fp16 chain
+    A[1, 5, 7] = np.nan
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    W[2, :] = 100.0
+    W[3, :] = -100.0
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    b16 = (b * 3 + 0.25).astype(np.float16)   # deliberately not b32 rounded
+    say("f16 gemm bias/overflow", K)
+    out, Wp = run_gpu(hip, A, W, b, act=2, b16=b16)
+    for i in range(B):
+        ref = O.gemm_f16(A[i], Wp, b, act=2, b16=np.pad(b16, (0, 8)))
+        assert same_bits(out[i], ref), i
+    assert np.isinf(out[0, 3, 2]) and np.isnan(out[1, 5]).any()
 
 
 @pytest.mark.parametrize("K,N,M", [(64, 48, 100), (200, 136, 64), (1152, 256, 256), (24, 8, 7)])
-def test_random_within_stated_tolerance(hip, K, N, M):
+def test_mfma_within_stated_tolerance(hip, K, N, M):
     rng = np.random.default_rng(K + N)
     B = 2
     Kp = (K + 7) // 8 * 8
@@ -96,8 +158,8 @@ def test_random_within_stated_tolerance(hip, K, N, M):
     A[:, :, :K] = rng.standard_normal((B, M, K))
     W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
     b = (rng.standard_normal(N) * 0.1).astype(np.float32)
-    say("f16 gemm random", K, N, M)
-    out, Wp = run_gpu(hip, A, W, b, B=B)
+    say("f16 gemm mfma random", K, N, M)
+    out, Wp = run_gpu(hip, A, W, b, fn="bnh_gemm_f16_mfma")
     nblk = (Kp + 127) // 128
     n = ((Kp + nblk - 1) // nblk + 7) // 8 * 8
     for i in range(B):
@@ -113,21 +175,35 @@ def test_random_within_stated_tolerance(hip, K, N, M):
         assert (np.abs(g - exact) <= 2.0 ** -10 * np.abs(exact) + 2.0 ** -24 + Kp * 2.0 ** -24 * S).all()
 
 
-def test_padded_output_and_silu(hip):
+@pytest.mark.parametrize("fn", ["bnh_gemm_f16", "bnh_gemm_f16_mfma"])
+def test_padded_output_and_silu(hip, fn):
     rng = np.random.default_rng(5)
     B, M, N, K, ow = 2, 48, 32, 64, 8
     A = rng.integers(-2, 3, (B, M, K)).astype(np.float16)
     W = rng.integers(-2, 3, (N, K)).astype(np.float16)
     b = rng.integers(-3, 4, N).astype(np.float32)
-    say("f16 gemm padded")
-    out, Wp = run_gpu(hip, A, W, b, act=1, ow=ow, opad=2, B=B)
+    say("f16 gemm padded", fn)
+    out, Wp = run_gpu(hip, A, W, b, act=1, ow=ow, opad=2, fn=fn)
     for i in range(B):
         ref = O.gemm_f16(A[i], Wp, b, act=1, ow=ow, opad=2)
         assert np.array_equal(out[i].view(np.uint16), ref.view(np.uint16))
 
 
+def test_padded_random_bit_exact(hip):
+    rng = np.random.default_rng(6)
+    B, ow, oh, N, K = 3, 64, 24, 72, 36
+    M = ow * oh
+    A = rng.standard_normal((B, M, 40)).astype(np.float16)   # K 36 -> Kp 40 = lda
+    W = (rng.standard_normal((N, K)) / 6).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    say("f16 gemm padded random")
+    out, Wp = run_gpu(hip, A, W, b, act=1, ow=ow, opad=1)
+    for i in range(B):
+        assert same_bits(out[i], O.gemm_f16(A[i], Wp, b, act=1, ow=ow, opad=1)), i
+
+
 def test_bad_params_refused(hip):
     H = hip
     w, b = np.zeros(256, np.float16), np.zeros(32, np.float32)
-    assert not H.lib().bnh_h16w_new(10, 16, 16, 10, w.ctypes.data, b.ctypes.data)
+    assert not H.lib().bnh_h16w_new(10, 16, 16, 10, w.ctypes.data, b.ctypes.data, None)
     assert b"Np = N rounded up to 8" in H.lib().bnh_last_error()
