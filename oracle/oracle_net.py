@@ -13,6 +13,18 @@ import pyoracle as O
 DT = {0: np.float32, 1: np.float16, 2: np.int8, 3: np.int32}
 OP_FE_LOGMEL, OP_STEM, OP_DW3, OP_DWK, OP_PAD, OP_MEAN = 8, 9, 4, 10, 11, 12
 OP_SE, OP_SE_GATE, OP_PW_S8, OP_GEMV_S8, OP_PROTO_S8 = 5, 25, 22, 23, 35
+OP_PW, OP_GEMV = 3, 15
+
+
+def unpack_h16(panels, N, Kp, Np):
+    """fp16 weights [N][Kp] from hp_pack's panels [Np/16][Kp][16] + tail [Kp][8] (src/gemm_f16.c:18-40)."""
+    panels = np.asarray(panels).view(np.float16).reshape(-1)
+    n16 = Np // 16
+    W = np.zeros((Np, Kp), np.float16)
+    W[:n16 * 16] = panels[:n16 * Kp * 16].reshape(n16, Kp, 16).transpose(0, 2, 1).reshape(n16 * 16, Kp)
+    if Np % 16:
+        W[n16 * 16:] = panels[n16 * Kp * 16:n16 * Kp * 16 + Kp * 8].reshape(Kp, 8).T
+    return W[:N]
 
 
 class OracleNet:
@@ -51,48 +63,76 @@ class OracleNet:
         spec = O.logmel(bufs[b[0]][:nsamp], frame, hop, pad, nfft, t[0], t[1].reshape(nmel, -1), t[2][0], t[2][1])
         self.put(bufs[b[1]], spec)
 
-    # STEM
+    # STEM (variant 1: fp32 math, fp16 output)
     def op_9(self, var, b, t, p, bufs):
         N, K, Kp, Np, H, W, Ho, Wo, k, s, act, ldo, opad = p
-        out = O.stem_f32(bufs[b[0]][:H * W].reshape(H, W), k, s, t[0], t[1], Kp, Np, act=act, opad=opad, ldo=ldo)
+        img = bufs[b[0]][:H * W].reshape(H, W)
+        if var == 1:
+            out = O.stem_f32to16(img, k, s, t[0], t[1], Kp, N, Np, act=act, opad=opad, ldo=ldo)
+        else:
+            out = O.stem_f32(img, k, s, t[0], t[1], Kp, Np, act=act, opad=opad, ldo=ldo)
         self.put(bufs[b[1]], out)
 
-    # DW3 (fp32)
+    # DW3 (variant 1: fp16 with TF-same offsets)
     def op_4(self, var, b, t, p, bufs):
-        assert var == 0
         H, W, C, s, Ho, Wo = p[:6]
-        out, cs = O.dw3_f32(bufs[b[0]][:(H + 2) * (W + 2) * C], H, W, C, s, t[0], t[1], Ho, Wo)
+        xp = bufs[b[0]][:(H + 2) * (W + 2) * C]
+        if var == 1:
+            out, cs = O.dw3_f16(xp, H, W, C, s, p[6], p[7], t[0], t[1], Ho, Wo)
+        else:
+            out, cs = O.dw3_f32(xp, H, W, C, s, t[0], t[1], Ho, Wo)
         self.put(bufs[b[1]], out)
         self.put(bufs[b[2]], cs)
 
-    # DWK (fp32)
+    # DWK (variant 1: fp16)
     def op_10(self, var, b, t, p, bufs):
-        assert var == 0
         H, W, C, k, s, pt, pl, Ho, Wo, act = p
         h = (k - 1) // 2
-        out, cs = O.dwk_f32(bufs[b[0]][:(H + 2 * h) * (W + 2 * h) * C], H, W, C, k, s, pt, pl, t[0], t[1], act, Ho,
-                            Wo)
+        xp = bufs[b[0]][:(H + 2 * h) * (W + 2 * h) * C]
+        f = O.dwk_f16 if var == 1 else O.dwk_f32
+        out, cs = f(xp, H, W, C, k, s, pt, pl, t[0], t[1], act, Ho, Wo)
         self.put(bufs[b[1]], out)
         self.put(bufs[b[2]], cs)
+
+    # PW (variant 1: the fp16 GEMM)
+    def op_3(self, var, b, t, p, bufs):
+        assert var == 1
+        N, K, Kp, Np, M, lda, act, ldo, ow, opad, ldr = p
+        W = unpack_h16(t[0], N, Kp, Np)
+        res = None if b[2] < 0 else bufs[b[2]][:M * ldr].reshape(M, ldr)
+        out = O.gemm_f16(bufs[b[0]][:M * lda].reshape(M, lda), W, t[1][:N], act=act, ldo=ldo, ow=ow, opad=opad,
+                         res=res, b16=np.asarray(t[2]).view(np.float16)[:Np])
+        self.put(bufs[b[1]], out)
+
+    # GEMV (variant 0: fp32 weights, 1: fp16 weights)
+    def op_15(self, var, b, t, p, bufs):
+        N, K, act = p
+        w = np.asarray(t[0]).view(np.float16 if var == 1 else np.float32).reshape(N, K)
+        self.put(bufs[b[1]], O.gemv(w, t[1], bufs[b[0]][:K], act))
 
     # PAD
     def op_11(self, var, b, t, p, bufs):
         H, W, C, ld, h = p
         self.put(bufs[b[1]], O.pad(bufs[b[0]][:H * W * ld].reshape(H * W, ld), H, W, C, h))
 
-    # MEAN
+    # MEAN (variant 1: of fp16 rows)
     def op_12(self, var, b, t, p, bufs):
         P_, C, ld = p
-        self.put(bufs[b[1]], O.mean_f32(bufs[b[0]][:P_ * ld].reshape(P_, ld), C))
+        f = O.mean_f16 if var == 1 else O.mean_f32
+        self.put(bufs[b[1]], f(bufs[b[0]][:P_ * ld].reshape(P_, ld), C))
 
     # SE_GATE
     def op_25(self, var, b, t, p, bufs):
         C, rd, P_ = p
         self.put(bufs[b[1]], O.se_gate_f32(bufs[b[0]][:C], P_, t[0].reshape(rd, C), t[1], t[2], t[3]))
 
-    # SE (in place)
+    # SE (in place; variant 1: the fp16 path's)
     def op_5(self, var, b, t, p, bufs):
         C, rd, P_ = p
+        if var == 1:
+            D = bufs[b[0]][:P_ * C].reshape(P_, C)
+            bufs[b[0]][:P_ * C] = O.se_f16(D, bufs[b[1]][:C], t[0].reshape(rd, C), t[1], t[2], t[3]).reshape(-1)
+            return
         g = O.se_gate_f32(bufs[b[1]][:C], P_, t[0].reshape(rd, C), t[1], t[2], t[3])
         D = bufs[b[0]][:P_ * C].reshape(P_, C)
         bufs[b[0]][:P_ * C] = (D * g[None, :]).reshape(-1)

@@ -459,3 +459,55 @@ def pad(x, H, W, C_, h):
     out = np.full(((H + 2 * h) * (W + 2 * h), C_), 7, x.dtype)
     lib().orc_pad(P(x), H, W, C_, ld, h, x.dtype.itemsize, P(out))
     return out
+
+
+_SIGS.update({
+    "orc_stem_f32to16": (None, [vp, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i32, i32]),
+    "orc_se_f16": (None, [vp, i32, i32, vp, i32, vp, vp, vp, vp]),
+    "orc_mean_f16": (None, [vp, i32, i32, i32, vp]),
+    "orc_gemv": (None, [vp, vp, vp, i32, i32, vp, i32, vp]),
+})
+
+
+def stem_f32to16(img, k, s, panels, bb, Kp, N, Np, act=1, opad=0, ldo=None, fill=0):
+    """The fp16 path's STEM: fp32 stem, then fp16 channels [0, N) of a zero-haloed output [rows][ldo]; the other
+    channels keep `fill`."""
+    img = _c(img, np.float32)
+    H, W = img.shape
+    Ho, Wo = (H - k) // s + 1, (W - k) // s + 1
+    ldo = ldo or Np
+    out = np.full(((Ho + 2 * opad) * (Wo + 2 * opad), ldo), fill, np.float16)
+    lib().orc_stem_f32to16(P(img), H, W, k, s, Ho, Wo, P(_c(panels, np.float32)), P(_c(bb, np.float32)), Kp, N, Np,
+                           act, P(out), ldo, opad)
+    return out
+
+
+def se_f16(D, chsum, w1, b1, w2t, b2):
+    """SE of the fp16 path on D fp16 [P][C] (a gated copy is returned)."""
+    D = np.array(D, np.float16, copy=True, order="C")
+    Pp, Cc = D.shape
+    w1 = _c(w1, np.float32)
+    rd = w1.shape[0]
+    lib().orc_se_f16(P(D), Pp, Cc, P(_c(chsum, np.float32)), rd, P(w1), P(_c(b1, np.float32)),
+                     P(_c(w2t, np.float32)), P(_c(b2, np.float32)))
+    return D
+
+
+def mean_f16(x, C_):
+    x = _c(x, np.float16)
+    Pp, ld = x.shape
+    out = np.zeros(C_, np.float32)
+    lib().orc_mean_f16(P(x), Pp, C_, ld, P(out))
+    return out
+
+
+def gemv(w, b, x, act=0):
+    """bnn_gemv_f32 (w float32 [N][K]) or bnn_gemv_h16 (w float16 [N][K]) on x f32 [K]."""
+    w = np.ascontiguousarray(w)
+    N, K = w.shape
+    out = np.zeros(N, np.float32)
+    w32 = P(w) if w.dtype == np.float32 else None
+    w16 = P(_c(w, np.float16)) if w.dtype == np.float16 else None
+    assert w32 is not None or w16 is not None
+    lib().orc_gemv(w32, w16, P(_c(b, np.float32)), N, K, P(_c(x, np.float32)), act, P(out))
+    return out

@@ -194,3 +194,97 @@ def test_mean_and_pad(hip):
         for i in range(B):
             assert np.array_equal(got[i].reshape(-1), O.pad(x[i], Hh, W, C, h).reshape(-1)), (esz, i)
         assert (dp.numpy()[:, per:] == 9).all()
+
+
+# ---------------------------------------------------------------- the fp16 path's ops around its GEMMs
+@pytest.mark.parametrize("Hh,W,k,s,co,opad,ldo", [(257, 96, 3, 2, 24, 0, 24), (33, 20, 5, 1, 12, 1, 16),
+                                                  (17, 19, 3, 2, 20, 2, 24)])
+def test_stem_f32to16(hip, Hh, W, k, s, co, opad, ldo):
+    H = hip
+    rng = np.random.default_rng(Hh + k + co)
+    B = 3
+    img = (rng.standard_normal((B, Hh, W)) * 3).astype(np.float32)
+    img[0, 0, :4] = [1e5, -1e5, 7e4, np.nan]    # fp16 overflow to +-inf and a NaN pixel
+    w = (rng.standard_normal((co, k * k)) * np.sqrt(2 / (k * k))).astype(np.float32)
+    b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    panels, bb, (N, K, Kp, Np) = O.fpack(w, b)
+    Ho, Wo = (Hh - k) // s + 1, (W - k) // s + 1
+    xs, x_ws = strided(img, 7)
+    dx = H.DeviceArray.from_host(xs)
+    dw = H.DeviceArray.from_host(panels)
+    db = H.DeviceArray.from_host(bb)
+    rows = (Ho + 2 * opad) * (Wo + 2 * opad)
+    o_ws = rows * ldo + 8
+    do = H.DeviceArray.from_host(np.full((B, o_ws), 5.0, np.float16))
+    say("stem f32to16", Hh, W, k, s, co, opad)
+    H.check(H.lib().bnh_stem_f32to16(dx.ptr, x_ws, Hh, W, k, s, Ho, Wo, dw.ptr, db.ptr, Kp, co, Np, 1, do.ptr, o_ws,
+                                     ldo, opad, B, None), "stem_f32to16")
+    H.sync()
+    got = do.numpy()
+    assert (got[:, rows * ldo:] == 5.0).all()
+    got = got[:, :rows * ldo].reshape(B, rows, ldo)
+    for i in range(B):
+        want = O.stem_f32to16(img[i], k, s, panels, bb, Kp, co, Np, act=1, opad=opad, ldo=ldo, fill=5.0)
+        assert same_bits(got[i], want), i
+
+
+@pytest.mark.parametrize("C,rd,P", [(72, 6, 1536), (1536, 48, 24), (288, 9, 384), (16, 1, 7)])
+def test_se_f16(hip, C, rd, P):
+    H = hip
+    rng = np.random.default_rng(C + rd)
+    B = 3
+    D = rng.standard_normal((B, P, C)).astype(np.float16)
+    D[0, 0, :3] = [np.inf, -np.inf, 60000]
+    chsum = np.stack([D[i].astype(np.float32).sum(0) for i in range(B)]).astype(np.float32)
+    chsum[0, :3] = [1.0, -2.0, 3.0]
+    w1 = (rng.standard_normal((rd, C)) * np.sqrt(2 / C)).astype(np.float32)
+    b1 = (rng.standard_normal(rd) * 2).astype(np.float32)
+    w2t = (rng.standard_normal((rd, C)) * np.sqrt(2 / rd)).astype(np.float32)
+    b2 = (rng.standard_normal(C) * 3).astype(np.float32)
+    cs, c_ws = strided(chsum, 3)
+    dc = H.DeviceArray.from_host(cs)
+    dt = [H.DeviceArray.from_host(a) for a in (w1, b1, w2t, b2)]
+    Ds, d_ws = strided(D, 9)
+    dD = H.DeviceArray.from_host(Ds)
+    say("se f16", C, rd, P)
+    H.check(H.lib().bnh_se_f16(dc.ptr, c_ws, C, rd, P, dt[0].ptr, dt[1].ptr, dt[2].ptr, dt[3].ptr, dD.ptr, d_ws, B,
+                               None), "se_f16")
+    H.sync()
+    got = dD.numpy()
+    for i in range(B):
+        assert same_bits(got[i, :P * C].reshape(P, C), O.se_f16(D[i], chsum[i], w1, b1, w2t, b2)), i
+        assert (got[i, P * C:] == 0).all()
+
+
+def test_mean_f16_and_gemv(hip):
+    H = hip
+    rng = np.random.default_rng(12)
+    B, P, C, ld = 3, 24, 1024, 1032
+    x = rng.standard_normal((B, P, ld)).astype(np.float16)
+    x[1, 3, 5] = np.inf
+    xs, x_ws = strided(x, 5)
+    dx = H.DeviceArray.from_host(xs)
+    do = H.DeviceArray.from_host(np.zeros((B, C + 4), np.float32))
+    say("mean f16")
+    H.check(H.lib().bnh_mean_f16(dx.ptr, x_ws, P, C, ld, do.ptr, C + 4, B, None), "mean_f16")
+    H.sync()
+    m = do.numpy()[:, :C]
+    for i in range(B):
+        assert same_bits(m[i], O.mean_f16(x[i], C))
+    # GEMV, fp16 and fp32 weights, K with 8-lane, 4-lane and scalar remainders, ReLU
+    for K, N, w16, act in ((1024, 6522, 1, 0), (1027, 300, 1, 2), (1536, 1000, 0, 0), (13, 33, 0, 2), (6, 17, 1, 0)):
+        w = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16 if w16 else np.float32)
+        b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+        xv = rng.standard_normal((B, K)).astype(np.float32)
+        xvs, xv_ws = strided(xv, 3)
+        dxv = H.DeviceArray.from_host(xvs)
+        dwt = H.DeviceArray.from_host(w)
+        dbt = H.DeviceArray.from_host(b)
+        dy = H.DeviceArray.from_host(np.full((B, N + 2), 9.0, np.float32))
+        say("gemv", K, N, w16, act)
+        H.check(H.lib().bnh_gemv(dwt.ptr, w16, dbt.ptr, N, K, dxv.ptr, xv_ws, act, dy.ptr, N + 2, B, None), "gemv")
+        H.sync()
+        y = dy.numpy()
+        assert (y[:, N:] == 9.0).all()
+        for i in range(B):
+            assert same_bits(y[i, :N], O.gemv(w, b, xv[i], act)), (K, N, w16, i)

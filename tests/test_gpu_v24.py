@@ -1,0 +1,58 @@
+"""The BirdNET-v2.4-shaped fp16 network end to end on the GPU (bnn_init /
+bnn_infer_batch on a .bnpk built by bnneon.v24net, path neon-fp16):
+FE_LOGMEL, STEM (fp16 output), PW (the exact fp16 GEMM: SiLU into zero-haloed
+buffers, residual adds, the ReLU head conv), DW3 fp16 with TF-same offsets, SE
+fp16, MEAN fp16 and the fp16-weight GEMV over 16 MBConv blocks. Every op
+computes in the reference's own arithmetic, so the logits and embeddings are
+bit-identical to the oracle's op-by-op run of the same package (a tolerance
+would be max |logit error| <= 0 and top-1 agreement 100 %), and identical
+whatever the batch size."""
+import numpy as np
+import pytest
+
+from bnneon import binding, v24net
+
+import oracle_net  # oracle/oracle_net.py
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def same(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    an, bn = np.isnan(a), np.isnan(b)
+    return np.array_equal(an, bn) and np.array_equal(a.view(np.uint32)[~an], b.view(np.uint32)[~bn])
+
+
+@pytest.fixture(scope="module")
+def v24(tmp_path_factory):
+    vn = v24net.V24Net(seed=5)
+    path = vn.write(str(tmp_path_factory.mktemp("v24") / "v24_f16.bnpk"))
+    return vn, path
+
+
+def test_v24_batch_bit_exact(hip, v24):
+    vn, path = v24
+    rng = np.random.default_rng(6)
+    B = 5
+    pcm = np.stack([v24net.signal(rng) for _ in range(B)])
+    pcm[1] = 0.0                 # silence: every frame at the log floor
+    pcm[2, 777] = 0.95           # a click
+    on = oracle_net.OracleNet(vn.net, 0, vn.net.last, vn.emb_buf)
+    say("v24 batch", B)
+    with binding.Model(path) as m:
+        assert m.info.n_classes == v24net.N_CLASSES and m.info.emb_dim == v24net.EMB
+        out, emb, status = m.infer_batch(pcm)
+        assert not status.any()
+        for w in (0, 1, 2):
+            ref, ref_emb, _ = on.run(pcm[w])
+            say("window", w)
+            assert same(out[w], ref[:v24net.N_CLASSES]), w
+            assert same(emb[w], ref_emb[:v24net.EMB]), w
+        o1, e1, s1 = m.infer_batch(pcm[4:5])
+        assert not s1.any() and same(o1[0], out[4]) and same(e1[0], emb[4])
+        o2, e2, s2 = m.infer_batch(pcm[1:4])
+        assert not s2.any() and same(o2, out[1:4]) and same(e2, emb[1:4])
