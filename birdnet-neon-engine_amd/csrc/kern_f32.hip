@@ -190,6 +190,56 @@ __global__ __launch_bounds__(256) void k_se_f32(const float *__restrict__ chsum,
   }
 }
 
+// SE scaling when the gates are in a buffer: D[p][c] *= gate[c] for every window, 8 channels per thread (C % 8 == 0)
+// over a grid that covers all windows; fp16: the gate rounded to fp16, the product in fp16 (v24k16_se_scale,
+// src/v24_fast.c:223-228); fp32: the fp32 product. VEC: 16-byte vector accesses (aligned strides), else scalar.
+template <bool F16, bool VEC>
+__global__ __launch_bounds__(256) void k_se_scale(const float *__restrict__ gate, long long g_ws, int C, long long n8,
+                                                  void *__restrict__ Dv, long long d_ws) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const long long win = blockIdx.y, e = i * 8;
+  const int c = (int)(e % C);
+  const float *g = gate + win * g_ws + c;
+  float gv[8];
+  if (VEC) {
+    const float4 g0 = *(const float4 *)g, g1 = *(const float4 *)(g + 4);
+    gv[0] = g0.x; gv[1] = g0.y; gv[2] = g0.z; gv[3] = g0.w; gv[4] = g1.x; gv[5] = g1.y; gv[6] = g1.z; gv[7] = g1.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; j++) gv[j] = g[j];
+  }
+  if (F16) {
+    uint16_t *d = (uint16_t *)Dv + win * d_ws + e;
+    if (VEC) {
+      uint4 v = *(const uint4 *)d;
+      uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const h16 lo = hfrom((uint16_t)(q[j] & 0xffffu)) * f2h(gv[2 * j]);
+        const h16 hi = hfrom((uint16_t)(q[j] >> 16)) * f2h(gv[2 * j + 1]);
+        q[j] = (uint32_t)hbits(lo) | ((uint32_t)hbits(hi) << 16);
+      }
+      *(uint4 *)d = make_uint4(q[0], q[1], q[2], q[3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) d[j] = hbits(hfrom(d[j]) * f2h(gv[j]));
+    }
+  } else {
+    float *d = (float *)Dv + win * d_ws + e;
+    if (VEC) {
+      float4 a = *(const float4 *)d, b = *(const float4 *)(d + 4);
+      a.x *= gv[0]; a.y *= gv[1]; a.z *= gv[2]; a.w *= gv[3];
+      b.x *= gv[4]; b.y *= gv[5]; b.z *= gv[6]; b.w *= gv[7];
+      *(float4 *)d = a;
+      *(float4 *)(d + 4) = b;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) d[j] = d[j] * gv[j];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ MEAN
 __global__ void k_mean_f32(const float *__restrict__ x, long long x_ws, int P, int C, int ld, float *__restrict__ out,
                            long long o_ws) {
@@ -302,15 +352,33 @@ static int se_launch(const float *chsum, long long c_ws, int C, int rd, int P, c
   if (wg > B) wg = B >= 4 ? 4 : B >= 2 ? 2 : 1;
   const dim3 grid((unsigned)bnh_ceil_div(B, wg));
   hipStream_t st = bnh_stream(stream);
+  // with a gate buffer and C % 8 == 0 the gates go there first and a second kernel over every window's pixels
+  // scales D (a block per group of windows scaling its own activations leaves most of the chip idle)
+  const bool split = gate && D && C % 8 == 0;
+  void *Dk = split ? nullptr : D;
 #define SE_LAUNCH(W, F)                                                                                                \
   hipLaunchKernelGGL((k_se_f32<W, F>), grid, dim3(256), per * W, st, chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate,    \
-                     g_ws, D, d_ws, B)
+                     g_ws, Dk, d_ws, B)
   if (f16) {
     if (wg == 4) SE_LAUNCH(4, true); else if (wg == 2) SE_LAUNCH(2, true); else SE_LAUNCH(1, true);
   } else {
     if (wg == 4) SE_LAUNCH(4, false); else if (wg == 2) SE_LAUNCH(2, false); else SE_LAUNCH(1, false);
   }
 #undef SE_LAUNCH
+  BNH_HIP(hipGetLastError());
+  if (!split) return 0;
+  const long long n8 = (long long)P * C / 8;
+  const unsigned esz = f16 ? 2 : 4;
+  const bool vec = ((uintptr_t)D & 15) == 0 && ((uintptr_t)gate & 15) == 0 && g_ws % 4 == 0 &&
+                   (d_ws * esz) % 16 == 0;
+  const dim3 sg((unsigned)bnh_ceil_div(n8, 256), (unsigned)B);
+  if (f16) {
+    if (vec) hipLaunchKernelGGL((k_se_scale<true, true>), sg, dim3(256), 0, st, gate, g_ws, C, n8, D, d_ws);
+    else hipLaunchKernelGGL((k_se_scale<true, false>), sg, dim3(256), 0, st, gate, g_ws, C, n8, D, d_ws);
+  } else {
+    if (vec) hipLaunchKernelGGL((k_se_scale<false, true>), sg, dim3(256), 0, st, gate, g_ws, C, n8, D, d_ws);
+    else hipLaunchKernelGGL((k_se_scale<false, false>), sg, dim3(256), 0, st, gate, g_ws, C, n8, D, d_ws);
+  }
   BNH_HIP(hipGetLastError());
   return 0;
 }
@@ -391,9 +459,10 @@ int bnh_se_f32(const float *chsum, long long c_ws, int C, int rd, int P, const f
 }
 
 int bnh_se_f16(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
-               const float *w2t, const float *b2, uint16_t *D, long long d_ws, int B, void *stream) {
+               const float *w2t, const float *b2, float *gate, long long g_ws, uint16_t *D, long long d_ws, int B,
+               void *stream) {
   BNH_REQ(D);
-  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, nullptr, 0, D, d_ws, B, true, stream);
+  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws, D, d_ws, B, true, stream);
 }
 
 int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,

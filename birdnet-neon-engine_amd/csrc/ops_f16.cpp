@@ -6,9 +6,9 @@
 
 int rt_dwk_check(rt_ctx *c, rt_op *op, size_t esz);             // ops_f32.cpp
 int rt_dw3_check(rt_ctx *c, rt_op *op, int dt, int pt, int pl);  // ops_f32.cpp
-int rt_dev_tensors(rt_ctx *c, rt_op *op, int n);
-void rt_dev_fini(rt_op *op);
-static inline const uint16_t *dev_h(const rt_op *op, int i) { return *((uint16_t *const *)op->state + i); }
+static inline const uint16_t *dev_h(const rt_op *op, int i) {
+  return (const uint16_t *)((const rt_dev_state *)op->state)->t[i];
+}
 int rt_pw_out_check(rt_ctx *c, rt_op *op, int dt);             // ops_s8n.cpp
 int rt_stem_check(rt_ctx *c, rt_op *op);                       // ops_f32.cpp
 int rt_mean_check(rt_ctx *c, rt_op *op);
@@ -133,8 +133,11 @@ static int se_init(rt_ctx *c, rt_op *op) {
 }
 static int se_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
+  const long long g_ws = p[0];  // C % 8 == 0: 16-byte aligned gate rows
+  float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)g_ws);
+  if (!g) return -1;
   return bnh_se_f16((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_h(op, 0),
-                    (const float *)dev_h(op, 1), (const float *)dev_h(op, 2), (const float *)dev_h(op, 3),
+                    (const float *)dev_h(op, 1), (const float *)dev_h(op, 2), (const float *)dev_h(op, 3), g, g_ws,
                     (uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
 }
 

@@ -7,9 +7,8 @@
 #include "rt.h"
 
 // device copies of an op's first `n` tensors (weights / biases), freed by dev_fini
-typedef struct { void *t[4]; } dev_state;
 int rt_dev_tensors(rt_ctx *c, rt_op *op, int n) {
-  dev_state *s = (dev_state *)calloc(1, sizeof *s);
+  rt_dev_state *s = (rt_dev_state *)calloc(1, sizeof *s);
   op->state = s;
   if (!s) return rt_oom(c, op, sizeof *s);
   for (int i = 0; i < n && i < 4; i++) {
@@ -22,13 +21,30 @@ int rt_dev_tensors(rt_ctx *c, rt_op *op, int n) {
   return 0;
 }
 void rt_dev_fini(rt_op *op) {
-  dev_state *s = (dev_state *)op->state;
-  if (s)
+  rt_dev_state *s = (rt_dev_state *)op->state;
+  if (s) {
     for (int i = 0; i < 4; i++)
       if (s->t[i]) bnh_free(s->t[i]);
+    if (s->scratch) bnh_free(s->scratch);
+  }
   free(s);
 }
-static inline void *dev_tn(const rt_op *op, int i) { return ((dev_state *)op->state)->t[i]; }
+void *rt_dev_scratch(rt_ctx *c, rt_op *op, size_t per_window) {
+  rt_dev_state *s = (rt_dev_state *)op->state;
+  const size_t want = per_window * (size_t)c->bcap;
+  if (s->scratch_cap < want) {
+    if (s->scratch) bnh_free(s->scratch);
+    s->scratch_cap = 0;
+    s->scratch = bnh_malloc(want);
+    if (!s->scratch) {
+      rt_oom(c, op, want);
+      return nullptr;
+    }
+    s->scratch_cap = want;
+  }
+  return s->scratch;
+}
+static inline void *dev_tn(const rt_op *op, int i) { return ((rt_dev_state *)op->state)->t[i]; }
 
 // -------- DWK: b = [xp (halo (k-1)/2), out [Ho][Wo][C], chsum f32 [C]]; t = [w [k*k][C], b [C]];
 //          p = [H W C k s pt pl Ho Wo act]   (rt_dwk_check, src/rt_ops_f32.c:435-458)
@@ -178,8 +194,11 @@ static int se_init(rt_ctx *c, rt_op *op) { return se_check(c, op, 0); }
 static int seg_init(rt_ctx *c, rt_op *op) { return se_check(c, op, 1); }
 static int se_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
+  const long long g_ws = (p[0] + 3) / 4 * 4;  // the gates of each window, 16-byte aligned rows
+  float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)g_ws);
+  if (!g) return -1;
   return bnh_se_f32((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_tn(op, 0),
-                    (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3), nullptr, 0,
+                    (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3), g, g_ws,
                     (float *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
 }
 static int seg_run(rt_ctx *c, rt_op *op) {

@@ -53,6 +53,18 @@ typedef struct rt_kernel {
 
 enum { RT_E_PARAM = -1, RT_E_OOM = -2 };
 
+// op state of the ops whose tensors live on the device: up to 4 uploaded tensors, plus an op-private per-window
+// scratch buffer grown with the arena's window capacity
+typedef struct {
+  void *t[4];
+  void *scratch;
+  size_t scratch_cap;  // bytes
+} rt_dev_state;
+int rt_dev_tensors(rt_ctx *c, rt_op *op, int n);
+void rt_dev_fini(rt_op *op);
+// the op's scratch, at least c->bcap windows of `per_window` bytes each (NULL after rt_oom when it cannot grow)
+void *rt_dev_scratch(rt_ctx *c, rt_op *op, size_t per_window);
+
 struct rt_ctx {
   rt_pkg *pkg;
   const rt_pathdesc *path;

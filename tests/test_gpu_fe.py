@@ -228,8 +228,10 @@ def test_stem_f32to16(hip, Hh, W, k, s, co, opad, ldo):
         assert same_bits(got[i], want), i
 
 
-@pytest.mark.parametrize("C,rd,P", [(72, 6, 1536), (1536, 48, 24), (288, 9, 384), (16, 1, 7)])
-def test_se_f16(hip, C, rd, P):
+@pytest.mark.parametrize("C,rd,P,ws", [(72, 6, 1536, True), (1536, 48, 24, True), (288, 9, 384, False),
+                                        (16, 1, 7, True), (40, 3, 33, False)])
+def test_se_f16(hip, C, rd, P, ws):
+    """ws: with a gate workspace (gates, then a scaling kernel over all pixels) or without (one kernel)."""
     H = hip
     rng = np.random.default_rng(C + rd)
     B = 3
@@ -246,14 +248,19 @@ def test_se_f16(hip, C, rd, P):
     dt = [H.DeviceArray.from_host(a) for a in (w1, b1, w2t, b2)]
     Ds, d_ws = strided(D, 9)
     dD = H.DeviceArray.from_host(Ds)
-    say("se f16", C, rd, P)
-    H.check(H.lib().bnh_se_f16(dc.ptr, c_ws, C, rd, P, dt[0].ptr, dt[1].ptr, dt[2].ptr, dt[3].ptr, dD.ptr, d_ws, B,
-                               None), "se_f16")
+    g_ws = C + 4
+    dg = H.DeviceArray.from_host(np.zeros((B, g_ws), np.float32)) if ws else None
+    say("se f16", C, rd, P, ws)
+    H.check(H.lib().bnh_se_f16(dc.ptr, c_ws, C, rd, P, dt[0].ptr, dt[1].ptr, dt[2].ptr, dt[3].ptr,
+                               dg.ptr if ws else None, g_ws, dD.ptr, d_ws, B, None), "se_f16")
     H.sync()
     got = dD.numpy()
     for i in range(B):
         assert same_bits(got[i, :P * C].reshape(P, C), O.se_f16(D[i], chsum[i], w1, b1, w2t, b2)), i
         assert (got[i, P * C:] == 0).all()
+        if ws:   # the gates as the fp32 SE computes them, with the dividing sigmoid
+            assert same_bits(O.se_f16(np.ones((P, C), np.float16), chsum[i], w1, b1, w2t, b2)[0],
+                             dg.numpy()[i, :C].astype(np.float16)), i
 
 
 def test_mean_f16_and_gemv(hip):
