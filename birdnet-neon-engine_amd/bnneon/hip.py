@@ -74,6 +74,7 @@ _SIGS = {
     "bnh_h16w_free": (None, [vp]),
     "bnh_gemm_f16": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
     "bnh_gemm_f16_mfma": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
+    "bnh_gemm_f16_body": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
     "bnh_wino16_new": (vp, [i32, i32, vp, vp]),
     "bnh_wino16_free": (None, [vp]),
     "bnh_wino_f16": (i32, [vp, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp, i64, i32, i32, i32, vp]),

@@ -38,7 +38,8 @@ static __constant__ uint16_t k_silu_c1[16] = {0xb40b, 0xb242, 0xaecc, 0xa9ea, 0x
                                               0x8daa, 0x882c, 0x8312, 0x8121, 0x806a, 0x8027, 0x800e, 0x8005};
 static __constant__ uint16_t k_silu_c2[16] = {0x23bd, 0x299d, 0x2915, 0x254c, 0x2073, 0x1ae1, 0x1528, 0x0fa3,
                                               0x09a2, 0x0426, 0x0187, 0x0090, 0x0035, 0x0013, 0x0007, 0x0003};
-BNH_DEV h16 silu_lut_h(h16 x) {
+// the same with the three coefficient tables at c0, c1, c2 (LDS copies in the GEMM epilogue)
+BNH_DEV h16 silu_lut_h_t(h16 x, const uint16_t *c0t, const uint16_t *c1t, const uint16_t *c2t) {
   const h16 magic = (h16)1536.0f;
   const h16 u = hfrom((uint16_t)(hbits(x) & 0x7fff));
   const h16 uc = hmin(u, hfrom(0x4bb3));  // (fp16)15.4f
@@ -46,10 +47,11 @@ BNH_DEV h16 silu_lut_h(h16 x) {
   const h16 f = uc - (tm - magic);
   unsigned n = hbits(tm) & 0xffu;
   if (n > 15) n = 0;
-  const h16 c0 = hfrom(k_silu_c0[n]), c1 = hfrom(k_silu_c1[n]), c2 = hfrom(k_silu_c2[n]);
+  const h16 c0 = hfrom(c0t[n]), c1 = hfrom(c1t[n]), c2 = hfrom(c2t[n]);
   h16 p = hfma(c2, f, c1);
   p = hfma(p, f, c0);
   return hfma(-u, p, hmax(x, (h16)0.0f));
 }
+BNH_DEV h16 silu_lut_h(h16 x) { return silu_lut_h_t(x, k_silu_c0, k_silu_c1, k_silu_c2); }
 
 #endif

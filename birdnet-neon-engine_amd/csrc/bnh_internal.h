@@ -31,10 +31,6 @@ extern "C" int bnh_stem_f32to16_body(const float *img, long long i_ws, int H, in
                                      const float *w, const float *bias, int Kp, int N, int Np, int act, uint16_t *out,
                                      long long o_ws, int ldo, int opad, int B, void *stream);
 
-// the fp16 GEMM without the halo zeroing of bnh_gemm_f16
-extern "C" int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W,
-                                 const bnh_epi16 *e, void *stream);
-
 static inline hipStream_t bnh_stream(void *s) { return (hipStream_t)s; }
 static inline long long bnh_ceil_div(long long a, long long b) { return (a + b - 1) / b; }
 static inline long long bnh_round_up(long long a, long long b) { return bnh_ceil_div(a, b) * b; }

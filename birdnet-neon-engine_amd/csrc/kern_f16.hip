@@ -1,6 +1,6 @@
 // fp16 pointwise-convolution GEMM (libbnneon's gemm_f16, src/gemm_f16.c, the PW op of the fp16 family) on gfx950,
 // in two forms:
-//  - k_gemm_f16x (bnh_gemm_f16): the reference's own arithmetic, bit-identical: per output an fp16 FMA chain over
+//  - k_gemm_f16e (bnh_gemm_f16): the reference's own arithmetic, bit-identical: per output an fp16 FMA chain over
 //    each K block, fp32 sums across blocks, its bias and epilogue; packed fp16 FMAs on the VALU.
 //  - k_gemm_f16 (bnh_gemm_f16_mfma): fp16 MFMA (v_mfma_f32_16x16x32_f16) with fp32 accumulation over the whole K,
 //    then the same epilogue (+ bias in fp32, one rounding to fp16, fp16 LUT SiLU or ReLU, fp16 residual add,
@@ -20,7 +20,8 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 struct bnh_h16w {
   int N, K, Kp, Np, Nt;
-  uint16_t *w;    // [Nt][Kp]
+  uint16_t *w;    // [Nt][Kp] (the MFMA form)
+  uint16_t *wk;   // [Kp][Nt] (the exact form)
   float *b;       // [Nt] fp32 bias
   uint16_t *b16;  // [Nt] fp16 bias
 };
@@ -100,112 +101,212 @@ __global__ __launch_bounds__(256) void k_gemm_f16(const uint16_t *__restrict__ A
 // the block results summed in fp32 when there are several (then + the fp32 bias, one rounding), else + the fp16
 // bias in fp16; then the epilogue above. No MFMA (its accumulation is fp32): packed fp16 FMAs on the VALU, each
 // lane one IEEE fp16 fused multiply-add, two channels per instruction.
-// A block owns 64 rows x 128 channels; a thread 4 rows x 8 channels (16 packed accumulators). K is staged through
-// LDS 32 at a time, A transposed to [k][row] and W as [k][channel], so a thread reads its 4 rows and 8 channels
-// of a k step with one 8-byte and one 16-byte LDS read.
+// A block owns TN = 8 TC channels (TC = 4..16 thread columns, chosen per layer so the channel tiles cover Np with
+// the least padding) x BM = 4 TR rows (TR = min(256 / TC, 64) thread rows; threads past TC x TR only load); a thread
+// computes 4 rows x 8 channels (16 packed accumulators). K goes through LDS 32 steps at a time: A as it lies
+// ([row][k], a row stride of 17 dwords so the 4-row reads of a wave hit distinct banks), W from its k-major copy
+// ([k][channel], a thread's 8 channels one 16-byte read). The next chunk's global loads are issued before the
+// current chunk is computed. Epilogue: the SiLU two channels at a time in packed fp16 with its table in LDS, 16-byte
+// residual loads and stores (VEC).
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-#define FX_KC 32
-__global__ __launch_bounds__(256) void k_gemm_f16x(const uint16_t *__restrict__ A, long long a_ws, int lda, int M,
-                                                   double rM, long long rows, const uint16_t *__restrict__ wt,
+#define FE_KC 32
+#define FE_AS 17   // A row stride in dwords (34 halves)
+#define FE_BM 256  // rows per block at most
+
+// silu_lut_h on both halves of a packed pair, with the same roundings lane by lane: u = |x|; min(u, 15.4) (u is
+// never NaN-sensitive here: a NaN x gives a NaN result through -u either way); the segment n in [0, 15] from the
+// low byte of u + 1536; max(x, 0) as the sign-cleared x (FMAX(x, +0) for every non-NaN x, -0 included).
+// t01[n] = c0 | c1 << 16, t2[n] = c2.
+BNH_DEV h2 silu2_lut(h2 x, const uint32_t *t01, const uint16_t *t2) {
+  const uint32_t xb = __builtin_bit_cast(uint32_t, x);
+  const h2 u = __builtin_bit_cast(h2, xb & 0x7fff7fffu);
+  const h2 uc = __builtin_elementwise_min(u, (h2){hfrom(0x4bb3), hfrom(0x4bb3)});
+  const h2 magic = (h2){(h16)1536.0f, (h16)1536.0f};
+  const h2 tm = uc + magic;
+  const h2 f = uc - (tm - magic);
+  const uint32_t tb = __builtin_bit_cast(uint32_t, tm);
+  const uint32_t na = tb & 15u, nb = (tb >> 16) & 15u;
+  const uint32_t ea = t01[na], eb = t01[nb];
+  const h2 c0 = __builtin_bit_cast(h2, (ea & 0xffffu) | (eb << 16));
+  const h2 c1 = __builtin_bit_cast(h2, (ea >> 16) | (eb & 0xffff0000u));
+  const h2 c2 = __builtin_bit_cast(h2, (uint32_t)t2[na] | ((uint32_t)t2[nb] << 16));
+  h2 p = __builtin_elementwise_fma(c2, f, c1);
+  p = __builtin_elementwise_fma(p, f, c0);
+  const uint32_t neg = ((xb >> 15) & 0x00010001u) * 0xffffu;  // all-ones halves where x is negative (or -0)
+  const h2 m = __builtin_bit_cast(h2, xb & ~neg);
+  return __builtin_elementwise_fma(-u, p, m);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ A, long long a_ws, int lda, int M,
+                                                   double rM, long long rows, const uint16_t *__restrict__ wk, int Ntp,
                                                    const float *__restrict__ b32, const uint16_t *__restrict__ b16,
-                                                   int Kp, int Np, int bs, Epi16Dev e) {
-  __shared__ __attribute__((aligned(16))) h16 As[FX_KC][64 + 4];
-  __shared__ __attribute__((aligned(16))) h16 Ws[FX_KC][128 + 8];
-  __shared__ long long s_a[64], s_o[64], s_r[64];
-  const int tid = threadIdx.x, tc = tid & 15, tr = tid >> 4;
-  const long long rowB = (long long)blockIdx.x * 64;
-  const int n0 = blockIdx.y * 128;
-  if (tid < 64) {
-    const long long row = rowB + tid < rows ? rowB + tid : rows - 1;
+                                                   int Kp, int Np, int bs, int TC, Epi16Dev e) {
+  const int TR = 256 / TC < 64 ? 256 / TC : 64, BM = 4 * TR, TN = 8 * TC;
+  __shared__ __attribute__((aligned(16))) uint32_t As[FE_BM * FE_AS];
+  __shared__ __attribute__((aligned(16))) uint4 Ws[FE_KC * 16];
+  __shared__ long long s_a[FE_BM], s_o[FE_BM], s_r[FE_BM];
+  __shared__ uint32_t s_t01[16];
+  __shared__ uint16_t s_t2[16];
+  const int tid = threadIdx.x, tc = tid % TC, tr = tid / TC;
+  const bool active = tr < TR;
+  const long long rowB = (long long)blockIdx.x * BM;
+  const int n0 = blockIdx.y * TN;
+  for (int i = tid; i < BM; i += 256) {
+    const long long row = rowB + i < rows ? rowB + i : rows - 1;
     const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
-    s_a[tid] = w * a_ws + (long long)m * lda;
+    s_a[i] = w * a_ws + (long long)m * lda;
     long long orow = m;
     if (e.opad) {
       const int y = m / e.ow;
       orow = (long long)(y + e.opad) * (e.ow + 2 * e.opad) + (m - y * e.ow) + e.opad;
     }
-    s_o[tid] = w * e.out_ws + orow * e.ldo;
-    s_r[tid] = w * e.res_ws + (long long)m * e.ldr;
+    s_o[i] = w * e.out_ws + orow * e.ldo;
+    s_r[i] = w * e.res_ws + (long long)m * e.ldr;
+  }
+  if (tid < 16) {
+    s_t01[tid] = (uint32_t)k_silu_c0[tid] | ((uint32_t)k_silu_c1[tid] << 16);
+    s_t2[tid] = k_silu_c2[tid];
   }
   __syncthreads();
-  const int nblk = (Kp + bs - 1) / bs;
+  // chunk loader: A rows [BM][kn] and W rows [kn][TN] of k0 into registers (kn a multiple of 8)
+  uint4 ra[FE_BM * FE_KC / 8 / 256], rw[2];
+  const int nav = BM * (FE_KC / 8), nwv = FE_KC * TC;
+  auto load = [&](int k0, int kn) {
+#pragma unroll
+    for (int j = 0; j < FE_BM * FE_KC / 8 / 256; j++) {
+      const int i = tid + 256 * j, r = i / (FE_KC / 8), kc = (i % (FE_KC / 8)) * 8;
+      ra[j] = i < nav && kc < kn ? *(const uint4 *)(A + s_a[r] + k0 + kc) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = tid + 256 * j, k = i / TC, c = i - k * TC;
+      rw[j] = i < nwv && k < kn ? *(const uint4 *)(wk + (long long)(k0 + k) * Ntp + n0 + 8 * c)
+                                : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int j = 0; j < FE_BM * FE_KC / 8 / 256; j++) {
+      const int i = tid + 256 * j, r = i / (FE_KC / 8), kc = (i % (FE_KC / 8)) * 8;
+      if (i < nav) {
+        uint32_t *d = As + r * FE_AS + kc / 2;
+        d[0] = ra[j].x; d[1] = ra[j].y; d[2] = ra[j].z; d[3] = ra[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = tid + 256 * j;
+      if (i < nwv) Ws[i] = rw[j];
+    }
+  };
   h2 acc[4][4];
   float fb[4][8];
 #pragma unroll
-  for (int r = 0; r < 4; r++)
+  for (int r = 0; r < 4; r++) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) acc[r][p] = (h2){(h16)0.0f, (h16)0.0f};
 #pragma unroll
     for (int c = 0; c < 8; c++) fb[r][c] = 0.f;
-  for (int kb = 0; kb < Kp; kb += bs) {
+  }
+  const int nblk = (Kp + bs - 1) / bs;
+  int kb = 0, k0 = 0;
+  int kn = bs < FE_KC ? bs : FE_KC;
+  if (kn > Kp) kn = Kp;
+  load(0, kn);
+  const uint32_t *Ar = As + 4 * (active ? tr : 0) * FE_AS;
+  const uint4 *Wt = Ws + tc;
+  while (true) {
+    __syncthreads();  // the previous chunk's reads are done
+    store();
+    __syncthreads();
+    // the next chunk: within this K block, or the first of the next
     const int ke = kb + bs < Kp ? kb + bs : Kp;
+    int nk0 = k0 + kn, nkb = kb;
+    if (nk0 >= ke) nkb = nk0 = ke;
+    const int nke = nkb + bs < Kp ? nkb + bs : Kp;
+    const int nkn = nk0 < Kp ? (nke - nk0 < FE_KC ? nke - nk0 : FE_KC) : 0;
+    if (nkn) load(nk0, nkn);
+    if (active) {
+      for (int k = 0; k < kn; k += 2) {
+        uint32_t a[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
-#pragma unroll
-      for (int p = 0; p < 4; p++) acc[r][p] = (h2){(h16)0.0f, (h16)0.0f};
-    for (int k0 = kb; k0 < ke; k0 += FX_KC) {
-      const int kn = ke - k0 < FX_KC ? ke - k0 : FX_KC;  // a multiple of 8
-      // stage A: 64 rows x kn k (8-half chunks), transposed
-      for (int i = tid; i < 64 * (kn / 8); i += 256) {
-        const int r = i / (kn / 8), kc = (i % (kn / 8)) * 8;
-        const uint4 v = *(const uint4 *)(A + s_a[r] + k0 + kc);
-        const uint32_t q[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          As[kc + 2 * j][r] = hfrom((uint16_t)(q[j] & 0xffffu));
-          As[kc + 2 * j + 1][r] = hfrom((uint16_t)(q[j] >> 16));
-        }
-      }
-      // stage W: 128 channel rows x kn k
-      for (int i = tid; i < 128 * (kn / 8); i += 256) {
-        const int cch = i / (kn / 8), kc = (i % (kn / 8)) * 8;
-        const uint4 v = *(const uint4 *)(wt + (long long)(n0 + cch) * Kp + k0 + kc);
-        const uint32_t q[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          Ws[kc + 2 * j][cch] = hfrom((uint16_t)(q[j] & 0xffffu));
-          Ws[kc + 2 * j + 1][cch] = hfrom((uint16_t)(q[j] >> 16));
-        }
-      }
-      __syncthreads();
-      for (int k = 0; k < kn; k++) {
-        const uint2 av = *(const uint2 *)&As[k][4 * tr];
-        const uint4 wv = *(const uint4 *)&Ws[k][8 * tc];
-        const h16 a[4] = {hfrom((uint16_t)(av.x & 0xffffu)), hfrom((uint16_t)(av.x >> 16)),
-                          hfrom((uint16_t)(av.y & 0xffffu)), hfrom((uint16_t)(av.y >> 16))};
-        const h2 w2[4] = {__builtin_bit_cast(h2, wv.x), __builtin_bit_cast(h2, wv.y), __builtin_bit_cast(h2, wv.z),
-                          __builtin_bit_cast(h2, wv.w)};
+        for (int r = 0; r < 4; r++) a[r] = Ar[r * FE_AS + k / 2];
+        const uint4 w0 = Wt[k * TC], w1 = Wt[(k + 1) * TC];
+        const h2 wa[4] = {__builtin_bit_cast(h2, w0.x), __builtin_bit_cast(h2, w0.y), __builtin_bit_cast(h2, w0.z),
+                          __builtin_bit_cast(h2, w0.w)};
+        const h2 wb[4] = {__builtin_bit_cast(h2, w1.x), __builtin_bit_cast(h2, w1.y), __builtin_bit_cast(h2, w1.z),
+                          __builtin_bit_cast(h2, w1.w)};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const h2 ar = (h2){a[r], a[r]};
+          const h2 av = __builtin_bit_cast(h2, a[r]);
+          const h2 lo = (h2){av.x, av.x}, hi = (h2){av.y, av.y};
 #pragma unroll
-          for (int p = 0; p < 4; p++) acc[r][p] = __builtin_elementwise_fma(w2[p], ar, acc[r][p]);
+          for (int p = 0; p < 4; p++) acc[r][p] = __builtin_elementwise_fma(wa[p], lo, acc[r][p]);
+#pragma unroll
+          for (int p = 0; p < 4; p++) acc[r][p] = __builtin_elementwise_fma(wb[p], hi, acc[r][p]);
         }
       }
-      __syncthreads();
-    }
-    if (nblk > 1) {
+      if (k0 + kn >= ke && nblk > 1) {  // a K block ends: its fp16 results into the fp32 sums
 #pragma unroll
-      for (int r = 0; r < 4; r++)
+        for (int r = 0; r < 4; r++)
 #pragma unroll
-        for (int p = 0; p < 4; p++) {
-          fb[r][2 * p] = fb[r][2 * p] + (float)acc[r][p].x;
-          fb[r][2 * p + 1] = fb[r][2 * p + 1] + (float)acc[r][p].y;
-        }
+          for (int p = 0; p < 4; p++) {
+            fb[r][2 * p] = fb[r][2 * p] + (float)acc[r][p].x;
+            fb[r][2 * p + 1] = fb[r][2 * p + 1] + (float)acc[r][p].y;
+            acc[r][p] = (h2){(h16)0.0f, (h16)0.0f};
+          }
+      }
     }
+    if (!nkn) break;
+    kb = nkb; k0 = nk0; kn = nkn;
+  }
+  // epilogue
+  const int n = n0 + 8 * tc;
+  const int nend = Np < e.ldo ? Np : e.ldo;
+  if (!active || n >= nend) return;
+  const bool full = VEC && n + 8 <= nend;
+  float bias32[8];
+  uint16_t bias16[8];
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    bias32[c] = n + c < nend ? b32[n + c] : 0.f;
+    bias16[c] = n + c < nend ? b16[n + c] : 0;
   }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int lr = 4 * tr + r;
-    if (rowB + lr >= rows) continue;
+    if (rowB + lr >= rows) break;
+    h2 v[4];
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
-      const int n = n0 + 8 * tc + c;
-      if (n >= Np || n >= e.ldo) continue;
-      const h16 a = (c & 1) ? acc[r][c >> 1].y : acc[r][c >> 1].x;
-      h16 v = nblk > 1 ? f2h(fb[r][c] + b32[n]) : a + hfrom(b16[n]);
-      if (e.act == 1) v = silu_lut_h(v);
-      else if (e.act == 2) v = hmax(v, (h16)0.0f);
-      if (e.res) v = v + hfrom(e.res[s_r[lr] + n]);
-      e.out[s_o[lr] + n] = hbits(v);
+    for (int p = 0; p < 4; p++) {
+      if (nblk > 1) {
+        v[p] = (h2){f2h(fb[r][2 * p] + bias32[2 * p]), f2h(fb[r][2 * p + 1] + bias32[2 * p + 1])};
+      } else {
+        v[p] = acc[r][p] + (h2){hfrom(bias16[2 * p]), hfrom(bias16[2 * p + 1])};
+      }
+      if (e.act == 1) v[p] = silu2_lut(v[p], s_t01, s_t2);
+      else if (e.act == 2) v[p] = (h2){hmax(v[p].x, (h16)0.0f), hmax(v[p].y, (h16)0.0f)};
+    }
+    if (full) {
+      if (e.res) {
+        const uint4 rv = *(const uint4 *)(e.res + s_r[lr] + n);
+        v[0] = v[0] + __builtin_bit_cast(h2, rv.x);
+        v[1] = v[1] + __builtin_bit_cast(h2, rv.y);
+        v[2] = v[2] + __builtin_bit_cast(h2, rv.z);
+        v[3] = v[3] + __builtin_bit_cast(h2, rv.w);
+      }
+      *(uint4 *)(e.out + s_o[lr] + n) =
+          make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                     __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        if (n + c >= nend) break;
+        h16 x = (c & 1) ? v[c >> 1].y : v[c >> 1].x;
+        if (e.res) x = x + hfrom(e.res[s_r[lr] + n + c]);
+        e.out[s_o[lr] + n + c] = hbits(x);
+      }
     }
   }
 }
@@ -219,11 +320,12 @@ bnh_h16w *bnh_h16w_new(int N, int K, int Kp, int Np, const uint16_t *w, const fl
     return nullptr;
   }
   const int Nt = (int)bnh_round_up(Np, 128), n16 = Np / 16;
-  uint16_t *hw = (uint16_t *)calloc((size_t)Nt * Kp, 2), *hb16 = (uint16_t *)calloc(Nt, 2);
+  uint16_t *hw = (uint16_t *)calloc((size_t)Nt * Kp, 2), *hwk = (uint16_t *)calloc((size_t)Nt * Kp, 2);
+  uint16_t *hb16 = (uint16_t *)calloc(Nt, 2);
   float *hb = (float *)calloc(Nt, 4);
   bnh_h16w *W = (bnh_h16w *)calloc(1, sizeof *W);
-  if (!hw || !hb || !hb16 || !W) {
-    free(hw); free(hb); free(hb16); free(W);
+  if (!hw || !hwk || !hb || !hb16 || !W) {
+    free(hw); free(hwk); free(hb); free(hb16); free(W);
     bnh_fail("bnh_h16w_new: out of host memory");
     return nullptr;
   }
@@ -232,6 +334,7 @@ bnh_h16w *bnh_h16w_new(int N, int K, int Kp, int Np, const uint16_t *w, const fl
       const int nb = n / 16;
       const size_t idx = nb < n16 ? ((size_t)nb * Kp + k) * 16 + n % 16 : (size_t)n16 * Kp * 16 + (size_t)k * 8 + n % 16;
       hw[(size_t)n * Kp + k] = w[idx];
+      hwk[(size_t)k * Nt + n] = w[idx];
     }
   memcpy(hb, b32, sizeof(float) * Np);
   for (int n = 0; n < Np; n++) {  // the package's fp16 bias, or the fp32 one rounded to nearest even
@@ -242,11 +345,11 @@ bnh_h16w *bnh_h16w_new(int N, int K, int Kp, int Np, const uint16_t *w, const fl
     }
   }
   W->N = N; W->K = K; W->Kp = Kp; W->Np = Np; W->Nt = Nt;
-  bool ok = (W->w = (uint16_t *)bnh_malloc((size_t)Nt * Kp * 2)) && (W->b = (float *)bnh_malloc(4 * (size_t)Nt)) &&
-            (W->b16 = (uint16_t *)bnh_malloc(2 * (size_t)Nt)) &&
-            !bnh_memcpy_h2d(W->w, hw, (size_t)Nt * Kp * 2) && !bnh_memcpy_h2d(W->b, hb, 4 * (size_t)Nt) &&
-            !bnh_memcpy_h2d(W->b16, hb16, 2 * (size_t)Nt);
-  free(hw); free(hb); free(hb16);
+  bool ok = (W->w = (uint16_t *)bnh_malloc((size_t)Nt * Kp * 2)) && (W->wk = (uint16_t *)bnh_malloc((size_t)Nt * Kp * 2)) &&
+            (W->b = (float *)bnh_malloc(4 * (size_t)Nt)) && (W->b16 = (uint16_t *)bnh_malloc(2 * (size_t)Nt)) &&
+            !bnh_memcpy_h2d(W->w, hw, (size_t)Nt * Kp * 2) && !bnh_memcpy_h2d(W->wk, hwk, (size_t)Nt * Kp * 2) &&
+            !bnh_memcpy_h2d(W->b, hb, 4 * (size_t)Nt) && !bnh_memcpy_h2d(W->b16, hb16, 2 * (size_t)Nt);
+  free(hw); free(hwk); free(hb); free(hb16);
   if (!ok) { bnh_h16w_free(W); return nullptr; }
   return W;
 }
@@ -254,6 +357,7 @@ bnh_h16w *bnh_h16w_new(int N, int K, int Kp, int Np, const uint16_t *w, const fl
 void bnh_h16w_free(bnh_h16w *W) {
   if (!W) return;
   if (W->w) (void)hipFree(W->w);
+  if (W->wk) (void)hipFree(W->wk);
   if (W->b) (void)hipFree(W->b);
   if (W->b16) (void)hipFree(W->b16);
   free(W);
@@ -283,9 +387,21 @@ int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, 
   const long long rows = (long long)M * B;
   Epi16Dev d = {e->act, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->res, e->res_ws, e->ldr};
   const int nblk = (W->Kp + 127) / 128, bs = ((W->Kp + nblk - 1) / nblk + 7) & ~7;  // kblocks (src/gemm_f16.c:55-58)
-  dim3 grid((unsigned)bnh_ceil_div(rows, 64), (unsigned)bnh_ceil_div(W->Np, 128));
-  hipLaunchKernelGGL(k_gemm_f16x, grid, dim3(256), 0, bnh_stream(stream), A, a_ws, lda, M, 1.0 / M, rows, W->w, W->b,
-                     W->b16, W->Kp, W->Np, bs, d);
+  // channel tiles: as few as cover Np with at most 128 channels each, TC = Np / 8 spread over them (at least 4)
+  const int np8 = W->Np / 8, ntile = (np8 + 15) / 16;
+  int tc = (np8 + ntile - 1) / ntile;
+  if (tc < 4) tc = 4;
+  const bool vec = ((uintptr_t)e->out & 15) == 0 && e->ldo % 8 == 0 && (B == 1 || e->out_ws % 8 == 0) &&
+                   (!e->res || (((uintptr_t)e->res & 15) == 0 && e->ldr % 8 == 0 && (B == 1 || e->res_ws % 8 == 0)));
+  const int tr = 256 / tc < 64 ? 256 / tc : 64, bm = 4 * tr;
+  const dim3 grid((unsigned)bnh_ceil_div(rows, bm), (unsigned)bnh_ceil_div(W->Np, 8 * tc));
+  hipStream_t st = bnh_stream(stream);
+  if (vec)
+    hipLaunchKernelGGL((k_gemm_f16e<true>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt, W->b,
+                       W->b16, W->Kp, W->Np, bs, tc, d);
+  else
+    hipLaunchKernelGGL((k_gemm_f16e<false>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt,
+                       W->b, W->b16, W->Kp, W->Np, bs, tc, d);
   BNH_HIP(hipGetLastError());
   return 0;
 }

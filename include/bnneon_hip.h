@@ -141,6 +141,10 @@ typedef struct {
  * VALU), fp32 sums across blocks, its bias and epilogue. */
 int bnh_gemm_f16(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
                  void *stream);
+/* bnh_gemm_f16 without its halo zeroing, for callers whose output halo is already zero (the runtime's buffers that
+ * own their arena slot keep the zero halo written when the arena was cleared) */
+int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
+                      void *stream);
 /* the same product on fp16 MFMA with fp32 accumulation over the whole K (no reference counterpart: a faster form
  * for callers that accept the fp16 accumulation error bound of the reference instead of its exact bits) */
 int bnh_gemm_f16_mfma(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,

@@ -45,7 +45,8 @@ def same_bits(a, b):
     return bool(np.array_equal(an, bn) and np.array_equal(a.view(np.uint16)[~an], b.view(np.uint16)[~bn]))
 
 
-def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, Kp=None, b16=None, fn="bnh_gemm_f16"):
+def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, Kp=None, b16=None, fn="bnh_gemm_f16", ldo=None,
+            o_slack=32):
     """A [B][M][lda] fp16 -> out [B][rows][ldo] fp16 through fn (bnh_gemm_f16 or bnh_gemm_f16_mfma)."""
     H = hip
     Bw, M, lda = A.shape
@@ -67,11 +68,11 @@ def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, Kp=None, b16=None, fn
         H.check(None, "bnh_h16w_new")
     try:
         rows = M if not opad else (M // ow + 2 * opad) * (ow + 2 * opad)
-        ldo = Np
+        ldo = ldo or Np
         a_ws = M * lda + 64
         ah = np.zeros((Bw, a_ws), np.float16)
         ah[:, :M * lda] = A.reshape(Bw, -1)
-        o_ws = rows * ldo + 32
+        o_ws = rows * ldo + o_slack
         dA = H.DeviceArray.from_host(ah)
         dO = H.DeviceArray.from_host(np.full((Bw, o_ws), np.float16(7.0)))   # garbage that the halo zeroing clears
         dR = None
@@ -125,6 +126,24 @@ def test_random_bit_exact(hip, K, N, M, B, act):
     for i in range(B):
         ref = O.gemm_f16(A[i], Wp, b, act=act, res=None if res is None else res[i])
         assert same_bits(out[i], ref), i
+
+
+@pytest.mark.parametrize("K,N,ldo,slack", [(72, 36, 44, 3), (300, 200, 204, 32), (40, 72, 76, 1)])
+def test_unaligned_output_strides(hip, K, N, ldo, slack):
+    """Output rows and window strides that are not multiples of 8 halves: the element-wise store path."""
+    rng = np.random.default_rng(K + ldo)
+    B, M = 3, 77
+    A = rng.standard_normal((B, M, (K + 7) // 8 * 8)).astype(np.float16)
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    res = rng.standard_normal((B, M, ldo)).astype(np.float16)
+    say("f16 gemm unaligned", K, N, ldo, slack)
+    out, Wp = run_gpu(hip, A, W, b, act=1, res=res, ldo=ldo, o_slack=slack)
+    for i in range(B):
+        ref = O.gemm_f16(A[i], Wp, b, act=1, ldo=ldo, res=res[i])
+        Np = (N + 7) // 8 * 8
+        assert same_bits(out[i][:, :Np], ref[:, :Np]), i
+        assert (out[i][:, Np:] == 7.0).all()
 
 
 @pytest.mark.parametrize("K", [96, 264])
@@ -207,3 +226,22 @@ def test_bad_params_refused(hip):
     w, b = np.zeros(256, np.float16), np.zeros(32, np.float32)
     assert not H.lib().bnh_h16w_new(10, 16, 16, 10, w.ctypes.data, b.ctypes.data, None)
     assert b"Np = N rounded up to 8" in H.lib().bnh_last_error()
+
+
+def test_silu_epilogue_every_fp16_input(hip):
+    """The GEMM's packed SiLU on every fp16 bit pattern: W picks k = 0, so the pre-activation of row m is the fp16
+    value with bits m (-0 becomes +0 through the chain's +0 start), and the outputs must equal the oracle's fp16 LUT
+    SiLU (src/silu_lut.h:28-42) bit for bit, NaNs as NaNs; ReLU the same way."""
+    M, K, N = 65536, 8, 16
+    A = np.zeros((1, M, K), np.float16)
+    A[0, :, 0] = np.arange(M, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    W = np.zeros((N, K), np.float16)
+    W[:, 0] = 1.0
+    b = np.zeros(N, np.float32)
+    for act in (1, 2):
+        say("f16 gemm every input, act", act)
+        out, Wp = run_gpu(hip, A, W, b, act=act)
+        ref = O.gemm_f16(A[0], Wp, b, act=act)
+        assert same_bits(out[0], ref)
+        # the NaN patterns stay NaN; the LUT SiLU of +inf is inf - inf = NaN as well (the reference's formula)
+        assert np.isnan(out[0][:, 0]).sum() == 2 * 1023 + (act == 1)
