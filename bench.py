@@ -524,7 +524,7 @@ def perch_roofline(H, pn, B, stream, a):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": PERCH_GEMM_TRAFFIC,
-            "kernel": "k_s8n_gemm<2, 2>",
+            "kernel": "k_s8n_gemm",
             "launch": f"PW_S8 GEMM {K}->{N} over {M} px x {B} windows, SiLU, halo-{opad} output",
             "ms_per_launch": round(ms, 4), "algorithmic_bytes_per_launch": nbytes}
 

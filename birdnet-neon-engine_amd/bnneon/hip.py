@@ -98,14 +98,14 @@ _SIGS = {
     "bnh_logmel_frames": (i32, [vp]),
     "bnh_logmel_run": (i32, [vp, vp, i64, vp, i64, i32, vp]),
     "bnh_stem_f32": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp, i64, i32, i32, i32, vp]),
-    "bnh_se_f32": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, i64, i32, vp]),
+    "bnh_se_f32": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, vp]),
     "bnh_mean_f32": (i32, [vp, i64, i32, i32, i32, vp, i64, i32, vp]),
     "bnh_pad": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, i64, i32, vp]),
     "bnh_zero_halo": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp]),
     "bnh_eval_expf": (i32, [vp, vp, i64, vp]),
     "bnh_stem_f32to16": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32,
                                i32, vp]),
-    "bnh_se_f16": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, i64, i32, vp]),
+    "bnh_se_f16": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, vp]),
     "bnh_mean_f16": (i32, [vp, i64, i32, i32, i32, vp, i64, i32, vp]),
     "bnh_gemv": (i32, [vp, i32, vp, i32, i32, vp, i64, i32, vp, i64, i32, vp]),
 }

@@ -117,11 +117,11 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
     for (int ky = 0; ky < K; ky++)
 #pragma unroll
       for (int kx = 0; kx < NC; kx++) xv[ky][kx] = kx < ncol ? x0[ky * rs + (long long)kx * C] : 0.f;
+    // all four outputs are computed (those past the item's end from the zeros above, then dropped), so the four
+    // chains and their SiLUs have no branches between them
     float v[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      v[q] = 0.f;
-      if (q >= item.n) continue;
       if (FORM == 2) {
         const int o = q * S;
         float acc = __builtin_fmaf(wv[0], xv[0][o], bias);
@@ -133,8 +133,8 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
         acc = __builtin_fmaf(wv[6], xv[2][o], acc);
         acb = __builtin_fmaf(wv[7], xv[2][o + 1], acb);
         acd = __builtin_fmaf(wv[8], xv[2][o + 2], acd);
-        v[q] = bnh_silu_f32_t(acc + (acb + acd), tbl);
-      } else {
+        v[q] = acc + (acb + acd);
+      } else if (item.split) {
         float a = bias, e = 0.f;
 #pragma unroll
         for (int ky = 0; ky < K; ky++)
@@ -142,13 +142,22 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
           for (int kx = 0; kx < K; kx++) {
             const int t = ky * K + kx;
             const float x = xv[ky][q * S + kx];
-            if (item.split && (t & 1)) e = __builtin_fmaf(x, wv[t], e);
+            if (t & 1) e = __builtin_fmaf(x, wv[t], e);
             else a = __builtin_fmaf(x, wv[t], a);
           }
-        float y = item.split ? a + e : a;
-        if (act == 1) y = bnh_silu_f32_t(y, tbl);
-        v[q] = y;
+        v[q] = a + e;
+      } else {
+        float a = bias;
+#pragma unroll
+        for (int ky = 0; ky < K; ky++)
+#pragma unroll
+          for (int kx = 0; kx < K; kx++) a = __builtin_fmaf(xv[ky][q * S + kx], wv[ky * K + kx], a);
+        v[q] = a;
       }
+    }
+    if (FORM == 2 || act == 1) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[q] = bnh_silu_f32_t(v[q], tbl);
     }
     float *o = ow + (long long)item.px * C;
 #pragma unroll

@@ -150,8 +150,12 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
   __shared__ uint16_t s_t2[16];
   const int tid = threadIdx.x, tc = tid % TC, tr = tid / TC;
   const bool active = tr < TR;
-  const long long rowB = (long long)blockIdx.x * BM;
-  const int n0 = blockIdx.y * TN;
+  // 1-D grid of (row block, channel tile) pairs, channel tile fastest, after the XCD remap: the blocks that write the
+  // parts of the same output rows run together under one L2, which merges their partial cache lines
+  const int nct = (Np + TN - 1) / TN;
+  const unsigned lb = bnh_xcd_block(blockIdx.x, gridDim.x);
+  const long long rowB = (long long)(lb / nct) * BM;
+  const int n0 = (int)(lb % nct) * TN;
   for (int i = tid; i < BM; i += 256) {
     const long long row = rowB + i < rows ? rowB + i : rows - 1;
     const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
@@ -394,7 +398,9 @@ int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, 
   const bool vec = ((uintptr_t)e->out & 15) == 0 && e->ldo % 8 == 0 && (B == 1 || e->out_ws % 8 == 0) &&
                    (!e->res || (((uintptr_t)e->res & 15) == 0 && e->ldr % 8 == 0 && (B == 1 || e->res_ws % 8 == 0)));
   const int tr = 256 / tc < 64 ? 256 / tc : 64, bm = 4 * tr;
-  const dim3 grid((unsigned)bnh_ceil_div(rows, bm), (unsigned)bnh_ceil_div(W->Np, 8 * tc));
+  const long long nb = bnh_ceil_div(rows, bm) * bnh_ceil_div(W->Np, 8 * tc);
+  BNH_REQ(nb < (1LL << 31));
+  const dim3 grid((unsigned)nb);
   hipStream_t st = bnh_stream(stream);
   if (vec)
     hipLaunchKernelGGL((k_gemm_f16e<true>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt, W->b,

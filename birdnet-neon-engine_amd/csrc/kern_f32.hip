@@ -86,7 +86,103 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
   }
 }
 
-// ------------------------------------------------------------------ SE_GATE / SE: one block per group of windows
+// ------------------------------------------------------------------ SE_GATE / SE
+// The gate's sigmoid: sigmoid_f32x4 (src/gemm_f32.h:93-96), 1 / (1 + exp2_f32x4(-a log2 e)) by FRECPE and two
+// Newton steps; F16: the fp16 path's sigm4 (src/v24_fast.c:182-195), the same 2^t divided into 1 (IEEE division)
+template <bool F16>
+BNH_DEV float se_sigmoid(float a) {
+  float t = a * -1.44269504f;
+  t = bnh_fmin(bnh_fmax(t, -126.f), 126.f);
+  const float n = __builtin_rintf(t), f = t - n;
+  float q = 1.5403530e-4f;
+  q = __builtin_fmaf(q, f, 1.3333558e-3f);
+  q = __builtin_fmaf(q, f, 9.6181291e-3f);
+  q = __builtin_fmaf(q, f, 5.5504109e-2f);
+  q = __builtin_fmaf(q, f, 2.4022651e-1f);
+  q = __builtin_fmaf(q, f, 6.9314718e-1f);
+  q = __builtin_fmaf(q, f, 1.f);
+  const float e = bnh_float(bnh_bits(q) + ((uint32_t)bnh_cvtz_s32(n) << 23));
+  const float d = 1.f + e;
+  if (F16) return 1.f / d;
+  float rr = bnh_frecpe(d);
+  rr = rr * bnh_frecps(d, rr);
+  return rr * bnh_frecps(d, rr);
+}
+
+// With a workspace the gates come from two kernels over all windows. k_se_fc1: a block per WB windows x 32 rows r of
+// w1; thread (r, l) runs lane chain l (c = l, l + 8, ...; the K % 8 remainder in lanes 0-3, as two 4-lane
+// accumulators over 8-channel steps do) for its WB windows; the chains are summed pairwise, + b1, SiLU by the C
+// library's expf, into s1 [B][rd].
+template <int WB>
+__global__ __launch_bounds__(256) void k_se_fc1(const float *__restrict__ chsum, long long c_ws, int C, int rd, float inv,
+                                                const float *__restrict__ w1, const float *__restrict__ b1,
+                                                float *__restrict__ s1, int B) {
+  extern __shared__ float sm[];
+  float *mean = sm, *part = sm + WB * C;  // [WB][C], [WB][32][8]
+  const int win0 = blockIdx.x * WB, nw = B - win0 < WB ? B - win0 : WB, r0 = blockIdx.y * 32, tid = threadIdx.x;
+  for (int i = tid; i < WB * C; i += 256) {
+    const int wg = i / C, c = i - wg * C;
+    mean[i] = wg < nw ? chsum[(win0 + wg) * c_ws + c] * inv : 0.f;
+  }
+  __syncthreads();
+  const int rl = tid / 8, l = tid % 8, r = r0 + rl, C8 = C / 8 * 8;
+  if (r < rd) {
+    const float *w = w1 + (long long)r * C;
+    float a[WB];
+#pragma unroll
+    for (int wg = 0; wg < WB; wg++) a[wg] = 0.f;
+#pragma unroll 4
+    for (int c = l; c < C8; c += 8) {
+      const float wv = w[c];
+#pragma unroll
+      for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv, mean[wg * C + c], a[wg]);
+    }
+    if (l < 4 && C8 + l < C) {
+      const float wv = w[C8 + l];
+#pragma unroll
+      for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv, mean[wg * C + C8 + l], a[wg]);
+    }
+#pragma unroll
+    for (int wg = 0; wg < WB; wg++) part[(wg * 32 + rl) * 8 + l] = a[wg];
+  }
+  __syncthreads();
+  for (int i = tid; i < WB * 32; i += 256) {
+    const int wg = i / 32, rr = r0 + i % 32;
+    if (wg >= nw || rr >= rd) continue;
+    const float *pp = part + i * 8;
+    const float v = ((pp[0] + pp[4]) + (pp[1] + pp[5])) + ((pp[2] + pp[6]) + (pp[3] + pp[7]));
+    const float x = v + b1[rr];
+    s1[(long long)(win0 + wg) * rd + rr] = x / (1.f + bnh_expf(-x));  // silu_s: the C library's expf
+  }
+}
+
+// k_se_fc2: a thread per channel c of WB windows: from b2, one FMA per row r, then the sigmoid, into gate
+template <int WB, bool F16>
+__global__ __launch_bounds__(256) void k_se_fc2(const float *__restrict__ s1, int C, int rd,
+                                                const float *__restrict__ w2t, const float *__restrict__ b2,
+                                                float *__restrict__ gate, long long g_ws, int B) {
+  extern __shared__ float ss[];  // [WB][rd]
+  const int win0 = blockIdx.y * WB, nw = B - win0 < WB ? B - win0 : WB, tid = threadIdx.x;
+  for (int i = tid; i < WB * rd; i += 256) ss[i] = i / rd < nw ? s1[(long long)win0 * rd + i] : 0.f;
+  __syncthreads();
+  const int c = blockIdx.x * 256 + tid;
+  if (c >= C) return;
+  float a[WB];
+  const float b = b2[c];
+#pragma unroll
+  for (int wg = 0; wg < WB; wg++) a[wg] = b;
+#pragma unroll 4
+  for (int r = 0; r < rd; r++) {
+    const float wv = w2t[(long long)r * C + c];
+#pragma unroll
+    for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv, ss[wg * rd + r], a[wg]);
+  }
+#pragma unroll
+  for (int wg = 0; wg < WB; wg++)
+    if (wg < nw) gate[(win0 + wg) * g_ws + c] = se_sigmoid<F16>(a[wg]);
+}
+
+// Without a workspace: one block per group of windows
 // A block computes the gates of WG windows (so each weight it streams serves WG windows), every value with the
 // reference's instructions in its order: mean = chsum * (1 / P); fc1 as eight lane chains (two 4-lane accumulators
 // over 8-channel steps) summed pairwise, + b1, SiLU by the C library's expf; fc2 from b2, one FMA per row r;
@@ -151,27 +247,7 @@ __global__ __launch_bounds__(256) void k_se_f32(const float *__restrict__ chsum,
     }
 #pragma unroll
     for (int wg = 0; wg < WG; wg++) {
-      // sigmoid_f32x4: 1 / (1 + exp2_f32x4(-a log2 e)) by FRECPE and two Newton steps
-      float t = a[wg] * -1.44269504f;
-      t = bnh_fmin(bnh_fmax(t, -126.f), 126.f);
-      const float n = __builtin_rintf(t), f = t - n;
-      float q = 1.5403530e-4f;
-      q = __builtin_fmaf(q, f, 1.3333558e-3f);
-      q = __builtin_fmaf(q, f, 9.6181291e-3f);
-      q = __builtin_fmaf(q, f, 5.5504109e-2f);
-      q = __builtin_fmaf(q, f, 2.4022651e-1f);
-      q = __builtin_fmaf(q, f, 6.9314718e-1f);
-      q = __builtin_fmaf(q, f, 1.f);
-      const float e = bnh_float(bnh_bits(q) + ((uint32_t)bnh_cvtz_s32(n) << 23));
-      const float d = 1.f + e;
-      float rr;
-      if (F16) {
-        rr = 1.f / d;
-      } else {
-        rr = bnh_frecpe(d);
-        rr = rr * bnh_frecps(d, rr);
-        rr = rr * bnh_frecps(d, rr);
-      }
+      const float rr = se_sigmoid<F16>(a[wg]);
       g[wg * C + c] = rr;
       if (gate && wg < nw) gate[(win0 + wg) * g_ws + c] = rr;
     }
@@ -323,49 +399,69 @@ __global__ void k_eval_expf(const float *__restrict__ x, float *__restrict__ y, 
 }
 
 // ------------------------------------------------------------------ PAD: every element of the padded buffer
-template <typename T>
-__global__ void k_pad(const T *__restrict__ x, long long x_ws, int H, int W, int C, int ld, int h, T *__restrict__ xp,
-                      long long p_ws, long long total) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int Wp = W + 2 * h;
-  const long long per = (long long)(H + 2 * h) * Wp * C;
-  const int win = (int)(i / per);
-  const long long e = i % per, px = e / C;
-  const int c = (int)(e % C), y = (int)(px / Wp) - h, xx = (int)(px % Wp) - h;
-  T v = (T)0;
-  if (y >= 0 && y < H && xx >= 0 && xx < W) v = x[win * x_ws + ((long long)y * W + xx) * ld + c];
-  xp[win * p_ws + e] = v;
+// PAD: a thread per V consecutive elements of one window's padded buffer (V = 16 bytes when the channel count, the
+// row stride and the window strides allow, else 1), windows on grid.y; halo elements get zero
+template <typename T, int V>
+__global__ __launch_bounds__(256) void k_pad(const T *__restrict__ x, long long x_ws, int H, int W, int C, int ld,
+                                             int h, T *__restrict__ xp, long long p_ws, int per) {
+  const int i = (blockIdx.x * 256 + threadIdx.x) * V;
+  if (i >= per) return;
+  const long long win = blockIdx.y;
+  const int Wp = W + 2 * h, px = i / C, c = i - px * C, y = px / Wp - h, xx = px - (px / Wp) * Wp - h;
+  typedef T vt __attribute__((ext_vector_type(V)));
+  vt v = (vt)0;
+  if (y >= 0 && y < H && xx >= 0 && xx < W) v = *(const vt *)(x + win * x_ws + ((long long)y * W + xx) * ld + c);
+  *(vt *)(xp + win * p_ws + i) = v;
 }
 
 
 static int se_launch(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
-                     const float *w2t, const float *b2, float *gate, long long g_ws, void *D, long long d_ws, int B,
-                     bool f16, void *stream) {
+                     const float *w2t, const float *b2, float *gate, long long g_ws, float *work, void *D,
+                     long long d_ws, int B, bool f16, void *stream) {
   BNH_REQ(chsum && w1 && b1 && w2t && b2 && (gate || D) && B > 0);
   BNH_REQ(C > 0 && C % 4 == 0 && C <= 4096 && rd > 0 && rd <= 512 && P > 0);
   BNH_REQ(B == 1 || (c_ws >= C && (!gate || g_ws >= C) && (!D || d_ws >= (long long)P * C)));
-  // windows per block: as many as 64 KB of LDS holds, at most 4
-  const size_t per = sizeof(float) * (2 * (size_t)C + 9 * (size_t)rd);
-  int wg = (int)((64 * 1024) / per);
-  wg = wg >= 4 ? 4 : wg >= 2 ? 2 : 1;
-  if (wg > B) wg = B >= 4 ? 4 : B >= 2 ? 2 : 1;
-  const dim3 grid((unsigned)bnh_ceil_div(B, wg));
   hipStream_t st = bnh_stream(stream);
   // with a gate buffer and C % 8 == 0 the gates go there first and a second kernel over every window's pixels
   // scales D (a block per group of windows scaling its own activations leaves most of the chip idle)
   const bool split = gate && D && C % 8 == 0;
-  void *Dk = split ? nullptr : D;
+  if (gate && work) {
+    // the two FCs as kernels over all windows: fc1 into work [B][rd], fc2 + sigmoid into gate
+    const int wb1 = (size_t)4 * C * 4 + 4 * 32 * 8 * 4 <= 64 * 1024 ? 4 : 1;
+    const float inv = 1.f / (float)P;
+    const dim3 g1((unsigned)bnh_ceil_div(B, wb1), (unsigned)bnh_ceil_div(rd, 32));
+    const size_t l1 = sizeof(float) * ((size_t)wb1 * C + (size_t)wb1 * 32 * 8);
+    if (wb1 == 4) hipLaunchKernelGGL((k_se_fc1<4>), g1, dim3(256), l1, st, chsum, c_ws, C, rd, inv, w1, b1, work, B);
+    else hipLaunchKernelGGL((k_se_fc1<1>), g1, dim3(256), l1, st, chsum, c_ws, C, rd, inv, w1, b1, work, B);
+    BNH_HIP(hipGetLastError());
+    const dim3 g2((unsigned)bnh_ceil_div(C, 256), (unsigned)bnh_ceil_div(B, 4));
+    const size_t l2 = sizeof(float) * 4 * (size_t)rd;
+    if (f16) hipLaunchKernelGGL((k_se_fc2<4, true>), g2, dim3(256), l2, st, work, C, rd, w2t, b2, gate, g_ws, B);
+    else hipLaunchKernelGGL((k_se_fc2<4, false>), g2, dim3(256), l2, st, work, C, rd, w2t, b2, gate, g_ws, B);
+    BNH_HIP(hipGetLastError());
+    if (D && !split) {  // C % 8 != 0: the one-kernel form gates D (recomputing the same gates)
+      work = nullptr;
+    }
+  }
+  if (!(gate && work)) {
+    // windows per block: as many as 64 KB of LDS holds, at most 4
+    const size_t per = sizeof(float) * (2 * (size_t)C + 9 * (size_t)rd);
+    int wg = (int)((64 * 1024) / per);
+    wg = wg >= 4 ? 4 : wg >= 2 ? 2 : 1;
+    if (wg > B) wg = B >= 4 ? 4 : B >= 2 ? 2 : 1;
+    const dim3 grid((unsigned)bnh_ceil_div(B, wg));
+    void *Dk = split ? nullptr : D;
 #define SE_LAUNCH(W, F)                                                                                                \
   hipLaunchKernelGGL((k_se_f32<W, F>), grid, dim3(256), per * W, st, chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate,    \
                      g_ws, Dk, d_ws, B)
-  if (f16) {
-    if (wg == 4) SE_LAUNCH(4, true); else if (wg == 2) SE_LAUNCH(2, true); else SE_LAUNCH(1, true);
-  } else {
-    if (wg == 4) SE_LAUNCH(4, false); else if (wg == 2) SE_LAUNCH(2, false); else SE_LAUNCH(1, false);
-  }
+    if (f16) {
+      if (wg == 4) SE_LAUNCH(4, true); else if (wg == 2) SE_LAUNCH(2, true); else SE_LAUNCH(1, true);
+    } else {
+      if (wg == 4) SE_LAUNCH(4, false); else if (wg == 2) SE_LAUNCH(2, false); else SE_LAUNCH(1, false);
+    }
 #undef SE_LAUNCH
-  BNH_HIP(hipGetLastError());
+    BNH_HIP(hipGetLastError());
+  }
   if (!split) return 0;
   const long long n8 = (long long)P * C / 8;
   const unsigned esz = f16 ? 2 : 4;
@@ -453,16 +549,16 @@ int bnh_stem_f32to16(const float *img, long long i_ws, int H, int W, int k, int 
 
 
 int bnh_se_f32(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
-               const float *w2t, const float *b2, float *gate, long long g_ws, float *D, long long d_ws, int B,
-               void *stream) {
-  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws, D, d_ws, B, false, stream);
+               const float *w2t, const float *b2, float *gate, long long g_ws, float *work, float *D, long long d_ws,
+               int B, void *stream) {
+  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws, work, D, d_ws, B, false, stream);
 }
 
 int bnh_se_f16(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
-               const float *w2t, const float *b2, float *gate, long long g_ws, uint16_t *D, long long d_ws, int B,
-               void *stream) {
+               const float *w2t, const float *b2, float *gate, long long g_ws, float *work, uint16_t *D,
+               long long d_ws, int B, void *stream) {
   BNH_REQ(D);
-  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws, D, d_ws, B, true, stream);
+  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws, work, D, d_ws, B, true, stream);
 }
 
 int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
@@ -510,15 +606,25 @@ int bnh_gemv(const void *w, int w16, const float *bias, int N, int K, const floa
 int bnh_pad(const void *x, long long x_ws, int H, int W, int C, int ld, int h, int esz, void *xp, long long p_ws, int B,
             void *stream) {
   BNH_REQ(x && xp && H > 0 && W > 0 && C > 0 && ld >= C && h >= 0 && h <= 3 && B > 0 && (esz == 4 || esz == 2));
-  const long long per = (long long)(H + 2 * h) * (W + 2 * h) * C, total = per * B;
+  const long long per = (long long)(H + 2 * h) * (W + 2 * h) * C;
   BNH_REQ(B == 1 || (x_ws >= (long long)H * W * ld && p_ws >= per));
-  const dim3 grid((unsigned)bnh_ceil_div(total, 256));
-  if (esz == 4)
-    hipLaunchKernelGGL(k_pad<uint32_t>, grid, dim3(256), 0, bnh_stream(stream), (const uint32_t *)x, x_ws, H, W, C, ld,
-                       h, (uint32_t *)xp, p_ws, total);
-  else
-    hipLaunchKernelGGL(k_pad<uint16_t>, grid, dim3(256), 0, bnh_stream(stream), (const uint16_t *)x, x_ws, H, W, C, ld,
-                       h, (uint16_t *)xp, p_ws, total);
+  BNH_REQ(per < (1LL << 31));
+  const int v = 16 / esz;  // elements per 16 bytes
+  const bool vec = C % v == 0 && ld % v == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)xp & 15) == 0 &&
+                   (B == 1 || (x_ws % v == 0 && p_ws % v == 0));
+  const dim3 grid((unsigned)bnh_ceil_div(per, 256LL * (vec ? v : 1)), (unsigned)B);
+  hipStream_t st = bnh_stream(stream);
+  if (esz == 4) {
+    if (vec) hipLaunchKernelGGL((k_pad<uint32_t, 4>), grid, dim3(256), 0, st, (const uint32_t *)x, x_ws, H, W, C, ld, h,
+                                (uint32_t *)xp, p_ws, (int)per);
+    else hipLaunchKernelGGL((k_pad<uint32_t, 1>), grid, dim3(256), 0, st, (const uint32_t *)x, x_ws, H, W, C, ld, h,
+                            (uint32_t *)xp, p_ws, (int)per);
+  } else {
+    if (vec) hipLaunchKernelGGL((k_pad<uint16_t, 8>), grid, dim3(256), 0, st, (const uint16_t *)x, x_ws, H, W, C, ld, h,
+                                (uint16_t *)xp, p_ws, (int)per);
+    else hipLaunchKernelGGL((k_pad<uint16_t, 1>), grid, dim3(256), 0, st, (const uint16_t *)x, x_ws, H, W, C, ld, h,
+                            (uint16_t *)xp, p_ws, (int)per);
+  }
   BNH_HIP(hipGetLastError());
   return 0;
 }

@@ -232,24 +232,30 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
 }
 
 // ------------------------------------------------------------------ int8 GEMM + fp32 dequant epilogue
-// A block owns WM * 32 rows (pixels of consecutive windows) x WN * 64 channels; its threads first resolve each row's
-// window, pixel, quantisation parameters and output / residual addresses into LDS (once per row), then every wave
-// runs 32 rows x 64 channels of i8 MFMAs and the reference's epilogue from those.
-template <int WM, int WN>
+// A block owns 128 rows (pixels of consecutive windows); its threads first resolve each row's window, pixel,
+// quantisation parameters and output / residual addresses into LDS (once per row). Each wave then owns 32 of the
+// rows and walks the 64-channel groups [g0, g1) of its block: per group 2 x 4 i8 MFMA tiles over K and the
+// reference's epilogue. A wave writing every channel of its rows, one group after the other, hands whole output rows
+// to its L2, where their cache lines complete before they are written back (rows split between blocks leave partial
+// lines, which cost HBM write rate). Blocks split the channel groups only when there are too few rows to fill the
+// chip (gsplit blocks per row block, consecutive after the XCD remap so that they share an L2).
 __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, long long q_ws,
                                                   const float *__restrict__ sa, long long sa_ws,
                                                   const int32_t *__restrict__ za, long long za_ws, int M, double rM,
                                                   long long rows, const int8_t *__restrict__ wt,
                                                   const float *__restrict__ sw, const int32_t *__restrict__ cs,
-                                                  const float *__restrict__ bias, int Kp, int Np, EpiDev e) {
-  constexpr int RB = WM * 32;
+                                                  const float *__restrict__ bias, int Kp, int Np, int gsplit,
+                                                  EpiDev e) {
+  constexpr int RB = 128;
   __shared__ long long s_q[RB], s_o[RB], s_r[RB];
   __shared__ float s_sa[RB];
   __shared__ uint32_t s_z[RB], s_tbl[256];
   bnh_silu_table(s_tbl);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const long long rowB = (long long)blockIdx.x * RB;
+  const unsigned lb = gsplit > 1 ? bnh_xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+  const long long rowB = (long long)(lb / gsplit) * RB;
+  const int ng = (Np + 63) / 64, part = (int)(lb % gsplit);
+  const int g0 = part * ng / gsplit, g1 = (part + 1) * ng / gsplit;
   for (int i = threadIdx.x; i < RB; i += 256) {
     const long long row = rowB + i < rows ? rowB + i : rows - 1;  // rows past the end repeat the last row
     const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
@@ -260,79 +266,103 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
     s_z[i] = (uint32_t)za[w * za_ws + m];
   }
   __syncthreads();
-  const int lr0 = wm * 32;  // the wave's first row within the block
+  const int lr0 = wave * 32;  // the wave's first row within the block
   if (rowB + lr0 >= rows) return;
-  const int n0 = blockIdx.y * (WN * 64) + wn * 64;
   const int kc = (lane >> 4) * 16;  // this lane's k chunk within a 64-wide step
   const int8_t *ap[2];
 #pragma unroll
   for (int t = 0; t < 2; t++) ap[t] = q + s_q[lr0 + 16 * t + (lane & 15)] + kc;
-  const int8_t *bp = wt + (long long)(n0 + (lane & 15)) * Kp + kc;
-  v4i acc[2][4];
-#pragma unroll
-  for (int t = 0; t < 2; t++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[t][j] = (v4i){0, 0, 0, 0};
   const int kmain = Kp & ~63;
-  for (int k = 0; k < kmain; k += 64) {
-    v4i a[2], b[4];
+  const bool kin = kmain + kc < Kp;  // this lane's chunk of the last partial step holds k < Kp
+  // one K step (Kp <= 64, the expansions): the A fragments once for every group
+  v4i a1[2];
+  if (Kp <= 64) {
 #pragma unroll
-    for (int t = 0; t < 2; t++) a[t] = *(const v4i *)(ap[t] + k);
-#pragma unroll
-    for (int j = 0; j < 4; j++) b[j] = *(const v4i *)(bp + (long long)16 * j * Kp + k);
+    for (int t = 0; t < 2; t++) a1[t] = kin ? *(const v4i *)(ap[t]) : (v4i){0, 0, 0, 0};
+  }
+  for (int g = g0; g < g1; g++) {
+    const int n0 = 64 * g;
+    const int jn = Np - n0 >= 64 ? 4 : (Np - n0 + 15) / 16;  // the 16-channel groups that hold channels < Np
+    const int8_t *bp = wt + (long long)(n0 + (lane & 15)) * Kp + kc;
+    v4i acc[2][4];
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[j], acc[t][j], 0, 0, 0);
-  }
-  if (kmain < Kp) {  // the last partial step: chunks at or past Kp contribute zeros
-    const bool in = kmain + kc < Kp;
-    v4i a[2], b[4];
+      for (int j = 0; j < 4; j++) acc[t][j] = (v4i){0, 0, 0, 0};
+    if (Kp <= 64) {
+      v4i b[4];
 #pragma unroll
-    for (int t = 0; t < 2; t++) a[t] = in ? *(const v4i *)(ap[t] + kmain) : (v4i){0, 0, 0, 0};
+      for (int j = 0; j < 4; j++) b[j] = kin && j < jn ? *(const v4i *)(bp + (long long)16 * j * Kp) : (v4i){0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < 4; j++) b[j] = in ? *(const v4i *)(bp + (long long)16 * j * Kp + kmain) : (v4i){0, 0, 0, 0};
+      for (int t = 0; t < 2; t++)
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+        for (int j = 0; j < 4; j++)
+          if (j < jn) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[t], b[j], acc[t][j], 0, 0, 0);
+    } else {
+      for (int k = 0; k < kmain; k += 64) {
+        v4i a[2], b[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[j], acc[t][j], 0, 0, 0);
-  }
-  // epilogue (deq4 + activation + store_rows, src/gemm_s8n.c:105-135): acc[t][j][r] is row 16t + 4 (lane >> 4) + r,
-  // channel 16j + (lane & 15) of the wave's tile
-  float swn[4], bn[4];
-  int32_t csn[4];
+        for (int t = 0; t < 2; t++) a[t] = *(const v4i *)(ap[t] + k);
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int n = n0 + 16 * j + (lane & 15);
-    swn[j] = sw[n];
-    bn[j] = bias[n];
-    csn[j] = cs[n];
-  }
+        for (int j = 0; j < 4; j++) b[j] = j < jn ? *(const v4i *)(bp + (long long)16 * j * Kp + k) : (v4i){0, 0, 0, 0};
 #pragma unroll
-  for (int t = 0; t < 2; t++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int lr = lr0 + 16 * t + 4 * (lane >> 4) + r;
-      if (rowB + lr >= rows) continue;
-      const float s_a = s_sa[lr];
-      const uint32_t z = s_z[lr];
-      float *orow = e.out + s_o[lr];
-      const float *rrow = e.res ? e.res + s_r[lr] : nullptr;
+          for (int j = 0; j < 4; j++)
+            if (j < jn) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[j], acc[t][j], 0, 0, 0);
+      }
+      if (kmain < Kp) {  // the last partial step: chunks at or past Kp contribute zeros
+        v4i a[2], b[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int n = n0 + 16 * j + (lane & 15);
-        if (n >= Np) continue;
-        const int32_t c = (int32_t)((uint32_t)acc[t][j][r] - (uint32_t)csn[j] * z);
-        const float f = (float)c;
-        const float scl = swn[j] * s_a;
-        float y = f * scl;
-        y = y + bn[j];
-        if (e.act == 1) y = bnh_silu_f32_t(y, s_tbl);
-        else if (e.act == 2) y = bnh_relu_f32(y);
-        if (rrow) y = y + rrow[n];
-        orow[n] = y;
+        for (int t = 0; t < 2; t++) a[t] = kin ? *(const v4i *)(ap[t] + kmain) : (v4i){0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          b[j] = kin && j < jn ? *(const v4i *)(bp + (long long)16 * j * Kp + kmain) : (v4i){0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            if (j < jn) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[j], acc[t][j], 0, 0, 0);
       }
     }
+    // epilogue (deq4 + activation + store_rows, src/gemm_s8n.c:105-135): acc[t][j][r] is row 16t + 4 (lane >> 4) + r,
+    // channel n0 + 16j + (lane & 15)
+    float swn[4], bn[4];
+    int32_t csn[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int n = n0 + 16 * j + (lane & 15);
+      swn[j] = sw[n];
+      bn[j] = bias[n];
+      csn[j] = cs[n];
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int lr = lr0 + 16 * t + 4 * (lane >> 4) + r;
+        if (rowB + lr >= rows) continue;
+        const float s_a = s_sa[lr];
+        const uint32_t z = s_z[lr];
+        float *orow = e.out + s_o[lr];
+        const float *rrow = e.res ? e.res + s_r[lr] : nullptr;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          if (j >= jn) break;
+          const int n = n0 + 16 * j + (lane & 15);
+          if (n >= Np) continue;
+          const int32_t c = (int32_t)((uint32_t)acc[t][j][r] - (uint32_t)csn[j] * z);
+          const float f = (float)c;
+          const float scl = swn[j] * s_a;
+          float y = f * scl;
+          y = y + bn[j];
+          if (e.act == 1) y = bnh_silu_f32_t(y, s_tbl);
+          else if (e.act == 2) y = bnh_relu_f32(y);
+          if (rrow) y = y + rrow[n];
+          orow[n] = y;
+        }
+      }
+  }
 }
 
 // ------------------------------------------------------------------ int8 GEMM, Q31 requant, NCHW
@@ -768,15 +798,16 @@ int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, long long sa_
               e->opad ? 1.0 / e->ow : 0.0, e->rpad ? 1.0 / e->rw : 0.0};
   hipStream_t s = bnh_stream(stream);
   const double rM = 1.0 / M;
-  if (W->Np > 64) {
-    dim3 grid((unsigned)bnh_ceil_div(rows, 64), (unsigned)bnh_ceil_div(W->Np, 128));
-    hipLaunchKernelGGL((k_s8n_gemm<2, 2>), grid, dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rM, rows, W->w,
-                       W->sw, W->colsum, W->b, W->Kp, W->Np, d);
-  } else {
-    dim3 grid((unsigned)bnh_ceil_div(rows, 128), 1);
-    hipLaunchKernelGGL((k_s8n_gemm<4, 1>), grid, dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rM, rows, W->w,
-                       W->sw, W->colsum, W->b, W->Kp, W->Np, d);
-  }
+  // 128 rows per block; the channel groups split over gsplit blocks only when the row blocks alone would leave the
+  // chip short of blocks (fewer than 1024)
+  const long long nrb = bnh_ceil_div(rows, 128);
+  const int ng = (W->Np + 63) / 64;
+  int gsplit = 1;
+  if (nrb < 1024) gsplit = (int)bnh_ceil_div(1024, nrb);
+  if (gsplit > ng) gsplit = ng;
+  BNH_REQ(nrb * gsplit < (1LL << 31));
+  hipLaunchKernelGGL(k_s8n_gemm, dim3((unsigned)(nrb * gsplit)), dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rM,
+                     rows, W->w, W->sw, W->colsum, W->b, W->Kp, W->Np, gsplit, d);
   BNH_HIP(hipGetLastError());
   return 0;
 }

@@ -133,12 +133,13 @@ static int se_init(rt_ctx *c, rt_op *op) {
 }
 static int se_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
-  const long long g_ws = p[0];  // C % 8 == 0: 16-byte aligned gate rows
-  float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)g_ws);
+  // op scratch per window: the gates (C % 8 == 0: 16-byte aligned rows), then the first FC's outputs
+  const long long g_ws = p[0];
+  float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)(g_ws + p[1]));
   if (!g) return -1;
   return bnh_se_f16((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_h(op, 0),
                     (const float *)dev_h(op, 1), (const float *)dev_h(op, 2), (const float *)dev_h(op, 3), g, g_ws,
-                    (uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
+                    g + g_ws * c->bcap, (uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
 }
 
 // -------- MEAN f16, PAD f16 (src/rt_ops_f16.c:204-214)

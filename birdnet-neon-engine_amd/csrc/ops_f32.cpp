@@ -194,18 +194,21 @@ static int se_init(rt_ctx *c, rt_op *op) { return se_check(c, op, 0); }
 static int seg_init(rt_ctx *c, rt_op *op) { return se_check(c, op, 1); }
 static int se_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
-  const long long g_ws = (p[0] + 3) / 4 * 4;  // the gates of each window, 16-byte aligned rows
-  float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)g_ws);
+  // op scratch per window: the gates (16-byte aligned rows), then the first FC's outputs
+  const long long g_ws = (p[0] + 3) / 4 * 4;
+  float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)(g_ws + p[1]));
   if (!g) return -1;
   return bnh_se_f32((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_tn(op, 0),
                     (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3), g, g_ws,
-                    (float *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
+                    g + g_ws * c->bcap, (float *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
 }
 static int seg_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
+  float *work = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)p[1]);  // the first FC's outputs
+  if (!work) return -1;
   return bnh_se_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[0], p[1], p[2], (const float *)dev_tn(op, 0),
                     (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3),
-                    (float *)rt_b(c, op, 1), rt_ws(c, op, 1), nullptr, 0, c->nwin, c->stream);
+                    (float *)rt_b(c, op, 1), rt_ws(c, op, 1), work, nullptr, 0, c->nwin, c->stream);
 }
 
 // -------- MEAN: b = [x [P][ld], out f32 [C]]; p = [P C ld]   (rt_mean_check, src/rt_ops_f32.c:510-522)

@@ -232,10 +232,12 @@ int bnh_stem_f32(const float *img, long long i_ws, int H, int W, int k, int s, i
  * 164-210): from the channel sums chsum [C] of P pixels, gate [C] = sigmoid(w2 silu(w1 mean + b1) + b2) (w1 [rd][C],
  * b1 [rd], w2t [rd][C], b2 [C]; silu by the C library's expf, as the reference). gate (or NULL) receives it; D (or
  * NULL) [P][C] is multiplied by it in place (with both and C % 8 == 0 by a second kernel over every window's
- * pixels, the fast form). C % 4 == 0, C <= 4096, rd <= 512. */
+ * pixels, the fast form). work (or NULL): a workspace of B x rd floats; with it and gate the two FCs run as
+ * kernels over all windows (the fast form), without it one kernel per group of windows computes them.
+ * C % 4 == 0, C <= 4096, rd <= 512. */
 int bnh_se_f32(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
-               const float *w2t, const float *b2, float *gate, long long g_ws, float *D, long long d_ws, int B,
-               void *stream);
+               const float *w2t, const float *b2, float *gate, long long g_ws, float *work, float *D, long long d_ws,
+               int B, void *stream);
 /* STEM of the fp16 path: replaces stem_run (src/rt_ops_f16.c:167-180): the fp32 stem above, then channels < N
  * rounded to fp16 into out fp16 [Ho+2opad][Wo+2opad][ldo] (halo zeroed; channels N..ldo untouched) */
 int bnh_stem_f32to16(const float *img, long long i_ws, int H, int W, int k, int s, int Ho, int Wo, const float *w,
@@ -245,10 +247,10 @@ int bnh_stem_f32to16(const float *img, long long i_ws, int H, int W, int k, int 
  * bnh_se_f32 computes it but with a dividing sigmoid, rounded to fp16; D fp16 [P][C] multiplied by it in fp16.
  * gate: optional workspace fp32 [B][g_ws >= C] that receives the (unrounded) gates; with it and C % 8 == 0 the
  * scaling runs as its own kernel over every window's pixels (the fast form); NULL computes and applies the gates in
- * one kernel per group of windows. */
+ * one kernel per group of windows. work: as for bnh_se_f32. */
 int bnh_se_f16(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
-               const float *w2t, const float *b2, float *gate, long long g_ws, uint16_t *D, long long d_ws, int B,
-               void *stream);
+               const float *w2t, const float *b2, float *gate, long long g_ws, float *work, uint16_t *D,
+               long long d_ws, int B, void *stream);
 /* MEAN of fp16 rows: replaces pc_mean_f16 (src/pc_kern_f16.c:115-121) */
 int bnh_mean_f16(const uint16_t *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
                  void *stream);

@@ -132,9 +132,12 @@ def test_stem(hip, Hh, W, k, s, co, act, opad):
             assert (got[i][:, Np:] == 5.0).all()   # channels past Np untouched
 
 
-@pytest.mark.parametrize("C,rd,P,inplace", [(40, 10, 15687, False), (2304, 96, 64, False), (36, 9, 100, True),
-                                            (4096, 512, 8, False), (816, 34, 256, True)])
-def test_se(hip, C, rd, P, inplace):
+@pytest.mark.parametrize("C,rd,P,inplace,ws", [(40, 10, 15687, False, True), (2304, 96, 64, False, True),
+                                               (2304, 96, 64, False, False), (36, 9, 100, True, True),
+                                               (4096, 512, 8, False, True), (816, 34, 256, True, True),
+                                               (816, 34, 256, True, False), (1392, 58, 5, False, True)])
+def test_se(hip, C, rd, P, inplace, ws):
+    """ws: with the FC workspace (two kernels over all windows) or without (one kernel per group of windows)."""
     H = hip
     rng = np.random.default_rng(C + rd)
     B = 3
@@ -154,9 +157,10 @@ def test_se(hip, C, rd, P, inplace):
     if inplace:
         Ds, d_ws = strided(D, 9)
         dD = H.DeviceArray.from_host(Ds)
-    say("se", C, rd, P, inplace)
+    dwk = H.DeviceArray.from_host(np.full((B, rd), 3.0, np.float32)) if ws else None
+    say("se", C, rd, P, inplace, ws)
     H.check(H.lib().bnh_se_f32(dc.ptr, c_ws, C, rd, P, dt[0].ptr, dt[1].ptr, dt[2].ptr, dt[3].ptr, dg.ptr, g_ws,
-                               dD.ptr if inplace else None, d_ws, B, None), "se")
+                               dwk.ptr if ws else None, dD.ptr if inplace else None, d_ws, B, None), "se")
     H.sync()
     g = dg.numpy()[:, :C]
     for i in range(B):
@@ -180,15 +184,17 @@ def test_mean_and_pad(hip):
     H.sync()
     for i in range(B):
         assert same_bits(do.numpy()[i, :C], O.mean_f32(x[i], C))
-    for esz, dt in ((4, np.float32), (2, np.float16)):
+    # 16-byte vectors (strides that allow them) and single elements (odd window strides)
+    for esz, dt, slack, pslack in ((4, np.float32, 3, 6), (2, np.float16, 3, 6), (4, np.float32, 8, 4),
+                                   (2, np.float16, 16, 8)):
         Hh, W, C, ld, h = 9, 7, 24, 32, 2
         x = rng.standard_normal((B, Hh * W, ld)).astype(dt)
-        xs, x_ws = strided(x, 3)
+        xs, x_ws = strided(x, slack)
         dx = H.DeviceArray.from_host(xs)
         per = (Hh + 2 * h) * (W + 2 * h) * C
-        dp = H.DeviceArray.from_host(np.full((B, per + 6), 9, dt))
-        say("pad", esz)
-        H.check(H.lib().bnh_pad(dx.ptr, x_ws, Hh, W, C, ld, h, esz, dp.ptr, per + 6, B, None), "pad")
+        dp = H.DeviceArray.from_host(np.full((B, per + pslack), 9, dt))
+        say("pad", esz, slack)
+        H.check(H.lib().bnh_pad(dx.ptr, x_ws, Hh, W, C, ld, h, esz, dp.ptr, per + pslack, B, None), "pad")
         H.sync()
         got = dp.numpy()[:, :per]
         for i in range(B):
@@ -250,9 +256,11 @@ def test_se_f16(hip, C, rd, P, ws):
     dD = H.DeviceArray.from_host(Ds)
     g_ws = C + 4
     dg = H.DeviceArray.from_host(np.zeros((B, g_ws), np.float32)) if ws else None
+    dwk = H.DeviceArray.from_host(np.zeros((B, rd), np.float32)) if ws else None
     say("se f16", C, rd, P, ws)
     H.check(H.lib().bnh_se_f16(dc.ptr, c_ws, C, rd, P, dt[0].ptr, dt[1].ptr, dt[2].ptr, dt[3].ptr,
-                               dg.ptr if ws else None, g_ws, dD.ptr, d_ws, B, None), "se_f16")
+                               dg.ptr if ws else None, g_ws, dwk.ptr if ws else None, dD.ptr, d_ws, B, None),
+            "se_f16")
     H.sync()
     got = dD.numpy()
     for i in range(B):
