@@ -319,15 +319,31 @@ __global__ __launch_bounds__(256) void k_chsum(const T *__restrict__ out, long l
   const int c0 = blockIdx.x * 64, S = C - c0 < 64 ? C - c0 : 64, S4 = S / 4, win = blockIdx.y;
   const int Tn = cs_terms<FORM>(Wo), per = R * Tn * S, nch = (Ho + R - 1) / R;
   const T *o = out + win * o_ws + c0;
+  // a chunk's terms: each thread takes items t0, t0 + nt, ...; CB items' loads are issued before any of their LDS
+  // stores, so that a thread keeps CB loads (4 CB for the 4-pixel terms) in flight
+  constexpr int CB = FORM == 2 ? 16 : 4;
   auto load = [&](int ch, int t0, int nt) {
     const int rows = Ho - ch * R < R ? Ho - ch * R : R;
     float *buf = tb + (ch & 1) * per;
     const int n = rows * Tn * S4;
-#pragma unroll 4
-    for (int it = t0; it < n; it += nt) {
-      const int c4 = it % S4, j = (it / S4) % Tn, r = it / (S4 * Tn);
-      const f4 v = cs_term<FORM>(o + (long long)(ch * R + r) * Wo * C + 4 * c4, C, Wo, j);
-      *(float4 *)(buf + (r * Tn + j) * S + 4 * c4) = make_float4(v.v[0], v.v[1], v.v[2], v.v[3]);
+    for (int base = t0; base < n; base += CB * nt) {
+      f4 v[CB];
+#pragma unroll
+      for (int u = 0; u < CB; u++) {
+        const int it = base + u * nt;
+        if (it < n) {
+          const int c4 = it % S4, j = (it / S4) % Tn, r = it / (S4 * Tn);
+          v[u] = cs_term<FORM>(o + (long long)(ch * R + r) * Wo * C + 4 * c4, C, Wo, j);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < CB; u++) {
+        const int it = base + u * nt;
+        if (it < n) {
+          const int c4 = it % S4, j = (it / S4) % Tn, r = it / (S4 * Tn);
+          *(float4 *)(buf + (r * Tn + j) * S + 4 * c4) = make_float4(v[u].v[0], v[u].v[1], v[u].v[2], v[u].v[3]);
+        }
+      }
     }
   };
   load(0, tid, 256);
@@ -355,9 +371,9 @@ __global__ __launch_bounds__(256) void k_chsum(const T *__restrict__ out, long l
   if (wave == 0 && lane < S) chsum[win * cs_ws + c0 + lane] = cs;
 }
 
-// rows per chunk: two buffers of at most 8 K floats (64 KB of LDS)
-static int chsum_rows(int Tn, int S, int Ho) {
-  int R = 8192 / (Tn * S);
+// rows per chunk: two buffers of at most `cap` floats
+static int chsum_rows(int Tn, int S, int Ho, int cap) {
+  int R = cap / (Tn * S);
   if (R < 1) R = 1;
   return R < Ho ? R : Ho;
 }
@@ -424,8 +440,14 @@ static int chsum_launch(const T *out, long long o_ws, int C, int Ho, int Wo, flo
     BNH_HIP(hipGetLastError());
     return 0;
   }
-  const int R = chsum_rows(Tn, S, Ho);
+  // a block's chunk is one memory round trip of its loading waves: with at most one block per CU (no more blocks
+  // than 2 per CU in the launch) the chunks take up to 144 KB of LDS, else 64 KB so that several blocks share a CU
+  const long long nblk = bnh_ceil_div(C, 64) * (long long)B;
+  const int cap = nblk <= 512 ? 18432 : 8192;
+  const int R = chsum_rows(Tn, S, Ho, cap);
   const size_t lds = 2 * sizeof(float) * (size_t)R * Tn * S;
+  if (lds > 64 * 1024)
+    BNH_HIP(hipFuncSetAttribute((const void *)k_chsum<T, FORM>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   hipLaunchKernelGGL((k_chsum<T, FORM>), dim3((unsigned)bnh_ceil_div(C, 64), (unsigned)B), dim3(256), lds, st, out,
                      o_ws, C, Ho, Wo, R, chsum, cs_ws);
   BNH_HIP(hipGetLastError());
