@@ -431,7 +431,7 @@ def cpu_baseline_perch(pn, rng):
     import oracle_net
     from bnneon import perchnet
     T = cpu_threads()
-    n_win = T
+    n_win = 8 * T   # about 10 s of the host's cores
     on = oracle_net.OracleNet(pn.net, 0, pn.net.last, pn.emb_buf)
     pcms = [perchnet.signal(rng) for _ in range(n_win)]
     t0 = time.perf_counter()
@@ -494,7 +494,7 @@ def run_perch(a, H, rng, B, stream):
 
 # HBM bytes per launch of that GEMM (24 -> 144 channels, 15,687 px, 256 windows): FETCH_SIZE x 2 + WRITE_SIZE from
 # rocprofv3 --pmc runs of this bench (profiles/k_s8n_gemm_pw_s8_24to144_249x63_b256.md)
-PERCH_GEMM_TRAFFIC = 2648826307
+PERCH_GEMM_TRAFFIC = 2591011232
 
 
 def perch_roofline(H, pn, B, stream, a):
@@ -548,7 +548,7 @@ def cpu_baseline_v24(vn, rng):
     import oracle_net
     from bnneon import v24net
     T = cpu_threads()
-    n_win = T
+    n_win = 2 * T   # about 20 s of the host's cores
     on = oracle_net.OracleNet(vn.net, 0, vn.net.last, vn.emb_buf)
     pcms = [v24net.signal(rng) for _ in range(n_win)]
     t0 = time.perf_counter()
@@ -608,6 +608,9 @@ def run_v24(a, H, rng, B, stream):
 
 
 FP16_MFMA_PEAK_TFLOPS = 2500.0
+# HBM bytes per launch of the replayed fp16 GEMM (72 -> 864 channels, 384 px, 256 windows): FETCH_SIZE x 2 +
+# WRITE_SIZE from rocprofv3 --pmc runs of this bench (profiles/k_gemm_f16e_pw_f16_72to864_24x16_b256.md)
+V24_GEMM_TRAFFIC = 185384640
 FP16_VALU_PEAK_TFLOPS = 157.3
 
 
@@ -639,7 +642,7 @@ def v24_roofline(H, vn, B, stream, a):
     H.lib().bnh_h16w_free(hw)
     tf = 2.0 * M * N * K * B / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "achieved": round(tf, 2), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+            "frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": V24_GEMM_TRAFFIC,
             "kernel": "k_gemm_f16e", "valu_peak": FP16_VALU_PEAK_TFLOPS,
             "valu_frac": round(tf / FP16_VALU_PEAK_TFLOPS, 4),
             "launch": f"PW f16 GEMM {K}->{N} over {M} px x {B} windows, act {act}, halo-{opad} output",

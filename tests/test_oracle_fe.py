@@ -180,3 +180,84 @@ def test_mean_and_pad():
     p = O.pad(x, 6, 5, 12, 2).reshape(10, 9, 12)
     assert np.array_equal(p[2:8, 2:7], x[:, :12].reshape(6, 5, 12))
     assert not p[:2].any() and not p[-2:].any() and not p[:, :2].any() and not p[:, -2:].any()
+
+
+# ---------------------------------------------------------------- the fp16 path's ops (oracle/fe.c)
+def test_stem_f32to16_is_the_fp32_stem_rounded():
+    rng = np.random.default_rng(7)
+    H, W, k, s, co = 13, 12, 3, 2, 20
+    img = (rng.standard_normal((H, W)) * 4).astype(np.float32)
+    img[0, 0] = 1e6   # past the fp16 range: +inf after the rounding
+    w = rng.standard_normal((co, k * k)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32)
+    panels, bb, (N, K, Kp, Np) = O.fpack(w, b)
+    ref32 = O.stem_f32(img, k, s, panels, bb, Kp, Np, act=1, opad=0)
+    got = O.stem_f32to16(img, k, s, panels, bb, Kp, co, Np, act=1, opad=1, ldo=Np, fill=3.0)
+    Ho, Wo = (H - k) // s + 1, (W - k) // s + 1
+    got = got.reshape(Ho + 2, Wo + 2, Np)
+    inner = got[1:-1, 1:-1].reshape(-1, Np)
+    want = ref32[:, :co].astype(np.float16)   # numpy's float32 -> float16 is round to nearest even
+    assert np.array_equal(inner[:, :co].view(np.uint16), want.view(np.uint16))
+    assert (inner[:, co:] == 3.0).all()        # channels past N untouched
+    assert np.isinf(inner).any()
+    assert not got[0].any() and not got[-1].any() and not got[:, 0].any() and not got[:, -1].any()
+
+
+def test_se_f16_gate_and_product():
+    rng = np.random.default_rng(8)
+    P_, Cc, rd = 40, 48, 6
+    D = rng.standard_normal((P_, Cc)).astype(np.float16)
+    chsum = (rng.standard_normal(Cc) * 10).astype(np.float32)
+    w1 = (rng.standard_normal((rd, Cc)) * 0.2).astype(np.float32)
+    b1 = rng.standard_normal(rd).astype(np.float32)
+    w2t = (rng.standard_normal((rd, Cc)) * 0.3).astype(np.float32)
+    b2 = rng.standard_normal(Cc).astype(np.float32)
+    got = O.se_f16(D, chsum, w1, b1, w2t, b2)
+    g16 = O.se_f16(np.ones((P_, Cc), np.float16), chsum, w1, b1, w2t, b2)[0]   # 1 x g is g itself
+    # the gate: the float64 formula, then one rounding to fp16 (the fp32 steps differ by ~1e-6 relative)
+    m = chsum.astype(np.float64) / P_
+    h = w1.astype(np.float64) @ m + b1
+    ex = 1 / (1 + np.exp(-(w2t.T.astype(np.float64) @ (h / (1 + np.exp(-h))) + b2)))
+    assert np.abs(g16.astype(np.float64) - ex).max() <= 2.0 ** -11 * ex.max() + 1e-6
+    # the product: one fp16 multiply per element (numpy's float16 multiply rounds the exact product once)
+    assert np.array_equal(got.view(np.uint16), (D * g16[None, :]).view(np.uint16))
+
+
+def test_mean_f16_is_the_sequential_fp32_sum():
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((300, 24)) * 100).astype(np.float16)
+    m = O.mean_f16(x, 20)
+    seq = np.add.accumulate(x[:, :20].astype(np.float32), axis=0, dtype=np.float32)[-1]
+    assert np.array_equal(m, (seq / np.float32(300)).astype(np.float32))
+    # the order shows: 60000, then 1e-4 terms each lost against it (ulp 2^-8 there), then -60000: the sequential
+    # fp32 sum is 0 where the exact sum is 100 x 1e-4
+    col = np.concatenate([[60000.0], np.full(100, 1e-4), [-60000.0]]).astype(np.float16)[:, None]
+    assert O.mean_f16(col, 1)[0] == 0.0
+
+
+def test_gemv_lane_order_and_exactness():
+    rng = np.random.default_rng(10)
+    # integer data: every fp32 operation exact, both weight forms, K with 8-lane, 4-lane and scalar parts
+    for K in (16, 20, 23, 3):
+        w = rng.integers(-4, 5, (7, K)).astype(np.float32)
+        x = rng.integers(-9, 10, K).astype(np.float32)
+        b = rng.integers(-5, 6, 7).astype(np.float32)
+        want = w.astype(np.float64) @ x + b
+        assert np.array_equal(O.gemv(w, b, x), want.astype(np.float32))
+        assert np.array_equal(O.gemv(w.astype(np.float16), b, x), want.astype(np.float32))
+        assert np.array_equal(O.gemv(w, b, x, act=2), np.maximum(want, 0).astype(np.float32))
+    # the lane pairing ((l0 + l4) + (l1 + l5)) + ((l2 + l6) + (l3 + l7)): with 2^25 in lane 0 and 1 in lane 4 the 1
+    # is lost (ulp 4 at 2^25) before lane 2's -2^25 cancels it; a sequential sum would keep both ones
+    x = np.array([2.0 ** 25, 0, -2.0 ** 25, 0, 1, 0, 1, 0], np.float32)
+    w = np.ones((1, 8), np.float32)
+    assert O.gemv(w, np.zeros(1, np.float32), x)[0] == 0.0
+    # the K % 4 tail: product and sum rounded apart (no fused multiply-add). The tail product is
+    # 2^-24 (1 + 2^-36), which rounds to 2^-24; 1 + 2^-24 is then a tie that rounds to even, 1.0 (one fused
+    # operation would see a value above the tie and give 1 + 2^-23)
+    x = np.zeros(9, np.float32)
+    w = np.zeros((1, 9), np.float32)
+    x[0], w[0, 0] = 1.0, 1.0
+    w[0, 8] = np.float32(1 + 2.0 ** -12)
+    x[8] = np.float32(2.0 ** -24 * (1 - 2.0 ** -12 + 2.0 ** -24))
+    assert float(w[0, 8]) * float(x[8]) == 2.0 ** -24 * (1 + 2.0 ** -36)
+    assert O.gemv(w, np.zeros(1, np.float32), x)[0] == np.float32(1.0)
