@@ -43,7 +43,9 @@ __global__ void k_zero_halo(T *__restrict__ out, long long ws, int H, int W, int
 // ------------------------------------------------------------------ STEM
 // thread per (window, output pixel, 4 channels); w panels [Np/8][Kp][8]. H16: the fp16-path form, channels < N
 // rounded to fp16 (pc_cvt_pad_f16, src/pc_kern_f16.c:104-113) and stored as fp16
-template <bool H16>
+// KK: the kernel size when it is 3 or 5 (the taps unrolled), 0 for any k. A thread owns 4 output channels of one
+// pixel; windows on grid.y; 32-bit index arithmetic; 16-byte stores when the output rows allow them (VEC).
+template <int KK, bool H16, bool VEC>
 __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img, long long i_ws, int W, int k, int s,
                                                   int Ho, int Wo, const float *__restrict__ w,
                                                   const float *__restrict__ bias, int Kp, int Np, int act,
@@ -52,20 +54,29 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
   bnh_silu_table(tbl);
   __syncthreads();
   const int ng = Np / 4;
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x, per = (long long)Ho * Wo * ng;
-  const int win = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x, per = Ho * Wo * ng;
+  const long long win = blockIdx.y;
   if (i >= per) return;
-  const int g = (int)(i % ng), m = (int)(i / ng), oy = m / Wo, ox = m % Wo, n0 = 4 * g;
-  const float *x = img + win * i_ws + (long long)(oy * s) * W + ox * s;
-  const float *wp = w + (long long)(n0 / 8) * Kp * 8 + n0 % 8;
+  const int m = i / ng, g = i - m * ng, oy = m / Wo, ox = m - oy * Wo, n0 = 4 * g;
+  const float *x = img + win * i_ws + (oy * s) * W + ox * s;
+  const float *wp = w + (n0 / 8) * Kp * 8 + n0 % 8;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int q = 0; q < Kp; q++) {
-    const float a = q < k * k ? x[(q / k) * W + q % k] : 0.f;
-    const float4 wv = *(const float4 *)(wp + (long long)q * 8);
+  auto tap = [&](int q, float a) {
+    const float4 wv = *(const float4 *)(wp + q * 8);
     acc[0] = __builtin_fmaf(wv.x, a, acc[0]);
     acc[1] = __builtin_fmaf(wv.y, a, acc[1]);
     acc[2] = __builtin_fmaf(wv.z, a, acc[2]);
     acc[3] = __builtin_fmaf(wv.w, a, acc[3]);
+  };
+  if constexpr (KK > 0) {
+    constexpr int KP = (KK * KK + 3) / 4 * 4;
+    float a[KP];
+#pragma unroll
+    for (int q = 0; q < KP; q++) a[q] = q < KK * KK ? x[(q / KK) * W + q % KK] : 0.f;
+#pragma unroll
+    for (int q = 0; q < KP; q++) tap(q, a[q]);
+  } else {
+    for (int q = 0; q < Kp; q++) tap(q, q < k * k ? x[(q / k) * W + q % k] : 0.f);
   }
   float y[4];
 #pragma unroll
@@ -77,13 +88,36 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
   const long long orow = opad ? (long long)(oy + opad) * (Wo + 2 * opad) + ox + opad : m;
   if (H16) {
     uint16_t *o = (uint16_t *)outv + win * o_ws + orow * ldo + n0;
+    if (VEC && n0 + 4 <= N) {
+      *(uint2 *)o = make_uint2((uint32_t)hbits(f2h(y[0])) | ((uint32_t)hbits(f2h(y[1])) << 16),
+                               (uint32_t)hbits(f2h(y[2])) | ((uint32_t)hbits(f2h(y[3])) << 16));
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-      if (n0 + j < N) o[j] = hbits(f2h(y[j]));  // one rounding to nearest even (no fused mix forms)
+      for (int j = 0; j < 4; j++)
+        if (n0 + j < N) o[j] = hbits(f2h(y[j]));  // one rounding to nearest even (no fused mix forms)
+    }
   } else {
     float *o = (float *)outv + win * o_ws + orow * ldo + n0;
-    o[0] = y[0]; o[1] = y[1]; o[2] = y[2]; o[3] = y[3];
+    if (VEC) {
+      *(float4 *)o = make_float4(y[0], y[1], y[2], y[3]);
+    } else {
+      o[0] = y[0]; o[1] = y[1]; o[2] = y[2]; o[3] = y[3];
+    }
   }
+}
+
+// the stem launch for kernel size k: the unrolled forms for 3 and 5
+template <bool H16>
+static void stem_launch(dim3 grid, hipStream_t st, bool vec, const float *img, long long i_ws, int W, int k, int s,
+                        int Ho, int Wo, const float *w, const float *bias, int Kp, int Np, int act, void *out,
+                        long long o_ws, int ldo, int opad, int N) {
+#define STEM_L(KK, V)                                                                                                  \
+  hipLaunchKernelGGL((k_stem_f32<KK, H16, V>), grid, dim3(256), 0, st, img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np,   \
+                     act, out, o_ws, ldo, opad, N)
+  if (k == 3 && Kp == 12) { if (vec) STEM_L(3, true); else STEM_L(3, false); }
+  else if (k == 5 && Kp == 28) { if (vec) STEM_L(5, true); else STEM_L(5, false); }
+  else { if (vec) STEM_L(0, true); else STEM_L(0, false); }
+#undef STEM_L
 }
 
 // ------------------------------------------------------------------ SE_GATE / SE
@@ -515,9 +549,10 @@ int bnh_stem_f32_body(const float *img, long long i_ws, int H, int W, int k, int
   BNH_REQ(((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 3) == 0);
   BNH_REQ(B == 1 || (i_ws >= (long long)H * W && o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo));
   const long long per = (long long)Ho * Wo * (Np / 4);
-  hipLaunchKernelGGL(k_stem_f32<false>, dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), dim3(256), 0,
-                     bnh_stream(stream), img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, act, (void *)out, o_ws, ldo, opad,
-                     Np);
+  BNH_REQ(per < (1LL << 31) && (long long)H * W < (1LL << 31));
+  const bool vec = ((uintptr_t)out & 15) == 0 && (B == 1 || o_ws % 4 == 0);  // ldo % 4 == 0 already
+  stem_launch<false>(dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), bnh_stream(stream), vec, img, i_ws, W, k, s,
+                     Ho, Wo, w, bias, Kp, Np, act, (void *)out, o_ws, ldo, opad, Np);
   BNH_HIP(hipGetLastError());
   return 0;
 }
@@ -531,9 +566,10 @@ int bnh_stem_f32to16_body(const float *img, long long i_ws, int H, int W, int k,
   BNH_REQ(((uintptr_t)w & 15) == 0);
   BNH_REQ(B == 1 || (i_ws >= (long long)H * W && o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo));
   const long long per = (long long)Ho * Wo * (Np / 4);
-  hipLaunchKernelGGL(k_stem_f32<true>, dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), dim3(256), 0,
-                     bnh_stream(stream), img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, act, (void *)out, o_ws, ldo, opad,
-                     N);
+  BNH_REQ(per < (1LL << 31) && (long long)H * W < (1LL << 31));
+  const bool vec = ((uintptr_t)out & 7) == 0 && ldo % 4 == 0 && (B == 1 || o_ws % 4 == 0);
+  stem_launch<true>(dim3((unsigned)bnh_ceil_div(per, 256), (unsigned)B), bnh_stream(stream), vec, img, i_ws, W, k, s,
+                    Ho, Wo, w, bias, Kp, Np, act, (void *)out, o_ws, ldo, opad, N);
   BNH_HIP(hipGetLastError());
   return 0;
 }
