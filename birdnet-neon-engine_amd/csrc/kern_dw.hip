@@ -46,12 +46,13 @@ static int items_per_row(int Wo, int form) {
 }
 
 // ------------------------------------------------------------------ the grid
-// A thread owns DW_NI consecutive items of one output row and one channel (weights loaded once, input columns shared
+// A thread owns dw_ni(k) consecutive items of one output row and one channel (weights loaded once, input columns shared
 // between neighbouring items reused from registers). Threads are numbered (window, row, strip, channel) across the
 // whole grid, and blocks are taken in that order after the XCD remap, so one XCD walks consecutive rows of a window
 // and finds the input rows they share in its L2.
-#define DW_NI 4
-struct DwGrid { int ns; double rC, rnc, rHo; };  // strips per row; 1 / C, 1 / (ns C), 1 / Ho
+// items per thread: 1 for 3 x 3 kernels (more threads in flight beat the reuse of weights), 4 for larger ones
+__host__ __device__ constexpr int dw_ni(int k) { return k <= 3 ? 1 : 4; }
+struct DwGrid { int ns, ni; double rC, rnc, rHo; };  // strips per row, items per strip; 1 / C, 1 / (ns C), 1 / Ho
 struct DwPos { int c, it0, oy, win; bool ok; };
 BNH_DEV DwPos dw_pos(int C, int Ho, long long total, DwGrid g) {
   const unsigned lb = bnh_xcd_block(blockIdx.x, gridDim.x);
@@ -63,13 +64,14 @@ BNH_DEV DwPos dw_pos(int C, int Ho, long long total, DwGrid g) {
   const int rowid = bnh_div(ii, nc, g.rnc), rem = (int)(ii - (long long)rowid * nc);
   const int strip = bnh_div(rem, C, g.rC);
   p.c = rem - strip * C;
-  p.it0 = strip * DW_NI;
+  p.it0 = strip * g.ni;
   p.win = bnh_div(rowid, Ho, g.rHo);
   p.oy = rowid - p.win * Ho;
   return p;
 }
-static int dw_grid(int nitems, int C, int Ho, int B, unsigned *blocks, long long *total, DwGrid *g) {
-  g->ns = (nitems + DW_NI - 1) / DW_NI;
+static int dw_grid(int nitems, int ni, int C, int Ho, int B, unsigned *blocks, long long *total, DwGrid *g) {
+  g->ni = ni;
+  g->ns = (nitems + ni - 1) / ni;
   g->rC = 1.0 / C;
   g->rnc = 1.0 / ((double)g->ns * C);
   g->rHo = 1.0 / Ho;
@@ -103,7 +105,7 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
   float *ow = out + win * o_ws + (long long)oy * Wo * C + c;
   const long long rs = (long long)Wp * C;
 #pragma unroll
-  for (int j = 0; j < DW_NI; j++) {
+  for (int j = 0; j < dw_ni(K); j++) {
     const int it = ps.it0 + j;
     if (it >= nitems) break;
     const Item item = item_of(it, Wo, FORM);
@@ -184,7 +186,7 @@ __global__ __launch_bounds__(256) void k_dw_f16(const h16 *__restrict__ xp, long
   const h16 *xw = xp + win * x_ws + (long long)iy0 * Wp * C + c;
   h16 *ow = out + win * o_ws + (long long)oy * Wo * C + c;
 #pragma unroll
-  for (int j = 0; j < DW_NI; j++) {
+  for (int j = 0; j < dw_ni(K); j++) {
     const int it = ps.it0 + j;
     if (it >= nitems) break;
     const Item item = item_of(it, Wo, FORM);
@@ -540,7 +542,7 @@ int bnh_dwk_f32(const float *xp, long long x_ws, int H, int W, int C, int k, int
   unsigned nb;
   long long total;
   DwGrid g;
-  if (dw_grid(nit, C, Ho, B, &nb, &total, &g)) return -1;
+  if (dw_grid(nit, dw_ni(k), C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   const int Wp = W + k - 1;
   dispatch_ks<float>(k, s, [&]<int K, int S>() {
@@ -563,7 +565,7 @@ int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, con
   unsigned nb;
   long long total;
   DwGrid g;
-  if (dw_grid(nit, C, Ho, B, &nb, &total, &g)) return -1;
+  if (dw_grid(nit, dw_ni(3), C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   if (s == 1)
     hipLaunchKernelGGL((k_dw_f32<3, 1, 2>), dim3(nb), dim3(256), 0, st, xp, x_ws, W + 2, C, 1, 1, w, b, 1, out, o_ws,
@@ -588,7 +590,7 @@ int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, 
   unsigned nb;
   long long total;
   DwGrid g;
-  if (dw_grid(nit, C, Ho, B, &nb, &total, &g)) return -1;
+  if (dw_grid(nit, dw_ni(k), C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   const int Wp = W + k - 1;
   dispatch_ks<h16>(k, s, [&]<int K, int S>() {
@@ -612,7 +614,7 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
   unsigned nb;
   long long total;
   DwGrid g;
-  if (dw_grid(nit, C, Ho, B, &nb, &total, &g)) return -1;
+  if (dw_grid(nit, dw_ni(3), C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   if (s == 1)
     hipLaunchKernelGGL((k_dw_f16<3, 1, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,
