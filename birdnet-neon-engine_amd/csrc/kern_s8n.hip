@@ -239,6 +239,7 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
 // to its L2, where their cache lines complete before they are written back (rows split between blocks leave partial
 // lines, which cost HBM write rate). Blocks split the channel groups only when there are too few rows to fill the
 // chip (gsplit blocks per row block, consecutive after the XCD remap so that they share an L2).
+template <bool RES>
 __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, long long q_ws,
                                                   const float *__restrict__ sa, long long sa_ws,
                                                   const int32_t *__restrict__ za, long long za_ws, int M, double rM,
@@ -337,7 +338,22 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
       csn[j] = cs[n];
     }
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+    for (int t = 0; t < 2; t++) {
+      // RES: the residuals of the tile's 16 rows first: loads issued together, and before any store (which the compiler
+      // may not move them past: out and res could alias), so their latency is paid once per tile, not per row
+      float rv[4][4];
+      if (RES) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int lr = lr0 + 16 * t + 4 * (lane >> 4) + r;
+          const float *rrow = e.res + s_r[lr];
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const int n = n0 + 16 * j + (lane & 15);
+            rv[r][j] = j < jn && n < Np && rowB + lr < rows ? rrow[n] : 0.f;
+          }
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int lr = lr0 + 16 * t + 4 * (lane >> 4) + r;
@@ -345,7 +361,6 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
         const float s_a = s_sa[lr];
         const uint32_t z = s_z[lr];
         float *orow = e.out + s_o[lr];
-        const float *rrow = e.res ? e.res + s_r[lr] : nullptr;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           if (j >= jn) break;
@@ -358,10 +373,11 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
           y = y + bn[j];
           if (e.act == 1) y = bnh_silu_f32_t(y, s_tbl);
           else if (e.act == 2) y = bnh_relu_f32(y);
-          if (rrow) y = y + rrow[n];
+          if (RES) y = y + rv[r][j];
           orow[n] = y;
         }
       }
+    }
   }
 }
 
@@ -806,8 +822,12 @@ int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, long long sa_
   if (nrb < 1024) gsplit = (int)bnh_ceil_div(1024, nrb);
   if (gsplit > ng) gsplit = ng;
   BNH_REQ(nrb * gsplit < (1LL << 31));
-  hipLaunchKernelGGL(k_s8n_gemm, dim3((unsigned)(nrb * gsplit)), dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws, M, rM,
-                     rows, W->w, W->sw, W->colsum, W->b, W->Kp, W->Np, gsplit, d);
+  if (e->res)
+    hipLaunchKernelGGL(k_s8n_gemm<true>, dim3((unsigned)(nrb * gsplit)), dim3(256), 0, s, q, q_ws, sa, sa_ws, za, za_ws,
+                       M, rM, rows, W->w, W->sw, W->colsum, W->b, W->Kp, W->Np, gsplit, d);
+  else
+    hipLaunchKernelGGL(k_s8n_gemm<false>, dim3((unsigned)(nrb * gsplit)), dim3(256), 0, s, q, q_ws, sa, sa_ws, za,
+                       za_ws, M, rM, rows, W->w, W->sw, W->colsum, W->b, W->Kp, W->Np, gsplit, d);
   BNH_HIP(hipGetLastError());
   return 0;
 }
