@@ -54,4 +54,30 @@ BNH_DEV h16 silu_lut_h_t(h16 x, const uint16_t *c0t, const uint16_t *c1t, const 
 }
 BNH_DEV h16 silu_lut_h(h16 x) { return silu_lut_h_t(x, k_silu_c0, k_silu_c1, k_silu_c2); }
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// silu_lut_h on both halves of a packed pair, with the same roundings lane by lane: u = |x|; min(u, 15.4) (u is
+// never NaN-sensitive here: a NaN x gives a NaN result through -u either way); the segment n in [0, 15] from the
+// low byte of u + 1536; max(x, 0) as the sign-cleared x (FMAX(x, +0) for every non-NaN x, -0 included).
+// t01[n] = c0 | c1 << 16, t2[n] = c2.
+BNH_DEV h2 silu2_lut(h2 x, const uint32_t *t01, const uint16_t *t2) {
+  const uint32_t xb = __builtin_bit_cast(uint32_t, x);
+  const h2 u = __builtin_bit_cast(h2, xb & 0x7fff7fffu);
+  const h2 uc = __builtin_elementwise_min(u, (h2){hfrom(0x4bb3), hfrom(0x4bb3)});
+  const h2 magic = (h2){(h16)1536.0f, (h16)1536.0f};
+  const h2 tm = uc + magic;
+  const h2 f = uc - (tm - magic);
+  const uint32_t tb = __builtin_bit_cast(uint32_t, tm);
+  const uint32_t na = tb & 15u, nb = (tb >> 16) & 15u;
+  const uint32_t ea = t01[na], eb = t01[nb];
+  const h2 c0 = __builtin_bit_cast(h2, (ea & 0xffffu) | (eb << 16));
+  const h2 c1 = __builtin_bit_cast(h2, (ea >> 16) | (eb & 0xffff0000u));
+  const h2 c2 = __builtin_bit_cast(h2, (uint32_t)t2[na] | ((uint32_t)t2[nb] << 16));
+  h2 p = __builtin_elementwise_fma(c2, f, c1);
+  p = __builtin_elementwise_fma(p, f, c0);
+  const uint32_t neg = ((xb >> 15) & 0x00010001u) * 0xffffu;  // all-ones halves where x is negative (or -0)
+  const h2 m = __builtin_bit_cast(h2, xb & ~neg);
+  return __builtin_elementwise_fma(-u, p, m);
+}
+
 #endif

@@ -233,6 +233,79 @@ __global__ __launch_bounds__(256) void k_dw_f16(const h16 *__restrict__ xp, long
   }
 }
 
+// The same on channel pairs (C even): a thread owns two adjacent channels and runs their two chains in the lanes of
+// packed fp16 instructions (each lane one IEEE fp16 operation, the same roundings as k_dw_f16), 4-byte loads and
+// stores, the LUT SiLU on both halves with its table in LDS.
+template <int K, int S, int FORM>
+__global__ __launch_bounds__(256) void k_dw_f16p(const h16 *__restrict__ xp, long long x_ws, int Wp, int C, int pt,
+                                                 int pl, const h16 *__restrict__ w, const h16 *__restrict__ b, int act,
+                                                 h16 *__restrict__ out, long long o_ws, int Ho, int Wo, int nitems,
+                                                 long long total, DwGrid g) {
+  __shared__ uint32_t s_t01[16];
+  __shared__ uint16_t s_t2[16];
+  if (threadIdx.x < 16) {
+    s_t01[threadIdx.x] = (uint32_t)k_silu_c0[threadIdx.x] | ((uint32_t)k_silu_c1[threadIdx.x] << 16);
+    s_t2[threadIdx.x] = k_silu_c2[threadIdx.x];
+  }
+  __syncthreads();
+  const DwPos ps = dw_pos(C / 2, Ho, total, g);
+  if (!ps.ok) return;
+  const int c = 2 * ps.c, oy = ps.oy, win = ps.win;
+  constexpr int H = (K - 1) / 2;
+  const int iy0 = FORM == 2 ? oy * S - pt + 1 : oy * S - pt + H;
+  auto ld2 = [](const h16 *p) { return __builtin_bit_cast(h2, *(const uint32_t *)p); };
+  h2 wv[K * K];
+#pragma unroll
+  for (int t = 0; t < K * K; t++) wv[t] = ld2(w + (long long)t * C + c);
+  const h2 bias = ld2(b + c);
+  const h16 *xw = xp + win * x_ws + (long long)iy0 * Wp * C + c;
+  h16 *ow = out + win * o_ws + (long long)oy * Wo * C + c;
+#pragma unroll
+  for (int j = 0; j < dw_ni(K); j++) {
+    const int it = ps.it0 + j;
+    if (it >= nitems) break;
+    const Item item = item_of(it, Wo, FORM);
+    const int ix0 = FORM == 2 ? item.px * S - pl + 1 : item.px * S - pl + H;
+    const h16 *x0 = xw + (long long)ix0 * C;
+    h2 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      if (q >= item.n) break;
+      if (FORM == 2) {
+        const h16 *r0 = x0 + (long long)q * S * C, *r1 = r0 + (long long)Wp * C, *r2 = r1 + (long long)Wp * C;
+        h2 a = __builtin_elementwise_fma(ld2(r0), wv[0], bias);
+        h2 a2 = ld2(r0 + C) * wv[1];
+        a = __builtin_elementwise_fma(ld2(r0 + 2 * C), wv[2], a);
+        a2 = __builtin_elementwise_fma(ld2(r1), wv[3], a2);
+        a = __builtin_elementwise_fma(ld2(r1 + C), wv[4], a);
+        a2 = __builtin_elementwise_fma(ld2(r1 + 2 * C), wv[5], a2);
+        a = __builtin_elementwise_fma(ld2(r2), wv[6], a);
+        a2 = __builtin_elementwise_fma(ld2(r2 + C), wv[7], a2);
+        a = __builtin_elementwise_fma(ld2(r2 + 2 * C), wv[8], a);
+        v[q] = silu2_lut(a + a2, s_t01, s_t2);
+      } else {
+        h2 a = bias, e = (h2){(h16)0.0f, (h16)0.0f};
+#pragma unroll
+        for (int ky = 0; ky < K; ky++)
+#pragma unroll
+          for (int kx = 0; kx < K; kx++) {
+            const int t = ky * K + kx;
+            const h2 xv = ld2(x0 + ((long long)ky * Wp + q * S + kx) * C);
+            if (item.split && (t & 1)) e = __builtin_elementwise_fma(xv, wv[t], e);
+            else a = __builtin_elementwise_fma(xv, wv[t], a);
+          }
+        h2 y = item.split ? a + e : a;
+        if (act == 1) y = silu2_lut(y, s_t01, s_t2);
+        v[q] = y;
+      }
+    }
+    h16 *o = ow + (long long)item.px * C;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      if (q < item.n) *(uint32_t *)(o + (long long)q * C) = __builtin_bit_cast(uint32_t, v[q]);
+  }
+}
+
 // ------------------------------------------------------------------ channel sums (pass 2)
 // The reference adds the outputs of each channel into one fp32 sum, row after row, in terms that depend on the kernel:
 //   form 0 (fp32 DWK): per row the 4-pixel groups (o0 + o1) + (o2 + o3), then each tail pixel;
@@ -518,6 +591,13 @@ static void dispatch_ks(int k, int s, L &&launch) {
   else launch.template operator()<7, 2>();
 }
 
+// the fp16 kernels run channel pairs when every pair is 4-byte aligned
+static bool dw_pairs(const void *xp, long long x_ws, const void *w, const void *b, const void *out, long long o_ws, int C,
+                     int B) {
+  return C % 2 == 0 && ((uintptr_t)xp & 3) == 0 && ((uintptr_t)w & 3) == 0 && ((uintptr_t)b & 3) == 0 &&
+         ((uintptr_t)out & 3) == 0 && (B == 1 || (x_ws % 2 == 0 && o_ws % 2 == 0));
+}
+
 static int dw_check(int H, int W, int C, int k, int s, int pt, int pl, int Ho, int Wo, int B, long long x_ws,
                     long long o_ws, int halo) {
   BNH_REQ(H > 0 && W > 0 && C > 0 && Ho > 0 && Wo > 0 && B > 0);
@@ -590,12 +670,17 @@ int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, 
   unsigned nb;
   long long total;
   DwGrid g;
-  if (dw_grid(nit, dw_ni(k), C, Ho, B, &nb, &total, &g)) return -1;
+  const bool pair = dw_pairs(xp, x_ws, w, b, out, o_ws, C, B);
+  if (dw_grid(nit, dw_ni(k), pair ? C / 2 : C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   const int Wp = W + k - 1;
   dispatch_ks<h16>(k, s, [&]<int K, int S>() {
-    hipLaunchKernelGGL((k_dw_f16<K, S, 1>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, Wp, C, pt, pl,
-                       (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, Ho, Wo, nit, total, g);
+    if (pair)
+      hipLaunchKernelGGL((k_dw_f16p<K, S, 1>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, Wp, C, pt, pl,
+                         (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, Ho, Wo, nit, total, g);
+    else
+      hipLaunchKernelGGL((k_dw_f16<K, S, 1>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, Wp, C, pt, pl,
+                         (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, Ho, Wo, nit, total, g);
   });
   BNH_HIP(hipGetLastError());
   if (chsum) {
@@ -614,14 +699,15 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
   unsigned nb;
   long long total;
   DwGrid g;
-  if (dw_grid(nit, dw_ni(3), C, Ho, B, &nb, &total, &g)) return -1;
+  const bool pair = dw_pairs(xp, x_ws, w, b, out, o_ws, C, B);
+  if (dw_grid(nit, dw_ni(3), pair ? C / 2 : C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
-  if (s == 1)
-    hipLaunchKernelGGL((k_dw_f16<3, 1, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,
-                       (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total, g);
-  else
-    hipLaunchKernelGGL((k_dw_f16<3, 2, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,
-                       (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total, g);
+#define DW3H(KERN, S_)                                                                                                 \
+  hipLaunchKernelGGL((KERN<3, S_, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,           \
+                     (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total, g)
+  if (pair) { if (s == 1) DW3H(k_dw_f16p, 1); else DW3H(k_dw_f16p, 2); }
+  else { if (s == 1) DW3H(k_dw_f16, 1); else DW3H(k_dw_f16, 2); }
+#undef DW3H
   BNH_HIP(hipGetLastError());
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);

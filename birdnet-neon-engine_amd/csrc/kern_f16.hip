@@ -108,36 +108,11 @@ __global__ __launch_bounds__(256) void k_gemm_f16(const uint16_t *__restrict__ A
 // ([k][channel], a thread's 8 channels one 16-byte read). The next chunk's global loads are issued before the
 // current chunk is computed. Epilogue: the SiLU two channels at a time in packed fp16 with its table in LDS, 16-byte
 // residual loads and stores (VEC).
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 #define FE_KC 32
 #define FE_AS 17   // A row stride in dwords (34 halves)
 #define FE_BM 256  // rows per block at most
 
-// silu_lut_h on both halves of a packed pair, with the same roundings lane by lane: u = |x|; min(u, 15.4) (u is
-// never NaN-sensitive here: a NaN x gives a NaN result through -u either way); the segment n in [0, 15] from the
-// low byte of u + 1536; max(x, 0) as the sign-cleared x (FMAX(x, +0) for every non-NaN x, -0 included).
-// t01[n] = c0 | c1 << 16, t2[n] = c2.
-BNH_DEV h2 silu2_lut(h2 x, const uint32_t *t01, const uint16_t *t2) {
-  const uint32_t xb = __builtin_bit_cast(uint32_t, x);
-  const h2 u = __builtin_bit_cast(h2, xb & 0x7fff7fffu);
-  const h2 uc = __builtin_elementwise_min(u, (h2){hfrom(0x4bb3), hfrom(0x4bb3)});
-  const h2 magic = (h2){(h16)1536.0f, (h16)1536.0f};
-  const h2 tm = uc + magic;
-  const h2 f = uc - (tm - magic);
-  const uint32_t tb = __builtin_bit_cast(uint32_t, tm);
-  const uint32_t na = tb & 15u, nb = (tb >> 16) & 15u;
-  const uint32_t ea = t01[na], eb = t01[nb];
-  const h2 c0 = __builtin_bit_cast(h2, (ea & 0xffffu) | (eb << 16));
-  const h2 c1 = __builtin_bit_cast(h2, (ea >> 16) | (eb & 0xffff0000u));
-  const h2 c2 = __builtin_bit_cast(h2, (uint32_t)t2[na] | ((uint32_t)t2[nb] << 16));
-  h2 p = __builtin_elementwise_fma(c2, f, c1);
-  p = __builtin_elementwise_fma(p, f, c0);
-  const uint32_t neg = ((xb >> 15) & 0x00010001u) * 0xffffu;  // all-ones halves where x is negative (or -0)
-  const h2 m = __builtin_bit_cast(h2, xb & ~neg);
-  return __builtin_elementwise_fma(-u, p, m);
-}
-
-template <bool VEC>
+template <bool VEC, bool RES>
 __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ A, long long a_ws, int lda, int M,
                                                    double rM, long long rows, const uint16_t *__restrict__ wk, int Ntp,
                                                    const float *__restrict__ b32, const uint16_t *__restrict__ b16,
@@ -277,6 +252,16 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
     bias32[c] = n + c < nend ? b32[n + c] : 0.f;
     bias16[c] = n + c < nend ? b16[n + c] : 0;
   }
+  // RES (with VEC): the residuals of the thread's 4 rows loaded together before any store (which the compiler may not
+  // move them past: out and res could alias)
+  uint4 rvs[4];
+  if (RES && full) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int lr = 4 * tr + r;
+      rvs[r] = rowB + lr < rows ? *(const uint4 *)(e.res + s_r[lr] + n) : make_uint4(0, 0, 0, 0);
+    }
+  }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int lr = 4 * tr + r;
@@ -294,7 +279,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
     }
     if (full) {
       if (e.res) {
-        const uint4 rv = *(const uint4 *)(e.res + s_r[lr] + n);
+        const uint4 rv = RES ? rvs[r] : *(const uint4 *)(e.res + s_r[lr] + n);
         v[0] = v[0] + __builtin_bit_cast(h2, rv.x);
         v[1] = v[1] + __builtin_bit_cast(h2, rv.y);
         v[2] = v[2] + __builtin_bit_cast(h2, rv.z);
@@ -402,12 +387,15 @@ int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, 
   BNH_REQ(nb < (1LL << 31));
   const dim3 grid((unsigned)nb);
   hipStream_t st = bnh_stream(stream);
-  if (vec)
-    hipLaunchKernelGGL((k_gemm_f16e<true>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt, W->b,
-                       W->b16, W->Kp, W->Np, bs, tc, d);
-  else
-    hipLaunchKernelGGL((k_gemm_f16e<false>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt,
+  if (vec && e->res)
+    hipLaunchKernelGGL((k_gemm_f16e<true, true>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt,
                        W->b, W->b16, W->Kp, W->Np, bs, tc, d);
+  else if (vec)
+    hipLaunchKernelGGL((k_gemm_f16e<true, false>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk,
+                       W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d);
+  else
+    hipLaunchKernelGGL((k_gemm_f16e<false, false>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk,
+                       W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d);
   BNH_HIP(hipGetLastError());
   return 0;
 }
