@@ -75,6 +75,8 @@ _SIGS = {
     "bnh_gemm_f16": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
     "bnh_gemm_f16_mfma": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
     "bnh_gemm_f16_body": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
+    "bnh_gemm_f16_ws_bytes": (C.c_size_t, [i32, i32, vp]),
+    "bnh_gemm_f16_ws": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp, C.c_size_t, vp]),
     "bnh_wino16_new": (vp, [i32, i32, vp, vp]),
     "bnh_wino16_free": (None, [vp]),
     "bnh_wino_f16": (i32, [vp, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp, i64, i32, i32, i32, vp]),

@@ -116,7 +116,8 @@ template <bool VEC, bool RES>
 __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ A, long long a_ws, int lda, int M,
                                                    double rM, long long rows, const uint16_t *__restrict__ wk, int Ntp,
                                                    const float *__restrict__ b32, const uint16_t *__restrict__ b16,
-                                                   int Kp, int Np, int bs, int TC, Epi16Dev e) {
+                                                   int Kp, int Np, int bs, int TC, Epi16Dev e,
+                                                   uint16_t *__restrict__ part, int nsplit) {
   const int TR = 256 / TC < 64 ? 256 / TC : 64, BM = 4 * TR, TN = 8 * TC;
   __shared__ __attribute__((aligned(16))) uint32_t As[FE_BM * FE_AS];
   __shared__ __attribute__((aligned(16))) uint4 Ws[FE_KC * 16];
@@ -127,10 +128,13 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
   const bool active = tr < TR;
   // 1-D grid of (row block, channel tile) pairs, channel tile fastest, after the XCD remap: the blocks that write the
   // parts of the same output rows run together under one L2, which merges their partial cache lines
+  // part: one K block per block (si, fastest), its fp16 chain results into part [si][rows][Np] for the combining kernel
   const int nct = (Np + TN - 1) / TN;
-  const unsigned lb = bnh_xcd_block(blockIdx.x, gridDim.x);
+  const unsigned lb0 = bnh_xcd_block(blockIdx.x, gridDim.x), si = part ? lb0 % nsplit : 0;
+  const unsigned lb = part ? lb0 / nsplit : lb0;
   const long long rowB = (long long)(lb / nct) * BM;
   const int n0 = (int)(lb % nct) * TN;
+  const int kbeg = (int)si * bs, Kend = part ? (kbeg + bs < Kp ? kbeg + bs : Kp) : Kp;
   for (int i = tid; i < BM; i += 256) {
     const long long row = rowB + i < rows ? rowB + i : rows - 1;
     const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
@@ -189,10 +193,10 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
     for (int c = 0; c < 8; c++) fb[r][c] = 0.f;
   }
   const int nblk = (Kp + bs - 1) / bs;
-  int kb = 0, k0 = 0;
+  int kb = kbeg, k0 = kbeg;
   int kn = bs < FE_KC ? bs : FE_KC;
-  if (kn > Kp) kn = Kp;
-  load(0, kn);
+  if (kn > Kend - kbeg) kn = Kend - kbeg;
+  load(kbeg, kn);
   const uint32_t *Ar = As + 4 * (active ? tr : 0) * FE_AS;
   const uint4 *Wt = Ws + tc;
   while (true) {
@@ -200,11 +204,11 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
     store();
     __syncthreads();
     // the next chunk: within this K block, or the first of the next
-    const int ke = kb + bs < Kp ? kb + bs : Kp;
+    const int ke = kb + bs < Kend ? kb + bs : Kend;
     int nk0 = k0 + kn, nkb = kb;
     if (nk0 >= ke) nkb = nk0 = ke;
-    const int nke = nkb + bs < Kp ? nkb + bs : Kp;
-    const int nkn = nk0 < Kp ? (nke - nk0 < FE_KC ? nke - nk0 : FE_KC) : 0;
+    const int nke = nkb + bs < Kend ? nkb + bs : Kend;
+    const int nkn = nk0 < Kend ? (nke - nk0 < FE_KC ? nke - nk0 : FE_KC) : 0;
     if (nkn) load(nk0, nkn);
     if (active) {
       for (int k = 0; k < kn; k += 2) {
@@ -226,7 +230,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
           for (int p = 0; p < 4; p++) acc[r][p] = __builtin_elementwise_fma(wb[p], hi, acc[r][p]);
         }
       }
-      if (k0 + kn >= ke && nblk > 1) {  // a K block ends: its fp16 results into the fp32 sums
+      if (k0 + kn >= ke && nblk > 1 && !part) {  // a K block ends: its fp16 results into the fp32 sums
 #pragma unroll
         for (int r = 0; r < 4; r++)
 #pragma unroll
@@ -242,6 +246,18 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
   }
   // epilogue
   const int n = n0 + 8 * tc;
+  if (part) {  // the block's fp16 results (Np % 8 == 0: a thread's 8 channels are all below Np or all past it)
+    if (!active || n >= Np) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const long long row = rowB + 4 * tr + r;
+      if (row >= rows) break;
+      *(uint4 *)(part + ((long long)si * rows + row) * Np + n) =
+          make_uint4(__builtin_bit_cast(uint32_t, acc[r][0]), __builtin_bit_cast(uint32_t, acc[r][1]),
+                     __builtin_bit_cast(uint32_t, acc[r][2]), __builtin_bit_cast(uint32_t, acc[r][3]));
+    }
+    return;
+  }
   const int nend = Np < e.ldo ? Np : e.ldo;
   if (!active || n >= nend) return;
   const bool full = VEC && n + 8 <= nend;
@@ -296,6 +312,70 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
         if (e.res) x = x + hfrom(e.res[s_r[lr] + n + c]);
         e.out[s_o[lr] + n + c] = hbits(x);
       }
+    }
+  }
+}
+
+// The split form's second kernel: per output the K blocks' fp16 results summed in fp32 in block order from +0 (the
+// reference's flush_add), + the fp32 bias, one rounding to fp16, the activation, the residual, the (padded) store.
+// A thread per row and 8 channels.
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_gemm_f16c(const uint16_t *__restrict__ part, int nsplit, long long rows, int M,
+                                                   double rM, const float *__restrict__ b32, int Np, Epi16Dev e) {
+  __shared__ uint32_t s_t01[16];
+  __shared__ uint16_t s_t2[16];
+  if (threadIdx.x < 16) {
+    s_t01[threadIdx.x] = (uint32_t)k_silu_c0[threadIdx.x] | ((uint32_t)k_silu_c1[threadIdx.x] << 16);
+    s_t2[threadIdx.x] = k_silu_c2[threadIdx.x];
+  }
+  __syncthreads();
+  const int np8 = Np / 8;
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * np8) return;
+  const long long row = i / np8;
+  const int n = (int)(i - row * np8) * 8;
+  float fb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int si = 0; si < nsplit; si++) {
+    const uint4 q = *(const uint4 *)(part + ((long long)si * rows + row) * Np + n);
+    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const h2 hv = __builtin_bit_cast(h2, w4[j]);
+      fb[2 * j] = fb[2 * j] + (float)hv.x;
+      fb[2 * j + 1] = fb[2 * j + 1] + (float)hv.y;
+    }
+  }
+  const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
+  long long orow = m;
+  if (e.opad) {
+    const int y = m / e.ow;
+    orow = (long long)(y + e.opad) * (e.ow + 2 * e.opad) + (m - y * e.ow) + e.opad;
+  }
+  uint16_t *o = e.out + w * e.out_ws + orow * e.ldo + n;
+  const uint16_t *rp = e.res ? e.res + w * e.res_ws + (long long)m * e.ldr + n : nullptr;
+  h2 v[4];
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    v[p] = (h2){f2h(fb[2 * p] + b32[n + 2 * p]), f2h(fb[2 * p + 1] + b32[n + 2 * p + 1])};
+    if (e.act == 1) v[p] = silu2_lut(v[p], s_t01, s_t2);
+    else if (e.act == 2) v[p] = (h2){hmax(v[p].x, (h16)0.0f), hmax(v[p].y, (h16)0.0f)};
+  }
+  if (VEC) {
+    if (rp) {
+      const uint4 rv = *(const uint4 *)rp;
+      v[0] = v[0] + __builtin_bit_cast(h2, rv.x);
+      v[1] = v[1] + __builtin_bit_cast(h2, rv.y);
+      v[2] = v[2] + __builtin_bit_cast(h2, rv.z);
+      v[3] = v[3] + __builtin_bit_cast(h2, rv.w);
+    }
+    *(uint4 *)o = make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                             __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+  } else {
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+      h16 x = (c & 1) ? v[c >> 1].y : v[c >> 1].x;
+      if (rp) x = x + hfrom(rp[c]);
+      o[c] = hbits(x);
     }
   }
 }
@@ -370,9 +450,16 @@ static int zero_halo16(const bnh_epi16 *e, int M, int B, void *stream) {
   return bnh_zero_halo(e->out, B == 1 ? per : e->out_ws, H, e->ow, e->ldo, e->opad, 2, B, stream);
 }
 
-int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
-                      void *stream) {
+size_t bnh_gemm_f16_ws_bytes(int M, int B, const bnh_h16w *W) {
+  if (!W || M <= 0 || B <= 0) return 0;
+  const int nblk = (W->Kp + 127) / 128;
+  return nblk > 1 ? (size_t)nblk * M * B * W->Np * 2 : 0;
+}
+
+int bnh_gemm_f16_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
+                    void *ws, size_t ws_bytes, void *stream) {
   if (gemm_f16_check(A, a_ws, lda, M, B, W, e)) return -1;
+  BNH_REQ(!ws || ((uintptr_t)ws & 15) == 0);
   const long long rows = (long long)M * B;
   Epi16Dev d = {e->act, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->res, e->res_ws, e->ldr};
   const int nblk = (W->Kp + 127) / 128, bs = ((W->Kp + nblk - 1) / nblk + 7) & ~7;  // kblocks (src/gemm_f16.c:55-58)
@@ -384,20 +471,37 @@ int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, 
                    (!e->res || (((uintptr_t)e->res & 15) == 0 && e->ldr % 8 == 0 && (B == 1 || e->res_ws % 8 == 0)));
   const int tr = 256 / tc < 64 ? 256 / tc : 64, bm = 4 * tr;
   const long long nb = bnh_ceil_div(rows, bm) * bnh_ceil_div(W->Np, 8 * tc);
-  BNH_REQ(nb < (1LL << 31));
-  const dim3 grid((unsigned)nb);
+  // fewer than two blocks per CU and several K blocks: one block per K block, then the combining kernel
+  const bool split = nblk > 1 && nb < 512 && ws && ws_bytes >= bnh_gemm_f16_ws_bytes(M, B, W);
+  const int nsplit = split ? nblk : 1;
+  uint16_t *part = split ? (uint16_t *)ws : nullptr;
+  BNH_REQ(nb * nsplit < (1LL << 31) && rows * np8 < (1LL << 40));
+  const dim3 grid((unsigned)(nb * nsplit));
   hipStream_t st = bnh_stream(stream);
-  if (vec && e->res)
+  if (vec && e->res && !split)
     hipLaunchKernelGGL((k_gemm_f16e<true, true>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt,
-                       W->b, W->b16, W->Kp, W->Np, bs, tc, d);
+                       W->b, W->b16, W->Kp, W->Np, bs, tc, d, part, nsplit);
   else if (vec)
     hipLaunchKernelGGL((k_gemm_f16e<true, false>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk,
-                       W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d);
+                       W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d, part, nsplit);
   else
     hipLaunchKernelGGL((k_gemm_f16e<false, false>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk,
-                       W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d);
+                       W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d, part, nsplit);
   BNH_HIP(hipGetLastError());
+  if (split) {
+    const dim3 g2((unsigned)bnh_ceil_div(rows * np8, 256));
+    if (vec)
+      hipLaunchKernelGGL((k_gemm_f16c<true>), g2, dim3(256), 0, st, part, nsplit, rows, M, 1.0 / M, W->b, W->Np, d);
+    else
+      hipLaunchKernelGGL((k_gemm_f16c<false>), g2, dim3(256), 0, st, part, nsplit, rows, M, 1.0 / M, W->b, W->Np, d);
+    BNH_HIP(hipGetLastError());
+  }
   return 0;
+}
+
+int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
+                      void *stream) {
+  return bnh_gemm_f16_ws(A, a_ws, lda, M, B, W, e, nullptr, 0, stream);
 }
 
 int bnh_gemm_f16(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,

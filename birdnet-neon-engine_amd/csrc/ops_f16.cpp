@@ -21,10 +21,17 @@ void *rt_dev_t(const rt_op *op, int i);
 // -------- PW f16: b = [in f16 [M][lda], out, res | -1]; t = [w (hpack panels), b32, b16];
 //          p = [N K Kp Np, M, lda, act, ldo, ow, opad, ldr]   (src/rt_ops_f16.c:14-27, 53-81; rt_pw_check,
 //          src/rt_ops_f32.c:129-152)
-typedef struct { bnh_h16w *W; } pw16_state;
+typedef struct {
+  bnh_h16w *W;
+  void *ws;       // the split form's workspace (device), grown with the arena
+  size_t ws_cap;  // bytes
+} pw16_state;
 static void pw16_fini(rt_op *op) {
   pw16_state *s = (pw16_state *)op->state;
-  if (s) bnh_h16w_free(s->W);
+  if (s) {
+    bnh_h16w_free(s->W);
+    if (s->ws) bnh_free(s->ws);
+  }
   free(s);
 }
 static int pw16_init(rt_ctx *c, rt_op *op) {
@@ -63,7 +70,7 @@ static int pw16_init(rt_ctx *c, rt_op *op) {
   return 0;
 }
 static int pw16_run(rt_ctx *c, rt_op *op) {
-  const pw16_state *s = (const pw16_state *)op->state;
+  pw16_state *s = (pw16_state *)op->state;
   const int *p = op->p;
   bnh_epi16 e = {p[6], (uint16_t *)rt_b(c, op, 1), rt_ws(c, op, 1), p[7], p[8], p[9], (const uint16_t *)rt_b(c, op, 2),
                  rt_ws(c, op, 2), p[10]};
@@ -71,7 +78,23 @@ static int pw16_run(rt_ctx *c, rt_op *op) {
     const int H = p[4] / p[8];
     if (bnh_zero_halo(e.out, e.out_ws, H, p[8], p[7], p[9], 2, c->nwin, c->stream)) return -1;
   }
-  return bnh_gemm_f16_body((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e, c->stream);
+  // the split form's workspace: op-private, grown with the arena (the fp16 results of every K block of each window)
+  void *ws = nullptr;
+  size_t wsb = bnh_gemm_f16_ws_bytes(p[4], c->bcap, s->W);
+  if (wsb) {
+    if (s->ws_cap < wsb) {
+      if (s->ws) bnh_free(s->ws);
+      s->ws_cap = 0;
+      if (!(s->ws = bnh_malloc(wsb))) {
+        rt_oom(c, op, wsb);
+        return -1;
+      }
+      s->ws_cap = wsb;
+    }
+    ws = s->ws;
+  }
+  return bnh_gemm_f16_ws((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e, ws,
+                         s->ws_cap, c->stream);
 }
 
 // -------- DWK f16: as the fp32 op, fp16 buffers and tensors (src/rt_ops_f16.c:192-203)

@@ -145,6 +145,13 @@ int bnh_gemm_f16(const uint16_t *A, long long a_ws, int lda, int M, int B, const
  * own their arena slot keep the zero halo written when the arena was cleared) */
 int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
                       void *stream);
+/* bnh_gemm_f16_body with a workspace ws (16-byte aligned) of at least bnh_gemm_f16_ws_bytes(M, B, W) bytes: when the
+ * product has several K blocks and too few rows to fill the GPU, every K block runs as its own set of blocks and a
+ * second kernel sums their fp16 results in fp32 in the reference's block order (the same bits). ws NULL or too small:
+ * the one-kernel form. */
+size_t bnh_gemm_f16_ws_bytes(int M, int B, const bnh_h16w *W);
+int bnh_gemm_f16_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
+                    void *ws, size_t ws_bytes, void *stream);
 /* the same product on fp16 MFMA with fp32 accumulation over the whole K (no reference counterpart: a faster form
  * for callers that accept the fp16 accumulation error bound of the reference instead of its exact bits) */
 int bnh_gemm_f16_mfma(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,

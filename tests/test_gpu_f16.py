@@ -82,6 +82,15 @@ def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, Kp=None, b16=None, fn
             r_ws = M * ldr
             dR = H.DeviceArray.from_host(res.reshape(Bw, -1))
         e = H.Epi16(act, dO.ptr, o_ws, ldo, ow, opad, dR.ptr if dR else None, r_ws, res.shape[2] if res is not None else 0)
+        if fn == "bnh_gemm_f16_ws":   # the split form (no halo zeroing: the output starts at zero here)
+            wsb = H.lib().bnh_gemm_f16_ws_bytes(M, Bw, hw)
+            dW = H.DeviceArray.zeros(max(int(wsb), 16), np.uint8)
+            dO = H.DeviceArray.zeros((Bw, o_ws), np.float16)
+            e = H.Epi16(act, dO.ptr, o_ws, ldo, ow, opad, dR.ptr if dR else None, r_ws,
+                        res.shape[2] if res is not None else 0)
+            H.check(H.lib().bnh_gemm_f16_ws(dA.ptr, a_ws, lda, M, Bw, hw, e, dW.ptr, wsb, None), fn)
+            H.sync()
+            return dO.numpy()[:, :rows * ldo].reshape(Bw, rows, ldo), Wp
         H.check(getattr(H.lib(), fn)(dA.ptr, a_ws, lda, M, Bw, hw, e, None), fn)
         H.sync()
         out = dO.numpy()
@@ -245,3 +254,24 @@ def test_silu_epilogue_every_fp16_input(hip):
         assert same_bits(out[0], ref)
         # the NaN patterns stay NaN; the LUT SiLU of +inf is inf - inf = NaN as well (the reference's formula)
         assert np.isnan(out[0][:, 0]).sum() == 2 * 1023 + (act == 1)
+
+
+# K blocks run as separate blocks and a combining kernel when rows are few (the v2.4 head shapes 1536 -> 192 and
+# 864 -> 108 at 24 / 96 pixels per window), with residual, SiLU, a padded output and unaligned rows
+@pytest.mark.parametrize("K,N,M,B,act,opad,ldo", [(1536, 192, 24, 8, 0, 0, None), (864, 108, 96, 4, 1, 1, None),
+                                                  (300, 200, 33, 3, 2, 0, None), (1536, 192, 24, 5, 1, 0, 196)])
+def test_split_k_blocks_bit_exact(hip, K, N, M, B, act, opad, ldo):
+    rng = np.random.default_rng(K + N + M)
+    Kp = (K + 7) // 8 * 8
+    A = np.zeros((B, M, Kp), np.float16)
+    A[:, :, :K] = rng.standard_normal((B, M, K))
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    Np = (N + 7) // 8 * 8
+    ow = 8 if opad else 0
+    res = rng.standard_normal((B, M, ldo or Np)).astype(np.float16) if not opad else None
+    say("f16 gemm split", K, N, M, B, act, opad, ldo)
+    out, Wp = run_gpu(hip, A, W, b, act=act, ow=ow, opad=opad, res=res, fn="bnh_gemm_f16_ws", ldo=ldo)
+    for i in range(B):
+        ref = O.gemm_f16(A[i], Wp, b, act=act, ldo=ldo, ow=ow, opad=opad, res=None if res is None else res[i])
+        assert same_bits(out[i][:, :Np], ref[:, :Np]), i
