@@ -461,17 +461,25 @@ static int se_launch(const float *chsum, long long c_ws, int C, int rd, int P, c
   const bool split = gate && D && C % 8 == 0;
   if (gate && work) {
     // the two FCs as kernels over all windows: fc1 into work [B][rd], fc2 + sigmoid into gate
-    const int wb1 = (size_t)4 * C * 4 + 4 * 32 * 8 * 4 <= 64 * 1024 ? 4 : 1;
+    // windows per block: 4 (each weight read serves 4 windows) unless that leaves fewer than 512 blocks, then 2 or 1
+    const long long rb1 = bnh_ceil_div(rd, 32);
+    int wb1 = bnh_ceil_div(B, 4) * rb1 >= 512 ? 4 : bnh_ceil_div(B, 2) * rb1 >= 512 ? 2 : 1;
+    if ((size_t)wb1 * C * 4 + (size_t)wb1 * 32 * 8 * 4 > 64 * 1024) wb1 = 1;
     const float inv = 1.f / (float)P;
-    const dim3 g1((unsigned)bnh_ceil_div(B, wb1), (unsigned)bnh_ceil_div(rd, 32));
+    const dim3 g1((unsigned)bnh_ceil_div(B, wb1), (unsigned)rb1);
     const size_t l1 = sizeof(float) * ((size_t)wb1 * C + (size_t)wb1 * 32 * 8);
     if (wb1 == 4) hipLaunchKernelGGL((k_se_fc1<4>), g1, dim3(256), l1, st, chsum, c_ws, C, rd, inv, w1, b1, work, B);
+    else if (wb1 == 2) hipLaunchKernelGGL((k_se_fc1<2>), g1, dim3(256), l1, st, chsum, c_ws, C, rd, inv, w1, b1, work, B);
     else hipLaunchKernelGGL((k_se_fc1<1>), g1, dim3(256), l1, st, chsum, c_ws, C, rd, inv, w1, b1, work, B);
     BNH_HIP(hipGetLastError());
-    const dim3 g2((unsigned)bnh_ceil_div(C, 256), (unsigned)bnh_ceil_div(B, 4));
-    const size_t l2 = sizeof(float) * 4 * (size_t)rd;
-    if (f16) hipLaunchKernelGGL((k_se_fc2<4, true>), g2, dim3(256), l2, st, work, C, rd, w2t, b2, gate, g_ws, B);
-    else hipLaunchKernelGGL((k_se_fc2<4, false>), g2, dim3(256), l2, st, work, C, rd, w2t, b2, gate, g_ws, B);
+    const long long cb2 = bnh_ceil_div(C, 256);
+    const int wb2 = bnh_ceil_div(B, 4) * cb2 >= 512 ? 4 : bnh_ceil_div(B, 2) * cb2 >= 512 ? 2 : 1;
+    const dim3 g2((unsigned)cb2, (unsigned)bnh_ceil_div(B, wb2));
+    const size_t l2 = sizeof(float) * wb2 * (size_t)rd;
+#define SE_FC2(W_, F_) hipLaunchKernelGGL((k_se_fc2<W_, F_>), g2, dim3(256), l2, st, work, C, rd, w2t, b2, gate, g_ws, B)
+    if (f16) { if (wb2 == 4) SE_FC2(4, true); else if (wb2 == 2) SE_FC2(2, true); else SE_FC2(1, true); }
+    else { if (wb2 == 4) SE_FC2(4, false); else if (wb2 == 2) SE_FC2(2, false); else SE_FC2(1, false); }
+#undef SE_FC2
     BNH_HIP(hipGetLastError());
     if (D && !split) {  // C % 8 != 0: the one-kernel form gates D (recomputing the same gates)
       work = nullptr;
