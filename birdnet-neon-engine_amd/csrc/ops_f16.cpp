@@ -91,10 +91,10 @@ static int pw16_run(rt_ctx *c, rt_op *op) {
       }
       s->ws_cap = wsb;
     }
-    ws = s->ws;
+    ws = (char *)s->ws + bnh_gemm_f16_ws_bytes(p[4], 1, s->W) * c->w0;  // this sub-batch's windows
   }
   return bnh_gemm_f16_ws((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e, ws,
-                         s->ws_cap, c->stream);
+                         bnh_gemm_f16_ws_bytes(p[4], c->nwin, s->W), c->stream);
 }
 
 // -------- DWK f16: as the fp32 op, fp16 buffers and tensors (src/rt_ops_f16.c:192-203)
@@ -161,8 +161,9 @@ static int se_run(rt_ctx *c, rt_op *op) {
   float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)(g_ws + p[1]));
   if (!g) return -1;
   return bnh_se_f16((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_h(op, 0),
-                    (const float *)dev_h(op, 1), (const float *)dev_h(op, 2), (const float *)dev_h(op, 3), g, g_ws,
-                    g + g_ws * c->bcap, (uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
+                    (const float *)dev_h(op, 1), (const float *)dev_h(op, 2), (const float *)dev_h(op, 3),
+                    g + g_ws * c->w0, g_ws, g + g_ws * c->bcap + (long long)p[1] * c->w0, (uint16_t *)rt_b(c, op, 0),
+                    rt_ws(c, op, 0), c->nwin, c->stream);
 }
 
 // -------- MEAN f16, PAD f16 (src/rt_ops_f16.c:204-214)

@@ -199,8 +199,9 @@ static int se_run(rt_ctx *c, rt_op *op) {
   float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)(g_ws + p[1]));
   if (!g) return -1;
   return bnh_se_f32((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_tn(op, 0),
-                    (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3), g, g_ws,
-                    g + g_ws * c->bcap, (float *)rt_b(c, op, 0), rt_ws(c, op, 0), c->nwin, c->stream);
+                    (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3),
+                    g + g_ws * c->w0, g_ws, g + g_ws * c->bcap + (long long)p[1] * c->w0, (float *)rt_b(c, op, 0),
+                    rt_ws(c, op, 0), c->nwin, c->stream);
 }
 static int seg_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
@@ -208,7 +209,8 @@ static int seg_run(rt_ctx *c, rt_op *op) {
   if (!work) return -1;
   return bnh_se_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[0], p[1], p[2], (const float *)dev_tn(op, 0),
                     (const float *)dev_tn(op, 1), (const float *)dev_tn(op, 2), (const float *)dev_tn(op, 3),
-                    (float *)rt_b(c, op, 1), rt_ws(c, op, 1), work, nullptr, 0, c->nwin, c->stream);
+                    (float *)rt_b(c, op, 1), rt_ws(c, op, 1), work + (long long)p[1] * c->w0, nullptr, 0, c->nwin,
+                    c->stream);
 }
 
 // -------- MEAN: b = [x [P][ld], out f32 [C]]; p = [P C ld]   (rt_mean_check, src/rt_ops_f32.c:510-522)

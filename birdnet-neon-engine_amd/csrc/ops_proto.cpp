@@ -99,12 +99,13 @@ int bnh_proto_s8_run(rt_ctx *c, rt_op *op) {
   }
   int8_t *qa = (int8_t *)rt_b(c, op, 2);
   float *cm = (float *)rt_b(c, op, 3);
-  if (bnh_quant_cells((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), P, C, ld, s->eps, qa, rt_ws(c, op, 2), Kp, s->sx,
-                      P, B, c->stream))
+  float *sx = s->sx + (size_t)P * c->w0;  // this sub-batch's windows
+  if (bnh_quant_cells((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), P, C, ld, s->eps, qa, rt_ws(c, op, 2), Kp, sx, P,
+                      B, c->stream))
     return -1;
-  if (bnh_proto_colmax(qa, rt_ws(c, op, 2), s->sx, P, P, s->W, cm, rt_ws(c, op, 3), B, c->stream)) return -1;
+  if (bnh_proto_colmax(qa, rt_ws(c, op, 2), sx, P, P, s->W, cm, rt_ws(c, op, 3), B, c->stream)) return -1;
   return bnh_proto_logits(cm, rt_ws(c, op, 3), s->clsw, s->clsb, nc, ppc, (float *)rt_b(c, op, 1), rt_ws(c, op, 1), B,
-                          c->win_fail, c->fail_op + 1, c->stream);
+                          c->win_fail + c->w0, c->fail_op + 1, c->stream);
 }
 
 void bnh_proto_s8_fini(rt_op *op) {

@@ -75,6 +75,10 @@ struct rt_ctx {
   // device memory: per buffer, window 0's address and the per-window stride in elements
   int bcap;              // windows the arena holds
   int nwin;              // windows of the current run (<= bcap): ops launch for this many
+  int w0;                // the first of them (a sub-batch of the run starts past window 0)
+  size_t *wsb;           // per buffer: bytes between windows
+  hipStream_t stream2;   // the second sub-batch's stream (created on first use; default priority)
+  hipEvent_t ev_fork, ev_join;
   size_t *slot_bytes;    // per slot: bytes of one window's copy (64-aligned, >= 64 bytes of zero slack)
   int *slot_users;       // per slot: the number of buffers placed in it
   size_t arena_bytes;
@@ -134,9 +138,10 @@ int rt_need_t(const rt_ctx *c, const rt_op *op, int i, size_t nbytes, int atleas
 int rt_need_args(const rt_ctx *c, const rt_op *op, int nb, int nt, int ni);
 #define RT_REQ(c, op, cond) \
   do { if (!(cond)) return rt_bad(c, op, "parameter check failed: %s", #cond); } while (0)
-// device address of window 0 of buffer argument i (NULL when absent) and its per-window stride (elements)
+// device address of buffer argument i for window w0, the current sub-batch's first (NULL when absent), and its
+// per-window stride (elements)
 static inline void *rt_b(const rt_ctx *c, const rt_op *op, int i) {
-  return i >= op->nb || op->b[i] < 0 ? nullptr : c->buf[op->b[i]];
+  return i >= op->nb || op->b[i] < 0 ? nullptr : (char *)c->buf[op->b[i]] + (size_t)c->w0 * c->wsb[op->b[i]];
 }
 static inline long long rt_ws(const rt_ctx *c, const rt_op *op, int i) {
   return i >= op->nb || op->b[i] < 0 ? 0 : c->ws[op->b[i]];

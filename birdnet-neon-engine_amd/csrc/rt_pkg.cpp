@@ -343,6 +343,7 @@ static int arena_alloc(rt_ctx *c, int windows, char *err, size_t errlen) {
     const rt_bufdesc *d = &c->bufd[i];
     c->buf[i] = a + slot_off[d->slot];
     c->ws[i] = (long long)(c->slot_bytes[d->slot] / rt_dsize(d->dtype));
+    c->wsb[i] = c->slot_bytes[d->slot];
   }
   free(slot_off);
   return 0;
@@ -386,9 +387,10 @@ rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
   c->bufd = (rt_bufdesc *)malloc(sizeof(rt_bufdesc) * d->n_buf);
   c->buf = (void **)calloc(d->n_buf, sizeof(void *));
   c->ws = (long long *)calloc(d->n_buf, sizeof(long long));
+  c->wsb = (size_t *)calloc(d->n_buf, sizeof(size_t));
   c->slot_bytes = (size_t *)calloc(d->n_buf, sizeof(size_t));
   c->slot_users = (int *)calloc(d->n_buf, sizeof(int));
-  if (!c->bufd || !c->buf || !c->ws || !c->slot_bytes || !c->slot_users) { KIND(RT_E_OOM); FAIL("out of memory (%u buffer descriptors)", d->n_buf); }
+  if (!c->bufd || !c->buf || !c->ws || !c->wsb || !c->slot_bytes || !c->slot_users) { KIND(RT_E_OOM); FAIL("out of memory (%u buffer descriptors)", d->n_buf); }
   memcpy(c->bufd, m + d->buf_off, sizeof(rt_bufdesc) * d->n_buf);
   for (uint32_t i = 0; i < d->n_buf; i++) {
     const rt_bufdesc *b = &c->bufd[i];
@@ -507,19 +509,56 @@ static double now_s(void) {
   return t.tv_sec + t.tv_nsec * 1e-9;
 }
 
+// the second stream and the fork / join events, created once (0 when the runtime refuses them: one stream then)
+static int ensure_stream2(rt_ctx *c) {
+  if (c->stream2) return 1;
+  hipStream_t s = nullptr;
+  hipEvent_t a = nullptr, b = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return 0;
+  if (hipEventCreateWithFlags(&a, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess) {
+    if (a) hipEventDestroy(a);
+    hipStreamDestroy(s);
+    return 0;
+  }
+  c->stream2 = s;
+  c->ev_fork = a;
+  c->ev_join = b;
+  return 1;
+}
+
 int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
   if (B > c->bcap) { snprintf(err, errlen, "rt_run_batch: %d windows but the arena holds %d", B, c->bcap); return -1; }
   if (hipMemsetAsync(c->win_fail, 0, sizeof(int) * (size_t)B, c->stream) != hipSuccess) {
     snprintf(err, errlen, "device error clearing the window flags");
     return -1;
   }
-  c->nwin = B;
+  // Two sub-batches on two streams, their launches interleaved op by op: the windows are independent, so the GPU
+  // may run one half's kernel beside the other half's (a latency-bound kernel beside a bandwidth-bound one). The
+  // second stream starts after everything the caller's stream holds and the caller's stream waits for it at the end.
+  const int split = !c->prof && B >= 64 && ensure_stream2(c) ? 1 : 0;
+  const int B1 = split ? (B + 1) / 2 : B;
+  hipStream_t s1 = c->stream;
+  if (split && (hipEventRecord(c->ev_fork, s1) != hipSuccess || hipStreamWaitEvent(c->stream2, c->ev_fork, 0) != hipSuccess)) {
+    snprintf(err, errlen, "device error forking the second stream");
+    return -1;
+  }
   double t0 = c->prof ? now_s() : 0;
   for (int i = 0; i < c->n_ops; i++) {
     rt_op *op = &c->ops[i];
     c->fail_op = i;  // ops read it to tag the windows they fail
-    int r = op->k->run(c, op);
+    int r = 0;
+    for (int h = 0; h <= split && !r; h++) {
+      c->w0 = h ? B1 : 0;
+      c->nwin = h ? B - B1 : B1;
+      c->stream = h ? c->stream2 : s1;
+      r = op->k->run(c, op);
+    }
+    c->w0 = 0;
+    c->nwin = B;
+    c->stream = s1;
     if (r) {
+      if (split) hipStreamSynchronize(c->stream2);  // leave no launch of this batch in flight
       char src[160];
       rt_op_src(c, i, src, sizeof src);
       const char *why = bnh_last_error();
@@ -535,6 +574,11 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
     }
   }
   c->fail_op = -1;
+  if (split && (hipEventRecord(c->ev_join, c->stream2) != hipSuccess || hipStreamWaitEvent(s1, c->ev_join, 0) != hipSuccess)) {
+    hipStreamSynchronize(c->stream2);
+    snprintf(err, errlen, "device error joining the second stream");
+    return -1;
+  }
   hipError_t e = hipMemcpyAsync(status, c->win_fail, sizeof(int) * (size_t)B, hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) { snprintf(err, errlen, "device error after the op list: %s", hipGetErrorString(e)); return -1; }
@@ -574,9 +618,16 @@ void rt_ctx_free(rt_ctx *c) {
   if (c->win_fail) hipFree(c->win_fail);
   free(c->buf);
   free(c->ws);
+  free(c->wsb);
   free(c->slot_bytes);
   free(c->slot_users);
   free(c->bufd);
   if (c->stream && c->own_stream) hipStreamDestroy(c->stream);
+  if (c->stream2) {
+    hipStreamSynchronize(c->stream2);
+    hipStreamDestroy(c->stream2);
+  }
+  if (c->ev_fork) hipEventDestroy(c->ev_fork);
+  if (c->ev_join) hipEventDestroy(c->ev_join);
   free(c);
 }

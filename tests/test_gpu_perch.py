@@ -54,3 +54,17 @@ def test_perch_batch_bit_exact(hip, perch):
             assert not s1.any() and same(o1[0], out[w]) and same(e1[0], emb[w])
         o2, e2, s2 = m.infer_batch(pcm[2:6])
         assert not s2.any() and same(o2, out[2:6]) and same(e2, emb[2:6])
+
+
+def test_perch_two_stream_batch(hip, perch):
+    """72 windows run as two halves on two streams: the bytes of the same windows in batches of 24 (one stream)."""
+    pn, path = perch
+    rng = np.random.default_rng(9)
+    pcm = np.stack([perchnet.signal(rng) for _ in range(72)])
+    say("perch two-stream batch 72")
+    with binding.Model(path) as m:
+        out, emb, status = m.infer_batch(pcm)
+        assert not status.any()
+        for lo in (0, 24, 48):
+            o, e, s = m.infer_batch(pcm[lo:lo + 24])
+            assert not s.any() and same(o, out[lo:lo + 24]) and same(e, emb[lo:lo + 24]), lo

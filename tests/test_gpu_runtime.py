@@ -109,6 +109,32 @@ def test_failed_window_is_reported(hip, tmp_path):
             assert same(out[w], spec.oracle(pcm[w])[1])
 
 
+def test_large_batch_two_streams(hip, tmp_path):
+    """From 64 windows up a batch runs as two halves on two streams: the same bytes and failure flags as batches
+    too small to split, a failing window in either half reported against its own index."""
+    spec = Spec(5)
+    path = spec.package(str(tmp_path / "net.bnpk"))
+    rng = np.random.default_rng(6)
+    B = 101
+    pcm = (rng.standard_normal((B, spec.M * spec.K0)) * 0.5).astype(np.float32)
+    bad = np.where(np.arange(pcm.shape[1]) % 2, -1.5e38, 1.5e38)
+    pcm[7] = bad                 # first half (windows 0..50)
+    pcm[77] = bad                # second half
+    say("runtime two-stream batch", B)
+    with binding.Model(path) as m:
+        out, _, status = m.infer_batch(pcm, check=False)
+        assert [w for w in range(B) if status[w]] == [7, 77] and status[77] == 3
+        for lo in range(0, B, 30):       # 30 windows: one stream
+            o, _, st = m.infer_batch(pcm[lo:lo + 30], check=False)
+            assert same(o, out[lo:lo + 30]) and np.array_equal(st, status[lo:lo + 30]), lo
+        for w in (0, 50, 51, 77, 100):
+            rc, ref = spec.oracle(pcm[w])
+            assert (rc != 0) == (w in (7, 77)) and same(out[w], ref), w
+        with pytest.raises(binding.BnnError) as e:
+            m.infer_batch(pcm)
+        assert e.value.kind == "window" and "window 7 of 101" in str(e.value)
+
+
 def test_device_resident_batch(hip, tmp_path):
     spec = Spec(5)
     path = spec.package(str(tmp_path / "net.bnpk"))

@@ -56,3 +56,18 @@ def test_v24_batch_bit_exact(hip, v24):
         assert not s1.any() and same(o1[0], out[4]) and same(e1[0], emb[4])
         o2, e2, s2 = m.infer_batch(pcm[1:4])
         assert not s2.any() and same(o2, out[1:4]) and same(e2, emb[1:4])
+
+
+def test_v24_two_stream_batch(hip, v24):
+    """72 windows run as two halves on two streams (the split-K GEMM workspaces and SE scratch offset per half):
+    the bytes of the same windows in batches of 24 (one stream)."""
+    vn, path = v24
+    rng = np.random.default_rng(10)
+    pcm = np.stack([v24net.signal(rng) for _ in range(72)])
+    say("v24 two-stream batch 72")
+    with binding.Model(path) as m:
+        out, emb, status = m.infer_batch(pcm)
+        assert not status.any()
+        for lo in (0, 24, 48):
+            o, e, s = m.infer_batch(pcm[lo:lo + 24])
+            assert not s.any() and same(o, out[lo:lo + 24]) and same(e, emb[lo:lo + 24]), lo
