@@ -88,6 +88,9 @@ _SIGS = {
                           i32, vp, i64, i32, i32, vp, i64, i32, vp]),
     "bnh_dw3_f32": (i32, [vp, i64, i32, i32, i32, i32, vp, vp, vp, i64, i32,
                           i32, vp, i64, i32, vp]),
+    "bnh_pwdw_f32": (i32, [vp, i64, vp, i64, vp, i64, i32, i32, vp, i32, i32,
+                           i32, i32, i32, i32, vp, vp, i32, vp, i64, i32, i32,
+                           vp, i64, i32, vp]),
     "bnh_dwk_f16": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, vp, vp,
                           i32, vp, i64, i32, i32, vp, i64, i32, vp]),
     "bnh_dw3_f16": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, vp,

@@ -31,6 +31,17 @@ extern "C" int bnh_stem_f32to16_body(const float *img, long long i_ws, int H, in
                                      const float *w, const float *bias, int Kp, int N, int Np, int act, uint16_t *out,
                                      long long o_ws, int ldo, int opad, int B, void *stream);
 
+// the int8 GEMM weights of PW_S8 / GEMV_S8 in HBM (kern_s8n.hip)
+struct bnh_s8w {
+  int N, K, Kp, Np, Nt;
+  int8_t *w;        // [Nt][Kp]: channel rows, zero past Np
+  float *sw, *b;    // [Nt]
+  int32_t *colsum;  // [Nt]
+};
+
+// whether bnh_pwdw_f32 takes this expansion + depthwise pair (0) or not (-1, with the reason in bnh_last_error)
+extern "C" int bnh_pwdw_f32_plan(int C, int Kp, int H, int W, int k, int s, int pt, int pl, int form, int Ho, int Wo);
+
 static inline hipStream_t bnh_stream(void *s) { return (hipStream_t)s; }
 static inline long long bnh_ceil_div(long long a, long long b) { return (a + b - 1) / b; }
 static inline long long bnh_round_up(long long a, long long b) { return bnh_ceil_div(a, b) * b; }

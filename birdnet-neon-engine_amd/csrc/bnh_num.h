@@ -108,10 +108,12 @@ BNH_DEV float bnh_frecps(float a, float b) {
 // normal-operand case (exponent 253 - e, 8 fraction bits from the 9-bit estimate of the leading 8 significand bits)
 // and FRECPS to one fused 2 - d r. A NaN x gives NaN through the final product x r whatever the clamp did with it
 // (the reference's NaN travels through d and r instead: the same NaN result, payloads aside).
-// The fraction bits of the estimate, per leading significand byte, at bits 22..15: a block puts this table in LDS
-// (bnh_silu_table, then a barrier) for bnh_silu_f32_t.
+// Per leading significand byte of d: 253 << 23 with the estimate's fraction bits at 22..15. bnh_silu_f32_t subtracts
+// d's exponent field from it, giving FRECPE's exponent 253 - e over the same fraction (no borrow reaches the fraction:
+// e <= 127 + 61). A block puts this table in LDS (bnh_silu_table, then a barrier) for bnh_silu_f32_t.
 BNH_DEV void bnh_silu_table(uint32_t *tbl) {
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) tbl[i] = (uint32_t)(bnh_recip_estimate(256 | i) & 0xff) << 15;
+  for (int i = threadIdx.x; i < 256; i += blockDim.x)
+    tbl[i] = 253u << 23 | (uint32_t)(bnh_recip_estimate(256 | i) & 0xff) << 15;
 }
 BNH_DEV float bnh_silu_d(float x) {  // the divisor d = 1 + 2^t, t = clamp(-x log2 e, -60, 60)
   const float magic = 12582912.0f;
@@ -130,7 +132,7 @@ BNH_DEV float bnh_silu_d(float x) {  // the divisor d = 1 + 2^t, t = clamp(-x lo
 BNH_DEV float bnh_silu_f32_t(float x, const uint32_t *tbl) {
   const float d = bnh_silu_d(x);
   const uint32_t db = bnh_bits(d);
-  float r = bnh_float(((253u << 23) - (db & 0x7f800000u)) | tbl[(db >> 15) & 0xffu]);
+  float r = bnh_float(tbl[(db >> 15) & 0xffu] - (db & 0x7f800000u));
   r = r * __builtin_fmaf(-d, r, 2.f);
   return x * r;
 }

@@ -82,8 +82,60 @@ static int dw_grid(int nitems, int ni, int C, int Ho, int B, unsigned *blocks, l
 }
 
 // ------------------------------------------------------------------ fp32 DWK (form 0) and DW3 (form 2)
-// DWK: input row oy*s - pt + h + ky, column px*s - pl + h + kx of the halo-h input. DW3: the reference's three column
-// partial sums, rows oy*s + ky, columns px*s + kx of the halo-1 input (pads 1), SiLU always.
+// The chains of one item's four outputs from its input window xv (rows ky, columns q S + kx for output q): DWK
+// (src/pc_kern_f32.c:163-334) one chain per pixel, or for a 4-pixel group two per pixel (even and odd taps) added at
+// the end; DW3 (src/gemm_f32.c:213-441) the three column partial sums. All four outputs are computed (those past the
+// item's end from zeros, then dropped), so the chains have no branches between them.
+// One input row ky of those chains (xr = row ky of the window): the chains run row by row, in the same order, whether
+// the window sits in registers (k_dw_f32) or is read one row at a time (k_pwdw_f32). a / e / d: the chains' partial
+// sums (DW3: the three column sums; DWK: even and odd taps, or one chain).
+template <int K, int S, int FORM>
+BNH_DEV void dw_row_f32(int ky, const float (&xr)[3 * S + K], const float (&wv)[K * K], float bias, bool split,
+                        float (&a)[4], float (&e)[4], float (&d)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    if (FORM == 2) {
+      const int o = q * S;
+      if (ky == 0) {
+        a[q] = __builtin_fmaf(wv[0], xr[o], bias);
+        e[q] = wv[1] * xr[o + 1];
+        d[q] = wv[2] * xr[o + 2];
+      } else {
+        a[q] = __builtin_fmaf(wv[3 * ky], xr[o], a[q]);
+        e[q] = __builtin_fmaf(wv[3 * ky + 1], xr[o + 1], e[q]);
+        d[q] = __builtin_fmaf(wv[3 * ky + 2], xr[o + 2], d[q]);
+      }
+    } else {
+      if (ky == 0) {
+        a[q] = bias;
+        e[q] = 0.f;
+      }
+#pragma unroll
+      for (int kx = 0; kx < K; kx++) {
+        const int t = ky * K + kx;
+        const float x = xr[q * S + kx];
+        if (split && (t & 1)) e[q] = __builtin_fmaf(x, wv[t], e[q]);
+        else a[q] = __builtin_fmaf(x, wv[t], a[q]);
+      }
+    }
+  }
+}
+template <int K, int S, int FORM>
+BNH_DEV void dw_finish_f32(bool split, const float (&a)[4], const float (&e)[4], const float (&d)[4], float (&v)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) v[q] = FORM == 2 ? a[q] + (e[q] + d[q]) : split ? a[q] + e[q] : a[q];
+}
+template <int K, int S, int FORM>
+BNH_DEV void dw_chains_f32(const float (&xv)[K][3 * S + K], const float (&wv)[K * K], float bias, bool split,
+                           float (&v)[4]) {
+  float a[4], e[4], d[4];
+#pragma unroll
+  for (int ky = 0; ky < K; ky++) dw_row_f32<K, S, FORM>(ky, xv[ky], wv, bias, split, a, e, d);
+  dw_finish_f32<K, S, FORM>(split, a, e, d, v);
+}
+
+// DWK: input row oy*s - pt + h + ky, column px*s - pl + h + kx of the halo-h input. DW3: rows oy*s + ky, columns
+// px*s + kx of the halo-1 input (pads 1), SiLU always.
 template <int K, int S, int FORM>
 __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, long long x_ws, int Wp, int C, int pt,
                                                 int pl, const float *__restrict__ w, const float *__restrict__ b,
@@ -119,44 +171,8 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
     for (int ky = 0; ky < K; ky++)
 #pragma unroll
       for (int kx = 0; kx < NC; kx++) xv[ky][kx] = kx < ncol ? x0[ky * rs + (long long)kx * C] : 0.f;
-    // all four outputs are computed (those past the item's end from the zeros above, then dropped), so the four
-    // chains and their SiLUs have no branches between them
     float v[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      if (FORM == 2) {
-        const int o = q * S;
-        float acc = __builtin_fmaf(wv[0], xv[0][o], bias);
-        float acb = wv[1] * xv[0][o + 1];
-        float acd = wv[2] * xv[0][o + 2];
-        acc = __builtin_fmaf(wv[3], xv[1][o], acc);
-        acb = __builtin_fmaf(wv[4], xv[1][o + 1], acb);
-        acd = __builtin_fmaf(wv[5], xv[1][o + 2], acd);
-        acc = __builtin_fmaf(wv[6], xv[2][o], acc);
-        acb = __builtin_fmaf(wv[7], xv[2][o + 1], acb);
-        acd = __builtin_fmaf(wv[8], xv[2][o + 2], acd);
-        v[q] = acc + (acb + acd);
-      } else if (item.split) {
-        float a = bias, e = 0.f;
-#pragma unroll
-        for (int ky = 0; ky < K; ky++)
-#pragma unroll
-          for (int kx = 0; kx < K; kx++) {
-            const int t = ky * K + kx;
-            const float x = xv[ky][q * S + kx];
-            if (t & 1) e = __builtin_fmaf(x, wv[t], e);
-            else a = __builtin_fmaf(x, wv[t], a);
-          }
-        v[q] = a + e;
-      } else {
-        float a = bias;
-#pragma unroll
-        for (int ky = 0; ky < K; ky++)
-#pragma unroll
-          for (int kx = 0; kx < K; kx++) a = __builtin_fmaf(xv[ky][q * S + kx], wv[ky * K + kx], a);
-        v[q] = a;
-      }
-    }
+    dw_chains_f32<K, S, FORM>(xv, wv, bias, item.split, v);
     if (FORM == 2 || act == 1) {
 #pragma unroll
       for (int q = 0; q < 4; q++) v[q] = bnh_silu_f32_t(v[q], tbl);
@@ -165,6 +181,181 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
 #pragma unroll
     for (int q = 0; q < 4; q++)
       if (q < item.n) o[(long long)q * C] = v[q];
+  }
+}
+
+// ------------------------------------------------------------------ PW_S8 expansion fused into the fp32 depthwise
+// An int8 1x1 expansion (PW_S8: the int8 GEMM over rows that are already quantized, its fp32 dequant epilogue and
+// activation, src/gemm_s8n.c:105-135) whose output only this depthwise conv reads. A block recomputes the expanded
+// pixels one band of output rows needs into LDS (int8 MFMA), 16 channels at a time, and runs the depthwise chains of
+// those channels from there, so the expanded tensor never reaches HBM. Every value is the one the two ops give: the
+// int32 sums are exact in any order, the fp32 operations are the same ones in the same order as k_s8n_gemm's epilogue
+// and k_dw_f32's chains, and cells outside the image hold the zero halo of the expansion's output buffer.
+// Block = (window, band of TH output rows, one of gsplit parts of the 16-channel groups). It stages the band's int8
+// rows, their scales and zero points and each pixel's LDS cell once, then walks its channel groups (each group's
+// weights loaded one group ahead): expansion into LDS, barrier, depthwise, barrier. The expansion is VALU work
+// (dequantisation and the exact SiLU of every expanded value); the kernel is bound by it, not by HBM.
+// LDS (floats): the band's RIN = (TH - 1) S + K input rows x WL = (Wo - 1) S + K padded columns x 16 channels at a
+// pixel stride of 20 (the four pixels 4 apart that one MFMA result store writes land in distinct banks) and a row
+// stride RS with S RS = 16 (mod 64) (the four output rows one wavefront's depthwise reads cover land in distinct
+// banks); 64 discard cells; then per band pixel (16 ntile of them) its scale, zero point and cell offset; then the
+// int8 rows (Kp bytes each).
+typedef int v4i __attribute__((ext_vector_type(4)));
+template <int K, int S, int FORM, int KS>
+__global__ __launch_bounds__(256) void k_pwdw_f32(const int8_t *__restrict__ q, long long q_ws,
+                                                  const float *__restrict__ sa, long long sa_ws,
+                                                  const int32_t *__restrict__ za, long long za_ws, int H, int W, int Kp,
+                                                  const int8_t *__restrict__ wt, const float *__restrict__ sw,
+                                                  const int32_t *__restrict__ cs, const float *__restrict__ pb, int pact,
+                                                  int C, int pt, int pl, const float *__restrict__ w,
+                                                  const float *__restrict__ b, int dact, float *__restrict__ out,
+                                                  long long o_ws, int Ho, int Wo, int nit, int TH, int nband,
+                                                  int gsplit, int WL, int RS, int sz_off, int npx, double rW) {
+  constexpr int CG = 16, PS = 20;  // channels per group, pixel stride
+  extern __shared__ float xs[];
+  __shared__ uint32_t tbl[256];
+  bnh_silu_table(tbl);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const unsigned lb = bnh_xcd_block(blockIdx.x, gridDim.x);
+  const int part = (int)(lb % gsplit);
+  const unsigned rest = lb / gsplit;
+  const int band = (int)(rest % nband), win = (int)(rest / nband);
+  const int ncg = C / CG, g0 = part * ncg / gsplit, g1 = (part + 1) * ncg / gsplit;
+  const int oy0 = band * TH, THb = Ho - oy0 < TH ? Ho - oy0 : TH;
+  const int RIN = (THb - 1) * S + K, ybase = oy0 * S - pt;  // LDS row r holds image row ybase + r
+  const int y0 = ybase > 0 ? ybase : 0, y1 = ybase + RIN < H ? ybase + RIN : H;
+  const int xr = pl + W < WL ? pl + W : WL;  // LDS columns [pl, xr) hold image columns [0, xr - pl)
+  const int p0 = y0 * W, np = (y1 - y0) * W, ntile = (np + 15) / 16;
+  float *s_sa = xs + sz_off;  // [npx] (npx >= 16 ntile of every band)
+  uint32_t *s_z = (uint32_t *)(s_sa + npx);
+  int *s_off = (int *)(s_z + npx);
+  int8_t *s_q = (int8_t *)(s_off + npx);  // [np][Kp]
+  const int trash = sz_off - 64;          // discard cells
+  // stage: the band's int8 rows (16-byte chunks), each pixel's scale, zero point and LDS cell (discard cells for the
+  // pixels of the last tile past the band)
+  {
+    const int8_t *qw = q + win * q_ws + (long long)p0 * Kp;
+    const int nch = np * Kp / 16;
+    for (int i = threadIdx.x; i < nch; i += 256) *(v4i *)(s_q + 16 * i) = *(const v4i *)(qw + 16 * i);
+    for (int i = threadIdx.x; i < 16 * ntile; i += 256) {
+      const int p = p0 + (i < np ? i : np - 1);
+      s_sa[i] = sa[win * sa_ws + p];
+      s_z[i] = (uint32_t)za[win * za_ws + p];
+      const int y = bnh_div(p, W, rW), x = p - y * W;
+      s_off[i] = i < np && pl + x < WL ? (y - ybase) * RS + (pl + x) * PS : trash;
+    }
+  }
+  // zeros of the cells outside the image (rows above and below it, then the columns left and right of it): written
+  // once, no channel group's expansion touches them
+  {
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int top = (y0 - ybase) * RS, bot = (y1 - ybase) * RS, end = RIN * RS;
+    for (int i = 4 * threadIdx.x; i < top; i += 1024) *(float4 *)(xs + i) = z4;
+    for (int i = bot + 4 * threadIdx.x; i < end; i += 1024) *(float4 *)(xs + i) = z4;
+    const int nh = WL - (xr - pl);  // halo columns per row
+    const int n = (y1 - y0) * nh * (CG / 4);
+    for (int i = threadIdx.x; i < n; i += 256) {
+      const int c4 = i % (CG / 4), cell = i / (CG / 4);
+      const int r = cell / nh, j = cell - r * nh;
+      const int xl = j < pl ? j : xr + (j - pl);
+      *(float4 *)(xs + (y0 - ybase + r) * RS + xl * PS + 4 * c4) = z4;
+    }
+  }
+  constexpr int NC = 3 * S + K;
+  const int c = threadIdx.x % CG, nl = lane & 15, kc = (lane >> 4) * 16;
+  const int npos = THb * nit;
+  // pos / THb as (pos + 0.5) / THb in float: its distance to the nearest integer, >= 0.5 / THb, exceeds the product's
+  // error, < npos 2^-23 / THb, for npos < 2^22 (the plan keeps npos < 2^16)
+  const float rth = 1.f / (float)THb;
+  float *ow = out + win * o_ws + (long long)oy0 * Wo * C + c;
+  // the first group's expansion constants and weight fragments (later groups': loaded one group ahead)
+  float swn = sw[16 * g0 + nl], bn = pb[16 * g0 + nl];
+  int32_t csn = cs[16 * g0 + nl];
+  v4i bf[KS];
+#pragma unroll
+  for (int k = 0; k < KS; k++)
+    bf[k] = 64 * k + kc < Kp ? *(const v4i *)(wt + (long long)(16 * g0 + nl) * Kp + 64 * k + kc) : (v4i){0, 0, 0, 0};
+  __syncthreads();  // the SiLU table, the staged rows, the zeros
+  for (int g = g0; g < g1; g++) {
+    const int c0 = 16 * g;
+    // this group's depthwise weights: consumed after the expansion, which hides their latency
+    float wv[K * K];
+#pragma unroll
+    for (int t = 0; t < K * K; t++) wv[t] = w[(long long)t * C + c0 + c];
+    const float bias = b[c0 + c];
+    // expansion of the band's pixels, channels c0 .. c0 + 15: lane l holds pixels 16 t + 4 (l >> 4) .. + 3 of channel
+    // c0 + (l & 15)
+    for (int t = wave; t < ntile; t += 4) {
+      const int8_t *arow = s_q + (16 * t + nl) * Kp + kc;
+      v4i acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int k = 0; k < KS; k++)
+        if (64 * k < Kp) {
+          const v4i a = 64 * k + kc < Kp && 16 * t + nl < np ? *(const v4i *)(arow + 64 * k) : (v4i){0, 0, 0, 0};
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bf[k], acc, 0, 0, 0);
+        }
+      const int pr0 = 16 * t + 4 * (lane >> 4);
+      const float4 s4 = *(const float4 *)(s_sa + pr0);
+      const uint4 z4 = *(const uint4 *)(s_z + pr0);
+      const int4 o4 = *(const int4 *)(s_off + pr0);
+      const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+      const uint32_t zv[4] = {z4.x, z4.y, z4.z, z4.w};
+      const int ov[4] = {o4.x, o4.y, o4.z, o4.w};
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int32_t cq = (int32_t)((uint32_t)acc[r] - (uint32_t)csn * zv[r]);
+        const float f = (float)cq;
+        const float scl = swn * sv[r];
+        const float yv = f * scl;
+        v[r] = yv + bn;
+      }
+      if (pact == 1) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[r] = bnh_silu_f32_t(v[r], tbl);
+      } else if (pact == 2) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) v[r] = bnh_relu_f32(v[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) xs[ov[r] + nl] = v[r];
+    }
+    __syncthreads();
+    // the next group's expansion constants, in flight during this group's depthwise
+    if (g + 1 < g1) {
+      const int n = 16 * (g + 1) + nl;
+      swn = sw[n];
+      bn = pb[n];
+      csn = cs[n];
+#pragma unroll
+      for (int k = 0; k < KS; k++)
+        bf[k] = 64 * k + kc < Kp ? *(const v4i *)(wt + (long long)n * Kp + 64 * k + kc) : (v4i){0, 0, 0, 0};
+    }
+    // the depthwise chains: thread = (channel c, position), positions = (item, output row) with the row fastest
+    for (int pos = threadIdx.x / CG; pos < npos; pos += 256 / CG) {
+      const int it = (int)(((float)pos + 0.5f) * rth), row = pos - it * THb;
+      const Item item = item_of(it, Wo, FORM);
+      const int ncol = (item.n - 1) * S + K;
+      const float *x0 = xs + row * S * RS + item.px * S * PS + c;
+      float pa[4], pe[4], pd[4], v[4];
+#pragma unroll
+      for (int ky = 0; ky < K; ky++) {  // one input row at a time
+        float xr_[NC];
+#pragma unroll
+        for (int kx = 0; kx < NC; kx++) xr_[kx] = kx < ncol ? x0[ky * RS + kx * PS] : 0.f;
+        dw_row_f32<K, S, FORM>(ky, xr_, wv, bias, item.split, pa, pe, pd);
+      }
+      dw_finish_f32<K, S, FORM>(item.split, pa, pe, pd, v);
+      if (FORM == 2 || dact == 1) {
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) v[qq] = bnh_silu_f32_t(v[qq], tbl);
+      }
+      float *o = ow + ((long long)row * Wo + item.px) * C + c0;
+#pragma unroll
+      for (int qq = 0; qq < 4; qq++)
+        if (qq < item.n) o[(long long)qq * C] = v[qq];
+    }
+    __syncthreads();  // the next group's expansion overwrites the cells
   }
 }
 
@@ -611,6 +802,59 @@ static int dw_check(int H, int W, int C, int k, int s, int pt, int pl, int Ho, i
   return 0;
 }
 
+// the fused kernel's plan: KS K steps per MFMA tile (a power of two: the weight fragments a lane holds), TH output
+// rows per band (nband bands of at most TH rows), gsplit blocks per band (parts of the channel groups), LDS rows of WL
+// padded columns at a stride of RS floats, the per-pixel arrays at float offset sz_off (npx pixels each), lds bytes
+// per block
+struct PwdwPlan {
+  int KS, TH, nband, gsplit, WL, RS, sz_off, npx;
+  size_t lds;
+};
+static int pwdw_plan(int C, int Kp, int H, int W, int k, int s, int pt, int pl, int form, int Ho, int Wo, int B,
+                     PwdwPlan *pp) {
+  BNH_REQ(C > 0 && C % 16 == 0 && Kp > 0 && Kp % 16 == 0);
+  BNH_REQ((k == 3 || k == 5) && (s == 1 || s == 2));
+  BNH_REQ(form == 0 || (form == 2 && k == 3 && pt == 1 && pl == 1));
+  const int h = (k - 1) / 2;
+  BNH_REQ(H > 0 && W > 0 && Ho > 0 && Wo > 0 && pt >= 0 && pt <= h && pl >= 0 && pl <= h);
+  BNH_REQ((Ho - 1) * s - pt + k <= H + h && (Wo - 1) * s - pl + k <= W + h);  // the last tap stays in the halo
+  BNH_REQ(Ho <= 65536 && (long long)Ho * items_per_row(Wo, form) < 65536);  // positions of a band (float indexing)
+  if (Kp > 512) return bnh_fail("bnh_pwdw_f32: K %d: the fused kernel holds at most 512 int8 columns per row", Kp);
+  int KS = 1;
+  while (64 * KS < Kp) KS *= 2;
+  const int WL = (Wo - 1) * s + k;
+  int RS = WL * 20;
+  while ((s * RS) % 64 != 16) RS += 4;
+  // LDS per block: three blocks per CU (the kernel's registers allow no more)
+  const long long budget = 52 * 1024;
+  auto bytes = [&](int TH) {  // RIN rows of cells + discard cells, 12 bytes per pixel + its int8 row
+    const long long rin = (long long)(TH - 1) * s + k, px = (rin * W + 15) / 16 * 16;
+    return 4 * (rin * RS + 64) + px * (12 + Kp);
+  };
+  if (bytes(1) > budget)
+    return bnh_fail("bnh_pwdw_f32: %d input columns (%d padded columns, K %d) leave no band of one output row in %lld "
+                    "bytes of LDS", W, WL, Kp, budget);
+  int TH = 1;
+  while (TH < Ho && bytes(TH + 1) <= budget) TH++;
+  const int nband = (Ho + TH - 1) / TH;
+  TH = (Ho + nband - 1) / nband;  // bands of equal height
+  // parts of the channel groups: enough blocks to fill the chip (about 2048), at least 2 groups per part
+  const long long nb = (long long)B * nband;
+  int gsplit = nb >= 2048 ? 1 : (int)bnh_ceil_div(2048, nb);
+  if (gsplit > C / 32) gsplit = C / 32 > 1 ? C / 32 : 1;
+  const long long rin = (long long)(TH - 1) * s + k;
+  pp->KS = KS;
+  pp->TH = TH;
+  pp->nband = nband;
+  pp->gsplit = gsplit;
+  pp->WL = WL;
+  pp->RS = RS;
+  pp->sz_off = (int)(rin * RS + 64);
+  pp->npx = (int)((rin * W + 15) / 16 * 16);
+  pp->lds = (size_t)bytes(TH);
+  return 0;
+}
+
 extern "C" {
 
 int bnh_dwk_f32(const float *xp, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl, const float *w,
@@ -657,6 +901,60 @@ int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, con
   if (chsum) {
     BNH_REQ(B == 1 || cs_ws >= C);
     if (chsum_launch<float, 2>(out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st)) return -1;
+  }
+  return 0;
+}
+
+int bnh_pwdw_f32_plan(int C, int Kp, int H, int W, int k, int s, int pt, int pl, int form, int Ho, int Wo) {
+  PwdwPlan pp;
+  return pwdw_plan(C, Kp, H, W, k, s, pt, pl, form, Ho, Wo, 1, &pp);
+}
+
+int bnh_pwdw_f32(const int8_t *q, long long q_ws, const float *sa, long long sa_ws, const int32_t *za, long long za_ws,
+                 int H, int W, const bnh_s8w *Wt, int pact, int k, int s, int pt, int pl, int form, const float *w,
+                 const float *b, int dact, float *out, long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws,
+                 int B, void *stream) {
+  BNH_REQ(q && sa && za && Wt && w && b && out && B > 0);
+  BNH_REQ(pact >= 0 && pact <= 2 && (dact == 0 || dact == 1));
+  const int C = Wt->Np, Kp = Wt->Kp;
+  PwdwPlan pp;
+  if (pwdw_plan(C, Kp, H, W, k, s, pt, pl, form, Ho, Wo, B, &pp)) return -1;
+  const long long M = (long long)H * W;
+  BNH_REQ(((uintptr_t)q & 15) == 0 && q_ws % 16 == 0);
+  BNH_REQ(B == 1 || (q_ws >= M * Kp && sa_ws >= M && za_ws >= M && o_ws >= (long long)Ho * Wo * C));
+  const long long nblk = (long long)B * pp.nband * pp.gsplit;
+  BNH_REQ(nblk < (1LL << 31));
+  const int nit = items_per_row(Wo, form);
+  hipStream_t st = bnh_stream(stream);
+#define PWDW(KK, SS, FF, KS_)                                                                                          \
+  hipLaunchKernelGGL((k_pwdw_f32<KK, SS, FF, KS_>), dim3((unsigned)nblk), dim3(256), pp.lds, st, q, q_ws, sa, sa_ws, za, \
+                     za_ws, H, W, Kp, Wt->w, Wt->sw, Wt->colsum, Wt->b, pact, C, pt, pl, w, b, dact, out, o_ws, Ho, Wo, \
+                     nit, pp.TH, pp.nband, pp.gsplit, pp.WL, pp.RS, pp.sz_off, pp.npx, 1.0 / W)
+#define PWDW_KS(KK, SS, FF)                                                                                            \
+  do {                                                                                                                 \
+    if (pp.KS == 1) PWDW(KK, SS, FF, 1);                                                                               \
+    else if (pp.KS == 2) PWDW(KK, SS, FF, 2);                                                                          \
+    else if (pp.KS == 4) PWDW(KK, SS, FF, 4);                                                                          \
+    else PWDW(KK, SS, FF, 8);                                                                                          \
+  } while (0)
+  if (form == 2) {
+    if (s == 1) PWDW_KS(3, 1, 2);
+    else PWDW_KS(3, 2, 2);
+  } else if (k == 3) {
+    if (s == 1) PWDW_KS(3, 1, 0);
+    else PWDW_KS(3, 2, 0);
+  } else {
+    if (s == 1) PWDW_KS(5, 1, 0);
+    else PWDW_KS(5, 2, 0);
+  }
+#undef PWDW_KS
+#undef PWDW
+  BNH_HIP(hipGetLastError());
+  if (chsum) {
+    BNH_REQ(B == 1 || cs_ws >= C);
+    if (form == 2 ? chsum_launch<float, 2>(out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st)
+                  : chsum_launch<float, 0>(out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st))
+      return -1;
   }
   return 0;
 }

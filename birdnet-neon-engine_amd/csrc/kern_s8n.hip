@@ -20,13 +20,6 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-struct bnh_s8w {
-  int N, K, Kp, Np, Nt;
-  int8_t *w;        // [Nt][Kp]
-  float *sw, *b;    // [Nt]
-  int32_t *colsum;  // [Nt]
-};
-
 struct bnh_q8w {
   int N, K, Kt, Nt, zx, zy, lo, hi;
   int8_t *w;          // [Nt][Kt], zero past K (Kt = K rounded up to 64) and past N

@@ -84,12 +84,23 @@ int rt_dw3_check(rt_ctx *c, rt_op *op, int dt, int pt, int pl) {
   return rt_need(c, op, 1, dt, (size_t)Ho * Wo * C) || rt_need(c, op, 2, RT_F32, (size_t)C) ? RT_E_PARAM : 0;
 }
 
+// the depthwise op computing its input itself: expansion op->pw's GEMM over the rows it quantized (bnh_pwdw_f32)
+static int dw_fused_run(rt_ctx *c, rt_op *op, int k, int s, int pt, int pl, int form, int dact, int Ho, int Wo) {
+  const rt_op *pw = op->pw;
+  return bnh_pwdw_f32((const int8_t *)rt_b(c, pw, 3), rt_ws(c, pw, 3), (const float *)rt_b(c, pw, 4), rt_ws(c, pw, 4),
+                      (const int32_t *)rt_b(c, pw, 5), rt_ws(c, pw, 5), op->p[0], op->p[1], rt_pw8_plain(pw),
+                      pw->p[6], k, s, pt, pl, form, (const float *)dev_tn(op, 0), (const float *)dev_tn(op, 1), dact,
+                      (float *)rt_b(c, op, 1), rt_ws(c, op, 1), Ho, Wo, (float *)rt_b(c, op, 2), rt_ws(c, op, 2),
+                      c->nwin, c->stream);
+}
+
 static int dwk_init(rt_ctx *c, rt_op *op) {
   if (rt_dwk_check(c, op, 4)) return RT_E_PARAM;
   return rt_dev_tensors(c, op, 2);
 }
 static int dwk_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
+  if (op->pw) return dw_fused_run(c, op, p[3], p[4], p[5], p[6], 0, p[9], p[7], p[8]);
   return bnh_dwk_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[0], p[1], p[2], p[3], p[4], p[5], p[6],
                      (const float *)dev_tn(op, 0), (const float *)dev_tn(op, 1), p[9], (float *)rt_b(c, op, 1),
                      rt_ws(c, op, 1), p[7], p[8], (float *)rt_b(c, op, 2), rt_ws(c, op, 2), c->nwin, c->stream);
@@ -101,6 +112,7 @@ static int dw3_init(rt_ctx *c, rt_op *op) {
 }
 static int dw3_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
+  if (op->pw) return dw_fused_run(c, op, 3, p[3], 1, 1, 2, 1, p[4], p[5]);
   return bnh_dw3_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[0], p[1], p[2], p[3],
                      (const float *)dev_tn(op, 0), (const float *)dev_tn(op, 1), (float *)rt_b(c, op, 1),
                      rt_ws(c, op, 1), p[4], p[5], (float *)rt_b(c, op, 2), rt_ws(c, op, 2), c->nwin, c->stream);
@@ -296,6 +308,26 @@ static const rt_kernel K_MEAN = {mean_init, mean_run, nullptr, "mean_f32", 0x2, 
 static const rt_kernel K_PAD = {pad_init, pad_run, nullptr, "pad_f32", 0x2, 0};
 static const rt_kernel K_DW3 = {dw3_init, dw3_run, rt_dev_fini, "dw3_f32", 0x6, 0};
 static const rt_kernel K_DWK = {dwk_init, dwk_run, rt_dev_fini, "dwk_f32", 0x6, 0};
+
+int rt_fuse_pwdw(rt_ctx *c, rt_op *pw, rt_op *dw) {
+  (void)c;
+  const bnh_s8w *W = rt_pw8_plain(pw);
+  if (!W || (dw->k != &K_DW3 && dw->k != &K_DWK) || dw->b[0] != pw->b[1]) return 0;
+  const int *p = pw->p, *d = dw->p;
+  const bool dw3 = dw->k == &K_DW3;
+  const int H = d[0], Wd = d[1], C = d[2];
+  const int k = dw3 ? 3 : d[3], s = dw3 ? d[3] : d[4], pt = dw3 ? 1 : d[5], pl = dw3 ? 1 : d[6];
+  const int Ho = dw3 ? d[4] : d[7], Wo = dw3 ? d[5] : d[8];
+  // the expansion fills exactly the depthwise input: C channels of H x W pixels, halo (k - 1) / 2
+  if (p[3] != C || p[7] != C || p[4] != H * Wd || p[8] != Wd || p[9] != (k - 1) / 2) return 0;
+  if (bnh_pwdw_f32_plan(C, p[2], H, Wd, k, s, pt, pl, dw3 ? 2 : 0, Ho, Wo)) {
+    bnh_clear_error();
+    return 0;
+  }
+  pw->quant_only = 1;
+  dw->pw = pw;
+  return 1;
+}
 
 const rt_kernel *rt_k_f32(int base) {
   switch (base) {

@@ -88,6 +88,10 @@ static int pw8_run(rt_ctx *c, rt_op *op) {
   const s8_state *s = (const s8_state *)op->state;
   const int *p = op->p;
   const int B = c->nwin;
+  if (op->quant_only)  // the depthwise op that reads the output recomputes the GEMM from the quantized rows
+    return bnh_s8n_quant_rows((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], p[1], p[2], nullptr, 0,
+                              (int8_t *)rt_b(c, op, 3), rt_ws(c, op, 3), (float *)rt_b(c, op, 4), rt_ws(c, op, 4),
+                              (int32_t *)rt_b(c, op, 5), rt_ws(c, op, 5), B, c->stream);
   const rt_bufdesc *r = rt_bd(c, op, 2);
   const bool gated = op->nb == 7 && op->b[6] >= 0;
   bnh_epi32 e = {p[6], (float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[7], p[8], p[9], (const float *)rt_b(c, op, 2),
@@ -138,6 +142,12 @@ static int gemv8_run(rt_ctx *c, rt_op *op) {
 static const rt_kernel K_PW_S8 = {pw8_init, pw8_run, s8_fini, "pw_s8n", 0x3a, 0x44};
 static const rt_kernel K_GEMV_S8 = {gemv8_init, gemv8_run, s8_fini, "gemv_s8n", 0x1e, 0};
 static const rt_kernel K_PROTO_S8 = {bnh_proto_s8_init, bnh_proto_s8_run, bnh_proto_s8_fini, "proto_s8n", 0xe, 0};
+
+const bnh_s8w *rt_pw8_plain(const rt_op *op) {
+  if (op->k != &K_PW_S8 || !op->state) return nullptr;
+  if ((op->nb == 7 && op->b[6] >= 0) || op->b[2] >= 0 || op->p[9] == 0) return nullptr;
+  return ((const s8_state *)op->state)->W;
+}
 
 const rt_kernel *rt_k_s8n(int base) {
   switch (base) {

@@ -41,6 +41,10 @@ typedef struct rt_op {
   const int32_t *b, *t, *p;  // into the mapped file
   void *state;               // device weights and launch plan built by init
   const struct rt_kernel *k;
+  // fusion (set after every op's init): an int8 expansion whose only reader is the next op, a fp32 depthwise conv,
+  // only quantizes its rows (quant_only), and the depthwise op recomputes the expansion from them (pw)
+  struct rt_op *pw;
+  int quant_only;
 } rt_op;
 
 typedef struct rt_kernel {
@@ -79,6 +83,7 @@ struct rt_ctx {
   size_t *wsb;           // per buffer: bytes between windows
   hipStream_t stream2;   // the second sub-batch's stream (created on first use; default priority)
   hipEvent_t ev_fork, ev_join;
+  int one_stream;        // never split a batch over two streams
   size_t *slot_bytes;    // per slot: bytes of one window's copy (64-aligned, >= 64 bytes of zero slack)
   int *slot_users;       // per slot: the number of buffers placed in it
   size_t arena_bytes;
@@ -124,6 +129,14 @@ int rt_op_src(const rt_ctx *c, int i, char *buf, size_t n);
 const char *rt_op_name(const rt_ctx *c, int i);
 const char *rt_dtype_name(uint32_t dt);
 size_t rt_dsize(uint32_t dt);
+
+// ---- fusion
+struct bnh_s8w;
+// PW_S8 (ops_s8n.cpp): its weights when the op is an expansion a reader may recompute (no gate, no residual, a
+// zero-haloed output), else NULL
+const struct bnh_s8w *rt_pw8_plain(const rt_op *op);
+// fp32 DW3 / DWK (ops_f32.cpp): fuse expansion pw into depthwise op dw when bnh_pwdw_f32 takes the pair; 1 if fused
+int rt_fuse_pwdw(rt_ctx *c, rt_op *pw, rt_op *dw);
 
 // ---- helpers for kernel init / run (the reference's contract helpers, src/rt.h:133-167)
 const void *rt_t(const rt_ctx *c, const rt_op *op, int i, size_t *nbytes);

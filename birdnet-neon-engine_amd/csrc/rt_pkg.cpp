@@ -354,6 +354,29 @@ int rt_reserve(rt_ctx *c, int windows, char *err, size_t errlen) {
   return arena_alloc(c, windows, err, errlen);
 }
 
+// An int8 expansion (PW_S8) followed by the fp32 depthwise conv that is the only reader of its output runs as one
+// kernel (bnh_pwdw_f32): the expansion op then only quantizes its rows. Its output buffer is then never written, so
+// no other op and no path output may read it.
+static void fuse_ops(rt_ctx *c) {
+  for (int i = 0; i + 1 < c->n_ops; i++) {
+    rt_op *pw = &c->ops[i], *dw = &c->ops[i + 1];
+    if (pw->nb < 2 || pw->b[1] < 0) continue;
+    const int32_t buf = pw->b[1];
+    bool other = buf == (int32_t)c->path->in_buf || buf == (int32_t)c->path->out_buf || buf == (int32_t)c->path->emb_buf;
+    for (int j = 0; j < c->n_ops && !other; j++)
+      for (int a = 0; a < c->ops[j].nb && !other; a++)
+        if (c->ops[j].b[a] == buf && !(j == i && a == 1) && !(j == i + 1 && a == 0)) other = true;
+    // the fused kernel reads the quantized rows (PW_S8 buffers 3..5, dead after the expansion in the package's slot
+    // plan) while it writes the depthwise outputs (buffers 1, 2): they must not share a memory slot
+    for (int a = 3; a <= 5 && !other; a++)
+      for (int o = 1; o <= 2 && !other; o++)
+        if (a < pw->nb && o < dw->nb && pw->b[a] >= 0 && dw->b[o] >= 0 &&
+            c->bufd[pw->b[a]].slot == c->bufd[dw->b[o]].slot)
+          other = true;
+    if (!other) rt_fuse_pwdw(c, pw, dw);
+  }
+}
+
 rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
   KIND(RT_E_PARAM);
   const rt_pathdesc *d = rt_path(p, pi);
@@ -491,6 +514,12 @@ rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
   }
   c->err = nullptr;
   {
+    const char *fe = getenv("BNH_FUSE");  // BNH_FUSE=0 runs every op as the package lists it
+    if (!fe || atoi(fe) != 0) fuse_ops(c);
+    const char *se = getenv("BNH_SPLIT");  // BNH_SPLIT=0 runs every batch on one stream
+    c->one_stream = se && atoi(se) == 0;
+  }
+  {
     const char *pe = getenv("BNN_PROF");
     c->prof = pe ? atoi(pe) : 0;
     if (c->prof) c->t_op = (double *)calloc(d->n_ops, sizeof(double));
@@ -536,7 +565,7 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
   // Two sub-batches on two streams, their launches interleaved op by op: the windows are independent, so the GPU
   // may run one half's kernel beside the other half's (a latency-bound kernel beside a bandwidth-bound one). The
   // second stream starts after everything the caller's stream holds and the caller's stream waits for it at the end.
-  const int split = !c->prof && B >= 64 && ensure_stream2(c) ? 1 : 0;
+  const int split = !c->prof && !c->one_stream && B >= 64 && ensure_stream2(c) ? 1 : 0;
   const int B1 = split ? (B + 1) / 2 : B;
   hipStream_t s1 = c->stream;
   if (split && (hipEventRecord(c->ev_fork, s1) != hipSuccess || hipStreamWaitEvent(c->stream2, c->ev_fork, 0) != hipSuccess)) {
@@ -604,7 +633,12 @@ void rt_ctx_free(rt_ctx *c) {
       tot += c->t_op[i];
       char src[120];
       rt_op_src(c, i, src, sizeof src);
-      if (c->prof > 1) fprintf(stderr, "  %3d %-14s %10.5f  %s\n", i, c->ops[i].k->name, 1e3 * c->t_op[i] / c->nprof, src);
+      const rt_op *op = &c->ops[i];
+      char fz[48] = "";
+      if (op->pw) snprintf(fz, sizeof fz, " [fused: computes op %d's expansion]", (int)(op->pw - c->ops));
+      else if (op->quant_only) snprintf(fz, sizeof fz, " [quantizes only]");
+      if (c->prof > 1)
+        fprintf(stderr, "  %3d %-14s %10.5f  %s%s\n", i, op->k->name, 1e3 * c->t_op[i] / c->nprof, src, fz);
     }
     fprintf(stderr, "  %-14s      %10.5f\n", "total", 1e3 * tot / c->nprof);
   }

@@ -200,6 +200,16 @@ int bnh_dwk_f32(const float *xp, long long x_ws, int H, int W, int C, int k, int
 /* DW3 fp32 (3x3, pads 1, SiLU): replaces dw3_f32 / dw3s2_f32 (src/gemm_f32.c:213-441) */
 int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, const float *w, const float *b, float *out,
                 long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws, int B, void *stream);
+/* An int8 1x1 expansion fused into the fp32 depthwise conv that is its only reader: no reference counterpart (the
+ * reference runs PW_S8 into a zero-haloed buffer, then DW3 / DWK over it; src/rt_ops_s8n.c:92-134 and
+ * src/rt_ops_f32.c:216-232, 435-458). From the PW_S8 rows already quantized by bnh_s8n_quant_rows (q, sa, za over
+ * M = H W pixels) and W's C = W->Np channels with activation pact, it writes exactly the outputs (and per-channel
+ * sums) bnh_s8n_gemm into a halo-(k-1)/2 buffer followed by bnh_dw3_f32 (form 2: k 3, pads 1) or bnh_dwk_f32
+ * (form 0, activation dact) would write, without the expanded tensor. C % 16 == 0, k in {3, 5}. */
+int bnh_pwdw_f32(const int8_t *q, long long q_ws, const float *sa, long long sa_ws, const int32_t *za, long long za_ws,
+                 int H, int W, const bnh_s8w *Wt, int pact, int k, int s, int pt, int pl, int form, const float *w,
+                 const float *b, int dact, float *out, long long o_ws, int Ho, int Wo, float *chsum, long long cs_ws,
+                 int B, void *stream);
 /* DWK fp16 (values as fp16 bit patterns): replaces dwk_f16_run (src/pc_kern_f16.c:16-96) */
 int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl,
                 const uint16_t *w, const uint16_t *b, int act, uint16_t *out, long long o_ws, int Ho, int Wo,

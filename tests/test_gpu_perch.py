@@ -68,3 +68,23 @@ def test_perch_two_stream_batch(hip, perch):
         for lo in (0, 24, 48):
             o, e, s = m.infer_batch(pcm[lo:lo + 24])
             assert not s.any() and same(o, out[lo:lo + 24]) and same(e, emb[lo:lo + 24]), lo
+
+
+def test_perch_fused_expansions(hip, perch, monkeypatch, capfd):
+    """Each of the 24 expansions runs inside its depthwise conv (one kernel, the expanded tensor never stored), and
+    the outputs are the bytes of the op list run as written (BNH_FUSE=0)."""
+    pn, path = perch
+    rng = np.random.default_rng(11)
+    pcm = np.stack([perchnet.signal(rng) for _ in range(8)])
+    say("perch fused vs op by op")
+    monkeypatch.setenv("BNN_PROF", "2")
+    with binding.Model(path) as m:
+        out, emb, status = m.infer_batch(pcm)
+    err = capfd.readouterr().err
+    assert err.count("[fused: computes op") == 24 and err.count("[quantizes only]") == 24, err[-2000:]
+    monkeypatch.delenv("BNN_PROF")
+    monkeypatch.setenv("BNH_FUSE", "0")
+    with binding.Model(path) as m:
+        o2, e2, s2 = m.infer_batch(pcm)
+    assert not status.any() and not s2.any()
+    assert same(out, o2) and same(emb, e2)
