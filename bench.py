@@ -492,41 +492,65 @@ def run_perch(a, H, rng, B, stream):
     print(json.dumps(line), flush=True)
 
 
-# HBM bytes per launch of that GEMM (24 -> 144 channels, 15,687 px, 256 windows): FETCH_SIZE x 2 + WRITE_SIZE from
-# rocprofv3 --pmc runs of this bench (profiles/k_s8n_gemm_pw_s8_24to144_249x63_b256.md)
-PERCH_GEMM_TRAFFIC = 2591011232
+# The fused kernel's launch below (24 -> 144 expansion into the 3 x 3 stride-2 depthwise, 249 x 63 -> 125 x 32 pixels,
+# 256 windows), from rocprofv3 --pmc runs of this bench (profiles/k_pwdw_f32_24to144_dw3s2_249x63_b256.md): HBM bytes
+# per launch (FETCH_SIZE x 2 + WRITE_SIZE, the copy-kernel calibration) and the VALU issue share (SQ_INSTS_VALU x 4
+# cycles per wave64 instruction on a 16-lane SIMD over the launch's SIMD-cycles at 2.4 GHz)
+PERCH_PWDW_TRAFFIC = 774989248
+PERCH_PWDW_VALU_BUSY = 0.92
+
+
+def perch_pairs(net):
+    """The (PW_S8 expansion, depthwise) op pairs the runtime fuses into k_pwdw_f32: a PW_S8 with a zero-haloed output
+    that the next op, a DW3 / DWK, reads."""
+    out = []
+    for x, y in zip(net.ops, net.ops[1:]):
+        if x[0] & 0xff == 22 and x[3][9] > 0 and y[0] & 0xff in (4, 10) and y[1][0] == x[1][1]:
+            out.append((x, y))
+    return out
 
 
 def perch_roofline(H, pn, B, stream, a):
-    """The dominant kernel of the net is the int8 pointwise GEMM with its dequant + SiLU epilogue (k_s8n_gemm, the
-    largest share of the step); its largest launch, the 24 -> 144 expansion over 249 x 63 pixels into a halo-1
-    buffer, is replayed with the net's own weights and shape on `stream` and timed with events. Algorithmic bytes
-    per launch: the int8 rows read (B x M x Kp), the fp32 outputs written (B x M x N x 4) and the weights."""
-    from bnneon import s8pack
-    _, big = perch_counts(pn.net)
-    code, b, t, p = big
-    N, K, Kp, Np, M, lda, act, ldo, ow, opad, ldr = p
+    """The dominant kernel of the net is the int8 expansion fused into its depthwise conv (k_pwdw_f32, the largest
+    share of the step); its largest launch, block 2's 24 -> 144 expansion into the 3 x 3 stride-2 depthwise over
+    249 x 63 pixels, is replayed with the net's own weights and shape on `stream` and timed with events. Algorithmic
+    bytes per launch: the int8 rows and their scales and zero points read (B x M x (Kp + 8)), the depthwise outputs
+    written (B x Ho x Wo x C x 4) and the weights. The kernel recomputes the expansion instead of storing it, so it
+    is bound by VALU issue (dequantisation and the exact SiLU of every expanded value), not by HBM: valu_busy is the
+    measured share of the SIMDs' issue cycles its VALU instructions take."""
+    # the launch with the most expansion work: pixels x expanded channels
+    (pc, pbf, ptn, pp), (dc, dbf, dtn, dp) = max(perch_pairs(pn.net), key=lambda pr: pr[0][3][4] * pr[0][3][0])
+    N, K, Kp, Np, M, lda, act, ldo, ow, opad, ldr = pp
+    if dc & 0xff == 4:  # DW3: H W C s Ho Wo, pads 1, SiLU
+        Hh, Wd, C, s, Ho, Wo = dp[:6]
+        k, pt, pl, form, dact = 3, 1, 1, 2, 1
+    else:               # DWK: H W C k s pt pl Ho Wo act
+        Hh, Wd, C, k, s, pt, pl, Ho, Wo, dact = dp
+        form = 0
     T = [arr for (_, arr, _) in pn.pkg.tensors]
-    Wt = H.S8Weights(N, K, Kp, Np, T[t[0]], T[t[1]], T[t[2]], T[t[3]])
+    Wt = H.S8Weights(N, K, Kp, Np, T[ptn[0]], T[ptn[1]], T[ptn[2]], T[ptn[3]])
+    dw = H.DeviceArray.from_host(np.asarray(T[dtn[0]], np.float32))
+    db = H.DeviceArray.from_host(np.asarray(T[dtn[1]], np.float32))
     rng = np.random.default_rng(5)
     dq = H.DeviceArray.from_host(rng.integers(-127, 128, (B, M * Kp)).astype(np.int8))
     dsa = H.DeviceArray.from_host(rng.uniform(0.005, 0.02, (B, M)).astype(np.float32))
     dza = H.DeviceArray.from_host(rng.integers(-20, 20, (B, M)).astype(np.int32))
-    Hh = M // ow if opad else M
-    rows = (Hh + 2 * opad) * (ow + 2 * opad) if opad else M
-    dout = H.DeviceArray.zeros((B, rows * ldo), np.float32)
-    e = H.epi32(dout, ldo, act=act, out_ws=rows * ldo, ow=ow if opad else 0, opad=opad)
+    o_ws = Ho * Wo * C
+    dout = H.DeviceArray.zeros((B, o_ws), np.float32)
 
     def launch():
-        H.check(H.lib().bnh_s8n_gemm(dq.ptr, M * Kp, dsa.ptr, M, dza.ptr, M, M, B, Wt.h, e, stream))
+        H.check(H.lib().bnh_pwdw_f32(dq.ptr, M * Kp, dsa.ptr, M, dza.ptr, M, Hh, Wd, Wt.h, act, k, s, pt, pl, form,
+                                     dw.ptr, db.ptr, dact, dout.ptr, o_ws, Ho, Wo, None, 0, B, stream), "pwdw_f32")
     ms, _ = time_steps(H, stream, launch, max(10, a.steps), 3)
-    nbytes = B * M * Kp + B * M * N * 4 + Np * Kp + 12 * Np
+    nbytes = B * M * (Kp + 8) + B * o_ws * 4 + Np * Kp + 12 * Np + (k * k + 1) * C * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": PERCH_GEMM_TRAFFIC,
-            "kernel": "k_s8n_gemm",
-            "launch": f"PW_S8 GEMM {K}->{N} over {M} px x {B} windows, SiLU, halo-{opad} output",
-            "ms_per_launch": round(ms, 4), "algorithmic_bytes_per_launch": nbytes}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": PERCH_PWDW_TRAFFIC,
+            "kernel": "k_pwdw_f32",
+            "launch": f"PW_S8 {K}->{N} expansion fused into the {k}x{k}/{s} depthwise, {Hh}x{Wd} -> {Ho}x{Wo} px "
+                      f"x {B} windows",
+            "ms_per_launch": round(ms, 4), "algorithmic_bytes_per_launch": nbytes,
+            "limiter": "VALU issue", "valu_busy": PERCH_PWDW_VALU_BUSY}
 
 
 def v24_counts(net):
