@@ -564,42 +564,53 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
   }
   // Two sub-batches on two streams, their launches interleaved op by op: the windows are independent, so the GPU
   // may run one half's kernel beside the other half's (a latency-bound kernel beside a bandwidth-bound one). The
-  // second stream starts after everything the caller's stream holds and the caller's stream waits for it at the end.
+  // second stream starts after everything the caller's stream holds (and the first half's first op) and the
+  // caller's stream waits for it at the end.
   const int split = !c->prof && !c->one_stream && B >= 64 && ensure_stream2(c) ? 1 : 0;
   const int B1 = split ? (B + 1) / 2 : B;
   hipStream_t s1 = c->stream;
-  if (split && (hipEventRecord(c->ev_fork, s1) != hipSuccess || hipStreamWaitEvent(c->stream2, c->ev_fork, 0) != hipSuccess)) {
+  // the second half runs one op behind the first, so that kernels of different kinds (a VALU-bound one beside a
+  // memory-bound one) run side by side more often than two copies of the same kernel (measured: 1.5-1.7 % faster
+  // than no skew on both nets, slower from 4 ops of skew up)
+  const int skew = split ? 1 : 0;
+  auto fork = [&]() {
+    return hipEventRecord(c->ev_fork, s1) == hipSuccess && hipStreamWaitEvent(c->stream2, c->ev_fork, 0) == hipSuccess;
+  };
+  if (split && skew == 0 && !fork()) {
     snprintf(err, errlen, "device error forking the second stream");
     return -1;
   }
   double t0 = c->prof ? now_s() : 0;
-  for (int i = 0; i < c->n_ops; i++) {
-    rt_op *op = &c->ops[i];
-    c->fail_op = i;  // ops read it to tag the windows they fail
-    int r = 0;
-    for (int h = 0; h <= split && !r; h++) {
+  // step t runs the first half's op t and the second half's op t - skew
+  for (int t = 0; t < c->n_ops + skew; t++) {
+    for (int h = 0; h <= split; h++) {
+      const int i = h ? t - skew : t;
+      if (i < 0 || i >= c->n_ops) continue;
+      rt_op *op = &c->ops[i];
+      c->fail_op = i;  // ops read it to tag the windows they fail
       c->w0 = h ? B1 : 0;
       c->nwin = h ? B - B1 : B1;
       c->stream = h ? c->stream2 : s1;
-      r = op->k->run(c, op);
-    }
-    c->w0 = 0;
-    c->nwin = B;
-    c->stream = s1;
-    if (r) {
-      if (split) hipStreamSynchronize(c->stream2);  // leave no launch of this batch in flight
-      char src[160];
-      rt_op_src(c, i, src, sizeof src);
-      const char *why = bnh_last_error();
-      snprintf(err, errlen, "op %d %s%s%s%s: launch failed (%s)", i, op->k->name, src[0] ? " (ONNX node " : "", src,
-               src[0] ? ")" : "", why && why[0] ? why : hipGetErrorString(hipGetLastError()));
-      return -1;
-    }
-    if (c->prof) {
-      hipStreamSynchronize(c->stream);
-      double t = now_s();
-      c->t_op[i] += t - t0;
-      t0 = t;
+      int r = op->k->run(c, op);
+      c->w0 = 0;
+      c->nwin = B;
+      c->stream = s1;
+      if (!r && split && !h && skew && i == skew - 1 && !fork()) r = -1;
+      if (r) {
+        if (split) hipStreamSynchronize(c->stream2);  // leave no launch of this batch in flight
+        char src[160];
+        rt_op_src(c, i, src, sizeof src);
+        const char *why = bnh_last_error();
+        snprintf(err, errlen, "op %d %s%s%s%s: launch failed (%s)", i, op->k->name, src[0] ? " (ONNX node " : "", src,
+                 src[0] ? ")" : "", why && why[0] ? why : hipGetErrorString(hipGetLastError()));
+        return -1;
+      }
+      if (c->prof) {
+        hipStreamSynchronize(c->stream);
+        double tn = now_s();
+        c->t_op[i] += tn - t0;
+        t0 = tn;
+      }
     }
   }
   c->fail_op = -1;
