@@ -35,6 +35,7 @@ typedef struct {
 
 struct rt_pkg;
 struct rt_ctx;
+#define RT_MAXSUB 4  // sub-batches of a run
 
 typedef struct rt_op {
   uint16_t code, nb, nt, ni;
@@ -81,8 +82,11 @@ struct rt_ctx {
   int nwin;              // windows of the current run (<= bcap): ops launch for this many
   int w0;                // the first of them (a sub-batch of the run starts past window 0)
   size_t *wsb;           // per buffer: bytes between windows
-  hipStream_t stream2;   // the second sub-batch's stream (created on first use; default priority)
-  hipEvent_t ev_fork, ev_join;
+  // sub-batches 1 .. RT_MAXSUB - 1: their streams (created on first use; default priority) and the events that start
+  // them (fork) and that the context's stream waits for (join); sub-batch 0 runs on `stream`
+  hipStream_t sub_stream[RT_MAXSUB];
+  hipEvent_t sub_fork[RT_MAXSUB], sub_join[RT_MAXSUB];
+  int n_sub;             // sub-batch streams created, including the context's own
   int one_stream;        // never split a batch over two streams
   size_t *slot_bytes;    // per slot: bytes of one window's copy (64-aligned, >= 64 bytes of zero slack)
   int *slot_users;       // per slot: the number of buffers placed in it

@@ -538,22 +538,26 @@ static double now_s(void) {
   return t.tv_sec + t.tv_nsec * 1e-9;
 }
 
-// the second stream and the fork / join events, created once (0 when the runtime refuses them: one stream then)
-static int ensure_stream2(rt_ctx *c) {
-  if (c->stream2) return 1;
-  hipStream_t s = nullptr;
-  hipEvent_t a = nullptr, b = nullptr;
-  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return 0;
-  if (hipEventCreateWithFlags(&a, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess) {
-    if (a) hipEventDestroy(a);
-    hipStreamDestroy(s);
-    return 0;
+// the streams and fork / join events of sub-batches 1 .. n - 1, created once (fewer when the runtime refuses them)
+static int ensure_subs(rt_ctx *c, int n) {
+  if (c->n_sub == 0) c->n_sub = 1;
+  while (c->n_sub < n) {
+    const int h = c->n_sub;
+    hipStream_t s = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) break;
+    if (hipEventCreateWithFlags(&a, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess) {
+      if (a) hipEventDestroy(a);
+      hipStreamDestroy(s);
+      break;
+    }
+    c->sub_stream[h] = s;
+    c->sub_fork[h] = a;
+    c->sub_join[h] = b;
+    c->n_sub = h + 1;
   }
-  c->stream2 = s;
-  c->ev_fork = a;
-  c->ev_join = b;
-  return 1;
+  return c->n_sub < n ? c->n_sub : n;
 }
 
 int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
@@ -562,42 +566,48 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
     snprintf(err, errlen, "device error clearing the window flags");
     return -1;
   }
-  // Two sub-batches on two streams, their launches interleaved op by op: the windows are independent, so the GPU
-  // may run one half's kernel beside the other half's (a latency-bound kernel beside a bandwidth-bound one). The
-  // second stream starts after everything the caller's stream holds (and the first half's first op) and the
-  // caller's stream waits for it at the end.
-  const int split = !c->prof && !c->one_stream && B >= 64 && ensure_stream2(c) ? 1 : 0;
-  const int B1 = split ? (B + 1) / 2 : B;
+  // Sub-batches on their own streams, their launches interleaved op by op: the windows are independent, so the GPU
+  // may run one sub-batch's kernel beside another's (a VALU-bound kernel beside a memory-bound one). Sub-batch h
+  // runs one op behind sub-batch h - 1 (it starts after that one's first op, and so after everything the context's
+  // stream held), so that kernels of different kinds meet more often than copies of the same kernel; the context's
+  // stream waits for every sub-batch at the end.
+  // two sub-batches (measured: three or four, on as many streams, are 15-25 % slower on both nets; one op of skew is
+  // 1.5-1.7 % faster than none, four or more slower)
+  int ns = 2;
+  if (c->prof || c->one_stream || B < 64) ns = 1;
+  if (ns > RT_MAXSUB) ns = RT_MAXSUB;
+  while (ns > 1 && B / ns < 32) ns--;  // sub-batches of at least 32 windows
+  if (ns > 1) ns = ensure_subs(c, ns);
   hipStream_t s1 = c->stream;
-  // the second half runs one op behind the first, so that kernels of different kinds (a VALU-bound one beside a
-  // memory-bound one) run side by side more often than two copies of the same kernel (measured: 1.5-1.7 % faster
-  // than no skew on both nets, slower from 4 ops of skew up)
-  const int skew = split ? 1 : 0;
-  auto fork = [&]() {
-    return hipEventRecord(c->ev_fork, s1) == hipSuccess && hipStreamWaitEvent(c->stream2, c->ev_fork, 0) == hipSuccess;
+  const int skew = 1;
+  auto first = [&](int h) { return (int)((long long)B * h / ns); };
+  auto strm = [&](int h) { return h ? c->sub_stream[h] : s1; };
+  auto drain = [&]() {
+    for (int h = 1; h < ns; h++) hipStreamSynchronize(c->sub_stream[h]);
   };
-  if (split && skew == 0 && !fork()) {
-    snprintf(err, errlen, "device error forking the second stream");
-    return -1;
-  }
   double t0 = c->prof ? now_s() : 0;
-  // step t runs the first half's op t and the second half's op t - skew
-  for (int t = 0; t < c->n_ops + skew; t++) {
-    for (int h = 0; h <= split; h++) {
-      const int i = h ? t - skew : t;
+  // step t runs sub-batch h's op t - h skew
+  for (int t = 0; t < c->n_ops + (ns - 1) * skew; t++) {
+    for (int h = 0; h < ns; h++) {
+      const int i = t - h * skew;
       if (i < 0 || i >= c->n_ops) continue;
       rt_op *op = &c->ops[i];
+      if (h && i == 0 && hipStreamWaitEvent(c->sub_stream[h], c->sub_fork[h], 0) != hipSuccess) {
+        drain();
+        snprintf(err, errlen, "device error starting sub-batch %d", h);
+        return -1;
+      }
       c->fail_op = i;  // ops read it to tag the windows they fail
-      c->w0 = h ? B1 : 0;
-      c->nwin = h ? B - B1 : B1;
-      c->stream = h ? c->stream2 : s1;
+      c->w0 = first(h);
+      c->nwin = first(h + 1) - first(h);
+      c->stream = strm(h);
       int r = op->k->run(c, op);
       c->w0 = 0;
       c->nwin = B;
       c->stream = s1;
-      if (!r && split && !h && skew && i == skew - 1 && !fork()) r = -1;
+      if (!r && h + 1 < ns && i == skew - 1 && hipEventRecord(c->sub_fork[h + 1], strm(h)) != hipSuccess) r = -1;
       if (r) {
-        if (split) hipStreamSynchronize(c->stream2);  // leave no launch of this batch in flight
+        drain();  // leave no launch of this batch in flight
         char src[160];
         rt_op_src(c, i, src, sizeof src);
         const char *why = bnh_last_error();
@@ -613,12 +623,14 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
       }
     }
   }
+  for (int h = 1; h < ns; h++)
+    if (hipEventRecord(c->sub_join[h], c->sub_stream[h]) != hipSuccess ||
+        hipStreamWaitEvent(s1, c->sub_join[h], 0) != hipSuccess) {
+      drain();
+      snprintf(err, errlen, "device error joining sub-batch %d", h);
+      return -1;
+    }
   c->fail_op = -1;
-  if (split && (hipEventRecord(c->ev_join, c->stream2) != hipSuccess || hipStreamWaitEvent(s1, c->ev_join, 0) != hipSuccess)) {
-    hipStreamSynchronize(c->stream2);
-    snprintf(err, errlen, "device error joining the second stream");
-    return -1;
-  }
   hipError_t e = hipMemcpyAsync(status, c->win_fail, sizeof(int) * (size_t)B, hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) { snprintf(err, errlen, "device error after the op list: %s", hipGetErrorString(e)); return -1; }
@@ -668,11 +680,11 @@ void rt_ctx_free(rt_ctx *c) {
   free(c->slot_users);
   free(c->bufd);
   if (c->stream && c->own_stream) hipStreamDestroy(c->stream);
-  if (c->stream2) {
-    hipStreamSynchronize(c->stream2);
-    hipStreamDestroy(c->stream2);
+  for (int h = 1; h < c->n_sub; h++) {
+    hipStreamSynchronize(c->sub_stream[h]);
+    hipStreamDestroy(c->sub_stream[h]);
+    hipEventDestroy(c->sub_fork[h]);
+    hipEventDestroy(c->sub_join[h]);
   }
-  if (c->ev_fork) hipEventDestroy(c->ev_fork);
-  if (c->ev_join) hipEventDestroy(c->ev_join);
   free(c);
 }
