@@ -637,6 +637,86 @@ __global__ __launch_bounds__(256) void k_chsum(const T *__restrict__ out, long l
   if (wave == 0 && lane < S) chsum[win * cs_ws + c0 + lane] = cs;
 }
 
+// fp32 channel sums, wave-private form (FORM 0 / 2, Wo <= 64): a wave owns 16 channels of one window and walks its
+// image rows in order. Lane l loads the 16 channels' float4 quad (l & 3) of pixels 16 i + (l >> 2); 8 rows of those
+// loads stay in flight in a register ring, so the wave keeps 8 x Wo x 64 bytes on the way (no LDS double buffer
+// bounds it). A row that has landed goes through a wave-private LDS row [Wo][16], from which lanes 0..15 (one per
+// channel) add the row's terms to their running sums in the reference's order: DW3 every pixel, DWK each 4-pixel
+// group as (o0 + o1) + (o2 + o3), then the tail pixels. No block barrier: a wave's LDS writes and reads are in order.
+template <int FORM, int NI>
+__global__ __launch_bounds__(256) void k_chsum_w(const float *__restrict__ out, long long o_ws, int C, int Ho, int Wo,
+                                                 float *__restrict__ chsum, long long cs_ws) {
+  constexpr int NR = 8;  // rows in flight (the ring's loop is unrolled: longer rings land in scratch memory)
+  __shared__ float rowb[4][64 * 16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, win = blockIdx.y;
+  const int c0 = blockIdx.x * 64 + wave * 16;
+  if (c0 >= C) return;
+  const int nc = C - c0 < 16 ? C - c0 : 16;  // a multiple of 4
+  const int p16 = lane >> 2, cq = lane & 3;
+  // every lane loads (no branch, so the loads' counters stay exact and the ring stays in flight): rows past the image,
+  // pixels past the row and quads past the channels read a valid address whose value no sum uses
+  const float *img = out + win * o_ws + c0;  // wave-uniform
+  int lofs[NI];                              // per lane: pixel 16 i + (l >> 2), quad (l & 3), in floats
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int px = 16 * i + p16;
+    lofs[i] = (px < Wo ? px : Wo - 1) * C + 4 * (4 * cq < nc ? cq : 0);
+  }
+  float *rb = rowb[wave];
+  float4 v[NR][NI];
+  auto rowp = [&](int y) { return img + (long long)(y < Ho ? y : Ho - 1) * Wo * C; };  // wave-uniform
+#pragma unroll
+  for (int s = 0; s < NR; s++) {
+    const float *rp = rowp(s);
+#pragma unroll
+    for (int i = 0; i < NI; i++)  // (the select keeps the compiler from placing the ring in scratch memory)
+      v[s][i] = s < Ho ? *(const float4 *)(rp + lofs[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const int g4 = Wo & ~3;
+  float cs = 0.f;
+  for (int y0 = 0; y0 < Ho; y0 += NR) {
+#pragma unroll
+    for (int s = 0; s < NR; s++) {
+      const int y = y0 + s;
+      if (y >= Ho) break;
+#pragma unroll
+      for (int i = 0; i < NI; i++) *(float4 *)(rb + (16 * i + p16) * 16 + 4 * cq) = v[s][i];  // px < 64: in the row
+      {  // the ring slot's next row
+        const float *rp = rowp(y + NR);
+#pragma unroll
+        for (int i = 0; i < NI; i++) v[s][i] = *(const float4 *)(rp + lofs[i]);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (lane < nc) {
+        const float *col = rb + lane;
+        if (FORM == 2) {
+          int x = 0;
+          for (; x + 16 <= Wo; x += 16) {  // sixteen LDS reads in flight, then the sixteen dependent adds in order
+            float t[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) t[u] = col[(x + u) * 16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) cs = cs + t[u];
+          }
+          for (; x < Wo; x++) cs = cs + col[x * 16];
+        } else {
+          for (int x = 0; x < g4; x += 4) {
+            const float a = col[x * 16], b = col[(x + 1) * 16], c2 = col[(x + 2) * 16], d = col[(x + 3) * 16];
+            cs = cs + ((a + b) + (c2 + d));
+          }
+          for (int x = g4; x < Wo; x++) cs = cs + col[x * 16];
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+  if (lane < nc) chsum[win * cs_ws + c0 + lane] = cs;
+}
+
 // rows per chunk: two buffers of at most `cap` floats
 static int chsum_rows(int Tn, int S, int Ho, int cap) {
   int R = cap / (Tn * S);
@@ -705,6 +785,19 @@ static int chsum_launch(const T *out, long long o_ws, int C, int Ho, int Wo, flo
                          (const h16 *)out, o_ws, C, Ho, Wo, FORM, chsum, cs_ws, B);
     BNH_HIP(hipGetLastError());
     return 0;
+  }
+  // fp32 sums over rows of at most 64 pixels: the wave-private form, from 33 channels up (with fewer, two waves per
+  // window keep too little in flight: 24 channels of 249 x 63 pixels take 233 us there against 160 us below)
+  if constexpr (sizeof(T) == 4 && (FORM == 0 || FORM == 2)) {
+    if (Wo <= 64 && C > 32) {
+      const dim3 grid((unsigned)bnh_ceil_div(C, 64), (unsigned)B);
+      const float *o = (const float *)out;
+      if (Wo <= 16) hipLaunchKernelGGL((k_chsum_w<FORM, 1>), grid, dim3(256), 0, st, o, o_ws, C, Ho, Wo, chsum, cs_ws);
+      else if (Wo <= 32) hipLaunchKernelGGL((k_chsum_w<FORM, 2>), grid, dim3(256), 0, st, o, o_ws, C, Ho, Wo, chsum, cs_ws);
+      else hipLaunchKernelGGL((k_chsum_w<FORM, 4>), grid, dim3(256), 0, st, o, o_ws, C, Ho, Wo, chsum, cs_ws);
+      BNH_HIP(hipGetLastError());
+      return 0;
+    }
   }
   // a block's chunk is one memory round trip of its loading waves: with at most one block per CU (no more blocks
   // than 2 per CU in the launch) the chunks take up to 144 KB of LDS, else 64 KB so that several blocks share a CU
