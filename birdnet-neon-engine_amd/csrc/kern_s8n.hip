@@ -138,16 +138,32 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
   // extremes (the sign of a zero extreme changes no later result); fminf / fmaxf plus a NaN flag give the same
   float lo = __builtin_inff(), hi = -__builtin_inff();
   int nan = 0;
-  for (int c = sub; c < n4; c += L) {
+  // the lane's first QC chunks (all of them when L < 64: 16 L >= Kp) stay in registers for the quantization pass,
+  // the gate already applied; chunks past them (L = 64, Kp > 1024) are read again there
+  constexpr int QC = 4;
+  float4 cv[QC];
+  auto chunk = [&](int c) {
     float4 v = *(const float4 *)(r + 4 * c);
     if (g) {
       const float4 gv = *(const float4 *)(g + 4 * c);
       v.x = v.x * gv.x; v.y = v.y * gv.y; v.z = v.z * gv.z; v.w = v.w * gv.w;
     }
+    return v;
+  };
+  auto minmax = [&](const float4 &v) {
     nan |= (v.x != v.x) | (v.y != v.y) | (v.z != v.z) | (v.w != v.w);
     lo = __builtin_fminf(__builtin_fminf(lo, v.x), __builtin_fminf(v.y, __builtin_fminf(v.z, v.w)));
     hi = __builtin_fmaxf(__builtin_fmaxf(hi, v.x), __builtin_fmaxf(v.y, __builtin_fmaxf(v.z, v.w)));
+  };
+#pragma unroll
+  for (int j = 0; j < QC; j++) {
+    const int c = sub + j * L;
+    if (c < n4) cv[j] = chunk(c);  // every load first, then the reductions
   }
+#pragma unroll
+  for (int j = 0; j < QC; j++)
+    if (sub + j * L < n4) minmax(cv[j]);
+  for (int c = sub + QC * L; c < n4; c += L) minmax(chunk(c));
 #pragma unroll
   for (int off = L / 2; off; off >>= 1) {
     lo = __builtin_fminf(lo, __shfl_xor(lo, off));
@@ -184,43 +200,43 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
   const bool fast = !nan && __builtin_fmaxf(__builtin_fabsf(lo), __builtin_fabsf(hi)) * inv < 1073741824.f;
   int8_t *o = q + w * q_ws + (long long)m * Kp;
   const uint32_t zb = (uint32_t)z & 0xffu;
-  for (int c = sub; c < Kp / 4; c += L) {
+#pragma unroll
+  for (int j = 0; j < QC + 1; j++) {  // j < QC: chunk sub + j L from registers; j = QC: the chunks past them
+   for (int c = sub + j * L; c < Kp / 4; c += L) {
     const int k0 = 4 * c;
     float v[4];
     if (k0 + 4 <= K4) {
-      float4 t = *(const float4 *)(r + k0);
-      if (g) {
-        const float4 gv = *(const float4 *)(g + k0);
-        t.x = t.x * gv.x; t.y = t.y * gv.y; t.z = t.z * gv.z; t.w = t.w * gv.w;
-      }
+      const float4 t = j < QC ? cv[j] : chunk(c);
       v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int k = k0 + j;
-        v[j] = 0.f;
+      for (int jj = 0; jj < 4; jj++) {
+        const int k = k0 + jj;
+        v[jj] = 0.f;
         if (k < K) {
-          v[j] = r[k];
-          if (g) v[j] = v[j] * g[k];
+          v[jj] = r[k];
+          if (g) v[jj] = v[jj] * g[k];
         }
       }
     }
     uint32_t word = 0;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int k = k0 + j;
+    for (int jj = 0; jj < 4; jj++) {
+      const int k = k0 + jj;
       uint32_t byte = zb;
       if (k < K) {
-        const float t = v[j] * inv;
+        const float t = v[jj] * inv;
         int32_t cq;
         if (fast) cq = (int32_t)__builtin_rintf(t) + z;
         else cq = (int32_t)((uint32_t)(k < K8 ? bnh_cvtn_s32(t) : bnh_lrintf_s32(t)) + (uint32_t)z);
         cq = cq < -127 ? -127 : cq > 127 ? 127 : cq;
         byte = (uint32_t)cq & 0xffu;
       }
-      word |= byte << (8 * j);
+      word |= byte << (8 * jj);
     }
     *(uint32_t *)(o + k0) = word;
+    if (j < QC) break;  // one chunk per register slot
+   }
   }
 }
 
