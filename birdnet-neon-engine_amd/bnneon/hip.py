@@ -77,6 +77,8 @@ _SIGS = {
     "bnh_gemm_f16_body": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp]),
     "bnh_gemm_f16_ws_bytes": (C.c_size_t, [i32, i32, vp]),
     "bnh_gemm_f16_ws": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp, C.c_size_t, vp]),
+    "bnh_gemm_f16_gated_ws": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp, i64, vp, C.c_size_t,
+                                    vp]),
     "bnh_wino16_new": (vp, [i32, i32, vp, vp]),
     "bnh_wino16_free": (None, [vp]),
     "bnh_wino_f16": (i32, [vp, i64, i32, i32, i32, vp, i32, vp, i64, i32, i32, vp, i64, i32, i32, i32, vp]),
@@ -111,6 +113,7 @@ _SIGS = {
     "bnh_stem_f32to16": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32,
                                i32, vp]),
     "bnh_se_f16": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, vp]),
+    "bnh_se_gate_f16": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, vp]),
     "bnh_mean_f16": (i32, [vp, i64, i32, i32, i32, vp, i64, i32, vp]),
     "bnh_gemv": (i32, [vp, i32, vp, i32, i32, vp, i64, i32, vp, i64, i32, vp]),
 }

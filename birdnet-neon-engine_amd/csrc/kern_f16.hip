@@ -112,16 +112,19 @@ __global__ __launch_bounds__(256) void k_gemm_f16(const uint16_t *__restrict__ A
 #define FE_AS 17   // A row stride in dwords (34 halves)
 #define FE_BM 256  // rows per block at most
 
-template <bool VEC, bool RES>
+// GATE: A's columns are multiplied by the window's fp16 gates gh [K] as they are staged (the fp16 SE's in-place
+// scaling of A, src/rt_ops_f32.c:256-327, done in the A-load: the same fp16 products, no pass over A)
+template <bool VEC, bool RES, bool GATE>
 __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ A, long long a_ws, int lda, int M,
                                                    double rM, long long rows, const uint16_t *__restrict__ wk, int Ntp,
                                                    const float *__restrict__ b32, const uint16_t *__restrict__ b16,
                                                    int Kp, int Np, int bs, int TC, Epi16Dev e,
+                                                   const uint16_t *__restrict__ gh, long long gh_ws,
                                                    uint16_t *__restrict__ part, int nsplit) {
   const int TR = 256 / TC < 64 ? 256 / TC : 64, BM = 4 * TR, TN = 8 * TC;
   __shared__ __attribute__((aligned(16))) uint32_t As[FE_BM * FE_AS];
   __shared__ __attribute__((aligned(16))) uint4 Ws[FE_KC * 16];
-  __shared__ long long s_a[FE_BM], s_o[FE_BM], s_r[FE_BM];
+  __shared__ long long s_a[FE_BM], s_o[FE_BM], s_r[FE_BM], s_g[GATE ? FE_BM : 1];
   __shared__ uint32_t s_t01[16];
   __shared__ uint16_t s_t2[16];
   const int tid = threadIdx.x, tc = tid % TC, tr = tid / TC;
@@ -146,6 +149,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
     }
     s_o[i] = w * e.out_ws + orow * e.ldo;
     s_r[i] = w * e.res_ws + (long long)m * e.ldr;
+    if (GATE) s_g[i] = w * gh_ws;
   }
   if (tid < 16) {
     s_t01[tid] = (uint32_t)k_silu_c0[tid] | ((uint32_t)k_silu_c1[tid] << 16);
@@ -153,13 +157,14 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
   }
   __syncthreads();
   // chunk loader: A rows [BM][kn] and W rows [kn][TN] of k0 into registers (kn a multiple of 8)
-  uint4 ra[FE_BM * FE_KC / 8 / 256], rw[2];
+  uint4 ra[FE_BM * FE_KC / 8 / 256], rw[2], rg[GATE ? FE_BM * FE_KC / 8 / 256 : 1];
   const int nav = BM * (FE_KC / 8), nwv = FE_KC * TC;
   auto load = [&](int k0, int kn) {
 #pragma unroll
     for (int j = 0; j < FE_BM * FE_KC / 8 / 256; j++) {
       const int i = tid + 256 * j, r = i / (FE_KC / 8), kc = (i % (FE_KC / 8)) * 8;
       ra[j] = i < nav && kc < kn ? *(const uint4 *)(A + s_a[r] + k0 + kc) : make_uint4(0, 0, 0, 0);
+      if (GATE) rg[j] = i < nav && kc < kn ? *(const uint4 *)(gh + s_g[r] + k0 + kc) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
@@ -174,7 +179,14 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
       const int i = tid + 256 * j, r = i / (FE_KC / 8), kc = (i % (FE_KC / 8)) * 8;
       if (i < nav) {
         uint32_t *d = As + r * FE_AS + kc / 2;
-        d[0] = ra[j].x; d[1] = ra[j].y; d[2] = ra[j].z; d[3] = ra[j].w;
+        if (GATE) {  // a x gate, two columns at a time (IEEE fp16 products)
+          const uint32_t av[4] = {ra[j].x, ra[j].y, ra[j].z, ra[j].w}, gv[4] = {rg[j].x, rg[j].y, rg[j].z, rg[j].w};
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+            d[u] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, av[u]) * __builtin_bit_cast(h2, gv[u]));
+        } else {
+          d[0] = ra[j].x; d[1] = ra[j].y; d[2] = ra[j].z; d[3] = ra[j].w;
+        }
       }
     }
 #pragma unroll
@@ -456,9 +468,11 @@ size_t bnh_gemm_f16_ws_bytes(int M, int B, const bnh_h16w *W) {
   return nblk > 1 ? (size_t)nblk * M * B * W->Np * 2 : 0;
 }
 
-int bnh_gemm_f16_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
-                    void *ws, size_t ws_bytes, void *stream) {
+static int gemm_f16e_run(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W,
+                         const bnh_epi16 *e, const uint16_t *gh, long long gh_ws, void *ws, size_t ws_bytes,
+                         void *stream) {
   if (gemm_f16_check(A, a_ws, lda, M, B, W, e)) return -1;
+  BNH_REQ(!gh || (((uintptr_t)gh & 15) == 0 && (B == 1 || (gh_ws >= W->Kp && gh_ws % 8 == 0))));
   BNH_REQ(!ws || ((uintptr_t)ws & 15) == 0);
   const long long rows = (long long)M * B;
   Epi16Dev d = {e->act, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->res, e->res_ws, e->ldr};
@@ -478,15 +492,19 @@ int bnh_gemm_f16_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, co
   BNH_REQ(nb * nsplit < (1LL << 31) && rows * np8 < (1LL << 40));
   const dim3 grid((unsigned)(nb * nsplit));
   hipStream_t st = bnh_stream(stream);
-  if (vec && e->res && !split)
-    hipLaunchKernelGGL((k_gemm_f16e<true, true>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt,
-                       W->b, W->b16, W->Kp, W->Np, bs, tc, d, part, nsplit);
-  else if (vec)
-    hipLaunchKernelGGL((k_gemm_f16e<true, false>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk,
-                       W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d, part, nsplit);
-  else
-    hipLaunchKernelGGL((k_gemm_f16e<false, false>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk,
-                       W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d, part, nsplit);
+#define GEMM_F16E(V_, R_, G_)                                                                                          \
+  hipLaunchKernelGGL((k_gemm_f16e<V_, R_, G_>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt,  \
+                     W->b, W->b16, W->Kp, W->Np, bs, tc, d, gh, gh_ws, part, nsplit)
+  if (gh) {
+    if (vec && e->res && !split) GEMM_F16E(true, true, true);
+    else if (vec) GEMM_F16E(true, false, true);
+    else GEMM_F16E(false, false, true);
+  } else {
+    if (vec && e->res && !split) GEMM_F16E(true, true, false);
+    else if (vec) GEMM_F16E(true, false, false);
+    else GEMM_F16E(false, false, false);
+  }
+#undef GEMM_F16E
   BNH_HIP(hipGetLastError());
   if (split) {
     const dim3 g2((unsigned)bnh_ceil_div(rows * np8, 256));
@@ -497,6 +515,18 @@ int bnh_gemm_f16_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, co
     BNH_HIP(hipGetLastError());
   }
   return 0;
+}
+
+int bnh_gemm_f16_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
+                    void *ws, size_t ws_bytes, void *stream) {
+  return gemm_f16e_run(A, a_ws, lda, M, B, W, e, nullptr, 0, ws, ws_bytes, stream);
+}
+
+int bnh_gemm_f16_gated_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W,
+                          const bnh_epi16 *e, const uint16_t *gh, long long gh_ws, void *ws, size_t ws_bytes,
+                          void *stream) {
+  BNH_REQ(gh);
+  return gemm_f16e_run(A, a_ws, lda, M, B, W, e, gh, gh_ws, ws, ws_bytes, stream);
 }
 
 int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,

@@ -194,7 +194,8 @@ __global__ __launch_bounds__(256) void k_se_fc1(const float *__restrict__ chsum,
 template <int WB, bool F16>
 __global__ __launch_bounds__(256) void k_se_fc2(const float *__restrict__ s1, int C, int rd,
                                                 const float *__restrict__ w2t, const float *__restrict__ b2,
-                                                float *__restrict__ gate, long long g_ws, int B) {
+                                                float *__restrict__ gate, long long g_ws, int B,
+                                                uint16_t *__restrict__ gh, long long gh_ws) {
   extern __shared__ float ss[];  // [WB][rd]
   const int win0 = blockIdx.y * WB, nw = B - win0 < WB ? B - win0 : WB, tid = threadIdx.x;
   for (int i = tid; i < WB * rd; i += 256) ss[i] = i / rd < nw ? s1[(long long)win0 * rd + i] : 0.f;
@@ -213,7 +214,11 @@ __global__ __launch_bounds__(256) void k_se_fc2(const float *__restrict__ s1, in
   }
 #pragma unroll
   for (int wg = 0; wg < WB; wg++)
-    if (wg < nw) gate[(win0 + wg) * g_ws + c] = se_sigmoid<F16>(a[wg]);
+    if (wg < nw) {
+      const float gv = se_sigmoid<F16>(a[wg]);
+      gate[(win0 + wg) * g_ws + c] = gv;
+      if (gh) gh[(win0 + wg) * gh_ws + c] = hbits(f2h(gv));  // the fp16 gate the scaling multiplies by
+    }
 }
 
 // Without a workspace: one block per group of windows
@@ -451,7 +456,7 @@ __global__ __launch_bounds__(256) void k_pad(const T *__restrict__ x, long long 
 
 static int se_launch(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
                      const float *w2t, const float *b2, float *gate, long long g_ws, float *work, void *D,
-                     long long d_ws, int B, bool f16, void *stream) {
+                     long long d_ws, int B, bool f16, void *stream, uint16_t *gh = nullptr, long long gh_ws = 0) {
   BNH_REQ(chsum && w1 && b1 && w2t && b2 && (gate || D) && B > 0);
   BNH_REQ(C > 0 && C % 4 == 0 && C <= 4096 && rd > 0 && rd <= 512 && P > 0);
   BNH_REQ(B == 1 || (c_ws >= C && (!gate || g_ws >= C) && (!D || d_ws >= (long long)P * C)));
@@ -476,7 +481,8 @@ static int se_launch(const float *chsum, long long c_ws, int C, int rd, int P, c
     const int wb2 = bnh_ceil_div(B, 4) * cb2 >= 512 ? 4 : bnh_ceil_div(B, 2) * cb2 >= 512 ? 2 : 1;
     const dim3 g2((unsigned)cb2, (unsigned)bnh_ceil_div(B, wb2));
     const size_t l2 = sizeof(float) * wb2 * (size_t)rd;
-#define SE_FC2(W_, F_) hipLaunchKernelGGL((k_se_fc2<W_, F_>), g2, dim3(256), l2, st, work, C, rd, w2t, b2, gate, g_ws, B)
+#define SE_FC2(W_, F_)                                                                                                 \
+  hipLaunchKernelGGL((k_se_fc2<W_, F_>), g2, dim3(256), l2, st, work, C, rd, w2t, b2, gate, g_ws, B, gh, gh_ws)
     if (f16) { if (wb2 == 4) SE_FC2(4, true); else if (wb2 == 2) SE_FC2(2, true); else SE_FC2(1, true); }
     else { if (wb2 == 4) SE_FC2(4, false); else if (wb2 == 2) SE_FC2(2, false); else SE_FC2(1, false); }
 #undef SE_FC2
@@ -603,6 +609,13 @@ int bnh_se_f16(const float *chsum, long long c_ws, int C, int rd, int P, const f
                long long d_ws, int B, void *stream) {
   BNH_REQ(D);
   return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws, work, D, d_ws, B, true, stream);
+}
+
+int bnh_se_gate_f16(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
+                    const float *w2t, const float *b2, float *gate, long long g_ws, float *work, uint16_t *gh,
+                    long long gh_ws, int B, void *stream) {
+  BNH_REQ(gate && work && gh && C % 8 == 0 && (B == 1 || gh_ws >= C));
+  return se_launch(chsum, c_ws, C, rd, P, w1, b1, w2t, b2, gate, g_ws, work, nullptr, 0, B, true, stream, gh, gh_ws);
 }
 
 int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,

@@ -69,6 +69,13 @@ static int pw16_init(rt_ctx *c, rt_op *op) {
   if (!s->W) return rt_oom(c, op, (size_t)Np * Kp * 2);
   return 0;
 }
+// the fp16 gates of a gates-only SE, window 0: op scratch [bcap][C] fp32 gates, [bcap][rd] first-FC outputs, then
+// [bcap][C] fp16 gates from the next 16-byte boundary (C % 8 == 0: every window's row stays 16-byte aligned)
+static uint16_t *se_gh(const rt_ctx *c, const rt_op *se) {
+  float *g = (float *)((const rt_dev_state *)se->state)->scratch;
+  return (uint16_t *)(g + (((size_t)(se->p[0] + se->p[1]) * c->bcap + 3) & ~(size_t)3));
+}
+
 static int pw16_run(rt_ctx *c, rt_op *op) {
   pw16_state *s = (pw16_state *)op->state;
   const int *p = op->p;
@@ -93,6 +100,10 @@ static int pw16_run(rt_ctx *c, rt_op *op) {
     }
     ws = (char *)s->ws + bnh_gemm_f16_ws_bytes(p[4], 1, s->W) * c->w0;  // this sub-batch's windows
   }
+  if (op->se)  // the SE that precedes it left its rows unscaled: the gates apply as the rows are loaded
+    return bnh_gemm_f16_gated_ws((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e,
+                                 se_gh(c, op->se) + (size_t)op->se->p[0] * c->w0, op->se->p[0], ws,
+                                 bnh_gemm_f16_ws_bytes(p[4], c->nwin, s->W), c->stream);
   return bnh_gemm_f16_ws((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e, ws,
                          bnh_gemm_f16_ws_bytes(p[4], c->nwin, s->W), c->stream);
 }
@@ -158,8 +169,14 @@ static int se_run(rt_ctx *c, rt_op *op) {
   const int *p = op->p;
   // op scratch per window: the gates (C % 8 == 0: 16-byte aligned rows), then the first FC's outputs
   const long long g_ws = p[0];
-  float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)(g_ws + p[1]));
+  float *g = (float *)rt_dev_scratch(c, op, sizeof(float) * (size_t)(g_ws + p[1]) +
+                                                (op->gate_only ? 2 * (size_t)p[0] + 16 : 0));
   if (!g) return -1;
+  if (op->gate_only)  // the next op applies the gates as it loads the rows
+    return bnh_se_gate_f16((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_h(op, 0),
+                           (const float *)dev_h(op, 1), (const float *)dev_h(op, 2), (const float *)dev_h(op, 3),
+                           g + g_ws * c->w0, g_ws, g + g_ws * c->bcap + (long long)p[1] * c->w0,
+                           se_gh(c, op) + (size_t)p[0] * c->w0, p[0], c->nwin, c->stream);
   return bnh_se_f16((const float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[0], p[1], p[2], (const float *)dev_h(op, 0),
                     (const float *)dev_h(op, 1), (const float *)dev_h(op, 2), (const float *)dev_h(op, 3),
                     g + g_ws * c->w0, g_ws, g + g_ws * c->bcap + (long long)p[1] * c->w0, (uint16_t *)rt_b(c, op, 0),
@@ -191,6 +208,18 @@ static const rt_kernel K_PAD = {pad_init, pad_run, nullptr, "pad_f16", 0x2, 0};
 static const rt_kernel K_GEMV = {gemv_init, gemv_run, rt_dev_fini, "gemv_h16", 0x2, 0};
 static const rt_kernel K_DW3 = {dw3_init, dw3_run, rt_dev_fini, "dw3_f16", 0x6, 0};
 static const rt_kernel K_DWK = {dwk_init, dwk_run, rt_dev_fini, "dwk_f16", 0x6, 0};
+
+int rt_fuse_se16(rt_ctx *c, rt_op *se, rt_op *pw) {
+  (void)c;
+  if (se->k != &K_SE || pw->k != &K_PW || pw->b[0] != se->b[0]) return 0;
+  const int C = se->p[0], P = se->p[2];
+  const int *p = pw->p;
+  // the PW's rows are the SE's buffer as it stands: P rows of C channels, K = Kp = lda = C
+  if (p[1] != C || p[2] != C || p[4] != P || p[5] != C) return 0;
+  se->gate_only = 1;
+  pw->se = se;
+  return 1;
+}
 
 const rt_kernel *rt_k_f16(int base) {
   switch (base) {

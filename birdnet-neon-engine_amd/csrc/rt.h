@@ -46,6 +46,10 @@ typedef struct rt_op {
   // only quantizes its rows (quant_only), and the depthwise op recomputes the expansion from them (pw)
   struct rt_op *pw;
   int quant_only;
+  // and an fp16 SE whose scaled buffer only the next op, an fp16 PW, reads computes the gates only (gate_only), which
+  // that PW applies as it loads its rows (se)
+  struct rt_op *se;
+  int gate_only;
 } rt_op;
 
 typedef struct rt_kernel {
@@ -141,6 +145,8 @@ struct bnh_s8w;
 const struct bnh_s8w *rt_pw8_plain(const rt_op *op);
 // fp32 DW3 / DWK (ops_f32.cpp): fuse expansion pw into depthwise op dw when bnh_pwdw_f32 takes the pair; 1 if fused
 int rt_fuse_pwdw(rt_ctx *c, rt_op *pw, rt_op *dw);
+// fp16 SE + PW (ops_f16.cpp): fuse when the PW reads the SE's buffer as its rows; 1 if fused
+int rt_fuse_se16(rt_ctx *c, rt_op *se, rt_op *pw);
 
 // ---- helpers for kernel init / run (the reference's contract helpers, src/rt.h:133-167)
 const void *rt_t(const rt_ctx *c, const rt_op *op, int i, size_t *nbytes);

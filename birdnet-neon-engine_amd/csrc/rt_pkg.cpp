@@ -375,6 +375,21 @@ static void fuse_ops(rt_ctx *c) {
           other = true;
     if (!other) rt_fuse_pwdw(c, pw, dw);
   }
+  // An fp16 SE (which scales its buffer D in place) followed by an fp16 PW whose rows are D: the SE computes its gates
+  // only and the PW applies them as it loads D, so D is never rewritten. No other op may read D.
+  for (int i = 0; i + 1 < c->n_ops; i++) {
+    rt_op *se = &c->ops[i], *pw = &c->ops[i + 1];
+    if (se->nb < 1 || se->b[0] < 0 || pw->quant_only || pw->pw || se->quant_only) continue;
+    const int32_t buf = se->b[0];
+    bool other = buf == (int32_t)c->path->in_buf || buf == (int32_t)c->path->out_buf || buf == (int32_t)c->path->emb_buf;
+    for (int j = 0; j < c->n_ops && !other; j++) {
+      if (j == i || j == i + 1) continue;
+      const rt_op *o = &c->ops[j];
+      for (int a = 0; a < o->nb && !other; a++)  // a reader (the op that writes D is no obstacle)
+        if (o->b[a] == buf && !(a < 32 && (o->k->outmask >> a & 1))) other = true;
+    }
+    if (!other) rt_fuse_se16(c, se, pw);
+  }
 }
 
 rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
@@ -660,6 +675,8 @@ void rt_ctx_free(rt_ctx *c) {
       char fz[48] = "";
       if (op->pw) snprintf(fz, sizeof fz, " [fused: computes op %d's expansion]", (int)(op->pw - c->ops));
       else if (op->quant_only) snprintf(fz, sizeof fz, " [quantizes only]");
+      else if (op->se) snprintf(fz, sizeof fz, " [fused: applies op %d's gates]", (int)(op->se - c->ops));
+      else if (op->gate_only) snprintf(fz, sizeof fz, " [gates only]");
       if (c->prof > 1)
         fprintf(stderr, "  %3d %-14s %10.5f  %s%s\n", i, op->k->name, 1e3 * c->t_op[i] / c->nprof, src, fz);
     }

@@ -152,6 +152,13 @@ int bnh_gemm_f16_body(const uint16_t *A, long long a_ws, int lda, int M, int B, 
 size_t bnh_gemm_f16_ws_bytes(int M, int B, const bnh_h16w *W);
 int bnh_gemm_f16_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
                     void *ws, size_t ws_bytes, void *stream);
+/* the same product of the gated rows A x gh: A's column k multiplied by the window's fp16 gate gh[k] (gh [B][gh_ws]
+ * fp16, gh_ws >= Kp) as it is loaded. The fp16 SE (src/rt_ops_f32.c:256-327) scales A in place by the same fp16
+ * products before the reference's 1x1 conv reads it; here the scaling happens in the GEMM's A-load and A is left as
+ * it was (no reference counterpart as an entry point). */
+int bnh_gemm_f16_gated_ws(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W,
+                          const bnh_epi16 *e, const uint16_t *gh, long long gh_ws, void *ws, size_t ws_bytes,
+                          void *stream);
 /* the same product on fp16 MFMA with fp32 accumulation over the whole K (no reference counterpart: a faster form
  * for callers that accept the fp16 accumulation error bound of the reference instead of its exact bits) */
 int bnh_gemm_f16_mfma(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
@@ -268,6 +275,11 @@ int bnh_stem_f32to16(const float *img, long long i_ws, int H, int W, int k, int 
 int bnh_se_f16(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
                const float *w2t, const float *b2, float *gate, long long g_ws, float *work, uint16_t *D,
                long long d_ws, int B, void *stream);
+/* the fp16 SE's gates alone (fp32 into gate, their fp16 roundings, the factors the scaling multiplies by, into gh
+ * [B][gh_ws]), D untouched: for bnh_gemm_f16_gated_ws (C % 8 == 0; no reference counterpart as an entry point) */
+int bnh_se_gate_f16(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
+                    const float *w2t, const float *b2, float *gate, long long g_ws, float *work, uint16_t *gh,
+                    long long gh_ws, int B, void *stream);
 /* MEAN of fp16 rows: replaces pc_mean_f16 (src/pc_kern_f16.c:115-121) */
 int bnh_mean_f16(const uint16_t *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
                  void *stream);

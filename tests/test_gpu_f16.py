@@ -46,8 +46,9 @@ def same_bits(a, b):
 
 
 def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, Kp=None, b16=None, fn="bnh_gemm_f16", ldo=None,
-            o_slack=32):
-    """A [B][M][lda] fp16 -> out [B][rows][ldo] fp16 through fn (bnh_gemm_f16 or bnh_gemm_f16_mfma)."""
+            o_slack=32, gh=None):
+    """A [B][M][lda] fp16 -> out [B][rows][ldo] fp16 through fn (bnh_gemm_f16 or bnh_gemm_f16_mfma; with
+    fn = bnh_gemm_f16_ws and gates gh [B][Kp] fp16, bnh_gemm_f16_gated_ws)."""
     H = hip
     Bw, M, lda = A.shape
     N, K = W.shape
@@ -88,7 +89,12 @@ def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, Kp=None, b16=None, fn
             dO = H.DeviceArray.zeros((Bw, o_ws), np.float16)
             e = H.Epi16(act, dO.ptr, o_ws, ldo, ow, opad, dR.ptr if dR else None, r_ws,
                         res.shape[2] if res is not None else 0)
-            H.check(H.lib().bnh_gemm_f16_ws(dA.ptr, a_ws, lda, M, Bw, hw, e, dW.ptr, wsb, None), fn)
+            if gh is None:
+                H.check(H.lib().bnh_gemm_f16_ws(dA.ptr, a_ws, lda, M, Bw, hw, e, dW.ptr, wsb, None), fn)
+            else:
+                dG = H.DeviceArray.from_host(np.ascontiguousarray(gh, np.float16))
+                H.check(H.lib().bnh_gemm_f16_gated_ws(dA.ptr, a_ws, lda, M, Bw, hw, e, dG.ptr, gh.shape[1], dW.ptr,
+                                                      wsb, None), "bnh_gemm_f16_gated_ws")
             H.sync()
             return dO.numpy()[:, :rows * ldo].reshape(Bw, rows, ldo), Wp
         H.check(getattr(H.lib(), fn)(dA.ptr, a_ws, lda, M, Bw, hw, e, None), fn)
@@ -275,3 +281,28 @@ def test_split_k_blocks_bit_exact(hip, K, N, M, B, act, opad, ldo):
     for i in range(B):
         ref = O.gemm_f16(A[i], Wp, b, act=act, ldo=ldo, ow=ow, opad=opad, res=None if res is None else res[i])
         assert same_bits(out[i][:, :Np], ref[:, :Np]), i
+
+
+# The fp16 SE's gates applied in the A-load (bnh_gemm_f16_gated_ws): the bytes the plain exact GEMM gives on the rows
+# scaled in place by the same fp16 products (the fp16 SE, src/rt_ops_f32.c:256-327), per-window gates, the split
+# K-block form, residual, padded output; rows holding inf / NaN and gates of 0 and 1; and the oracle on the scaled rows
+@pytest.mark.parametrize("K,N,M,B,act,opad", [(72, 288, 96, 3, 1, 1), (288, 72, 96, 3, 0, 0), (1536, 192, 24, 5, 2, 0),
+                                              (864, 108, 96, 4, 1, 0)])
+def test_gated_rows_bit_exact(hip, K, N, M, B, act, opad):
+    rng = np.random.default_rng(K + 7 * N + M)
+    A = rng.standard_normal((B, M, K)).astype(np.float16)
+    A[0, 0, :3] = [np.inf, -np.inf, np.nan]
+    gh = rng.uniform(0, 1, (B, K)).astype(np.float16)
+    gh[0, :4] = [0.0, 1.0, 0.5, 0.0]
+    scaled = (A.astype(np.float32) * gh[:, None, :].astype(np.float32)).astype(np.float16)  # one rounding each
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    Np = (N + 7) // 8 * 8
+    ow = 8 if opad else 0
+    res = rng.standard_normal((B, M, Np)).astype(np.float16) if not opad else None
+    say("f16 gemm gated", K, N, M, B, act, opad)
+    got, Wp = run_gpu(hip, A, W, b, act=act, ow=ow, opad=opad, res=res, fn="bnh_gemm_f16_ws", gh=gh)
+    want, _ = run_gpu(hip, scaled, W, b, act=act, ow=ow, opad=opad, res=res, fn="bnh_gemm_f16_ws")
+    assert same_bits(got, want)
+    ref = O.gemm_f16(scaled[1], Wp, b, act=act, ow=ow, opad=opad, res=None if res is None else res[1])
+    assert same_bits(got[1][:, :Np], ref[:, :Np])

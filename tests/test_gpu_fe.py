@@ -269,6 +269,16 @@ def test_se_f16(hip, C, rd, P, ws):
         if ws:   # the gates as the fp32 SE computes them, with the dividing sigmoid
             assert same_bits(O.se_f16(np.ones((P, C), np.float16), chsum[i], w1, b1, w2t, b2)[0],
                              dg.numpy()[i, :C].astype(np.float16)), i
+    if ws and C % 8 == 0:   # the gates alone: fp32 and their fp16 roundings
+        dg2 = H.DeviceArray.from_host(np.zeros((B, g_ws), np.float32))
+        gh_ws = C + 8
+        dh = H.DeviceArray.from_host(np.zeros((B, gh_ws), np.float16))
+        H.check(H.lib().bnh_se_gate_f16(dc.ptr, c_ws, C, rd, P, dt[0].ptr, dt[1].ptr, dt[2].ptr, dt[3].ptr, dg2.ptr,
+                                        g_ws, dwk.ptr, dh.ptr, gh_ws, B, None), "se_gate_f16")
+        H.sync()
+        assert np.array_equal(dg2.numpy()[:, :C].view(np.uint32), dg.numpy()[:, :C].view(np.uint32))
+        assert same_bits(dh.numpy()[:, :C], dg.numpy()[:, :C].astype(np.float16))
+        assert (dh.numpy()[:, C:] == 0).all()
 
 
 def test_mean_f16_and_gemv(hip):

@@ -71,3 +71,23 @@ def test_v24_two_stream_batch(hip, v24):
         for lo in (0, 24, 48):
             o, e, s = m.infer_batch(pcm[lo:lo + 24])
             assert not s.any() and same(o, out[lo:lo + 24]) and same(e, emb[lo:lo + 24]), lo
+
+
+def test_v24_se_gates_in_the_gemm(hip, v24, monkeypatch, capfd):
+    """Each of the 16 SEs computes its gates only and the projection after it applies them as it loads its rows (the
+    scaled activations never written), giving the bytes of the op list run as written (BNH_FUSE=0)."""
+    vn, path = v24
+    rng = np.random.default_rng(12)
+    pcm = np.stack([v24net.signal(rng) for _ in range(8)])
+    say("v24 fused vs op by op")
+    monkeypatch.setenv("BNN_PROF", "2")
+    with binding.Model(path) as m:
+        out, emb, status = m.infer_batch(pcm)
+    err = capfd.readouterr().err
+    assert err.count("[fused: applies op") == 16 and err.count("[gates only]") == 16, err[-2000:]
+    monkeypatch.delenv("BNN_PROF")
+    monkeypatch.setenv("BNH_FUSE", "0")
+    with binding.Model(path) as m:
+        o2, e2, s2 = m.infer_batch(pcm)
+    assert not status.any() and not s2.any()
+    assert same(out, o2) and same(emb, e2)
