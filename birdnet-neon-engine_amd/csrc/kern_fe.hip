@@ -22,7 +22,8 @@ struct bnh_logmel {
   float *mel_w;       // [nnz]
 };
 
-#define FE_FPB 4  // frames per block
+#define FE_FPB 4  // frames per block (the frame index of a flat item is three comparisons)
+static_assert(FE_FPB == 4, "k_logmel finds a flat item's frame with three comparisons");
 
 // log2_acc_f32x4 (src/gemm_f32.h:57-71) on one lane
 __device__ __forceinline__ float fe_log2_acc(float x) {
@@ -55,9 +56,11 @@ __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, l
   const int t0 = blockIdx.x * FE_FPB, win = blockIdx.y;
   const float *x = pcm + win * p_ws;
   const int nz = (F.frame + 1) / 2;
+  // M = 2^lg (lg >= 3): every index split of the FFT passes is a shift and a mask, not an integer division
+  const int lg = F.lg;
   // z[n] = w[2n] y[2n] + i w[2n+1] y[2n+1], stored at the bit-reversed position
   for (int it = tid; it < FE_FPB * M; it += 256) {
-    const int f = it / M, n = it % M;
+    const int f = it >> lg, n = it & (M - 1);
     const int t = t0 + f < F.nfr ? t0 + f : F.nfr - 1;
     const int r = (int)(__builtin_bitreverse32((uint32_t)n) >> (32 - F.lg));
     float vr = 0.f, vi = 0.f;
@@ -73,7 +76,7 @@ __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, l
   __syncthreads();
   // levels 1 and 2 fused, no twiddles
   for (int it = tid; it < FE_FPB * (M / 4); it += 256) {
-    const int f = it / (M / 4), i = 4 * (it % (M / 4));
+    const int f = it >> (lg - 2), i = 4 * (it & (M / 4 - 1));
     float *pr = re + f * M + i, *pi = im + f * M + i;
     const float ar = pr[0], ai = pi[0], br = pr[1], bi = pi[1], cr = pr[2], ci = pi[2], dr = pr[3], di = pi[3];
     const float s0r = ar + br, s0i = ai + bi, d0r = ar - br, d0i = ai - bi;
@@ -83,12 +86,12 @@ __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, l
     pr[1] = d0r + d1i; pi[1] = d0i - d1r;
     pr[3] = d0r - d1i; pi[3] = d0i + d1r;
   }
-  int len = 8;
-  for (; 2 * len <= M; len <<= 2) {  // radix-2^2 passes: levels len and 2 len
+  int len = 8, lgl = 3;
+  for (; 2 * len <= M; len <<= 2, lgl += 2) {  // radix-2^2 passes: levels len and 2 len
     __syncthreads();
     const int h = len / 2, st1 = M / len, st2 = M / (2 * len);
     for (int it = tid; it < FE_FPB * (M / 4); it += 256) {
-      const int f = it / (M / 4), g = it % (M / 4), j = g % h, i = (g / h) * 2 * len;
+      const int f = it >> (lg - 2), g = it & (M / 4 - 1), j = g & (h - 1), i = (g >> (lgl - 1)) << (lgl + 1);
       const float w1r = F.twr[j * st1], w1i = F.twi[j * st1], w2r = F.twr[j * st2], w2i = F.twi[j * st2];
       float *pr = re + f * M + i + j, *pi = im + f * M + i + j;
       const float ar = pr[0], ai = pi[0], br = pr[h], bi = pi[h], cr = pr[2 * h], ci = pi[2 * h], dr = pr[3 * h],
@@ -107,11 +110,11 @@ __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, l
       pr[3 * h] = b1r - ui; pi[3 * h] = b1i + ur;
     }
   }
-  for (; len <= M; len <<= 1) {  // a last single level
+  for (; len <= M; len <<= 1, lgl++) {  // a last single level
     __syncthreads();
     const int half = len / 2, step = M / len;
     for (int it = tid; it < FE_FPB * (M / 2); it += 256) {
-      const int f = it / (M / 2), g = it % (M / 2), j = g % half, i = (g / half) * len;
+      const int f = it >> (lg - 1), g = it & (M / 2 - 1), j = g & (half - 1), i = (g >> (lgl - 1)) << lgl;
       const float wr = F.twr[j * step], wi = F.twi[j * step];
       float *pr = re + f * M + i + j, *pi = im + f * M + i + j;
       float vr, vi;
@@ -125,7 +128,7 @@ __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, l
   // real-input split and magnitudes of bins [klo, khi)
   const int nk = F.khi - F.klo;
   for (int it = tid; it < FE_FPB * nk; it += 256) {
-    const int f = it / nk, k = F.klo + it % nk;
+    const int f = (it >= nk) + (it >= 2 * nk) + (it >= 3 * nk), k = F.klo + it - f * nk;  // FPB 4 frames
     const int k2 = (k == 0 || k == M) ? 0 : M - k, ka = k == M ? 0 : k;
     const float *fr = re + f * M, *fi = im + f * M;
     const float Ar = fr[ka], Ai = fi[ka], Br = fr[k2], Bi = -fi[k2];
@@ -138,7 +141,7 @@ __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, l
   }
   __syncthreads();
   for (int it = tid; it < FE_FPB * F.nmel; it += 256) {
-    const int f = it / F.nmel, j = it % F.nmel, t = t0 + f;
+    const int f = (it >= F.nmel) + (it >= 2 * F.nmel) + (it >= 3 * F.nmel), j = it - f * F.nmel, t = t0 + f;
     if (t >= F.nfr) continue;
     float a0 = 0.f, a1 = 0.f;
     const int e0 = F.mel_off[j], e1 = F.mel_off[j + 1];
