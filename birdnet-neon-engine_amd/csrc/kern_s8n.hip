@@ -36,6 +36,7 @@ struct EpiDev {  // the fp32 epilogue, by value into the kernel
   long long res_ws;
   int ldr, rpad, rw;
   double r_ow, r_rw;  // 1 / ow, 1 / rw (padded row arithmetic)
+  int vec;            // k_s8n_gemm: rows stored (and residuals read) as 16-byte quads through LDS
 };
 
 // the padded row of pixel m (ow pixels per image row, halo opad)
@@ -260,6 +261,8 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
   __shared__ long long s_q[RB], s_o[RB], s_r[RB];
   __shared__ float s_sa[RB];
   __shared__ uint32_t s_z[RB], s_tbl[256];
+  constexpr int TS = 68;  // the vector epilogue's tile row stride in floats (64 channels + 4)
+  __shared__ float s_t[RES ? 4 : 1][RES ? 16 * TS : 1];  // (the form without residual stores values directly)
   bnh_silu_table(s_tbl);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const unsigned lb = gsplit > 1 ? bnh_xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
@@ -345,6 +348,65 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
       swn[j] = sw[n];
       bn[j] = bias[n];
       csn[j] = cs[n];
+    }
+    if (RES && e.vec) {
+      // the tile's 16 rows x 64 channels go through the wave's LDS tile: each value dequantised and activated in the
+      // accumulator layout (the same operations as below), then read back as 16-byte quads of a row, its residual
+      // quad added, and stored whole (4 times fewer memory instructions than one 4-byte access per value)
+      float *T = s_t[wave];
+      const int nq = ((Np - n0 < 64 ? Np - n0 : 64) + 3) / 4;  // quads holding channels < Np (Np % 4 == 0)
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int lr = lr0 + 16 * t + 4 * (lane >> 4) + r;
+          const float s_a = s_sa[lr];
+          const uint32_t z = s_z[lr];
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            if (j >= jn) break;
+            const int32_t c = (int32_t)((uint32_t)acc[t][j][r] - (uint32_t)csn[j] * z);
+            const float f = (float)c;
+            const float scl = swn[j] * s_a;
+            float y = f * scl;
+            y = y + bn[j];
+            if (e.act == 1) y = bnh_silu_f32_t(y, s_tbl);
+            else if (e.act == 2) y = bnh_relu_f32(y);
+            T[(4 * (lane >> 4) + r) * TS + 16 * j + (lane & 15)] = y;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int qd = lane & 15;
+        float4 rq[4];
+        if (RES) {  // every residual quad of the tile first (out and res may alias: loads before any store)
+#pragma unroll
+          for (int it = 0; it < 4; it++) {
+            const int lr = lr0 + 16 * t + 4 * it + (lane >> 4);
+            rq[it] = qd < nq && rowB + lr < rows ? *(const float4 *)(e.res + s_r[lr] + n0 + 4 * qd)
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+          const int rr = 4 * it + (lane >> 4), lr = lr0 + 16 * t + rr;
+          if (qd < nq && rowB + lr < rows) {
+            float4 y = *(const float4 *)(T + rr * TS + 4 * qd);
+            if (RES) {
+              y.x = y.x + rq[it].x;
+              y.y = y.y + rq[it].y;
+              y.z = y.z + rq[it].z;
+              y.w = y.w + rq[it].w;
+            }
+            *(float4 *)(e.out + s_o[lr] + n0 + 4 * qd) = y;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      continue;
     }
 #pragma unroll
     for (int t = 0; t < 2; t++) {
@@ -820,7 +882,12 @@ int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, long long sa_
   if (check_epi(e, M, W->Np, B)) return -1;
   const long long rows = (long long)M * B;
   EpiDev d = {e->act, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->res, e->res_ws, e->ldr, e->rpad, e->rw,
-              e->opad ? 1.0 / e->ow : 0.0, e->rpad ? 1.0 / e->rw : 0.0};
+              e->opad ? 1.0 / e->ow : 0.0, e->rpad ? 1.0 / e->rw : 0.0, 0};
+  // with a residual, 16-byte quads when every output and residual quad lies 16-byte aligned (block 1's 24 -> 24
+  // projection over 249 x 63 pixels 341 -> 322 us; without a residual the quads' LDS round trip made the launches
+  // 10-30 % slower, so those store values directly)
+  auto al4 = [](const void *p, long long ws, int ld) { return ((uintptr_t)p & 15) == 0 && ws % 4 == 0 && ld % 4 == 0; };
+  d.vec = W->Np % 4 == 0 && e->res && al4(e->out, e->out_ws, e->ldo) && al4(e->res, e->res_ws, e->ldr);
   hipStream_t s = bnh_stream(stream);
   const double rM = 1.0 / M;
   // 128 rows per block; the channel groups split over gsplit blocks only when the row blocks alone would leave the

@@ -156,7 +156,7 @@ def test_quant_rows_gate(hip):
     assert quant_case(hip, x, K, Kp, gate=g)
 
 
-def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, gate=False):
+def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, gate=False, ldo_extra=8):
     H = hip
     rng = np.random.default_rng(seed)
     M = H_ * W_
@@ -168,7 +168,7 @@ def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, g
     N_, K_, Kp, Np = pk["shape"]
     x = (rng.standard_normal((B, M, lda)) * 2).astype(np.float32)
     gt = rng.uniform(0, 1, (B, K)).astype(np.float32) if gate else None
-    ldo = Np + 8
+    ldo = Np + ldo_extra
     out_rows = M if not opad else (H_ + 2 * opad) * (W_ + 2 * opad)
     rs = rng.standard_normal((B, M, Np)).astype(np.float32) if res else None
     M4 = (M + 3) // 4 * 4
@@ -215,6 +215,13 @@ def test_pw_s8_residual_halo_gate(hip):
     assert pw_case(hip, 3, 7, 9, 48, 40, 1, opad=2, res=True, lda_extra=5, seed=9)
     assert pw_case(hip, 2, 5, 6, 96, 136, 2, opad=1, seed=10, gate=True)
     assert pw_case(hip, 1, 1, 1, 24, 8, 0, seed=11)   # a single row (GEMV-like)
+
+
+def test_pw_s8_unaligned_output_rows(hip):
+    # output rows 4-byte aligned only (ldo odd): the epilogue's one-value-per-access form; with a residual and ldo a
+    # multiple of 4 (above) the GEMM takes the 16-byte-quad form through LDS
+    assert pw_case(hip, 2, 9, 11, 144, 24, 0, res=True, seed=12, ldo_extra=3)
+    assert pw_case(hip, 2, 7, 5, 40, 136, 1, opad=1, seed=13, ldo_extra=1)
 
 
 def test_gemm_requant_config0(hip):
