@@ -68,6 +68,14 @@ def test_perch_two_stream_batch(hip, perch):
         for lo in (0, 24, 48):
             o, e, s = m.infer_batch(pcm[lo:lo + 24])
             assert not s.any() and same(o, out[lo:lo + 24]) and same(e, emb[lo:lo + 24]), lo
+        # the same 72 windows read from device memory where the caller keeps them (stride n_samples)
+        dp = hip.DeviceArray.from_host(pcm)
+        do = hip.DeviceArray.zeros((72, m.info.n_classes), np.float32)
+        de = hip.DeviceArray.zeros((72, m.info.emb_dim), np.float32)
+        st = np.zeros(72, np.int32)
+        r = m.L.bnn_infer_batch_device(m.ctx, dp.ptr, 72, do.ptr, de.ptr, st.ctypes.data_as(binding._IP), None)
+        assert r == 0 and not st.any()
+        assert same(do.numpy(), out) and same(de.numpy(), emb)
 
 
 def test_perch_fused_expansions(hip, perch, monkeypatch, capfd):

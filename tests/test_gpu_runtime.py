@@ -135,20 +135,26 @@ def test_large_batch_two_streams(hip, tmp_path):
         assert e.value.kind == "window" and "window 7 of 101" in str(e.value)
 
 
-def test_device_resident_batch(hip, tmp_path):
+@pytest.mark.parametrize("n", [9, 72])
+def test_device_resident_batch(hip, tmp_path, n):
+    """Windows read where the caller keeps them (stride n_samples) give the host path's bytes; 72 windows run as two
+    sub-batches, the second of which starts at window 36 of the caller's buffer."""
     spec = Spec(5)
     path = spec.package(str(tmp_path / "net.bnpk"))
     rng = np.random.default_rng(6)
-    pcm = rng.standard_normal((9, spec.M * spec.K0)).astype(np.float32)
-    say("runtime device batch")
+    pcm = rng.standard_normal((n, spec.M * spec.K0)).astype(np.float32)
+    say("runtime device batch", n)
     with binding.Model(path) as m:
         dp = hip.DeviceArray.from_host(pcm)
-        do = hip.DeviceArray.zeros((9, spec.nc), np.float32)
-        st = np.zeros(9, np.int32)
-        r = m.L.bnn_infer_batch_device(m.ctx, dp.ptr, 9, do.ptr, None, st.ctypes.data_as(binding._IP), None)
+        do = hip.DeviceArray.zeros((n, spec.nc), np.float32)
+        st = np.zeros(n, np.int32)
+        r = m.L.bnn_infer_batch_device(m.ctx, dp.ptr, n, do.ptr, None, st.ctypes.data_as(binding._IP), None)
         assert r == 0
         host, _, _ = m.infer_batch(pcm)
         assert same(do.numpy(), host)
+        for w in (0, n // 2, n - 1):
+            _, ref = spec.oracle(pcm[w])
+            assert same(host[w], ref), w
 
 
 def test_forged_n4_flags_are_refused(hip, tmp_path):
