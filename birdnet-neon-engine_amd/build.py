@@ -21,12 +21,15 @@ LIB = os.path.join(HERE, "libbnneon_hip.so")
 SOURCES = [
     "device.hip",
     "kern_s8n.hip",
+    "pw_s8_static.hip",
     "kern_proto.hip",
     "kern_dw.hip",
     "kern_wino.hip",
     "kern_f16.hip",
     "kern_fe.hip",
     "kern_f32.hip",
+    "pkg_file.cpp",
+    "rt_contract.cpp",
     "rt_pkg.cpp",
     "ops_table.cpp",
     "ops_s8n.cpp",

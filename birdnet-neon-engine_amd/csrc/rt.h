@@ -106,8 +106,10 @@ struct rt_ctx {
   size_t errlen;
   int err_kind;
   char err_params[160];
-  const char *src;
+  const char *src;       // the package's source-node lines of this path (one per op), or NULL
   size_t src_len;
+  size_t *src_line_at;   // byte offset of each line in src
+  int n_src_lines;
   int fail_op;
   int prof;
   double *t_op;
@@ -121,7 +123,11 @@ int rt_meta_str(const rt_pkg *p, const char *key, char *buf, size_t n);
 int rt_meta_i64(const rt_pkg *p, const char *key, int64_t *v);
 int rt_meta_f64(const rt_pkg *p, const char *key, double *v);
 int rt_n_paths(const rt_pkg *p);
+int rt_n_tensors(const rt_pkg *p);
 int rt_format_version(const rt_pkg *p);
+const uint8_t *rt_pkg_bytes(const rt_pkg *p);  // the mapped file
+// a metadata record's value (NULL when the key is absent), its type (0 text, 1 i64, 2 f64, 3 bytes) and size
+const uint8_t *rt_meta_raw(const rt_pkg *p, const char *key, uint16_t *type, uint32_t *bytes);
 const rt_pathdesc *rt_path(const rt_pkg *p, int i);
 const rt_tensor *rt_tensor_at(const rt_pkg *p, int i, const void **data);
 

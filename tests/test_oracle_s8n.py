@@ -267,3 +267,111 @@ def test_requant_gemm_brute_force():
         for m in range(M):
             y = L.orc_rdbypot(_srdhm_exact(int(acc[n, m]), int(mult[n])), int(shift[n])) - 128
             assert out[n, m] == max(-128, min(127, y))
+
+
+# ------------------------------------------------------------------ discriminating closed forms (exact arithmetic)
+def _f32_rne(fr):
+    """The fp32 nearest to a Fraction (ties to even), normal and subnormal range, computed in integers."""
+    from fractions import Fraction
+    fr = Fraction(fr)
+    if fr == 0:
+        return 0.0
+    sign, a = (-1 if fr < 0 else 1), abs(fr)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    quantum = Fraction(2) ** (max(e, -126) - 23)          # one ulp at this exponent (2^-149 for subnormals)
+    q, r = divmod(a, quantum)
+    if r * 2 > quantum or (r * 2 == quantum and q % 2 == 1):
+        q += 1
+    return float(np.float32(sign * float(q * quantum)))
+
+
+def test_f32_rne_helper_against_numpy():
+    from fractions import Fraction
+    rng = np.random.default_rng(0)
+    for _ in range(2000):
+        a, b = rng.standard_normal(2).astype(np.float32)
+        assert _f32_rne(Fraction(float(a)) * Fraction(float(b))) == float(np.float32(a) * np.float32(b))
+        assert _f32_rne(Fraction(float(a)) + Fraction(float(b))) == float(np.float32(a) + np.float32(b))
+
+
+def _integer_t_inputs():
+    """fp32 x where t = fl(x * -1.44269504f) is an exact integer n (then the exp2 split has f = 0, p = 1)."""
+    c = np.float32(-1.44269504)
+    out = []
+    for n in list(range(-23, -8)) + list(range(9, 60)):
+        x0 = np.float32(n / float(c))
+        for k in range(-64, 65):
+            x = np.nextafter(x0, np.float32(np.inf) if k > 0 else np.float32(-np.inf)) if k else x0
+            for _ in range(abs(k) - 1):
+                x = np.nextafter(x, np.float32(np.inf) if k > 0 else np.float32(-np.inf))
+            if float(np.float32(x) * c) == float(n):
+                out.append((float(x), n))
+                break
+    return out
+
+
+def test_silu_where_t_is_an_integer():
+    """SiLU(x) = x * r with d = 1 + 2^n exactly rounded, r0 = FRECPE(d) = 511/512 * 2^-E (the published FRECPE(1.0),
+    scaled by d's binary exponent E: for these n the top 8 fraction bits of d are 0), and one Newton step
+    r = r0 * fl(2 - d r0). A slip in the magic-number split, the exponent shift, the clamp or the step shows here."""
+    from fractions import Fraction
+    L = O.lib()
+    cases = _integer_t_inputs()
+    assert len(cases) >= 40, len(cases)
+    for x, n in cases:
+        d = _f32_rne(1 + Fraction(2) ** n)
+        E = math.frexp(d)[1] - 1
+        r0 = Fraction(511, 512) / Fraction(2) ** E
+        s = _f32_rne(2 - Fraction(d) * r0)
+        r = _f32_rne(r0 * Fraction(s))
+        want = _f32_rne(Fraction(x) * Fraction(r))
+        assert L.orc_silu_f32(x) == want, (x, n)
+
+
+def test_frecps_is_one_fused_rounding():
+    """FRECPS(d, r) = fl(2 - d r) with one rounding (FPRecipStepFused), not fl(2 - fl(d r)): on random operands of
+    the SiLU's range the two differ, and the oracle gives the fused value every time."""
+    from fractions import Fraction
+    L = O.lib()
+    rng = np.random.default_rng(12)
+    d = (1 + rng.uniform(0, 2 ** 20, 3000)).astype(np.float32)
+    r = np.array([L.orc_frecpe(float(v)) for v in d], np.float32)
+    differ = 0
+    for dv, rv in zip(d, r):
+        fused = _f32_rne(2 - Fraction(float(dv)) * Fraction(float(rv)))
+        assert L.orc_frecps(float(dv), float(rv)) == fused
+        differ += _f32_rne(2 - Fraction(_f32_rne(Fraction(float(dv)) * Fraction(float(rv))))) != fused
+    assert differ > 100, differ
+
+
+def test_dequant_order_discriminated():
+    """y = fl(fl(f * fl(sw * sa)) + b) (src/gemm_s8n.c:105-114: vmulq(vcvtq(acc), vmulq(sw, sa)), then + b, three
+    roundings, no fusion), checked in exact arithmetic on entries where the other orders give other floats."""
+    from fractions import Fraction
+    rng = np.random.default_rng(8)
+    M, K, N = 48, 72, 40
+    x = (rng.standard_normal((M, K)) * rng.uniform(0.1, 30, (M, 1))).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * rng.uniform(0.01, 3, (N, 1))).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) * 5
+    pk = s8pack.pack_s8(w, b)
+    _, _, Kp, Np = pk["shape"]
+    out, q, sa, za = O.pw_s8(x, pk)
+    wq = s8pack.unpack_panels(pk["q"], Np, Kp).astype(np.int64)
+    acc = q[:M].astype(np.int64) @ wq.T - za[:M, None].astype(np.int64) * pk["cs"][None, :Np]
+    F = Fraction
+    decisive = 0
+    for m in range(M):
+        for n in range(N):
+            f = _f32_rne(F(int(acc[m, n])))
+            sw_, sa_, bb = float(pk["sw"][n]), float(sa[m]), float(pk["b"][n])
+            ref = _f32_rne(F(_f32_rne(F(f) * F(_f32_rne(F(sw_) * F(sa_))))) + F(bb))
+            others = {
+                _f32_rne(F(_f32_rne(F(_f32_rne(F(f) * F(sw_))) * F(sa_))) + F(bb)),
+                _f32_rne(F(_f32_rne(F(_f32_rne(F(f) * F(sa_))) * F(sw_))) + F(bb)),
+                _f32_rne(F(f) * F(_f32_rne(F(sw_) * F(sa_))) + F(bb)),
+            }
+            assert float(out[m, n]) == ref, (m, n)
+            decisive += ref not in others
+    assert decisive >= 100, decisive
