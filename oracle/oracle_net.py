@@ -104,6 +104,15 @@ class OracleNet:
                          res=res, b16=np.asarray(t[2]).view(np.float16)[:Np])
         self.put(bufs[b[1]], out)
 
+    # PROTO_S8: buffers [cells, logits, q, colmax], tensors [q panels, sw, n4, clsw, clsb, eps]
+    def op_35(self, var, b, t, p, bufs):
+        N, K, Kp, Np, P_, C, ld, nc, ppc = p
+        x = bufs[b[0]][:P_ * ld].reshape(P_, ld)
+        rc, lg, cm, _ = O.proto_s8(x, C, float(np.asarray(t[5]).reshape(-1)[0]), t[0], t[1][:Np], Np, Kp,
+                                   np.asarray(t[3]).reshape(-1), t[4], nc, ppc)
+        self.put(bufs[b[1]], lg)
+        self.put(bufs[b[3]], cm)
+
     # GEMV (variant 0: fp32 weights, 1: fp16 weights)
     def op_15(self, var, b, t, p, bufs):
         N, K, act = p
