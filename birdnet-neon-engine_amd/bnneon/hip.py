@@ -60,6 +60,7 @@ _SIGS = {
                            C.POINTER(Epi32), vp]),
     "bnh_pw_s8": (i32, [vp, i64, i32, i32, vp, i64, vp, i64, vp, i64, vp,
                         i64, i32, vp, C.POINTER(Epi32), vp]),
+    "bnh_pw_s8_static": (i32, [vp, i64, i32, i32, vp, i64, i32, vp, C.POINTER(Epi32), vp]),
     "bnh_s8p_new": (vp, [i32, i32, vp, vp]),
     "bnh_s8p_free": (None, [vp]),
     "bnh_quant_cells": (i32, [vp, i64, i32, i32, i32, C.c_float, vp, i64, i32,

@@ -83,6 +83,14 @@ int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, long long sa_
 int bnh_pw_s8(const float *in, long long in_ws, int lda, int M, const float *gate, long long gate_ws, int8_t *q,
               long long q_ws, float *sa, long long sa_ws, int32_t *za, long long za_ws, int B, const bnh_s8w *W,
               const bnh_epi32 *e, void *stream);
+/* bnh_pw_s8 without a workspace and without any device allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, serving loops or harnesses that forbid hipMalloc).
+ * The quantized rows, scales and zero points live in a library-owned static device array of 64 MiB per device:
+ * B * M * Kp + 8 * B * M bytes (each part rounded up to 256) must fit, else -1 with a message and nothing launched.
+ * Calls on one device share that array, so calls that overlap on one device (other streams, other threads) race;
+ * each call rewrites every part of it that it reads. Same outputs as bnh_pw_s8, bit for bit. */
+int bnh_pw_s8_static(const float *in, long long in_ws, int lda, int M, const float *gate, long long gate_ws, int B,
+                     const bnh_s8w *W, const bnh_epi32 *e, void *stream);
 
 /* ------------------------------------------------------------------ int8 prototype head (PROTO_S8)
  * Prototypes from the package tensors of PROTO_S8 (src/rt_ops_s8n.c:212-236): qw int8 [Np/4][Kp/16][4][16] and sw
