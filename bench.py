@@ -97,7 +97,37 @@ def time_steps(H, stream, launch, steps, warmup):
 
 
 def cpu_threads():
-    return max(1, min(16, os.cpu_count() or 1))
+    """Worker threads of the CPU legs: every host core this process may use, at most 16 (a GPU box grants one
+    GPU's job a 16-thread CPU share, whatever os.cpu_count() reports there)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def host_description():
+    """The host the CPU legs ran on: core counts, CPU model and the oracle's compiler."""
+    import subprocess
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        cc = subprocess.run(["gcc", "--version"], capture_output=True, text=True).stdout.splitlines()[0]
+    except (OSError, IndexError):
+        cc = "unknown"
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    return {"nproc": os.cpu_count(), "usable_cores": affinity, "threads_used": cpu_threads(), "cpu_model": model,
+            "oracle_compiler": cc + " -O2 -ffp-contract=off"}
 
 
 def cpu_baseline_gemm_s8_requant(w, bias, mult, shift, rng):
@@ -133,6 +163,36 @@ def cpu_baseline_pw_s8(pk, rng):
             "sample": f"{n_win} windows of PW_S8 1152->256 x 1536 pixels (quantize + GEMM + "
                       f"dequant + SiLU), one window per thread ({T} threads), scalar C oracle; "
                       f"{dt:.2f} s wall"}
+
+
+def gemm_s8_leg(H, rng, B, stream, steps, warmup, check_windows=(0, -1)):
+    """The int8 pointwise GEMM of the second half of the metric: 1152 -> 256 channels over 24 x 64 pixels per window,
+    int8 NCHW activations with zero point -128, per-channel Q31 requant (k_gemm_s8_requant4), B windows per launch,
+    timed with events on `stream`; windows check_windows of the batch are compared with the oracle bit for bit."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    N, K, M = 256, 1152, 1536
+    w, x, bias, mult, shift = config0_inputs(rng, B)
+    Wq = H.Q8Weights(w, bias, mult, shift, -128, -128)
+    dx = H.DeviceArray.from_host(x)
+    dout = H.DeviceArray.zeros((B, N, M), np.int8)
+
+    def launch():
+        H.check(H.lib().bnh_gemm_s8_requant(Wq.h, dx.ptr, K * M, M, B, dout.ptr, N * M, stream))
+    ms, _ = time_steps(H, stream, launch, steps, warmup)
+    got = dout.numpy()
+    ok = [bool(np.array_equal(got[i], O.gemm_s8_requant(w, x[i], bias, mult, shift, -128, -128)))
+          for i in check_windows]
+    nbytes = B * (K * M + N * M) + N * K + 3 * 4 * N
+    ops = 2.0 * B * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"kernel": "k_gemm_s8_requant4",
+            "launch": f"int8 1x1 conv {K}->{N} over 24x64 px x {B} windows, NCHW, Q31 requant, int8 out",
+            "ms_per_launch": round(ms, 4), "tops": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
+            "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_launch": nbytes, "ops_per_launch": int(ops),
+            "parity_windows": f"{sum(ok)}/{len(ok)} bit-exact vs the oracle (windows {list(check_windows)})"}
 
 
 def same_pads(n, k, s):
@@ -425,23 +485,29 @@ def perch_counts(net):
     return ops, big
 
 
-def cpu_baseline_perch(pn, rng):
-    """The oracle's op-by-op run of the same package, one window per thread, on a bounded sample."""
+def cpu_baseline_perch(pn, pcms, n_one=6):
+    """The oracle's op-by-op run of the same package on the host cores: len(pcms) windows one per thread on
+    cpu_threads() threads (about 10 s), then n_one of them on one thread. Returns (baseline dict, the oracle's
+    logits of every window in pcms)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle_net
-    from bnneon import perchnet
     T = cpu_threads()
-    n_win = 8 * T   # about 10 s of the host's cores
     on = oracle_net.OracleNet(pn.net, 0, pn.net.last, pn.emb_buf)
-    pcms = [perchnet.signal(rng) for _ in range(n_win)]
     t0 = time.perf_counter()
     with concurrent.futures.ThreadPoolExecutor(T) as ex:
-        list(ex.map(lambda i: on.run(pcms[i]), range(n_win)))
+        outs = list(ex.map(lambda p: on.run(p)[0].copy(), pcms))
     dt = time.perf_counter() - t0
-    return {"value": round(n_win / dt, 3), "unit": "windows/s", "cores": T, "kind": "port",
-            "sample": f"{n_win} windows of the same package through the scalar C oracle's op-by-op "
-                      f"restatement (log-mel, stem, 26 blocks, head), one window per thread ({T} threads), "
-                      f"-O2 -ffp-contract=off; {dt:.2f} s wall"}
+    t1 = time.perf_counter()
+    for p in pcms[:n_one]:
+        on.run(p)
+    dt1 = time.perf_counter() - t1
+    base = {"value": round(len(pcms) / dt, 3), "unit": "windows/s", "cores": T, "kind": "port",
+            "sample": f"{len(pcms)} windows of the same package through the scalar C oracle's op-by-op restatement "
+                      f"(log-mel, stem, 26 blocks, head), one window per thread ({T} threads); {dt:.2f} s wall",
+            "one_thread": {"value": round(n_one / dt1, 3), "unit": "windows/s", "cores": 1,
+                           "sample": f"{n_one} of those windows on one thread; {dt1:.2f} s wall"},
+            "host": host_description()}
+    return base, outs
 
 
 def run_perch(a, H, rng, B, stream):
@@ -455,8 +521,11 @@ def run_perch(a, H, rng, B, stream):
     os.unlink(path)
     os.rmdir(tmp)
     nc, ne, ns = m.info.n_classes, m.info.emb_dim, m.info.n_samples
-    pcm = np.stack([perchnet.signal(rng) for _ in range(min(B, 16))])
-    pcm = np.concatenate([pcm] * ((B + len(pcm) - 1) // len(pcm)))[:B]
+    # the batch: n_distinct synthetic windows, repeated; the CPU leg scores the same windows on the oracle and the
+    # GPU's logits of every window of the batch (both sub-batches) are compared with them bit for bit
+    n_distinct = min(B, 8 * cpu_threads())
+    pcms = [perchnet.signal(rng) for _ in range(n_distinct)]
+    pcm = np.stack([pcms[i % n_distinct] for i in range(B)])
     dx = H.DeviceArray.from_host(pcm)
     dout = H.DeviceArray.zeros((B, nc), np.float32)
     demb = H.DeviceArray.zeros((B, ne), np.float32)
@@ -468,6 +537,7 @@ def run_perch(a, H, rng, B, stream):
         if r != 0:
             raise RuntimeError(f"bnn_infer_batch_device returned {r}: {L.bnn_last_error()}")
     ms, wall = time_steps(H, stream, launch, a.steps, a.warmup)
+    logits = dout.numpy()
     ops_win, _ = perch_counts(pn.net)
     value = B / (ms * 1e-3)
     tops = ops_win * B / (ms * 1e-3) / 1e12
@@ -487,17 +557,24 @@ def run_perch(a, H, rng, B, stream):
     }
     line["roofline"] = perch_roofline(H, pn, B, stream, a)
     m.close()
+    line["gemm_s8"] = gemm_s8_leg(H, rng, B, stream, max(10, a.steps), 3)
     if not a.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_perch(pn, rng)
+        line["cpu_baseline"], ref = cpu_baseline_perch(pn, pcms)
+        same = [bool(np.array_equal(logits[w].view(np.uint32), ref[w % n_distinct][:nc].view(np.uint32)))
+                for w in range(B)]
+        line["parity_windows"] = f"{sum(same)}/{B} windows' logits bit-identical to the oracle's"
     print(json.dumps(line), flush=True)
 
 
-# The fused kernel's launch below (24 -> 144 expansion into the 3 x 3 stride-2 depthwise, 249 x 63 -> 125 x 32 pixels,
-# 256 windows), from rocprofv3 --pmc runs of this bench (profiles/k_pwdw_f32_24to144_dw3s2_249x63_b256.md): HBM bytes
-# per launch (FETCH_SIZE x 2 + WRITE_SIZE, the copy-kernel calibration) and the VALU issue share (SQ_INSTS_VALU x 4
-# cycles per wave64 instruction on a 16-lane SIMD over the launch's SIMD-cycles at 2.4 GHz)
+# Counter figures of the fused kernel's launch below (24 -> 144 expansion into the 3 x 3 stride-2 depthwise,
+# 249 x 63 -> 125 x 32 pixels, 256 windows), from rocprofv3 --pmc runs of this bench, named with their source:
+# HBM bytes per launch (FETCH_SIZE x 2 + WRITE_SIZE, the copy-kernel calibration) and the VALU wave instructions per
+# launch. The VALU issue share is computed in the run from the instruction count and this run's launch time: a wave64
+# VALU instruction occupies a 16-lane SIMD for 4 cycles; the chip has 1,024 SIMDs at 2.4 GHz.
+PERCH_PWDW_PROFILE = "profiles/k_pwdw_f32_24to144_dw3s2_249x63_b256.md"
 PERCH_PWDW_TRAFFIC = 774989248
-PERCH_PWDW_VALU_BUSY = 0.92
+PERCH_PWDW_VALU_INSTS = 508447744
+SIMDS, SCLK_HZ = 1024, 2.4e9
 
 
 def perch_pairs(net):
@@ -544,13 +621,17 @@ def perch_roofline(H, pn, B, stream, a):
     ms, _ = time_steps(H, stream, launch, max(10, a.steps), 3)
     nbytes = B * M * (Kp + 8) + B * o_ws * 4 + Np * Kp + 12 * Np + (k * k + 1) * C * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
+    valu_busy = PERCH_PWDW_VALU_INSTS * 4 / (ms * 1e-3 * SCLK_HZ * SIMDS)
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": PERCH_PWDW_TRAFFIC,
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": PERCH_PWDW_TRAFFIC if B == 256 else None,
             "kernel": "k_pwdw_f32",
             "launch": f"PW_S8 {K}->{N} expansion fused into the {k}x{k}/{s} depthwise, {Hh}x{Wd} -> {Ho}x{Wo} px "
                       f"x {B} windows",
             "ms_per_launch": round(ms, 4), "algorithmic_bytes_per_launch": nbytes,
-            "limiter": "VALU issue", "valu_busy": PERCH_PWDW_VALU_BUSY}
+            "limiter": {"resource": "VALU issue", "frac": round(valu_busy, 3),
+                        "valu_wave_insts_per_launch": PERCH_PWDW_VALU_INSTS,
+                        "note": "frac = VALU wave instructions x 4 cycles / (this run's launch time x 2.4 GHz x "
+                                "1,024 SIMDs); instruction count and traffic from " + PERCH_PWDW_PROFILE}}
 
 
 def v24_counts(net):
