@@ -15,6 +15,9 @@ windows already resident in HBM):
                    log-mel 257 x 96 -> stem -> 16 MBConv blocks (exact fp16
                    1x1 convs, fp16 depthwise, fp16 SE) -> 1024 embedding ->
                    6,522-class fp16-weight linear head, batch 256 windows.
+  proto_s8         the int8 prototype head (PROTO_S8) at Perch v2's shape:
+                   64 cells x 1536 channels per window against 59,180
+                   int8 prototypes (14,795 classes x 4), batch 256 windows.
   gemm_s8_requant  the int8 pointwise convolution 1152 -> 256 over
                    24 x 64 pixels per window, int8 NCHW activations with zero
                    point -128, per-channel Q31 requant, batch 256 windows.
@@ -58,7 +61,8 @@ def parse():
     ap.add_argument("--batch", type=int, default=None,
                     help="windows per launch (256; 64 for the depthwise workloads)")
     ap.add_argument("--workload", default="perch_s8",
-                    choices=["perch_s8", "v24_f16", "gemm_s8_requant", "pw_s8", "dw_f16", "dw_s8", "wino_f16", "copy"])
+                    choices=["perch_s8", "v24_f16", "gemm_s8_requant", "pw_s8", "proto_s8", "dw_f16", "dw_s8",
+                             "wino_f16", "copy"])
     ap.add_argument("--k", type=int, default=5, choices=[3, 5], help="depthwise kernel size")
     ap.add_argument("--s", type=int, default=1, choices=[1, 2], help="depthwise stride")
     ap.add_argument("--no-cpu", action="store_true",
@@ -294,6 +298,9 @@ def main():
     if a.workload == "v24_f16":
         run_v24(a, H, rng, B, stream)
         return
+    if a.workload == "proto_s8":
+        run_proto(a, H, rng, B, stream)
+        return
     if a.workload == "gemm_s8_requant":
         w, x, bias, mult, shift = config0_inputs(rng, B)
         Wq = H.Q8Weights(w, bias, mult, shift, -128, -128)
@@ -470,6 +477,83 @@ def run_wino(a, H, rng, B, stream):
     L.bnh_wino16_free(P)
     print(json.dumps(line), flush=True)
 
+
+
+def run_proto(a, H, rng, B, stream):
+    """The int8 prototype head (PROTO_S8) at Perch v2's shape: per window 64 cells of 1536 channels (fp32, as the
+    body leaves them) against 14,795 classes x 4 prototypes. Timed: cell quantization + column-max GEMM + logits per
+    step; the column-max GEMM (k_proto_gemm64, the MFMA-bound kernel) also alone, for the roofline."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    from bnneon import s8pack
+    P, C, nc, ppc = 64, 1536, 14795, 4
+    N = nc * ppc
+    protos = rng.standard_normal((N, C)).astype(np.float32)
+    clsw = rng.uniform(0, 1, N).astype(np.float32)
+    clsb = (rng.standard_normal(nc) * 0.1).astype(np.float32)
+    Kp, Np = s8pack.r16(C), (N + 3) // 4 * 4
+    q, sw = s8pack.quant_rows_s8(protos)
+    qp = np.zeros((Np, Kp), np.int8)
+    qp[:N, :C] = q
+    swp = np.zeros(Np, np.float32)
+    swp[:N] = sw
+    qw = s8pack.pack_panels(qp)
+    L = H.lib()
+    W = L.bnh_s8p_new(Np, Kp, qw.ctypes.data, swp.ctypes.data)
+    if not W:
+        H.check(None, "bnh_s8p_new")
+    n_distinct = min(B, 2 * cpu_threads())
+    cells = [np.maximum(rng.standard_normal((P, C)), 0).astype(np.float32) for _ in range(n_distinct)]
+    dx = H.DeviceArray.from_host(np.stack([cells[i % n_distinct] for i in range(B)]))
+    dqa = H.DeviceArray.zeros((B, P * Kp), np.int8)
+    dsx = H.DeviceArray.zeros((B, P), np.float32)
+    dcm = H.DeviceArray.zeros((B, Np), np.float32)
+    dlg = H.DeviceArray.zeros((B, nc), np.float32)
+    dcw = H.DeviceArray.from_host(clsw)
+    dcb = H.DeviceArray.from_host(clsb)
+
+    def quant():
+        H.check(L.bnh_quant_cells(dx.ptr, P * C, P, C, C, 1e-5, dqa.ptr, P * Kp, Kp, dsx.ptr, P, B, stream))
+
+    def colmax():
+        H.check(L.bnh_proto_colmax(dqa.ptr, P * Kp, dsx.ptr, P, P, W, dcm.ptr, Np, B, stream))
+
+    def head():
+        quant()
+        colmax()
+        H.check(L.bnh_proto_logits(dcm.ptr, Np, dcw.ptr, dcb.ptr, nc, ppc, dlg.ptr, nc, B, None, 7, stream))
+    ms, wall = time_steps(H, stream, head, a.steps, a.warmup)
+    logits = dlg.numpy()
+    ms_gemm, _ = time_steps(H, stream, colmax, max(10, a.steps), 3)
+    ops = 2.0 * B * P * C * N
+    tops = ops / (ms_gemm * 1e-3) / 1e12
+    line = {
+        "metric": "windows/s (int8 prototype head, batch 256)", "value": round(B / (ms * 1e-3), 1),
+        "unit": "windows/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: ReLU(N(0,1)) cells, N(0,1) prototypes quantized per row",
+        "config": {"workload": "PROTO_S8 at Perch v2's head: 64 cells x 1536 channels per window, 14,795 classes x "
+                               "4 prototypes (59,180 x 1536 int8), cell quantization + column maxima + logits",
+                   "global_batch": B, "parallelism": "1 GPU, windows batched per launch",
+                   "wall_s_timed_region": round(wall, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None, "kernel": "k_proto_gemm64",
+                     "ms_per_launch": round(ms_gemm, 4), "ops_per_launch": int(ops),
+                     "algorithmic_bytes_per_launch": B * P * (Kp + 4) + Np * (Kp + 4) + B * Np * 4},
+    }
+    if not a.no_cpu:
+        T = cpu_threads()
+        t0 = time.perf_counter()
+        with concurrent.futures.ThreadPoolExecutor(T) as ex:
+            ref = list(ex.map(lambda c: O.proto_s8(c, C, 1e-5, qw, swp, Np, Kp, clsw, clsb, nc, ppc)[1], cells))
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(n_distinct / dt, 3), "unit": "windows/s", "cores": T, "kind": "port",
+                                "sample": f"{n_distinct} windows of the head through the scalar C oracle, one window "
+                                          f"per thread ({T} threads); {dt:.2f} s wall", "host": host_description()}
+        same = [bool(np.array_equal(logits[w].view(np.uint32), ref[w % n_distinct].view(np.uint32))) for w in range(B)]
+        line["parity_windows"] = f"{sum(same)}/{B} windows' logits bit-identical to the oracle's"
+    L.bnh_s8p_free(W)
+    print(json.dumps(line), flush=True)
 
 
 def perch_counts(net):

@@ -3,21 +3,28 @@
 // whose epilogue keeps only the column maxima over each window's cells, and the class logits. Bit-identical to the
 // reference (exact int32 sums; the max is exact and order-free; every float op as the reference rounds it).
 //
-// Prototypes are repacked at load from [Np/4][Kp/16][4][16] into rows [Npt][Kp] (Npt = Np rounded up to 256, zero
-// rows past Np). A block computes one window's cells (row tiles of 64, running max) against 256 prototypes; blockIdx.x
-// runs over windows so that concurrently resident blocks share one prototype tile.
+// Prototypes are repacked at load from [Np/4][Kp/16][4][16] into K-blocks of 16 prototypes x 64 channels (1 KB each,
+// prototype-group-major), zero past Np (rounded up to 256) and Kp (rounded up to 64). Two column-max kernels: k_proto_gemm64, the batched GEMM over every window's cells at once (64 cells
+// per window), and k_proto_colmax, one window per block, for other cell counts.
+#include <stdlib.h>
 #include <string.h>
 
 #include "bnh_internal.h"
+#include "bnh_lds_dma.h"
 #include "bnh_num.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct bnh_s8p {
-  int Np, Kp, Npt;
-  int8_t *w;  // [Npt][Kp]
-  float *sw;  // [Npt]
+  int Np, Kp, Npt, Kt;  // Npt = Np rounded up to 256, Kt = Kp rounded up to 64
+  int8_t *w;            // K-blocked: prototype n, byte k at ((n / 16) (Kt / 64) + k / 64) 1024 + (n % 16) 64 + k % 64,
+                        // zero past Np and Kp
+  float *sw;            // [Npt]
 };
+// byte offset of prototype n, channel k in the K-blocked rows
+static inline size_t s8p_at(int n, int k, int Kt) {
+  return ((size_t)(n >> 4) * (Kt >> 6) + (k >> 6)) * 1024 + (n & 15) * 64 + (k & 63);
+}
 
 // ------------------------------------------------------------------ cell quantization (pc_quant_cells_f32)
 // One wave per cell. The reference's sum of squares is 8 fused chains (channel c feeds chain c % 8, in order of c):
@@ -92,7 +99,8 @@ __global__ __launch_bounds__(256) void k_proto_colmax(const int8_t *__restrict__
   const int kc = (lane >> 4) * 16;
   const int8_t *aw = qa + win * qa_ws;
   const float *sxw = sx + win * sx_ws;
-  const int8_t *bp = wt + (long long)(n0 + (lane & 15)) * Kp + kc;
+  const long long kblk = (long long)((Kp + 63) >> 6) * 1024;  // one 16-prototype group of the K-blocked rows
+  const int8_t *bp = wt + (long long)(n0 >> 4) * kblk + (lane & 15) * 64 + kc;  // + j kblk + k / 64 1024
   float run[4] = {-__builtin_inff(), -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
   const int kmain = Kp & ~63;
   for (int r0 = 0; r0 < P; r0 += 64) {
@@ -113,7 +121,7 @@ __global__ __launch_bounds__(256) void k_proto_colmax(const int8_t *__restrict__
 #pragma unroll
       for (int t = 0; t < 4; t++) a[t] = *(const v4i *)(ap[t] + k);
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = *(const v4i *)(bp + (long long)16 * j * Kp + k);
+      for (int j = 0; j < 4; j++) b[j] = *(const v4i *)(bp + j * kblk + (k >> 6) * 1024);
 #pragma unroll
       for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -125,7 +133,7 @@ __global__ __launch_bounds__(256) void k_proto_colmax(const int8_t *__restrict__
 #pragma unroll
       for (int t = 0; t < 4; t++) a[t] = in ? *(const v4i *)(ap[t] + kmain) : (v4i){0, 0, 0, 0};
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = in ? *(const v4i *)(bp + (long long)16 * j * Kp + kmain) : (v4i){0, 0, 0, 0};
+      for (int j = 0; j < 4; j++) b[j] = in ? *(const v4i *)(bp + j * kblk + (kmain >> 6) * 1024) : (v4i){0, 0, 0, 0};
 #pragma unroll
       for (int t = 0; t < 4; t++)
 #pragma unroll
@@ -148,6 +156,191 @@ __global__ __launch_bounds__(256) void k_proto_colmax(const int8_t *__restrict__
     const float m = wave16_max_cols(run[j]);
     const int n = n0 + 16 * j + (lane & 15);
     if (lane < 16 && n < Np) colmax[win * cm_ws + n] = m * sw[n];
+  }
+}
+
+// ------------------------------------------------------------------ column maxima as one batched GEMM
+// The cells of all windows (64 per window: rows win * 64 + p of the product) times all prototypes, K = Kp, in tiles
+// of 256 cells (4 windows) x 256 prototypes. Persistent blocks, one per CU; 4 waves of 128 cells (2 windows) x 128
+// prototypes = 8 x 8 i8 MFMA tiles each (256 accumulators in AGPRs). The K slices (64 bytes of k) of every tile a
+// block owns form one 4-stage LDS ring (32 KB a stage) fed by direct global -> LDS loads issued three slices ahead,
+// so a tile's epilogue runs while the next tile's first slices load. In LDS both operands are [row][64 bytes] with
+// XOR-swizzled 16-byte chunks (chunk c of row r at r * 64 + 16 (c ^ ((r >> 1) & 3))): a DMA instruction's 64 lanes
+// fill 16 whole rows, and the 16 rows one ds_read_b128 phase serves land on distinct banks. The prototypes are stored
+// K-blocked (see bnh_s8p), so each of their DMA instructions reads 1 KB of contiguous memory.
+//
+// Tile order: the tile grid (cell tiles x prototype tiles) is cut into 8 regions, one per XCD (blocks b, b + 8, ...
+// run on XCD b % 8), 8 x 1 when there are at least 8 cell tiles (each XCD's cells stay in its L2 while it streams every
+// prototype once), fewer cell parts and more prototype parts for small batches. Within a region the tiles go
+// prototype-major, and the blocks of an XCD run through the same K slices at about the same time, so a slice one
+// block fetches is an L2 hit for the others.
+//
+// Epilogue (pc_proto_colmax_s8n, src/proto_s8n.c:139-164): per window and prototype, the maximum over the window's 64
+// cells of (float)acc * sx (one rounding each; the maximum is exact and order-free), times sw. The maximum is the
+// IEEE 754-2019 maximum (v_maximum3_f32, two elements per instruction): like the reference's FMAX it returns NaN when
+// either operand is NaN and orders -0 below +0; only the payload of a NaN may differ (such a window fails either way).
+// The tile's 256 cell scales and 256 prototype scales reach LDS by DMA with the tile's first K slice
+// (double-buffered by tile parity).
+#define PG_TM 256
+#define PG_TN 256
+#define PG_BK 64
+#define PG_AB (PG_TM * PG_BK)
+#define PG_STAGE (PG_AB + PG_TN * PG_BK)
+#define PG_NST 4
+#define PG_SCL (PG_NST * PG_STAGE)  // 2 x (256 sx + 256 sw) floats after the ring
+typedef __attribute__((address_space(3))) v4i lds_v4i;
+typedef __attribute__((address_space(3))) float lds_f32;
+
+// the saddr form of the LDS DMA: a wave-uniform 64-bit base (SGPRs) plus a 32-bit per-lane byte offset
+BNH_DEV void pg_dma16(const void *base, uint32_t off, const lds_i8 *dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
+}
+
+BNH_DEV float pg_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// an accumulator element read out of its AGPR where the epilogue uses it: without this the compiler copies all 256
+// accumulators into VGPRs when the K loop ends and spills the block's other values to scratch
+BNH_DEV int32_t pg_acc(int32_t x) {
+  int32_t v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(x));
+  return v;
+}
+
+// tile i of this block in its region: cell tile m_t, prototype tile n_t
+struct PgRegion {
+  int lid, nlb, m_lo, mx, n_lo;
+  __device__ void tile(int i, int &m_t, int &n_t) const {
+    const int u = lid + i * nlb;
+    m_t = m_lo + u % mx;
+    n_t = n_lo + u / mx;
+  }
+};
+
+__global__ __launch_bounds__(256, 1) void k_proto_gemm64(const int8_t *__restrict__ qa, long long qa_ws,
+                                                        const float *__restrict__ sx, long long sx_ws, int B, int Kp,
+                                                        const int8_t *__restrict__ wt, const float *__restrict__ sw,
+                                                        int Np, int n_mt, int n_nt, float *__restrict__ colmax,
+                                                        long long cm_ws) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds_raw[PG_SCL + 2 * 2048];
+  lds_i8 *lds = (lds_i8 *)lds_raw;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  // this block's region of the tile grid and its tiles in it
+  const int xcd = (int)(blockIdx.x & 7);
+  PgRegion R;
+  R.lid = (int)(blockIdx.x >> 3);
+  R.nlb = (int)(gridDim.x >> 3);
+  const int gm = n_mt >= 8 ? 8 : n_mt >= 4 ? 4 : n_mt >= 2 ? 2 : 1, gn = 8 / gm;
+  const int rm = xcd / gn, rn = xcd % gn;
+  R.m_lo = rm * n_mt / gm;
+  R.mx = (rm + 1) * n_mt / gm - R.m_lo;
+  R.n_lo = rn * n_nt / gn;
+  const int nx = (rn + 1) * n_nt / gn - R.n_lo;
+  const int xtiles = R.mx * nx;
+  const int mytiles = xtiles > R.lid ? (xtiles - 1 - R.lid) / R.nlb + 1 : 0;
+  const int steps = Kp / PG_BK;
+  // DMA lane roles: an instruction fills 16 rows of 64 bytes, lane -> row lane / 4, its 16-byte slot lane % 4
+  // holding k chunk (lane % 4) ^ ((lane / 8) % 4). Per K slice a wave issues 4 cell instructions (rows 64 wave ..
+  // 64 wave + 63 of the tile: window m_t 4 + wave) and 4 prototype instructions (rows 64 wave .. 64 wave + 63).
+  const int dchunk = 16 * ((lane & 3) ^ ((lane >> 3) & 3));
+  const uint32_t loff_a = (uint32_t)((lane >> 2) * Kp + dchunk);  // cell rows: Kp apart
+  const uint32_t loff_b = (uint32_t)((lane >> 2) * PG_BK + dchunk);  // a K-blocked 16-row group: 64 bytes apart
+  const long long a16 = 16LL * Kp, b16 = (long long)(Kp / PG_BK) * 1024;  // the next 16 rows of each operand
+  // Issue state, advanced incrementally (the scalar unit is shared by the CU's waves): the next (tile, K step) to
+  // issue, the stage it fills, and the tile's operand bases.
+  int iss_i = 0, iss_k = 0, iss_st = 0;
+  const int8_t *a_tile = qa, *b_tile = wt;
+  auto issue = [&]() {
+    if (iss_k == 0) {  // a new tile: its operand bases and scales
+      int m_t, n_t;
+      R.tile(iss_i, m_t, n_t);
+      int win = m_t * 4 + wave;
+      if (win > B - 1) win = B - 1;  // cells past the last window: valid memory, results dropped
+      a_tile = qa + (long long)win * qa_ws;
+      b_tile = wt + (long long)(n_t * 16 + 4 * wave) * b16;
+      if (wave < 2) {  // the tile's scales: wave 0 the cell scales, wave 1 the prototype scales
+        lds_i8 *sc = lds + PG_SCL + (iss_i & 1) * 2048 + wave * 1024;
+        if (wave == 0) {
+          const int last = B - 1 - m_t * 4;  // windows past the last one read the last window's scales (unused)
+          const int wl = (lane >> 4) < last ? (lane >> 4) : last;
+          pg_dma16(sx + (long long)m_t * 4 * sx_ws, (uint32_t)(wl * sx_ws * 4 + 16 * (lane & 15)), sc);
+        } else {
+          pg_dma16(sw + n_t * PG_TN, (uint32_t)(16 * lane), sc);
+        }
+      }
+    }
+    lds_i8 *st = lds + iss_st * PG_STAGE;
+    const int8_t *ab = a_tile + iss_k * PG_BK, *bb = b_tile + iss_k * 1024;
+#pragma unroll
+    for (int h = 0; h < 4; h++) pg_dma16(ab + h * a16, loff_a, st + (4 * wave + h) * 1024);
+#pragma unroll
+    for (int h = 0; h < 4; h++) pg_dma16(bb + h * b16, loff_b, st + PG_AB + (4 * wave + h) * 1024);
+    if (++iss_st == PG_NST) iss_st = 0;
+    if (++iss_k == steps) { iss_k = 0; iss_i++; }
+  };
+  // fragment reads: row r of a stage's operand at r * 64 + 16 (chunk ^ ((r >> 1) & 3)); for the rows 16 t + (lane & 15)
+  // of a wave's tile the swizzle depends on the lane only, so tile t is an immediate offset t * 1024
+  const int g = lane >> 4, j16 = lane & 15;
+  const int foff = j16 * PG_BK + 16 * (g ^ ((j16 >> 1) & 3));
+  const int fa_off = wm * 128 * PG_BK + foff, fb_off = PG_AB + wn * 128 * PG_BK + foff;
+  const int total = mytiles * steps;
+  for (int gs = 0; gs < PG_NST - 1 && gs < total; gs++) issue();
+  int gs = 0, cst = 0;  // the global step being computed and its stage
+  for (int ci = 0; ci < mytiles; ci++) {
+    v4i acc[8][8];
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++) acc[t][jj] = (v4i){0, 0, 0, 0};
+    for (int ck = 0; ck < steps; ck++, gs++) {
+      // this wave's loads of step gs have landed once at most those of the two later steps (8 a step) are
+      // outstanding; the scale loads and the epilogue's stores only make the wait longer
+      if (gs + 2 < total) RQ_WAIT_VM(16);
+      else if (gs + 1 < total) RQ_WAIT_VM(8);
+      else RQ_WAIT_VM(0);
+      RQ_BARRIER();  // every wave's loads of step gs have landed; the stage of step gs - 1 is no longer read
+      if (gs + PG_NST - 1 < total) issue();
+      const lds_i8 *st = lds + cst * PG_STAGE;
+      if (++cst == PG_NST) cst = 0;
+      const lds_i8 *pa = st + fa_off, *pb = st + fb_off;
+      v4i a[8], b[8];
+#pragma unroll
+      for (int t = 0; t < 8; t++) a[t] = *(const lds_v4i *)(pa + t * 1024);
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++) b[jj] = *(const lds_v4i *)(pb + jj * 1024);
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[jj], acc[t][jj], 0, 0, 0);
+    }
+    // ---- epilogue: acc[t][jj][r] is cell row 16 (t % 4) + 4 g + r of window m_t 4 + 2 wm + t / 4, prototype
+    // wn 128 + 16 jj + j16 of the tile
+    int m_t, n_t;
+    R.tile(ci, m_t, n_t);
+    const lds_f32 *sxs = (const lds_f32 *)(lds + PG_SCL + (ci & 1) * 2048);
+    const lds_f32 *sws = sxs + 256;
+#pragma unroll
+    for (int wl = 0; wl < 2; wl++) {
+      float srow[4][4];
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) srow[t][r] = sxs[wm * 128 + 64 * wl + 16 * t + 4 * g + r];
+      const int win = m_t * 4 + wm * 2 + wl;
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++) {
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) m = pg_max(m, (float)pg_acc(acc[4 * wl + t][jj][r]) * srow[t][r]);
+        m = pg_max(m, __shfl_xor(m, 16));
+        m = pg_max(m, __shfl_xor(m, 32));
+        const int nl = wn * 128 + 16 * jj + j16, n = n_t * PG_TN + nl;
+        if (lane < 16 && win < B && n < Np) colmax[win * cm_ws + n] = m * sws[nl];
+      }
+    }
   }
 }
 
@@ -178,8 +371,8 @@ bnh_s8p *bnh_s8p_new(int Np, int Kp, const int8_t *qw, const float *sw) {
     bnh_fail("bnh_s8p_new: Np %d Kp %d: expected Np a multiple of 4, Kp a multiple of 16, both tensors", Np, Kp);
     return nullptr;
   }
-  const int Npt = (int)bnh_round_up(Np, 256);
-  int8_t *hw = (int8_t *)calloc((size_t)Npt * Kp, 1);
+  const int Npt = (int)bnh_round_up(Np, 256), Kt = (int)bnh_round_up(Kp, 64);
+  int8_t *hw = (int8_t *)calloc((size_t)Npt * Kt, 1);
   float *hs = (float *)calloc(Npt, 4);
   bnh_s8p *W = (bnh_s8p *)calloc(1, sizeof *W);
   if (!hw || !hs || !W) {
@@ -189,11 +382,11 @@ bnh_s8p *bnh_s8p_new(int Np, int Kp, const int8_t *qw, const float *sw) {
   }
   const int kb = Kp / 16;
   for (int n = 0; n < Np; n++)
-    for (int k = 0; k < Kp; k++) hw[(size_t)n * Kp + k] = qw[((size_t)(n / 4) * kb + k / 16) * 64 + (n % 4) * 16 + k % 16];
+    for (int k = 0; k < Kp; k++) hw[s8p_at(n, k, Kt)] = qw[((size_t)(n / 4) * kb + k / 16) * 64 + (n % 4) * 16 + k % 16];
   memcpy(hs, sw, sizeof(float) * Np);
-  W->Np = Np; W->Kp = Kp; W->Npt = Npt;
-  bool ok = (W->w = (int8_t *)bnh_malloc((size_t)Npt * Kp)) && (W->sw = (float *)bnh_malloc(4 * (size_t)Npt)) &&
-            !bnh_memcpy_h2d(W->w, hw, (size_t)Npt * Kp) && !bnh_memcpy_h2d(W->sw, hs, 4 * (size_t)Npt);
+  W->Np = Np; W->Kp = Kp; W->Npt = Npt; W->Kt = Kt;
+  bool ok = (W->w = (int8_t *)bnh_malloc((size_t)Npt * Kt)) && (W->sw = (float *)bnh_malloc(4 * (size_t)Npt)) &&
+            !bnh_memcpy_h2d(W->w, hw, (size_t)Npt * Kt) && !bnh_memcpy_h2d(W->sw, hs, 4 * (size_t)Npt);
   free(hw);
   free(hs);
   if (!ok) { bnh_s8p_free(W); return nullptr; }
@@ -225,6 +418,25 @@ int bnh_proto_colmax(const int8_t *qa, long long qa_ws, const float *sx, long lo
   BNH_REQ(qa && sx && W && colmax && P > 0 && B > 0);
   BNH_REQ(((uintptr_t)qa & 15) == 0 && qa_ws % 16 == 0);
   BNH_REQ(B == 1 || (qa_ws >= (long long)P * W->Kp && cm_ws >= W->Np && sx_ws >= P));
+  // the batched GEMM: 64 cells per window, K in 64-byte slices (at least 4: the scale buffers are reused two tiles
+  // later), 16-byte aligned cell scales
+  const bool batched = P == 64 && W->Kp % PG_BK == 0 && W->Kp >= 4 * PG_BK && ((uintptr_t)sx & 15) == 0 &&
+                       (B == 1 || sx_ws % 4 == 0) && !getenv("BNH_PROTO_WINDOW");
+  if (batched) {
+    static int ncu = 0;
+    if (!ncu) {
+      int dev = 0;
+      BNH_HIP(hipGetDevice(&dev));
+      BNH_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    }
+    const int n_mt = (int)bnh_ceil_div((long long)B * 64, PG_TM), n_nt = W->Npt / PG_TN;
+    int grid = ncu / 8 * 8;  // one block per CU
+    if (grid < 8) grid = 8;
+    hipLaunchKernelGGL(k_proto_gemm64, dim3((unsigned)grid), dim3(256), 0, bnh_stream(stream), qa, B == 1 ? 0 : qa_ws, sx,
+                       B == 1 ? 0 : sx_ws, B, W->Kp, W->w, W->sw, W->Np, n_mt, n_nt, colmax, B == 1 ? 0 : cm_ws);
+    BNH_HIP(hipGetLastError());
+    return 0;
+  }
   BNH_REQ(B <= 65535 * 1024);
   dim3 grid((unsigned)B, (unsigned)(W->Npt / 256));
   hipLaunchKernelGGL(k_proto_colmax, grid, dim3(256), 0, bnh_stream(stream), qa, qa_ws, W->Kp, sx, sx_ws, P, W->w, W->sw,

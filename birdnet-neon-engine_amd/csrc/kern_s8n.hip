@@ -17,6 +17,7 @@
 
 #include "bnh_internal.h"
 #include "bnh_num.h"
+#include "bnh_lds_dma.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -600,18 +601,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_s8_requant2(const int8_t *__res
 #define RQ4_STAGE (RQ4_XB + RQ4_CH * RQ4_BK)
 #define RQ4_NST 4
 #define RQ4_NLD 4  // DMA instructions per wave per K step: 2 activation + 2 weight
-typedef __attribute__((address_space(3))) int8_t lds_i8;
 typedef int v2i __attribute__((ext_vector_type(2)));
-
-// The DMA loads are issued from inline assembly and awaited with explicit vmcnt waits: the compiler, seeing an
-// LDS-writing load, would otherwise wait for every outstanding load (vmcnt(0)) before each LDS read and serialise the
-// ring. The "memory" clobbers keep the compiler from moving LDS accesses across the waits and the barriers.
-BNH_DEV void rq_dma16(const int8_t *src, const lds_i8 *dst) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
-}
-#define RQ_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
-#define RQ_BARRIER() asm volatile("s_barrier" ::: "memory")
+// (direct global -> LDS loads: bnh_lds_dma.h)
 
 __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__restrict__ x, long long x_ws, int M, int K,
                                                           int Kt, int tpw, int nblk, int ntiles,

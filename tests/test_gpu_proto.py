@@ -51,7 +51,10 @@ def run_head(H, x, protos, clsw, clsb, nc, eps=1e-5):
     return res, (qw, swp, Np, Kp)
 
 
-@pytest.mark.parametrize("P,C,N,nc", [(4, 8, 4, 1), (12, 48, 20, 5), (64, 136, 400, 100), (100, 96, 1000, 250)])
+# (64, 256, ...) and (64, 512, ...) take the batched GEMM (64 cells per window, K in 64-byte slices); the others the
+# per-window kernel
+@pytest.mark.parametrize("P,C,N,nc", [(4, 8, 4, 1), (12, 48, 20, 5), (64, 136, 400, 100), (100, 96, 1000, 250),
+                                      (64, 256, 1000, 250), (64, 512, 2044, 511)])
 def test_head_small_shapes(hip, P, C, N, nc):
     rng = np.random.default_rng(P + C)
     B = 3
@@ -91,3 +94,28 @@ def test_head_perch_shape(hip):
         assert np.array_equal(qa[b], rqa)
         assert same(cm[b], rcm)
         assert same(lg[b], rlg)
+
+
+@pytest.mark.parametrize("B", [5, 37])
+def test_batched_gemm_matches_per_window_kernel(hip, monkeypatch, B):
+    """The batched column-max GEMM (tiles of 4 windows x 256 prototypes, split over the XCDs) against the
+    one-window-per-block kernel on every window, and both against the oracle on some: B = 5 leaves a partial cell
+    tile and splits the prototypes over XCD regions, B = 37 gives 10 cell tiles over 8 regions."""
+    H = hip
+    rng = np.random.default_rng(40 + B)
+    P, C, nc, ppc = 64, 1536, 1500, 4
+    N = nc * ppc
+    x = np.maximum(rng.standard_normal((B, P, C)), 0).astype(np.float32)
+    x[B - 1, 5, :] = 0                    # a zero cell in the last window
+    protos = rng.standard_normal((N, C)).astype(np.float32)
+    protos[7] = 0
+    clsw = rng.uniform(0, 1, N).astype(np.float32)
+    clsb = rng.standard_normal(nc).astype(np.float32)
+    say("proto batched gemm B", B)
+    (qa, sx, cm, lg, fl), (qw, swp, Np, Kp) = run_head(H, x, protos, clsw, clsb, nc)
+    monkeypatch.setenv("BNH_PROTO_WINDOW", "1")
+    (qa2, sx2, cm2, lg2, fl2), _ = run_head(H, x, protos, clsw, clsb, nc)
+    assert same(cm, cm2) and same(lg, lg2)
+    for b in (0, B // 2, B - 1):
+        rc, rlg, rcm, rqa = O.proto_s8(x[b], C, 1e-5, qw, swp, Np, Kp, clsw, clsb, nc, ppc)
+        assert same(cm[b], rcm) and same(lg[b], rlg), b
