@@ -156,7 +156,7 @@ def test_quant_rows_gate(hip):
     assert quant_case(hip, x, K, Kp, gate=g)
 
 
-def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, gate=False, ldo_extra=8):
+def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, gate=False, ldo_extra=8, rpad=0):
     H = hip
     rng = np.random.default_rng(seed)
     M = H_ * W_
@@ -170,7 +170,13 @@ def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, g
     gt = rng.uniform(0, 1, (B, K)).astype(np.float32) if gate else None
     ldo = Np + ldo_extra
     out_rows = M if not opad else (H_ + 2 * opad) * (W_ + 2 * opad)
-    rs = rng.standard_normal((B, M, Np)).astype(np.float32) if res else None
+    rrows = (H_ + 2 * rpad) * (W_ + 2 * rpad) if rpad else M
+    rs = rng.standard_normal((B, rrows, Np)).astype(np.float32) if res else None
+    if res and rpad:  # a zero-haloed residual buffer, as the runtime's haloed activations
+        rs.reshape(B, H_ + 2 * rpad, W_ + 2 * rpad, Np)[:, :rpad] = 0
+        rs.reshape(B, H_ + 2 * rpad, W_ + 2 * rpad, Np)[:, -rpad:] = 0
+        rs.reshape(B, H_ + 2 * rpad, W_ + 2 * rpad, Np)[:, :, :rpad] = 0
+        rs.reshape(B, H_ + 2 * rpad, W_ + 2 * rpad, Np)[:, :, -rpad:] = 0
     M4 = (M + 3) // 4 * 4
     Wt = H.S8Weights(N_, K_, Kp, Np, pk["q"], pk["sw"], pk["cs"], pk["b"])
     dx = H.DeviceArray.from_host(x)
@@ -182,7 +188,7 @@ def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, g
     dout = H.DeviceArray.from_host(np.full((B, out_rows * ldo), 7.0, np.float32))
     dres = H.DeviceArray.from_host(rs) if res else None
     e = H.epi32(dout, ldo, act=act, ow=W_ if opad else 0, opad=opad, res=dres,
-                ldr=Np if res else 0, out_ws=out_rows * ldo, res_ws=M * Np)
+                ldr=Np if res else 0, rpad=rpad, rw=W_ if rpad else 0, out_ws=out_rows * ldo, res_ws=rrows * Np)
     say(f"pw_s8 B{B} {H_}x{W_} K{K} N{N} act{act} opad{opad} res{res} gate{gate}")
     H.check(H.lib().bnh_pw_s8(dx.ptr, M * lda, lda, M, H.ptr(dg), K if gate else 0, dq.ptr, M4 * Kp,
                               dsa.ptr, M4, dza.ptr, M4, B, Wt.h, e, None), "pw_s8")
@@ -193,7 +199,7 @@ def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, g
     for bi in range(B):
         ref_out, rq, rsa, rza = O.pw_s8(x[bi], pk, act=act, ldo=ldo, ow=W_ if opad else 0, opad=opad,
                                         res=None if rs is None else rs[bi], ldr=Np if res else 0,
-                                        gate=None if gt is None else gt[bi])
+                                        rpad=rpad, rw=W_ if rpad else 0, gate=None if gt is None else gt[bi])
         got = out[bi].copy()
         # columns [Np, ldo) are never written: the garbage stays, as in the reference
         ok &= same_f32(got[:, :Np], ref_out[:, :Np])
@@ -215,6 +221,15 @@ def test_pw_s8_residual_halo_gate(hip):
     assert pw_case(hip, 3, 7, 9, 48, 40, 1, opad=2, res=True, lda_extra=5, seed=9)
     assert pw_case(hip, 2, 5, 6, 96, 136, 2, opad=1, seed=10, gate=True)
     assert pw_case(hip, 1, 1, 1, 24, 8, 0, seed=11)   # a single row (GEMV-like)
+
+
+def test_pw_s8_residual_quads_split_groups(hip):
+    """The residual epilogue's 16-byte-quad form (ldo and ldr multiples of 4) with three 64-channel groups, the last
+    one partial (N = 136), the groups split over blocks (few rows: gsplit > 1), and zero-haloed residual and output
+    buffers (rpad 1, opad 1), as well as an unhaloed residual into a haloed output."""
+    assert pw_case(hip, 3, 7, 9, 48, 136, 1, opad=1, res=True, rpad=1, seed=14)
+    assert pw_case(hip, 2, 6, 11, 96, 136, 0, opad=2, res=True, rpad=0, seed=15)
+    assert pw_case(hip, 2, 5, 5, 232, 200, 2, opad=0, res=True, rpad=2, seed=16, gate=True)
 
 
 def test_pw_s8_unaligned_output_rows(hip):
