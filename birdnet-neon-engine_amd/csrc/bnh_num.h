@@ -163,19 +163,57 @@ BNH_DEV unsigned bnh_xcd_block(unsigned b, unsigned n) {
 // ReLU as vmaxq_f32(y, 0): -0 -> +0, NaN stays NaN
 BNH_DEV float bnh_relu_f32(float y) { return bnh_fmax(y, 0.f); }
 
-// gemmlowp fixed point (the Q31 requant specification of the int8 GEMM / depthwise of this library), in closed
-// forms that need one 64-bit multiply-add and no branches:
+// gemmlowp fixed point (the Q31 requant specification of the int8 GEMM / depthwise of this library, shift 0..31),
+// in 32-bit forms around one 64-bit multiply-add, with no branches:
 //  * SaturatingRoundingDoublingHighMul(a, b) = (a b + nudge) / 2^31 truncated, nudge = 2^30 for a b >= 0 and
 //    1 - 2^30 below; both cases equal floor((a b + 2^30) / 2^31) (for a b < 0 the truncation of n = a b + 1 - 2^30 is
-//    floor((n + 2^31 - 1) / 2^31)); the one overflow, INT32_MIN x INT32_MIN, saturates to INT32_MAX.
-//  * RoundingDivideByPOT(x, e) (round half away from zero) = floor((x + 2^(e-1) - [x < 0]) / 2^e) for e >= 1, x for
-//    e = 0.
+//    floor((n + 2^31 - 1) / 2^31)). That floor lies in [-2^31 + 1, 2^31] and reaches 2^31, whose low 32 bits read
+//    INT32_MIN, only for INT32_MIN x INT32_MIN: the one overflow, which saturates to INT32_MAX.
+//  * RoundingDivideByPOT(x, e) (round half away from zero) = (x >> e) + [(x & mask) > (mask >> 1) + [x < 0]],
+//    mask = 2^e - 1 (for e = 0 the mask is 0 and x is returned).
 BNH_DEV int32_t bnh_requant(int32_t acc, int32_t mult, int shift, int zy, int lo, int hi) {
-  const int64_t p = (int64_t)acc * mult + (1LL << 30);
-  int32_t r = (int32_t)(p >> 31);
-  r = (acc == INT32_MIN) & (mult == INT32_MIN) ? INT32_MAX : r;
-  const int64_t t = (int64_t)r + (shift ? (1LL << (shift - 1)) - (r < 0 ? 1 : 0) : 0);
-  const int32_t v = __builtin_elementwise_add_sat((int32_t)(t >> shift), zy);
-  return v < lo ? lo : v > hi ? hi : v;
+  int32_t r = (int32_t)(uint32_t)((uint64_t)((int64_t)acc * mult + (1LL << 30)) >> 31);
+  r = r == INT32_MIN ? INT32_MAX : r;
+  const int32_t mask = (int32_t)((1u << shift) - 1u);
+  const int32_t v = (r >> shift) + ((r & mask) > (mask >> 1) + (int32_t)((uint32_t)r >> 31) ? 1 : 0);
+  // clamp(v + zy (saturating), lo, hi) for lo <= hi: the median of the three, one v_med3_i32
+  int32_t y;
+  asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y) : "v"(__builtin_elementwise_add_sat(v, zy)), "v"(lo), "v"(hi));
+  return y;
+}
+// The same for shift e in 1..31 as one rounding of the 64-bit product: floor((floor(p / 2^31) + c) / 2^e) =
+// floor((p + c 2^31) / 2^(31 + e)) for integer c, so with c = 2^(e-1) - [p < 0] and p = acc m + 2^30
+//   RDBYPOT(SRDHM(acc, m), e) = floor((acc m + 2^30 + 2^(30+e) - [p < 0] 2^31) / 2^(31+e)),
+// the high word of one 64-bit multiply-add shifted right by e - 1. [p < 0] may be read from the operands' signs:
+// where they disagree (acc m in [-2^30, 0), or a zero product with a negative operand) SRDHM is 0 and so is the
+// result either way. INT32_MIN x INT32_MIN gives 2^(31-e), the value of the saturated SRDHM, by itself. The two
+// addends per shift are taken out of the loop by the caller (BnhRqS1).
+struct BnhRqS1 {
+  int64_t a0, a1;  // 2^30 + 2^(30+e), and that minus 2^31
+  int e1;          // e - 1
+};
+BNH_DEV BnhRqS1 bnh_rq_s1(int shift) {
+  BnhRqS1 c;
+  c.a0 = (1LL << 30) + (1LL << (30 + shift));
+  c.a1 = c.a0 - (1LL << 31);
+  c.e1 = shift - 1;
+  return c;
+}
+BNH_DEV int32_t bnh_requant_s1(int32_t acc, int32_t mult, BnhRqS1 c, int zy, int lo, int hi) {
+  const int64_t q = (int64_t)acc * mult + ((acc ^ mult) < 0 ? c.a1 : c.a0);
+  const int32_t v = (int32_t)(q >> 32) >> c.e1;
+  int32_t y;
+  asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y) : "v"(__builtin_elementwise_add_sat(v, zy)), "v"(lo), "v"(hi));
+  return y;
+}
+// 4 x 4 byte transpose: r_i holds bytes (i, 0..3); c_j receives bytes (0..3, j)
+BNH_DEV void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, uint32_t c[4]) {
+  // r_i = bytes of k row i for pixels 0..3; c_j = bytes of pixel j for k rows 0..3
+  const uint32_t a_lo = __builtin_amdgcn_perm(r1, r0, 0x05010400u), a_hi = __builtin_amdgcn_perm(r1, r0, 0x07030602u);
+  const uint32_t b_lo = __builtin_amdgcn_perm(r3, r2, 0x05010400u), b_hi = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+  c[0] = __builtin_amdgcn_perm(b_lo, a_lo, 0x05040100u);
+  c[1] = __builtin_amdgcn_perm(b_lo, a_lo, 0x07060302u);
+  c[2] = __builtin_amdgcn_perm(b_hi, a_hi, 0x05040100u);
+  c[3] = __builtin_amdgcn_perm(b_hi, a_hi, 0x07060302u);
 }
 #endif

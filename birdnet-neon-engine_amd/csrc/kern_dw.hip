@@ -835,52 +835,144 @@ static int chsum_launch(const T *out, long long o_ws, int C, int Ho, int Wo, flo
 }
 
 // ------------------------------------------------------------------ int8 depthwise (own specification)
-// a thread owns 4 channels (one 32-bit word of every pixel) of one output pixel
-template <int K, int S>
-__global__ __launch_bounds__(256) void k_dw_s8(const int8_t *__restrict__ x, long long x_ws, int H, int W, int C, int pt,
-                                               int pl, const int8_t *__restrict__ w, const int32_t *__restrict__ bias,
-                                               const int32_t *__restrict__ mult, const int32_t *__restrict__ shift,
-                                               int zx, int zy, int lo, int hi, const int8_t *__restrict__ lut,
-                                               int8_t *__restrict__ out, long long o_ws, int Ho, int Wo,
-                                               long long total) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int C4 = C >> 2;
-  const int c4 = (int)(i % C4);
-  long long r = i / C4;
-  const int ox = (int)(r % Wo);
-  r /= Wo;
-  const int oy = (int)(r % Ho);
-  const int win = (int)(r / Ho);
-  const int c = c4 * 4;
-  int32_t acc[4];
+// A thread owns 4 channels (one 32-bit word of every pixel) of a strip of NP consecutive output pixels of one row,
+// numbered like the float kernels (window, row, strip, channel quad; XCD-contiguous blocks). Taps outside the image
+// read the zero point, so that w (x - zx) vanishes there and
+//   acc = bias - zx sum_t w[t] + sum_t w[t] x[t]   (mod 2^32, the specification's wrapping sum)
+// holds for every output. Per input row the thread loads the strip's columns once, transposes each 4 columns x 4
+// channels block so that a word holds 4 consecutive columns of one channel, and takes each output's taps of that row
+// as a byte-aligned window of two such words: one v_dot4 per 4 taps, the row's taps packed the same way (zero past
+// k). Loads and stores are buffer instructions: a per-lane 32-bit offset for the row plus a scalar column offset, so
+// a strip inside the image spends no vector instruction on addresses; a strip at the left or right edge (EDGE)
+// clamps its column offsets and selects the zero point outside. The activation table (LUT) sits in LDS.
+// output pixels per thread: 8 at stride 1 (the setup, the taps and the transposes shared by more outputs), 4 at 2
+__host__ __device__ constexpr int dw_s8_np(int s) { return s == 1 ? 8 : 4; }
+template <int K, int S, bool EDGE>
+BNH_DEV void dw_s8_strip(__amdgpu_buffer_rsrc_t xr, int x_off, int ix0, int H, int W, int C, int iy0, uint32_t zxw,
+                         const uint32_t (&wp)[K][(K + 3) / 4][4], int32_t (&acc)[dw_s8_np(S)][4]) {
+  constexpr int NP = dw_s8_np(S), NG = (K + 3) / 4, NCOL = (NP - 1) * S + K;
+  constexpr int ND = ((NP - 1) * S + 4 * (NG - 1)) / 4 + 2;  // 4-column words per channel and row
+  int coff[NCOL];
+  bool cok[NCOL];
 #pragma unroll
-  for (int j = 0; j < 4; j++) acc[j] = bias[c + j];
-  const int8_t *xw = x + win * x_ws;
+  for (int col = 0; col < NCOL; col++) {
+    const int ix = ix0 + col;
+    cok[col] = (unsigned)ix < (unsigned)W;
+    coff[col] = (ix < 0 ? 0 : ix >= W ? W - 1 : ix) * C;
+  }
 #pragma unroll
   for (int ky = 0; ky < K; ky++) {
-    const int iy = oy * S - pt + ky;
-    if (iy < 0 || iy >= H) continue;
+    const int iy = iy0 + ky;
+    uint32_t r[4 * ND];
 #pragma unroll
-    for (int kx = 0; kx < K; kx++) {
-      const int ix = ox * S - pl + kx;
-      if (ix < 0 || ix >= W) continue;
-      const uint32_t xv = *(const uint32_t *)(xw + ((long long)iy * W + ix) * C + c);
-      const uint32_t wv = *(const uint32_t *)(w + (long long)(ky * K + kx) * C + c);
+    for (int col = 0; col < 4 * ND; col++) r[col] = col < NCOL ? zxw : 0u;
+    if ((unsigned)iy < (unsigned)H) {
+      const int ro = x_off + iy * W * C;
 #pragma unroll
-      for (int j = 0; j < 4; j++)
-        acc[j] = (int32_t)((uint32_t)acc[j] + (uint32_t)((int32_t)(int8_t)(wv >> (8 * j)) *
-                                                          ((int32_t)(int8_t)(xv >> (8 * j)) - zx)));
+      for (int col = 0; col < NCOL; col++) {
+        if (EDGE) {
+          const uint32_t v = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(xr, ro + coff[col], 0, 0);
+          r[col] = cok[col] ? v : zxw;
+        } else {  // the lane's first column in the vector offset, the column step in the scalar one
+          r[col] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(xr, ro + ix0 * C, col * C, 0);
+        }
+      }
     }
-  }
-  uint32_t word = 0;
+    uint32_t d[ND][4];  // d[j][ch]: columns 4j..4j+3 of channel ch
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    int32_t y = bnh_requant(acc[j], mult[c + j], shift[c + j], zy, lo, hi);
-    if (lut) y = lut[y + 128];
-    word |= ((uint32_t)y & 0xffu) << (8 * j);
+    for (int j = 0; j < ND; j++) transpose4x4(r[4 * j], r[4 * j + 1], r[4 * j + 2], r[4 * j + 3], d[j]);
+#pragma unroll
+    for (int q = 0; q < NP; q++)
+#pragma unroll
+      for (int j = 0; j < NG; j++) {
+        const int o = q * S + 4 * j, b = o >> 2, sh = o & 3;
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++) {
+          const uint32_t v = sh ? __builtin_amdgcn_alignbyte(d[b + 1][ch], d[b][ch], sh) : d[b][ch];
+          acc[q][ch] = __builtin_amdgcn_sdot4((int)v, (int)wp[ky][j][ch], acc[q][ch], false);
+        }
+      }
   }
-  *(uint32_t *)(out + win * o_ws + ((long long)oy * Wo + ox) * C + c) = word;
+}
+
+template <int K, int S, bool LUT>
+__global__ __launch_bounds__(256) void k_dw_s8(const int8_t *__restrict__ x, long long x_ws, unsigned x_len, int H,
+                                               int W, int C, int pt, int pl, const int8_t *__restrict__ w,
+                                               const int32_t *__restrict__ bias, const int32_t *__restrict__ mult,
+                                               const int32_t *__restrict__ shift, int zx, int zy, int lo, int hi,
+                                               const int8_t *__restrict__ lut, int8_t *__restrict__ out,
+                                               long long o_ws, unsigned o_len, int Ho, int Wo, long long total,
+                                               DwGrid g) {
+  constexpr int NP = dw_s8_np(S), NG = (K + 3) / 4, NCOL = (NP - 1) * S + K;
+  __shared__ int8_t s_lut[256];
+  if (LUT) {
+    s_lut[threadIdx.x] = lut[threadIdx.x];
+    __syncthreads();
+  }
+  const DwPos ps = dw_pos(C >> 2, Ho, total, g);
+  if (!ps.ok) return;
+  const int c = ps.c * 4, oy = ps.oy, px0 = ps.it0;
+  const uint32_t zxw = (uint32_t)(uint8_t)zx * 0x01010101u;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)w, 0, K * K * C, 0x00020000);
+  // the taps, per row ky, group j and channel ch: bytes w[ky][4j + 0..3][c + ch]
+  uint32_t wp[K][NG][4];
+  uint32_t wsum[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int ky = 0; ky < K; ky++)
+#pragma unroll
+    for (int j = 0; j < NG; j++) {
+      uint32_t r[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        r[i] = 4 * j + i < K ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(wr, c, (ky * K + 4 * j + i) * C, 0) : 0u;
+      transpose4x4(r[0], r[1], r[2], r[3], wp[ky][j]);
+#pragma unroll
+      for (int ch = 0; ch < 4; ch++)
+        wsum[ch] = (uint32_t)__builtin_amdgcn_sdot4((int)wp[ky][j][ch], 0x01010101, (int)wsum[ch], false);
+    }
+  int32_t acc[NP][4];
+#pragma unroll
+  for (int ch = 0; ch < 4; ch++) {
+    const int32_t a0 = (int32_t)((uint32_t)bias[c + ch] - (uint32_t)zx * wsum[ch]);
+#pragma unroll
+    for (int q = 0; q < NP; q++) acc[q][ch] = a0;
+  }
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)x, 0, (int)x_len, 0x00020000);
+  const int x_off = (int)(ps.win * x_ws) + c, ix0 = px0 * S - pl, iy0 = oy * S - pt;
+  if (ix0 < 0 || ix0 + NCOL > W) dw_s8_strip<K, S, true>(xr, x_off, ix0, H, W, C, iy0, zxw, wp, acc);
+  else dw_s8_strip<K, S, false>(xr, x_off, ix0, H, W, C, iy0, zxw, wp, acc);
+  int32_t m[4], e[4];
+  bool s1 = true;  // every shift of the thread's channels in 1..31: the one-rounding requant
+#pragma unroll
+  for (int ch = 0; ch < 4; ch++) {
+    m[ch] = mult[c + ch];
+    e[ch] = shift[c + ch];
+    s1 = s1 && e[ch] >= 1 && e[ch] <= 31;
+  }
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc((void *)out, 0, (int)o_len, 0x00020000);
+  const int o_off = (int)(ps.win * o_ws) + (oy * Wo + px0) * C + c;
+  auto store = [&](auto requant) {
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+      if (px0 + q >= Wo) break;
+      uint32_t word = 0;
+#pragma unroll
+      for (int ch = 0; ch < 4; ch++) {
+        int32_t y = requant(acc[q][ch], ch);
+        if (LUT) y = s_lut[y + 128];
+        word |= ((uint32_t)y & 0xffu) << (8 * ch);
+      }
+      __builtin_amdgcn_raw_buffer_store_b32(word, orr, o_off, q * C, 0);
+    }
+  };
+  if (s1) {
+    BnhRqS1 rc[4];
+#pragma unroll
+    for (int ch = 0; ch < 4; ch++) rc[ch] = bnh_rq_s1(e[ch]);
+    store([&](int32_t a, int ch) { return bnh_requant_s1(a, m[ch], rc[ch], zy, lo, hi); });
+  } else {
+    store([&](int32_t a, int ch) { return bnh_requant(a, m[ch], e[ch], zy, lo, hi); });
+  }
 }
 
 // ================================================================== host side
@@ -1134,13 +1226,25 @@ int bnh_dw_s8(const int8_t *x, long long x_ws, int H, int W, int C, int k, int s
   BNH_REQ(x && w && bias && mult && shift && out && H > 0 && W > 0 && Ho > 0 && Wo > 0 && B > 0);
   BNH_REQ(C > 0 && C % 4 == 0 && (k == 1 || k == 3 || k == 5 || k == 7) && (s == 1 || s == 2));
   BNH_REQ(pt >= 0 && pl >= 0 && pt < k && pl < k && lo >= -128 && hi <= 127 && lo <= hi);
+  BNH_REQ(zx >= -128 && zx <= 127);
   BNH_REQ(((uintptr_t)x & 3) == 0 && ((uintptr_t)w & 3) == 0 && ((uintptr_t)out & 3) == 0);
   BNH_REQ(B == 1 || (x_ws % 4 == 0 && o_ws % 4 == 0 && x_ws >= (long long)H * W * C && o_ws >= (long long)Ho * Wo * C));
-  const long long total = (long long)B * Ho * Wo * (C / 4);
+  // 32-bit buffer offsets: the batch's input and output each under 2 GiB
+  const long long x_len = (long long)(B - 1) * x_ws + (long long)H * W * C;
+  const long long o_len = (long long)(B - 1) * o_ws + (long long)Ho * Wo * C;
+  BNH_REQ(x_len < (1LL << 31) && o_len < (1LL << 31) && (long long)k * k * C < (1LL << 31));
+  unsigned nb;
+  long long total;
+  DwGrid g;
+  if (dw_grid(Wo, dw_s8_np(s), C / 4, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   dispatch_ks<int8_t>(k, s, [&]<int K, int S>() {
-    hipLaunchKernelGGL((k_dw_s8<K, S>), dim3((unsigned)bnh_ceil_div(total, 256)), dim3(256), 0, st, x, x_ws, H, W, C, pt,
-                       pl, w, bias, mult, shift, zx, zy, lo, hi, lut, out, o_ws, Ho, Wo, total);
+    if (lut)
+      hipLaunchKernelGGL((k_dw_s8<K, S, true>), dim3(nb), dim3(256), 0, st, x, x_ws, (unsigned)x_len, H, W, C, pt, pl, w,
+                         bias, mult, shift, zx, zy, lo, hi, lut, out, o_ws, (unsigned)o_len, Ho, Wo, total, g);
+    else
+      hipLaunchKernelGGL((k_dw_s8<K, S, false>), dim3(nb), dim3(256), 0, st, x, x_ws, (unsigned)x_len, H, W, C, pt, pl,
+                         w, bias, mult, shift, zx, zy, lo, hi, lut, out, o_ws, (unsigned)o_len, Ho, Wo, total, g);
   });
   BNH_HIP(hipGetLastError());
   return 0;

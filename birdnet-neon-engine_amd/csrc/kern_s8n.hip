@@ -458,15 +458,6 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
 // LDS transposed to [pixel][k] (4 x 4 byte blocks transposed in registers with v_perm), from where lane l reads its
 // 16 k bytes of pixel (l & 15). B operand = w [Nt][K] rows straight from global (L2-resident).
 // Accumulator lane layout: 4 consecutive pixels x 1 channel -> one 32-bit store of 4 output bytes.
-BNH_DEV void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, uint32_t c[4]) {
-  // r_i = bytes of k row i for pixels 0..3; c_j = bytes of pixel j for k rows 0..3
-  const uint32_t a_lo = __builtin_amdgcn_perm(r1, r0, 0x05010400u), a_hi = __builtin_amdgcn_perm(r1, r0, 0x07030602u);
-  const uint32_t b_lo = __builtin_amdgcn_perm(r3, r2, 0x05010400u), b_hi = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
-  c[0] = __builtin_amdgcn_perm(b_lo, a_lo, 0x05040100u);
-  c[1] = __builtin_amdgcn_perm(b_lo, a_lo, 0x07060302u);
-  c[2] = __builtin_amdgcn_perm(b_hi, a_hi, 0x05040100u);
-  c[3] = __builtin_amdgcn_perm(b_hi, a_hi, 0x07060302u);
-}
 
 #define RQ_LDS_STRIDE 80  // bytes per staged pixel row: 64 k + 16 pad
 
@@ -738,12 +729,16 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
   }
 }
 
-// requant arithmetic check: y[i] = bnh_requant(acc[i], mult[i], shift[i], zy, lo, hi)
+// requant arithmetic check: y[i] = bnh_requant(acc[i], mult[i], shift[i], zy, lo, hi), where for shift 1..31 the
+// one-rounding form must agree (INT32_MIN, outside every clamp range, marks a disagreement)
 __global__ void k_eval_requant(const int32_t *__restrict__ acc, const int32_t *__restrict__ mult,
                                const int32_t *__restrict__ shift, int zy, int lo, int hi, int32_t *__restrict__ y,
                                long long n) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = bnh_requant(acc[i], mult[i], shift[i], zy, lo, hi);
+  if (i >= n) return;
+  const int32_t r = bnh_requant(acc[i], mult[i], shift[i], zy, lo, hi);
+  const bool s1 = shift[i] >= 1 && shift[i] <= 31;
+  y[i] = !s1 || bnh_requant_s1(acc[i], mult[i], bnh_rq_s1(shift[i]), zy, lo, hi) == r ? r : INT32_MIN;
 }
 
 // ------------------------------------------------------------------ numerics probe

@@ -44,7 +44,8 @@ int bnh_copy(void *dst, const void *src, size_t bytes, void *stream);
  * with 0), 3: the same SiLU without the table. Used to pin the device numerics against the oracle. */
 int bnh_eval_f32(int f, const float *x, float *y, long long n, void *stream);
 /* y[i] = the Q31 requantisation of the int8 GEMM / depthwise below applied to acc[i] with mult[i], shift[i] (0..31),
- * zy, clamp [lo, hi]: pins the device fixed-point arithmetic against the oracle */
+ * zy, clamp [lo, hi]: pins the device fixed-point arithmetic against the oracle. Both device forms (the general one
+ * and the one-rounding form for shift 1..31) are evaluated; where they disagree y[i] = INT32_MIN. */
 int bnh_eval_requant(const int32_t *acc, const int32_t *mult, const int32_t *shift, int zy, int lo, int hi, int32_t *y,
                      long long n, void *stream);
 
@@ -236,7 +237,8 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
 /* int8 depthwise: no counterpart in the reference (its depthwise layers are fp32 / fp16); the static int8 form of
  * the same layer. x int8 [H][W][C] unpadded (C % 4 == 0), taps outside the image skipped (a zero-point pad):
  *   acc = bias[c] + sum_taps w[t][c] (x - zx);  y = clamp(RDBYPOT(SRDHM(acc, mult[c]), shift[c]) + zy, lo, hi);
- *   out = lut ? lut[y + 128] : y   (lut: an int8 -> int8 activation table, e.g. SiLU) */
+ *   out = lut ? lut[y + 128] : y   (lut: an int8 -> int8 activation table, e.g. SiLU)
+ * zx is the input's int8 zero point (-128..127); x, w and out 4-byte aligned. */
 int bnh_dw_s8(const int8_t *x, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl, const int8_t *w,
               const int32_t *bias, const int32_t *mult, const int32_t *shift, int zx, int zy, int lo, int hi,
               const int8_t *lut, int8_t *out, long long o_ws, int Ho, int Wo, int B, void *stream);
