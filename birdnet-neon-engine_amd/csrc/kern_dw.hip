@@ -497,6 +497,126 @@ __global__ __launch_bounds__(256) void k_dw_f16p(const h16 *__restrict__ xp, lon
   }
 }
 
+// The same on channel quads (C % 4 == 0, 8-byte aligned data): a thread owns 4 channels (two packed pairs) of a strip
+// of NP output pixels (whole items) in a band of up to R output rows. It loads each input row of the band's strip
+// once (8-byte buffer loads: the lane's row in the vector offset, the column step in the scalar one; the input is
+// haloed, so no checks: a strip past the row's end reads the next row or, at the batch's end, the buffer's
+// out-of-range zeros, and stores nothing there) and keeps the rows in registers while the band's output rows that
+// share them are computed. Each pixel runs its chains row by row in the reference's tap order: the two chains of a
+// 4-pixel group (even / odd taps; DW3: its a / a2 chains, a2 opened by a product) or the one chain of a DWK tail
+// pixel. ALL: every pixel of the strip lies in a 4-pixel group.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// a packed pair from a 32-bit word (by value: clang's __builtin_bit_cast of an ext_vector element reads element 0)
+BNH_DEV h2 h2_bits(uint32_t u) { return __builtin_bit_cast(h2, u); }
+// output rows per band: input rows shared by more outputs against registers and the number of waves
+__host__ __device__ constexpr int dw_f16v_np(int k, int s) { return k == 3 && s == 1 ? 8 : 4; }
+__host__ __device__ constexpr int dw_f16v_rows(int k, int s) { return s == 1 ? 4 : 2; }
+
+template <int K, int S, int FORM, int NP, int R, bool ALL>
+BNH_DEV void dw_f16v_band(__amdgpu_buffer_rsrc_t xr, int xo, int rstep, int cstep, int px0, int g4, int nrows,
+                          const h2 (&wv)[K * K][2], const h2 (&bias)[2], bool silu, const uint32_t *t01,
+                          const uint16_t *t2, __amdgpu_buffer_rsrc_t orr, int oo, int ostep, int Wo) {
+  constexpr int NCOL = (NP - 1) * S + K, NIN = (R - 1) * S + K;
+  // every row of a full band: the rows a short last band does not use are read (from the next window, or as the
+  // buffer's out-of-range zeros) and dropped
+  h2 xin[NIN][NCOL][2];
+#pragma unroll
+  for (int i = 0; i < NIN; i++)
+#pragma unroll
+    for (int col = 0; col < NCOL; col++) {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep, col * cstep, 0);
+      xin[i][col][0] = h2_bits(v[0]);
+      xin[i][col][1] = h2_bits(v[1]);
+    }
+  const h2 z = (h2){(h16)0.0f, (h16)0.0f};
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    if (r >= nrows) break;
+    h2 a[NP][2], e[NP][2];
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+      const bool split = FORM == 2 || ALL || px0 + q < g4;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        a[q][j] = bias[j];
+        e[q][j] = z;
+      }
+#pragma unroll
+      for (int ky = 0; ky < K; ky++)
+#pragma unroll
+        for (int kx = 0; kx < K; kx++) {
+          const int t = ky * K + kx;
+#pragma unroll
+          for (int j = 0; j < 2; j++) {
+            const h2 x = xin[r * S + ky][q * S + kx][j];
+            if (FORM == 2 && t == 1) e[q][j] = x * wv[t][j];
+            else if (split && (t & 1)) e[q][j] = __builtin_elementwise_fma(x, wv[t][j], e[q][j]);
+            else a[q][j] = __builtin_elementwise_fma(x, wv[t][j], a[q][j]);
+          }
+        }
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        h2 y = split ? a[q][j] + e[q][j] : a[q][j];
+        if (silu) y = silu2_lut(y, t01, t2);
+        a[q][j] = y;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+      if (px0 + q >= Wo) break;
+      const u32x2 v = {__builtin_bit_cast(uint32_t, a[q][0]), __builtin_bit_cast(uint32_t, a[q][1])};
+      __builtin_amdgcn_raw_buffer_store_b64(v, orr, oo + r * ostep, q * cstep, 0);
+    }
+  }
+}
+
+template <int K, int S, int FORM, int NP, int R>
+__global__ __launch_bounds__(256) void k_dw_f16v(const h16 *__restrict__ xp, long long x_ws, unsigned x_len, int Wp,
+                                                 int C, int pt, int pl, const h16 *__restrict__ w,
+                                                 const h16 *__restrict__ b, int act, h16 *__restrict__ out,
+                                                 long long o_ws, unsigned o_len, int Ho, int Wo, long long total,
+                                                 DwGrid g) {
+  __shared__ uint32_t s_t01[16];
+  __shared__ uint16_t s_t2[16];
+  if (threadIdx.x < 16) {
+    s_t01[threadIdx.x] = (uint32_t)k_silu_c0[threadIdx.x] | ((uint32_t)k_silu_c1[threadIdx.x] << 16);
+    s_t2[threadIdx.x] = k_silu_c2[threadIdx.x];
+  }
+  __syncthreads();
+  const int nband = (Ho + R - 1) / R;
+  const DwPos ps = dw_pos(C / 4, nband, total, g);
+  if (!ps.ok) return;
+  const int c = 4 * ps.c, oy0 = ps.oy * R, px0 = ps.it0, nrows = Ho - oy0 < R ? Ho - oy0 : R;
+  constexpr int HH = (K - 1) / 2;
+  const int iy0 = FORM == 2 ? oy0 * S - pt + 1 : oy0 * S - pt + HH;
+  const int ix0 = FORM == 2 ? px0 * S - pl + 1 : px0 * S - pl + HH;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)w, 0, K * K * C * 2, 0x00020000);
+  h2 wv[K * K][2], bias[2];
+#pragma unroll
+  for (int t = 0; t < K * K; t++) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(wr, 2 * c, t * C * 2, 0);
+    wv[t][0] = h2_bits(v[0]);
+    wv[t][1] = h2_bits(v[1]);
+  }
+  {
+    const uint2 v = *(const uint2 *)(b + c);
+    bias[0] = __builtin_bit_cast(h2, v.x);
+    bias[1] = __builtin_bit_cast(h2, v.y);
+  }
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)xp, 0, (int)x_len, 0x00020000);
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc((void *)out, 0, (int)o_len, 0x00020000);
+  const int xo = 2 * ((int)(ps.win * x_ws) + (iy0 * Wp + ix0) * C + c);
+  const int oo = 2 * ((int)(ps.win * o_ws) + (oy0 * Wo + px0) * C + c);
+  const int g4 = FORM == 2 ? Wo : Wo & ~3;
+  const bool silu = FORM == 2 || act == 1;
+  if (px0 + NP <= g4)
+    dw_f16v_band<K, S, FORM, NP, R, true>(xr, xo, 2 * Wp * C, 2 * C, px0, g4, nrows, wv, bias, silu, s_t01, s_t2, orr,
+                                          oo, 2 * Wo * C, Wo);
+  else
+    dw_f16v_band<K, S, FORM, NP, R, false>(xr, xo, 2 * Wp * C, 2 * C, px0, g4, nrows, wv, bias, silu, s_t01, s_t2, orr,
+                                           oo, 2 * Wo * C, Wo);
+}
+
 // ------------------------------------------------------------------ channel sums (pass 2)
 // The reference adds the outputs of each channel into one fp32 sum, row after row, in terms that depend on the kernel:
 //   form 0 (fp32 DWK): per row the 4-pixel groups (o0 + o1) + (o2 + o3), then each tail pixel;
@@ -995,6 +1115,16 @@ static bool dw_pairs(const void *xp, long long x_ws, const void *w, const void *
          ((uintptr_t)out & 3) == 0 && (B == 1 || (x_ws % 2 == 0 && o_ws % 2 == 0));
 }
 
+// the fp16 kernels run channel quads when every quad is 8-byte aligned and the batch's input and output each stay
+// under 2 GiB (32-bit buffer offsets); px_in / px_out: pixels per window (haloed input)
+static bool dw_quads(const void *xp, long long x_ws, const void *w, const void *b, const void *out, long long o_ws,
+                     int C, int B, long long px_in, long long px_out) {
+  return C % 4 == 0 && ((uintptr_t)xp & 7) == 0 && ((uintptr_t)w & 7) == 0 && ((uintptr_t)b & 7) == 0 &&
+         ((uintptr_t)out & 7) == 0 && (B == 1 || (x_ws % 4 == 0 && o_ws % 4 == 0)) &&
+         2 * ((long long)(B - 1) * x_ws + px_in * C) < (1LL << 31) &&
+         2 * ((long long)(B - 1) * o_ws + px_out * C) < (1LL << 31) && 2LL * 49 * C < (1LL << 31);
+}
+
 static int dw_check(int H, int W, int C, int k, int s, int pt, int pl, int Ho, int Wo, int B, long long x_ws,
                     long long o_ws, int halo) {
   BNH_REQ(H > 0 && W > 0 && C > 0 && Ho > 0 && Wo > 0 && B > 0);
@@ -1174,10 +1304,27 @@ int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, 
   unsigned nb;
   long long total;
   DwGrid g;
-  const bool pair = dw_pairs(xp, x_ws, w, b, out, o_ws, C, B);
-  if (dw_grid(nit, dw_ni(k), pair ? C / 2 : C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
   const int Wp = W + k - 1;
+  if (dw_quads(xp, x_ws, w, b, out, o_ws, C, B, (long long)(H + k - 1) * Wp, (long long)Ho * Wo)) {
+    const unsigned x_len = (unsigned)(2 * ((long long)(B - 1) * x_ws + (long long)(H + k - 1) * Wp * C));
+    const unsigned o_len = (unsigned)(2 * ((long long)(B - 1) * o_ws + (long long)Ho * Wo * C));
+    const int R = dw_f16v_rows(k, s);
+    if (dw_grid(Wo, dw_f16v_np(k, s), C / 4, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
+    dispatch_ks<h16>(k, s, [&]<int K, int S>() {
+      constexpr int NP = dw_f16v_np(K, S), RR = dw_f16v_rows(K, S);
+      hipLaunchKernelGGL((k_dw_f16v<K, S, 1, NP, RR>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, x_len, Wp, C, pt,
+                         pl, (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, o_len, Ho, Wo, total, g);
+    });
+    BNH_HIP(hipGetLastError());
+    if (chsum) {
+      BNH_REQ(B == 1 || cs_ws >= C);
+      if (chsum_launch<h16, 1>((const h16 *)out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st)) return -1;
+    }
+    return 0;
+  }
+  const bool pair = dw_pairs(xp, x_ws, w, b, out, o_ws, C, B);
+  if (dw_grid(nit, dw_ni(k), pair ? C / 2 : C, Ho, B, &nb, &total, &g)) return -1;
   dispatch_ks<h16>(k, s, [&]<int K, int S>() {
     if (pair)
       hipLaunchKernelGGL((k_dw_f16p<K, S, 1>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, Wp, C, pt, pl,
@@ -1203,9 +1350,28 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
   unsigned nb;
   long long total;
   DwGrid g;
+  hipStream_t st = bnh_stream(stream);
+  if (dw_quads(xp, x_ws, w, b, out, o_ws, C, B, (long long)(H + 2) * (W + 2), (long long)Ho * Wo)) {
+    const unsigned x_len = (unsigned)(2 * ((long long)(B - 1) * x_ws + (long long)(H + 2) * (W + 2) * C));
+    const unsigned o_len = (unsigned)(2 * ((long long)(B - 1) * o_ws + (long long)Ho * Wo * C));
+    const int R = dw_f16v_rows(3, s);
+    if (dw_grid(Wo, dw_f16v_np(3, s), C / 4, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
+    auto launch = [&]<int S>() {
+      constexpr int NP = dw_f16v_np(3, S), RR = dw_f16v_rows(3, S);
+      hipLaunchKernelGGL((k_dw_f16v<3, S, 2, NP, RR>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, x_len, W + 2, C,
+                         pt, pl, (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, o_len, Ho, Wo, total, g);
+    };
+    if (s == 1) launch.template operator()<1>();
+    else launch.template operator()<2>();
+    BNH_HIP(hipGetLastError());
+    if (chsum) {
+      BNH_REQ(B == 1 || cs_ws >= C);
+      if (chsum_launch<h16, 3>((const h16 *)out, o_ws, C, Ho, Wo, chsum, cs_ws, B, st)) return -1;
+    }
+    return 0;
+  }
   const bool pair = dw_pairs(xp, x_ws, w, b, out, o_ws, C, B);
   if (dw_grid(nit, dw_ni(3), pair ? C / 2 : C, Ho, B, &nb, &total, &g)) return -1;
-  hipStream_t st = bnh_stream(stream);
 #define DW3H(KERN, S_)                                                                                                 \
   hipLaunchKernelGGL((KERN<3, S_, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, W + 2, C, pt, pl,           \
                      (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, Ho, Wo, nit, total, g)

@@ -138,7 +138,9 @@ def test_dwk_row_tails(hip, dtype, Wd):
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
 def test_dwk_k7_and_odd_channels(hip, dtype):
-    for (H, W, C, k, s, seed) in ((9, 13, 72, 7, 2, 3), (7, 11, 3, 5, 1, 4), (10, 9, 5, 7, 1, 5)):
+    # C = 22: the fp16 channel-pair kernel (C % 4 == 2); 72: channel quads; 3, 5: single channels
+    for (H, W, C, k, s, seed) in ((9, 13, 72, 7, 2, 3), (7, 11, 3, 5, 1, 4), (10, 9, 5, 7, 1, 5),
+                                  (8, 10, 22, 3, 1, 6), (6, 9, 22, 5, 2, 7)):
         _, pt = same_pads(H, k, s)
         _, pl = same_pads(W, k, s)
         check_case(hip, "dwk", dtype, 2, H, W, C, k, s, pt, pl, 1, seed=seed)
@@ -147,7 +149,7 @@ def test_dwk_k7_and_odd_channels(hip, dtype):
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
 @pytest.mark.parametrize("s", [1, 2])
 def test_dw3(hip, dtype, s):
-    for H, W, C in ((24, 64, 144), (5, 7, 24), (6, 2, 8)):
+    for H, W, C in ((24, 64, 144), (5, 7, 24), (6, 2, 8), (7, 9, 18)):
         _, pt = same_pads(H, 3, s)
         _, pl = same_pads(W, 3, s)
         check_case(hip, "dw3", dtype, 2, H, W, C, 3, s, pt, pl, 1, seed=H + W + s)
