@@ -524,7 +524,9 @@ BNH_DEV void dw_f16v_band(__amdgpu_buffer_rsrc_t xr, int xo, int rstep, int cste
   for (int i = 0; i < NIN; i++)
 #pragma unroll
     for (int col = 0; col < NCOL; col++) {
-      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep, col * cstep, 0);
+      // a strip past the row's end (not ALL) keeps its whole offset in the vector operand, the range-checked one
+      const u32x2 v = ALL ? __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep, col * cstep, 0)
+                          : __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep + col * cstep, 0, 0);
       xin[i][col][0] = h2_bits(v[0]);
       xin[i][col][1] = h2_bits(v[1]);
     }

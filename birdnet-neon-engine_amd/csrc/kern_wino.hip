@@ -9,11 +9,20 @@
 // B^T = [[1,0,-1,0],[0,1,1,0],[0,-1,1,0],[0,1,0,-1]], G = [[1,0,0],[.5,.5,.5],[.5,-.5,.5],[0,0,1]],
 // A^T = [[1,1,1,0],[0,1,-1,-1]].
 //
-// Work split: a block owns one window's strip of 32 output columns (16 tiles across) and walks its row pairs
-// (one tile row per step). A wave owns 16 output channels and keeps their U fragments for all 16 positions and all
-// input channels in registers for the whole strip (loaded once). Per step the block transforms the 16 tiles' input
-// into LDS (V [16 positions][16 tiles][Cp]), every wave runs 16 x Cp/32 MFMAs (A = V rows of 16 tiles, B = its U),
-// and each lane, holding all 16 positions of 4 tiles for one channel, applies the output transform in registers.
+// Work split: a block owns one window's strip of 32 output columns (16 tiles across) and walks its tile rows
+// (steps) in a software pipeline of two wave groups, one block barrier per phase:
+//   * producers (NCO waves), in phase P: the input transform of step P from a 6-row LDS ring of input rows into
+//     V[P & 1] [16 positions][16 tiles][Cp]; the ring rows of step P + 1 written from registers, and the loads of
+//     the rows after issued (coalesced 8-byte loads of whole row segments: each input row is read once per strip);
+//     and the epilogue of step P - 2 from the fp32 LDS output tile Os[P & 1] (bias, activation, rounding to fp16,
+//     residual) stored as channel-contiguous 16-byte rows;
+//   * consumers (NCO waves, each owning 16 output channels and their U fragments for all 16 positions and input
+//     channels in registers for the whole strip), in phase P: the 16 x Cp/32 MFMAs of step P - 1 (A = V rows of 16
+//     tiles, B = its U) and the output transform in registers (a lane holds all 16 positions of 4 tiles for one
+//     channel) into Os[(P - 1) & 1] (fp32).
+// The two groups share each SIMD, so the transforms, matrix products and memory traffic of neighbouring steps
+// overlap. The epilogue's SiLU is y / (1 + 2^(-y log2 e)) on the hardware exp2 and reciprocal (about 1 ulp of fp32
+// each), far inside the fp16 tolerance of this path.
 #include <math.h>
 #include <string.h>
 
@@ -33,110 +42,221 @@ struct bnh_wino16 {
 };
 
 #define WT_TILES 16  // tiles per step (the MFMA row dimension)
+#define WT_COLS 34   // input columns of a strip: 2 x 16 + 2
 
-template <int NCO, int NCH>  // NCO waves of 16 output channels, NCH = Cp / 32 MFMA k steps
-__global__ __launch_bounds__(64 * NCO) void k_wino_f16(const uint16_t *__restrict__ x, long long x_ws, int H, int W,
-                                                       int C, int ldx, const uint16_t *__restrict__ U,
-                                                       const float *__restrict__ bias, int K, int act,
-                                                       uint16_t *__restrict__ out, long long o_ws, int ldo, int opad,
-                                                       const uint16_t *__restrict__ res, long long r_ws, int ldr,
-                                                       int rpad, int strips) {
-  constexpr int CP = 32 * NCH;
-  __shared__ __attribute__((aligned(16))) _Float16 V[16 * WT_TILES * CP];
+BNH_DEV float wino_silu(float y) {
+  const float t = __builtin_amdgcn_exp2f(-1.44269504f * y);
+  const float s = y * __builtin_amdgcn_rcpf(1.0f + t);
+  return y == -INFINITY ? -0.0f : s;
+}
+
+template <int NCO, int NCH, int ACT>  // NCO waves of 16 output channels, NCH = Cp / 32 MFMA k steps, ACT 0/1/2
+__global__ __launch_bounds__(128 * NCO) void k_wino_f16(const uint16_t *__restrict__ x, long long x_ws, int H, int W,
+                                                        int C, int ldx, const uint16_t *__restrict__ U,
+                                                        const float *__restrict__ bias, int K,
+                                                        uint16_t *__restrict__ out, long long o_ws, int ldo, int opad,
+                                                        const uint16_t *__restrict__ res, long long r_ws, int ldr,
+                                                        int rpad, int strips, int vec) {
+  constexpr int CP = 32 * NCH, KP = 16 * NCO, NA = 64 * NCO, RING = 6;
+  // padded strides: ring pixel (halves; two pixels apart = 32 banks, so a wave's in-transform reads of two tiles
+  // share no bank), V tile (halves; the 16 tiles of an MFMA operand read in distinct banks), output pixel (floats)
+  constexpr int XS = CP == 64 ? 96 : 48, VS = CP + 8, OS = KP + 4;
+  constexpr int VSZ = 16 * WT_TILES * VS, OSZ = 2 * 2 * WT_TILES * OS;
+  constexpr int PRE = (2 * WT_COLS * (CP / 4) + NA - 1) / NA;   // prefetch slots per producer (8-byte chunks)
+  constexpr int SV = (2 * 2 * WT_TILES * KP / 8 + NA - 1) / NA;  // 16-byte output items per producer
+  __shared__ __attribute__((aligned(16))) _Float16 Xs[RING * WT_COLS * XS];
+  __shared__ __attribute__((aligned(16))) _Float16 V[2 * VSZ];
+  __shared__ __attribute__((aligned(16))) float Os[2 * OSZ];
+  __shared__ __attribute__((aligned(16))) float Bs[KP];  // the bias
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool prod = tid < NA;
   const int win = blockIdx.x / strips, strip = blockIdx.x % strips;
-  const int T = W / 2, tx0 = strip * WT_TILES;  // first tile column of the strip
-  const int Wp = W + 2;
-  const h16 *xw = (const h16 *)x + win * x_ws;
-  // this wave's U fragments: position p, k step c -> lane holds channels co = 16 wave + (lane & 15), input channels
-  // 32 c + 8 (lane >> 4) .. + 7
-  const int co = 16 * wave + (lane & 15);
+  const int T = W / 2, tx0 = strip * WT_TILES, Wp = W + 2, c4 = C / 4, NS = H / 2;
+  const int npx = 2 * (T - tx0 < WT_TILES ? T - tx0 : WT_TILES);  // output columns of the strip
+  // ---- producer state: the window's haloed input as a buffer (columns past the image read zeros or the next row;
+  // tiles past T are never stored); per prefetch slot: its row (-1: none), byte offset from the first row's strip
+  // start and LDS offset within a ring row; per 16-byte output item: Os offset (-1: none) and element offsets of the
+  // output and residual from output row 2 step's start
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(x + win * x_ws), 0, (int)((long long)(H + 2) * Wp * ldx * 2), 0x00020000);
+  uint2 pre[PRE];
+  int pr[PRE], pg[PRE], pl[PRE];
+#pragma unroll
+  for (int j = 0; j < PRE; j++) {
+    const int i = tid + NA * j, r = i / (WT_COLS * c4), rem = i - r * (WT_COLS * c4), px = rem / c4, g = rem - px * c4;
+    pr[j] = prod && r < 2 ? r : -1;
+    pg[j] = ((r * Wp + 2 * tx0 + px) * ldx + 4 * g) * 2;
+    pl[j] = px * XS + 4 * g;
+  }
+  int so[SV], sg[SV], sr[SV];
+  {
+    const int k8 = vec ? K / 8 : 1;
+#pragma unroll
+    for (int j = 0; j < SV; j++) {
+      const int it = tid + NA * j, i = it / (npx * k8), rem = it - i * (npx * k8), px = rem / k8, ch = 8 * (rem - px * k8);
+      const int ox = 2 * tx0 + px;
+      so[j] = prod && vec && it < 2 * npx * k8 ? (i * 2 * WT_TILES + px) * OS + ch : -1;
+      sg[j] = ((i + opad) * (W + 2 * opad) + ox + opad) * ldo + ch;
+      sr[j] = ((i + rpad) * (W + 2 * rpad) + ox + rpad) * ldr + ch;
+    }
+  }
+  const long long orowb = (long long)(W + 2 * opad) * ldo, rrowb = (long long)(W + 2 * rpad) * ldr;
+  const int rowb = Wp * ldx * 2;
+  auto fetch = [&](uint2 (&dst)[PRE], int r0) {  // rows r0, r0 + 1 -> registers (the whole offset range-checked)
+#pragma unroll
+    for (int j = 0; j < PRE; j++) {
+      dst[j] = make_uint2(0u, 0u);
+      if (pr[j] >= 0) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(xr, pg[j] + r0 * rowb, 0, 0);
+        dst[j] = make_uint2(v[0], v[1]);
+      }
+    }
+  };
+  auto commit = [&](int r0) {  // the prefetched rows r0, r0 + 1 into their ring slots
+#pragma unroll
+    for (int j = 0; j < PRE; j++)
+      if (pr[j] >= 0) *(uint2 *)(Xs + ((r0 + pr[j]) % RING) * WT_COLS * XS + pl[j]) = pre[j];
+  };
+  // ---- consumer state: this wave's U fragments (position p, k step c -> channels co = 16 (wave - NCO) + (lane & 15),
+  // input channels 32 c + 8 (lane >> 4) .. + 7)
+  const int co = 16 * (wave - NCO) + (lane & 15);
   v8h u[16][NCH];
+  if (!prod) {
 #pragma unroll
-  for (int p = 0; p < 16; p++)
+    for (int p = 0; p < 16; p++)
 #pragma unroll
-    for (int c = 0; c < NCH; c++)
-      u[p][c] = *(const v8h *)(U + ((long long)(p * (16 * NCO) + co)) * CP + 32 * c + 8 * (lane >> 4));
-  const float bco = bias[co];
-  // input-transform work items: (tile, group of 4 input channels)
-  const int groups = C / 4;
-  for (int ty = 0; ty < H / 2; ty++) {
-    // ---- V = B^T d B for the 16 tiles of this step (fp16, wino_s0.c in_tf order)
-    for (int it = tid; it < WT_TILES * (CP / 4); it += 64 * NCO) {
-      const int t = it % WT_TILES, g4 = it / WT_TILES;
-      v4h vv[16];
-      if (g4 < groups && tx0 + t < T) {
-        const h16 *d = xw + ((long long)(2 * ty) * Wp + 2 * (tx0 + t)) * ldx + 4 * g4;
-        v4h dd[4][4];
+      for (int c = 0; c < NCH; c++)
+        u[p][c] = *(const v8h *)(U + ((long long)(p * KP + co)) * CP + 32 * c + 8 * (lane >> 4));
+  }
+  if (prod) {  // the bias; rows 0..3 of step 0, and the loads of rows 4, 5
+    for (int i = tid; i < KP; i += NA) Bs[i] = bias[i];
+    fetch(pre, 0);
+    commit(0);
+    fetch(pre, 2);
+    commit(2);
+    if (NS > 1) fetch(pre, 4);
+  }
+  __syncthreads();
+  for (int P = 0; P <= NS + 1; P++) {
+    if (prod) {
+      // ---- V = B^T d B for the 16 tiles of step P (fp16, wino_s0.c in_tf order); channel quads past C are zero
+      if (P < NS) {
+        _Float16 *Vb = V + (P & 1) * VSZ;
+        for (int it = tid; it < WT_TILES * (CP / 4); it += NA) {
+          const int g = it % (CP / 4), t = it / (CP / 4);
+          v4h vv[16];
+          if (g < c4) {
+            v4h dd[4][4];
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+            for (int r = 0; r < 4; r++)
 #pragma unroll
-          for (int cc = 0; cc < 4; cc++) dd[r][cc] = *(const v4h *)(d + ((long long)r * Wp + cc) * ldx);
-        v4h tt[4][4];
+              for (int cc = 0; cc < 4; cc++)
+                dd[r][cc] = *(const v4h *)(Xs + (((2 * P + r) % RING) * WT_COLS + 2 * t + cc) * XS + 4 * g);
+            v4h tt[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              tt[0][j] = dd[0][j] - dd[2][j];
+              tt[1][j] = dd[1][j] + dd[2][j];
+              tt[2][j] = dd[2][j] - dd[1][j];
+              tt[3][j] = dd[1][j] - dd[3][j];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              vv[4 * i + 0] = tt[i][0] - tt[i][2];
+              vv[4 * i + 1] = tt[i][1] + tt[i][2];
+              vv[4 * i + 2] = tt[i][2] - tt[i][1];
+              vv[4 * i + 3] = tt[i][1] - tt[i][3];
+            }
+          } else {
+#pragma unroll
+            for (int p = 0; p < 16; p++) vv[p] = (v4h){};
+          }
+#pragma unroll
+          for (int p = 0; p < 16; p++) *(v4h *)(Vb + (p * WT_TILES + t) * VS + 4 * g) = vv[p];
+        }
+        if (P + 1 < NS) commit(2 * P + 4);  // rows of step P + 1, read after this phase's barrier
+        if (P + 2 < NS) fetch(pre, 2 * P + 6);
+      }
+      // ---- step P - 2's two output rows: + b, activation, fp16 (residual added in fp16 after the rounding)
+      if (P >= 2) {
+        const int ty = P - 2;
+        const float *Ob = Os + (P & 1) * OSZ;
+        auto epi = [&](float y, float b) {
+          y = y + b;
+          if (ACT == 1) y = wino_silu(y);
+          else if (ACT == 2) y = bnh_relu_f32(y);
+          return f2h(y);
+        };
+        if (vec) {  // 8 channels per item: 16-byte stores
+#pragma unroll
+          for (int j = 0; j < SV; j++) {
+            if (so[j] < 0) continue;
+            const float4 y0 = *(const float4 *)(Ob + so[j]), y1 = *(const float4 *)(Ob + so[j] + 4);
+            const int ch = so[j] % OS;
+            const float4 b0 = *(const float4 *)(Bs + ch), b1 = *(const float4 *)(Bs + ch + 4);
+            auto pk = [&](float a, float b, float ba, float bb) {
+              const h2 v = (h2){epi(a, ba), epi(b, bb)};
+              return __builtin_bit_cast(uint32_t, v);
+            };
+            uint4 v = make_uint4(pk(y0.x, y0.y, b0.x, b0.y), pk(y0.z, y0.w, b0.z, b0.w), pk(y1.x, y1.y, b1.x, b1.y),
+                                 pk(y1.z, y1.w, b1.z, b1.w));
+            if (res) {
+              const uint4 rv = *(const uint4 *)(res + win * r_ws + (long long)(2 * ty) * rrowb + sr[j]);
+              v = make_uint4(__builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.x) + __builtin_bit_cast(h2, rv.x)),
+                             __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.y) + __builtin_bit_cast(h2, rv.y)),
+                             __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.z) + __builtin_bit_cast(h2, rv.z)),
+                             __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v.w) + __builtin_bit_cast(h2, rv.w)));
+            }
+            *(uint4 *)(out + win * o_ws + (long long)(2 * ty) * orowb + sg[j]) = v;
+          }
+        } else {
+          for (int it = tid; it < 2 * npx * K; it += NA) {
+            const int i = it / (npx * K), rem = it - i * (npx * K), px = rem / K, ch = rem - px * K;
+            const int oy = 2 * ty + i, ox = 2 * tx0 + px;
+            h16 v = epi(Ob[(i * 2 * WT_TILES + px) * OS + ch], Bs[ch]);
+            if (res) {
+              const long long rrow = rpad ? (long long)(oy + rpad) * (W + 2 * rpad) + ox + rpad : (long long)oy * W + ox;
+              v = v + hfrom(res[win * r_ws + rrow * ldr + ch]);
+            }
+            const long long orow = opad ? (long long)(oy + opad) * (W + 2 * opad) + ox + opad : (long long)oy * W + ox;
+            out[win * o_ws + orow * ldo + ch] = hbits(v);
+          }
+        }
+      }
+    } else if (P >= 1 && P <= NS) {
+      // ---- M_p = V_p U_p for step P - 1: lane rows = tiles 4 (lane >> 4) + r, column = channel co
+      const _Float16 *Vb = V + ((P - 1) & 1) * VSZ;
+      v4f acc[16];
+#pragma unroll
+      for (int p = 0; p < 16; p++) {
+        acc[p] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+          const v8h a = *(const v8h *)(Vb + (p * WT_TILES + (lane & 15)) * VS + 32 * c + 8 * (lane >> 4));
+          acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u[p][c], acc[p], 0, 0, 0);
+        }
+      }
+      // ---- y = A^T M A per tile (fp32): 2 x 2 outputs of channel co into the output tile
+      float *Ob = Os + ((P - 1) & 1) * OSZ;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int t = 4 * (lane >> 4) + r;
+        float s[2][4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          tt[0][j] = dd[0][j] - dd[2][j];
-          tt[1][j] = dd[1][j] + dd[2][j];
-          tt[2][j] = dd[2][j] - dd[1][j];
-          tt[3][j] = dd[1][j] - dd[3][j];
+          s[0][j] = (acc[j][r] + acc[4 + j][r]) + acc[8 + j][r];
+          s[1][j] = (acc[4 + j][r] - acc[8 + j][r]) - acc[12 + j][r];
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          vv[4 * i + 0] = tt[i][0] - tt[i][2];
-          vv[4 * i + 1] = tt[i][1] + tt[i][2];
-          vv[4 * i + 2] = tt[i][2] - tt[i][1];
-          vv[4 * i + 3] = tt[i][1] - tt[i][3];
-        }
-      } else {
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int p = 0; p < 16; p++) vv[p] = (v4h){};  // input channels past C, tiles past the image: zero rows
+          for (int jx = 0; jx < 2; jx++) {
+            Ob[(i * 2 * WT_TILES + 2 * t + jx) * OS + co] =
+                jx == 0 ? (s[i][0] + s[i][1]) + s[i][2] : (s[i][1] - s[i][2]) - s[i][3];
+          }
       }
-#pragma unroll
-      for (int p = 0; p < 16; p++) *(v4h *)(V + (p * WT_TILES + t) * CP + 4 * g4) = vv[p];
     }
     __syncthreads();
-    // ---- M_p = V_p U_p: lane rows = tiles 4 (lane >> 4) + r, column = channel co
-    v4f acc[16];
-#pragma unroll
-    for (int p = 0; p < 16; p++) {
-      acc[p] = (v4f){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < NCH; c++) {
-        const v8h a = *(const v8h *)(V + (p * WT_TILES + (lane & 15)) * CP + 32 * c + 8 * (lane >> 4));
-        acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u[p][c], acc[p], 0, 0, 0);
-      }
-    }
-    __syncthreads();  // V is rewritten by the next step
-    if (co >= K) continue;
-    // ---- y = A^T M A + b per tile; 2 x 2 outputs of channel co
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int t = 4 * (lane >> 4) + r;
-      if (tx0 + t >= T) continue;
-      float s[2][4];
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        s[0][j] = (acc[j][r] + acc[4 + j][r]) + acc[8 + j][r];
-        s[1][j] = (acc[4 + j][r] - acc[8 + j][r]) - acc[12 + j][r];
-      }
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int jx = 0; jx < 2; jx++) {
-          float y = jx == 0 ? (s[i][0] + s[i][1]) + s[i][2] : (s[i][1] - s[i][2]) - s[i][3];
-          y = y + bco;
-          if (act == 1) y = bnh_silu_f32(y);
-          else if (act == 2) y = bnh_relu_f32(y);
-          const int oy = 2 * ty + i, ox = 2 * (tx0 + t) + jx;
-          h16 v = f2h(y);
-          if (res) {
-            const long long rrow = rpad ? (long long)(oy + rpad) * (W + 2 * rpad) + ox + rpad : (long long)oy * W + ox;
-            v = v + hfrom(res[win * r_ws + rrow * ldr + co]);
-          }
-          const long long orow = opad ? (long long)(oy + opad) * (W + 2 * opad) + ox + opad : (long long)oy * W + ox;
-          out[win * o_ws + orow * ldo + co] = hbits(v);
-        }
-    }
   }
 }
 
@@ -219,9 +339,22 @@ int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const
   const int strips = (int)bnh_ceil_div(W / 2, WT_TILES);
   const dim3 grid((unsigned)((long long)strips * B));
   const int nco = P->Kp / 16, nch = P->Cp / 32;
+  // a window's input is one buffer resource; per-window element offsets of the output and residual fit 32 bits
+  BNH_REQ((long long)(H + 2) * (W + 2) * ldx * 2 < (1LL << 31));
+  BNH_REQ((long long)(H + 2 * opad) * (W + 2 * opad) * ldo < (1LL << 31));
+  BNH_REQ(!res || (long long)(H + 2 * rpad) * (W + 2 * rpad) * ldr < (1LL << 31));
+  // 16-byte output rows when every 8-channel group is aligned
+  const int vec = P->K % 8 == 0 && ldo % 8 == 0 && ((uintptr_t)out & 15) == 0 && (B == 1 || o_ws % 8 == 0) &&
+                  (!res || (ldr % 8 == 0 && ((uintptr_t)res & 15) == 0 && (B == 1 || r_ws % 8 == 0)));
 #define WINO_LAUNCH(NCO, NCH)                                                                                          \
-  hipLaunchKernelGGL((k_wino_f16<NCO, NCH>), grid, dim3(64 * NCO), 0, st, x, x_ws, H, W, P->C, ldx, P->U, P->b, P->K, \
-                     act, out, o_ws, ldo, opad, res, r_ws, ldr, rpad, strips)
+  do {                                                                                                                 \
+    if (act == 1) WINO_LAUNCH_A(NCO, NCH, 1);                                                                          \
+    else if (act == 2) WINO_LAUNCH_A(NCO, NCH, 2);                                                                     \
+    else WINO_LAUNCH_A(NCO, NCH, 0);                                                                                   \
+  } while (0)
+#define WINO_LAUNCH_A(NCO, NCH, ACT)                                                                                   \
+  hipLaunchKernelGGL((k_wino_f16<NCO, NCH, ACT>), grid, dim3(128 * NCO), 0, st, x, x_ws, H, W, P->C, ldx, P->U, P->b,   \
+                     P->K, out, o_ws, ldo, opad, res, r_ws, ldr, rpad, strips, vec)
   if (nch == 1) {
     if (nco == 1) WINO_LAUNCH(1, 1); else if (nco == 2) WINO_LAUNCH(2, 1); else if (nco == 3) WINO_LAUNCH(3, 1);
     else WINO_LAUNCH(4, 1);
@@ -231,6 +364,7 @@ int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const
   } else {
     BNH_REQ(nch <= 2);  // C <= 64 in this kernel family
   }
+#undef WINO_LAUNCH_A
 #undef WINO_LAUNCH
   BNH_HIP(hipGetLastError());
   return 0;
