@@ -249,6 +249,39 @@ class Net:
         self.last = ob
         return ob
 
+    @staticmethod
+    def fpack(w, b, K_pad=4):
+        """fp_pack (src/gemm_f32.c:22-35): w [N][K] -> panels [Np/8][Kp][8] (Kp = K rounded up to 4), bias [Np + 8]."""
+        w = np.asarray(w, np.float32)
+        N, K = w.shape
+        Kp, Np = (K + K_pad - 1) // K_pad * K_pad, (N + 7) // 8 * 8
+        wp = np.zeros((Np, Kp), np.float32)
+        wp[:N, :K] = w
+        panels = np.ascontiguousarray(wp.reshape(Np // 8, 8, Kp).transpose(0, 2, 1))
+        bb = np.zeros(Np + 8, np.float32)
+        bb[:N] = b
+        return panels, bb, (N, K, Kp, Np)
+
+    def pw(self, ib, w, b, act=None, H=None, W=None, opad=0, res=-1, gate=-1):
+        """A 1x1 conv in fp32 (PW, variant 0; the projections the reference's default int8 policy keeps in fp32,
+        lower.py:874-881): fp32 panels; the input buffer grows to whole 8-row tiles (rt_pw_check)."""
+        d = self.bufs[ib]
+        H = d[1] if H is None else H
+        W = d[2] if W is None else W
+        M, lda = H * W, d[4]
+        panels, bb, (N, K, Kp, Np) = self.fpack(w, b)
+        assert lda >= Kp, "the input rows must hold Kp channels"
+        mr = (M + 7) // 8 * 8
+        if d[6] < mr * lda:
+            self.bufs[ib] = d[:6] + (mr * lda,) + d[7:]
+        tl = [self.tensor("f32/pw.w", panels), self.tensor("f32/pw.b", bb)]
+        ob = self.buf(F32, H, W, N, ld=Np, halo=opad)
+        ldr = self.bufs[res][4] if res >= 0 else 0
+        bl = [ib, ob, res] + ([gate] if gate >= 0 else [])
+        self.emit(OP["PW"], bl, tl, [N, K, Kp, Np, M, lda, ACT[act], Np, W, opad, ldr])
+        self.last = ob
+        return ob
+
     def stem(self, ib, w, b, k, s, act="silu", opad=0, ldo=None):
         """k x k VALID conv of stride s on the 1-channel image ib (stem, lower.py:760-785): fp32 panels
         [Np/8][Kp][8], Kp = k*k rounded up to 4; output [Ho][Wo][ldo] with halo opad."""

@@ -26,6 +26,7 @@ SOURCES = [
     "kern_dw.hip",
     "kern_wino.hip",
     "kern_f16.hip",
+    "kern_gemm_f32.hip",
     "kern_fe.hip",
     "kern_f32.hip",
     "pkg_file.cpp",

@@ -187,6 +187,58 @@ static int stem_run(rt_ctx *c, rt_op *op) {
                            (float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[11], p[12], c->nwin, c->stream);
 }
 
+// -------- PW: b = [in f32 [M][lda], out, res | -1 (, gate f32 [K] | -1)]; t = [w panels [Np/8][Kp][8], b];
+//          p = [N K Kp Np, M, lda, act, ldo, ow, opad, ldr]   (pw_init / rt_pw_check / rt_fpack_view,
+//          src/rt_ops_f32.c:49-59, 129-162; pw_run :194-208)
+int rt_pw_out_check(rt_ctx *c, rt_op *op, int dt);  // ops_s8n.cpp
+static int pw_init(rt_ctx *c, rt_op *op) {
+  if (rt_need_args(c, op, op->nb == 4 ? 4 : 3, 2, 11)) return RT_E_PARAM;  // the gate is optional
+  const int *p = op->p;
+  const int N = p[0], K = p[1], Kp = p[2], Np = p[3];
+  if (N <= 0 || K <= 0 || Np != ((N + 7) & ~7) || Kp < K || Kp % 4)
+    return rt_bad(c, op, "GEMM shape N %d K %d Kp %d Np %d: expected Np = N rounded up to 8, Kp >= K, Kp %% 4 == 0", N,
+                  K, Kp, Np);
+  if (rt_need_t(c, op, 0, (size_t)Np * Kp * 4, 1) || rt_need_t(c, op, 1, (size_t)Np * 4, 1)) return RT_E_PARAM;
+  if (op->nb == 4 && op->b[3] >= 0) {
+    RT_REQ(c, op, K == Kp);
+    if (rt_need(c, op, 3, RT_F32, (size_t)K)) return RT_E_PARAM;
+  }
+  const int M = p[4], lda = p[5], act = p[6], ldo = p[7], opad = p[9], ldr = p[10];
+  const size_t Mr = ((size_t)M + 7) & ~(size_t)7;
+  RT_REQ(c, op, M > 0);
+  RT_REQ(c, op, lda >= Kp);  // the input channel stride covers the packed K
+  RT_REQ(c, op, ldo >= Np);  // the output channel stride covers the packed N
+  RT_REQ(c, op, act >= 0 && act <= 2);
+  RT_REQ(c, op, opad >= 0 && opad <= 3);
+  if (rt_need(c, op, 0, RT_F32, Mr * lda) || rt_pw_out_check(c, op, RT_F32)) return RT_E_PARAM;  // 8-row tiles
+  if (op->b[2] >= 0) {
+    RT_REQ(c, op, ldr >= Np);
+    const rt_bufdesc *r = rt_bd(c, op, 2);
+    if (r->halo) {  // a residual in a zero-haloed buffer: the same pixel grid as the M rows
+      if (r->dtype != RT_F32 || r->ld != (uint32_t)ldr || (size_t)r->H * r->W != (size_t)M || !r->W)
+        return rt_bad(c, op, "buffer argument 2 (buffer #%d, residual): halo %u needs an fp32 buffer with ld %d and H x W = "
+                      "%d rows, found %s ld %u %ux%u", op->b[2], r->halo, ldr, M, rt_dtype_name(r->dtype), r->ld, r->H, r->W);
+      if (rt_need(c, op, 2, RT_F32, (size_t)(r->H + 2 * r->halo) * (r->W + 2 * r->halo) * ldr)) return RT_E_PARAM;
+    } else if (rt_need(c, op, 2, RT_F32, (size_t)M * ldr)) {
+      return RT_E_PARAM;
+    }
+  }
+  return rt_dev_tensors(c, op, 2);
+}
+static int pw_run(rt_ctx *c, rt_op *op) {
+  const int *p = op->p;
+  const rt_bufdesc *r = rt_bd(c, op, 2);
+  const bool gated = op->nb == 4 && op->b[3] >= 0;
+  bnh_epi32 e = {p[6], (float *)rt_b(c, op, 1), rt_ws(c, op, 1), p[7], p[9] ? p[8] : 0, p[9],
+                 (const float *)rt_b(c, op, 2), rt_ws(c, op, 2), p[10], r ? (int)r->halo : 0, r ? (int)r->W : 0};
+  if (e.opad && !rt_halo_kept(c, op, 1) &&
+      bnh_zero_halo(e.out, e.out_ws, p[4] / p[8], p[8], p[7], p[9], 4, c->nwin, c->stream))
+    return -1;
+  return bnh_gemm_f32((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4],
+                      gated ? (const float *)rt_b(c, op, 3) : nullptr, gated ? rt_ws(c, op, 3) : 0,
+                      (const float *)dev_tn(op, 0), (const float *)dev_tn(op, 1), p[2], p[3], &e, c->nwin, c->stream);
+}
+
 // -------- SE / SE_GATE: SE b = [D [P][C], chsum]; SE_GATE b = [chsum, gate f32 [C]]; t = [w1 [rd][C], b1 [rd],
 //          w2t [rd][C], b2 [C]]; p = [C rd P]   (rt_se_check, src/rt_ops_f32.c:256-266)
 static int se_check(rt_ctx *c, rt_op *op, int gate) {
@@ -300,6 +352,7 @@ static int gemv_run(rt_ctx *c, rt_op *op) { return rt_gemv_run(c, op, 0); }
 void *rt_dev_t(const rt_op *op, int i) { return dev_tn(op, i); }
 
 static const rt_kernel K_GEMV = {gemv_init, gemv_run, rt_dev_fini, "gemv_f32", 0x2, 0};
+static const rt_kernel K_PW = {pw_init, pw_run, rt_dev_fini, "pw_f32", 0x2, 0xc};
 static const rt_kernel K_LOGMEL = {logmel_init, logmel_run, logmel_fini, "fe_logmel", 0x2, 0};
 static const rt_kernel K_STEM = {stem_init, stem_run, rt_dev_fini, "stem_f32", 0x6, 0};
 static const rt_kernel K_SE = {se_init, se_run, rt_dev_fini, "se_f32", 0x1, 0};
@@ -331,6 +384,7 @@ int rt_fuse_pwdw(rt_ctx *c, rt_op *pw, rt_op *dw) {
 
 const rt_kernel *rt_k_f32(int base) {
   switch (base) {
+    case RT_OP_PW: return &K_PW;
     case RT_OP_DW3: return &K_DW3;
     case RT_OP_DWK: return &K_DWK;
     case RT_OP_FE_LOGMEL: return &K_LOGMEL;

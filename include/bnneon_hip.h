@@ -256,6 +256,13 @@ bnh_logmel *bnh_logmel_new(int nsamp, int frame, int hop, int pad, int nfft, int
 void bnh_logmel_free(bnh_logmel *F);
 int bnh_logmel_frames(const bnh_logmel *F);
 int bnh_logmel_run(const bnh_logmel *F, const float *pcm, long long p_ws, float *spec, long long s_ws, int B, void *stream);
+/* fp32 GEMM of the PW op: replaces gemm_f32 / gemm_f32_range_gate (src/gemm_f32.c:141-197; called by pw_run,
+ * src/rt_ops_f32.c:198-207): A f32 [M][lda] per window (lda >= Kp; rows < M read), gate (or NULL) f32 [Kp] per window
+ * scaling A[m][k] first, w the package's fp32 panels [Np/8][Kp][8] (Kp % 4 == 0, 16-byte aligned), bias [Np] ->
+ * e->out rows [0, M) x channels [0, Np) = act(A . W + b) (+ residual), stored by the epi32 rules. Every output is the
+ * reference's FMA chain over k < Kp, bit for bit. */
+int bnh_gemm_f32(const float *A, long long a_ws, int lda, int M, const float *gate, long long g_ws, const float *w,
+                 const float *bias, int Kp, int Np, const bnh_epi32 *e, int B, void *stream);
 /* STEM: replaces stem_run (src/rt_ops_f32.c:416-425; pc_im2col1 + gemm_f32): a 1-channel image [H][W], VALID k x k
  * stride s -> out [Ho][Wo][ldo] (opad: zero-haloed [Ho+2opad][Wo+2opad][ldo]) = act(conv + b), channels < Np stored;
  * w the package's fp32 panels [Np/8][Kp][8] (Kp >= k*k, Kp % 4 == 0; 16-byte aligned), bias [Np]. act 0/1/2. */

@@ -94,10 +94,20 @@ class OracleNet:
         self.put(bufs[b[1]], out)
         self.put(bufs[b[2]], cs)
 
-    # PW (variant 1: the fp16 GEMM)
+    # PW (variant 0: the fp32 GEMM, optional gate b[3]; variant 1: the fp16 GEMM)
     def op_3(self, var, b, t, p, bufs):
-        assert var == 1
         N, K, Kp, Np, M, lda, act, ldo, ow, opad, ldr = p
+        if var == 0:
+            rd = None if b[2] < 0 else self.desc(b[2])
+            res = None if b[2] < 0 else bufs[b[2]]
+            gate = bufs[b[3]][:K] if len(b) == 4 and b[3] >= 0 else None
+            out = O.gemm_f32(bufs[b[0]][:M * lda].reshape(M, lda), np.asarray(t[0], np.float32),
+                             np.asarray(t[1], np.float32), Kp, Np, act=act, gate=gate, res=res, ldr=ldr,
+                             rpad=rd["halo"] if rd else 0, rw=rd["W"] if rd else 0, ow=ow if opad else 0, opad=opad,
+                             ldo=ldo)
+            self.put(bufs[b[1]], out)
+            return
+        assert var == 1
         W = unpack_h16(t[0], N, Kp, Np)
         res = None if b[2] < 0 else bufs[b[2]][:M * ldr].reshape(M, ldr)
         out = O.gemm_f16(bufs[b[0]][:M * lda].reshape(M, lda), W, t[1][:N], act=act, ldo=ldo, ow=ow, opad=opad,
