@@ -105,6 +105,8 @@ _SIGS = {
     "bnh_logmel_free": (None, [vp]),
     "bnh_logmel_frames": (i32, [vp]),
     "bnh_logmel_run": (i32, [vp, vp, i64, vp, i64, i32, vp]),
+    "bnh_stem3_f16": (i32, [vp, i64, i32, i32, vp, vp, vp, i64, i32, vp]),
+    "bnh_unpad_f16": (i32, [vp, i64, i32, i32, i32, vp, i64, i32, vp]),
     "bnh_gemm_f32": (i32, [vp, i64, i32, i32, vp, i64, vp, vp, i32, i32, C.POINTER(Epi32), i32, vp]),
     "bnh_stem_f32": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, vp, i64, i32, i32, i32, vp]),
     "bnh_se_f32": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, vp]),

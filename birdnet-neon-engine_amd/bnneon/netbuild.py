@@ -16,7 +16,8 @@ F32, F16, I8, I32 = 0, 1, 2, 3
 HW_FP16 = 1
 OP = {"PW": 3, "DW3": 4, "SE": 5, "FE_LOGMEL": 8, "STEM": 9, "DWK": 10,
       "PAD": 11, "MEAN": 12, "GEMV": 15, "PW_S8": 22, "GEMV_S8": 23,
-      "SE_GATE": 25, "PROTO_S8": 35}
+      "SE_GATE": 25, "STEM3": 26, "CONV3C24": 27, "UNPAD": 28, "WINO_S8": 29, "PROTO_S8": 35}
+HW_DOTPROD = 2
 ACT = {None: 0, "none": 0, "silu": 1, "relu": 2}
 
 
@@ -343,6 +344,57 @@ class Net:
         self.emit(OP["PAD"], [ib, pb], [], [d[1], d[2], d[3], d[4], h], var=1 if d[0] == F16 else 0)
         self.last = pb
         return pb
+
+    # ---------------------------------------------------------------- the dotprod + fp16 family (variant 2)
+    def stem3(self, ib, w, b):
+        """STEM3 (src/rt_ops_dot.c:46-61): the 3-channel fp32 image ib [H][W][3] (H, W even) -> zero-haloed fp16
+        [H/2][W/2][24] = SiLU(3 x 3 stride-2 conv + b); w OHWI fp32 [24][3][3][3]."""
+        d = self.bufs[ib]
+        H, W = d[1], d[2]
+        assert d[0] == F32 and d[3] == 3 and d[4] == 3 and d[5] == 0
+        tl = [self.tensor("dot/stem3.w", np.asarray(w, np.float32).reshape(24, 3, 3, 3)),
+              self.tensor("dot/stem3.b", np.asarray(b, np.float32).reshape(24))]
+        ob = self.buf(F16, H // 2, W // 2, 24, halo=1)
+        self.emit(OP["STEM3"], [ib, ob], tl, [H, W, H // 2, W // 2], var=2)
+        self.last = ob
+        return ob
+
+    def wino_s8(self, ib, w, b):
+        """WINO_S8 (src/rt_ops_dot.c:130-170): x f32 rows [H][W][C] -> fp16 rows [H][W][K] = SiLU(3 x 3 conv + b)
+        through the int8 Winograd; w OHWI fp32 [K][3][3][C]."""
+        d = self.bufs[ib]
+        H, W, C = d[1], d[2], d[3]
+        assert d[0] == F32 and d[4] == C and d[5] == 0
+        w = np.asarray(w, np.float32)
+        K = w.shape[0]
+        tl = [self.tensor("dot/wino.w", w), self.tensor("dot/wino.b", np.asarray(b, np.float32).reshape(K))]
+        ob = self.buf(F16, H, W, K)
+        self.emit(OP["WINO_S8"], [ib, ob], tl, [H, W, C, K], var=2)
+        self.last = ob
+        return ob
+
+    def conv3c24(self, ib, w, b):
+        """CONV3C24 (src/rt_ops_dot.c:63-107): SiLU(3 x 3 conv + b) + x on the zero-haloed fp16 buffer ib of 24
+        channels, into a zero-haloed buffer; w OHWI fp32 [24][3][3][24]."""
+        d = self.bufs[ib]
+        H, W = d[1], d[2]
+        assert d[0] == F16 and d[3] == 24 and d[4] == 24 and d[5] == 1
+        tl = [self.tensor("dot/c24.w", np.asarray(w, np.float32).reshape(24, 3, 3, 24)),
+              self.tensor("dot/c24.b", np.asarray(b, np.float32).reshape(24))]
+        ob = self.buf(F16, H, W, 24, halo=1)
+        self.emit(OP["CONV3C24"], [ib, ob], tl, [H, W], var=2)
+        self.last = ob
+        return ob
+
+    def unpad(self, ib):
+        """UNPAD (src/rt_ops_dot.c:109-128): the interior of a zero-haloed fp16 buffer as fp32 rows."""
+        d = self.bufs[ib]
+        H, W, C = d[1], d[2], d[3]
+        assert d[0] == F16 and d[4] == C and d[5] == 1
+        ob = self.buf(F32, H, W, C)
+        self.emit(OP["UNPAD"], [ib, ob], [], [H, W, C], var=2)
+        self.last = ob
+        return ob
 
     def add_to(self, name="neon-int8", hwcap=0, in_buf=0, out_buf=None, emb_buf=None):
         self.pkg.add_path(name, hwcap, self.bufs, self.ops, in_buf,

@@ -27,6 +27,7 @@ SOURCES = [
     "kern_wino.hip",
     "kern_f16.hip",
     "kern_gemm_f32.hip",
+    "kern_dot.hip",
     "kern_fe.hip",
     "kern_f32.hip",
     "pkg_file.cpp",
@@ -37,6 +38,7 @@ SOURCES = [
     "ops_proto.cpp",
     "ops_f32.cpp",
     "ops_f16.cpp",
+    "ops_dot.cpp",
     "bnneon.cpp",
 ]
 

@@ -453,6 +453,22 @@ __global__ __launch_bounds__(256) void k_pad(const T *__restrict__ x, long long 
   *(vt *)(xp + win * p_ws + i) = v;
 }
 
+// UNPAD (src/rt_ops_dot.c:109-128): the interior of a zero-haloed fp16 buffer [H+2][W+2][C] widened to fp32 rows
+// [H][W][C]; a thread per 4 consecutive output elements of one window (W C % 4 == 0), windows on grid.y
+__global__ __launch_bounds__(256) void k_unpad_f16(const uint16_t *__restrict__ x, long long x_ws, int H, int W, int C,
+                                                   float *__restrict__ out, long long o_ws) {
+  const int i = (blockIdx.x * 256 + threadIdx.x) * 4, row = W * C;
+  if (i >= H * row) return;
+  const long long win = blockIdx.y;
+  const int y = i / row, r = i - y * row;
+  const uint16_t *s = x + win * x_ws + ((long long)(y + 1) * (W + 2) + 1) * C + r;
+  float4 v;
+  v.x = (float)hfrom(s[0]);
+  v.y = (float)hfrom(s[1]);
+  v.z = (float)hfrom(s[2]);
+  v.w = (float)hfrom(s[3]);
+  *(float4 *)(out + win * o_ws + i) = v;
+}
 
 static int se_launch(const float *chsum, long long c_ws, int C, int rd, int P, const float *w1, const float *b1,
                      const float *w2t, const float *b2, float *gate, long long g_ws, float *work, void *D,
@@ -682,6 +698,18 @@ int bnh_pad(const void *x, long long x_ws, int H, int W, int C, int ld, int h, i
     else hipLaunchKernelGGL((k_pad<uint16_t, 1>), grid, dim3(256), 0, st, (const uint16_t *)x, x_ws, H, W, C, ld, h,
                             (uint16_t *)xp, p_ws, (int)per);
   }
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_unpad_f16(const uint16_t *x, long long x_ws, int H, int W, int C, float *out, long long o_ws, int B,
+                  void *stream) {
+  BNH_REQ(x && out && H > 0 && W > 0 && C > 0 && (W * C) % 4 == 0 && B > 0);
+  BNH_REQ(((uintptr_t)out & 15) == 0 && (B == 1 || (x_ws >= (long long)(H + 2) * (W + 2) * C &&
+                                                    o_ws >= (long long)H * W * C && o_ws % 4 == 0)));
+  BNH_REQ((long long)H * W * C < (1LL << 31));
+  const dim3 grid((unsigned)bnh_ceil_div((long long)H * W * C, 1024), (unsigned)B);
+  hipLaunchKernelGGL(k_unpad_f16, grid, dim3(256), 0, bnh_stream(stream), x, x_ws, H, W, C, out, o_ws);
   BNH_HIP(hipGetLastError());
   return 0;
 }

@@ -195,5 +195,6 @@ enum { RT_ACT_NONE = 0, RT_ACT_SILU = 1, RT_ACT_RELU = 2 };
 // kernel tables (indexed by base opcode; an entry without run = not in the table), by variant
 extern const rt_kernel *rt_k_var0(int base);  // fp32 arithmetic and the int8 no-dotprod GEMMs
 extern const rt_kernel *rt_k_var1(int base);  // fp16 arithmetic
+extern const rt_kernel *rt_k_var2(int base);  // the dotprod + fp16 family
 const rt_kernel *rt_kernel_for(int code);
 #endif

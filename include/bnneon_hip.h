@@ -307,6 +307,16 @@ int bnh_gemv(const void *w, int w16, const float *bias, int N, int K, const floa
 /* MEAN: replaces pc_mean_f32 (src/pc_kern_f32.c:342-348): out [C] = (sum over P rows of x [P][ld]) / P */
 int bnh_mean_f32(const float *x, long long x_ws, int P, int C, int ld, float *out, long long o_ws, int B,
                  void *stream);
+/* STEM3: replaces stem3_run (src/rt_ops_dot.c:46-61; stem_conv_f32_h, src/kern_f16.c:15-71): img f32 [H][W][3] ->
+ * out fp16 zero-haloed [(H+1)/2 + 2][(W+1)/2 + 2][24] (the halo is left as it is) = the table SiLU of the fp16 rounding
+ * of the 3 x 3 stride-2 conv (taps past the bottom / right edge skipped) + b; w OHWI fp32 [24][3][3][3], b [24]. out
+ * 16-byte aligned. Bit-identical. */
+int bnh_stem3_f16(const float *img, long long i_ws, int H, int W, const float *w, const float *b, uint16_t *out,
+                  long long o_ws, int B, void *stream);
+/* UNPAD: replaces unpad_run (src/rt_ops_dot.c:109-128): the interior of a zero-haloed fp16 buffer [H+2][W+2][C]
+ * widened to fp32 rows [H][W][C] (W C % 4 == 0; out 16-byte aligned) */
+int bnh_unpad_f16(const uint16_t *x, long long x_ws, int H, int W, int C, float *out, long long o_ws, int B,
+                  void *stream);
 /* PAD: replaces pad_run (src/rt_ops_f32.c:503-508, src/rt_ops_f16.c:204-210): rows [H][W][ld] -> zero-haloed
  * [H+2h][W+2h][C], elements of esz (4 or 2) bytes */
 int bnh_pad(const void *x, long long x_ws, int H, int W, int C, int ld, int h, int esz, void *xp, long long p_ws, int B,

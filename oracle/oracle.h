@@ -176,6 +176,9 @@ void orc_mean_f16(const uint16_t *x, int P, int C, int ld, float *out);  /* src/
 /* GEMV with fp32 (w16 NULL) or fp16 weights (src/gemv.c:13-49) */
 void orc_gemv(const float *w32, const uint16_t *w16, const float *b, int N, int K, const float *x, int act, float *out);
 
+/* ---------------------------------------------------------------- dotprod + fp16 family (dot.c) */
+void orc_stem3_f32h(const float *img, int H, int W, const float *w, const float *b, uint16_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -114,6 +114,31 @@ class OracleNet:
                          res=res, b16=np.asarray(t[2]).view(np.float16)[:Np])
         self.put(bufs[b[1]], out)
 
+    # STEM3 (variant 2): the 3-channel image's stride-2 conv into 24 fp16 channels
+    def op_26(self, var, b, t, p, bufs):
+        H, W, Ho, Wo = p
+        img = bufs[b[0]][:H * W * 3].reshape(H, W, 3)
+        self.put(bufs[b[1]], O.stem3(img, np.asarray(t[0], np.float32), np.asarray(t[1], np.float32)))
+
+    # CONV3C24 (variant 2): the fp16 Winograd of src/wino_s0.c, residual = its own input, zero-haloed output
+    def op_27(self, var, b, t, p, bufs):
+        H, W = p
+        xp = bufs[b[0]][:(H + 2) * (W + 2) * 24].reshape(H + 2, W + 2, 24)
+        w = np.asarray(t[0], np.float32).reshape(24, 3, 3, 24)
+        self.put(bufs[b[1]], O.wino_s0(xp, w, np.asarray(t[1], np.float32)))
+
+    # UNPAD (variant 2): the haloed fp16 interior widened to fp32 rows
+    def op_28(self, var, b, t, p, bufs):
+        H, W, C = p
+        xp = bufs[b[0]][:(H + 2) * (W + 2) * C].reshape(H + 2, W + 2, C)
+        self.put(bufs[b[1]], xp[1:-1, 1:-1].astype(np.float32))
+
+    # WINO_S8 (variant 2): the int8 Winograd of src/wino.c
+    def op_29(self, var, b, t, p, bufs):
+        H, W, C, K = p
+        w = np.asarray(t[0], np.float32).reshape(K, 3, 3, C)
+        self.put(bufs[b[1]], O.wino8(bufs[b[0]][:H * W * C].reshape(H, W, C), O.wino8_pack(w), t[1]))
+
     # PROTO_S8: buffers [cells, logits, q, colmax], tensors [q panels, sw, n4, clsw, clsb, eps]
     def op_35(self, var, b, t, p, bufs):
         N, K, Kp, Np, P_, C, ld, nc, ppc = p

@@ -511,3 +511,17 @@ def gemv(w, b, x, act=0):
     assert w32 is not None or w16 is not None
     lib().orc_gemv(w32, w16, P(_c(b, np.float32)), N, K, P(_c(x, np.float32)), act, P(out))
     return out
+
+
+_SIGS.update({"orc_stem3_f32h": (None, [vp, i32, i32, vp, vp, vp])})
+
+
+def stem3(img, w, b):
+    """STEM3 of one window: img f32 [H][W][3] -> fp16 zero-haloed [(H+1)/2 + 2][(W+1)/2 + 2][24]."""
+    img = _c(img, np.float32)
+    H, W = img.shape[:2]
+    Ho, Wo = (H + 1) // 2, (W + 1) // 2
+    out = np.zeros((Ho + 2, Wo + 2, 24), np.uint16)
+    lib().orc_stem3_f32h(img.ctypes.data, H, W, _c(w, np.float32).ctypes.data, _c(b, np.float32).ctypes.data,
+                         out.ctypes.data)
+    return out.view(np.float16)
