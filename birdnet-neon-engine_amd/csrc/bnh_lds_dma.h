@@ -17,6 +17,12 @@ __device__ __forceinline__ void rq_dma16(const int8_t *src, const lds_i8 *dst) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
 }
+// the saddr form: a wave-uniform 64-bit base (SGPRs) plus a 32-bit per-lane byte offset, so a ring whose lane
+// offsets do not change from step to step spends no vector instruction on addresses
+__device__ __forceinline__ void rq_dma16s(const void *base, uint32_t off, const lds_i8 *dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
+}
 #define RQ_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 #define RQ_BARRIER() asm volatile("s_barrier" ::: "memory")
 

@@ -191,12 +191,6 @@ __global__ __launch_bounds__(256) void k_proto_colmax(const int8_t *__restrict__
 typedef __attribute__((address_space(3))) v4i lds_v4i;
 typedef __attribute__((address_space(3))) float lds_f32;
 
-// the saddr form of the LDS DMA: a wave-uniform 64-bit base (SGPRs) plus a 32-bit per-lane byte offset
-BNH_DEV void pg_dma16(const void *base, uint32_t off, const lds_i8 *dst) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
-}
-
 BNH_DEV float pg_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 // an accumulator element read out of its AGPR where the epilogue uses it: without this the compiler copies all 256
 // accumulators into VGPRs when the K loop ends and spills the block's other values to scratch
@@ -264,18 +258,18 @@ __global__ __launch_bounds__(256, 1) void k_proto_gemm64(const int8_t *__restric
         if (wave == 0) {
           const int last = B - 1 - m_t * 4;  // windows past the last one read the last window's scales (unused)
           const int wl = (lane >> 4) < last ? (lane >> 4) : last;
-          pg_dma16(sx + (long long)m_t * 4 * sx_ws, (uint32_t)(wl * sx_ws * 4 + 16 * (lane & 15)), sc);
+          rq_dma16s(sx + (long long)m_t * 4 * sx_ws, (uint32_t)(wl * sx_ws * 4 + 16 * (lane & 15)), sc);
         } else {
-          pg_dma16(sw + n_t * PG_TN, (uint32_t)(16 * lane), sc);
+          rq_dma16s(sw + n_t * PG_TN, (uint32_t)(16 * lane), sc);
         }
       }
     }
     lds_i8 *st = lds + iss_st * PG_STAGE;
     const int8_t *ab = a_tile + iss_k * PG_BK, *bb = b_tile + iss_k * 1024;
 #pragma unroll
-    for (int h = 0; h < 4; h++) pg_dma16(ab + h * a16, loff_a, st + (4 * wave + h) * 1024);
+    for (int h = 0; h < 4; h++) rq_dma16s(ab + h * a16, loff_a, st + (4 * wave + h) * 1024);
 #pragma unroll
-    for (int h = 0; h < 4; h++) pg_dma16(bb + h * b16, loff_b, st + PG_AB + (4 * wave + h) * 1024);
+    for (int h = 0; h < 4; h++) rq_dma16s(bb + h * b16, loff_b, st + PG_AB + (4 * wave + h) * 1024);
     if (++iss_st == PG_NST) iss_st = 0;
     if (++iss_k == steps) { iss_k = 0; iss_i++; }
   };

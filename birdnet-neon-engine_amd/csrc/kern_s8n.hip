@@ -592,6 +592,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_s8_requant2(const int8_t *__res
 #define RQ4_STAGE (RQ4_XB + RQ4_CH * RQ4_BK)
 #define RQ4_NST 4
 #define RQ4_NLD 4  // DMA instructions per wave per K step: 2 activation + 2 weight
+#define RQ4_MAXNT 1024  // channels (padded) whose requant vectors the kernel keeps in LDS
 typedef int v2i __attribute__((ext_vector_type(2)));
 // (direct global -> LDS loads: bnh_lds_dma.h)
 
@@ -603,10 +604,19 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
                                                           const int32_t *__restrict__ shift, int N, int zy, int lo,
                                                           int hi, int8_t *__restrict__ out, long long out_ws) {
   __shared__ __attribute__((aligned(1024))) int8_t lds_raw[RQ4_NST * RQ4_STAGE];
+  // the per-channel requant vectors of all Nt channels (bias_eff, mult, shift), read by the epilogues from LDS: a
+  // global load there would make the compiler wait for every DMA in flight (it counts only its own loads)
+  __shared__ int32_t s_chan[3 * RQ4_MAXNT];
   lds_i8 *lds = (lds_i8 *)lds_raw;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int steps = Kt / RQ4_BK;
+  for (int i = tid; i < nblk * RQ4_CH; i += 512) {
+    s_chan[i] = bias_eff[i];
+    s_chan[RQ4_MAXNT + i] = mult[i];
+    s_chan[2 * RQ4_MAXNT + i] = shift[i];
+  }
+  __syncthreads();
   const int rot = (int)(blockIdx.x % steps);
   const int mytiles = ntiles > (int)blockIdx.x ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
   const int total = mytiles * steps;
@@ -616,6 +626,16 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
   // lane -> row 16q + lane / 4, slot lane % 4 = chunk (lane % 4) ^ ((lane / 8) % 4)
   const int xr = lane >> 4, xslot = lane & 15;
   const int wrow = lane >> 2, wchunk = (lane & 3) ^ ((lane >> 3) & 3);
+  // whole tiles (K % 64 == 0, M % 256 == 0): no row or column clamps, so each lane's offsets from the step's base
+  // are the same at every step and the DMA takes its base in SGPRs
+  const bool whole = K % RQ4_BK == 0 && M % RQ4_PIX == 0;
+  uint32_t xoff[2], woff[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int q = 2 * wave + h, row = 4 * q + xr;
+    xoff[h] = (uint32_t)(row * M + 16 * (xslot ^ (row & 7)));
+    woff[h] = (uint32_t)((16 * q + wrow) * Kt + 16 * wchunk);
+  }
   auto issue = [&](int gs) {
     const int t = (int)blockIdx.x + (gs / steps) * (int)gridDim.x;
     int s = gs % steps + rot;
@@ -623,6 +643,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
     const int cb = t % nblk, rest = t / nblk, p0 = (rest % tpw) * RQ4_PIX, win = rest / tpw;
     const int8_t *xw = x + win * x_ws;
     lds_i8 *st = lds + (gs % RQ4_NST) * RQ4_STAGE;
+    if (whole) {
+      const int8_t *xb = xw + (long long)s * RQ4_BK * M + p0, *wb = wt + (long long)cb * RQ4_CH * Kt + s * RQ4_BK;
+#pragma unroll
+      for (int h = 0; h < 2; h++) rq_dma16s(xb, xoff[h], st + (2 * wave + h) * 1024);
+#pragma unroll
+      for (int h = 0; h < 2; h++) rq_dma16s(wb, woff[h], st + RQ4_XB + (2 * wave + h) * 1024);
+      return;
+    }
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const int q = 2 * wave + h, row = 4 * q + xr;
@@ -659,11 +687,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) acc[t][jj] = (v4i){0, 0, 0, 0};
   for (int gs = 0; gs < RQ4_NST - 1 && gs < total; gs++) issue(gs);
+  int last_epi = -RQ4_NST;  // the step whose end ran the latest epilogue
   for (int gs = 0; gs < total; gs++) {
-    // this wave's loads of step gs have landed once at most the loads of the RQ4_NST - 2 later steps are outstanding
-    // (vector-memory loads retire in order; the epilogue's stores only make the wait longer)
-    if (gs + RQ4_NST - 2 < total) RQ_WAIT_VM(8);  // RQ4_NLD * (RQ4_NST - 2)
-    else RQ_WAIT_VM(0);
+    // this wave's loads of step gs have landed once at most the RQ4_NLD loads of each of the RQ4_NST - 2 later steps
+    // are outstanding, and in the RQ4_NST - 1 steps after an epilogue its 8 stores as well (vector-memory
+    // operations retire in issue order; every epilogue issues exactly 8 store instructions per wave)
+    if (gs + RQ4_NST - 2 >= total) RQ_WAIT_VM(0);
+    else if (gs - last_epi <= RQ4_NST - 1) RQ_WAIT_VM(16);  // RQ4_NLD * (RQ4_NST - 2) + 8
+    else RQ_WAIT_VM(8);                                     // RQ4_NLD * (RQ4_NST - 2)
     RQ_BARRIER();  // every wave's loads of step gs have landed; the stage step gs - 1 used is no longer read
     if (gs + RQ4_NST - 1 < total) issue(gs + RQ4_NST - 1);
     const lds_i8 *st = lds + (gs % RQ4_NST) * RQ4_STAGE;
@@ -684,19 +715,26 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
     // ---- epilogue of tile t: requantise, stage 128 channels x 256 pixels at a time, store whole rows
     const int t = (int)blockIdx.x + (gs / steps) * (int)gridDim.x;
     const int cb = t % nblk, rest = t / nblk, p0 = (rest % tpw) * RQ4_PIX, win = rest / tpw;
-    int8_t *ow = out + win * out_ws;
+    // the window's output as a buffer: a store past it (channels >= N, pixels >= M) is dropped by the range check,
+    // so every wave issues the same 8 store instructions
+    const __amdgpu_buffer_rsrc_t orr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(out + win * out_ws), 0, N * M, 0x00020000);
     uint32_t wd[8][4];
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) {
       const int n = cb * RQ4_CH + wn * 128 + 16 * jj + j;  // < Nt: the per-channel vectors are padded to Nt
-      const int32_t be = bias_eff[n], mu = mult[n], sh = shift[n];
+      const int32_t be = s_chan[n], mu = s_chan[RQ4_MAXNT + n], sh = s_chan[2 * RQ4_MAXNT + n];
+      const bool s1 = sh >= 1 && sh <= 31;
+      const BnhRqS1 rc = bnh_rq_s1(s1 ? sh : 1);
 #pragma unroll
       for (int tt = 0; tt < 4; tt++) {
         uint32_t word = 0;
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-          word |= ((uint32_t)bnh_requant((int32_t)((uint32_t)acc[tt][jj][r] + (uint32_t)be), mu, sh, zy, lo, hi) &
-                   0xffu) << (8 * r);
+        for (int r = 0; r < 4; r++) {
+          const int32_t a32 = (int32_t)((uint32_t)acc[tt][jj][r] + (uint32_t)be);
+          const int32_t y = s1 ? bnh_requant_s1(a32, mu, rc, zy, lo, hi) : bnh_requant(a32, mu, sh, zy, lo, hi);
+          word |= ((uint32_t)y & 0xffu) << (8 * r);
+        }
         wd[jj][tt] = word;
         acc[tt][jj] = (v4i){0, 0, 0, 0};
       }
@@ -722,10 +760,11 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
         const int chunk = i * 512 + tid, ch = chunk >> 4, cp = chunk & 15;
         const v4i val = *(const __attribute__((address_space(3))) v4i *)(ob + ch * 256 + 16 * cp);
         const int n = cb * RQ4_CH + half * 128 + ch, p = p0 + 16 * (cp ^ (ch & 15));
-        if (n < N && p < M) *(v4i *)(ow + (long long)n * M + p) = val;
+        __builtin_amdgcn_raw_buffer_store_b128(val, orr, n < N && p < M ? n * M + p : 0x7ffffff0, 0, 0);
       }
       RQ_BARRIER();
     }
+    last_epi = gs;
   }
 }
 
@@ -966,7 +1005,8 @@ int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M
   BNH_REQ(B == 1 || (x_ws % 4 == 0 && out_ws % 4 == 0 && x_ws >= (long long)W->K * M && out_ws >= (long long)W->N * M));
   BNH_REQ(W->K % 16 == 0);
   hipStream_t st = bnh_stream(stream);
-  if (M % 16 == 0 && ((uintptr_t)x & 15) == 0 && (B == 1 || x_ws % 16 == 0)) {
+  if (M % 16 == 0 && ((uintptr_t)x & 15) == 0 && (B == 1 || x_ws % 16 == 0) && W->Nt <= RQ4_MAXNT &&
+      (long long)W->N * M < (1LL << 31)) {
     static int ncu = 0;
     if (!ncu) {
       int dev = 0;
