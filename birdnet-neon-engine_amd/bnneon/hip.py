@@ -34,6 +34,13 @@ class Epi16(C.Structure):
                 ("ldr", i32)]
 
 
+class QdEpi(C.Structure):
+    """bnh_qd_epi: the dotprod int8 GEMM's epilogue (per-window strides)."""
+    _fields_ = [("act", i32), ("out_f16", i32), ("out", vp), ("out_ws", i64),
+                ("ldo", i32), ("ow", i32), ("opad", i32), ("res", vp),
+                ("res_ws", i64)]
+
+
 _SIGS = {
     "bnh_last_error": (C.c_char_p, []),
     "bnh_device_count": (i32, []),
@@ -120,6 +127,22 @@ _SIGS = {
     "bnh_se_gate_f16": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, vp]),
     "bnh_mean_f16": (i32, [vp, i64, i32, i32, i32, vp, i64, i32, vp]),
     "bnh_gemv": (i32, [vp, i32, vp, i32, i32, vp, i64, i32, vp, i64, i32, vp]),
+    "bnh_qdw_new": (vp, [vp, vp, i32, i32, i32]),
+    "bnh_qdw_free": (None, [vp]),
+    "bnh_qdw_shape": (i32, [vp, vp, vp, vp, vp]),
+    "bnh_qd_quant_rows": (i32, [vp, i32, i64, i32, i32, i32, vp, i64, vp, i64, vp, i64, i32, vp]),
+    "bnh_qd_gemm": (i32, [vp, i64, i32, vp, i64, i32, i32, vp, C.POINTER(QdEpi), i32, vp]),
+    "bnh_qconv3_work_bytes": (C.c_size_t, [i32, i32, i32]),
+    "bnh_qconv3": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, i64, i32, vp, C.c_size_t, vp]),
+    "bnh_heads8_new": (vp, [i32, i32, i32, vp, vp]),
+    "bnh_heads8_free": (None, [vp]),
+    "bnh_heads8_work_bytes": (C.c_size_t, [i32, i32, i32, i32, i32]),
+    "bnh_heads_s8": (i32, [vp, i64, vp, i64, i32, i32, vp, vp, i64, vp, i64, vp, i64, i32, vp, C.c_size_t, vp]),
+    "bnh_seg16_new": (vp, [i32, i32, vp, vp, vp, vp]),
+    "bnh_seg16_free": (None, [vp]),
+    "bnh_se_gate16": (i32, [vp, i64, i32, vp, vp, i64, i32, vp]),
+    "bnh_gem_a": (i32, [vp, i64, i32, i32, C.c_float, C.c_float, vp, i64, i32, vp]),
+    "bnh_eval_qd": (i32, [i32, vp, vp, i64, vp]),
 }
 
 

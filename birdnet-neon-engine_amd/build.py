@@ -28,6 +28,7 @@ SOURCES = [
     "kern_f16.hip",
     "kern_gemm_f32.hip",
     "kern_dot.hip",
+    "kern_qdot.hip",
     "kern_fe.hip",
     "kern_f32.hip",
     "pkg_file.cpp",

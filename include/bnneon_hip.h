@@ -326,6 +326,68 @@ int bnh_zero_halo(void *xp, long long ws, int H, int W, int C, int h, int esz, i
 /* test hook: y = expf(x) as the C library computes it (glibc's table method), elementwise on the device */
 int bnh_eval_expf(const float *x, float *y, long long n, void *stream);
 
+/* ------------------------------------------------------------------ dotprod int8 family (QPW, QCONV3, HEADS_S8)
+ * libbnneon's int8 SDOT arithmetic (src/gemm_s8.c), bit-identical: activations quantised per row (or per tensor) to
+ * [-128, 127] with scale s and float zero point zp (rq = {s, zp} pairs), weights per channel to [-127, 127]; int32
+ * sums, then v = (b + (acc sw) s) + swsum (s zp), both sums fused; fp16 out (act 0 / 1: the table SiLU) or fp32 out
+ * (act 0 / 1 / 2: silu_f32_a / ReLU, then + res). Inputs with NaNs are outside what the parity tests cover. */
+typedef struct bnh_qdw bnh_qdw;
+/* qw_pack (src/gemm_s8.c:10-35): w fp32 [N][K], bias [N] (or NULL); Np >= N, Np % 16 == 0: channels past N are zero
+ * rows (pack_padded, src/rt_ops_dot.c:467-473) */
+bnh_qdw *bnh_qdw_new(const float *w, const float *bias, int N, int K, int Np);
+void bnh_qdw_free(bnh_qdw *W);
+int bnh_qdw_shape(const bnh_qdw *W, int *N, int *K, int *Kp, int *Np);
+/* quant_rows_f32 / quant_rows_f16 (src/gemm_s8.c:306-371): x rows [M][ldx] (fp32, or fp16 when in_f16, optionally
+ * multiplied channel-wise by the fp16 gate [K]) -> a int8 [M][Kp] (Kp = K rounded up to 16, zero past K, a and a_ws
+ * 4-byte aligned), rq fp32 [M][2] */
+int bnh_qd_quant_rows(const void *x, int in_f16, long long x_ws, int ldx, int M, int K, const uint16_t *gate,
+                      long long g_ws, int8_t *a, long long a_ws, float *rq, long long rq_ws, int B, void *stream);
+typedef struct {
+  int act;          /* 0 none, 1 SiLU, 2 ReLU (fp32 out only) */
+  int out_f16;      /* 1: out is fp16, 0: fp32 */
+  void *out;        /* rows [M][ldo], or zero-haloed (opad 1, image width ow) rows */
+  long long out_ws; /* elements */
+  int ldo, ow, opad;
+  const float *res; /* fp32 out only: residual rows [M][ldo] (no halo), or NULL */
+  long long res_ws;
+} bnh_qd_epi;       /* epi (src/kern.h:33-40) */
+/* gemm_s8 (src/gemm_s8.c:153-278): a int8 rows [M][lda] (16-byte aligned), rq per row [M][2] (per_tensor: one pair per
+ * window) -> the epilogue e over W->Np channels */
+int bnh_qd_gemm(const int8_t *a, long long a_ws, int lda, const float *rq, long long rq_ws, int per_tensor, int M,
+                const bnh_qdw *W, const bnh_qd_epi *e, int B, void *stream);
+/* QCONV3: replaces qconv_run (src/rt_ops_dot.c:177-216): x f32 [H][W][C] -> out fp16 rows [Ho][Wo][Wq->Np] = the table
+ * SiLU of the 3 x 3 stride-s conv (TF-same low pads pt, pl) over the per-tensor quantised input; Wq from OHWI weights
+ * viewed as [K][9 C]. work: per-window device scratch slots of work_ws >= bnh_qconv3_work_bytes bytes (256-aligned). */
+size_t bnh_qconv3_work_bytes(int H, int W, int C);
+int bnh_qconv3(const float *x, long long x_ws, int H, int W, int C, int s, int pt, int pl, int Ho, int Wo,
+               const bnh_qdw *Wq, uint16_t *out, long long o_ws, int B, void *work, size_t work_ws, void *stream);
+/* HEADS_S8: replaces heads_run (src/rt_ops_dot.c:520-572): logits [ncp] = lin(emb) + the two SED heads over F [H*W][C]
+ * (per time step the mean over the other axis, max + average pool 3, fc + ReLU, att clipped to [-10, 10] and
+ * soft-maxed over time, cla weighted by it). w / b: lin [nc][C], then per head fc [hid][C], att [nc][hid], cla
+ * [nc][hid]. a8 / rq: the op's int8 rows ((L + 4) max(C, hid) bytes) and scales (2 (L + 4) floats), L = max(H, W);
+ * work: per-window scratch slots of work_ws >= bnh_heads8_work_bytes bytes. */
+typedef struct bnh_heads8 bnh_heads8;
+bnh_heads8 *bnh_heads8_new(int C, int hid, int nc, const float *const *w, const float *const *b);
+void bnh_heads8_free(bnh_heads8 *P);
+size_t bnh_heads8_work_bytes(int H, int W, int C, int hid, int nc);
+int bnh_heads_s8(const float *F, long long f_ws, const float *emb, long long e_ws, int H, int W, const bnh_heads8 *P,
+                 float *logits, long long l_ws, int8_t *a8, long long a8_ws, float *rq, long long rq_ws, int B,
+                 void *work, size_t work_ws, void *stream);
+/* SE_GATE16: replaces seg_run (src/rt_ops_dot.c:381-420): chsum [C] scaled to means in place (x (1/P)), gate fp16 [C]
+ * = sigmoid(fc2(SiLU(fc1(means)))) with fp16-held weights w1 [rd][C], w2 [C][rd] and fp32 arithmetic */
+typedef struct bnh_seg16 bnh_seg16;
+bnh_seg16 *bnh_seg16_new(int C, int rd, const float *w1, const float *b1, const float *w2, const float *b2);
+void bnh_seg16_free(bnh_seg16 *S);
+int bnh_se_gate16(float *chsum, long long c_ws, int P, const bnh_seg16 *S, uint16_t *gate, long long g_ws, int B,
+                  void *stream);
+/* GEM_A: replaces gem_run (src/rt_ops_dot.c:439-465): e [C] = (mean over the M rows of F [M][C] of max(F, eps)^p)^(1/p)
+ * with the reference's exp2 / log2 polynomials; the final power is rounded once from double precision, so it may
+ * differ from the C library's powf by one unit in the last place */
+int bnh_gem_a(const float *F, long long f_ws, int M, int C, float eps, float p, float *e, long long e_ws, int B,
+              void *stream);
+/* test hook: the family's scalar functions elementwise (f 0 exp2_p5, 1 silu_f32_a, 2 log2_f32, 3 the SE sigmoid) */
+int bnh_eval_qd(int f, const float *x, float *y, long long n, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

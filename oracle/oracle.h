@@ -179,6 +179,35 @@ void orc_gemv(const float *w32, const uint16_t *w16, const float *b, int N, int 
 /* ---------------------------------------------------------------- dotprod + fp16 family (dot.c) */
 void orc_stem3_f32h(const float *img, int H, int W, const float *w, const float *b, uint16_t *out);
 
+/* ---------------------------------------------------------------- dotprod int8 (qdot.c) */
+typedef struct {
+  int act;          /* 0 none, 1 SiLU, 2 ReLU (src/kern.h:31) */
+  uint16_t *out16;  /* fp16 output, or NULL */
+  float *out32;     /* fp32 output, or NULL */
+  int ldo, ow, opad;
+  const float *res32;  /* fp32 residual rows [M][ldo], or NULL */
+} orc_qd_epi;          /* src/kern.h:33-40 */
+void orc_qd_wpack(const float *w, const float *bias, int N, int K, int8_t *q, float *scale, float *swsum, float *b);
+void orc_qd_params(float mn, float mx, float *scale, float *zp, float *inv);
+void orc_qd_quant_rows_f32(const float *x, int ldx, int M, int C, int8_t *a, int lda, int Cp, float *rq);
+void orc_qd_quant_rows_f16(const uint16_t *x, int ldx, int M, int C, const uint16_t *gate, int8_t *a, int lda, int Cp,
+                           float *rq);
+float orc_exp2_p5(float t);
+float orc_silu_f32_a(float x);
+float orc_log2_dot(float x);
+void orc_qd_gemm(const int8_t *a, int lda, const float *rq, int per_tensor, int M, int N, int Kp, const int8_t *q,
+                 const float *scale, const float *swsum, const float *b, const orc_qd_epi *e);
+void orc_qpw(const void *x, int in_f16, int ldx, int M, int K, const uint16_t *gate, int8_t *a8, float *rq, int N,
+             const int8_t *q, const float *scale, const float *swsum, const float *b, const orc_qd_epi *e);
+void orc_qd_quant_tensor_pad(const float *x, int H, int W, int C, int8_t *out, float *rq);
+void orc_qconv3(const float *x, int H, int W, int C, int K, int s, int pt, int pl, int Ho, int Wo, const int8_t *q,
+                const float *scale, const float *swsum, const float *b, int8_t *xp, int8_t *col, uint16_t *out);
+void orc_se_gate16(float *chsum, int C, int rd, int P, const float *w1, const float *b1, const float *w2,
+                   const float *b2, uint16_t *gate);
+void orc_gem_a(const float *F, int M, int C, float eps, float p, float *e);
+void orc_heads_s8(const float *F, const float *emb, int H, int W, int C, int hid, int nc, const int8_t *const *wq,
+                  const float *const *sc, const float *const *ss, const float *const *bb, float *logits, float *work);
+
 #ifdef __cplusplus
 }
 #endif

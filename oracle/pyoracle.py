@@ -525,3 +525,153 @@ def stem3(img, w, b):
     lib().orc_stem3_f32h(img.ctypes.data, H, W, _c(w, np.float32).ctypes.data, _c(b, np.float32).ctypes.data,
                          out.ctypes.data)
     return out.view(np.float16)
+
+
+# ---------------------------------------------------------------- dotprod int8 family (qdot.c)
+class OrcQdEpi(C.Structure):
+    _fields_ = [("act", i32), ("out16", vp), ("out32", vp), ("ldo", i32), ("ow", i32), ("opad", i32),
+                ("res32", vp)]
+
+
+_SIGS.update({
+    "orc_qd_wpack": (None, [vp, vp, i32, i32, vp, vp, vp, vp]),
+    "orc_qd_quant_rows_f32": (None, [vp, i32, i32, i32, vp, i32, i32, vp]),
+    "orc_qd_quant_rows_f16": (None, [vp, i32, i32, i32, vp, vp, i32, i32, vp]),
+    "orc_exp2_p5": (f32, [f32]),
+    "orc_silu_f32_a": (f32, [f32]),
+    "orc_log2_dot": (f32, [f32]),
+    "orc_qd_params": (None, [f32, f32, vp, vp, vp]),
+    "orc_qd_gemm": (None, [vp, i32, vp, i32, i32, i32, i32, vp, vp, vp, vp, C.POINTER(OrcQdEpi)]),
+    "orc_qd_quant_tensor_pad": (None, [vp, i32, i32, i32, vp, vp]),
+    "orc_qconv3": (None, [vp, i32, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp]),
+    "orc_se_gate16": (None, [vp, i32, i32, i32, vp, vp, vp, vp, vp]),
+    "orc_gem_a": (None, [vp, i32, i32, f32, f32, vp]),
+    "orc_heads_s8": (None, [vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, vp]),
+})
+
+
+def qd_wpack(w, b, Np=None):
+    """qw_pack of w f32 [N][K] -> dict(q int8 [Np][Kp], scale, swsum, b [Np]); rows past N are zero (pack_padded)."""
+    w = _c(w, np.float32)
+    N, K = w.shape
+    Np = Np or N
+    Kp = (K + 15) // 16 * 16
+    wp = np.zeros((Np, K), np.float32)
+    wp[:N] = w
+    bp = np.zeros(Np, np.float32)
+    if b is not None:
+        bp[:N] = b
+    q = np.zeros((Np, Kp), np.int8)
+    sc, ss, bb = (np.zeros(Np, np.float32) for _ in range(3))
+    lib().orc_qd_wpack(P(wp), P(bp), Np, K, P(q), P(sc), P(ss), P(bb))
+    return dict(q=q, scale=sc, swsum=ss, b=bb, shape=(N, K, Kp, Np))
+
+
+def qd_params(mn, mx):
+    s, zp, inv = (np.zeros(1, np.float32) for _ in range(3))
+    lib().orc_qd_params(float(mn), float(mx), P(s), P(zp), P(inv))
+    return float(s[0]), float(zp[0]), float(inv[0])
+
+
+def qd_quant_rows(x, K, gate=None):
+    """quant_rows_f32 (x float32) or quant_rows_f16 (x float16, optional fp16 gate) of x [M][ldx] -> (a [M][Kp], rq)."""
+    x = np.ascontiguousarray(x)
+    M, ldx = x.shape
+    Kp = (K + 15) // 16 * 16
+    a = np.zeros((M, Kp), np.int8)
+    rq = np.zeros((M, 2), np.float32)
+    if x.dtype == np.float16:
+        g = None if gate is None else _c(gate, np.float16)
+        lib().orc_qd_quant_rows_f16(P(x), ldx, M, K, P(g), P(a), Kp, Kp, P(rq))
+    else:
+        assert gate is None
+        lib().orc_qd_quant_rows_f32(P(_c(x, np.float32)), ldx, M, K, P(a), Kp, Kp, P(rq))
+    return a, rq
+
+
+def qd_gemm(a, rq, pk, act=0, out16=False, ldo=None, ow=0, opad=0, res=None, per_tensor=False, M=None):
+    """gemm_s8 of a int8 [M][Kp] -> out [rows][ldo] (fp16 when out16)."""
+    a = _c(a, np.int8)
+    M = M or a.shape[0]
+    N, K, Kp, Np = pk["shape"]
+    ldo = ldo or Np
+    rows = M if not opad else (M // ow + 2) * (ow + 2)
+    out = np.zeros((rows, ldo), np.float16 if out16 else np.float32)
+    r = None if res is None else _c(res, np.float32)
+    e = OrcQdEpi(act, P(out) if out16 else None, None if out16 else P(out), ldo, ow, opad, P(r))
+    lib().orc_qd_gemm(P(a), a.shape[1], P(_c(rq, np.float32)), int(per_tensor), M, Np, Kp, P(pk["q"]),
+                      P(pk["scale"]), P(pk["swsum"]), P(pk["b"]), C.byref(e))
+    return out
+
+
+def qpw(x, pk, act=0, out16=False, ldo=None, ow=0, opad=0, res=None, gate=None):
+    """QPW of one window: x rows [M][ldx] (float32, or float16 with an optional gate) -> (out, a8, rq)."""
+    N, K, Kp, Np = pk["shape"]
+    a, rq = qd_quant_rows(x, K, gate)
+    return qd_gemm(a, rq, pk, act, out16, ldo, ow, opad, res), a, rq
+
+
+def qd_quant_tensor_pad(x):
+    x = _c(x, np.float32)
+    H, W, Cc = x.shape
+    out = np.zeros((H + 2, W + 2, Cc), np.int8)
+    rq = np.zeros(2, np.float32)
+    lib().orc_qd_quant_tensor_pad(P(x), H, W, Cc, P(out), P(rq))
+    return out, rq
+
+
+def tf_same(n, k, s):
+    o = (n + s - 1) // s
+    tot = (o - 1) * s + k - n
+    return o, max(tot, 0) // 2
+
+
+def qconv3(x, pk, s):
+    """QCONV3 of one window: x f32 [H][W][C], pk = qd_wpack of OHWI weights viewed [K][9C] -> fp16 [Ho*Wo][K]."""
+    x = _c(x, np.float32)
+    H, W, Cc = x.shape
+    N, K9, Kp, Np = pk["shape"]
+    Ho, pt = tf_same(H, 3, s)
+    Wo, pl = tf_same(W, 3, s)
+    xp = np.zeros((H + 2) * (W + 2) * Cc, np.int8)
+    col = np.zeros(Ho * Wo * Kp, np.int8)
+    out = np.zeros((Ho * Wo, Np), np.float16)
+    lib().orc_qconv3(P(x), H, W, Cc, Np, s, pt, pl, Ho, Wo, P(pk["q"]), P(pk["scale"]), P(pk["swsum"]),
+                     P(pk["b"]), P(xp), P(col), P(out))
+    return out
+
+
+def se_gate16(chsum, P_, w1, b1, w2, b2):
+    """SE_GATE16 of one window -> (means [C], gate fp16 [C])."""
+    cs = _c(chsum, np.float32).copy()
+    rd, Cc = w1.shape
+    g = np.zeros(Cc, np.float16)
+    lib().orc_se_gate16(P(cs), Cc, rd, P_, P(_c(w1, np.float32)), P(_c(b1, np.float32)), P(_c(w2, np.float32)),
+                        P(_c(b2, np.float32)), P(g))
+    return cs, g
+
+
+def gem_a(F, eps, p):
+    F = _c(F, np.float32)
+    M, Cc = F.shape
+    e = np.zeros(Cc, np.float32)
+    lib().orc_gem_a(P(F), M, Cc, float(eps), float(p), P(e))
+    return e
+
+
+def heads_s8(F, emb, H, W, packs):
+    """HEADS_S8 of one window: F f32 [H*W][C], emb f32 [C]; packs: 7 qd_wpack dicts (lin, fc0, att0, cla0, fc1,
+    att1, cla1; lin / att / cla padded to ncp) -> logits [ncp]."""
+    F = _c(F, np.float32)
+    Cc = F.shape[1]
+    hid = packs[1]["shape"][3]
+    nc = packs[0]["shape"][0]
+    ncp = packs[0]["shape"][3]
+    L = max(H, W)
+    wmax = max(Cc, hid, ncp)
+    work = np.zeros(5 * (L + 4) * wmax + (L + 4) * max(Cc, hid) // 4 + 16, np.float32)
+    logits = np.zeros(ncp, np.float32)
+    arr = lambda key: (vp * 7)(*[pk[key].ctypes.data for pk in packs])
+    lib().orc_heads_s8(P(F), P(_c(emb, np.float32)), H, W, Cc, hid, nc, arr("q"), arr("scale"), arr("swsum"),
+                       arr("b"), P(logits), P(work))
+    return logits
