@@ -16,7 +16,8 @@ F32, F16, I8, I32 = 0, 1, 2, 3
 HW_FP16 = 1
 OP = {"PW": 3, "DW3": 4, "SE": 5, "FE_LOGMEL": 8, "STEM": 9, "DWK": 10,
       "PAD": 11, "MEAN": 12, "GEMV": 15, "PW_S8": 22, "GEMV_S8": 23,
-      "SE_GATE": 25, "STEM3": 26, "CONV3C24": 27, "UNPAD": 28, "WINO_S8": 29, "PROTO_S8": 35}
+      "SE_GATE": 25, "STEM3": 26, "CONV3C24": 27, "UNPAD": 28, "WINO_S8": 29, "QCONV3": 30, "QPW": 31,
+      "SE_GATE16": 32, "GEM_A": 33, "HEADS_S8": 34, "PROTO_S8": 35}
 HW_DOTPROD = 2
 ACT = {None: 0, "none": 0, "silu": 1, "relu": 2}
 
@@ -393,6 +394,87 @@ class Net:
         assert d[0] == F16 and d[4] == C and d[5] == 1
         ob = self.buf(F32, H, W, C)
         self.emit(OP["UNPAD"], [ib, ob], [], [H, W, C], var=2)
+        self.last = ob
+        return ob
+
+    def qconv3(self, ib, w, b, s):
+        """QCONV3 (src/rt_ops_dot.c:173-216; conv3_s8, python/bnneon/compiler/lower_dot.py:192-223): fp32 rows
+        [H][W][C] -> fp16 rows [Ho][Wo][K] = SiLU(3 x 3 stride-s TF-same conv + b) on per-tensor int8 inputs;
+        w OHWI fp32 [K][3][3][C]."""
+        d = self.bufs[ib]
+        H, W, C = d[1], d[2], d[3]
+        assert d[0] == F32 and d[4] == C and d[5] == 0
+        w = np.asarray(w, np.float32)
+        K = w.shape[0]
+        Ho, Wo = (H + s - 1) // s, (W + s - 1) // s
+        tl = [self.tensor("dot/qconv.w", w.reshape(K, 3, 3, C)),
+              self.tensor("dot/qconv.b", np.asarray(b, np.float32).reshape(K))]
+        ob = self.buf(F16, Ho, Wo, K)
+        self.emit(OP["QCONV3"], [ib, ob], tl, [H, W, C, K, s, Ho, Wo], var=2)
+        self.last = ob
+        return ob
+
+    def qpw(self, ib, w, b, act=None, gate=-1, res=-1, out16=False, opad=0):
+        """QPW (src/rt_ops_dot.c:226-339; qpw, lower_dot.py:248-271): 1 x 1 conv of fp32 rows, or of fp16 rows
+        (multiplied by an SE_GATE16 gate when one is given), with per-row int8 inputs; fp16 out (zero-haloed for a
+        depthwise consumer when opad) or fp32 rows (+ the fp32 rows res); w [N][K]."""
+        d = self.bufs[ib]
+        idt, H, W, K, ldx = d[0], d[1], d[2], d[3], d[4]
+        assert d[5] == 0 and idt in (F32, F16)
+        w = np.asarray(w, np.float32)
+        N = w.shape[0]
+        M, Kp = H * W, (K + 15) // 16 * 16
+        odt = F16 if out16 else F32
+        ob = self.buf(odt, H, W, N, halo=opad)
+        a8 = self.buf(I8, M + 4, 1, Kp)
+        rq = self.buf(F32, M + 4, 1, 2)
+        tl = [self.tensor("dot/qpw.w", w.reshape(N, K)), self.tensor("dot/qpw.b", np.asarray(b, np.float32))]
+        self.emit(OP["QPW"], [ib, ob, a8, rq, res, gate], tl,
+                  [N, K, M, idt, ldx, ACT[act], odt, N, W if opad else 0, opad], var=2)
+        self.last = ob
+        return ob
+
+    def se_gate16(self, cs, P, w1, b1, w2, b2):
+        """SE_GATE16 (src/rt_ops_dot.c:347-420): the fp16 gate [C] from the channel sums cs of P pixels (scaled to
+        means in place); w1 [rd][C], w2 [C][rd] fp32."""
+        w1 = np.asarray(w1, np.float32)
+        rd, C = w1.shape
+        tl = [self.tensor("dot/seg.w1", w1), self.tensor("dot/seg.b1", np.asarray(b1, np.float32)),
+              self.tensor("dot/seg.w2", np.asarray(w2, np.float32).reshape(C, rd)),
+              self.tensor("dot/seg.b2", np.asarray(b2, np.float32))]
+        gb = self.buf(F16, 1, 1, C, elems=C)
+        self.emit(OP["SE_GATE16"], [cs, gb], tl, [C, rd, P], var=2)
+        return gb
+
+    def gem_a(self, ib, eps, p):
+        """GEM_A (src/rt_ops_dot.c:428-465): fp32 rows [M][C] -> the generalised mean [C]."""
+        d = self.bufs[ib]
+        assert d[0] == F32 and d[4] == d[3] and d[5] == 0
+        M, C = d[1] * d[2], d[3]
+        ob = self.buf(F32, 1, 1, C)
+        self.emit(OP["GEM_A"], [ib, ob], [self.tensor("dot/gem.k", np.array([eps, p], np.float32))], [M, C],
+                  var=2)
+        self.last = ob
+        return ob
+
+    def heads_s8(self, fb, eb, H, W, lin, heads):
+        """HEADS_S8 (src/rt_ops_dot.c:467-585): logits [ncp] = lin(e) + the SED heads over F fp32 rows [H*W][C];
+        lin = (w [nc][C], b), heads = two (fc w [hid][C], fc b, att w [nc][hid], att b, cla w [nc][hid], cla b)."""
+        d = self.bufs[fb]
+        C = d[3]
+        assert d[0] == F32 and d[4] == C and d[5] == 0 and d[1] * d[2] == H * W
+        nc = np.asarray(lin[0]).shape[0]
+        hid = np.asarray(heads[0][0]).shape[0]
+        ncp, L = (nc + 15) // 16 * 16, max(H, W)
+        tl = [self.tensor("dot/heads.lin.w", np.asarray(lin[0], np.float32)),
+              self.tensor("dot/heads.lin.b", np.asarray(lin[1], np.float32))]
+        for hd in heads:
+            for j, a in enumerate(hd):
+                tl.append(self.tensor(f"dot/heads.{j}", np.asarray(a, np.float32)))
+        ob = self.buf(F32, 1, 1, ncp, elems=ncp)
+        a8 = self.buf(I8, 1, 1, 1, elems=(L + 4) * max(C, hid))
+        rq = self.buf(F32, 1, 1, 1, elems=2 * (L + 4))
+        self.emit(OP["HEADS_S8"], [fb, eb, ob, a8, rq], tl, [H, W, C, hid, nc], var=2)
         self.last = ob
         return ob
 

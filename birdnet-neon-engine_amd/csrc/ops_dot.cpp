@@ -121,7 +121,10 @@ int wino_init(rt_ctx *c, rt_op *op) {
 int wino_run(rt_ctx *c, rt_op *op) {
   wino_st *s = (wino_st *)op->state;
   const int *p = op->p;
-  const size_t need = bnh_wino8_work_bytes(p[0], p[1], p[2], c->bcap);
+  // one 256-byte-aligned slot per window, so that the two sub-batches of a split batch (running concurrently on
+  // two streams) use disjoint slots: this sub-batch's start at window w0
+  const size_t per = (bnh_wino8_work_bytes(p[0], p[1], p[2], 1) + 255) / 256 * 256;
+  const size_t need = per * (size_t)c->bcap;
   if (s->cap < need) {
     if (s->work) bnh_free(s->work);
     s->cap = 0;
@@ -132,7 +135,7 @@ int wino_run(rt_ctx *c, rt_op *op) {
     s->cap = need;
   }
   return bnh_wino_s8((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[0], p[1], s->P, (uint16_t *)rt_b(c, op, 1),
-                     rt_ws(c, op, 1), c->nwin, s->work, bnh_wino8_work_bytes(p[0], p[1], p[2], c->nwin), c->stream);
+                     rt_ws(c, op, 1), c->nwin, (char *)s->work + per * c->w0, per * c->nwin, c->stream);
 }
 
 // TF-same output size and low pad of a k-tap stride-s axis (tf_same, src/rt_ops_dot.c:32-36)
@@ -193,7 +196,8 @@ int qconv_run(rt_ctx *c, rt_op *op) {
     st->cap = need;
   }
   return bnh_qconv3((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), p[0], p[1], p[2], p[4], st->pt, st->pl, p[5],
-                    p[6], st->q, (uint16_t *)rt_b(c, op, 1), rt_ws(c, op, 1), c->nwin, st->work, st->ws, c->stream);
+                    p[6], st->q, (uint16_t *)rt_b(c, op, 1), rt_ws(c, op, 1), c->nwin,
+                    (char *)st->work + st->ws * c->w0, st->ws, c->stream);  // this sub-batch's window slots
 }
 
 // -------- QPW: b = [in, out, a8 int8 [M][Kp], rq f32 [2 M], res f32 | -1, gate f16 [K] | -1]; t = [w [N][K], b [N]];
@@ -344,7 +348,8 @@ int heads_run(rt_ctx *c, rt_op *op) {
   }
   return bnh_heads_s8((const float *)rt_b(c, op, 0), rt_ws(c, op, 0), (const float *)rt_b(c, op, 1), rt_ws(c, op, 1),
                       p[0], p[1], s->P, (float *)rt_b(c, op, 2), rt_ws(c, op, 2), (int8_t *)rt_b(c, op, 3),
-                      rt_ws(c, op, 3), (float *)rt_b(c, op, 4), rt_ws(c, op, 4), c->nwin, s->work, s->ws, c->stream);
+                      rt_ws(c, op, 3), (float *)rt_b(c, op, 4), rt_ws(c, op, 4), c->nwin,
+                      (char *)s->work + s->ws * c->w0, s->ws, c->stream);  // this sub-batch's window slots
 }
 
 const rt_kernel K_STEM3 = {stem3_init, stem3_run, rt_dev_fini, "stem3_f32to16", 0x2, 0};

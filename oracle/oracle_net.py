@@ -139,6 +139,50 @@ class OracleNet:
         w = np.asarray(t[0], np.float32).reshape(K, 3, 3, C)
         self.put(bufs[b[1]], O.wino8(bufs[b[0]][:H * W * C].reshape(H, W, C), O.wino8_pack(w), t[1]))
 
+    # QCONV3: x f32 [H][W][C] -> fp16 rows
+    def op_30(self, var, b, t, p, bufs):
+        H, W, C, K, s, Ho, Wo = p
+        pk = O.qd_wpack(np.asarray(t[0], np.float32).reshape(K, 9 * C), t[1])
+        self.put(bufs[b[1]], O.qconv3(bufs[b[0]][:H * W * C].reshape(H, W, C), pk, s))
+
+    # QPW: buffers [in, out, a8, rq, res | -1, gate | -1]
+    def op_31(self, var, b, t, p, bufs):
+        N, K, M, idt, ldx, act, odt, ldo, ow, opad = p
+        pk = O.qd_wpack(np.asarray(t[0], np.float32).reshape(N, K), t[1])
+        x = bufs[b[0]][:M * ldx].reshape(M, ldx)
+        res = None if b[4] < 0 else bufs[b[4]][:M * ldo].reshape(M, ldo)
+        gate = None if b[5] < 0 else bufs[b[5]][:K]
+        out, a8, rq = O.qpw(x, pk, act, out16=odt == 1, ldo=ldo, ow=ow, opad=opad, res=res, gate=gate)
+        self.put(bufs[b[1]], out)
+        self.put(bufs[b[2]], a8)
+        self.put(bufs[b[3]], rq)
+
+    # SE_GATE16: buffers [chsum (scaled in place), gate]
+    def op_32(self, var, b, t, p, bufs):
+        C, rd, P_ = p
+        m, g = O.se_gate16(bufs[b[0]][:C], P_, np.asarray(t[0]).reshape(rd, C), t[1], np.asarray(t[2]).reshape(C, rd),
+                           t[3])
+        self.put(bufs[b[0]], m)
+        self.put(bufs[b[1]], g)
+
+    # GEM_A
+    def op_33(self, var, b, t, p, bufs):
+        M, C = p
+        k = np.asarray(t[0], np.float32).reshape(-1)
+        self.put(bufs[b[1]], O.gem_a(bufs[b[0]][:M * C].reshape(M, C), k[0], k[1]))
+
+    # HEADS_S8: buffers [F, e, logits, a8, rq]
+    def op_34(self, var, b, t, p, bufs):
+        H, W, C, hid, nc = p
+        ncp = (nc + 15) // 16 * 16
+        T = [np.asarray(a, np.float32) for a in t]
+        packs = [O.qd_wpack(T[0].reshape(nc, C), T[1], ncp)]
+        for i in range(2):
+            j = 2 + 6 * i
+            packs += [O.qd_wpack(T[j].reshape(hid, C), T[j + 1]), O.qd_wpack(T[j + 2].reshape(nc, hid), T[j + 3], ncp),
+                      O.qd_wpack(T[j + 4].reshape(nc, hid), T[j + 5], ncp)]
+        self.put(bufs[b[2]], O.heads_s8(bufs[b[0]][:H * W * C].reshape(H * W, C), bufs[b[1]][:C], H, W, packs))
+
     # PROTO_S8: buffers [cells, logits, q, colmax], tensors [q panels, sw, n4, clsw, clsb, eps]
     def op_35(self, var, b, t, p, bufs):
         N, K, Kp, Np, P_, C, ld, nc, ppc = p

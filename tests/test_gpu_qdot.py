@@ -334,3 +334,97 @@ def _sig(v):
     r = float(np.float32(r) * np.float32(L.orc_frecps(d, r)))
     r = float(np.float32(r) * np.float32(L.orc_frecps(d, r)))
     return r
+
+
+# ------------------------------------------------------------------ the ops in packages
+def v3_net(rng, H, W, C0=16):
+    """rows [H][W][C0] -> QCONV3 s2 (32) -> QPW fp16 in, SiLU, zero-haloed fp16 out (64) -> DW3 fp16 (chsum) ->
+    SE_GATE16 -> QPW gated fp16 in, fp32 out (32) -> QPW fp32 in, ReLU, + that as residual (32) -> MEAN -> HEADS_S8:
+    the dense-conv models' int8 plan (python/bnneon/compiler/lower_dot.py), every op but GEM_A."""
+    from bnneon import netbuild, pkgfmt
+    pkg = pkgfmt.Package()
+    net = netbuild.Net(pkg)
+    ib = net.buf(netbuild.F32, H, W, C0)
+    nrm = lambda *s: (rng.standard_normal(s) / np.sqrt(s[-1])).astype(np.float32)
+    x1 = net.qconv3(ib, nrm(32, 3, 3, C0) * 1.4, rng.standard_normal(32) * 0.1, 2)
+    x2 = net.qpw(x1, nrm(64, 32), rng.standard_normal(64) * 0.1, act="silu", out16=True, opad=1)
+    x3, cs = net.dw3(x2, (rng.standard_normal((9, 64)) * 0.3), rng.standard_normal(64) * 0.1, 1, 1, 1, fp16=True)
+    Ho, Wo = net.bufs[x3][1], net.bufs[x3][2]
+    g = net.se_gate16(cs, Ho * Wo, nrm(8, 64), rng.standard_normal(8) * 0.1, nrm(64, 8), rng.standard_normal(64) * 0.1)
+    x4 = net.qpw(x3, nrm(32, 64), rng.standard_normal(32) * 0.1, gate=g)
+    x5 = net.qpw(x4, nrm(32, 32), rng.standard_normal(32) * 0.1, act="relu", res=x4)
+    e = net.mean(x5)
+    nc, hid = 20, 48
+    heads = [(nrm(hid, 32), rng.standard_normal(hid) * 0.1, nrm(nc, hid), rng.standard_normal(nc) * 0.1,
+              nrm(nc, hid), rng.standard_normal(nc) * 0.1) for _ in range(2)]
+    out = net.heads_s8(x5, e, Ho, Wo, (nrm(nc, 32), rng.standard_normal(nc) * 0.1), heads)
+    net.add_to("neon-fp16", netbuild.HW_FP16 | netbuild.HW_DOTPROD, in_buf=ib, out_buf=out, emb_buf=e)
+    netbuild.standard_meta(pkg, H * W * C0, 32, model_id="synthetic_v3_int8", emb_dim=32)
+    return pkg, net, ib, out, e
+
+
+@pytest.mark.parametrize("H,W,n", [(12, 16, 5), (9, 14, 70)])
+def test_v3_int8_plan_package(hip, tmp_path, H, W, n):
+    """every window of the batch against the op-by-op oracle interpreter, bit for bit (70 windows: two sub-batches)"""
+    from bnneon import binding
+    from oracle_net import OracleNet
+    rng = np.random.default_rng(H * W)
+    pkg, net, ib, out, e = v3_net(rng, H, W)
+    path = str(tmp_path / "v3.bnpk")
+    pkg.write(path)
+    pcm = rng.standard_normal((n, H * W * 16)).astype(np.float32)
+    say("v3 int8 plan package", H, W, n)
+    with binding.Model(path) as m:
+        got, emb, status = m.infer_batch(pcm)
+        assert not status.any()
+    orc = OracleNet(net, ib, out, e)
+    for i in sorted({0, 1, n // 2, n - 1}):
+        ro, re, _ = orc.run(pcm[i])
+        assert same(got[i], ro[:got.shape[1]]), i
+        assert same(emb[i], re[:32]), i
+
+
+def test_gem_a_package(hip, tmp_path):
+    from bnneon import binding, netbuild, pkgfmt
+    from oracle_net import OracleNet
+    rng = np.random.default_rng(11)
+    M, C = 96, 64
+    pkg = pkgfmt.Package()
+    net = netbuild.Net(pkg)
+    ib = net.buf(netbuild.F32, 8, 12, C)
+    out = net.gem_a(ib, 1e-6, 3.0)
+    net.add_to("neon-fp16", netbuild.HW_FP16 | netbuild.HW_DOTPROD, in_buf=ib, out_buf=out)
+    netbuild.standard_meta(pkg, M * C, C, model_id="synthetic_gem")
+    path = str(tmp_path / "gem.bnpk")
+    pkg.write(path)
+    pcm = np.abs(rng.standard_normal((4, M * C))).astype(np.float32)
+    with binding.Model(path) as m:
+        got, _, status = m.infer_batch(pcm)
+        assert not status.any()
+    orc = OracleNet(net, ib, out)
+    for i in range(4):
+        ro, _, _ = orc.run(pcm[i])
+        d = np.abs(got[i, :C].view(np.int32).astype(np.int64) - ro[:C].view(np.int32).astype(np.int64))
+        assert d.max() <= 1, i
+
+
+def test_qpw_contract_refusals(hip, tmp_path):
+    """QPW records the reference refuses: ReLU into fp16, a residual with fp16 out, a gate on fp32 rows"""
+    from bnneon import binding, netbuild, pkgfmt
+    rng = np.random.default_rng(12)
+    for bad in ("relu16", "gate32"):
+        pkg = pkgfmt.Package()
+        net = netbuild.Net(pkg)
+        ib = net.buf(netbuild.F32, 4, 4, 16)
+        if bad == "relu16":
+            out = net.qpw(ib, rng.standard_normal((16, 16)), np.zeros(16), act="relu", out16=True)
+        else:
+            gb = net.buf(netbuild.F16, 1, 1, 16, elems=16)
+            out = net.qpw(ib, rng.standard_normal((16, 16)), np.zeros(16), gate=gb)
+        net.add_to("neon-fp16", netbuild.HW_FP16 | netbuild.HW_DOTPROD, in_buf=ib, out_buf=out)
+        netbuild.standard_meta(pkg, 256, 16, model_id="bad_qpw")
+        path = str(tmp_path / f"{bad}.bnpk")
+        pkg.write(path)
+        with pytest.raises(Exception) as ei:
+            binding.Model(path)
+        assert "parameter check failed" in str(ei.value), (bad, str(ei.value))
