@@ -143,6 +143,8 @@ _SIGS = {
     "bnh_se_gate16": (i32, [vp, i64, i32, vp, vp, i64, i32, vp]),
     "bnh_gem_a": (i32, [vp, i64, i32, i32, C.c_float, C.c_float, vp, i64, i32, vp]),
     "bnh_eval_qd": (i32, [i32, vp, vp, i64, vp]),
+    "bnh_quant_cells_f16": (i32, [vp, i64, i32, i32, i32, C.c_float, vp, i64, i32, vp, i64, i32, vp]),
+    "bnh_s8p_new_c12": (vp, [i32, i32, vp, vp]),
 }
 
 

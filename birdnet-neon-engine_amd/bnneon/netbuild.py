@@ -14,7 +14,7 @@ from . import pkgfmt, s8pack
 
 F32, F16, I8, I32 = 0, 1, 2, 3
 HW_FP16 = 1
-OP = {"PW": 3, "DW3": 4, "SE": 5, "FE_LOGMEL": 8, "STEM": 9, "DWK": 10,
+OP = {"PW": 3, "DW3": 4, "SE": 5, "FE_LOGMEL": 8, "STEM": 9, "DWK": 10, "PROTO": 13,
       "PAD": 11, "MEAN": 12, "GEMV": 15, "PW_S8": 22, "GEMV_S8": 23,
       "SE_GATE": 25, "STEM3": 26, "CONV3C24": 27, "UNPAD": 28, "WINO_S8": 29, "QCONV3": 30, "QPW": 31,
       "SE_GATE16": 32, "GEM_A": 33, "HEADS_S8": 34, "PROTO_S8": 35}
@@ -475,6 +475,28 @@ class Net:
         a8 = self.buf(I8, 1, 1, 1, elems=(L + 4) * max(C, hid))
         rq = self.buf(F32, 1, 1, 1, elems=2 * (L + 4))
         self.emit(OP["HEADS_S8"], [fb, eb, ob, a8, rq], tl, [H, W, C, hid, nc], var=2)
+        self.last = ob
+        return ob
+
+    def proto_dot(self, ib, qw12, sw, clsw, clsb, eps=1e-5, C=None):
+        """PROTO variant 2 (src/rt_ops_f16.c:252-281): the dotprod prototype head on the first C channels (all by
+        default) of the fp16 cells ib [P][ld]; qw12 int8 [Np/12][C/4][12][4] prototype panels, sw [Np], clsw [nc][ppc],
+        clsb [nc]."""
+        d = self.bufs[ib]
+        P, C, ld = d[1] * d[2], d[3] if C is None else C, d[4]
+        assert d[0] == F16 and d[5] == 0
+        clsw = np.asarray(clsw, np.float32)
+        nc, ppc = clsw.shape
+        N = nc * ppc
+        sw = np.asarray(sw, np.float32)
+        Np = sw.shape[0]
+        tl = [self.tensor("dot/proto.qw", np.asarray(qw12, np.int8)), self.tensor("dot/proto.sw", sw),
+              self.tensor("dot/proto.clsw", clsw), self.tensor("dot/proto.clsb", np.asarray(clsb, np.float32)),
+              self.tensor("dot/proto.eps", np.array([eps], np.float32))]
+        ob = self.buf(F32, 1, 1, nc)
+        qb = self.buf(I8, P, 1, C)
+        cb = self.buf(F32, 1, 1, Np)
+        self.emit(OP["PROTO"], [ib, ob, qb, cb], tl, [N, C, Np, P, C, ld, nc, ppc], var=2)
         self.last = ob
         return ob
 

@@ -31,7 +31,10 @@ static inline size_t s8p_at(int n, int k, int Kt) {
 // lanes 0..7 run them over a 512-float LDS chunk the whole wave stages, then combine as ((t0 + t1) + (t2 + t3)),
 // t_j = chain_j + chain_{j+4}. max |x| (FMAX, NaN-propagating) is order-free: all lanes, then a wave reduction.
 #define QC_CHUNK 512
-__global__ __launch_bounds__(256) void k_quant_cells(const float *__restrict__ x, long long x_ws, int P, int C, int ld,
+// F16: the cells are fp16 (pc_quant_cells_f16, src/pc_proto_s8.c:14-45: the same sums of the widened values, and
+// codes narrowed with saturation to [-128, 127] without the floor at -127)
+template <bool F16>
+__global__ __launch_bounds__(256) void k_quant_cells(const void *__restrict__ xv, long long x_ws, int P, int C, int ld,
                                                      float eps, int8_t *__restrict__ qa, long long qa_ws, int Kp,
                                                      float *__restrict__ sx, long long sx_ws, long long cells) {
   __shared__ float stage[4][QC_CHUNK];
@@ -39,13 +42,14 @@ __global__ __launch_bounds__(256) void k_quant_cells(const float *__restrict__ x
   const long long cell = (long long)blockIdx.x * 4 + wv;
   const bool live = cell < cells;
   const int w = live ? (int)(cell / P) : 0, p = live ? (int)(cell % P) : 0;
-  const float *r = x + w * x_ws + (long long)p * ld;
+  const float *r = F16 ? nullptr : (const float *)xv + w * x_ws + (long long)p * ld;
+  const _Float16 *rh = F16 ? (const _Float16 *)xv + w * x_ws + (long long)p * ld : nullptr;
   float chain = 0.f, mx = 0.f;
   for (int c0 = 0; c0 < C; c0 += QC_CHUNK) {
     const int n = C - c0 < QC_CHUNK ? C - c0 : QC_CHUNK;
     if (live)
       for (int i = lane; i < n; i += 64) {
-        const float v = r[c0 + i];
+        const float v = F16 ? (float)rh[c0 + i] : r[c0 + i];
         stage[wv][i] = v;
         mx = bnh_fmax(mx, __builtin_fabsf(v));
       }
@@ -71,10 +75,10 @@ __global__ __launch_bounds__(256) void k_quant_cells(const float *__restrict__ x
     for (int j = 0; j < 4; j++) {
       int32_t b = 0;
       if (c + j < C) {
-        int32_t v = bnh_cvta_s32(r[c + j] * inv);
+        int32_t v = bnh_cvta_s32((F16 ? (float)rh[c + j] : r[c + j]) * inv);
         v = v < -32768 ? -32768 : v > 32767 ? 32767 : v;
         v = v < -128 ? -128 : v > 127 ? 127 : v;
-        b = v < -127 ? -127 : v;
+        b = F16 || v >= -127 ? v : -127;
       }
       word |= ((uint32_t)b & 0xffu) << (8 * j);
     }
@@ -401,10 +405,44 @@ int bnh_quant_cells(const float *x, long long x_ws, int P, int C, int ld, float 
   BNH_REQ(((uintptr_t)qa & 3) == 0 && qa_ws % 4 == 0);
   BNH_REQ(B == 1 || (qa_ws >= (long long)P * Kp && sx_ws >= P && x_ws >= (long long)(P - 1) * ld + C));
   const long long cells = (long long)P * B;
-  hipLaunchKernelGGL(k_quant_cells, dim3((unsigned)bnh_ceil_div(cells, 4)), dim3(256), 0, bnh_stream(stream), x, x_ws, P,
-                     C, ld, eps, qa, qa_ws, Kp, sx, sx_ws, cells);
+  hipLaunchKernelGGL(k_quant_cells<false>, dim3((unsigned)bnh_ceil_div(cells, 4)), dim3(256), 0, bnh_stream(stream), x,
+                     x_ws, P, C, ld, eps, qa, qa_ws, Kp, sx, sx_ws, cells);
   BNH_HIP(hipGetLastError());
   return 0;
+}
+
+int bnh_quant_cells_f16(const uint16_t *x, long long x_ws, int P, int C, int ld, float eps, int8_t *qa,
+                        long long qa_ws, int Kp, float *sx, long long sx_ws, int B, void *stream) {
+  BNH_REQ(x && qa && sx && P > 0 && C > 0 && B > 0);
+  BNH_REQ(C % 8 == 0 && C <= Kp && Kp % 16 == 0 && ld >= C);
+  BNH_REQ(((uintptr_t)qa & 3) == 0 && qa_ws % 4 == 0);
+  BNH_REQ(B == 1 || (qa_ws >= (long long)P * Kp && sx_ws >= P && x_ws >= (long long)(P - 1) * ld + C));
+  const long long cells = (long long)P * B;
+  hipLaunchKernelGGL(k_quant_cells<true>, dim3((unsigned)bnh_ceil_div(cells, 4)), dim3(256), 0, bnh_stream(stream), x,
+                     x_ws, P, C, ld, eps, qa, qa_ws, Kp, sx, sx_ws, cells);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+// the dotprod head's prototype panels [Np/12][K/4][12][4] (src/pc_proto_s8.c:4-6) into this library's layout
+bnh_s8p *bnh_s8p_new_c12(int Np, int K, const int8_t *qw, const float *sw) {
+  if (!qw || !sw || Np <= 0 || Np % 12 || K <= 0 || K % 4) {
+    bnh_fail("bnh_s8p_new_c12: Np %d K %d: expected Np %% 12 == 0, K %% 4 == 0 and both tensors", Np, K);
+    return nullptr;
+  }
+  const int Kp = (K + 15) & ~15, kb = Kp / 16;
+  int8_t *q4 = (int8_t *)calloc((size_t)Np * Kp, 1);
+  if (!q4) {
+    bnh_fail("bnh_s8p_new_c12: out of host memory");
+    return nullptr;
+  }
+  for (int n = 0; n < Np; n++)
+    for (int k = 0; k < K; k++)
+      q4[((size_t)(n / 4) * kb + k / 16) * 64 + (n % 4) * 16 + k % 16] =
+          qw[((size_t)(n / 12) * (K / 4) + k / 4) * 48 + (n % 12) * 4 + k % 4];
+  bnh_s8p *W = bnh_s8p_new(Np, Kp, q4, sw);
+  free(q4);
+  return W;
 }
 
 int bnh_proto_colmax(const int8_t *qa, long long qa_ws, const float *sx, long long sx_ws, int P, const bnh_s8p *W,

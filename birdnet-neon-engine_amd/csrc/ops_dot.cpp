@@ -17,6 +17,10 @@
 #include "bnh_internal.h"
 #include "rt.h"
 
+int bnh_proto8_dot_init(rt_ctx *c, rt_op *op);  // ops_proto.cpp
+int bnh_proto8_dot_run(rt_ctx *c, rt_op *op);
+void bnh_proto8_dot_fini(rt_op *op);
+
 namespace {
 
 // the reference's activation names, so the parameter-check messages read as its own
@@ -353,6 +357,7 @@ int heads_run(rt_ctx *c, rt_op *op) {
 }
 
 const rt_kernel K_STEM3 = {stem3_init, stem3_run, rt_dev_fini, "stem3_f32to16", 0x2, 0};
+const rt_kernel K_PROTO8 = {bnh_proto8_dot_init, bnh_proto8_dot_run, bnh_proto8_dot_fini, "proto_s8", 0xe, 0};
 const rt_kernel K_CONV3C24 = {c24_init, c24_run, c24_fini, "conv3c24_wino16", 0x2, 0};
 const rt_kernel K_UNPAD = {unpad_init, unpad_run, nullptr, "unpad_f16to32", 0x2, 0};
 const rt_kernel K_WINO_S8 = {wino_init, wino_run, wino_fini, "wino3_s8", 0x2, 0};
@@ -366,6 +371,7 @@ const rt_kernel K_HEADS_S8 = {heads_init, heads_run, heads_fini, "heads_s8", 0x1
 
 const rt_kernel *rt_k_dot(int base) {
   switch (base) {
+    case RT_OP_PROTO: return &K_PROTO8;  // the dotprod prototype head (src/rt_ops_f16.c:284-286)
     case RT_OP_STEM3: return &K_STEM3;
     case RT_OP_CONV3C24: return &K_CONV3C24;
     case RT_OP_UNPAD: return &K_UNPAD;

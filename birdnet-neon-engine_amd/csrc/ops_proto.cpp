@@ -118,3 +118,78 @@ void bnh_proto_s8_fini(rt_op *op) {
   }
   free(s);
 }
+
+// -------- PROTO variant 2 (proto8_init / proto8_run, src/rt_ops_f16.c:252-281): the dotprod prototype head on fp16
+//   cells. b = [x f16 [P][ld], logits f32 [nc], qa int8 [P][K], colmax f32 [Np]];
+//   t = [qw int8 [Np/12][K/4][12][4], sw f32 [Np], cls w, cls b, eps]; p = [N K Np, P C ld nc ppc]
+// The cells' int8 rows are padded to Kp = K rounded up to 16, so they live in op-private scratch rather than in qa.
+typedef struct {
+  bnh_s8p *W;
+  float *clsw, *clsb;
+  float eps;
+  void *work;  // per window: sx [P] floats, then the rows [P][Kp]
+  size_t cap, ws;
+} proto8_state;
+
+int bnh_proto8_dot_init(rt_ctx *c, rt_op *op) {
+  proto8_state *s = (proto8_state *)calloc(1, sizeof *s);
+  op->state = s;
+  if (!s) return rt_oom(c, op, sizeof *s);
+  /* K <= 2^17: an int32 sum of K products of at most 128 x 127 cannot overflow */
+  if (proto_geom(c, op, 5, 8, 1 << 17)) return RT_E_PARAM;
+  const int *p = op->p;
+  int N = p[0], K = p[1], Np = p[2], P = p[3], ld = p[5], nc = p[6];
+  RT_REQ(c, op, K % 8 == 0);
+  RT_REQ(c, op, P % 8 == 0 && Np % 12 == 0 && Np >= N);
+  if (rt_need_t(c, op, 0, (size_t)Np * K, 1) || rt_need_t(c, op, 1, (size_t)Np * 4, 1)) return RT_E_PARAM;
+  if (rt_need_t(c, op, 2, (size_t)N * 4, 0) || rt_need_t(c, op, 3, (size_t)nc * 4, 0) || rt_need_t(c, op, 4, 4, 0))
+    return RT_E_PARAM;
+  if (rt_need_nohalo(c, op, 0, RT_F16, (size_t)P * ld) || rt_need(c, op, 1, RT_F32, (size_t)nc)) return RT_E_PARAM;
+  if (rt_need(c, op, 2, RT_I8, (size_t)P * K) || rt_need(c, op, 3, RT_F32, (size_t)Np)) return RT_E_PARAM;
+  memcpy(&s->eps, rt_t(c, op, 4, nullptr), 4);
+  s->W = bnh_s8p_new_c12(Np, K, (const int8_t *)rt_t(c, op, 0, nullptr), (const float *)rt_t(c, op, 1, nullptr));
+  s->clsw = upload_f32(rt_t(c, op, 2, nullptr), (size_t)N);
+  s->clsb = upload_f32(rt_t(c, op, 3, nullptr), (size_t)nc);
+  const size_t Kp = (size_t)((K + 15) & ~15);
+  s->ws = ((size_t)P * 4 + (size_t)P * Kp + 255) / 256 * 256;
+  if (!s->W || !s->clsw || !s->clsb) return rt_oom(c, op, (size_t)Np * Kp);
+  return 0;
+}
+
+int bnh_proto8_dot_run(rt_ctx *c, rt_op *op) {
+  proto8_state *s = (proto8_state *)op->state;
+  const int *p = op->p;
+  const int K = p[1], P = p[3], C = p[4], ld = p[5], nc = p[6], ppc = p[7], B = c->nwin, Kp = (K + 15) & ~15;
+  const size_t need = s->ws * (size_t)c->bcap;
+  if (s->cap < need) {
+    if (s->work) hipFree(s->work);
+    s->cap = 0;
+    if (!(s->work = bnh_malloc(need))) {
+      rt_oom(c, op, need);
+      return -1;
+    }
+    s->cap = need;
+  }
+  char *base = (char *)s->work + s->ws * c->w0;  // this sub-batch's window slots
+  float *sx = (float *)base;
+  int8_t *qa = (int8_t *)(base + (size_t)P * 4);
+  const long long ws = (long long)s->ws;
+  float *cm = (float *)rt_b(c, op, 3);
+  if (bnh_quant_cells_f16((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), P, C, ld, s->eps, qa, ws, Kp, sx, ws / 4,
+                          B, c->stream))
+    return -1;
+  if (bnh_proto_colmax(qa, ws, sx, ws / 4, P, s->W, cm, rt_ws(c, op, 3), B, c->stream)) return -1;
+  return bnh_proto_logits(cm, rt_ws(c, op, 3), s->clsw, s->clsb, nc, ppc, (float *)rt_b(c, op, 1), rt_ws(c, op, 1), B,
+                          c->win_fail + c->w0, c->fail_op + 1, c->stream);
+}
+
+void bnh_proto8_dot_fini(rt_op *op) {
+  proto8_state *s = (proto8_state *)op->state;
+  if (s) {
+    bnh_s8p_free(s->W);
+    if (s->clsw) hipFree(s->clsw);
+    if (s->clsb) hipFree(s->clsb);
+    if (s->work) hipFree(s->work);
+  }
+  free(s);
+}

@@ -103,6 +103,12 @@ void bnh_s8p_free(bnh_s8p *W);
  * -> qa int8 [P][Kp] in [-127, 127] (zeros past C) and sx f32 [P], the scales of the L2-normalised cells */
 int bnh_quant_cells(const float *x, long long x_ws, int P, int C, int ld, float eps, int8_t *qa, long long qa_ws,
                     int Kp, float *sx, long long sx_ws, int B, void *stream);
+/* pc_quant_cells_f16 (src/pc_proto_s8.c:14-45): fp16 cells; the codes saturate to [-128, 127] (no floor at -127) */
+int bnh_quant_cells_f16(const uint16_t *x, long long x_ws, int P, int C, int ld, float eps, int8_t *qa,
+                        long long qa_ws, int Kp, float *sx, long long sx_ws, int B, void *stream);
+/* the dotprod head's prototypes (PROTO variant 2, src/rt_ops_f16.c:252-281): qw int8 [Np/12][K/4][12][4], sw f32
+ * [Np], K % 4 == 0, repacked as bnh_s8p_new's with Kp = K rounded up to 16 */
+bnh_s8p *bnh_s8p_new_c12(int Np, int K, const int8_t *qw, const float *sw);
 /* pc_proto_colmax_s8n over every panel (src/proto_s8n.c:139-164; src/pc_kern.h:64-65): colmax f32 [Np] per window,
  * the maximum over the window's P cells of (float)(qa . qw) * sx, times sw */
 int bnh_proto_colmax(const int8_t *qa, long long qa_ws, const float *sx, long long sx_ws, int P, const bnh_s8p *W,

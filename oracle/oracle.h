@@ -179,6 +179,10 @@ void orc_gemv(const float *w32, const uint16_t *w16, const float *b, int N, int 
 /* ---------------------------------------------------------------- dotprod + fp16 family (dot.c) */
 void orc_stem3_f32h(const float *img, int H, int W, const float *w, const float *b, uint16_t *out);
 
+void orc_quant_cells_f16(const uint16_t *x, int P, int C, int ld, float eps, int8_t *qa, int Kp, float *sx);
+void orc_proto_colmax_c12(const int8_t *qa, int Kp, const float *sx, int P, int K, const int8_t *qw, const float *sw,
+                          int Np, float *colmax);
+
 /* ---------------------------------------------------------------- dotprod int8 (qdot.c) */
 typedef struct {
   int act;          /* 0 none, 1 SiLU, 2 ReLU (src/kern.h:31) */

@@ -139,6 +139,17 @@ class OracleNet:
         w = np.asarray(t[0], np.float32).reshape(K, 3, 3, C)
         self.put(bufs[b[1]], O.wino8(bufs[b[0]][:H * W * C].reshape(H, W, C), O.wino8_pack(w), t[1]))
 
+    # PROTO variant 2 (the dotprod head): buffers [cells f16, logits, qa, colmax], tensors [qw 12-panels, sw, clsw,
+    # clsb, eps]
+    def op_13(self, var, b, t, p, bufs):
+        assert var == 2
+        N, K, Np, P_, C, ld, nc, ppc = p
+        x = bufs[b[0]][:P_ * ld].reshape(P_, ld)
+        rc, lg, cm = O.proto_s8_dot(x, C, float(np.asarray(t[4]).reshape(-1)[0]), t[0], t[1][:Np], Np,
+                                    np.asarray(t[2]).reshape(-1), t[3], nc, ppc)
+        self.put(bufs[b[1]], lg)
+        self.put(bufs[b[3]], cm)
+
     # QCONV3: x f32 [H][W][C] -> fp16 rows
     def op_30(self, var, b, t, p, bufs):
         H, W, C, K, s, Ho, Wo = p

@@ -102,3 +102,54 @@ int orc_proto_s8(const float *x, int P, int C, int ld, float eps, int8_t *qa, in
   orc_proto_colmax_s8n(qa, Kp, sx, P, qw, sw, Np, colmax);
   return orc_proto_logits(colmax, clsw, clsb, nc, ppc, logits);
 }
+
+/* src/pc_proto_s8.c:14-45 (pc_quant_cells_f16): the fp16 cells widened, the same sums and maxima as
+ * orc_quant_cells_f32, q = FCVTAS(x * (127 / mx)) narrowed with saturation to int16 then int8 (no floor at -127);
+ * rows [P][Kp], zeros from C */
+void orc_quant_cells_f16(const uint16_t *x, int P, int C, int ld, float eps, int8_t *qa, int Kp, float *sx) {
+  float *row = malloc(sizeof(float) * (size_t)C);
+  for (int p = 0; p < P; p++) {
+    const uint16_t *r = x + (size_t)p * ld;
+    float s0[4] = {0, 0, 0, 0}, s1[4] = {0, 0, 0, 0}, m0[4] = {0, 0, 0, 0}, m1[4] = {0, 0, 0, 0};
+    for (int c = 0; c < C; c++) row[c] = orc_h2f(r[c]);
+    for (int c = 0; c < C; c += 8)
+      for (int j = 0; j < 4; j++) {
+        float u0 = row[c + j], u1 = row[c + 4 + j];
+        s0[j] = fmaf(u0, u0, s0[j]);
+        s1[j] = fmaf(u1, u1, s1[j]);
+        m0[j] = orc_fmax(m0[j], fabsf(u0));
+        m1[j] = orc_fmax(m1[j], fabsf(u1));
+      }
+    float t[4], m[4];
+    for (int j = 0; j < 4; j++) { t[j] = s0[j] + s1[j]; m[j] = orc_fmax(m0[j], m1[j]); }
+    float den = sqrtf((t[0] + t[1]) + (t[2] + t[3])) + eps;
+    float mx = orc_fmax(orc_fmax(m[0], m[1]), orc_fmax(m[2], m[3]));
+    if (!(mx > 0)) mx = 1e-30f;
+    sx[p] = mx / (127.f * den);
+    const float inv = 127.f / mx;
+    int8_t *q = qa + (size_t)p * Kp;
+    for (int c = 0; c < C; c++) {
+      int32_t v = orc_cvta_s32(row[c] * inv);
+      int32_t h = v < -32768 ? -32768 : v > 32767 ? 32767 : v;
+      q[c] = (int8_t)(h < -128 ? -128 : h > 127 ? 127 : h);
+    }
+    memset(q + C, 0, (size_t)(Kp - C));
+  }
+  free(row);
+}
+
+/* src/pc_proto_s8.c:47-88 (pc_proto_colmax_s8): colmax[j] = (max over cells p, from -inf, FMAX, of
+ * (float)acc[p][j] * sx[p]) * sw[j], the prototypes read from their panels qw [Np/12][K/4][12][4] */
+void orc_proto_colmax_c12(const int8_t *qa, int Kp, const float *sx, int P, int K, const int8_t *qw, const float *sw,
+                          int Np, float *colmax) {
+  for (int j = 0; j < Np; j++) {
+    float mx = -INFINITY;
+    for (int p = 0; p < P; p++) {
+      const int8_t *a = qa + (size_t)p * Kp;
+      int32_t acc = 0;
+      for (int k = 0; k < K; k++) acc += (int32_t)a[k] * (int32_t)qw[((size_t)(j / 12) * (K / 4) + k / 4) * 48 + (j % 12) * 4 + k % 4];
+      mx = orc_fmax(mx, (float)acc * sx[p]);
+    }
+    colmax[j] = mx * sw[j];
+  }
+}

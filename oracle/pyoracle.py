@@ -675,3 +675,25 @@ def heads_s8(F, emb, H, W, packs):
     lib().orc_heads_s8(P(F), P(_c(emb, np.float32)), H, W, Cc, hid, nc, arr("q"), arr("scale"), arr("swsum"),
                        arr("b"), P(logits), P(work))
     return logits
+
+
+_SIGS.update({
+    "orc_quant_cells_f16": (None, [vp, i32, i32, i32, f32, vp, i32, vp]),
+    "orc_proto_colmax_c12": (None, [vp, i32, vp, i32, i32, vp, vp, i32, vp]),
+})
+
+
+def proto_s8_dot(x, C, eps, qw, sw, Np, clsw, clsb, nc, ppc):
+    """PROTO variant 2 of one window (src/rt_ops_f16.c:268-281): fp16 cells x [P][ld], panels qw [Np/12][K/4][12][4]
+    -> (rc, logits, colmax)."""
+    x = np.ascontiguousarray(x, np.float16)
+    Pn, ld = x.shape
+    Kp = (C + 15) // 16 * 16
+    qa = np.zeros((Pn, Kp), np.int8)
+    sx = np.zeros(Pn, np.float32)
+    cm = np.zeros(Np, np.float32)
+    lg = np.zeros(nc, np.float32)
+    lib().orc_quant_cells_f16(P(x), Pn, C, ld, float(eps), P(qa), Kp, P(sx))
+    lib().orc_proto_colmax_c12(P(qa), Kp, P(sx), Pn, C, P(_c(qw, np.int8)), P(_c(sw, np.float32)), Np, P(cm))
+    rc = lib().orc_proto_logits(P(cm), P(_c(clsw, np.float32)), P(_c(clsb, np.float32)), nc, ppc, P(lg))
+    return rc, lg, cm

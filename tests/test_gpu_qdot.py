@@ -428,3 +428,37 @@ def test_qpw_contract_refusals(hip, tmp_path):
         with pytest.raises(Exception) as ei:
             binding.Model(path)
         assert "parameter check failed" in str(ei.value), (bad, str(ei.value))
+
+
+@pytest.mark.parametrize("P,C,n", [(64, 64, 6), (24, 40, 70)])
+def test_proto_dot_package(hip, tmp_path, P, C, n):
+    """QPW (fp32 rows -> fp16 cells) -> PROTO variant 2: logits and colmax against the oracle interpreter, bit for
+    bit (64 cells: the batched GEMM; 24: the per-window kernel; 70 windows: two sub-batches)"""
+    from bnneon import binding, netbuild, pkgfmt
+    from oracle_net import OracleNet
+    rng = np.random.default_rng(P * C)
+    nc, ppc = 8, 3
+    Np = 24
+    pkg = pkgfmt.Package()
+    net = netbuild.Net(pkg)
+    ib = net.buf(netbuild.F32, P, 1, 32)
+    ld = (C + 15) // 16 * 16  # QPW's channels are a multiple of 16: the head reads the first C of them
+    cells = net.qpw(ib, (rng.standard_normal((ld, 32)) / 5).astype(np.float32), np.zeros(ld, np.float32),
+                    out16=True)
+    q = rng.integers(-127, 128, (Np, C)).astype(np.int8)
+    q12 = np.ascontiguousarray(q.reshape(Np // 12, 12, C // 4, 4).transpose(0, 2, 1, 3))
+    sw = rng.uniform(0.001, 0.01, Np).astype(np.float32)
+    out = net.proto_dot(cells, q12, sw, rng.standard_normal((nc, ppc)), rng.standard_normal(nc), C=C)
+    net.add_to("neon-fp16", netbuild.HW_FP16 | netbuild.HW_DOTPROD, in_buf=ib, out_buf=out)
+    netbuild.standard_meta(pkg, P * 32, nc, model_id="synthetic_proto_dot")
+    path = str(tmp_path / "pd.bnpk")
+    pkg.write(path)
+    pcm = rng.standard_normal((n, P * 32)).astype(np.float32)
+    say("proto dot package", P, C, n)
+    with binding.Model(path) as m:
+        got, _, status = m.infer_batch(pcm)
+        assert not status.any()
+    orc = OracleNet(net, ib, out)
+    for i in sorted({0, n // 2, n - 1}):
+        ro, _, _ = orc.run(pcm[i])
+        assert same(got[i, :nc], ro[:nc]), i

@@ -280,3 +280,36 @@ def test_gem_a_against_float_statement():
     e = O.gem_a(F, 1e-6, 3.0)
     ref = (np.maximum(F.astype(np.float64), 1e-6) ** 3).mean(0) ** (1 / 3)
     assert np.allclose(e, ref, rtol=3e-6)
+
+
+# ------------------------------------------------------------------ the dotprod prototype head (PROTO variant 2)
+def pack_c12(q):
+    """prototype rows q [Np][K] -> panels [Np/12][K/4][12][4]"""
+    Np, K = q.shape
+    return np.ascontiguousarray(q.reshape(Np // 12, 12, K // 4, 4).transpose(0, 2, 1, 3))
+
+
+def pack_c4(q, Kp):
+    """prototype rows q [Np][K] -> the no-dotprod head's panels [Np/4][Kp/16][4][16]"""
+    Np, K = q.shape
+    qp = np.zeros((Np, Kp), np.int8)
+    qp[:, :K] = q
+    return np.ascontiguousarray(qp.reshape(Np // 4, 4, Kp // 16, 16).transpose(0, 2, 1, 3))
+
+
+@pytest.mark.parametrize("P,C,Np", [(24, 40, 36), (64, 64, 24)])
+def test_proto_dot_against_the_no_dotprod_head(P, C, Np):
+    """fp16 cells widened give the fp32 head's sums and scales (its -127 floor is unreachable: |x| <= max|x|), and
+    the 12-prototype panels hold the same prototypes as the 4-prototype ones: colmax and logits agree bit for bit"""
+    rng = np.random.default_rng(P + C)
+    x = (rng.standard_normal((P, C + 8)) * 2).astype(np.float16)
+    q = rng.integers(-127, 128, (Np, C)).astype(np.int8)
+    sw = rng.uniform(0.001, 0.01, Np).astype(np.float32)
+    nc, ppc = Np // 3, 3
+    clsw = rng.standard_normal((nc, ppc)).astype(np.float32)
+    clsb = rng.standard_normal(nc).astype(np.float32)
+    rc, lg, cm = O.proto_s8_dot(x, C, 1e-5, pack_c12(q), sw, Np, clsw, clsb, nc, ppc)
+    Kp = (C + 15) // 16 * 16
+    rc0, lg0, cm0, _ = O.proto_s8(x.astype(np.float32), C, 1e-5, pack_c4(q, Kp), sw, Np, Kp, clsw, clsb, nc, ppc)
+    assert rc == rc0 == 0
+    assert np.array_equal(cm, cm0) and np.array_equal(lg, lg0)
