@@ -65,6 +65,9 @@ def parse():
                              "wino_f16", "copy"])
     ap.add_argument("--k", type=int, default=5, choices=[3, 5], help="depthwise kernel size")
     ap.add_argument("--s", type=int, default=1, choices=[1, 2], help="depthwise stride")
+    ap.add_argument("--f16-mfma", action="store_true",
+                    help="v24_f16: run the fp16 1x1 convs on fp16 MFMA with fp32 accumulation (BNH_F16_MFMA=1) "
+                         "instead of the reference's exact fp16 chains")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     return ap.parse_args()
@@ -757,6 +760,8 @@ def run_v24(a, H, rng, B, stream):
     tmp = tempfile.mkdtemp(prefix="bnn_bench_")
     path = vn.write(os.path.join(tmp, "birdnet_v24_shaped_f16.bnpk"))
     L = binding.load_library()
+    if a.f16_mfma:
+        os.environ["BNH_F16_MFMA"] = "1"   # read by bnn_init
     m = binding.Model(path)
     os.unlink(path)
     os.rmdir(tmp)
@@ -786,9 +791,14 @@ def run_v24(a, H, rng, B, stream):
                                "conv, mean, 6,522-class fp16 GEMV), 144,000 samples @ 48 kHz per window",
                    "global_batch": B, "n_samples": ns, "n_classes": nc,
                    "parallelism": "1 GPU, windows batched per launch",
+                   "fp16_gemm": ("fp16 MFMA, fp32 accumulation (within the fp16 accumulation bound)" if a.f16_mfma
+                                 else "the reference's exact fp16 FMA chains (bit-identical)"),
                    "wall_s_timed_region": round(wall, 4)},
         "fp16_tflops": round(flops_win * B / (ms * 1e-3) / 1e12, 3),
     }
+    if a.f16_mfma:
+        line["config"]["workload"] = line["config"]["workload"].replace("exact fp16 1x1 convs",
+                                                                      "fp16-MFMA 1x1 convs")
     line["roofline"] = v24_roofline(H, vn, B, stream, a)
     m.close()
     if not a.no_cpu:
@@ -825,17 +835,26 @@ def v24_roofline(H, vn, B, stream, a):
     e = H.Epi16(act, dout.ptr, rows * ldo, ldo, ow if opad else 0, opad, None, 0, 0)
 
     def launch():   # the GEMM kernel alone: the halo was zeroed once (as the net's arena slots keep it)
-        H.check(H.lib().bnh_gemm_f16_body(dA.ptr, M * lda, lda, M, B, hw, ctypes.byref(e), stream))
+        if a.f16_mfma:
+            H.check(H.lib().bnh_gemm_f16_mfma(dA.ptr, M * lda, lda, M, B, hw, ctypes.byref(e), stream))
+        else:
+            H.check(H.lib().bnh_gemm_f16_body(dA.ptr, M * lda, lda, M, B, hw, ctypes.byref(e), stream))
     H.check(H.lib().bnh_gemm_f16(dA.ptr, M * lda, lda, M, B, hw, ctypes.byref(e), stream))
     ms, _ = time_steps(H, stream, launch, max(10, a.steps), 3)
     H.lib().bnh_h16w_free(hw)
     tf = 2.0 * M * N * K * B / (ms * 1e-3) / 1e12
-    return {"bound": "mfma", "achieved": round(tf, 2), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": V24_GEMM_TRAFFIC,
-            "kernel": "k_gemm_f16e", "valu_peak": FP16_VALU_PEAK_TFLOPS,
-            "valu_frac": round(tf / FP16_VALU_PEAK_TFLOPS, 4),
-            "launch": f"PW f16 GEMM {K}->{N} over {M} px x {B} windows, act {act}, halo-{opad} output",
-            "ms_per_launch": round(ms, 4), "algorithmic_flops_per_launch": 2 * M * N * K * B}
+    hbm_bytes = B * (M * lda + rows * ldo) * 2 + Np * Kp * 2   # fp16 rows in and out, the weights once
+    gbps = hbm_bytes / (ms * 1e-3) / 1e9
+    r = {"bound": "mfma", "achieved": round(tf, 2), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+         "frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": V24_GEMM_TRAFFIC,
+         "kernel": "k_gemm_f16" if a.f16_mfma else "k_gemm_f16e",
+         "launch": f"PW f16 GEMM {K}->{N} over {M} px x {B} windows, act {act}, halo-{opad} output",
+         "ms_per_launch": round(ms, 4), "algorithmic_flops_per_launch": 2 * M * N * K * B,
+         "algorithmic_bytes_per_launch": hbm_bytes, "hbm_GBps": round(gbps, 1), "hbm_frac": round(gbps / 8000.0, 4)}
+    if not a.f16_mfma:
+        r["valu_peak"] = FP16_VALU_PEAK_TFLOPS
+        r["valu_frac"] = round(tf / FP16_VALU_PEAK_TFLOPS, 4)
+    return r
 
 
 if __name__ == "__main__":

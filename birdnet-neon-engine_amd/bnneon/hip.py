@@ -145,6 +145,7 @@ _SIGS = {
     "bnh_eval_qd": (i32, [i32, vp, vp, i64, vp]),
     "bnh_quant_cells_f16": (i32, [vp, i64, i32, i32, i32, C.c_float, vp, i64, i32, vp, i64, i32, vp]),
     "bnh_s8p_new_c12": (vp, [i32, i32, vp, vp]),
+    "bnh_gemm_f16_mfma_gated": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp, i64, vp]),
 }
 
 

@@ -40,6 +40,10 @@ struct bnh_s8w {
 };
 
 // whether bnh_pwdw_f32 takes this expansion + depthwise pair (0) or not (-1, with the reason in bnh_last_error)
+extern "C" int bnh_gemm_f16_mfma_body(const uint16_t *A, long long a_ws, int lda, int M, int B,
+                                      const struct bnh_h16w *W, const bnh_epi16 *e, const uint16_t *gh,
+                                      long long gh_ws, void *stream);
+
 extern "C" int bnh_pwdw_f32_plan(int C, int Kp, int H, int W, int k, int s, int pt, int pl, int form, int Ho, int Wo);
 
 static inline hipStream_t bnh_stream(void *s) { return (hipStream_t)s; }

@@ -36,23 +36,55 @@ struct Epi16Dev {
   int ldr;
 };
 
-// 4 waves as 2 (rows) x 2 (channels); a wave computes 32 rows x 64 channels (2 x 4 MFMA tiles)
+// 4 waves as 2 (rows) x 2 (channels); a wave computes 32 rows x 64 channels (2 x 4 MFMA tiles). Each block resolves
+// its 64 rows' window, A / output / residual / gate addresses into LDS once. GATE: A's columns are multiplied by the
+// window's fp16 gates as they are loaded (the fp16 SE's scaling, one fp16 rounding per product, as in k_gemm_f16e).
+// VEC: each wave's 16 x 64 tile leaves the accumulators through LDS (bias, rounding and activation done in the
+// accumulator layout), and goes out as 16-byte rows of 8 channels with their residual added in fp16.
+template <bool GATE, bool VEC>
 __global__ __launch_bounds__(256) void k_gemm_f16(const uint16_t *__restrict__ A, long long a_ws, int lda, int M,
-                                                  long long rows, const uint16_t *__restrict__ wt,
-                                                  const float *__restrict__ bias, int Kp, int Np, Epi16Dev e) {
+                                                  double rM, long long rows, const uint16_t *__restrict__ wt,
+                                                  const float *__restrict__ bias, int Kp, int Np, Epi16Dev e,
+                                                  const uint16_t *__restrict__ gh, long long gh_ws) {
+  constexpr int TS = 72;  // the tile's LDS row stride in halves (64 channels + 8)
+  __shared__ long long s_a[64], s_o[64], s_r[64], s_g[GATE ? 64 : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_t[VEC ? 4 : 1][VEC ? 16 * TS : 1];
+  __shared__ uint32_t s_t01[16];  // the SiLU table in LDS (c0 | c1 << 16, c2) for the packed form
+  __shared__ uint16_t s_t2[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const long long row0 = (long long)blockIdx.x * 64 + wm * 32;
-  const int n0 = blockIdx.y * 128 + wn * 64;
-  if (row0 >= rows) return;
+  // the channel blocks of a row block are consecutive logical blocks on one XCD: its output rows' cache lines fill
+  // in that XCD's L2 while the row block is being written (partial lines from far-apart blocks cost HBM write rate)
+  const int nnb = (Np + 127) / 128;
+  const unsigned lb = bnh_xcd_block(blockIdx.x, gridDim.x);
+  const long long rowB = (long long)(lb / nnb) * 64;
+  const int nblk = (int)(lb % nnb);
+  if (threadIdx.x < 64) {
+    const long long r = rowB + threadIdx.x < rows ? rowB + threadIdx.x : rows - 1;  // a valid row past the end
+    const int w = bnh_div(r, M, rM), m = (int)(r - (long long)w * M);
+    s_a[threadIdx.x] = w * a_ws + (long long)m * lda;
+    long long orow = m;
+    if (e.opad) {
+      const int y = m / e.ow;
+      orow = (long long)(y + e.opad) * (e.ow + 2 * e.opad) + (m - y * e.ow) + e.opad;
+    }
+    s_o[threadIdx.x] = w * e.out_ws + orow * e.ldo;
+    s_r[threadIdx.x] = e.res ? w * e.res_ws + (long long)m * e.ldr : 0;
+    if (GATE) s_g[threadIdx.x] = w * gh_ws;
+  }
+  if (threadIdx.x < 16) {
+    s_t01[threadIdx.x] = (uint32_t)k_silu_c0[threadIdx.x] | ((uint32_t)k_silu_c1[threadIdx.x] << 16);
+    s_t2[threadIdx.x] = k_silu_c2[threadIdx.x];
+  }
+  __syncthreads();
+  const int lr0 = wm * 32, n0 = nblk * 128 + wn * 64;
+  if (rowB + lr0 >= rows) return;
   const int kc = (lane >> 4) * 8;  // this lane's k chunk within a 32-wide step (halves)
-  const uint16_t *ap[2];
+  const uint16_t *ap[2], *gp[2];
 #pragma unroll
   for (int t = 0; t < 2; t++) {
-    long long r = row0 + 16 * t + (lane & 15);
-    if (r >= rows) r = rows - 1;  // a valid row; its results are not stored
-    const int w = (int)(r / M), m = (int)(r % M);
-    ap[t] = A + w * a_ws + (long long)m * lda + kc;
+    ap[t] = A + s_a[lr0 + 16 * t + (lane & 15)] + kc;
+    gp[t] = GATE ? gh + s_g[lr0 + 16 * t + (lane & 15)] + kc : nullptr;
   }
   const uint16_t *bp = wt + (long long)(n0 + (lane & 15)) * Kp + kc;
   v4f acc[2][4];
@@ -64,7 +96,10 @@ __global__ __launch_bounds__(256) void k_gemm_f16(const uint16_t *__restrict__ A
     const bool in = k + kc < Kp;  // Kp % 8 == 0: a lane's 8-half chunk is all in or all out
     v8h a[2], b[4];
 #pragma unroll
-    for (int t = 0; t < 2; t++) a[t] = in ? *(const v8h *)(ap[t] + k) : (v8h){};
+    for (int t = 0; t < 2; t++) {
+      a[t] = in ? *(const v8h *)(ap[t] + k) : (v8h){};
+      if (GATE && in) a[t] = a[t] * *(const v8h *)(gp[t] + k);
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++) b[j] = in ? *(const v8h *)(bp + (long long)16 * j * Kp + k) : (v8h){};
 #pragma unroll
@@ -73,26 +108,69 @@ __global__ __launch_bounds__(256) void k_gemm_f16(const uint16_t *__restrict__ A
       for (int j = 0; j < 4; j++) acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b[j], acc[t][j], 0, 0, 0);
   }
   // accumulator lane layout: acc[t][j][r] = row 16 t + 4 (lane >> 4) + r, channel 16 j + (lane & 15)
+  float bn[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int n = n0 + 16 * j + (lane & 15);
-    if (n >= Np || n >= e.ldo) continue;
-    const float bn = bias[n];
+    bn[j] = n < Np ? bias[n] : 0.f;
+  }
+  const int nlim = Np < e.ldo ? Np : e.ldo;  // channels stored
 #pragma unroll
-    for (int t = 0; t < 2; t++)
+  for (int t = 0; t < 2; t++) {
+    if (VEC) {
+      uint16_t *T = s_t[wave];
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const long long row = row0 + 16 * t + 4 * (lane >> 4) + r;
-        if (row >= rows) continue;
-        const int w = (int)(row / M), m = (int)(row % M);
-        h16 v = f2h(acc[t][j][r] + bn);  // fp32 add, then one rounding to fp16 (nearest even)
-        if (e.act == 1) v = silu_lut_h(v);
-        else if (e.act == 2) v = hmax(v, (h16)0.0f);
-        if (e.res) v = v + hfrom(e.res[w * e.res_ws + (long long)m * e.ldr + n]);
-        long long orow = m;
-        if (e.opad) orow = (long long)((m / e.ow) + e.opad) * (e.ow + 2 * e.opad) + (m % e.ow) + e.opad;
-        e.out[w * e.out_ws + orow * e.ldo + n] = hbits(v);
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          // fp32 adds, then one rounding each to fp16 (nearest even); the SiLU on the pair in packed fp16
+          h2 v = (h2){f2h(acc[t][j][r] + bn[j]), f2h(acc[t][j][r + 1] + bn[j])};
+          if (e.act == 1) v = silu2_lut(v, s_t01, s_t2);
+          else if (e.act == 2) v = (h2){hmax(v[0], (h16)0.0f), hmax(v[1], (h16)0.0f)};
+          T[(4 * (lane >> 4) + r) * TS + 16 * j + (lane & 15)] = hbits(v[0]);
+          T[(4 * (lane >> 4) + r + 1) * TS + 16 * j + (lane & 15)] = hbits(v[1]);
+        }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // 16 rows x 8 chunks of 8 channels: two chunks per lane
+      const int ch = lane & 7;
+      const int n = n0 + 8 * ch;
+      v8h rv[2];
+#pragma unroll
+      for (int it = 0; it < 2; it++) {  // the residual chunks first (out and res may alias)
+        const int rr = 2 * (lane >> 3) + it, lr = lr0 + 16 * t + rr;
+        rv[it] = e.res && n < nlim && rowB + lr < rows ? *(const v8h *)(e.res + s_r[lr] + n) : (v8h){};
       }
+#pragma unroll
+      for (int it = 0; it < 2; it++) {
+        const int rr = 2 * (lane >> 3) + it, lr = lr0 + 16 * t + rr;
+        if (n < nlim && rowB + lr < rows) {
+          v8h y = *(const v8h *)(T + rr * TS + 8 * ch);
+          if (e.res) y = y + rv[it];
+          *(v8h *)(e.out + s_o[lr] + n) = y;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int n = n0 + 16 * j + (lane & 15);
+        if (n >= nlim) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int lr = lr0 + 16 * t + 4 * (lane >> 4) + r;
+          if (rowB + lr >= rows) continue;
+          h16 v = f2h(acc[t][j][r] + bn[j]);
+          if (e.act == 1) v = silu_lut_h(v);
+          else if (e.act == 2) v = hmax(v, (h16)0.0f);
+          if (e.res) v = v + hfrom(e.res[s_r[lr] + n]);
+          e.out[s_o[lr] + n] = hbits(v);
+        }
+      }
+    }
   }
 }
 
@@ -540,16 +618,50 @@ int bnh_gemm_f16(const uint16_t *A, long long a_ws, int lda, int M, int B, const
   return bnh_gemm_f16_body(A, a_ws, lda, M, B, W, e, stream);
 }
 
-int bnh_gemm_f16_mfma(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
-                      void *stream) {
-  if (gemm_f16_check(A, a_ws, lda, M, B, W, e) || zero_halo16(e, M, B, stream)) return -1;
+static int gemm_f16_mfma_run(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W,
+                             const bnh_epi16 *e, const uint16_t *gh, long long gh_ws, bool zero, void *stream) {
+  if (gemm_f16_check(A, a_ws, lda, M, B, W, e) || (zero && zero_halo16(e, M, B, stream))) return -1;
+  BNH_REQ(!gh || (((uintptr_t)gh & 15) == 0 && (B == 1 || (gh_ws % 8 == 0 && gh_ws >= W->Kp))));
+  BNH_REQ(lda % 8 == 0 && ((uintptr_t)A & 15) == 0 && (B == 1 || a_ws % 8 == 0));
   const long long rows = (long long)M * B;
   Epi16Dev d = {e->act, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->res, e->res_ws, e->ldr};
-  dim3 grid((unsigned)bnh_ceil_div(rows, 64), (unsigned)bnh_ceil_div(W->Np, 128));
-  hipLaunchKernelGGL(k_gemm_f16, grid, dim3(256), 0, bnh_stream(stream), A, a_ws, lda, M, rows, W->w, W->b, W->Kp,
-                     W->Np, d);
+  // 16-byte row chunks: 8-channel aligned rows in both the output and the residual
+  const bool vec = ((uintptr_t)e->out & 15) == 0 && e->ldo % 8 == 0 && (B == 1 || e->out_ws % 8 == 0) &&
+                   (!e->res || (((uintptr_t)e->res & 15) == 0 && e->ldr % 8 == 0 && (B == 1 || e->res_ws % 8 == 0))) &&
+                   W->Np % 8 == 0;
+  const long long nblocks = bnh_ceil_div(rows, 64) * bnh_ceil_div(W->Np, 128);
+  BNH_REQ(nblocks < (1LL << 31));
+  const dim3 grid((unsigned)nblocks);
+  const double rM = 1.0 / M;
+#define F16M_LAUNCH(G, V)                                                                                          \
+  hipLaunchKernelGGL((k_gemm_f16<G, V>), grid, dim3(256), 0, bnh_stream(stream), A, a_ws, lda, M, rM, rows, W->w, \
+                     W->b, W->Kp, W->Np, d, gh, gh_ws)
+  if (gh) {
+    if (vec) F16M_LAUNCH(true, true);
+    else F16M_LAUNCH(true, false);
+  } else {
+    if (vec) F16M_LAUNCH(false, true);
+    else F16M_LAUNCH(false, false);
+  }
+#undef F16M_LAUNCH
   BNH_HIP(hipGetLastError());
   return 0;
+}
+
+int bnh_gemm_f16_mfma(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
+                      void *stream) {
+  return gemm_f16_mfma_run(A, a_ws, lda, M, B, W, e, nullptr, 0, true, stream);
+}
+// the op's form: the PW op zeroes the output halo itself, only when its buffer does not keep it
+int bnh_gemm_f16_mfma_body(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W,
+                           const bnh_epi16 *e, const uint16_t *gh, long long gh_ws, void *stream) {
+  return gemm_f16_mfma_run(A, a_ws, lda, M, B, W, e, gh, gh_ws, false, stream);
+}
+
+int bnh_gemm_f16_mfma_gated(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W,
+                            const bnh_epi16 *e, const uint16_t *gh, long long gh_ws, void *stream) {
+  BNH_REQ(gh);
+  return gemm_f16_mfma_run(A, a_ws, lda, M, B, W, e, gh, gh_ws, true, stream);
 }
 
 }  // extern "C"

@@ -85,6 +85,11 @@ static int pw16_run(rt_ctx *c, rt_op *op) {
     const int H = p[4] / p[8];
     if (bnh_zero_halo(e.out, e.out_ws, H, p[8], p[7], p[9], 2, c->nwin, c->stream)) return -1;
   }
+  if (c->f16_mfma) {  // fp32 accumulation on the matrix cores: within the fp16 accumulation bound, not bit-exact
+    const uint16_t *gh = op->se ? se_gh(c, op->se) + (size_t)op->se->p[0] * c->w0 : nullptr;
+    return bnh_gemm_f16_mfma_body((const uint16_t *)rt_b(c, op, 0), rt_ws(c, op, 0), p[5], p[4], c->nwin, s->W, &e,
+                                  gh, op->se ? op->se->p[0] : 0, c->stream);
+  }
   // the split form's workspace: op-private, grown with the arena (the fp16 results of every K block of each window)
   void *ws = nullptr;
   size_t wsb = bnh_gemm_f16_ws_bytes(p[4], c->bcap, s->W);

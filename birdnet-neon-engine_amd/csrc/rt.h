@@ -92,6 +92,7 @@ struct rt_ctx {
   hipEvent_t sub_fork[RT_MAXSUB], sub_join[RT_MAXSUB];
   int n_sub;             // sub-batch streams created, including the context's own
   int one_stream;        // never split a batch over two streams
+  int f16_mfma;          // fp16 PW ops on fp16 MFMA (fp32 accumulation) instead of the reference's exact fp16 chains
   size_t *slot_bytes;    // per slot: bytes of one window's copy (64-aligned, >= 64 bytes of zero slack)
   int *slot_users;       // per slot: the number of buffers placed in it
   size_t arena_bytes;

@@ -178,6 +178,10 @@ int bnh_gemm_f16_gated_ws(const uint16_t *A, long long a_ws, int lda, int M, int
  * for callers that accept the fp16 accumulation error bound of the reference instead of its exact bits) */
 int bnh_gemm_f16_mfma(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W, const bnh_epi16 *e,
                       void *stream);
+/* the same with A's columns multiplied by the window's fp16 gates gh [>= Kp] (stride gh_ws) as they are loaded (no
+ * reference counterpart: the MFMA form of bnh_gemm_f16_gated_ws, an fp16 SE's scaling fused into its projection) */
+int bnh_gemm_f16_mfma_gated(const uint16_t *A, long long a_ws, int lda, int M, int B, const bnh_h16w *W,
+                            const bnh_epi16 *e, const uint16_t *gh, long long gh_ws, void *stream);
 
 /* ------------------------------------------------------------------ fp16 Winograd F(2x2, 3x3) convolution
  * The Winograd / fp16 GEMM path (src/wino_s0.c:1-165 for the transforms, src/wino.c for the tiling): a 3 x 3,

@@ -97,7 +97,11 @@ def run_gpu(hip, A, W, b32, act=0, ow=0, opad=0, res=None, Kp=None, b16=None, fn
                                                       wsb, None), "bnh_gemm_f16_gated_ws")
             H.sync()
             return dO.numpy()[:, :rows * ldo].reshape(Bw, rows, ldo), Wp
-        H.check(getattr(H.lib(), fn)(dA.ptr, a_ws, lda, M, Bw, hw, e, None), fn)
+        if fn == "bnh_gemm_f16_mfma_gated":
+            dG = H.DeviceArray.from_host(np.ascontiguousarray(gh, np.float16))
+            H.check(H.lib().bnh_gemm_f16_mfma_gated(dA.ptr, a_ws, lda, M, Bw, hw, e, dG.ptr, gh.shape[1], None), fn)
+        else:
+            H.check(getattr(H.lib(), fn)(dA.ptr, a_ws, lda, M, Bw, hw, e, None), fn)
         H.sync()
         out = dO.numpy()
         assert (out[:, rows * ldo:] == 7.0).all()   # nothing past each window's output
@@ -306,3 +310,26 @@ def test_gated_rows_bit_exact(hip, K, N, M, B, act, opad):
     assert same_bits(got, want)
     ref = O.gemm_f16(scaled[1], Wp, b, act=act, ow=ow, opad=opad, res=None if res is None else res[1])
     assert same_bits(got[1][:, :Np], ref[:, :Np])
+
+
+@pytest.mark.parametrize("K,N,M,ldo,opad", [(72, 864, 384, None, 1), (136, 40, 100, 44, 0), (48, 24, 64, None, 0)])
+def test_mfma_gated_equals_pregated(hip, K, N, M, ldo, opad):
+    """the gated MFMA form multiplies each loaded value by its channel's fp16 gate, one rounding, so it equals the
+    ungated MFMA form on A * gate rounded to fp16 (numpy), bit for bit: SiLU, residual, halo, the vector epilogue
+    (ldo % 8 == 0) and the scalar one (ldo 44)"""
+    rng = np.random.default_rng(K + N + M)
+    B, ow = 3, 16
+    Kp = (K + 7) // 8 * 8
+    A = np.zeros((B, M, Kp), np.float16)
+    A[:, :, :K] = rng.standard_normal((B, M, K))
+    g = np.zeros((B, Kp), np.float16)
+    g[:, :K] = rng.uniform(0, 1, (B, K))
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    res = None if opad else rng.standard_normal((B, M, ldo or (N + 7) // 8 * 8)).astype(np.float16)
+    say("f16 mfma gated", K, N, M, ldo, opad)
+    kw = dict(act=1, res=res, ldo=ldo, ow=ow if opad else 0, opad=opad)
+    got, _ = run_gpu(hip, A, W, b, fn="bnh_gemm_f16_mfma_gated", gh=g, **kw)
+    pre = (A * g[:, None, :]).astype(np.float16)
+    ref, _ = run_gpu(hip, pre, W, b, fn="bnh_gemm_f16_mfma", **kw)
+    assert same_bits(got, ref)

@@ -91,3 +91,28 @@ def test_v24_se_gates_in_the_gemm(hip, v24, monkeypatch, capfd):
         o2, e2, s2 = m.infer_batch(pcm)
     assert not status.any() and not s2.any()
     assert same(out, o2) and same(emb, e2)
+
+
+def test_v24_fp16_mfma_within_tolerance(hip, v24, monkeypatch):
+    """BNH_F16_MFMA=1 runs every fp16 1x1 conv on fp16 MFMA with fp32 accumulation (the SE gates still applied as
+    the rows load) instead of the reference's fp16 FMA chains. Over 64 windows, against the exact path: the largest
+    logit error stays within 2 % of the logits' range and the top-1 class agrees on at least 62 of 64 windows."""
+    vn, path = v24
+    rng = np.random.default_rng(21)
+    pcm = np.stack([v24net.signal(rng) for _ in range(64)])
+    say("v24 fp16 MFMA vs exact, 64 windows")
+    with binding.Model(path) as m:
+        ref, ref_emb, s0 = m.infer_batch(pcm)
+    monkeypatch.setenv("BNH_F16_MFMA", "1")
+    with binding.Model(path) as m:
+        got, emb, s1 = m.infer_batch(pcm)
+    assert not s0.any() and not s1.any()
+    d = np.abs(got.astype(np.float64) - ref)
+    span = float(ref.max() - ref.min())
+    top1 = int((got.argmax(1) == ref.argmax(1)).sum())
+    de = float(np.abs(emb.astype(np.float64) - ref_emb).max())
+    say(f"max |dlogit| {d.max():.4g} (logit range {span:.4g}, mean |dlogit| {d.mean():.3g}); top-1 agreement "
+        f"{top1}/64; max |demb| {de:.4g}")
+    assert not same(got, ref)   # the MFMA form really ran
+    assert d.max() <= 0.02 * span, (d.max(), span)
+    assert top1 >= 62, top1
