@@ -23,6 +23,9 @@ windows already resident in HBM):
                    point -128, per-channel Q31 requant, batch 256 windows.
   pw_s8            libbnneon's PW_S8 op (fp32 rows, per-row dynamic int8,
                    fp32 dequant + SiLU) at the same shape, batch 256.
+  qpw_s8           the dotprod family's QPW (gated fp16 rows, per-row
+                   asymmetric int8, fp32 FMA epilogue, fp16 SiLU out) 64 ->
+                   256 over 56 x 117 pixels, batch 64 windows.
   dw_f16, dw_s8    the depthwise convolution, NHWC, C = 672, 24 x 64, k x k
                    (--k 3|5) at stride --s 1|2, 'same' padding, bias + SiLU,
                    batch 64 windows: fp16 (libbnneon's DWK fp16 kernel) or
@@ -61,7 +64,7 @@ def parse():
     ap.add_argument("--batch", type=int, default=None,
                     help="windows per launch (256; 64 for the depthwise workloads)")
     ap.add_argument("--workload", default="perch_s8",
-                    choices=["perch_s8", "v24_f16", "gemm_s8_requant", "pw_s8", "proto_s8", "dw_f16", "dw_s8",
+                    choices=["perch_s8", "v24_f16", "gemm_s8_requant", "pw_s8", "proto_s8", "qpw_s8", "dw_f16", "dw_s8",
                              "wino_f16", "copy"])
     ap.add_argument("--k", type=int, default=5, choices=[3, 5], help="depthwise kernel size")
     ap.add_argument("--s", type=int, default=1, choices=[1, 2], help="depthwise stride")
@@ -274,7 +277,7 @@ def main():
     if H.lib().bnh_device_count() < 1:
         raise SystemExit("no HIP device visible")
     rng = np.random.default_rng(20240601)
-    B = a.batch or (64 if a.workload.startswith(("dw_", "wino")) else 256)
+    B = a.batch or (64 if a.workload.startswith(("dw_", "wino", "qpw")) else 256)
     N, K, M = 256, 1152, 1536
     stream = H.lib().bnh_stream_new()
     if a.workload == "copy":
@@ -303,6 +306,9 @@ def main():
         return
     if a.workload == "proto_s8":
         run_proto(a, H, rng, B, stream)
+        return
+    if a.workload == "qpw_s8":
+        run_qpw(a, H, rng, B, stream)
         return
     if a.workload == "gemm_s8_requant":
         w, x, bias, mult, shift = config0_inputs(rng, B)
@@ -480,6 +486,82 @@ def run_wino(a, H, rng, B, stream):
     L.bnh_wino16_free(P)
     print(json.dumps(line), flush=True)
 
+
+
+def run_qpw(a, H, rng, B, stream):
+    """The dotprod family's QPW (src/rt_ops_dot.c:326-339) at a BirdNET-v3.0-like MBConv expansion: per window
+    fp16 rows of 56 x 117 pixels x 64 channels, gated by an SE's fp16 gates, quantised per row to int8 (k_qd_quant),
+    the int8 MFMA GEMM to 256 channels with the fp32 FMA epilogue, fp16 + table SiLU into a zero-haloed buffer
+    (k_qd_gemm). Timed: both kernels per step; the GEMM also alone, for the roofline."""
+    import ctypes
+    Hh, W, K, N = 56, 117, 64, 256
+    M, Kp = Hh * W, 64
+    L = H.lib()
+    w = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    Wq = L.bnh_qdw_new(w.ctypes.data, bias.ctypes.data, N, K, N)
+    if not Wq:
+        H.check(None, "bnh_qdw_new")
+    x = (rng.standard_normal((B, M * K)) * 2).astype(np.float16)
+    g = rng.uniform(0, 1, (B, K)).astype(np.float16)
+    dx, dg = H.DeviceArray.from_host(x), H.DeviceArray.from_host(g)
+    a_ws, rq_ws = (M + 4) * Kp, 2 * (M + 4)
+    rows_out = (Hh + 2) * (W + 2)
+    o_ws = rows_out * N
+    da = H.DeviceArray.zeros((B, a_ws), np.int8)
+    dr = H.DeviceArray.zeros((B, rq_ws), np.float32)
+    do = H.DeviceArray.zeros((B, o_ws), np.float16)
+    e = H.QdEpi(1, 1, do.ptr, o_ws, N, W, 1, None, 0)
+
+    def quant():
+        H.check(L.bnh_qd_quant_rows(dx.ptr, 1, M * K, K, M, K, dg.ptr, K, da.ptr, a_ws, dr.ptr, rq_ws, B, stream))
+
+    def gemm():
+        H.check(L.bnh_qd_gemm(da.ptr, a_ws, Kp, dr.ptr, rq_ws, 0, M, Wq, ctypes.byref(e), B, stream))
+
+    def launch():
+        quant()
+        gemm()
+    ms, wall = time_steps(H, stream, launch, a.steps, a.warmup)
+    ms_g, _ = time_steps(H, stream, gemm, max(10, a.steps), 3)
+    op_bytes = B * (M * K * 2 + K * 2 + M * N * 2) + N * Kp + 12 * N   # the op's own inputs and outputs
+    gemm_bytes = B * (M * Kp + 8 * M + rows_out * N * 2) + N * Kp + 12 * N
+    gbs = gemm_bytes / (ms_g * 1e-3) / 1e9
+    line = {
+        "metric": "windows/s (dotprod QPW, batch 64)", "value": round(B / (ms * 1e-3), 1), "unit": "windows/s",
+        "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded normal rows, uniform gates, random weights)",
+        "config": {"workload": "dotprod QPW 64->256 over 56x117 px per window: gated fp16 rows, per-row asymmetric "
+                               "int8, int8 MFMA GEMM, fp32 FMA epilogue, fp16 table SiLU into a zero-haloed buffer",
+                   "global_batch": B, "channels_in": K, "channels_out": N, "pixels": M,
+                   "parallelism": "1 GPU, windows batched per launch", "wall_s_timed_region": round(wall, 4),
+                   "op_bytes_per_step": op_bytes},
+        "int8_tops": round(2.0 * B * M * N * K / (ms_g * 1e-3) / 1e12, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_qd_gemm",
+                     "ms_per_launch": round(ms_g, 4), "algorithmic_bytes_per_launch": gemm_bytes},
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_qpw(x, g, w, bias, Hh, W)
+    L.bnh_qdw_free(Wq)
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_qpw(x, g, w, bias, Hh, W):
+    """The oracle's QPW (quantisation + int8 GEMM + epilogue, scalar C) on a bounded sample of windows."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    K = w.shape[1]
+    pk = O.qd_wpack(w, bias)
+    t0 = time.perf_counter()
+    n = 0
+    while n == 0 or time.perf_counter() - t0 < 5.0:
+        O.qpw(x[n % x.shape[0]].reshape(Hh * W, K), pk, act=1, out16=True, ow=W, opad=1, gate=g[n % g.shape[0]])
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "windows/s", "cores": 1, "kind": "port",
+            "sample": f"{n} windows of the oracle's QPW (scalar C, 1 thread), {dt:.2f} s wall"}
 
 
 def run_proto(a, H, rng, B, stream):

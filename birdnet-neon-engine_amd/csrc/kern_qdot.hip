@@ -175,6 +175,91 @@ __global__ __launch_bounds__(256) void k_qd_quant(const void *__restrict__ xv, l
   }
 }
 
+// The same with L lanes per row (64 / L rows per wavefront) and 8 channels per lane per pass: 16-byte loads (fp16)
+// or two 16-byte loads (fp32), one 8-byte store of codes. K % 8 == 0, so every 8-channel chunk lies wholly in the
+// range part and wholly in the fp16 (or magic-number) code part or in the fp32 tail part; the lane group's range
+// reduction is order-free (NaN-propagating minima).
+typedef _Float16 qv8h __attribute__((ext_vector_type(8)));
+template <int L, bool F16>
+__global__ __launch_bounds__(256) void k_qd_quant_v(const void *__restrict__ xv, long long x_ws, int ldx, int M,
+                                                    double rM, int K, int Kp, const uint16_t *__restrict__ gate,
+                                                    long long g_ws, int8_t *__restrict__ a, long long a_ws,
+                                                    float *__restrict__ rq, long long rq_ws, long long rows) {
+  const int lane = threadIdx.x & 63, sub = lane % L;
+  long long row = ((long long)blockIdx.x * 256 + threadIdx.x) / L;
+  const bool live = row < rows;
+  if (!live) row = rows - 1;  // a valid row: the group's lanes take part in the shuffles, nothing is stored
+  const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
+  int8_t *o = a + w * a_ws + (long long)m * Kp;
+  const float *r32 = F16 ? nullptr : (const float *)xv + w * x_ws + (long long)m * ldx;
+  const _Float16 *r16 = F16 ? (const _Float16 *)xv + w * x_ws + (long long)m * ldx : nullptr;
+  const _Float16 *g = F16 && gate ? (const _Float16 *)gate + w * g_ws : nullptr;
+  float mn = 0.f, mx = 0.f;
+  for (int c0 = 8 * sub; c0 < K; c0 += 8 * L) {
+    if (F16) {
+      qv8h h = *(const qv8h *)(r16 + c0);
+      if (g) h = h * *(const qv8h *)(g + c0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        mn = bnh_fmin(mn, (float)h[i]);
+        mx = bnh_fmax(mx, (float)h[i]);
+      }
+    } else {
+      const float4 u = *(const float4 *)(r32 + c0), v = *(const float4 *)(r32 + c0 + 4);
+      const float e[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        mn = bnh_fmin(mn, e[i]);
+        mx = bnh_fmax(mx, e[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < L; off <<= 1) {
+    mn = bnh_fmin(mn, __shfl_xor(mn, off));
+    mx = bnh_fmax(mx, __shfl_xor(mx, off));
+  }
+  float s, zp, inv;
+  qd_params(mn, mx, s, zp, inv);
+  if (live && sub == 0) {
+    rq[w * rq_ws + 2 * m] = s;
+    rq[w * rq_ws + 2 * m + 1] = zp;
+  }
+  if (!live) return;
+  const int32_t zofs = 0x4B400000 + (int32_t)zp;
+  const h16 hinv = f2h(inv);
+  const uint16_t zo = (uint16_t)(0x6600 + (int)zp);
+  const int kq = F16 ? K & ~15 : K;  // fp16 codes below kq, the fp32 tail from there (the fp32 rows: magic codes)
+  for (int c0 = 8 * sub; c0 < Kp; c0 += 8 * L) {
+    uint32_t lo = 0, hi = 0;
+    if (c0 < K) {
+      if (F16) {
+        const qv8h xr = *(const qv8h *)(r16 + c0);
+        const qv8h gr = g ? *(const qv8h *)(g + c0) : (qv8h){};
+        if (c0 < kq) {
+          const qv8h h = g ? xr * gr : xr;  // the gated product rounded to fp16
+#pragma unroll
+          for (int i = 0; i < 8; i++)
+            (i < 4 ? lo : hi) |= (uint32_t)(uint8_t)qd_clamp8((int16_t)(uint16_t)(hbits(hfma(h[i], hinv, (h16)1536.0f)) -
+                                                                                    zo)) << (8 * (i & 3));
+        } else {  // the fp32 tail: the unrounded product (exact in fp32), times the fp32 inv
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            const float v = (float)xr[i] * (g ? (float)gr[i] : 1.f);
+            (i < 4 ? lo : hi) |= (uint32_t)(uint8_t)qd_tail(v * inv, zp) << (8 * (i & 3));
+          }
+        }
+      } else {
+        const float4 u = *(const float4 *)(r32 + c0), v = *(const float4 *)(r32 + c0 + 4);
+        const float e[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) (i < 4 ? lo : hi) |= (uint32_t)(uint8_t)qd_magic(e[i], inv, zofs) << (8 * (i & 3));
+      }
+    }
+    *(uint2 *)(o + c0) = make_uint2(lo, hi);
+  }
+}
+
 // ------------------------------------------------------------------ GEMM + fp32 FMA epilogue
 struct QdEpi {
   int act;          // 0 none, 1 SiLU, 2 ReLU
@@ -199,15 +284,25 @@ struct QdConv {  // the 3 x 3 implicit im2col: A row m = output pixel (m / Wo, m
 // A block owns 128 rows; each wave 32 of them (2 MFMA row tiles) across the 64-channel groups [g0, g1) of its part.
 // CONV: k = 3 C ky + (kx C + c) over the haloed copy (its rows hold the 3 C bytes of kx = 0..2 contiguously), each
 // 16-byte chunk as two 8-byte halves, zero past 9 C.
-template <bool CONV>
+// VEC: each wave's 16 x 64 tile leaves the accumulators through LDS after its epilogue (the same operations, the
+// fp16 SiLU two values at a time from an LDS table) and is stored as 16-byte row chunks (fp32: the residual chunk
+// added to each), instead of one 2- or 4-byte store per value.
+template <bool CONV, bool VEC>
 __global__ __launch_bounds__(256) void k_qd_gemm(const int8_t *__restrict__ a, long long a_ws, int lda,
                                                  const float *__restrict__ rq, long long rq_ws, int per_tensor, int M,
                                                  double rM, long long rows, const int8_t *__restrict__ wt,
                                                  const float *__restrict__ sw, const float *__restrict__ sws,
                                                  const float *__restrict__ bias, int Kp, int Np, int gsplit, QdEpi e,
                                                  QdConv cv) {
-  constexpr int RB = 128;
+  constexpr int RB = 128, TS = 68;  // TS: the tile's LDS row stride in floats (64 channels + 4)
   __shared__ long long s_a[RB], s_o[RB], s_r[RB];
+  __shared__ __attribute__((aligned(16))) float s_t[VEC ? 4 : 1][VEC ? 16 * TS : 1];
+  __shared__ uint32_t s_t01[16];
+  __shared__ uint16_t s_t2[16];
+  if (threadIdx.x < 16) {
+    s_t01[threadIdx.x] = (uint32_t)k_silu_c0[threadIdx.x] | ((uint32_t)k_silu_c1[threadIdx.x] << 16);
+    s_t2[threadIdx.x] = k_silu_c2[threadIdx.x];
+  }
   __shared__ float s_sa[RB], s_zs[RB];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const unsigned lb = gsplit > 1 ? bnh_xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
@@ -283,6 +378,82 @@ __global__ __launch_bounds__(256) void k_qd_gemm(const int8_t *__restrict__ a, l
       swn[j] = ok ? sw[n] : 0.f;
       ssn[j] = ok ? sws[n] : 0.f;
       bn[j] = ok ? bias[n] : 0.f;
+    }
+    if (VEC) {
+      float *T = s_t[wave];
+      const int nv = Np - n0 < 64 ? Np - n0 : 64;  // channels of this group (a multiple of 16)
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          if (j >= jn) break;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int lr = lr0 + 16 * t + 4 * (lane >> 4) + r;
+            const float f = (float)acc[t][j][r];
+            const float v0 = f * swn[j];
+            v[r] = __builtin_fmaf(ssn[j], s_zs[lr], __builtin_fmaf(v0, s_sa[lr], bn[j]));
+          }
+          const int col = 16 * j + (lane & 15), rb = 4 * (lane >> 4);
+          if (e.out_f16) {
+            uint16_t *Th = (uint16_t *)T;  // [16][2 TS] halves
+#pragma unroll
+            for (int r = 0; r < 4; r += 2) {
+              h2 hv = (h2){f2h(v[r]), f2h(v[r + 1])};
+              if (e.act == 1) hv = silu2_lut(hv, s_t01, s_t2);
+              Th[(rb + r) * 2 * TS + col] = hbits(hv[0]);
+              Th[(rb + r + 1) * 2 * TS + col] = hbits(hv[1]);
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              float y = v[r];
+              if (e.act == 1) y = qd_silu_f32_a(y);
+              else if (e.act == 2) y = bnh_relu_f32(y);
+              T[(rb + r) * TS + col] = y;
+            }
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (e.out_f16) {  // 16 rows x 8 chunks of 8 halves: two per lane
+#pragma unroll
+          for (int it = 0; it < 2; it++) {
+            const int rr = 8 * it + (lane >> 3), ch = lane & 7, lr = lr0 + 16 * t + rr;
+            if (8 * ch < nv && rowB + lr < rows)
+              *(uint4 *)((uint16_t *)e.out + s_o[lr] + n0 + 8 * ch) =
+                  *(const uint4 *)((const uint16_t *)T + rr * 2 * TS + 8 * ch);
+          }
+        } else {  // 16 rows x 16 chunks of 4 floats: four per lane, the residual chunks loaded first
+          float4 rv4[4];
+#pragma unroll
+          for (int it = 0; it < 4; it++) {
+            const int rr = 4 * it + (lane >> 4), ch = lane & 15, lr = lr0 + 16 * t + rr;
+            rv4[it] = e.res && 4 * ch < nv && rowB + lr < rows ? *(const float4 *)(e.res + s_r[lr] + n0 + 4 * ch)
+                                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+#pragma unroll
+          for (int it = 0; it < 4; it++) {
+            const int rr = 4 * it + (lane >> 4), ch = lane & 15, lr = lr0 + 16 * t + rr;
+            if (4 * ch < nv && rowB + lr < rows) {
+              float4 y = *(const float4 *)(T + rr * TS + 4 * ch);
+              if (e.res) {
+                y.x = y.x + rv4[it].x;
+                y.y = y.y + rv4[it].y;
+                y.z = y.z + rv4[it].z;
+                y.w = y.w + rv4[it].w;
+              }
+              *(float4 *)((float *)e.out + s_o[lr] + n0 + 4 * ch) = y;
+            }
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      continue;
     }
 #pragma unroll
     for (int t = 0; t < 2; t++) {
@@ -592,6 +763,30 @@ int bnh_qd_quant_rows(const void *x, int in_f16, long long x_ws, int ldx, int M,
   BNH_REQ(((uintptr_t)a & 3) == 0 && (B == 1 || (a_ws % 4 == 0 && a_ws >= (long long)M * Kp)));
   BNH_REQ(B == 1 || (x_ws >= (long long)(M - 1) * ldx + K && rq_ws >= 2LL * M && (!gate || g_ws >= K)));
   const long long rows = (long long)M * B;
+  // the vector form: 8-channel chunks (16-byte aligned rows of fp16, 32-byte of fp32; 8-byte aligned code rows)
+  const int esz = in_f16 ? 2 : 4;
+  const bool vec = K % 8 == 0 && ((uintptr_t)x & 15) == 0 && (ldx * esz) % 16 == 0 && (B == 1 || (x_ws * esz) % 16 == 0) &&
+                   (!gate || (((uintptr_t)gate & 15) == 0 && (B == 1 || (g_ws * 2) % 16 == 0))) &&
+                   ((uintptr_t)a & 7) == 0 && (B == 1 || a_ws % 8 == 0);
+  if (vec) {
+    int L = 1;
+    while (L < 64 && 8 * L < K) L *= 2;  // lanes per row: enough for one pass over K where that fits in a wave
+    const unsigned nbv = (unsigned)bnh_ceil_div(rows * L, 256);
+    hipStream_t st = bnh_stream(stream);
+#define QDQ(LL)                                                                                                        \
+  if (L == LL) {                                                                                                      \
+    if (in_f16)                                                                                                        \
+      hipLaunchKernelGGL((k_qd_quant_v<LL, true>), dim3(nbv), dim3(256), 0, st, x, x_ws, ldx, M, 1.0 / M, K, Kp,       \
+                         gate, g_ws, a, a_ws, rq, rq_ws, rows);                                                        \
+    else                                                                                                               \
+      hipLaunchKernelGGL((k_qd_quant_v<LL, false>), dim3(nbv), dim3(256), 0, st, x, x_ws, ldx, M, 1.0 / M, K, Kp,      \
+                         nullptr, 0LL, a, a_ws, rq, rq_ws, rows);                                                      \
+  }
+    QDQ(1) QDQ(2) QDQ(4) QDQ(8) QDQ(16) QDQ(32) QDQ(64)
+#undef QDQ
+    BNH_HIP(hipGetLastError());
+    return 0;
+  }
   const unsigned nb = (unsigned)bnh_ceil_div(rows, 4);
   if (in_f16)
     hipLaunchKernelGGL(k_qd_quant<true>, dim3(nb), dim3(256), 0, bnh_stream(stream), x, x_ws, ldx, M, 1.0 / M, K, Kp,
@@ -623,12 +818,21 @@ static int qd_gemm_launch(bool conv, const int8_t *a, long long a_ws, int lda, c
   QdEpi d = {e->act, e->out_f16, e->out, e->out_ws, e->ldo, e->ow, e->opad, e->ow > 0 ? 1.0 / e->ow : 0.0, e->res,
              e->res_ws};
   const dim3 grid((unsigned)(nrb * gsplit));
-  if (conv)
-    hipLaunchKernelGGL(k_qd_gemm<true>, grid, dim3(256), 0, bnh_stream(stream), a, a_ws, lda, rq, rq_ws, per_tensor,
-                       M, 1.0 / M, rows, W->w, W->scale, W->swsum, W->bias, W->Kp, W->Np, gsplit, d, cv);
-  else
-    hipLaunchKernelGGL(k_qd_gemm<false>, grid, dim3(256), 0, bnh_stream(stream), a, a_ws, lda, rq, rq_ws, per_tensor,
-                       M, 1.0 / M, rows, W->w, W->scale, W->swsum, W->bias, W->Kp, W->Np, gsplit, d, cv);
+  // 16-byte row chunks: 16-byte aligned rows (8 halves / 4 floats) in the output and the residual
+  const int esz = e->out_f16 ? 2 : 4;
+  const bool vec = ((uintptr_t)e->out & 15) == 0 && (e->ldo * esz) % 16 == 0 && (B == 1 || (e->out_ws * esz) % 16 == 0) &&
+                   (!e->res || (((uintptr_t)e->res & 15) == 0 && (B == 1 || e->res_ws % 4 == 0)));
+#define QDG(CV, VC)                                                                                                    \
+  hipLaunchKernelGGL((k_qd_gemm<CV, VC>), grid, dim3(256), 0, bnh_stream(stream), a, a_ws, lda, rq, rq_ws, per_tensor, \
+                     M, 1.0 / M, rows, W->w, W->scale, W->swsum, W->bias, W->Kp, W->Np, gsplit, d, cv)
+  if (conv) {
+    if (vec) QDG(true, true);
+    else QDG(true, false);
+  } else {
+    if (vec) QDG(false, true);
+    else QDG(false, false);
+  }
+#undef QDG
   BNH_HIP(hipGetLastError());
   return 0;
 }

@@ -68,9 +68,11 @@ def rand_rows(rng, B, M, K, kind):
 
 @pytest.mark.parametrize("K", [8, 20, 23, 40, 136, 1152])
 @pytest.mark.parametrize("kind", [0, 1, 2])
-def test_quant_rows_f32(hip, K, kind):
+@pytest.mark.parametrize("pad", [5, 8])
+def test_quant_rows_f32(hip, K, kind, pad):
+    """pad 8 with K % 8 == 0: the multi-row vector kernel; pad 5 or K % 8 != 0: one wavefront per row"""
     rng = np.random.default_rng(K * 3 + kind)
-    B, M, ldx = 3, 37, K + 5
+    B, M, ldx = 3, 37, K + pad
     x = np.zeros((B, M, ldx), np.float32)
     x[:, :, :K] = rand_rows(rng, B, M, K, kind)
     Kp = (K + 15) // 16 * 16
@@ -98,6 +100,7 @@ def test_quant_rows_f16(hip, K, gated):
     x = np.zeros((B, M, ldx), np.float16)
     x[:, :, :K] = (rng.standard_normal((B, M, K)) * 3).astype(np.float16)
     x[:, 0, :] = 0
+    x[:, 1, :] = np.float16(0.75)  # a constant row
     g = rng.uniform(0, 1, (B, K)).astype(np.float16) if gated else None
     Kp = (K + 15) // 16 * 16
     say("quant_rows_f16", K, gated)
