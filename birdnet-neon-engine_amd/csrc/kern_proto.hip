@@ -196,6 +196,13 @@ typedef __attribute__((address_space(3))) v4i lds_v4i;
 typedef __attribute__((address_space(3))) float lds_f32;
 
 BNH_DEV float pg_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// the maximum of lanes l, l ^ 16, l ^ 32 and l ^ 48 (gfx950 row swaps: no LDS traffic)
+BNH_DEV float pg_max16(float m) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  m = pg_max(__uint_as_float(r[0]), __uint_as_float(r[1]));  // rows (0, 1) and (2, 3)
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return pg_max(__uint_as_float(q[0]), __uint_as_float(q[1]));  // halves (0, 1)
+}
 // an accumulator element read out of its AGPR where the epilogue uses it: without this the compiler copies all 256
 // accumulators into VGPRs when the K loop ends and spills the block's other values to scratch
 BNH_DEV int32_t pg_acc(int32_t x) {
@@ -342,6 +349,177 @@ __global__ __launch_bounds__(256, 1) void k_proto_gemm64(const int8_t *__restric
   }
 }
 
+// The same GEMM with 8 waves in two ping-pong groups. Waves 0-3 (group 0) and 4-7 (group 1) put one wave of each
+// group on every SIMD; the wave of group g owns cells 128 g .. 128 g + 127 (2 windows) x prototypes 64 (wave % 4) ..
+// + 63 of the tile (8 x 4 MFMA tiles, 128 accumulators). Every K slice is a memory phase (issue the DMA three slices
+// ahead, read the slice's 12 fragments into registers) then a compute phase (32 MFMAs, and the epilogue after a tile's
+// last slice), with a block barrier after each phase. Group 1 starts one barrier late, so between any two barriers one
+// group reads LDS while the other runs MFMAs: the matrix cores of a SIMD are fed by one wave while the other waits
+// on its fragment reads.
+//   Slice s is read by group 0 in interval 2s and by group 1 in interval 2s + 1 (interval i lies between barrier i and
+// barrier i + 1). Every wave waits for its own DMA of slice s + 1 (vmcnt) before the barrier that opens interval
+// 2s + 2, and for its fragment reads (lgkmcnt) before the barrier that ends its memory phase; the DMA of slice s + 3
+// issued in interval 2s (group 0) or 2s + 1 (group 1) refills the stage of slice s - 1, whose last reads were in
+// interval 2s - 1. The tile's scales use the same double buffer as the 4-wave kernel (K slices >= 4).
+BNH_DEV void pp_sync() {
+  __builtin_amdgcn_sched_barrier(0);  // no instruction moves across a phase boundary
+  RQ_BARRIER();
+  __builtin_amdgcn_sched_barrier(0);
+}
+// this wave's DMA of slice s + 1 has landed: at most the loads of the (up to two) slices issued after it are pending
+BNH_DEV void pp_wait_next(int total, int s) {
+  const int later = total - 2 - s;
+  if (later >= 2) RQ_WAIT_VM(8);
+  else if (later == 1) RQ_WAIT_VM(4);
+  else RQ_WAIT_VM(0);
+}
+
+__global__ __launch_bounds__(512, 1) void k_proto_gemm_pp(const int8_t *__restrict__ qa, long long qa_ws,
+                                                         const float *__restrict__ sx, long long sx_ws, int B, int Kp,
+                                                         const int8_t *__restrict__ wt, const float *__restrict__ sw,
+                                                         int Np, int n_mt, int n_nt, float *__restrict__ colmax,
+                                                         long long cm_ws) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds_raw[PG_SCL + 2 * 2048];
+  lds_i8 *lds = (lds_i8 *)lds_raw;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wn = wave & 3;
+  const int xcd = (int)(blockIdx.x & 7);
+  PgRegion R;
+  R.lid = (int)(blockIdx.x >> 3);
+  R.nlb = (int)(gridDim.x >> 3);
+  const int gm = n_mt >= 8 ? 8 : n_mt >= 4 ? 4 : n_mt >= 2 ? 2 : 1, gn = 8 / gm;
+  const int rm = xcd / gn, rn = xcd % gn;
+  R.m_lo = rm * n_mt / gm;
+  R.mx = (rm + 1) * n_mt / gm - R.m_lo;
+  R.n_lo = rn * n_nt / gn;
+  const int nx = (rn + 1) * n_nt / gn - R.n_lo;
+  const int xtiles = R.mx * nx;
+  const int mytiles = xtiles > R.lid ? (xtiles - 1 - R.lid) / R.nlb + 1 : 0;
+  const int steps = Kp / PG_BK;
+  // DMA roles: per K slice a wave issues 2 cell instructions (rows 32 wave .. 32 wave + 31 of the tile: cells
+  // 32 (wave % 2) .. of window m_t 4 + wave / 2) and 2 prototype instructions (rows 32 wave .. 32 wave + 31)
+  const int dchunk = 16 * ((lane & 3) ^ ((lane >> 3) & 3));
+  const uint32_t loff_a = (uint32_t)((lane >> 2) * Kp + dchunk);
+  const uint32_t loff_b = (uint32_t)((lane >> 2) * PG_BK + dchunk);
+  const long long a16 = 16LL * Kp, b16 = (long long)(Kp / PG_BK) * 1024;
+  int iss_i = 0, iss_k = 0, iss_st = 0;
+  const int8_t *a_tile = qa, *b_tile = wt;
+  auto issue = [&]() {
+    if (iss_k == 0) {
+      int m_t, n_t;
+      R.tile(iss_i, m_t, n_t);
+      int win = m_t * 4 + (wave >> 1);
+      if (win > B - 1) win = B - 1;
+      a_tile = qa + (long long)win * qa_ws + (long long)(wave & 1) * 32 * Kp;
+      b_tile = wt + (long long)(n_t * 16 + 2 * wave) * b16;
+      if (wave < 2) {
+        lds_i8 *sc = lds + PG_SCL + (iss_i & 1) * 2048 + wave * 1024;
+        if (wave == 0) {
+          const int last = B - 1 - m_t * 4;
+          const int wl = (lane >> 4) < last ? (lane >> 4) : last;
+          rq_dma16s(sx + (long long)m_t * 4 * sx_ws, (uint32_t)(wl * sx_ws * 4 + 16 * (lane & 15)), sc);
+        } else {
+          rq_dma16s(sw + n_t * PG_TN, (uint32_t)(16 * lane), sc);
+        }
+      }
+    }
+    lds_i8 *st = lds + iss_st * PG_STAGE;
+    const int8_t *ab = a_tile + iss_k * PG_BK, *bb = b_tile + iss_k * 1024;
+#pragma unroll
+    for (int h = 0; h < 2; h++) rq_dma16s(ab + h * a16, loff_a, st + (2 * wave + h) * 1024);
+#pragma unroll
+    for (int h = 0; h < 2; h++) rq_dma16s(bb + h * b16, loff_b, st + PG_AB + (2 * wave + h) * 1024);
+    if (++iss_st == PG_NST) iss_st = 0;
+    if (++iss_k == steps) { iss_k = 0; iss_i++; }
+  };
+  const int g = lane >> 4, j16 = lane & 15;
+  const int foff = j16 * PG_BK + 16 * (g ^ ((j16 >> 1) & 3));
+  const int fa_off = grp * 128 * PG_BK + foff, fb_off = PG_AB + wn * 64 * PG_BK + foff;
+  const int total = mytiles * steps;
+  for (int s = 0; s < PG_NST - 1 && s < total; s++) issue();
+  if (total > 2) RQ_WAIT_VM(8);  // slice 0 has landed
+  else if (total == 2) RQ_WAIT_VM(4);
+  else RQ_WAIT_VM(0);
+  pp_sync();
+  if (grp) pp_sync();  // group 1 runs one phase behind group 0
+  v4i acc[8][4];
+  // the column maxima of tile i: acc[t][jj][r] is cell row 16 (t % 4) + 4 g + r of window m_t 4 + 2 grp + t / 4,
+  // prototype wn 64 + 16 jj + j16 of the tile
+  auto epilogue = [&](int i) {
+    int m_t, n_t;
+    R.tile(i, m_t, n_t);
+    const lds_f32 *sxs = (const lds_f32 *)(lds + PG_SCL + (i & 1) * 2048);
+    const lds_f32 *sws = sxs + 256;
+#pragma unroll
+    for (int wl = 0; wl < 2; wl++) {
+      float srow[4][4];
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) srow[t][r] = sxs[grp * 128 + 64 * wl + 16 * t + 4 * g + r];
+      const int win = m_t * 4 + grp * 2 + wl;
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) m = pg_max(m, (float)acc[4 * wl + t][jj][r] * srow[t][r]);
+        m = pg_max16(m);
+        const int nl = wn * 64 + 16 * jj + j16, n = n_t * PG_TN + nl;
+        if (lane < 16 && win < B && n < Np) colmax[win * cm_ws + n] = m * sws[nl];
+      }
+    }
+  };
+  int cst = 0, ci = 0, ck = 0;
+  int done = -1;  // a tile whose sums are complete and whose epilogue has not run
+  for (int s = 0; s < total; s++) {
+    asm volatile("" : "+s"(done));  // opaque to the optimiser: no peeled first iteration (it would spill)
+    // ---- memory phase of slice s: its DMA three slices ahead, its fragments, and (on a tile's first slice) the
+    // previous tile's epilogue, whose VALU work runs beside the other group's MFMAs
+    if (s + PG_NST - 1 < total) issue();
+    if (done >= 0) {
+      epilogue(done);
+      done = -1;
+    }
+    const lds_i8 *st = lds + cst * PG_STAGE;
+    if (++cst == PG_NST) cst = 0;
+    const lds_i8 *pa = st + fa_off, *pb = st + fb_off;
+    v4i a[8], b[4];
+#pragma unroll
+    for (int t = 0; t < 8; t++) a[t] = *(const lds_v4i *)(pa + t * 1024);
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) b[jj] = *(const lds_v4i *)(pb + jj * 1024);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (grp) pp_wait_next(total, s);
+    pp_sync();
+    // ---- compute phase of slice s
+    if (ck == 0) {  // a tile's first slice starts its sums from zero
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+          acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[jj], (v4i){0, 0, 0, 0}, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+          acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[jj], acc[t][jj], 0, 0, 0);
+    }
+    if (++ck == steps) {
+      done = ci;
+      ck = 0;
+      ci++;
+    }
+    if (!grp) pp_wait_next(total, s);
+    pp_sync();
+  }
+  if (done >= 0) epilogue(done);
+  if (!grp) pp_sync();  // every wave passes the same number of barriers
+}
+
 // ------------------------------------------------------------------ class logits (pc_proto_logits)
 __global__ void k_proto_logits(const float *__restrict__ colmax, long long cm_ws, const float *__restrict__ w,
                                const float *__restrict__ b, int nc, int ppc, float *__restrict__ logits, long long lg_ws,
@@ -464,8 +642,13 @@ int bnh_proto_colmax(const int8_t *qa, long long qa_ws, const float *sx, long lo
     const int n_mt = (int)bnh_ceil_div((long long)B * 64, PG_TM), n_nt = W->Npt / PG_TN;
     int grid = ncu / 8 * 8;  // one block per CU
     if (grid < 8) grid = 8;
-    hipLaunchKernelGGL(k_proto_gemm64, dim3((unsigned)grid), dim3(256), 0, bnh_stream(stream), qa, B == 1 ? 0 : qa_ws, sx,
-                       B == 1 ? 0 : sx_ws, B, W->Kp, W->w, W->sw, W->Np, n_mt, n_nt, colmax, B == 1 ? 0 : cm_ws);
+    static const bool four = getenv("BNH_PROTO_4W") != nullptr;  // the 4-wave form, for comparison
+    if (four)
+      hipLaunchKernelGGL(k_proto_gemm64, dim3((unsigned)grid), dim3(256), 0, bnh_stream(stream), qa, B == 1 ? 0 : qa_ws,
+                         sx, B == 1 ? 0 : sx_ws, B, W->Kp, W->w, W->sw, W->Np, n_mt, n_nt, colmax, B == 1 ? 0 : cm_ws);
+    else
+      hipLaunchKernelGGL(k_proto_gemm_pp, dim3((unsigned)grid), dim3(512), 0, bnh_stream(stream), qa, B == 1 ? 0 : qa_ws,
+                         sx, B == 1 ? 0 : sx_ws, B, W->Kp, W->w, W->sw, W->Np, n_mt, n_nt, colmax, B == 1 ? 0 : cm_ws);
     BNH_HIP(hipGetLastError());
     return 0;
   }

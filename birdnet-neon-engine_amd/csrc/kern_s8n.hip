@@ -23,6 +23,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct bnh_q8w {
   int N, K, Kt, Nt, zx, zy, lo, hi;
+  int all_s1;         // every shift in 1..31: the epilogues need only the one-rounding form
   int8_t *w;          // [Nt][Kt], zero past K (Kt = K rounded up to 64) and past N
   int32_t *bias_eff;  // [Nt]: bias[n] - zx * sum_k w[n][k] (wrapping int32)
   int32_t *mult, *shift;
@@ -687,14 +688,12 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) acc[t][jj] = (v4i){0, 0, 0, 0};
   for (int gs = 0; gs < RQ4_NST - 1 && gs < total; gs++) issue(gs);
-  int last_epi = -RQ4_NST;  // the step whose end ran the latest epilogue
   for (int gs = 0; gs < total; gs++) {
     // this wave's loads of step gs have landed once at most the RQ4_NLD loads of each of the RQ4_NST - 2 later steps
-    // are outstanding, and in the RQ4_NST - 1 steps after an epilogue its 8 stores as well (vector-memory
-    // operations retire in issue order; every epilogue issues exactly 8 store instructions per wave)
+    // are outstanding (loads retire in issue order; the count leaves out the epilogue's stores, which may retire
+    // before older loads, so a pending store only lengthens the wait)
     if (gs + RQ4_NST - 2 >= total) RQ_WAIT_VM(0);
-    else if (gs - last_epi <= RQ4_NST - 1) RQ_WAIT_VM(16);  // RQ4_NLD * (RQ4_NST - 2) + 8
-    else RQ_WAIT_VM(8);                                     // RQ4_NLD * (RQ4_NST - 2)
+    else RQ_WAIT_VM(8);  // RQ4_NLD * (RQ4_NST - 2)
     RQ_BARRIER();  // every wave's loads of step gs have landed; the stage step gs - 1 used is no longer read
     if (gs + RQ4_NST - 1 < total) issue(gs + RQ4_NST - 1);
     const lds_i8 *st = lds + (gs % RQ4_NST) * RQ4_STAGE;
@@ -764,8 +763,209 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant4(const int8_t *__res
       }
       RQ_BARRIER();
     }
-    last_epi = gs;
   }
+}
+
+// Version 5 (M % 16 == 0, 16-byte aligned output rows): the tiles, ring, LDS layouts and DMA roles of version 4,
+// with the 8 waves in two ping-pong groups. Waves 0-3 (group 0) and 4-7 (group 1) put one wave of each group on every
+// SIMD; the wave of group g owns pixels 128 g + 64 ((wave % 4) / 2) .. + 63 x channels 128 (wave % 2) .. + 127 of the
+// tile. Each K step is a memory phase (the DMA three steps ahead, the step's 12 fragments into registers) then a
+// compute phase (32 MFMAs), with a block barrier after each phase; group 1 starts one barrier late, so one group's
+// fragment reads and waits overlap the other group's MFMAs. Step s is read by group 0 in interval 2s and by group 1
+// in interval 2s + 1; the DMA of step s + 3 (issued in interval 2s or 2s + 1) refills the stage of step s - 1, last
+// read in interval 2s - 1; every wave waits for its DMA of step s + 1 (vmcnt, counting only the loads issued after
+// it) before the barrier that opens interval 2s + 2.
+//   A tile's epilogue runs in the memory phase after its last compute phase and touches no LDS but the channel
+// vectors: the 128 sums are requantised into 32 words (4 pixels each), a 4 x 4 word transpose across the lanes of
+// each channel (permlane swaps) gives every lane 16 consecutive pixels of one channel, and each wave stores 8 x 16
+// bytes per lane, 64 contiguous bytes per channel row.
+BNH_DEV void rq_sync() {
+  __builtin_amdgcn_sched_barrier(0);
+  RQ_BARRIER();
+  __builtin_amdgcn_sched_barrier(0);
+}
+// this wave's DMA of step s + 1 has landed: at most the loads of the (up to two) steps issued after it are pending
+BNH_DEV void rq_wait_next(int total, int s) {
+  const int later = total - 2 - s;
+  if (later >= 2) RQ_WAIT_VM(8);
+  else if (later == 1) RQ_WAIT_VM(4);
+  else RQ_WAIT_VM(0);
+}
+// w[t] of lane (c, q) (c = lane % 16, q = lane / 16) -> w[i] of lane (c, q) = the old w[q] of lane (c, i)
+BNH_DEV void rq_transpose_rows(uint32_t w[4]) {
+  const auto p = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);  // rows 2, 3 of w0 <-> rows 0, 1 of w2
+  const auto q = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  const auto r = __builtin_amdgcn_permlane16_swap(p[0], q[0], false, false);  // rows 1, 3 of w0 <-> rows 0, 2 of w1
+  const auto u = __builtin_amdgcn_permlane16_swap(p[1], q[1], false, false);
+  w[0] = r[0];
+  w[1] = r[1];
+  w[2] = u[0];
+  w[3] = u[1];
+}
+
+template <bool ALL_S1>  // every channel's shift is in 1..31
+__global__ __launch_bounds__(512, 1) void k_gemm_s8_requant_pp(const int8_t *__restrict__ x, long long x_ws, int M,
+                                                              int K, int Kt, int tpw, int nblk, int ntiles,
+                                                              const int8_t *__restrict__ wt,
+                                                              const int32_t *__restrict__ bias_eff,
+                                                              const int32_t *__restrict__ mult,
+                                                              const int32_t *__restrict__ shift, int N, int zy, int lo,
+                                                              int hi, int8_t *__restrict__ out, long long out_ws) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds_raw[RQ4_NST * RQ4_STAGE];
+  __shared__ int32_t s_chan[3 * RQ4_MAXNT];
+  lds_i8 *lds = (lds_i8 *)lds_raw;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wm = 2 * grp + ((wave & 3) >> 1), wn = wave & 1;
+  const int steps = Kt / RQ4_BK;
+  for (int i = tid; i < nblk * RQ4_CH; i += 512) {
+    s_chan[i] = bias_eff[i];
+    s_chan[RQ4_MAXNT + i] = mult[i];
+    s_chan[2 * RQ4_MAXNT + i] = shift[i];
+  }
+  __syncthreads();
+  const int rot = (int)(blockIdx.x % steps);
+  const int mytiles = ntiles > (int)blockIdx.x ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int total = mytiles * steps;
+  const int xr = lane >> 4, xslot = lane & 15;
+  const int wrow = lane >> 2, wchunk = (lane & 3) ^ ((lane >> 3) & 3);
+  const bool whole = K % RQ4_BK == 0 && M % RQ4_PIX == 0;
+  uint32_t xoff[2], woff[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int q = 2 * wave + h, row = 4 * q + xr;
+    xoff[h] = (uint32_t)(row * M + 16 * (xslot ^ (row & 7)));
+    woff[h] = (uint32_t)((16 * q + wrow) * Kt + 16 * wchunk);
+  }
+  int iss = 0;  // the next step to issue
+  auto issue = [&]() {
+    const int gs = iss++;
+    const int t = (int)blockIdx.x + (gs / steps) * (int)gridDim.x;
+    int s = gs % steps + rot;
+    if (s >= steps) s -= steps;
+    const int cb = t % nblk, rest = t / nblk, p0 = (rest % tpw) * RQ4_PIX, win = rest / tpw;
+    const int8_t *xw = x + win * x_ws;
+    lds_i8 *st = lds + (gs % RQ4_NST) * RQ4_STAGE;
+    if (whole) {
+      const int8_t *xb = xw + (long long)s * RQ4_BK * M + p0, *wb = wt + (long long)cb * RQ4_CH * Kt + s * RQ4_BK;
+#pragma unroll
+      for (int h = 0; h < 2; h++) rq_dma16s(xb, xoff[h], st + (2 * wave + h) * 1024);
+#pragma unroll
+      for (int h = 0; h < 2; h++) rq_dma16s(wb, woff[h], st + RQ4_XB + (2 * wave + h) * 1024);
+      return;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int q = 2 * wave + h, row = 4 * q + xr;
+      int k = s * RQ4_BK + row;
+      if (k > K - 1) k = K - 1;
+      int px = p0 + 16 * (xslot ^ (row & 7));
+      if (px > M - 16) px = M - 16;
+      rq_dma16(xw + (long long)k * M + px, st + q * 1024);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int q = 2 * wave + h;
+      rq_dma16(wt + (long long)(cb * RQ4_CH + 16 * q + wrow) * Kt + s * RQ4_BK + 16 * wchunk, st + RQ4_XB + q * 1024);
+    }
+  };
+  const int g = lane >> 4, j = lane & 15;
+  int aoff[4][2], boff[8];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+      const int r = 16 * g + 8 * hf + (j >> 1), c = 4 * wm + t;
+      aoff[t][hf] = r * RQ4_PIX + 16 * (c ^ (j >> 1)) + 8 * (j & 1);
+    }
+#pragma unroll
+  for (int jj = 0; jj < 8; jj++) {
+    const int n = wn * 128 + 16 * jj + j;
+    boff[jj] = RQ4_XB + n * 64 + 16 * (g ^ ((n >> 1) & 3));
+  }
+  v4i acc[4][8];
+  // tile i's outputs: acc[tt][jj][r] is pixel wm 64 + 16 tt + 4 g + r, channel wn 128 + 16 jj + j of the tile
+  auto epilogue = [&](int i) {
+    const int t = (int)blockIdx.x + i * (int)gridDim.x;
+    const int cb = t % nblk, rest = t / nblk, p0 = (rest % tpw) * RQ4_PIX, win = rest / tpw;
+    // the window's output as a buffer: stores past it are dropped, so every wave issues the same 8 stores
+    const __amdgpu_buffer_rsrc_t orr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(out + win * out_ws), 0, N * M, 0x00020000);
+    const int p = p0 + wm * 64 + 16 * g;  // this lane's 16 pixels after the transpose
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int nl = wn * 128 + 16 * jj + j, n = cb * RQ4_CH + nl;  // < Nt: the channel vectors are padded to Nt
+      const int32_t be = s_chan[n], mu = s_chan[RQ4_MAXNT + n], sh = s_chan[2 * RQ4_MAXNT + n];
+      const bool s1 = ALL_S1 || (sh >= 1 && sh <= 31);
+      const BnhRqS1 rc = bnh_rq_s1(s1 ? sh : 1);
+      uint32_t w[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; tt++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int32_t a32 = (int32_t)((uint32_t)acc[tt][jj][r] + (uint32_t)be);
+          const int32_t y = s1 ? bnh_requant_s1(a32, mu, rc, zy, lo, hi) : bnh_requant(a32, mu, sh, zy, lo, hi);
+          word |= ((uint32_t)y & 0xffu) << (8 * r);
+        }
+        w[tt] = word;
+      }
+      rq_transpose_rows(w);
+      const v4i val = (v4i){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      __builtin_amdgcn_raw_buffer_store_b128(val, orr, n < N && p < M ? n * M + p : 0x7ffffff0, 0, 0);
+    }
+  };
+  for (int s = 0; s < RQ4_NST - 1 && s < total; s++) issue();
+  if (total > 2) RQ_WAIT_VM(8);  // step 0 has landed
+  else if (total == 2) RQ_WAIT_VM(4);
+  else RQ_WAIT_VM(0);
+  rq_sync();
+  if (grp) rq_sync();  // group 1 runs one phase behind group 0
+  int ck = 0, ci = 0, done = -1;
+  for (int s = 0; s < total; s++) {
+    asm volatile("" : "+s"(done));  // opaque to the optimiser: no peeled first iteration
+    // ---- memory phase of step s
+    if (s + RQ4_NST - 1 < total) issue();
+    if (done >= 0) {
+      epilogue(done);
+      done = -1;
+    }
+    const lds_i8 *st = lds + (s % RQ4_NST) * RQ4_STAGE;
+    v4i a[4], b[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const v2i lo8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(st + aoff[t][0]));
+      const v2i hi8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(st + aoff[t][1]));
+      a[t] = (v4i){lo8.x, lo8.y, hi8.x, hi8.y};
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) b[jj] = *(const __attribute__((address_space(3))) v4i *)(st + boff[jj]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (grp) rq_wait_next(total, s);
+    rq_sync();
+    // ---- compute phase of step s (a tile's first step starts its sums from zero)
+    if (ck == 0) {
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++)
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[jj], (v4i){0, 0, 0, 0}, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[jj], acc[t][jj], 0, 0, 0);
+    }
+    if (++ck == steps) {
+      done = ci;
+      ck = 0;
+      ci++;
+    }
+    if (!grp) rq_wait_next(total, s);
+    rq_sync();
+  }
+  if (done >= 0) epilogue(done);
+  if (!grp) rq_sync();  // every wave passes the same number of barriers
 }
 
 // requant arithmetic check: y[i] = bnh_requant(acc[i], mult[i], shift[i], zy, lo, hi), where for shift 1..31 the
@@ -980,6 +1180,8 @@ bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const i
     hs[n] = shift[n];
   }
   W->N = N; W->K = K; W->Kt = Kt; W->Nt = Nt; W->zx = zx; W->zy = zy; W->lo = lo; W->hi = hi;
+  W->all_s1 = 1;
+  for (int n = 0; n < N; n++) W->all_s1 &= shift[n] >= 1;
   bool ok = (W->w = (int8_t *)bnh_malloc((size_t)Nt * Kt)) && (W->bias_eff = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
             (W->mult = (int32_t *)bnh_malloc(4 * (size_t)Nt)) && (W->shift = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
             !bnh_memcpy_h2d(W->w, hw, (size_t)Nt * Kt) && !bnh_memcpy_h2d(W->bias_eff, hb, 4 * (size_t)Nt) &&
@@ -1017,8 +1219,15 @@ int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M
     const long long nt = (long long)tpw * nblk * B;
     BNH_REQ(nt < (1LL << 31));
     const int grid = (int)(nt < ncu ? nt : ncu);
-    hipLaunchKernelGGL(k_gemm_s8_requant4, dim3(grid), dim3(512), 0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt,
-                       W->w, W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
+    // the ping-pong form stores 16 bytes per lane: 16-byte aligned output rows
+    static const bool v4 = getenv("BNH_RQ_V4") != nullptr;  // version 4, for comparison
+    if (!v4 && ((uintptr_t)out & 15) == 0 && (B == 1 || out_ws % 16 == 0))
+      hipLaunchKernelGGL(W->all_s1 ? k_gemm_s8_requant_pp<true> : k_gemm_s8_requant_pp<false>, dim3(grid), dim3(512),
+                         0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt, W->w, W->bias_eff, W->mult, W->shift,
+                         W->N, W->zy, W->lo, W->hi, out, out_ws);
+    else
+      hipLaunchKernelGGL(k_gemm_s8_requant4, dim3(grid), dim3(512), 0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt,
+                         W->w, W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
   } else {
     const int tpw = (int)bnh_ceil_div(M, RQ2_PIX);
     dim3 grid((unsigned)((long long)tpw * B), (unsigned)(W->Nt / RQ2_CH));

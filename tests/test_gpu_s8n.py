@@ -309,6 +309,31 @@ def test_gemm_requant_ring_kernel_shapes(hip):
             assert not got[b, N * M:].any()   # nothing written past the window's output
 
 
+def test_gemm_requant_output_rows_4_byte_aligned(hip):
+    """Window output strides that are multiples of 4 but not of 16: the ring kernel whose epilogue stages the tile in
+    LDS and stores whole rows (the ping-pong kernel stores 16 bytes per lane and needs 16-byte aligned rows)."""
+    H = hip
+    rng = np.random.default_rng(78)
+    for (N, K, M, B) in ((24, 48, 144, 3), (256, 1152, 512, 2)):
+        w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+        x = rng.integers(-128, 128, (B, K, M)).astype(np.int8)
+        bias = rng.integers(-2 ** 20, 2 ** 20, N).astype(np.int32)
+        mult = rng.integers(2 ** 30, 2 ** 31, N).astype(np.int32)
+        shift = rng.integers(1, 16, N).astype(np.int32)
+        Wq = H.Q8Weights(w, bias, mult, shift, -7, 4, -120, 127)
+        o_ws = N * M + 4
+        dx = H.DeviceArray.from_host(x)
+        dout = H.DeviceArray.zeros((B, o_ws), np.int8)
+        say("requant 4-byte rows", N, K, M, B)
+        H.check(H.lib().bnh_gemm_s8_requant(Wq.h, dx.ptr, K * M, M, B, dout.ptr, o_ws, None), "requant")
+        H.sync()
+        got = dout.numpy()
+        for b in range(B):
+            ref = O.gemm_s8_requant(w, x[b], bias, mult, shift, -7, 4, -120, 127)
+            assert np.array_equal(got[b, :N * M].reshape(N, M), ref), (N, K, M, b)
+            assert not got[b, N * M:].any()
+
+
 def test_requant_arithmetic_edges(hip):
     """The device's closed-form Q31 requantisation against the oracle's
     textbook SaturatingRoundingDoublingHighMul + RoundingDivideByPOT on the
