@@ -177,7 +177,7 @@ def cpu_baseline_pw_s8(pk, rng):
 
 def gemm_s8_leg(H, rng, B, stream, steps, warmup, check_windows=(0, -1)):
     """The int8 pointwise GEMM of the second half of the metric: 1152 -> 256 channels over 24 x 64 pixels per window,
-    int8 NCHW activations with zero point -128, per-channel Q31 requant (k_gemm_s8_requant4), B windows per launch,
+    int8 NCHW activations with zero point -128, per-channel Q31 requant (k_gemm_s8_requant_pp), B windows per launch,
     timed with events on `stream`; windows check_windows of the batch are compared with the oracle bit for bit."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as O
@@ -197,7 +197,7 @@ def gemm_s8_leg(H, rng, B, stream, steps, warmup, check_windows=(0, -1)):
     ops = 2.0 * B * M * N * K
     tops = ops / (ms * 1e-3) / 1e12
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"kernel": "k_gemm_s8_requant4",
+    return {"kernel": "k_gemm_s8_requant_pp",
             "launch": f"int8 1x1 conv {K}->{N} over 24x64 px x {B} windows, NCHW, Q31 requant, int8 out",
             "ms_per_launch": round(ms, 4), "tops": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
             "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -322,7 +322,7 @@ def main():
         bytes_per_launch = B * (K * M + N * M) + N * K + 3 * 4 * N
         workload = ("int8 pointwise conv 1152->256 over 24x64 pixels per window, NCHW int8 "
                     "activations (zero point -128), per-channel Q31 requant, int8 out")
-        kernel = "k_gemm_s8_requant4"
+        kernel = "k_gemm_s8_requant_pp"
         dtype = "int8"
     else:
         sys.path.insert(0, os.path.join(ROOT, "birdnet-neon-engine_amd"))
@@ -567,7 +567,7 @@ def cpu_baseline_qpw(x, g, w, bias, Hh, W):
 def run_proto(a, H, rng, B, stream):
     """The int8 prototype head (PROTO_S8) at Perch v2's shape: per window 64 cells of 1536 channels (fp32, as the
     body leaves them) against 14,795 classes x 4 prototypes. Timed: cell quantization + column-max GEMM + logits per
-    step; the column-max GEMM (k_proto_gemm64, the MFMA-bound kernel) also alone, for the roofline."""
+    step; the column-max GEMM (k_proto_gemm_pp, the MFMA-bound kernel) also alone, for the roofline."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as O
     from bnneon import s8pack
@@ -622,7 +622,7 @@ def run_proto(a, H, rng, B, stream):
                    "global_batch": B, "parallelism": "1 GPU, windows batched per launch",
                    "wall_s_timed_region": round(wall, 4)},
         "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                     "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None, "kernel": "k_proto_gemm64",
+                     "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None, "kernel": "k_proto_gemm_pp",
                      "ms_per_launch": round(ms_gemm, 4), "ops_per_launch": int(ops),
                      "algorithmic_bytes_per_launch": B * P * (Kp + 4) + Np * (Kp + 4) + B * Np * 4},
     }
