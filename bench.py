@@ -423,9 +423,26 @@ def run_dw(a, H, rng, B, stream):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
                      "algorithmic_bytes_per_launch": bytes_per_launch},
     }
+    line["parity_windows"] = dw_parity(dout.numpy(), d, kind, C, Hh, W, k, s, (0, B - 1))
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_dw(d, kind, C, Hh, W, k, s)
     print(json.dumps(line), flush=True)
+
+
+def dw_parity(got, d, kind, C, H, W, k, s, wins):
+    """The batch's outputs of windows `wins` against the oracle's depthwise kernel, bit for bit."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    ok = []
+    for i in wins:
+        if kind == "f16":
+            ref = O.dwk_f16(d["x"][i], H, W, C, k, s, d["pt"], d["pl"], d["w"], d["b"], 1, d["Ho"], d["Wo"])[0]
+            ok.append(bool(np.array_equal(got[i].view(np.uint16), ref.reshape(-1).view(np.uint16))))
+        else:
+            ref = O.dw_s8(d["x"][i], k, s, d["pt"], d["pl"], d["w"], d["bias"], d["mult"], d["shift"], -128, -128,
+                          -128, 127, d["lut"], d["Ho"], d["Wo"])
+            ok.append(bool(np.array_equal(got[i], ref.reshape(-1))))
+    return f"{sum(ok)}/{len(ok)} bit-exact vs the oracle (windows {list(wins)})"
 
 
 def cpu_baseline_wino(xp, w, b):
@@ -481,6 +498,18 @@ def run_wino(a, H, rng, B, stream):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_wino_f16",
                      "algorithmic_bytes_per_launch": bytes_per_launch},
     }
+    got = dout.numpy().reshape(B, Hh, W, K).astype(np.float64)
+    u = 2.0 ** -11
+    worst = 0.0
+    for i in (0, B - 1):
+        x64 = xp[i].astype(np.float64)
+        cols = np.stack([x64[ky:ky + Hh, kx:kx + W] for ky in range(3) for kx in range(3)], axis=2)
+        y = (cols.reshape(Hh * W, -1) @ w.reshape(K, -1).T.astype(np.float64) + b).reshape(Hh, W, K)
+        y = y / (1 + np.exp(-y))
+        worst = max(worst, float(np.abs(got[i] - y).max() / (8 * u * np.abs(y).max())))
+    line["parity_windows"] = (f"windows [0, {B - 1}] against a float64 direct conv + SiLU: max |error| = "
+                              f"{worst:.3f} x the stated whole-output bound 8 u max|y| (u = 2^-11)"
+                              + (" (within)" if worst <= 1.0 else " (EXCEEDED)"))
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_wino(xp, w, b)
     L.bnh_wino16_free(P)
@@ -883,9 +912,27 @@ def run_v24(a, H, rng, B, stream):
                                                                       "fp16-MFMA 1x1 convs")
     line["roofline"] = v24_roofline(H, vn, B, stream, a)
     m.close()
+    line["parity_windows"] = v24_parity(vn, pcm, dout.numpy(), nc, (0, B - 1), a.f16_mfma)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_v24(vn, rng)
     print(json.dumps(line), flush=True)
+
+
+def v24_parity(vn, pcm, logits, nc, wins, f16_mfma):
+    """The batch's logits of windows `wins` against the oracle's op-by-op run of the package: bit for bit for the
+    exact path; for the fp16-MFMA form, the largest logit difference and top-1 agreement."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_net
+    on = oracle_net.OracleNet(vn.net, 0, vn.net.last, vn.emb_buf)
+    refs = [on.run(pcm[i])[0][:nc].copy() for i in wins]
+    if not f16_mfma:
+        same = sum(bool(np.array_equal(logits[i].view(np.uint32), r.view(np.uint32))) for i, r in zip(wins, refs))
+        return f"{same}/{len(wins)} windows' logits bit-identical to the oracle's (windows {list(wins)})"
+    d = max(float(np.abs(logits[i] - r).max()) for i, r in zip(wins, refs))
+    top = sum(int(np.argmax(logits[i]) == np.argmax(r)) for i, r in zip(wins, refs))
+    rng_ = max(float(r.max() - r.min()) for r in refs)
+    return (f"windows {list(wins)} against the oracle's exact path: max |logit difference| {d:.3g} of a "
+            f"{rng_:.3g} logit range, top-1 {top}/{len(wins)}")
 
 
 FP16_MFMA_PEAK_TFLOPS = 2500.0
