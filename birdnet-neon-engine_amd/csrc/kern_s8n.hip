@@ -27,6 +27,12 @@ struct bnh_q8w {
   int8_t *w;          // [Nt][Kt], zero past K (Kt = K rounded up to 64) and past N
   int32_t *bias_eff;  // [Nt]: bias[n] - zx * sum_k w[n][k] (wrapping int32)
   int32_t *mult, *shift;
+  // the short epilogue (every shift in 1..31, zy <= lo, and |bias_eff| + K 2^14 < 2^31 so that acc + bias_eff never
+  // wraps): cq[n] = bias_eff[n] mult[n] + 2^30 + 2^(30 + shift[n]) and e1[n] = shift[n] - 1, so a requantised output
+  // is zy + clamp((acc mult + cq) >> (32 + e1), lo - zy, hi - zy)
+  int fast;
+  int32_t *cq;  // [2 Nt]: the low words of cq, then the high words
+  int32_t *e1;
 };
 
 struct EpiDev {  // the fp32 epilogue, by value into the kernel
@@ -968,6 +974,235 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant_pp(const int8_t *__r
   if (!grp) rq_sync();  // every wave passes the same number of barriers
 }
 
+// Version 6 (split rings): version 5's tiles, wave roles, phases and epilogue, with the activations and the weights
+// in LDS rings of their own, each filled by one group: group 0 (waves 0-3) issues the activation DMA XST - 1 steps
+// ahead, group 1 (waves 4-7) the weight DMA WST - 1 steps ahead. A wave's vmcnt counts only its own loads, so the
+// weight loads (L2 hits) never hold up an activation wait, and XST stages of 16 KB keep (XST - 1) x 16 KB of HBM reads
+// in flight per CU where version 5's shared ring holds 3 x 16 KB.
+//   Step s is read by group 0 in interval 2s and by group 1 in interval 2s + 1. The activation DMA of step s + XST - 1
+// (group 0, interval 2s) refills the stage of step s - 1, last read in interval 2s - 1; the weight DMA of step
+// s + WST - 1 (group 1, interval 2s + 1) refills the stage of step s - 1 as well (WST >= 3: the weights of step s + 1
+// are read in interval 2s + 2). Each wave waits for its own DMA of step s + 1 before the barrier that opens interval
+// 2s + 2; a wave's epilogue stores are counted by the same vmcnt and can only lengthen that wait.
+//   Measured at 1152 -> 256 channels over 1536 pixels x 256 windows, deeper activation rings (6 + 3, 5 + 4 stages) ran
+// slower than 4 + 4, so the launcher instantiates 4 + 4.
+//   The short epilogue (EPI 2, bnh_q8w::fast) needs no sign test: when zy <= lo a negative product requantises to
+// lo under either rounding of its sign, so every output is zy + clamp(hi32(acc mult + cq) >> e1, lo - zy, hi - zy)
+// (one 64-bit multiply-add, a shift and a median per output; zy added to four packed bytes at once), about 5 VALU
+// instructions per output where the general form takes about 12.
+#define RQ6_SB 16384  // one stage of either ring: 64 k rows x 256 pixels, or 256 channels x 64 k
+template <int N>
+BNH_DEV void rq_wait_vm_steps(int later) {  // at most `later` steps of N loads each outstanding (later in 0..4)
+  static_assert(N == 4, "four DMA instructions per wave and step");
+  if (later >= 4) RQ_WAIT_VM(16);
+  else if (later == 3) RQ_WAIT_VM(12);
+  else if (later == 2) RQ_WAIT_VM(8);
+  else if (later == 1) RQ_WAIT_VM(4);
+  else RQ_WAIT_VM(0);
+}
+
+template <int EPI, int XST, int WST>  // EPI: 0 any shift, 1 shifts 1..31, 2 the short epilogue (bnh_q8w::fast)
+__global__ __launch_bounds__(512, 1) void k_gemm_s8_requant_sr(const int8_t *__restrict__ x, long long x_ws, int M,
+                                                              int K, int Kt, int tpw, int nblk, int ntiles,
+                                                              const int8_t *__restrict__ wt,
+                                                              const int32_t *__restrict__ bias_eff,
+                                                              const int32_t *__restrict__ mult,
+                                                              const int32_t *__restrict__ shift, int N, int zy, int lo,
+                                                              int hi, int8_t *__restrict__ out, long long out_ws,
+                                                              const int32_t *__restrict__ cq,
+                                                              const int32_t *__restrict__ e1v) {
+  static_assert(WST >= 3 && XST >= 2 && XST - 2 <= 4 && WST - 2 <= 4, "ring depths");
+  __shared__ __attribute__((aligned(1024))) int8_t lds_raw[(XST + WST) * RQ6_SB];
+  __shared__ int32_t s_chan[4 * RQ4_MAXNT];
+  lds_i8 *xlds = (lds_i8 *)lds_raw, *wlds = xlds + XST * RQ6_SB;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wq = wave & 3, wm = 2 * grp + (wq >> 1), wn = wave & 1;
+  const int steps = Kt / RQ4_BK;
+  const int Nt = nblk * RQ4_CH;
+  for (int i = tid; i < Nt; i += 512) {
+    if (EPI == 2) {
+      s_chan[i] = cq[i];
+      s_chan[RQ4_MAXNT + i] = cq[Nt + i];
+      s_chan[3 * RQ4_MAXNT + i] = e1v[i];
+    } else {
+      s_chan[i] = bias_eff[i];
+      s_chan[3 * RQ4_MAXNT + i] = shift[i];
+    }
+    s_chan[2 * RQ4_MAXNT + i] = mult[i];
+  }
+  __syncthreads();
+  const int rot = (int)(blockIdx.x % steps);
+  const int mytiles = ntiles > (int)blockIdx.x ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int total = mytiles * steps;
+  // the short epilogue's output bytes: c = clamp(v, lo - zy, hi - zy) in 0..255, then c + zy in each byte of a word
+  // of four (a carry-free bytewise add)
+  const int lz = lo - zy, hz = hi - zy;
+  const uint32_t zb = (uint32_t)(zy & 0xff) * 0x01010101u, zb7 = zb & 0x7f7f7f7fu;
+  const int nst = grp ? WST : XST;  // this wave's ring
+  // this wave's 4 DMA instructions of a step, q = 4 (wave % 4) + h. Group 0: activation instruction q fills k rows
+  // 4q .. 4q + 3, lane -> row 4q + lane / 16, its 16-byte slot lane % 16 holding pixel column (lane % 16) ^ (row % 8).
+  // Group 1: weight instruction q fills channel rows 16q .. 16q + 15, lane -> row 16q + lane / 4, its slot lane % 4
+  // holding k chunk (lane % 4) ^ ((lane / 8) % 4).
+  const int xr = lane >> 4, xslot = lane & 15;
+  const int wrow = lane >> 2, wchunk = (lane & 3) ^ ((lane >> 3) & 3);
+  const bool whole = K % RQ4_BK == 0 && M % RQ4_PIX == 0;
+  uint32_t doff[4];
+#pragma unroll
+  for (int h = 0; h < 4; h++) {
+    const int q = 4 * wq + h, row = 4 * q + xr;
+    doff[h] = grp ? (uint32_t)((16 * q + wrow) * Kt + 16 * wchunk) : (uint32_t)(row * M + 16 * (xslot ^ (row & 7)));
+  }
+  int iss = 0;  // the next step this wave issues
+  auto issue = [&]() {
+    const int gs = iss++;
+    const int t = (int)blockIdx.x + (gs / steps) * (int)gridDim.x;
+    const int cb = t % nblk, rest = t / nblk, p0 = (rest % tpw) * RQ4_PIX, win = rest / tpw;
+    int s = gs % steps + rot;
+    if (s >= steps) s -= steps;
+    if (grp) {  // weights: padded to Nt x Kt, never clamped
+      lds_i8 *st = wlds + (gs % WST) * RQ6_SB;
+      const int8_t *wb = wt + (long long)cb * RQ4_CH * Kt + s * RQ4_BK;
+#pragma unroll
+      for (int h = 0; h < 4; h++) rq_dma16s(wb, doff[h], st + (4 * wq + h) * 1024);
+      return;
+    }
+    lds_i8 *st = xlds + (gs % XST) * RQ6_SB;
+    const int8_t *xw = x + win * x_ws;
+    if (whole) {
+      const int8_t *xb = xw + (long long)s * RQ4_BK * M + p0;
+#pragma unroll
+      for (int h = 0; h < 4; h++) rq_dma16s(xb, doff[h], st + (4 * wq + h) * 1024);
+      return;
+    }
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+      const int q = 4 * wq + h, row = 4 * q + xr;
+      int k = s * RQ4_BK + row;
+      if (k > K - 1) k = K - 1;
+      int px = p0 + 16 * (xslot ^ (row & 7));
+      if (px > M - 16) px = M - 16;
+      rq_dma16(xw + (long long)k * M + px, st + q * 1024);
+    }
+  };
+  const int g = lane >> 4, j = lane & 15;
+  int aoff[4][2], boff[8];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+      const int r = 16 * g + 8 * hf + (j >> 1), c = 4 * wm + t;
+      aoff[t][hf] = r * RQ4_PIX + 16 * (c ^ (j >> 1)) + 8 * (j & 1);
+    }
+#pragma unroll
+  for (int jj = 0; jj < 8; jj++) {
+    const int n = wn * 128 + 16 * jj + j;
+    boff[jj] = n * 64 + 16 * (g ^ ((n >> 1) & 3));
+  }
+  v4i acc[4][8];
+  // tile i's outputs: acc[tt][jj][r] is pixel wm 64 + 16 tt + 4 g + r, channel wn 128 + 16 jj + j of the tile
+  auto epilogue = [&](int i) {
+    const int t = (int)blockIdx.x + i * (int)gridDim.x;
+    const int cb = t % nblk, rest = t / nblk, p0 = (rest % tpw) * RQ4_PIX, win = rest / tpw;
+    const __amdgpu_buffer_rsrc_t orr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(out + win * out_ws), 0, N * M, 0x00020000);
+    const int p = p0 + wm * 64 + 16 * g;  // this lane's 16 pixels after the transpose
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int nl = wn * 128 + 16 * jj + j, n = cb * RQ4_CH + nl;
+      const int32_t mu = s_chan[2 * RQ4_MAXNT + n];
+      uint32_t w[4];
+      if (EPI == 2) {
+        const int64_t c = (int64_t)(((uint64_t)(uint32_t)s_chan[RQ4_MAXNT + n] << 32) | (uint32_t)s_chan[n]);
+        const int e1 = s_chan[3 * RQ4_MAXNT + n];
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int32_t v = (int32_t)(((int64_t)acc[tt][jj][r] * mu + c) >> 32) >> e1;
+            int32_t cl;
+            asm("v_med3_i32 %0, %1, %2, %3" : "=v"(cl) : "v"(v), "v"(lz), "v"(hz));
+            word |= (uint32_t)cl << (8 * r);
+          }
+          w[tt] = ((word & 0x7f7f7f7fu) + zb7) ^ ((word ^ zb) & 0x80808080u);
+        }
+      } else {
+        const int32_t be = s_chan[n], sh = s_chan[3 * RQ4_MAXNT + n];
+        const bool s1 = EPI == 1 || (sh >= 1 && sh <= 31);
+        const BnhRqS1 rc = bnh_rq_s1(s1 ? sh : 1);
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const int32_t a32 = (int32_t)((uint32_t)acc[tt][jj][r] + (uint32_t)be);
+            const int32_t y = s1 ? bnh_requant_s1(a32, mu, rc, zy, lo, hi) : bnh_requant(a32, mu, sh, zy, lo, hi);
+            word |= ((uint32_t)y & 0xffu) << (8 * r);
+          }
+          w[tt] = word;
+        }
+      }
+      rq_transpose_rows(w);
+      const v4i val = (v4i){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      __builtin_amdgcn_raw_buffer_store_b128(val, orr, n < N && p < M ? n * M + p : 0x7ffffff0, 0, 0);
+    }
+  };
+  // prologue: each group issues its ring's first nst - 1 steps and waits for step 0
+  const int pre = nst - 1 < total ? nst - 1 : total;
+  for (int s = 0; s < pre; s++) issue();
+  if (pre > 0) rq_wait_vm_steps<4>(pre - 1);
+  rq_sync();
+  if (grp) rq_sync();  // group 1 runs one phase behind group 0
+  int ck = 0, ci = 0, done = -1;
+  for (int s = 0; s < total; s++) {
+    asm volatile("" : "+s"(done));  // opaque to the optimiser: no peeled first iteration
+    // ---- memory phase of step s
+    if (s + nst - 1 < total) issue();
+    if (done >= 0) {
+      epilogue(done);
+      done = -1;
+    }
+    const lds_i8 *xs = xlds + (s % XST) * RQ6_SB, *ws = wlds + (s % WST) * RQ6_SB;
+    v4i a[4], b[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const v2i lo8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(xs + aoff[t][0]));
+      const v2i hi8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i *)(xs + aoff[t][1]));
+      a[t] = (v4i){lo8.x, lo8.y, hi8.x, hi8.y};
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) b[jj] = *(const __attribute__((address_space(3))) v4i *)(ws + boff[jj]);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // this wave's DMA of step s + 1 has landed once at most the steps it issued after that one are outstanding
+    const int later = (total - 2 - s < nst - 2 ? total - 2 - s : nst - 2);
+    if (grp) rq_wait_vm_steps<4>(later);
+    rq_sync();
+    // ---- compute phase of step s (a tile's first step starts its sums from zero)
+    if (ck == 0) {
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++)
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[jj], (v4i){0, 0, 0, 0}, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[jj], acc[t][jj], 0, 0, 0);
+    }
+    if (++ck == steps) {
+      done = ci;
+      ck = 0;
+      ci++;
+    }
+    if (!grp) rq_wait_vm_steps<4>(later);
+    rq_sync();
+  }
+  if (done >= 0) epilogue(done);
+  if (!grp) rq_sync();  // every wave passes the same number of barriers
+}
+
 // requant arithmetic check: y[i] = bnh_requant(acc[i], mult[i], shift[i], zy, lo, hi), where for shift 1..31 the
 // one-rounding form must agree (INT32_MIN, outside every clamp range, marks a disagreement)
 __global__ void k_eval_requant(const int32_t *__restrict__ acc, const int32_t *__restrict__ mult,
@@ -1182,11 +1417,27 @@ bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const i
   W->N = N; W->K = K; W->Kt = Kt; W->Nt = Nt; W->zx = zx; W->zy = zy; W->lo = lo; W->hi = hi;
   W->all_s1 = 1;
   for (int n = 0; n < N; n++) W->all_s1 &= shift[n] >= 1;
+  W->fast = W->all_s1 && zy <= lo && lo <= hi;
+  for (int n = 0; n < N; n++) W->fast &= llabs((long long)hb[n]) + (long long)K * 16384 < (1LL << 31);
+  int32_t *hc = (int32_t *)calloc(2 * (size_t)Nt, 4), *he = (int32_t *)calloc(Nt, 4);
+  if (!hc || !he) {
+    free(hw); free(hb); free(hm); free(hs); free(hc); free(he); free(W);
+    bnh_fail("bnh_q8w_new: out of host memory");
+    return nullptr;
+  }
+  for (int n = 0; n < N && W->fast; n++) {
+    const uint64_t c = (uint64_t)((int64_t)hb[n] * mult[n] + (1LL << 30) + (1LL << (30 + shift[n])));
+    hc[n] = (int32_t)(uint32_t)c;
+    hc[Nt + n] = (int32_t)(uint32_t)(c >> 32);
+    he[n] = shift[n] - 1;
+  }
   bool ok = (W->w = (int8_t *)bnh_malloc((size_t)Nt * Kt)) && (W->bias_eff = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
             (W->mult = (int32_t *)bnh_malloc(4 * (size_t)Nt)) && (W->shift = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
             !bnh_memcpy_h2d(W->w, hw, (size_t)Nt * Kt) && !bnh_memcpy_h2d(W->bias_eff, hb, 4 * (size_t)Nt) &&
-            !bnh_memcpy_h2d(W->mult, hm, 4 * (size_t)Nt) && !bnh_memcpy_h2d(W->shift, hs, 4 * (size_t)Nt);
-  free(hw); free(hb); free(hm); free(hs);
+            !bnh_memcpy_h2d(W->mult, hm, 4 * (size_t)Nt) && !bnh_memcpy_h2d(W->shift, hs, 4 * (size_t)Nt) &&
+            (W->cq = (int32_t *)bnh_malloc(8 * (size_t)Nt)) && (W->e1 = (int32_t *)bnh_malloc(4 * (size_t)Nt)) &&
+            !bnh_memcpy_h2d(W->cq, hc, 8 * (size_t)Nt) && !bnh_memcpy_h2d(W->e1, he, 4 * (size_t)Nt);
+  free(hw); free(hb); free(hm); free(hs); free(hc); free(he);
   if (!ok) { bnh_q8w_free(W); return nullptr; }
   return W;
 }
@@ -1197,6 +1448,8 @@ void bnh_q8w_free(bnh_q8w *W) {
   if (W->bias_eff) (void)hipFree(W->bias_eff);
   if (W->mult) (void)hipFree(W->mult);
   if (W->shift) (void)hipFree(W->shift);
+  if (W->cq) (void)hipFree(W->cq);
+  if (W->e1) (void)hipFree(W->e1);
   free(W);
 }
 
@@ -1220,12 +1473,20 @@ int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M
     BNH_REQ(nt < (1LL << 31));
     const int grid = (int)(nt < ncu ? nt : ncu);
     // the ping-pong form stores 16 bytes per lane: 16-byte aligned output rows
-    static const bool v4 = getenv("BNH_RQ_V4") != nullptr;  // version 4, for comparison
-    if (!v4 && ((uintptr_t)out & 15) == 0 && (B == 1 || out_ws % 16 == 0))
-      hipLaunchKernelGGL(W->all_s1 ? k_gemm_s8_requant_pp<true> : k_gemm_s8_requant_pp<false>, dim3(grid), dim3(512),
-                         0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt, W->w, W->bias_eff, W->mult, W->shift,
-                         W->N, W->zy, W->lo, W->hi, out, out_ws);
-    else
+    // BNH_RQ_FORM=pp / v4 selects an older form, for comparison
+    static const char *form_env = getenv("BNH_RQ_FORM");
+    static const int form = !form_env ? 6 : !strcmp(form_env, "v4") ? 4 : !strcmp(form_env, "pp") ? 5 : 6;
+    if (form != 4 && ((uintptr_t)out & 15) == 0 && (B == 1 || out_ws % 16 == 0)) {
+      if (form == 5)
+        hipLaunchKernelGGL(W->all_s1 ? k_gemm_s8_requant_pp<true> : k_gemm_s8_requant_pp<false>, dim3(grid), dim3(512),
+                           0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt, W->w, W->bias_eff, W->mult, W->shift,
+                           W->N, W->zy, W->lo, W->hi, out, out_ws);
+      else
+        hipLaunchKernelGGL(W->fast ? k_gemm_s8_requant_sr<2, 4, 4> : W->all_s1 ? k_gemm_s8_requant_sr<1, 4, 4>
+                                                                               : k_gemm_s8_requant_sr<0, 4, 4>,
+                           dim3(grid), dim3(512), 0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt, W->w,
+                           W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws, W->cq, W->e1);
+    } else
       hipLaunchKernelGGL(k_gemm_s8_requant4, dim3(grid), dim3(512), 0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt,
                          W->w, W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
   } else {

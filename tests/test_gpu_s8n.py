@@ -334,6 +334,47 @@ def test_gemm_requant_output_rows_4_byte_aligned(hip):
             assert not got[b, N * M:].any()
 
 
+def test_gemm_requant_short_epilogue(hip):
+    """Output zero points at or below the clamp's low end (zy <= lo) with every shift in 1..31 and bias_eff small
+    enough that acc + bias_eff cannot wrap: the kernel folds bias, rounding and the zero point into one 64-bit
+    multiply-add per output and adds zy bytewise. Covers shifts 1 and 31, negative, zero and extreme multipliers,
+    zy = lo (config 0), zy < lo, zy >= 0 (a bytewise add with no wrap), partial tiles and K tails; then the same data
+    with bias_eff one past the bound, which must take the general path and agree as well."""
+    H = hip
+    rng = np.random.default_rng(31)
+    K_BOUND = 16384
+    cases = ((256, 1152, 1536, 2, -128, -128, 127), (40, 208, 272, 3, -20, -10, 100), (300, 64, 256, 1, -128, -100, 90),
+             (24, 48, 144, 2, 0, 0, 127), (136, 1152, 512, 2, 5, 5, 127))
+    for (N, K, M, B, zy, lo, hi) in cases:
+        zx = -128 if zy == -128 else -3
+        w = rng.integers(-128, 128, (N, K)).astype(np.int8)
+        x = rng.integers(-128, 128, (B, K, M)).astype(np.int8)
+        mult = rng.integers(-2 ** 31, 2 ** 31, N).astype(np.int64)
+        mult[:6] = [2 ** 31 - 1, -2 ** 31, 0, 1, -1, 2 ** 30]
+        mult = mult.astype(np.int32)
+        shift = rng.integers(1, 32, N).astype(np.int32)
+        shift[:4] = [1, 31, 1, 31]
+        cs = w.astype(np.int64).sum(1)
+        room = 2 ** 31 - 1 - K * K_BOUND           # |bias_eff| must stay below this
+        for over in (False, True):
+            be = rng.integers(-room + 1, room, N).astype(np.int64)
+            if over:
+                be[N // 2] = room + 1               # one channel past the bound: the general epilogue
+            bias = (be + zx * cs).astype(np.int64)
+            bias = ((bias + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int32)   # bias_eff = bias - zx cs, wrapping
+            Wq = H.Q8Weights(w, bias, mult, shift, zx, zy, lo, hi)
+            dx = H.DeviceArray.from_host(x)
+            dout = H.DeviceArray.zeros((B, N * M), np.int8)
+            say("requant short epilogue", N, K, M, B, zy, lo, hi, "over" if over else "")
+            H.check(H.lib().bnh_gemm_s8_requant(Wq.h, dx.ptr, K * M, M, B, dout.ptr, N * M, None), "requant")
+            H.sync()
+            got = dout.numpy()
+            for b in range(B):
+                ref = O.gemm_s8_requant(w, x[b], bias, mult, shift, zx, zy, lo, hi)
+                assert np.array_equal(got[b].reshape(N, M), ref), (N, K, M, zy, lo, hi, over, b,
+                                                                   np.argwhere(got[b].reshape(N, M) != ref)[:4])
+
+
 def test_requant_arithmetic_edges(hip):
     """The device's closed-form Q31 requantisation against the oracle's
     textbook SaturatingRoundingDoublingHighMul + RoundingDivideByPOT on the
