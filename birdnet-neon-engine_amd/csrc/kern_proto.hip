@@ -520,185 +520,6 @@ __global__ __launch_bounds__(512, 1) void k_proto_gemm_pp(const int8_t *__restri
   if (!grp) pp_sync();  // every wave passes the same number of barriers
 }
 
-// The same GEMM with software-pipelined fragment reads (8 waves, no phase groups). A wave owns the same 128 cells x
-// 64 prototypes as in the ping-pong form and keeps two register sets of fragments: in iteration s it reads slice
-// s + 1's 12 fragments while its 32 MFMAs of slice s issue, so the LDS latency hides behind the wave's own MFMAs and
-// the other wave of its SIMD. One block barrier per slice:
-//   iteration s: wait for this wave's DMA of slice s + 1; barrier (every wave's DMA of slice s + 1 has landed, and
-//   every wave has consumed its fragments of slice s - 1, read in iteration s - 2); issue the DMA of slice s + 3
-//   into the stage of slice s - 1; on a tile's first slice, the previous tile's epilogue; read slice s + 1's
-//   fragments; the MFMAs of slice s.
-// The epilogue runs after the barrier of the iteration that follows a tile's last slice, so its stores are issued
-// one iteration before the next wait that counts them. The tile's scales use the ping-pong form's double buffer.
-__global__ __launch_bounds__(512, 1) void k_proto_gemm_sp(const int8_t *__restrict__ qa, long long qa_ws,
-                                                         const float *__restrict__ sx, long long sx_ws, int B, int Kp,
-                                                         const int8_t *__restrict__ wt, const float *__restrict__ sw,
-                                                         int Np, int n_mt, int n_nt, float *__restrict__ colmax,
-                                                         long long cm_ws) {
-  __shared__ __attribute__((aligned(1024))) int8_t lds_raw[PG_SCL + 2 * 2048];
-  lds_i8 *lds = (lds_i8 *)lds_raw;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int mh = wave >> 2, wn = wave & 3;
-  const int xcd = (int)(blockIdx.x & 7);
-  PgRegion R;
-  R.lid = (int)(blockIdx.x >> 3);
-  R.nlb = (int)(gridDim.x >> 3);
-  const int gm = n_mt >= 8 ? 8 : n_mt >= 4 ? 4 : n_mt >= 2 ? 2 : 1, gn = 8 / gm;
-  const int rm = xcd / gn, rn = xcd % gn;
-  R.m_lo = rm * n_mt / gm;
-  R.mx = (rm + 1) * n_mt / gm - R.m_lo;
-  R.n_lo = rn * n_nt / gn;
-  const int nx = (rn + 1) * n_nt / gn - R.n_lo;
-  const int xtiles = R.mx * nx;
-  const int mytiles = xtiles > R.lid ? (xtiles - 1 - R.lid) / R.nlb + 1 : 0;
-  const int steps = Kp / PG_BK;
-  // DMA roles as in the ping-pong form: per K slice a wave issues 2 cell instructions (rows 32 wave .. 32 wave + 31
-  // of the tile) and 2 prototype instructions (rows 32 wave .. 32 wave + 31)
-  const int dchunk = 16 * ((lane & 3) ^ ((lane >> 3) & 3));
-  const uint32_t loff_a = (uint32_t)((lane >> 2) * Kp + dchunk);
-  const uint32_t loff_b = (uint32_t)((lane >> 2) * PG_BK + dchunk);
-  const long long a16 = 16LL * Kp, b16 = (long long)(Kp / PG_BK) * 1024;
-  int iss_i = 0, iss_k = 0, iss_st = 0;
-  const int8_t *a_tile = qa, *b_tile = wt;
-  // the lane id computed afresh where a once-per-tile path needs it (volatile: not hoisted out of the loop), so the
-  // values derived from it do not occupy registers through the K loop
-  auto lane_now = []() {
-    int l;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-    return l;
-  };
-  auto issue = [&]() {
-    if (iss_k == 0) {
-      const int lane = lane_now();
-      int m_t, n_t;
-      R.tile(iss_i, m_t, n_t);
-      int win = m_t * 4 + (wave >> 1);
-      if (win > B - 1) win = B - 1;
-      a_tile = qa + (long long)win * qa_ws + (long long)(wave & 1) * 32 * Kp;
-      b_tile = wt + (long long)(n_t * 16 + 2 * wave) * b16;
-      if (wave < 2) {
-        lds_i8 *sc = lds + PG_SCL + (iss_i & 1) * 2048 + wave * 1024;
-        if (wave == 0) {
-          const int last = B - 1 - m_t * 4;
-          const int wl = (lane >> 4) < last ? (lane >> 4) : last;
-          rq_dma16s(sx + (long long)m_t * 4 * sx_ws, (uint32_t)(wl * sx_ws * 4 + 16 * (lane & 15)), sc);
-        } else {
-          rq_dma16s(sw + n_t * PG_TN, (uint32_t)(16 * lane), sc);
-        }
-      }
-    }
-    lds_i8 *st = lds + iss_st * PG_STAGE;
-    const int8_t *ab = a_tile + iss_k * PG_BK, *bb = b_tile + iss_k * 1024;
-#pragma unroll
-    for (int h = 0; h < 2; h++) rq_dma16s(ab + h * a16, loff_a, st + (2 * wave + h) * 1024);
-#pragma unroll
-    for (int h = 0; h < 2; h++) rq_dma16s(bb + h * b16, loff_b, st + PG_AB + (2 * wave + h) * 1024);
-    if (++iss_st == PG_NST) iss_st = 0;
-    if (++iss_k == steps) { iss_k = 0; iss_i++; }
-  };
-  const int g = lane >> 4, j16 = lane & 15;
-  const int foff = j16 * PG_BK + 16 * (g ^ ((j16 >> 1) & 3));
-  const int fa_off = mh * 128 * PG_BK + foff, fb_off = PG_AB + wn * 64 * PG_BK + foff;
-  const int total = mytiles * steps;
-  v4i acc[8][4];
-  // the column maxima of tile i: acc[t][jj][r] is cell row 16 (t % 4) + 4 g + r of window m_t 4 + 2 mh + t / 4,
-  // prototype wn 64 + 16 jj + j16 of the tile
-  auto epilogue = [&](int i) {
-    const int ln = lane_now(), g = ln >> 4, j16 = ln & 15, lane = ln;
-    int m_t, n_t;
-    R.tile(i, m_t, n_t);
-    const lds_f32 *sxs = (const lds_f32 *)(lds + PG_SCL + (i & 1) * 2048);
-    const lds_f32 *sws = sxs + 256;
-#pragma unroll
-    for (int wl = 0; wl < 2; wl++) {
-      const int win = m_t * 4 + mh * 2 + wl;
-#pragma unroll
-      for (int jj = 0; jj < 4; jj++) {
-        float m = -__builtin_inff();
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-          // the cell scales of rows 16 t + 4 g .. + 3, read where they are used (registers are short here)
-          typedef float f4 __attribute__((ext_vector_type(4)));
-          const f4 sr = *(const __attribute__((address_space(3))) f4 *)(sxs + mh * 128 + 64 * wl + 16 * t + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; r++) m = pg_max(m, (float)acc[4 * wl + t][jj][r] * sr[r]);
-        }
-        m = pg_max16(m);
-        const int nl = wn * 64 + 16 * jj + j16, n = n_t * PG_TN + nl;
-        if (lane < 16 && win < B && n < Np) colmax[win * cm_ws + n] = m * sws[nl];
-      }
-    }
-    // the next tile's sums start from zero (the MFMAs always accumulate: no branch between a slice's fragment
-    // reads and its MFMAs, which would make the compiler wait for every LDS read in flight)
-#pragma unroll
-    for (int t = 0; t < 8; t++)
-#pragma unroll
-      for (int jj = 0; jj < 4; jj++) acc[t][jj] = (v4i){0, 0, 0, 0};
-  };
-  v4i a[2][8], b[2][4];
-  auto read_frags = [&](int buf, int stage) {
-    const lds_i8 *st = lds + stage * PG_STAGE;
-    const lds_i8 *pa = st + fa_off, *pb = st + fb_off;
-#pragma unroll
-    for (int t = 0; t < 8; t++) a[buf][t] = *(const lds_v4i *)(pa + t * 1024);
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) b[buf][jj] = *(const lds_v4i *)(pb + jj * 1024);
-  };
-  for (int s = 0; s < PG_NST - 1 && s < total; s++) issue();
-  // slice 0 has landed once at most the loads of the (up to two) later slices are outstanding
-  if (total > 2) RQ_WAIT_VM(8);
-  else if (total == 2) RQ_WAIT_VM(4);
-  else RQ_WAIT_VM(0);
-  pp_sync();
-  if (total > 0) read_frags(0, 0);
-#pragma unroll
-  for (int t = 0; t < 8; t++)
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) acc[t][jj] = (v4i){0, 0, 0, 0};
-  // nothing of the LGKM counter (these fragments, the kernel-argument loads) is pending when the loop starts, so the
-  // compiler's wait before a slice's MFMAs counts only the fragment reads issued just before them
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  int ck = 0, ci = 0, done = -1;
-  for (int s = 0; s < total; s += 2) {
-#pragma unroll
-    for (int h = 0; h < 2; h++) {  // two slices per trip: the fragment buffers alternate at compile-time indices
-      const int ss = s + h;
-      if (ss >= total) break;
-      asm volatile("" : "+s"(done));
-      // this wave's DMA of slice ss + 1 has landed: at most that of slice ss + 2 is outstanding (and, where the
-      // previous iteration ran an epilogue, its stores, which only lengthen the wait)
-      if (ss + 2 < total) RQ_WAIT_VM(4);
-      else RQ_WAIT_VM(0);
-      pp_sync();
-      if (ss + PG_NST - 1 < total) issue();
-      if (done >= 0) {
-        epilogue(done);
-        done = -1;
-      }
-      // slice ss + 1's fragments (past the last slice: a stage's stale bytes, never used), then slice ss's MFMAs,
-      // straight-line so that the MFMAs wait only for the older fragment set
-      read_frags(h ^ 1, (ss + 1) % PG_NST);
-      __builtin_amdgcn_sched_barrier(0);  // the reads issue before the MFMAs, not among their tail
-#pragma unroll
-      for (int jj = 0; jj < 4; jj++)
-#pragma unroll
-        for (int t = 0; t < 8; t++) acc[t][jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[h][t], b[h][jj], acc[t][jj], 0, 0, 0);
-      // the next slice's fragments have landed by now (they were read before these 32 MFMAs issued): say so with a
-      // wait the compiler sees (lgkmcnt(0), no vmcnt / expcnt wait), so that no LDS read is pending at the next
-      // iteration's join points and its MFMAs need no wait for the fragments read just before them
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      if (++ck == steps) {
-        done = ci;
-        ck = 0;
-        ci++;
-      }
-    }
-  }
-  if (done >= 0) epilogue(done);
-}
-
 // ------------------------------------------------------------------ class logits (pc_proto_logits)
 __global__ void k_proto_logits(const float *__restrict__ colmax, long long cm_ws, const float *__restrict__ w,
                                const float *__restrict__ b, int nc, int ppc, float *__restrict__ logits, long long lg_ws,
@@ -821,13 +642,8 @@ int bnh_proto_colmax(const int8_t *qa, long long qa_ws, const float *sx, long lo
     const int n_mt = (int)bnh_ceil_div((long long)B * 64, PG_TM), n_nt = W->Npt / PG_TN;
     int grid = ncu / 8 * 8;  // one block per CU
     if (grid < 8) grid = 8;
-    // BNH_PROTO_FORM=4w / pp selects the 4-wave or the ping-pong form, for comparison
-    static const char *fe = getenv("BNH_PROTO_FORM");
-    static const int form = !fe ? 2 : !strcmp(fe, "4w") ? 0 : !strcmp(fe, "pp") ? 1 : 2;
-    if (form == 2)
-      hipLaunchKernelGGL(k_proto_gemm_sp, dim3((unsigned)grid), dim3(512), 0, bnh_stream(stream), qa, B == 1 ? 0 : qa_ws,
-                         sx, B == 1 ? 0 : sx_ws, B, W->Kp, W->w, W->sw, W->Np, n_mt, n_nt, colmax, B == 1 ? 0 : cm_ws);
-    else if (form == 0)
+    static const bool four = getenv("BNH_PROTO_4W") != nullptr;  // the 4-wave form, for comparison
+    if (four)
       hipLaunchKernelGGL(k_proto_gemm64, dim3((unsigned)grid), dim3(256), 0, bnh_stream(stream), qa, B == 1 ? 0 : qa_ws,
                          sx, B == 1 ? 0 : sx_ws, B, W->Kp, W->w, W->sw, W->Np, n_mt, n_nt, colmax, B == 1 ? 0 : cm_ws);
     else

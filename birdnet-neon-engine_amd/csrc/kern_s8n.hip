@@ -1481,11 +1481,12 @@ int bnh_gemm_s8_requant(const bnh_q8w *W, const int8_t *x, long long x_ws, int M
         hipLaunchKernelGGL(W->all_s1 ? k_gemm_s8_requant_pp<true> : k_gemm_s8_requant_pp<false>, dim3(grid), dim3(512),
                            0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt, W->w, W->bias_eff, W->mult, W->shift,
                            W->N, W->zy, W->lo, W->hi, out, out_ws);
-      else
-        hipLaunchKernelGGL(W->fast ? k_gemm_s8_requant_sr<2, 4, 4> : W->all_s1 ? k_gemm_s8_requant_sr<1, 4, 4>
-                                                                               : k_gemm_s8_requant_sr<0, 4, 4>,
-                           dim3(grid), dim3(512), 0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt, W->w,
+      else {
+        auto k = W->fast ? k_gemm_s8_requant_sr<2, 4, 4> : W->all_s1 ? k_gemm_s8_requant_sr<1, 4, 4>
+                                                                     : k_gemm_s8_requant_sr<0, 4, 4>;
+        hipLaunchKernelGGL(k, dim3(grid), dim3(512), 0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt, W->w,
                            W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws, W->cq, W->e1);
+      }
     } else
       hipLaunchKernelGGL(k_gemm_s8_requant4, dim3(grid), dim3(512), 0, st, x, x_ws, M, W->K, W->Kt, tpw, nblk, (int)nt,
                          W->w, W->bias_eff, W->mult, W->shift, W->N, W->zy, W->lo, W->hi, out, out_ws);
