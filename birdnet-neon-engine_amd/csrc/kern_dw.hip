@@ -1053,9 +1053,12 @@ __global__ __launch_bounds__(256) void k_dw_s8(const int8_t *__restrict__ x, lon
         wsum[ch] = (uint32_t)__builtin_amdgcn_sdot4((int)wp[ky][j][ch], 0x01010101, (int)wsum[ch], false);
     }
   int32_t acc[NP][4];
+  // the short requantisation (below) needs sums that cannot wrap: |bias - zx sum w| + K^2 2^14 < 2^31
+  bool nowrap = true;
 #pragma unroll
   for (int ch = 0; ch < 4; ch++) {
     const int32_t a0 = (int32_t)((uint32_t)bias[c + ch] - (uint32_t)zx * wsum[ch]);
+    nowrap = nowrap && (a0 < 0 ? -(long long)a0 : (long long)a0) + (long long)K * K * 16384 < (1LL << 31);
 #pragma unroll
     for (int q = 0; q < NP; q++) acc[q][ch] = a0;
   }
@@ -1087,7 +1090,26 @@ __global__ __launch_bounds__(256) void k_dw_s8(const int8_t *__restrict__ x, lon
       __builtin_amdgcn_raw_buffer_store_b32(word, orr, o_off, q * C, 0);
     }
   };
-  if (s1) {
+  if (s1 && nowrap && zy <= lo) {
+    // zy <= lo: a negative product requantises to lo under either rounding of its sign, so the one-rounding form
+    // needs no sign test and the zero point moves outside the clamp: zy + clamp(hi32(acc m + 2^30 + 2^(30+e)) >> (e-1),
+    // lo - zy, hi - zy) (|acc m| < 2^62: the shifted value is far from int32's ends, so the saturating add never
+    // saturates)
+    long long a0[4];
+    int e1[4];
+#pragma unroll
+    for (int ch = 0; ch < 4; ch++) {
+      a0[ch] = (1LL << 30) + (1LL << (30 + e[ch]));
+      e1[ch] = e[ch] - 1;
+    }
+    const int lz = lo - zy, hz = hi - zy;
+    store([&](int32_t a, int ch) {
+      const int32_t v = (int32_t)(((long long)a * m[ch] + a0[ch]) >> 32) >> e1[ch];
+      int32_t cl;
+      asm("v_med3_i32 %0, %1, %2, %3" : "=v"(cl) : "v"(v), "v"(lz), "v"(hz));
+      return cl + zy;
+    });
+  } else if (s1) {
     BnhRqS1 rc[4];
 #pragma unroll
     for (int ch = 0; ch < 4; ch++) rc[ch] = bnh_rq_s1(e[ch]);

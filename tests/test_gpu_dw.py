@@ -209,3 +209,51 @@ def test_dw_s8(hip, k, s):
             ref = O.dw_s8(x[i], k, s, pt, pl, w, bias, mult, shift, zx, zy, -100, 120, lut if use_lut else None,
                           Ho, Wo)
             assert np.array_equal(out[i], ref), ("window", i, "lut", use_lut)
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k,s", [(3, 1), (5, 1), (5, 2)])
+def test_dw_s8_short_requant(hip, k, s):
+    """Output zero points at or below the clamp's low end (zy <= lo, config 1: zy = lo = -128) with every shift in
+    1..31 take the kernel's short requantisation (no sign test, the zero point outside the clamp): shifts 1 and 31,
+    negative and extreme multipliers, zy = lo, zy < lo, with and without the SiLU table; then biases past the no-wrap
+    bound on some channels, which must take the general form."""
+    rng = np.random.default_rng(50 + k * 3 + s)
+    B, H, W, C = 2, 24, 64, 672
+    Ho, pt = same_pads(H, k, s)
+    Wo, pl = same_pads(W, k, s)
+    x = rng.integers(-128, 128, (B, H, W, C)).astype(np.int8)
+    w = rng.integers(-128, 128, (k * k, C)).astype(np.int8)
+    mult = rng.integers(-2 ** 31, 2 ** 31, C, dtype=np.int64)
+    mult[:6] = [2 ** 31 - 1, -2 ** 31, 0, 1, -1, 2 ** 30]
+    mult = mult.astype(np.int32)
+    shift = rng.integers(1, 32, C).astype(np.int32)
+    shift[:4] = [1, 31, 1, 31]
+    lut = rng.integers(-128, 128, 256).astype(np.int8)
+    H_ = hip
+    dx = H_.DeviceArray.from_host(x)
+    dwt = H_.DeviceArray.from_host(w)
+    dm, dsh, dl = H_.DeviceArray.from_host(mult), H_.DeviceArray.from_host(shift), H_.DeviceArray.from_host(lut)
+    x_ws, o_ws = H * W * C, Ho * Wo * C
+    for (zx, zy, lo, hi) in ((-128, -128, -128, 127), (7, -20, -10, 100)):
+        wsum = w.astype(np.int64).sum(0)
+        room = 2 ** 31 - 1 - k * k * 16384
+        for over in (False, True):
+            a0 = rng.integers(-room + 1, room, C).astype(np.int64)
+            if over:
+                a0[5::97] = room + 1 + rng.integers(0, 1000, a0[5::97].size)
+            bias = a0 + zx * wsum
+            bias = ((bias + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int32)
+            dbias = H_.DeviceArray.from_host(bias)
+            for use_lut in (False, True):
+                say("dw_s8 short requant k", k, "s", s, "zy", zy, "lo", lo, "over", over, "lut", use_lut)
+                do = H_.DeviceArray.zeros((B, o_ws), np.int8)
+                H_.check(H_.lib().bnh_dw_s8(dx.ptr, x_ws, H, W, C, k, s, pt, pl, dwt.ptr, dbias.ptr, dm.ptr, dsh.ptr,
+                                            zx, zy, lo, hi, dl.ptr if use_lut else None, do.ptr, o_ws, Ho, Wo, B,
+                                            None), "dw_s8")
+                H_.sync()
+                out = do.numpy().reshape(B, Ho, Wo, C)
+                for i in range(B):
+                    ref = O.dw_s8(x[i], k, s, pt, pl, w, bias, mult, shift, zx, zy, lo, hi,
+                                  lut if use_lut else None, Ho, Wo)
+                    assert np.array_equal(out[i], ref), ("window", i, "zy", zy, "over", over, "lut", use_lut,
+                                                         np.argwhere(out[i] != ref)[:4])
