@@ -9,7 +9,11 @@ windows already resident in HBM):
                    through bnn_infer_batch_device: 5 s of 32 kHz audio per
                    window -> log-mel 500 x 128 -> stem -> 26 MBConv blocks
                    (int8 1x1 convs, fp32 depthwise, SE) -> 1536 embedding ->
-                   14,795-class int8 linear head, batch 256 windows.
+                   14,795-class int8 linear head, batch 256 windows. The line
+                   also carries the path's two int8 GEMMs timed on their
+                   own, each checked against the oracle: "gemm_s8" (the
+                   pointwise conv 1152 -> 256 below) and "gemm_s8_proto"
+                   (the prototype head's column-max GEMM below).
   v24_f16          the BirdNET-v2.4-shaped fp16 network end to end through
                    bnn_infer_batch_device: 3 s of 48 kHz audio per window ->
                    log-mel 257 x 96 -> stem -> 16 MBConv blocks (exact fp16
@@ -203,6 +207,57 @@ def gemm_s8_leg(H, rng, B, stream, steps, warmup, check_windows=(0, -1)):
             "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "algorithmic_bytes_per_launch": nbytes, "ops_per_launch": int(ops),
             "parity_windows": f"{sum(ok)}/{len(ok)} bit-exact vs the oracle (windows {list(check_windows)})"}
+
+
+def proto_s8_leg(H, rng, B, stream, steps, warmup):
+    """The int8 prototype head's column-max GEMM (k_proto_gemm_pp) at Perch v2's shape: 64 cells x 1536 channels per
+    window against 59,180 prototypes, B windows per launch, timed with events on `stream` after `warmup` launches;
+    window 0's logits (cell quantization + GEMM + logits) are compared with the oracle bit for bit."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    from bnneon import s8pack
+    P, C, nc, ppc = 64, 1536, 14795, 4
+    N = nc * ppc
+    protos = rng.standard_normal((N, C)).astype(np.float32)
+    clsw = rng.uniform(0, 1, N).astype(np.float32)
+    clsb = (rng.standard_normal(nc) * 0.1).astype(np.float32)
+    Kp, Np = s8pack.r16(C), (N + 3) // 4 * 4
+    q, sw = s8pack.quant_rows_s8(protos)
+    qp = np.zeros((Np, Kp), np.int8)
+    qp[:N, :C] = q
+    swp = np.zeros(Np, np.float32)
+    swp[:N] = sw
+    qw = s8pack.pack_panels(qp)
+    L = H.lib()
+    W = L.bnh_s8p_new(Np, Kp, qw.ctypes.data, swp.ctypes.data)
+    if not W:
+        H.check(None, "bnh_s8p_new")
+    cells = np.maximum(rng.standard_normal((B, P, C)), 0).astype(np.float32)
+    dx = H.DeviceArray.from_host(cells)
+    dqa = H.DeviceArray.zeros((B, P * Kp), np.int8)
+    dsx = H.DeviceArray.zeros((B, P), np.float32)
+    dcm = H.DeviceArray.zeros((B, Np), np.float32)
+    dlg = H.DeviceArray.zeros((B, nc), np.float32)
+    dcw = H.DeviceArray.from_host(clsw)
+    dcb = H.DeviceArray.from_host(clsb)
+    H.check(L.bnh_quant_cells(dx.ptr, P * C, P, C, C, 1e-5, dqa.ptr, P * Kp, Kp, dsx.ptr, P, B, stream))
+
+    def colmax():
+        H.check(L.bnh_proto_colmax(dqa.ptr, P * Kp, dsx.ptr, P, P, W, dcm.ptr, Np, B, stream))
+    ms, _ = time_steps(H, stream, colmax, steps, warmup)
+    H.check(L.bnh_proto_logits(dcm.ptr, Np, dcw.ptr, dcb.ptr, nc, ppc, dlg.ptr, nc, B, None, 7, stream))
+    got = dlg.numpy()[0]
+    ref = O.proto_s8(cells[0], C, 1e-5, qw, swp, Np, Kp, clsw, clsb, nc, ppc)[1]
+    L.bnh_s8p_free(W)
+    ops = 2.0 * B * P * C * N
+    tops = ops / (ms * 1e-3) / 1e12
+    return {"kernel": "k_proto_gemm_pp",
+            "launch": f"int8 prototype head {B} windows x {P} cells x {C} channels against {N:,} prototypes, column "
+                      "maxima per window",
+            "ms_per_launch": round(ms, 4), "tops": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
+            "ops_per_launch": int(ops),
+            "parity_windows": f"{int(np.array_equal(got.view(np.uint32), ref.view(np.uint32)))}/1 window's logits "
+                              "bit-exact vs the oracle (window 0)"}
 
 
 def same_pads(n, k, s):
@@ -758,6 +813,8 @@ def run_perch(a, H, rng, B, stream):
     # the GEMM takes ~0.15 ms: 200 untimed launches (~30 ms) bring the clocks back up after the host-side input
     # generation, and 300 timed ones average over ~45 ms
     line["gemm_s8"] = gemm_s8_leg(H, rng, B, stream, max(300, a.steps), 200)
+    # the other int8 GEMM of the path, the prototype head (~1.1 ms a launch): 60 warmup launches, 100 timed
+    line["gemm_s8_proto"] = proto_s8_leg(H, rng, B, stream, max(100, a.steps), 60)
     if not a.no_cpu:
         line["cpu_baseline"], ref = cpu_baseline_perch(pn, pcms)
         same = [bool(np.array_equal(logits[w].view(np.uint32), ref[w % n_distinct][:nc].view(np.uint32)))
