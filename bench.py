@@ -807,6 +807,9 @@ def run_perch(a, H, rng, B, stream):
                    "parallelism": "1 GPU, windows batched per launch",
                    "wall_s_timed_region": round(wall, 4)},
         "int8_tops": round(tops, 3), "mfma_frac": round(tops / INT8_PEAK_TOPS, 5),
+        "int8_tops_scope": "the whole net: its int8 GEMM operations per step over the step's time (most of a step is "
+                           "depthwise, SE and quantisation work); the int8 GEMMs timed on their own are under "
+                           "gemm_s8 and gemm_s8_proto",
     }
     line["roofline"] = perch_roofline(H, pn, B, stream, a)
     m.close()
