@@ -23,6 +23,11 @@ __device__ __forceinline__ void rq_dma16s(const void *base, uint32_t off, const 
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
 }
+// the same for a stream read once (nt: non-temporal, so that it does not push L2-resident operands such as weights out)
+__device__ __forceinline__ void rq_dma16s_nt(const void *base, uint32_t off, const lds_i8 *dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "s"(m0) : "memory", "m0");
+}
 #define RQ_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 #define RQ_BARRIER() asm volatile("s_barrier" ::: "memory")
 

@@ -1072,7 +1072,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_s8_requant_sr(const int8_t *__r
     if (whole) {
       const int8_t *xb = xw + (long long)s * RQ4_BK * M + p0;
 #pragma unroll
-      for (int h = 0; h < 4; h++) rq_dma16s(xb, doff[h], st + (4 * wq + h) * 1024);
+      for (int h = 0; h < 4; h++) rq_dma16s_nt(xb, doff[h], st + (4 * wq + h) * 1024);  // read once: non-temporal
       return;
     }
 #pragma unroll
