@@ -146,6 +146,10 @@ _SIGS = {
     "bnh_quant_cells_f16": (i32, [vp, i64, i32, i32, i32, C.c_float, vp, i64, i32, vp, i64, i32, vp]),
     "bnh_s8p_new_c12": (vp, [i32, i32, vp, vp]),
     "bnh_gemm_f16_mfma_gated": (i32, [vp, i64, i32, i32, i32, vp, C.POINTER(Epi16), vp, i64, vp]),
+    "bnh_fproto_new": (vp, [i32, i32, i32, vp]),
+    "bnh_fproto_free": (None, [vp]),
+    "bnh_l2norm_cells": (i32, [vp, i64, i32, i32, i32, C.c_float, i32, vp, i64, i32, vp]),
+    "bnh_fproto_colmax": (i32, [vp, i64, i32, vp, vp, i64, i32, vp]),
 }
 
 
@@ -288,6 +292,26 @@ class Q8Weights:
         try:
             if self.h:
                 lib().bnh_q8w_free(self.h)
+        except Exception:
+            pass
+
+
+class FProto:
+    """bnh_fproto: the prototypes of an fp32 / fp16 prototype head in HBM. kind 0: fp32 panels [Np/8][K][8]
+    (PROTO variant 0), 1: fp16 panels [Np/8][K][8] (PROTO_F32H), 2: fp16 hpack panels (PROTO variant 1)."""
+
+    def __init__(self, kind, Np, K, w):
+        w = np.asarray(w)
+        w = np.ascontiguousarray(w.view(np.uint16) if w.dtype == np.float16 else w)
+        self.kind, self.Np, self.K = kind, Np, K
+        self.h = lib().bnh_fproto_new(kind, Np, K, w.ctypes.data)
+        if not self.h:
+            check(None, "bnh_fproto_new")
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().bnh_fproto_free(self.h)
         except Exception:
             pass
 

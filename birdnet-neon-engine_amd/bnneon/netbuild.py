@@ -17,7 +17,7 @@ HW_FP16 = 1
 OP = {"PW": 3, "DW3": 4, "SE": 5, "FE_LOGMEL": 8, "STEM": 9, "DWK": 10, "PROTO": 13,
       "PAD": 11, "MEAN": 12, "GEMV": 15, "PW_S8": 22, "GEMV_S8": 23,
       "SE_GATE": 25, "STEM3": 26, "CONV3C24": 27, "UNPAD": 28, "WINO_S8": 29, "QCONV3": 30, "QPW": 31,
-      "SE_GATE16": 32, "GEM_A": 33, "HEADS_S8": 34, "PROTO_S8": 35}
+      "SE_GATE16": 32, "GEM_A": 33, "HEADS_S8": 34, "PROTO_S8": 35, "PROTO_F32H": 14}
 HW_DOTPROD = 2
 ACT = {None: 0, "none": 0, "silu": 1, "relu": 2}
 
@@ -105,6 +105,42 @@ class Net:
         qb = self.buf(I8, P, 1, Kp)
         cb = self.buf(F32, 1, 1, Np)
         self.emit(OP["PROTO_S8"], [ib, ob, qb, cb], tl, [N, K, Kp, Np, P, C, ld, nc, ppc])
+        self.last = ob
+        return ob
+
+    def proto_fp(self, ib, protos, clsw, clsb, eps=1e-5, kind="f32"):
+        """The fp32 / fp16 prototype heads on cells [P][C] of buffer ib (l_proto / emit_proto / proto_f32h,
+        python/bnneon/compiler/lower.py:429-504): kind "f32" PROTO variant 0 (fp32 panels, zero bias, Kp = C),
+        "f16" PROTO variant 1 (hpack panels; fp16 cells), "f32h" PROTO_F32H (fp16 panels [Np/8][K][8], fp32 cells).
+        The record's buffers: cells, logits [nc], the normalised cells [P][C], column maxima [Np]."""
+        d = self.bufs[ib]
+        P, C, ld = d[1] * d[2], d[3], d[4]
+        protos = np.asarray(protos, np.float32)
+        N, K = protos.shape
+        assert K == C and C % 8 == 0 and P % 8 == 0
+        nc = len(clsb)
+        ppc = N // nc
+        Np = (N + 7) // 8 * 8
+        cls = [self.tensor("cls.w", np.asarray(clsw, np.float32).reshape(nc, ppc)),
+               self.tensor("cls.b", np.asarray(clsb, np.float32)), self.tensor("cls.eps", np.array([eps], np.float32))]
+        if kind == "f32":
+            panels, bb, shp = self.fpack(protos, np.zeros(N, np.float32), K_pad=8)
+            tl = [self.tensor("proto.w", panels), self.tensor("proto.b", bb)] + cls
+            code, var, ints, adt = OP["PROTO"], 0, list(shp) + [P, C, ld, nc, ppc], F32
+        elif kind == "f16":
+            w16, b32, b16, shp = self.pack_h16(protos, np.zeros(N, np.float32), K)
+            tl = [self.tensor("proto.w", w16), self.tensor("proto.b32", b32), self.tensor("proto.b16", b16)] + cls
+            code, var, ints, adt = OP["PROTO"], 1, list(shp) + [P, C, ld, nc, ppc], F16
+        else:
+            w16p = np.zeros((Np, C), np.float16)
+            w16p[:N] = protos.astype(np.float16)
+            wp = np.ascontiguousarray(w16p.reshape(Np // 8, 8, C).transpose(0, 2, 1))
+            tl = [self.tensor("f32h/proto.w", wp)] + cls
+            code, var, ints, adt = OP["PROTO_F32H"], 0, [N, C, Np, P, C, ld, nc, ppc], F32
+        ob = self.buf(F32, 1, 1, nc)
+        ab = self.buf(adt, P, 1, C)
+        cb = self.buf(F32, 1, 1, Np)
+        self.emit(code, [ib, ob, ab, cb], tl, ints, var=var)
         self.last = ob
         return ob
 

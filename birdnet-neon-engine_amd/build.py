@@ -23,6 +23,7 @@ SOURCES = [
     "kern_s8n.hip",
     "pw_s8_static.hip",
     "kern_proto.hip",
+    "kern_fproto.hip",
     "kern_dw.hip",
     "kern_wino.hip",
     "kern_f16.hip",

@@ -1417,7 +1417,8 @@ bnh_q8w *bnh_q8w_new(int N, int K, const int8_t *w, const int32_t *bias, const i
   W->N = N; W->K = K; W->Kt = Kt; W->Nt = Nt; W->zx = zx; W->zy = zy; W->lo = lo; W->hi = hi;
   W->all_s1 = 1;
   for (int n = 0; n < N; n++) W->all_s1 &= shift[n] >= 1;
-  W->fast = W->all_s1 && zy <= lo && lo <= hi;
+  // the short epilogue clamps to [lo - zy, hi - zy] and adds zy bytewise: every clamped value must fit one byte
+  W->fast = W->all_s1 && zy <= lo && lo <= hi && (long long)hi - zy <= 255;
   for (int n = 0; n < N; n++) W->fast &= llabs((long long)hb[n]) + (long long)K * 16384 < (1LL << 31);
   int32_t *hc = (int32_t *)calloc(2 * (size_t)Nt, 4), *he = (int32_t *)calloc(Nt, 4);
   if (!hc || !he) {

@@ -226,8 +226,15 @@ int rt_fuse_se16(rt_ctx *c, rt_op *se, rt_op *pw) {
   return 1;
 }
 
+// the fp16 prototype head (ops_proto.cpp)
+int bnh_proto_f16_init(rt_ctx *c, rt_op *op);
+int bnh_proto_fp_run(rt_ctx *c, rt_op *op);
+void bnh_proto_fp_fini(rt_op *op);
+static const rt_kernel K_PROTO = {bnh_proto_f16_init, bnh_proto_fp_run, bnh_proto_fp_fini, "proto_f16", 0xe, 0};
+
 const rt_kernel *rt_k_f16(int base) {
   switch (base) {
+    case RT_OP_PROTO: return &K_PROTO;
     case RT_OP_PW: return &K_PW;
     case RT_OP_DW3: return &K_DW3;
     case RT_OP_DWK: return &K_DWK;

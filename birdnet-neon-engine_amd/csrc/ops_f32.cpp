@@ -382,8 +382,18 @@ int rt_fuse_pwdw(rt_ctx *c, rt_op *pw, rt_op *dw) {
   return 1;
 }
 
+// the fp32 prototype heads (ops_proto.cpp)
+int bnh_proto_f32_init(rt_ctx *c, rt_op *op);
+int bnh_proto_f32h_init(rt_ctx *c, rt_op *op);
+int bnh_proto_fp_run(rt_ctx *c, rt_op *op);
+void bnh_proto_fp_fini(rt_op *op);
+static const rt_kernel K_PROTO = {bnh_proto_f32_init, bnh_proto_fp_run, bnh_proto_fp_fini, "proto_f32", 0xe, 0};
+static const rt_kernel K_PROTO_F32H = {bnh_proto_f32h_init, bnh_proto_fp_run, bnh_proto_fp_fini, "proto_f32h", 0xe, 0};
+
 const rt_kernel *rt_k_f32(int base) {
   switch (base) {
+    case RT_OP_PROTO: return &K_PROTO;
+    case RT_OP_PROTO_F32H: return &K_PROTO_F32H;
     case RT_OP_PW: return &K_PW;
     case RT_OP_DW3: return &K_DW3;
     case RT_OP_DWK: return &K_DWK;

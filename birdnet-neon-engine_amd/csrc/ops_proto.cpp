@@ -193,3 +193,116 @@ void bnh_proto8_dot_fini(rt_op *op) {
   }
   free(s);
 }
+
+// -------- PROTO variant 0 (proto_init / proto_run, src/rt_ops_f32.c:548-570), PROTO_F32H (proto_h_init /
+// proto_h_run, :572-591) and PROTO variant 1 (src/rt_ops_f16.c:227-250): the fp32 / fp16 prototype heads.
+//   b = [x [P][ld], logits f32 [nc], a [P][C] scratch, colmax f32 [Np]];
+//   PROTO f32: t = [w fp32 panels, b, cls w, cls b, eps], p = [N K Kp Np, P C ld nc ppc];
+//   PROTO f16: t = [w hpack panels, b32, b16, cls w, cls b, eps], p = [N K Kp Np, P C ld nc ppc];
+//   PROTO_F32H: t = [w16 [Np/8][K][8], cls w, cls b, eps], p = [N K Np, P C ld nc ppc]
+typedef struct {
+  bnh_fproto *W;
+  float *clsw, *clsb;
+  float eps;
+  int f16;
+} fproto_state;
+
+// the class tensors at ct, ct + 1, ct + 2, the unpadded cells (buffer 0, dtype dt) and the logits (rt_proto_io,
+// src/rt_ops_f32.c:537-546)
+static int proto_io(rt_ctx *c, rt_op *op, int ct, int dt) {
+  const int *p = op->p, *q = p + op->ni - 5;
+  const int N = p[0], P = q[0], ld = q[2], nc = q[3];
+  if (rt_need_t(c, op, ct, (size_t)N * 4, 0) || rt_need_t(c, op, ct + 1, (size_t)nc * 4, 0) ||
+      rt_need_t(c, op, ct + 2, 4, 0))
+    return RT_E_PARAM;
+  if (rt_need_nohalo(c, op, 0, dt, (size_t)P * ld)) return RT_E_PARAM;
+  return rt_need(c, op, 1, RT_F32, (size_t)nc);
+}
+
+// after the geometry and the pack view: Kp = K, 8-cell / 8-channel tiles, then tensors and buffers (rt_proto_check,
+// src/rt_ops_f32.c:547-556); nw = the pack's tensor count (2 fp32, 3 fp16)
+static int proto_check(rt_ctx *c, rt_op *op, int nw) {
+  const int *p = op->p;
+  const int K = p[1], P = p[4], C = p[5], dt = nw == 3 ? RT_F16 : RT_F32;
+  RT_REQ(c, op, p[2] == K);
+  RT_REQ(c, op, C % 8 == 0 && P % 8 == 0);
+  if (proto_io(c, op, nw, dt)) return RT_E_PARAM;
+  return rt_need(c, op, 2, dt, (size_t)P * C) || rt_need(c, op, 3, RT_F32, (size_t)p[3]) ? RT_E_PARAM : 0;
+}
+
+static int fproto_finish(rt_ctx *c, rt_op *op, fproto_state *s, int kind, int Np, int K, const void *w, int ct) {
+  const int N = op->p[0], nc = op->p[op->ni - 2];
+  memcpy(&s->eps, rt_t(c, op, ct + 2, nullptr), 4);
+  s->f16 = kind == 2;
+  s->W = bnh_fproto_new(kind, Np, K, w);
+  s->clsw = upload_f32(rt_t(c, op, ct, nullptr), (size_t)N);
+  s->clsb = upload_f32(rt_t(c, op, ct + 1, nullptr), (size_t)nc);
+  if (!s->W || !s->clsw || !s->clsb) return rt_oom(c, op, (size_t)Np * K * (kind ? 2 : 4));
+  return 0;
+}
+
+// PROTO variant 0 and variant 1: the GEMM pack view (rt_fpack_view / hpack_view) then rt_proto_check
+static int proto_fp_init(rt_ctx *c, rt_op *op, bool f16) {
+  fproto_state *s = (fproto_state *)calloc(1, sizeof *s);
+  op->state = s;
+  if (!s) return rt_oom(c, op, sizeof *s);
+  if (proto_geom(c, op, f16 ? 6 : 5, 9, 1 << 20)) return RT_E_PARAM;
+  const int *p = op->p;
+  const int N = p[0], K = p[1], Kp = p[2], Np = p[3];
+  if (f16) {
+    if (Np != ((N + 7) & ~7) || Kp < K || Kp % 8)
+      return rt_bad(c, op, "GEMM shape N %d K %d Kp %d Np %d: expected Np = N rounded up to 8, Kp >= K, Kp %% 8 == 0",
+                    N, K, Kp, Np);
+    if (rt_need_t(c, op, 0, (size_t)Np * Kp * 2, 1) || rt_need_t(c, op, 1, (size_t)(Np + 16) * 4, 1) ||
+        rt_need_t(c, op, 2, (size_t)(Np + 16) * 2, 1))
+      return RT_E_PARAM;
+  } else {
+    if (N <= 0 || K <= 0 || Np != ((N + 7) & ~7) || Kp < K || Kp % 4)
+      return rt_bad(c, op, "GEMM shape N %d K %d Kp %d Np %d: expected Np = N rounded up to 8, Kp >= K, Kp %% 4 == 0",
+                    N, K, Kp, Np);
+    if (rt_need_t(c, op, 0, (size_t)Np * Kp * 4, 1) || rt_need_t(c, op, 1, (size_t)Np * 4, 1)) return RT_E_PARAM;
+  }
+  if (proto_check(c, op, f16 ? 3 : 2)) return RT_E_PARAM;
+  return fproto_finish(c, op, s, f16 ? 2 : 0, Np, K, rt_t(c, op, 0, nullptr), f16 ? 3 : 2);
+}
+int bnh_proto_f32_init(rt_ctx *c, rt_op *op) { return proto_fp_init(c, op, false); }
+int bnh_proto_f16_init(rt_ctx *c, rt_op *op) { return proto_fp_init(c, op, true); }
+
+int bnh_proto_f32h_init(rt_ctx *c, rt_op *op) {
+  fproto_state *s = (fproto_state *)calloc(1, sizeof *s);
+  op->state = s;
+  if (!s) return rt_oom(c, op, sizeof *s);
+  if (proto_geom(c, op, 4, 8, 1 << 20)) return RT_E_PARAM;
+  const int *p = op->p;
+  const int N = p[0], K = p[1], Np = p[2], P = p[3], C = p[4];
+  RT_REQ(c, op, K % 4 == 0);
+  RT_REQ(c, op, P % 8 == 0 && Np % 8 == 0 && Np >= N);
+  if (rt_need_t(c, op, 0, (size_t)Np * K * 2, 1) || proto_io(c, op, 1, RT_F32)) return RT_E_PARAM;
+  if (rt_need(c, op, 2, RT_F32, (size_t)P * C) || rt_need(c, op, 3, RT_F32, (size_t)Np)) return RT_E_PARAM;
+  // the GPU's repack and chains take K in steps of 8 (every package's cells are 8-channel rows: C % 8 == 0)
+  if (K % 8) return rt_bad(c, op, "K %d: this library's fp32 prototype head takes K %% 8 == 0", K);
+  return fproto_finish(c, op, s, 1, Np, K, rt_t(c, op, 0, nullptr), 1);
+}
+
+int bnh_proto_fp_run(rt_ctx *c, rt_op *op) {
+  fproto_state *s = (fproto_state *)op->state;
+  const int *q = op->p + op->ni - 5;
+  const int P = q[0], C = q[1], ld = q[2], nc = q[3], ppc = q[4], B = c->nwin;
+  float *cm = (float *)rt_b(c, op, 3);
+  void *a = rt_b(c, op, 2);
+  if (bnh_l2norm_cells(rt_b(c, op, 0), rt_ws(c, op, 0), P, C, ld, s->eps, s->f16, a, rt_ws(c, op, 2), B, c->stream))
+    return -1;
+  if (bnh_fproto_colmax(a, rt_ws(c, op, 2), P, s->W, cm, rt_ws(c, op, 3), B, c->stream)) return -1;
+  return bnh_proto_logits(cm, rt_ws(c, op, 3), s->clsw, s->clsb, nc, ppc, (float *)rt_b(c, op, 1), rt_ws(c, op, 1), B,
+                          c->win_fail + c->w0, c->fail_op + 1, c->stream);
+}
+
+void bnh_proto_fp_fini(rt_op *op) {
+  fproto_state *s = (fproto_state *)op->state;
+  if (s) {
+    bnh_fproto_free(s->W);
+    if (s->clsw) hipFree(s->clsw);
+    if (s->clsb) hipFree(s->clsb);
+  }
+  free(s);
+}

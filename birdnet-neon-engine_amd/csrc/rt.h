@@ -124,6 +124,7 @@ int rt_meta_str(const rt_pkg *p, const char *key, char *buf, size_t n);
 int rt_meta_i64(const rt_pkg *p, const char *key, int64_t *v);
 int rt_meta_f64(const rt_pkg *p, const char *key, double *v);
 int rt_n_paths(const rt_pkg *p);
+int rt_path_served(const rt_pkg *p, int i);  // 1 when every op of path i has a kernel here
 int rt_n_tensors(const rt_pkg *p);
 int rt_format_version(const rt_pkg *p);
 const uint8_t *rt_pkg_bytes(const rt_pkg *p);  // the mapped file

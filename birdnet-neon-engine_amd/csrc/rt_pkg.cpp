@@ -322,7 +322,7 @@ class ContextBuilder {
     char compiler[48];
     if (rt_meta_str(p_, "compiler", compiler, sizeof compiler) < 0) snprintf(compiler, sizeof compiler, "unknown");
     return refuse(RT_E_PARAM, "%s: unknown opcode 0x%x (base %d variant %d); this library runs opcodes 1..%d of "
-                  "variants 0 and 1 on the GPU (reader version %d), the package was written by compiler '%s'; hint: "
+                  "variants 0, 1 and 2 on the GPU, not every opcode of each (reader version %d), the package was written by compiler '%s'; hint: "
                   "pick a path of the package this library runs (mode 0), or update libbnneon_hip", who((int)i, nullptr),
                   op.code, op.code & 0xff, op.code >> 8, RT_OP_N - 1, RT_READER_VERSION, compiler);
   }
@@ -383,6 +383,23 @@ class ContextBuilder {
 };
 
 }  // namespace
+
+// 1 when this library has a kernel for every op record of path `pi` (a list it cannot walk counts as served, so
+// that bnn_init names the defect), else 0
+int rt_path_served(const rt_pkg *p, int pi) {
+  const rt_pathdesc *d = rt_path(p, pi);
+  if (!d) return 0;
+  const uint8_t *at = rt_pkg_bytes(p) + d->ops_off, *end = at + d->ops_bytes;
+  for (uint32_t i = 0; i < d->n_ops; i++) {
+    OpHead h;
+    if (end - at < (ptrdiff_t)sizeof h) return 1;
+    memcpy(&h, at, sizeof h);
+    if (h.bytes < sizeof h || end - at < (ptrdiff_t)h.bytes) return 1;
+    if (!rt_kernel_for(h.code)) return 0;
+    at += h.bytes;
+  }
+  return 1;
+}
 
 rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
   ContextBuilder b(p, pi, err, errlen);

@@ -119,6 +119,25 @@ int bnh_proto_colmax(const int8_t *qa, long long qa_ws, const float *sx, long lo
 int bnh_proto_logits(const float *colmax, long long cm_ws, const float *clsw, const float *clsb, int nc, int ppc,
                      float *logits, long long lg_ws, int B, int *win_fail, int fail_code, void *stream);
 
+/* ------------------------------------------------------------------ fp32 / fp16 prototype heads
+ * PROTO variant 0 (src/rt_ops_f32.c:548-570), PROTO_F32H (src/rt_ops_f32.c:572-591) and PROTO variant 1
+ * (src/rt_ops_f16.c:227-250). Prototypes from the package tensor, K % 8 == 0 and Np % 8 == 0:
+ *   kind 0: fp32 panels [Np/8][K][8] (fpack, Kp = K), kind 1: fp16 panels [Np/8][K][8] (PROTO_F32H),
+ *   kind 2: fp16 panels [Np/16][K][16] then a tail panel [K][8] when Np % 16 == 8 (hpack, Kp = K);
+ * repacked once into k-major rows in HBM. */
+typedef struct bnh_fproto bnh_fproto;
+bnh_fproto *bnh_fproto_new(int kind, int Np, int K, const void *w);
+void bnh_fproto_free(bnh_fproto *W);
+/* pc_l2norm_f32 (src/pc_kern_f32.c:350-362) or, f16 != 0, pc_l2norm_f16 (src/pc_kern_f16.c:123-140): cells x [P][ld]
+ * (fp32, or fp16 bit patterns) -> a [P][C] of the same type, each cell divided by sqrtf(sum of squares) + eps */
+int bnh_l2norm_cells(const void *x, long long x_ws, int P, int C, int ld, float eps, int f16, void *a, long long a_ws,
+                     int B, void *stream);
+/* gemm_f32_colmax (src/gemm_f32.c:443-460), pc_proto_colmax_f32h (src/pc_kern_f32.c:378-407) or gemm_f16_colmax
+ * (src/gemm_f16.c:210-253) by W's kind: colmax f32 [Np] per window, the maximum over the window's P cells a [P][K]
+ * (fp32; fp16 for kind 2; 16-byte aligned) of their products with each prototype, summed as the reference does */
+int bnh_fproto_colmax(const void *a, long long a_ws, int P, const bnh_fproto *W, float *colmax, long long cm_ws, int B,
+                      void *stream);
+
 /* ------------------------------------------------------------------ int8 GEMM with Q31 requantisation
  * No counterpart in the reference (whose int8 GEMM dequantises to fp32): the TFLite-style static int8 pointwise
  * convolution, NCHW. Per window: x int8 [K][M] (pixels contiguous), out int8 [N][M];

@@ -72,6 +72,25 @@ int orc_proto_logits(const float *colmax, const float *w, const float *b, int nc
 int orc_proto_s8(const float *x, int P, int C, int ld, float eps, int8_t *qa, int Kp, float *sx, const int8_t *qw,
                  const float *sw, int Np, float *colmax, const float *clsw, const float *clsb, int nc, int ppc,
                  float *logits);
+/* ---------------------------------------------------------------- fp32 / fp16 prototype heads */
+/* src/pc_kern_f32.c:350-362 */
+void orc_l2norm_f32(const float *x, int P, int C, int ld, float eps, float *a);
+/* src/pc_kern_f16.c:123-140 */
+void orc_l2norm_f16(const uint16_t *x, int P, int C, int ld, float eps, uint16_t *a);
+/* src/gemm_f32.c:443-460: fp32 panels [Np/8][Kp][8] */
+void orc_colmax_f32(const float *A, int lda, int M, const float *wp, int Kp, int Np, float *colmax);
+/* src/pc_kern_f32.c:378-407: fp16 panels [Np/8][K][8] */
+void orc_colmax_f32h(const float *a, int P, int K, const uint16_t *w16, int Np, float *colmax);
+/* src/gemm_f16.c:210-253: hpack panels [Np/16][Kp][16] + tail [Kp][8] */
+void orc_colmax_f16(const uint16_t *A, int lda, int M, const uint16_t *W, int Kp, int Np, float *colmax);
+/* PROTO variant 0 (src/rt_ops_f32.c:563-570), PROTO_F32H (:583-590), PROTO variant 1 (src/rt_ops_f16.c:236-250) */
+int orc_proto_f32(const float *x, int P, int C, int ld, float eps, float *a, const float *wp, int Np, float *colmax,
+                  const float *clsw, const float *clsb, int nc, int ppc, float *logits);
+int orc_proto_f32h(const float *x, int P, int C, int ld, float eps, float *a, const uint16_t *w16, int Np,
+                   float *colmax, const float *clsw, const float *clsb, int nc, int ppc, float *logits);
+int orc_proto_f16(const uint16_t *x, int P, int C, int ld, float eps, uint16_t *a, const uint16_t *W, int Np,
+                  float *colmax, const float *clsw, const float *clsb, int nc, int ppc, float *logits);
+
 
 /* ---------------------------------------------------------------- depthwise convolutions */
 /* fp16 values as bit patterns; one rounding to nearest even per operation, denormals kept */

@@ -141,13 +141,35 @@ class OracleNet:
 
     # PROTO variant 2 (the dotprod head): buffers [cells f16, logits, qa, colmax], tensors [qw 12-panels, sw, clsw,
     # clsb, eps]
+    # PROTO variants 0 (fp32) and 1 (fp16): buffers [cells, logits, a, colmax], tensors [panels, bias (fp16: b32, b16),
+    # clsw, clsb, eps]
     def op_13(self, var, b, t, p, bufs):
+        if var in (0, 1):
+            N, K, Kp, Np, P_, C, ld, nc, ppc = p
+            x = bufs[b[0]][:P_ * ld].reshape(P_, ld)
+            ct = 2 if var == 0 else 3
+            rc, lg, cm, a = O.proto_fp("f32" if var == 0 else "f16", x, C, float(np.asarray(t[ct + 2]).reshape(-1)[0]),
+                                       t[0], Np, np.asarray(t[ct]).reshape(-1), t[ct + 1], nc, ppc)
+            self.put(bufs[b[1]], lg)
+            self.put(bufs[b[2]], a.view(np.float16) if var == 1 else a)
+            self.put(bufs[b[3]], cm)
+            return
         assert var == 2
         N, K, Np, P_, C, ld, nc, ppc = p
         x = bufs[b[0]][:P_ * ld].reshape(P_, ld)
         rc, lg, cm = O.proto_s8_dot(x, C, float(np.asarray(t[4]).reshape(-1)[0]), t[0], t[1][:Np], Np,
                                     np.asarray(t[2]).reshape(-1), t[3], nc, ppc)
         self.put(bufs[b[1]], lg)
+        self.put(bufs[b[3]], cm)
+
+    # PROTO_F32H: buffers [cells f32, logits, a, colmax], tensors [fp16 panels [Np/8][K][8], clsw, clsb, eps]
+    def op_14(self, var, b, t, p, bufs):
+        N, K, Np, P_, C, ld, nc, ppc = p
+        x = bufs[b[0]][:P_ * ld].reshape(P_, ld)
+        rc, lg, cm, a = O.proto_fp("f32h", x, C, float(np.asarray(t[3]).reshape(-1)[0]), t[0], Np,
+                                   np.asarray(t[1]).reshape(-1), t[2], nc, ppc)
+        self.put(bufs[b[1]], lg)
+        self.put(bufs[b[2]], a)
         self.put(bufs[b[3]], cm)
 
     # QCONV3: x f32 [H][W][C] -> fp16 rows

@@ -153,3 +153,132 @@ void orc_proto_colmax_c12(const int8_t *qa, int Kp, const float *sx, int P, int 
     colmax[j] = mx * sw[j];
   }
 }
+
+/* ---------------------------------------------------------------- fp32 / fp16 prototype heads (PROTO variants 0
+ * and 1, PROTO_F32H) */
+
+/* src/pc_kern_f32.c:350-362 (pc_l2norm_f32): per cell, the sum of squares in two 4-lane fused accumulators over
+ * 8-channel steps reduced as ((t0 + t1) + (t2 + t3)), t_j = s0_j + s1_j (FADDP); den = sqrtf(sum) + eps; a = x / den
+ * (IEEE division), rows [P][C] */
+void orc_l2norm_f32(const float *x, int P, int C, int ld, float eps, float *a) {
+  for (int p = 0; p < P; p++) {
+    const float *r = x + (size_t)p * ld;
+    float s0[4] = {0, 0, 0, 0}, s1[4] = {0, 0, 0, 0};
+    for (int c = 0; c < C; c += 8)
+      for (int j = 0; j < 4; j++) {
+        s0[j] = fmaf(r[c + j], r[c + j], s0[j]);
+        s1[j] = fmaf(r[c + 4 + j], r[c + 4 + j], s1[j]);
+      }
+    float t[4];
+    for (int j = 0; j < 4; j++) t[j] = s0[j] + s1[j];
+    const float den = sqrtf((t[0] + t[1]) + (t[2] + t[3])) + eps;
+    for (int c = 0; c < C; c++) a[(size_t)p * C + c] = r[c] / den;
+  }
+}
+
+/* src/pc_kern_f16.c:123-140 (pc_l2norm_f16): the same sums of the widened fp16 values; a = fp16(fp32(x) / den),
+ * rounded to nearest even */
+void orc_l2norm_f16(const uint16_t *x, int P, int C, int ld, float eps, uint16_t *a) {
+  for (int p = 0; p < P; p++) {
+    const uint16_t *r = x + (size_t)p * ld;
+    float s0[4] = {0, 0, 0, 0}, s1[4] = {0, 0, 0, 0};
+    for (int c = 0; c < C; c += 8)
+      for (int j = 0; j < 4; j++) {
+        const float u0 = orc_h2f(r[c + j]), u1 = orc_h2f(r[c + 4 + j]);
+        s0[j] = fmaf(u0, u0, s0[j]);
+        s1[j] = fmaf(u1, u1, s1[j]);
+      }
+    float t[4];
+    for (int j = 0; j < 4; j++) t[j] = s0[j] + s1[j];
+    const float den = sqrtf((t[0] + t[1]) + (t[2] + t[3])) + eps;
+    for (int c = 0; c < C; c++) a[(size_t)p * C + c] = orc_f2h(orc_h2f(r[c]) / den);
+  }
+}
+
+/* src/gemm_f32.c:443-460 (gemm_f32_colmax, the KB k-block of src/gemm_f32_kblock.h): colmax[n] = FMAX over rows m,
+ * from -inf, of one fused chain from +0 over k < Kp in order of k; prototypes as fp32 panels [Np/8][Kp][8] */
+void orc_colmax_f32(const float *A, int lda, int M, const float *wp, int Kp, int Np, float *colmax) {
+  for (int n = 0; n < Np; n++) {
+    const float *w = wp + (size_t)(n / 8) * Kp * 8 + n % 8;
+    float mx = -INFINITY;
+    for (int m = 0; m < M; m++) {
+      float acc = 0.f;
+      for (int k = 0; k < Kp; k++) acc = fmaf(w[(size_t)k * 8], A[(size_t)m * lda + k], acc);
+      mx = orc_fmax(mx, acc);
+    }
+    colmax[n] = mx;
+  }
+}
+
+/* src/pc_kern_f32.c:378-407 (pc_proto_colmax_f32h): as orc_colmax_f32 with the prototypes stored in fp16 panels
+ * [Np/8][K][8], each weight widened exactly (FCVTL) before its fused multiply-add; cells a [P][K] */
+void orc_colmax_f32h(const float *a, int P, int K, const uint16_t *w16, int Np, float *colmax) {
+  for (int n = 0; n < Np; n++) {
+    const uint16_t *w = w16 + (size_t)(n / 8) * K * 8 + n % 8;
+    float mx = -INFINITY;
+    for (int p = 0; p < P; p++) {
+      float acc = 0.f;
+      for (int k = 0; k < K; k++) acc = fmaf(orc_h2f(w[(size_t)k * 8]), a[(size_t)p * K + k], acc);
+      mx = orc_fmax(mx, acc);
+    }
+    colmax[n] = mx;
+  }
+}
+
+/* K blocks of the fp16 GEMM (kblocks, src/gemm_f16.c:55-58) */
+static void f16_kblocks(int Kp, int *nblk, int *bs) {
+  *nblk = (Kp + 127) / 128;
+  *bs = ((Kp + *nblk - 1) / *nblk + 7) & ~7;
+}
+
+/* src/gemm_f16.c:210-253 (gemm_f16_colmax_range over every panel): per output and K block, an fp16 fused chain from
+ * +0 over the block's k in order; one block: the chain widened; several: an fp32 sum from +0 of the widened chains
+ * in block order. colmax[n] = FMAX over rows, from -inf. Prototypes as hpack panels [Np/16][Kp][16], then a tail
+ * panel [Kp][8] when Np % 16 == 8 */
+void orc_colmax_f16(const uint16_t *A, int lda, int M, const uint16_t *W, int Kp, int Np, float *colmax) {
+  int nblk, bs;
+  f16_kblocks(Kp, &nblk, &bs);
+  const int n16 = Np / 16;
+  for (int n = 0; n < Np; n++) {
+    const int pan = n / 16, wide = pan < n16, ws = wide ? 16 : 8;
+    const uint16_t *w = W + (size_t)pan * Kp * 16 + (wide ? n % 16 : n - 16 * n16);
+    float mx = -INFINITY;
+    for (int m = 0; m < M; m++) {
+      float fb = 0.f, v = 0.f;
+      for (int kb = 0; kb < Kp; kb += bs) {
+        const int kn = Kp - kb < bs ? Kp - kb : bs;
+        uint16_t acc = 0;
+        for (int k = kb; k < kb + kn; k++) acc = orc_h_fma(w[(size_t)k * ws], A[(size_t)m * lda + k], acc);
+        if (nblk > 1) fb = fb + orc_h2f(acc);
+        else v = orc_h2f(acc);
+      }
+      mx = orc_fmax(mx, nblk > 1 ? fb : v);
+    }
+    colmax[n] = mx;
+  }
+}
+
+/* PROTO variant 0 of one window (proto_run, src/rt_ops_f32.c:563-570): cells x [P][ld] -> scratch a [P][C],
+ * colmax [Np], logits [nc]; returns orc_proto_logits' code */
+int orc_proto_f32(const float *x, int P, int C, int ld, float eps, float *a, const float *wp, int Np, float *colmax,
+                  const float *clsw, const float *clsb, int nc, int ppc, float *logits) {
+  orc_l2norm_f32(x, P, C, ld, eps, a);
+  orc_colmax_f32(a, C, P, wp, C, Np, colmax);
+  return orc_proto_logits(colmax, clsw, clsb, nc, ppc, logits);
+}
+
+/* PROTO_F32H of one window (proto_h_run, src/rt_ops_f32.c:583-590) */
+int orc_proto_f32h(const float *x, int P, int C, int ld, float eps, float *a, const uint16_t *w16, int Np,
+                   float *colmax, const float *clsw, const float *clsb, int nc, int ppc, float *logits) {
+  orc_l2norm_f32(x, P, C, ld, eps, a);
+  orc_colmax_f32h(a, P, C, w16, Np, colmax);
+  return orc_proto_logits(colmax, clsw, clsb, nc, ppc, logits);
+}
+
+/* PROTO variant 1 of one window (proto_run, src/rt_ops_f16.c:236-250): fp16 cells, fp16 scratch a [P][C] */
+int orc_proto_f16(const uint16_t *x, int P, int C, int ld, float eps, uint16_t *a, const uint16_t *W, int Np,
+                  float *colmax, const float *clsw, const float *clsb, int nc, int ppc, float *logits) {
+  orc_l2norm_f16(x, P, C, ld, eps, a);
+  orc_colmax_f16(a, C, P, W, C, Np, colmax);
+  return orc_proto_logits(colmax, clsw, clsb, nc, ppc, logits);
+}

@@ -697,3 +697,72 @@ def proto_s8_dot(x, C, eps, qw, sw, Np, clsw, clsb, nc, ppc):
     lib().orc_proto_colmax_c12(P(qa), Kp, P(sx), Pn, C, P(_c(qw, np.int8)), P(_c(sw, np.float32)), Np, P(cm))
     rc = lib().orc_proto_logits(P(cm), P(_c(clsw, np.float32)), P(_c(clsb, np.float32)), nc, ppc, P(lg))
     return rc, lg, cm
+
+
+def _h(a):
+    """fp16 data as contiguous uint16 bit patterns (float16 arrays are reinterpreted, not converted)."""
+    a = np.asarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    assert a.dtype == np.uint16, a.dtype
+    return np.ascontiguousarray(a)
+
+
+_SIGS.update({
+    "orc_l2norm_f32": (None, [vp, i32, i32, i32, f32, vp]),
+    "orc_l2norm_f16": (None, [vp, i32, i32, i32, f32, vp]),
+    "orc_colmax_f32": (None, [vp, i32, i32, vp, i32, i32, vp]),
+    "orc_colmax_f32h": (None, [vp, i32, i32, vp, i32, vp]),
+    "orc_colmax_f16": (None, [vp, i32, i32, vp, i32, i32, vp]),
+    "orc_proto_f32": (i32, [vp, i32, i32, i32, f32, vp, vp, i32, vp, vp, vp, i32, i32, vp]),
+    "orc_proto_f32h": (i32, [vp, i32, i32, i32, f32, vp, vp, i32, vp, vp, vp, i32, i32, vp]),
+    "orc_proto_f16": (i32, [vp, i32, i32, i32, f32, vp, vp, i32, vp, vp, vp, i32, i32, vp]),
+})
+
+
+def l2norm(x, C, eps, f16=False):
+    """orc_l2norm_f32 / _f16 of cells x [P][ld] -> a [P][C] (fp32, or fp16 bit patterns)."""
+    x = _h(x) if f16 else _c(x, np.float32)
+    Pn, ld = x.shape
+    a = np.zeros((Pn, C), np.uint16 if f16 else np.float32)
+    (lib().orc_l2norm_f16 if f16 else lib().orc_l2norm_f32)(P(x), Pn, C, ld, float(eps), P(a))
+    return a
+
+
+def colmax_f32(a, wp, Kp, Np):
+    """orc_colmax_f32: rows a [M][lda], fp32 panels [Np/8][Kp][8] -> colmax [Np]."""
+    a = _c(a, np.float32)
+    cm = np.zeros(Np, np.float32)
+    lib().orc_colmax_f32(P(a), a.shape[1], a.shape[0], P(_c(wp, np.float32)), Kp, Np, P(cm))
+    return cm
+
+
+def colmax_f32h(a, w16, Np):
+    """orc_colmax_f32h: cells a [P][K] fp32, fp16 panels [Np/8][K][8] (bit patterns) -> colmax [Np]."""
+    a = _c(a, np.float32)
+    cm = np.zeros(Np, np.float32)
+    lib().orc_colmax_f32h(P(a), a.shape[0], a.shape[1], P(_h(w16)), Np, P(cm))
+    return cm
+
+
+def colmax_f16(a, W, Kp, Np):
+    """orc_colmax_f16: fp16 rows a [M][lda] (bit patterns), hpack panels (bit patterns) -> colmax [Np]."""
+    a = _h(a)
+    cm = np.zeros(Np, np.float32)
+    lib().orc_colmax_f16(P(a), a.shape[1], a.shape[0], P(_h(W)), Kp, Np, P(cm))
+    return cm
+
+
+def proto_fp(kind, x, C, eps, w, Np, clsw, clsb, nc, ppc):
+    """PROTO variant 0 (kind "f32": fp32 panels), PROTO_F32H ("f32h": fp16 panels [Np/8][K][8]) or PROTO variant 1
+    ("f16": fp16 cells, hpack panels) of one window -> (rc, logits, colmax, a)."""
+    f16 = kind == "f16"
+    x = _h(x) if f16 else _c(x, np.float32)
+    Pn, ld = x.shape
+    a = np.zeros((Pn, C), np.uint16 if f16 else np.float32)
+    cm = np.zeros(Np, np.float32)
+    lg = np.zeros(nc, np.float32)
+    fn = {"f32": lib().orc_proto_f32, "f32h": lib().orc_proto_f32h, "f16": lib().orc_proto_f16}[kind]
+    rc = fn(P(x), Pn, C, ld, float(eps), P(a), P(_c(w, np.float32) if kind == "f32" else _h(w)), Np, P(cm), P(_c(clsw, np.float32)),
+            P(_c(clsb, np.float32)), nc, ppc, P(lg))
+    return rc, lg, cm, a

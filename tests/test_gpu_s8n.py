@@ -344,7 +344,9 @@ def test_gemm_requant_short_epilogue(hip):
     rng = np.random.default_rng(31)
     K_BOUND = 16384
     cases = ((256, 1152, 1536, 2, -128, -128, 127), (40, 208, 272, 3, -20, -10, 100), (300, 64, 256, 1, -128, -100, 90),
-             (24, 48, 144, 2, 0, 0, 127), (136, 1152, 512, 2, 5, 5, 127))
+             (24, 48, 144, 2, 0, 0, 127), (136, 1152, 512, 2, 5, 5, 127),
+             # zy far below lo: hi - zy = 327 does not fit a byte, so the general epilogue must run
+             (64, 208, 272, 2, -200, -128, 127), (32, 64, 144, 1, -129, -128, 127))
     for (N, K, M, B, zy, lo, hi) in cases:
         zx = -128 if zy == -128 else -3
         w = rng.integers(-128, 128, (N, K)).astype(np.int8)

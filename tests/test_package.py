@@ -129,3 +129,36 @@ def test_api_version_and_threads_symbol():
     L = binding.load_library()
     assert L.bnn_api_version() == 2
     assert L.bnn_set_threads(None, 2) == -1
+
+
+def test_mode0_passes_over_unserved_paths(tmp_path):
+    """Mode 0 takes the first path (packages store them fastest first, src/bnneon.c:79-89) whose every op this
+    library serves: a neon-fp16 path whose first op is the v3.0 front end FE_DBIMG (not served on the GPU) is passed
+    over for the neon-int8 path behind it; a package of that path alone still names it, so init names the op."""
+    rng = np.random.default_rng(4)
+    K, N = 40, 3
+    pkg = pkgfmt.Package()
+    a = netbuild.Net(pkg, prefix="a/")
+    ia = a.buf(netbuild.F32, 1, 1, K)
+    oa = a.buf(netbuild.F32, 1, 1, N)
+    a.emit(16, [ia, oa], [], [K, N])   # FE_DBIMG
+    a.add_to("neon-fp16", netbuild.HW_FP16, in_buf=ia, out_buf=oa)
+    b = netbuild.Net(pkg, prefix="b/")
+    ib = b.buf(netbuild.F32, 1, 1, K)
+    b.gemv_s8(ib, rng.standard_normal((N, K)), rng.standard_normal(N))
+    b.add_to("neon-int8", 0, in_buf=ib)
+    netbuild.standard_meta(pkg, K, N, model_id="two_paths_one_served")
+    p = str(tmp_path / "t.bnpk")
+    pkg.write(p)
+    assert binding.probe(p).path == b"neon-int8"
+
+    pkg = pkgfmt.Package()
+    a = netbuild.Net(pkg)
+    ia = a.buf(netbuild.F32, 1, 1, K)
+    oa = a.buf(netbuild.F32, 1, 1, N)
+    a.emit(16, [ia, oa], [], [K, N])
+    a.add_to("neon-fp16", netbuild.HW_FP16, in_buf=ia, out_buf=oa)
+    netbuild.standard_meta(pkg, K, N, model_id="one_unserved_path")
+    p = str(tmp_path / "u.bnpk")
+    pkg.write(p)
+    assert binding.probe(p).path == b"neon-fp16"
