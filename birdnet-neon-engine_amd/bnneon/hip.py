@@ -121,6 +121,7 @@ _SIGS = {
     "bnh_pad": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, i64, i32, vp]),
     "bnh_zero_halo": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp]),
     "bnh_eval_expf": (i32, [vp, vp, i64, vp]),
+    "bnh_eval_powf": (i32, [vp, vp, vp, i64, vp]),
     "bnh_stem_f32to16": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32,
                                i32, vp]),
     "bnh_se_f16": (i32, [vp, i64, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, vp]),

@@ -13,6 +13,7 @@
 #include "bnh_internal.h"
 #include "bnh_num.h"
 #include "bnh_expf.h"
+#include "bnh_powf.h"
 #include "bnh_f16.h"
 
 // ------------------------------------------------------------------ halo zeroing, any element size (4 or 2 bytes)
@@ -437,6 +438,13 @@ __global__ void k_eval_expf(const float *__restrict__ x, float *__restrict__ y, 
   if (i < n) y[i] = bnh_expf(x[i]);
 }
 
+// the device powf on its own (for its parity test against the C library)
+__global__ void k_eval_powf(const float *__restrict__ x, const float *__restrict__ y, float *__restrict__ z,
+                            long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) z[i] = bnh_powf(x[i], y[i]);
+}
+
 // ------------------------------------------------------------------ PAD: every element of the padded buffer
 // PAD: a thread per V consecutive elements of one window's padded buffer (V = 16 bytes when the channel count, the
 // row stride and the window strides allow, else 1), windows on grid.y; halo elements get zero
@@ -710,6 +718,14 @@ int bnh_unpad_f16(const uint16_t *x, long long x_ws, int H, int W, int C, float 
   BNH_REQ((long long)H * W * C < (1LL << 31));
   const dim3 grid((unsigned)bnh_ceil_div((long long)H * W * C, 1024), (unsigned)B);
   hipLaunchKernelGGL(k_unpad_f16, grid, dim3(256), 0, bnh_stream(stream), x, x_ws, H, W, C, out, o_ws);
+  BNH_HIP(hipGetLastError());
+  return 0;
+}
+
+int bnh_eval_powf(const float *x, const float *y, float *z, long long n, void *stream) {
+  BNH_REQ(x && y && z && n >= 0);
+  if (!n) return 0;
+  hipLaunchKernelGGL(k_eval_powf, dim3((unsigned)bnh_ceil_div(n, 256)), dim3(256), 0, bnh_stream(stream), x, y, z, n);
   BNH_HIP(hipGetLastError());
   return 0;
 }

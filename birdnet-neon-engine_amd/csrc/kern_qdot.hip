@@ -15,6 +15,7 @@
 #include "bnh_expf.h"
 #include "bnh_f16.h"
 #include "bnh_internal.h"
+#include "bnh_powf.h"
 #include "bnh_num.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -675,9 +676,8 @@ __global__ __launch_bounds__(256) void k_se_gate16(float *__restrict__ chsum, lo
 }
 
 // ------------------------------------------------------------------ generalised mean (GEM_A, src/rt_ops_dot.c:439-465)
-// e[c] = pow(mean over rows of exp2_p5(max(p log2(max(F, eps)), -126)), 1 / p): the sums in row order from 0; the
-// final power in double precision, rounded once (the C library's powf, which this follows, is not correctly rounded:
-// a result can differ from it by one unit in the last place)
+// e[c] = powf(mean over rows of exp2_p5(max(p log2(max(F, eps)), -126)), 1 / p): the sums in row order from 0; the
+// final power with the C library's powf results (bnh_powf.h: glibc's table method, restated)
 __global__ __launch_bounds__(256) void k_gem_a(const float *__restrict__ F, long long f_ws, int M, int C, float eps,
                                                float p, float *__restrict__ e, long long e_ws) {
   const int w = blockIdx.y, ch = blockIdx.x * 256 + threadIdx.x;
@@ -689,7 +689,7 @@ __global__ __launch_bounds__(256) void k_gem_a(const float *__restrict__ F, long
     acc = acc + qd_exp2_p5(bnh_fmax(p * qd_log2(v), -126.f));
   }
   const float mean = acc / (float)M, ip = 1.0f / p;
-  e[w * e_ws + ch] = (float)pow((double)mean, (double)ip);
+  e[w * e_ws + ch] = bnh_powf(mean, ip);
 }
 
 // ------------------------------------------------------------------ host side

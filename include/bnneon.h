@@ -50,9 +50,8 @@ typedef struct bnn_ctx bnn_ctx;
 int bnn_api_version(void);                                                   /* src/bnneon.h:59 */
 /* 1 for a known model family code when a GPU this library runs on is visible, else 0 (src/bnneon.h:60-66). As in the
  * reference this says nothing about a given package: whether this library runs one of its paths is bnn_probe's
- * info.path ("" = none). Paths whose ops this library does not serve (the v2.4 front-end and head ops FE_STFT2,
- * C0POOL, POSTPC, DENSE; the v3.0 FE_DBIMG front end; the fp32 / fp16 prototype heads PROTO variants 0 and 1 and
- * PROTO_F32H where not listed as served) are passed over in mode 0. */
+ * info.path ("" = none). Mode 0 passes over paths with ops this library does not serve (the hand-written v2.4 front
+ * end and head FE_STFT2, C0POOL, POSTPC, DENSE; the v3.0 front end FE_DBIMG), so such a package may be refused. */
 int bnn_cpu_supported(int model);
 int bnn_probe(const char *weights_path, bnn_info *info);                     /* src/bnneon.h:68 */
 int bnn_probe_meta(const char *weights_path, const char *key, char *buf, size_t n); /* src/bnneon.h:74 */

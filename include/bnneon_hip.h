@@ -354,6 +354,8 @@ int bnh_pad(const void *x, long long x_ws, int H, int W, int C, int ld, int h, i
 int bnh_zero_halo(void *xp, long long ws, int H, int W, int C, int h, int esz, int B, void *stream);
 /* test hook: y = expf(x) as the C library computes it (glibc's table method), elementwise on the device */
 int bnh_eval_expf(const float *x, float *y, long long n, void *stream);
+/* test hook: z = powf(x, y) as the C library computes it (glibc's table method), elementwise on the device */
+int bnh_eval_powf(const float *x, const float *y, float *z, long long n, void *stream);
 
 /* ------------------------------------------------------------------ dotprod int8 family (QPW, QCONV3, HEADS_S8)
  * libbnneon's int8 SDOT arithmetic (src/gemm_s8.c), bit-identical: activations quantised per row (or per tensor) to

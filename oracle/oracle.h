@@ -228,6 +228,8 @@ void orc_qconv3(const float *x, int H, int W, int C, int K, int s, int pt, int p
 void orc_se_gate16(float *chsum, int C, int rd, int P, const float *w1, const float *b1, const float *w2,
                    const float *b2, uint16_t *gate);
 void orc_gem_a(const float *F, int M, int C, float eps, float p, float *e);
+/* the C library's powf, elementwise */
+void orc_powf_vec(const float *x, const float *y, float *z, long long n);
 void orc_heads_s8(const float *F, const float *emb, int H, int W, int C, int hid, int nc, const int8_t *const *wq,
                   const float *const *sc, const float *const *ss, const float *const *bb, float *logits, float *work);
 

@@ -766,3 +766,15 @@ def proto_fp(kind, x, C, eps, w, Np, clsw, clsb, nc, ppc):
     rc = fn(P(x), Pn, C, ld, float(eps), P(a), P(_c(w, np.float32) if kind == "f32" else _h(w)), Np, P(cm), P(_c(clsw, np.float32)),
             P(_c(clsb, np.float32)), nc, ppc, P(lg))
     return rc, lg, cm, a
+
+
+_SIGS.update({"orc_powf_vec": (None, [vp, vp, vp, C.c_longlong])})
+
+
+def powf(x, y):
+    """The C library's powf, elementwise on float32 arrays."""
+    x, y = np.broadcast_arrays(np.asarray(x, np.float32), np.asarray(y, np.float32))
+    x, y = _c(x, np.float32), _c(y, np.float32)
+    z = np.empty_like(x)
+    lib().orc_powf_vec(P(x), P(y), P(z), x.size)
+    return z

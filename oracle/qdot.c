@@ -363,3 +363,8 @@ void orc_heads_s8(const float *F, const float *emb, int H, int W, int C, int hid
     }
   }
 }
+
+/* the C library's powf elementwise (the reference of GEM_A's final power, src/rt_ops_dot.c:452) */
+void orc_powf_vec(const float *x, const float *y, float *z, long long n) {
+  for (long long i = 0; i < n; i++) z[i] = powf(x[i], y[i]);
+}

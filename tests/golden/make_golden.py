@@ -1,11 +1,12 @@
-"""Writes tests/golden/pkg_two_paths.bnpk with the reference compiler's own
-package writer (python/bnneon/compiler/pkgfmt.py, Package.write).
+"""Writes tests/golden/pkg_two_paths.bnpk and pkg_three_paths.bnpk with the
+reference compiler's own package writer (python/bnneon/compiler/pkgfmt.py,
+Package.write).
 
 Run in the build container only, where the reference checkout is present:
     python tests/golden/make_golden.py
 The writer is loaded by file path as a standalone module (it imports only
 struct and numpy); nothing else of the reference is imported. The package's
-content comes from golden_pkg.build, which the tests also run against this
+content comes from golden_pkg.build / build3, which the tests also run against this
 library's writer. The .bnpk byte layout is otherwise pinned only by this
 library's own writer / reader pair, which is why the reference writer is used.
 """
@@ -31,11 +32,12 @@ def reference_writer():
 def main():
     import golden_pkg
     ref = reference_writer()
-    pkg = ref.Package()
-    golden_pkg.build(pkg)
-    out = os.path.join(HERE, "pkg_two_paths.bnpk")
-    n = pkg.write(out)
-    print("wrote", out, n, "bytes")
+    for build, name in ((golden_pkg.build, "pkg_two_paths.bnpk"), (golden_pkg.build3, "pkg_three_paths.bnpk")):
+        pkg = ref.Package()
+        build(pkg)
+        out = os.path.join(HERE, name)
+        n = pkg.write(out)
+        print("wrote", out, n, "bytes")
 
 
 if __name__ == "__main__":

@@ -79,3 +79,42 @@ def test_reference_package_scores_as_the_oracle(hip, mode, path):
         for w in (0, 17, 39):
             ref, _, _ = on.run(pcm[w])
             assert same(out[w], ref[:golden_pkg.NC]), w
+
+
+FIXTURE3 = os.path.join(GOLDEN, "pkg_three_paths.bnpk")
+
+
+def test_three_path_fixture_bytes_and_mode0():
+    """pkg_three_paths.bnpk (fp16, fp32, int8 paths, fastest first): this library's writer gives the same bytes; the
+    reader sees the paths in order with their prototype-head opcodes; mode 0 (bnn_probe's choice) takes the first
+    path, whose every op the GPU serves"""
+    pkg = pkgfmt.Package()
+    golden_pkg.build3(pkg)
+    assert pkg.to_bytes() == open(FIXTURE3, "rb").read()
+    r = pkgfmt.read(FIXTURE3)
+    assert [p["name"] for p in r["paths"]] == ["neon-fp16", "neon-fp32", "neon-int8"]
+    assert [op[0] for op in r["paths"][0]["ops"]] == [9 | 1 << 8, 13 | 1 << 8]
+    assert [op[0] for op in r["paths"][1]["ops"]] == [3, 13]
+    assert [op[0] for op in r["paths"][2]["ops"]] == [22, 35]
+    assert binding.probe(FIXTURE3).path == b"neon-fp16"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode,path", [(binding.MODE_DEFAULT, "neon-fp16"), (binding.MODE_FP16, "neon-fp16"),
+                                       (binding.MODE_FP32, "neon-fp32"), (binding.MODE_INT8, "neon-int8")])
+def test_three_path_package_scores_as_the_oracle(hip, mode, path):
+    import oracle_net
+    pkg = pkgfmt.Package()
+    nets = dict(zip(("neon-fp16", "neon-fp32", "neon-int8"), golden_pkg.build3(pkg)))
+    net, ib = nets[path]
+    on = oracle_net.OracleNet(net, ib, net.last)
+    rng = np.random.default_rng(6)
+    pcm = rng.standard_normal((70, golden_pkg.H3 * golden_pkg.W3)).astype(np.float32)
+    print("golden three-path package", mode, path, flush=True)
+    with binding.Model(FIXTURE3, mode) as m:
+        assert m.info.path == path.encode()
+        out, _, status = m.infer_batch(pcm)
+        assert not status.any()
+        for w in (0, 35, 69):
+            ref, _, _ = on.run(pcm[w])
+            assert same(out[w], ref[:golden_pkg.NC]), w

@@ -49,6 +49,30 @@ def test_expf_matches_c_library(hip):
     assert same_bits(dy.numpy(), O.expf(x))
 
 
+def test_powf_matches_c_library(hip):
+    """the device powf (GEM_A's final power) against the C library's on GEM_A's arguments (means over [2^-130, 2^8)
+    with y = 1/p), on random finite pairs and on the special cases"""
+    H = hip
+    rng = np.random.default_rng(1)
+    n = 1 << 21
+    xb = rng.integers(0x00400000, 0x43800000, n, dtype=np.uint64).astype(np.uint32)
+    ys = (np.float32(1) / np.array([1, 1.5, 2, 2.5, 3, 3.5, 4, 5, 6, 8, 10], np.float32)).astype(np.float32)
+    x = np.concatenate([xb.view(np.float32), rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32)
+                        .view(np.float32)])
+    y = np.concatenate([ys[rng.integers(0, ys.size, n)], (rng.standard_normal(n) * 8).astype(np.float32)])
+    sp = np.array([0, -0.0, 1, -1, 2, -2, 0.5, np.inf, -np.inf, np.nan, 1e-45, 3e38, -3], np.float32)
+    sy = np.array([0, -0.0, 1, -1, 2, 3, -3, 0.5, np.inf, -np.inf, np.nan, 1.5, 200], np.float32)
+    gx, gy = np.meshgrid(sp, sy)
+    x = np.concatenate([x, gx.ravel()]).astype(np.float32)
+    y = np.concatenate([y, gy.ravel()]).astype(np.float32)
+    say("powf", x.size)
+    dx, dy = H.DeviceArray.from_host(x), H.DeviceArray.from_host(y)
+    dz = H.DeviceArray(x.shape, np.float32)
+    H.check(H.lib().bnh_eval_powf(dx.ptr, dy.ptr, dz.ptr, x.size, None), "eval_powf")
+    H.sync()
+    assert same_bits(dz.numpy(), O.powf(x, y))
+
+
 def run_logmel(H, pcm, frame, hop, pad, nfft, window, mel, floor_, scale, slack=5):
     B, nsamp = pcm.shape
     nmel = mel.shape[0]
