@@ -110,6 +110,9 @@ static void fft_dit(float *re, float *im, int M, const float *twr, const float *
   }
 }
 
+/* the FFT on its own: M points of one lane in bit-reversed order, in place (for its order tests) */
+void orc_fft_dit(float *re, float *im, int M, const float *twr, const float *twi) { fft_dit(re, im, M, twr, twi); }
+
 int orc_logmel_frames(int nsamp, int frame, int hop, int pad) { return (nsamp + 2 * pad - frame) / hop + 1; }
 
 int orc_logmel(const float *pcm, int nsamp, int frame, int hop, int pad, int nfft, int nmel, const float *window,
@@ -231,23 +234,31 @@ void orc_stem_f32(const float *img, int H, int W, int k, int s, int Ho, int Wo, 
 /* the gate of v24k32_se_fc1 + se_gate_range (src/v24_f32.c:164-179, src/rt_ops_f32.c:269-283): mean = chsum * (1/P);
  * fc1 with eight lane chains (two 4-lane accumulators over 8-channel steps) summed pairwise, + b1, SiLU by the C
  * library's expf (silu_s, src/v24_f32.c:160); fc2 from the bias, one FMA per row r; sigmoid_f32x4 */
-void orc_se_gate_f32(const float *chsum, int C, int rd, int P, const float *w1, const float *b1, const float *w2t,
-                     const float *b2, float *gate) {
-  float *mean = malloc(sizeof(float) * C), *s1 = malloc(sizeof(float) * rd);
-  const float inv = 1.f / (float)P;
-  for (int c = 0; c < C; c++) mean[c] = chsum[c] * inv;
+/* the first FC of the SE gate (v24k32_se_fc1, src/v24_f32.c:164-179): per output r, eight lane chains over the
+ * channels (two 4-lane accumulators over 8-channel steps: channel c feeds chain c % 8, a 4-channel tail the first
+ * four), summed as ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)) (vaddvq of a0 + a1), + b1, SiLU by the C
+ * library's expf: s1 = x / (1 + expf(-x)). h16: the weights are rounded to fp16 first (SE_GATE16's fp16-held fc1) */
+void orc_se_fc1(const float *mean, int C, int rd, const float *w1, int h16, const float *b1, float *s1) {
   for (int r = 0; r < rd; r++) {
     float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     const float *w = w1 + (size_t)r * C;
     int c = 0;
     for (; c + 8 <= C; c += 8)
-      for (int l = 0; l < 8; l++) a[l] = fmaf(w[c + l], mean[c + l], a[l]);
+      for (int l = 0; l < 8; l++) a[l] = fmaf(h16 ? orc_h2f(orc_f2h(w[c + l])) : w[c + l], mean[c + l], a[l]);
     for (; c < C; c += 4)
-      for (int l = 0; l < 4; l++) a[l] = fmaf(w[c + l], mean[c + l], a[l]);
+      for (int l = 0; l < 4; l++) a[l] = fmaf(h16 ? orc_h2f(orc_f2h(w[c + l])) : w[c + l], mean[c + l], a[l]);
     const float v = ((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7])); /* vaddvq(a0 + a1) */
     const float x = v + b1[r];
     s1[r] = x / (1.f + expf(-x));
   }
+}
+
+void orc_se_gate_f32(const float *chsum, int C, int rd, int P, const float *w1, const float *b1, const float *w2t,
+                     const float *b2, float *gate) {
+  float *mean = calloc(C, sizeof(float)), *s1 = calloc(rd, sizeof(float));
+  const float inv = 1.f / (float)P;
+  for (int c = 0; c < C; c++) mean[c] = chsum[c] * inv;
+  orc_se_fc1(mean, C, rd, w1, 0, b1, s1);
   for (int c = 0; c < C; c++) {
     float g = b2[c];
     for (int r = 0; r < rd; r++) g = fmaf(w2t[(size_t)r * C + c], s1[r], g);
@@ -311,21 +322,11 @@ void orc_stem_f32to16(const float *img, int H, int W, int k, int s, int Ho, int 
  * fp16 */
 void orc_se_f16(uint16_t *D, int P, int C, const float *chsum, int rd, const float *w1, const float *b1, const float *w2t,
                 const float *b2) {
-  float *mean = malloc(sizeof(float) * C), *s1 = malloc(sizeof(float) * rd);
+  float *mean = calloc(C, sizeof(float)), *s1 = calloc(rd, sizeof(float));
   uint16_t *g = malloc(sizeof(uint16_t) * C);
   const float inv = 1.f / (float)P;
   for (int c = 0; c < C; c++) mean[c] = chsum[c] * inv;
-  for (int r = 0; r < rd; r++) {
-    float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const float *w = w1 + (size_t)r * C;
-    int c = 0;
-    for (; c + 8 <= C; c += 8)
-      for (int l = 0; l < 8; l++) a[l] = fmaf(w[c + l], mean[c + l], a[l]);
-    for (; c < C; c += 4)
-      for (int l = 0; l < 4; l++) a[l] = fmaf(w[c + l], mean[c + l], a[l]);
-    const float x = (((a[0] + a[4]) + (a[1] + a[5])) + ((a[2] + a[6]) + (a[3] + a[7]))) + b1[r];
-    s1[r] = x / (1.f + expf(-x));
-  }
+  orc_se_fc1(mean, C, rd, w1, 0, b1, s1);
   for (int c = 0; c < C; c++) {
     float v = b2[c];
     for (int r = 0; r < rd; r++) v = fmaf(w2t[(size_t)r * C + c], s1[r], v);

@@ -236,4 +236,13 @@ void orc_heads_s8(const float *F, const float *emb, int H, int W, int C, int hid
 #ifdef __cplusplus
 }
 #endif
+/* ---------------------------------------------------------------- sub-steps exposed for their order tests */
+/* fft_dit_x4 (src/fft_tab.h:25-80) on one lane */
+void orc_fft_dit(float *re, float *im, int M, const float *twr, const float *twi);
+/* v24k32_se_fc1 (src/v24_f32.c:164-179); h16: fp16-held weights (SE_GATE16, src/rt_ops_dot.c:381-420) */
+void orc_se_fc1(const float *mean, int C, int rd, const float *w1, int h16, const float *b1, float *s1);
+/* HEADS_S8's pooling and attention pooling of one head (src/rt_ops_dot.c:531-570) */
+void orc_heads_pool(const float *F, int H, int W, int C, int i, float *s, float *pooled);
+void orc_heads_softmax(float *att, const float *cla, int L, int nc, int ncp, float *logits);
+
 #endif

@@ -778,3 +778,55 @@ def powf(x, y):
     z = np.empty_like(x)
     lib().orc_powf_vec(P(x), P(y), P(z), x.size)
     return z
+
+
+_SIGS.update({
+    "orc_fft_dit": (None, [vp, vp, i32, vp, vp]),
+    "orc_se_fc1": (None, [vp, i32, i32, vp, i32, vp, vp]),
+    "orc_heads_pool": (None, [vp, i32, i32, i32, i32, vp, vp]),
+    "orc_heads_softmax": (None, [vp, vp, i32, i32, i32, vp]),
+})
+
+
+def fft_twiddles(M):
+    """fft_twiddles (src/fft_tab.h:9-14): e^{-2 pi i k / M}, k < M / 2, in double, rounded once to float."""
+    a = -2 * np.pi * np.arange(M // 2) / M
+    return np.cos(a).astype(np.float32), np.sin(a).astype(np.float32)
+
+
+def fft_dit(re, im):
+    """orc_fft_dit: M points (bit-reversed order) of one lane -> (re, im)."""
+    re, im = _c(re, np.float32).copy(), _c(im, np.float32).copy()
+    twr, twi = fft_twiddles(re.size)
+    lib().orc_fft_dit(P(re), P(im), re.size, P(twr), P(twi))
+    return re, im
+
+
+def se_fc1(mean, w1, b1, h16=False):
+    """orc_se_fc1: mean [C], w1 [rd][C], b1 [rd] -> s1 [rd]."""
+    w1 = _c(w1, np.float32)
+    rd, C = w1.shape
+    s1 = np.zeros(rd, np.float32)
+    lib().orc_se_fc1(P(_c(mean, np.float32)), C, rd, P(w1), int(h16), P(_c(b1, np.float32)), P(s1))
+    return s1
+
+
+def heads_pool(F, H, W, i):
+    """orc_heads_pool: F [H*W][C], head i -> (means [L][C], pooled [L][C])."""
+    F = _c(F, np.float32)
+    C = F.shape[-1]
+    L = H if i == 0 else W
+    s = np.zeros((L, C), np.float32)
+    pooled = np.zeros((L, C), np.float32)
+    lib().orc_heads_pool(P(F), H, W, C, i, P(s), P(pooled))
+    return s, pooled
+
+
+def heads_softmax(att, cla, nc, logits):
+    """orc_heads_softmax: att, cla [L][ncp] -> logits [ncp] (+= the attention-pooled class scores; att is clipped)."""
+    att = _c(att, np.float32).copy()
+    cla = _c(cla, np.float32)
+    lg = _c(logits, np.float32).copy()
+    L, ncp = att.shape
+    lib().orc_heads_softmax(P(att), P(cla), L, nc, ncp, P(lg))
+    return lg

@@ -260,15 +260,7 @@ void orc_se_gate16(float *chsum, int C, int rd, int P, const float *w1, const fl
   const float inv = 1.f / P;
   for (int ch = 0; ch < C; ch++) chsum[ch] *= inv;
   float tmp[4096];
-  for (int r = 0; r < rd; r++) {
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int ch = 0; ch < C; ch += 8)
-      for (int l = 0; l < 8; l++) acc[l] = fmaf(orc_h2f(orc_f2h(w1[(size_t)r * C + ch + l])), chsum[ch + l], acc[l]);
-    float s4[4];
-    for (int l = 0; l < 4; l++) s4[l] = acc[l] + acc[l + 4];
-    const float v = ((s4[0] + s4[1]) + (s4[2] + s4[3])) + b1[r];
-    tmp[r] = v / (1.f + expf(-v));
-  }
+  orc_se_fc1(chsum, C, rd, w1, 1, b1, tmp);
   for (int ch = 0; ch < C; ch++) {
     float g = b2[ch];
     for (int r = 0; r < rd; r++) g = fmaf(orc_h2f(orc_f2h(w2[(size_t)ch * rd + r])), tmp[r], g);
@@ -294,6 +286,59 @@ void orc_gem_a(const float *F, int M, int C, float eps, float p, float *e) {
   }
 }
 
+/* HEADS_S8's pooling of one head (src/rt_ops_dot.c:531-550): i = 0, per time step t < H the mean over W of F
+ * [H*W][C]; i = 1, per t < W the mean over H; each a sum from 0 in order of the other axis, divided by its length;
+ * then per t max-pool 3 (fmaxf from -FLT_MAX) + average-pool 3 (sum from 0 of v * 0.33333334f, multiply then add,
+ * in order of t - 1, t, t + 1, edges skipped): s [L][C] the means, pooled [L][C] */
+void orc_heads_pool(const float *F, int H, int W, int C, int i, float *s, float *pooled) {
+  const int Lt = i == 0 ? H : W;
+  for (int t = 0; t < Lt; t++)
+    for (int ch = 0; ch < C; ch++) {
+      float a2 = 0;
+      if (i == 0) {
+        for (int u = 0; u < W; u++) a2 += F[(size_t)(t * W + u) * C + ch];
+        s[t * C + ch] = a2 / W;
+      } else {
+        for (int u = 0; u < H; u++) a2 += F[(size_t)(u * W + t) * C + ch];
+        s[t * C + ch] = a2 / H;
+      }
+    }
+  for (int t = 0; t < Lt; t++)
+    for (int ch = 0; ch < C; ch++) {
+      float mx = -FLT_MAX, sum = 0;
+      for (int d = -1; d <= 1; d++) {
+        const int u = t + d;
+        if (u < 0 || u >= Lt) continue;
+        const float v = s[u * C + ch];
+        mx = fmaxf(mx, v);
+        sum += v * 0.33333334f;
+      }
+      pooled[t * C + ch] = mx + sum;
+    }
+}
+
+/* HEADS_S8's attention pooling of one head (src/rt_ops_dot.c:559-570): per class k < nc, att [L][ncp] clipped to
+ * [-10, 10] in place, mx = fmaxf over t from -FLT_MAX; then in order of t from 0: ev = expf(att - mx) (the C
+ * library's), z += ev, acc += ev * cla (multiply, then add); logits[k] += acc / z */
+void orc_heads_softmax(float *att, const float *cla, int L, int nc, int ncp, float *logits) {
+  for (int k = 0; k < nc; k++) {
+    float mx = -FLT_MAX;
+    for (int t = 0; t < L; t++) {
+      float a2 = att[(size_t)t * ncp + k];
+      a2 = a2 < -10.f ? -10.f : (a2 > 10.f ? 10.f : a2);
+      att[(size_t)t * ncp + k] = a2;
+      mx = fmaxf(mx, a2);
+    }
+    float z = 0, acc = 0;
+    for (int t = 0; t < L; t++) {
+      const float ev = expf(att[(size_t)t * ncp + k] - mx);
+      z += ev;
+      acc += ev * cla[(size_t)t * ncp + k];
+    }
+    logits[k] += acc / z;
+  }
+}
+
 /* HEADS_S8 (src/rt_ops_dot.c:520-572). logits [ncp] = lin(e) (int8 GEMM, 1 row), then for the head over H (i = 0:
  * per time step t < H the mean over W) and over W (i = 1: per t < W the mean over H): max-pool 3 + average-pool 3
  * (weights 0.33333334, zero-padded) of the means, fc + ReLU, att and cla (int8 GEMMs with per-row quantised inputs),
@@ -314,29 +359,7 @@ void orc_heads_s8(const float *F, const float *emb, int H, int W, int C, int hid
   orc_qd_gemm(a8, Kc, rq, 0, 1, ncp, Kc, wq[0], sc[0], ss[0], bb[0], &el);
   for (int i = 0; i < 2; i++) {
     const int Lt = i == 0 ? H : W, j = 1 + 3 * i;
-    for (int t = 0; t < Lt; t++)
-      for (int ch = 0; ch < C; ch++) {
-        float a2 = 0;
-        if (i == 0) {
-          for (int u = 0; u < W; u++) a2 += F[(size_t)(t * W + u) * C + ch];
-          s[t * C + ch] = a2 / W;
-        } else {
-          for (int u = 0; u < H; u++) a2 += F[(size_t)(u * W + t) * C + ch];
-          s[t * C + ch] = a2 / H;
-        }
-      }
-    for (int t = 0; t < Lt; t++)
-      for (int ch = 0; ch < C; ch++) {
-        float mx = -FLT_MAX, sum = 0;
-        for (int d = -1; d <= 1; d++) {
-          const int u = t + d;
-          if (u < 0 || u >= Lt) continue;
-          const float v = s[u * C + ch];
-          mx = fmaxf(mx, v);
-          sum += v * 0.33333334f;
-        }
-        pooled[t * C + ch] = mx + sum;
-      }
+    orc_heads_pool(F, H, W, C, i, s, pooled);
     orc_qd_quant_rows_f32(pooled, C, Lt, C, a8, Kc, Kc, rq);
     orc_qd_epi ef = {.act = 2, .out32 = h, .ldo = hid};
     orc_qd_gemm(a8, Kc, rq, 0, Lt, hid, Kc, wq[j], sc[j], ss[j], bb[j], &ef);
@@ -345,22 +368,7 @@ void orc_heads_s8(const float *F, const float *emb, int H, int W, int C, int hid
     orc_qd_gemm(a8, Kh, rq, 0, Lt, ncp, Kh, wq[j + 1], sc[j + 1], ss[j + 1], bb[j + 1], &ea);
     orc_qd_epi ec = {.act = 0, .out32 = cla, .ldo = ncp};
     orc_qd_gemm(a8, Kh, rq, 0, Lt, ncp, Kh, wq[j + 2], sc[j + 2], ss[j + 2], bb[j + 2], &ec);
-    for (int k = 0; k < nc; k++) {
-      float mx = -FLT_MAX;
-      for (int t = 0; t < Lt; t++) {
-        float a2 = att[(size_t)t * ncp + k];
-        a2 = a2 < -10.f ? -10.f : (a2 > 10.f ? 10.f : a2);
-        att[(size_t)t * ncp + k] = a2;
-        mx = fmaxf(mx, a2);
-      }
-      float z = 0, acc = 0;
-      for (int t = 0; t < Lt; t++) {
-        const float ev = expf(att[(size_t)t * ncp + k] - mx);
-        z += ev;
-        acc += ev * cla[(size_t)t * ncp + k];
-      }
-      logits[k] += acc / z;
-    }
+    orc_heads_softmax(att, cla, Lt, nc, ncp, logits);
   }
 }
 
