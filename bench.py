@@ -75,6 +75,8 @@ def parse():
     ap.add_argument("--f16-mfma", action="store_true",
                     help="v24_f16: run the fp16 1x1 convs on fp16 MFMA with fp32 accumulation (BNH_F16_MFMA=1) "
                          "instead of the reference's exact fp16 chains")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="default workload: skip the timed legs of configs 1-3 (depthwise, Winograd, v2.4 net)")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     return ap.parse_args()
@@ -428,7 +430,7 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def run_dw(a, H, rng, B, stream):
+def run_dw(a, H, rng, B, stream, emit=True):
     C, Hh, W, k, s = 672, 24, 64, a.k, a.s
     kind = a.workload[3:]
     d = dw_inputs(rng, B, C, Hh, W, k, s, kind)
@@ -481,6 +483,8 @@ def run_dw(a, H, rng, B, stream):
     line["parity_windows"] = dw_parity(dout.numpy(), d, kind, C, Hh, W, k, s, (0, B - 1))
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_dw(d, kind, C, Hh, W, k, s)
+    if not emit:
+        return line
     print(json.dumps(line), flush=True)
 
 
@@ -518,7 +522,7 @@ def cpu_baseline_wino(xp, w, b):
                       f"(numpy, BLAS threads as configured), {dt:.2f} s wall"}
 
 
-def run_wino(a, H, rng, B, stream):
+def run_wino(a, H, rng, B, stream, emit=True):
     Hh, W, C, K = 96, 256, 64, 64
     xp = np.zeros((B, Hh + 2, W + 2, C), np.float16)
     xp[:, 1:-1, 1:-1] = rng.standard_normal((B, Hh, W, C))
@@ -568,6 +572,8 @@ def run_wino(a, H, rng, B, stream):
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_wino(xp, w, b)
     L.bnh_wino16_free(P)
+    if not emit:
+        return line
     print(json.dumps(line), flush=True)
 
 
@@ -771,8 +777,6 @@ def run_perch(a, H, rng, B, stream):
     path = pn.write(os.path.join(tmp, "perch_v2_shaped_s8.bnpk"))
     L = binding.load_library()
     m = binding.Model(path)
-    os.unlink(path)
-    os.rmdir(tmp)
     nc, ne, ns = m.info.n_classes, m.info.emb_dim, m.info.n_samples
     # the batch: n_distinct synthetic windows, repeated; the CPU leg scores the same windows on the oracle and the
     # GPU's logits of every window of the batch (both sub-batches) are compared with them bit for bit
@@ -813,17 +817,82 @@ def run_perch(a, H, rng, B, stream):
     }
     line["roofline"] = perch_roofline(H, pn, B, stream, a)
     m.close()
+    line["host_buffers"] = host_buffers_leg(L, path, pcm, a)
+    os.unlink(path)
+    os.rmdir(tmp)
     # the GEMM takes ~0.15 ms: 200 untimed launches (~30 ms) bring the clocks back up after the host-side input
     # generation, and 300 timed ones average over ~45 ms
     line["gemm_s8"] = gemm_s8_leg(H, rng, B, stream, max(300, a.steps), 200)
     # the other int8 GEMM of the path, the prototype head (~1.1 ms a launch): 60 warmup launches, 100 timed
     line["gemm_s8_proto"] = proto_s8_leg(H, rng, B, stream, max(100, a.steps), 60)
+    if not a.no_legs:
+        line.update(config_legs(a, H, rng, stream))
     if not a.no_cpu:
         line["cpu_baseline"], ref = cpu_baseline_perch(pn, pcms)
         same = [bool(np.array_equal(logits[w].view(np.uint32), ref[w % n_distinct][:nc].view(np.uint32)))
                 for w in range(B)]
         line["parity_windows"] = f"{sum(same)}/{B} windows' logits bit-identical to the oracle's"
     print(json.dumps(line), flush=True)
+
+
+def host_buffers_leg(L, path, pcm, a):
+    """The Perch-shaped batch scored from host buffers through bnn_infer_batch (a fresh context): the PCIe copies of
+    the windows in and of the logits and embeddings out are inside the timed region. Reported beside the
+    device-resident rate, never as the value."""
+    from bnneon import binding
+    m = binding.Model(path)
+    B = pcm.shape[0]
+    out = np.empty((B, m.info.n_classes), np.float32)
+    emb = np.empty((B, m.info.emb_dim), np.float32)
+    status = np.zeros(B, np.int32)
+    pin = np.ascontiguousarray(pcm, np.float32)
+
+    def once():
+        r = m.L.bnn_infer_batch(m.ctx, binding._fp(pin), B, binding._fp(out), binding._fp(emb),
+                                status.ctypes.data_as(binding._IP))
+        if r != 0:
+            raise RuntimeError(f"bnn_infer_batch returned {r}")
+    for _ in range(3):
+        once()
+    n = max(5, a.steps // 2)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        once()
+    dt = (time.perf_counter() - t0) / n
+    m.close()
+    return {"value": round(B / dt, 1), "unit": "windows/s", "ms_per_batch": round(dt * 1e3, 3), "batches": n,
+            "note": "bnn_infer_batch from pageable host buffers (copies in and out included, host clock around "
+                    "each call); the line's value is the device-resident rate"}
+
+
+def compact_leg(line):
+    """The fields of a workload line that the default line carries for it."""
+    keep = ("value", "unit", "ms_per_step", "dtype", "parity_windows", "fp16_tflops", "direct_equivalent_tflops")
+    out = {k: line[k] for k in keep if k in line}
+    out["workload"] = line["config"]["workload"]
+    out["global_batch"] = line["config"]["global_batch"]
+    rf = line["roofline"]
+    out["roofline"] = {k: rf[k] for k in ("bound", "achieved", "peak", "unit", "frac", "kernel", "ms_per_launch")
+                       if k in rf}
+    return out
+
+
+def config_legs(a, H, rng, stream):
+    """The other configurations, each timed on its own, with its roofline fraction and its parity windows against
+    the oracle: config 1 (the depthwise convs at 5x5 stride 1, fp16 and int8, batch 64), config 2 (the fp16
+    Winograd conv, batch 64), config 3 (the v2.4-shaped fp16 net, batch 256)."""
+    legs = {}
+    for kind in ("f16", "s8"):
+        b = argparse.Namespace(**vars(a))
+        b.workload, b.k, b.s, b.no_cpu, b.steps, b.warmup = "dw_" + kind, 5, 1, True, max(50, a.steps), 10
+        legs[f"config1_dw_{kind}"] = compact_leg(run_dw(b, H, rng, 64, stream, emit=False))
+    b = argparse.Namespace(**vars(a))
+    b.workload, b.no_cpu, b.steps, b.warmup = "wino_f16", True, max(50, a.steps), 10
+    legs["config2_wino_f16"] = compact_leg(run_wino(b, H, rng, 64, stream, emit=False))
+    b = argparse.Namespace(**vars(a))
+    b.workload, b.no_cpu, b.steps, b.warmup = "v24_f16", True, max(20, a.steps), 5
+    legs["config3_v24_f16"] = compact_leg(run_v24(b, H, rng, 256, stream, emit=False))
+    return legs
 
 
 # Counter figures of the fused kernel's launch below (24 -> 144 expansion into the 3 x 3 stride-2 depthwise,
@@ -881,17 +950,23 @@ def perch_roofline(H, pn, B, stream, a):
     ms, _ = time_steps(H, stream, launch, max(10, a.steps), 3)
     nbytes = B * M * (Kp + 8) + B * o_ws * 4 + Np * Kp + 12 * Np + (k * k + 1) * C * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
-    valu_busy = PERCH_PWDW_VALU_INSTS * 4 / (ms * 1e-3 * SCLK_HZ * SIMDS)
-    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": PERCH_PWDW_TRAFFIC if B == 256 else None,
+    # the profile counted one launch over 256 windows; every window runs the same instructions
+    insts = PERCH_PWDW_VALU_INSTS * B / 256
+    issue = insts / (ms * 1e-3) / 1e9                      # G wave-instructions / s
+    peak_issue = SIMDS * SCLK_HZ / 4 / 1e9                  # a wave64 VALU instruction holds a SIMD 4 cycles
+    return {"bound": "valu", "achieved": round(issue, 1), "peak": round(peak_issue, 1),
+            "unit": "G VALU wave-instructions/s", "frac": round(issue / peak_issue, 4),
+            "traffic": PERCH_PWDW_TRAFFIC if B == 256 else None,
             "kernel": "k_pwdw_f32",
             "launch": f"PW_S8 {K}->{N} expansion fused into the {k}x{k}/{s} depthwise, {Hh}x{Wd} -> {Ho}x{Wo} px "
                       f"x {B} windows",
-            "ms_per_launch": round(ms, 4), "algorithmic_bytes_per_launch": nbytes,
-            "limiter": {"resource": "VALU issue", "frac": round(valu_busy, 3),
-                        "valu_wave_insts_per_launch": PERCH_PWDW_VALU_INSTS,
-                        "note": "frac = VALU wave instructions x 4 cycles / (this run's launch time x 2.4 GHz x "
-                                "1,024 SIMDs); instruction count and traffic from " + PERCH_PWDW_PROFILE}}
+            "ms_per_launch": round(ms, 4), "valu_wave_insts_per_launch": int(insts),
+            "algorithmic_bytes_per_launch": nbytes,
+            "hbm": {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "note": "the kernel recomputes each expanded value (dequantisation + exact SiLU) instead of storing it, "
+                    "so VALU issue binds it, not HBM: frac = its VALU wave instructions x 4 cycles / (this run's "
+                    "launch time x 2.4 GHz x 1,024 SIMDs); instruction count and traffic from " + PERCH_PWDW_PROFILE}
 
 
 def v24_counts(net):
@@ -926,7 +1001,7 @@ def cpu_baseline_v24(vn, rng):
                       f"-O2 -ffp-contract=off; {dt:.2f} s wall"}
 
 
-def run_v24(a, H, rng, B, stream):
+def run_v24(a, H, rng, B, stream, emit=True):
     import tempfile
     from bnneon import binding, v24net
     vn = v24net.V24Net(seed=7)
@@ -977,6 +1052,8 @@ def run_v24(a, H, rng, B, stream):
     line["parity_windows"] = v24_parity(vn, pcm, dout.numpy(), nc, (0, B - 1), a.f16_mfma)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline_v24(vn, rng)
+    if not emit:
+        return line
     print(json.dumps(line), flush=True)
 
 
@@ -986,7 +1063,8 @@ def v24_parity(vn, pcm, logits, nc, wins, f16_mfma):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle_net
     on = oracle_net.OracleNet(vn.net, 0, vn.net.last, vn.emb_buf)
-    refs = [on.run(pcm[i])[0][:nc].copy() for i in wins]
+    with concurrent.futures.ThreadPoolExecutor(len(wins)) as ex:   # one window per thread
+        refs = list(ex.map(lambda i: on.run(pcm[i])[0][:nc].copy(), wins))
     if not f16_mfma:
         same = sum(bool(np.array_equal(logits[i].view(np.uint32), r.view(np.uint32))) for i, r in zip(wins, refs))
         return f"{same}/{len(wins)} windows' logits bit-identical to the oracle's (windows {list(wins)})"
