@@ -460,6 +460,217 @@ __global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, 
   }
 }
 
+// ------------------------------------------------------------------ int8 GEMM + fp32 dequant epilogue, large K
+// For Kp > 64 the per-group K loop of k_s8n_gemm re-reads a row's int8 bytes once per 64-channel group and waits on
+// every fragment load; here a block owns a tile of TR = 64 WM rows x TN = 128 WN channels (WM x WN = 4 waves, each
+// 64 rows x 128 channels = 4 x 8 MFMA tiles, 128 accumulator registers) and walks K once: each 64-byte K step of the
+// tile's rows and weight rows is fetched from global memory into registers while the previous step's MFMAs run, then
+// staged in one of two LDS buffers (rows at an 80-byte stride: the 16 rows a fragment read serves land on disjoint
+// bank groups). Chunks at or past Kp load as zeros. The epilogue is k_s8n_gemm's, element for element.
+#define SL_STRIDE 80
+template <int WM, int WN, bool RES>
+__global__ __launch_bounds__(256, 2) void k_s8n_gemm_lds(const int8_t *__restrict__ q, long long q_ws,
+                                                         const float *__restrict__ sa, long long sa_ws,
+                                                         const int32_t *__restrict__ za, long long za_ws, int M,
+                                                         double rM, long long rows, const int8_t *__restrict__ wt,
+                                                         const float *__restrict__ sw, const int32_t *__restrict__ cs,
+                                                         const float *__restrict__ bias, int Kp, int Np, int Nt, int nct,
+                                                         EpiDev e) {
+  constexpr int TR = 64 * WM, TN = 128 * WN;
+  constexpr int ACH = TR * 4 / 256, BCH = TN * 4 / 256;  // 16-byte chunks per thread per K step
+  __shared__ __attribute__((aligned(16))) int8_t lds[2][(TR + TN) * SL_STRIDE];
+  __shared__ long long s_q[TR], s_o[TR], s_r[RES ? TR : 1];
+  __shared__ float s_sa[TR];
+  __shared__ uint32_t s_z[TR], s_tbl[256];
+  bnh_silu_table(s_tbl);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  // logical block: the channel tiles of a row tile consecutive, and consecutive blocks on one XCD (they share the
+  // tile's rows in L2)
+  const unsigned lb = bnh_xcd_block(blockIdx.x, gridDim.x);
+  const long long rowB = (long long)(lb / nct) * TR;
+  const int n0 = (int)(lb % nct) * TN;
+  for (int i = tid; i < TR; i += 256) {
+    const long long row = rowB + i < rows ? rowB + i : rows - 1;  // rows past the end repeat the last row
+    const int w = bnh_div(row, M, rM), m = (int)(row - (long long)w * M);
+    s_q[i] = w * q_ws + (long long)m * Kp;
+    s_o[i] = w * e.out_ws + epi_prow(m, e.ow, e.opad, e.r_ow) * e.ldo;
+    if (RES) s_r[i] = w * e.res_ws + epi_prow(m, e.rw, e.rpad, e.r_rw) * e.ldr;
+    s_sa[i] = sa[w * sa_ws + m];
+    s_z[i] = (uint32_t)za[w * za_ws + m];
+  }
+  __syncthreads();
+  // staging roles: chunk i = tid + 256 c of the step: row i / 4, 16-byte chunk i % 4
+  v4i ra[ACH], rb[BCH];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int c = 0; c < ACH; c++) {
+      const int i = tid + 256 * c, r = i >> 2, k = k0 + 16 * (i & 3);
+      ra[c] = k < Kp ? *(const v4i *)(q + s_q[r] + k) : (v4i){0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int c = 0; c < BCH; c++) {
+      const int i = tid + 256 * c, n = n0 + (i >> 2), k = k0 + 16 * (i & 3);
+      rb[c] = k < Kp && n < Nt ? *(const v4i *)(wt + (long long)n * Kp + k) : (v4i){0, 0, 0, 0};
+    }
+  };
+  auto stage = [&](int8_t *buf) {
+#pragma unroll
+    for (int c = 0; c < ACH; c++) {
+      const int i = tid + 256 * c;
+      *(v4i *)(buf + (i >> 2) * SL_STRIDE + 16 * (i & 3)) = ra[c];
+    }
+#pragma unroll
+    for (int c = 0; c < BCH; c++) {
+      const int i = tid + 256 * c;
+      *(v4i *)(buf + (TR + (i >> 2)) * SL_STRIDE + 16 * (i & 3)) = rb[c];
+    }
+  };
+  v4i acc[4][8];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[t][j] = (v4i){0, 0, 0, 0};
+  const int kc = (lane >> 4) * 16;
+  fetch(0);
+  stage(lds[0]);
+  __syncthreads();
+  int cur = 0;
+  for (int k0 = 0; k0 < Kp; k0 += 64) {
+    const bool more = k0 + 64 < Kp;
+    if (more) fetch(k0 + 64);  // in flight during this step's MFMAs
+    const int8_t *as = lds[cur], *bs = lds[cur] + TR * SL_STRIDE;
+    v4i a[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) a[t] = *(const v4i *)(as + (wm * 64 + 16 * t + (lane & 15)) * SL_STRIDE + kc);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const v4i b = *(const v4i *)(bs + (wn * 128 + 16 * j + (lane & 15)) * SL_STRIDE + kc);
+#pragma unroll
+      for (int t = 0; t < 4; t++) acc[t][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b, acc[t][j], 0, 0, 0);
+    }
+    if (more) {
+      stage(lds[cur ^ 1]);  // the other buffer: its last reads were before the previous barrier
+      __syncthreads();
+      cur ^= 1;
+    }
+  }
+  // epilogue (deq4 + activation + store_rows, src/gemm_s8n.c:105-135): acc[t][j][r] is row wm 64 + 16 t + 4 (lane >>
+  // 4) + r, channel n0 + wn 128 + 16 j + (lane & 15)
+  float swn[8], bn[8];
+  int32_t csn[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int n = n0 + wn * 128 + 16 * j + (lane & 15);
+    const bool in = n < Np;
+    swn[j] = in ? sw[n] : 0.f;
+    bn[j] = in ? bias[n] : 0.f;
+    csn[j] = in ? cs[n] : 0;
+  }
+  if (e.vec) {
+    // each 16-row tile through the wave's part of the (now idle) LDS buffers, [16][132] floats: the values
+    // dequantised and activated in the accumulator layout, then read back as 16-byte quads of a row (residual quads
+    // added) and stored whole, so every instruction writes whole 256-byte runs of rows
+    constexpr int TS = 132;
+    __syncthreads();  // every wave's last MFMA operand reads are done
+    float *T = (float *)&lds[0][0] + wave * 16 * TS;
+    const int nlim = Np - (n0 + wn * 128);  // channels of this wave's 128 that exist (a multiple of 4)
+    const int nq = (nlim < 128 ? nlim : 128) / 4;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int lr = wm * 64 + 16 * t + 4 * (lane >> 4) + r;
+        const float s_a = s_sa[lr];
+        const uint32_t z = s_z[lr];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int32_t c = (int32_t)((uint32_t)acc[t][j][r] - (uint32_t)csn[j] * z);
+          const float f = (float)c;
+          const float scl = swn[j] * s_a;
+          float y = f * scl;
+          y = y + bn[j];
+          if (e.act == 1) y = bnh_silu_f32_t(y, s_tbl);
+          else if (e.act == 2) y = bnh_relu_f32(y);
+          T[(4 * (lane >> 4) + r) * TS + 16 * j + (lane & 15)] = y;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // lane: quad (lane % 32) of rows 2 it + lane / 32
+      const int qd = lane & 31;
+      float4 rq[8];
+      if (RES) {  // every residual quad of the tile before any store (out and res may alias)
+#pragma unroll
+        for (int it = 0; it < 8; it++) {
+          const int rr = 2 * it + (lane >> 5), lr = wm * 64 + 16 * t + rr;
+          rq[it] = qd < nq && rowB + lr < rows
+                       ? *(const float4 *)(e.res + s_r[lr] + n0 + wn * 128 + 4 * qd)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < 8; it++) {
+        const int rr = 2 * it + (lane >> 5), lr = wm * 64 + 16 * t + rr;
+        if (qd < nq && rowB + lr < rows) {
+          float4 y = *(const float4 *)(T + rr * TS + 4 * qd);
+          if (RES) {
+            y.x = y.x + rq[it].x;
+            y.y = y.y + rq[it].y;
+            y.z = y.z + rq[it].z;
+            y.w = y.w + rq[it].w;
+          }
+          *(float4 *)(e.out + s_o[lr] + n0 + wn * 128 + 4 * qd) = y;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    // the tile's residuals first (out and res may alias: every load of the tile before its stores)
+    float rv[4][8];
+    if (RES) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int lr = wm * 64 + 16 * t + 4 * (lane >> 4) + r;
+        const float *rrow = e.res + s_r[lr];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int n = n0 + wn * 128 + 16 * j + (lane & 15);
+          rv[r][j] = n < Np && rowB + lr < rows ? rrow[n] : 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int lr = wm * 64 + 16 * t + 4 * (lane >> 4) + r;
+      if (rowB + lr >= rows) continue;
+      const float s_a = s_sa[lr];
+      const uint32_t z = s_z[lr];
+      float *orow = e.out + s_o[lr];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int n = n0 + wn * 128 + 16 * j + (lane & 15);
+        if (n >= Np) continue;
+        const int32_t c = (int32_t)((uint32_t)acc[t][j][r] - (uint32_t)csn[j] * z);
+        const float f = (float)c;
+        const float scl = swn[j] * s_a;
+        float y = f * scl;
+        y = y + bn[j];
+        if (e.act == 1) y = bnh_silu_f32_t(y, s_tbl);
+        else if (e.act == 2) y = bnh_relu_f32(y);
+        if (RES) y = y + rv[r][j];
+        orow[n] = y;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ int8 GEMM, Q31 requant, NCHW
 // A operand = x^T (pixels x K): x [K][M] has pixels contiguous, so each block stages a 64 k x 64 pixel tile through
 // LDS transposed to [pixel][k] (4 x 4 byte blocks transposed in registers with v_perm), from where lane l reads its
@@ -1354,6 +1565,28 @@ int bnh_s8n_gemm(const int8_t *q, long long q_ws, const float *sa, long long sa_
   // chip short of blocks (fewer than 1024)
   const long long nrb = bnh_ceil_div(rows, 128);
   const int ng = (W->Np + 63) / 64;
+  // large K with rows enough for 4 tiles per CU: the LDS-staged tile kernel (each row read once, fragment loads
+  // pipelined; config 0's 1152 -> 256 over 393,216 rows: 0.70 -> 0.32 ms). Fewer rows (the Perch-shaped
+  // projections, 16k-65k rows) keep the group-split kernel, which fills the chip with more, smaller blocks.
+  const bool wide = W->Np > 128;  // 128 rows x 256 channels, else 256 rows x 128 channels
+  const int TR = wide ? 128 : 256, TN = wide ? 256 : 128;
+  const int nct = (int)bnh_ceil_div(W->Np, TN);
+  const long long blocks = bnh_ceil_div(rows, TR) * nct;
+  if (W->Kp >= 256 && blocks >= 1024) {
+    // rows stored as 16-byte quads when every output (and residual) row start is 16-byte aligned
+    d.vec = W->Np % 4 == 0 && al4(e->out, e->out_ws, e->ldo) && (!e->res || al4(e->res, e->res_ws, e->ldr));
+    BNH_REQ(blocks < (1LL << 31));
+#define S8N_LDS_LAUNCH(WM_, WN_, RES_)                                                                             \
+  hipLaunchKernelGGL((k_s8n_gemm_lds<WM_, WN_, RES_>), dim3((unsigned)blocks), dim3(256), 0, s, q, q_ws, sa, sa_ws, za, \
+                     za_ws, M, rM, rows, W->w, W->sw, W->colsum, W->b, W->Kp, W->Np, W->Nt, nct, d)
+    if (wide && e->res) S8N_LDS_LAUNCH(2, 2, true);
+    else if (wide) S8N_LDS_LAUNCH(2, 2, false);
+    else if (e->res) S8N_LDS_LAUNCH(4, 1, true);
+    else S8N_LDS_LAUNCH(4, 1, false);
+#undef S8N_LDS_LAUNCH
+    BNH_HIP(hipGetLastError());
+    return 0;
+  }
   int gsplit = 1;
   if (nrb < 1024) gsplit = (int)bnh_ceil_div(1024, nrb);
   if (gsplit > ng) gsplit = ng;

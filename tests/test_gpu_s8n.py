@@ -156,7 +156,8 @@ def test_quant_rows_gate(hip):
     assert quant_case(hip, x, K, Kp, gate=g)
 
 
-def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, gate=False, ldo_extra=8, rpad=0):
+def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, gate=False, ldo_extra=8, rpad=0,
+            wins=None):
     H = hip
     rng = np.random.default_rng(seed)
     M = H_ * W_
@@ -196,7 +197,7 @@ def pw_case(hip, B, H_, W_, K, N, act, opad=0, res=False, lda_extra=0, seed=0, g
     out = dout.numpy().reshape(B, out_rows, ldo)
     q = dq.numpy().reshape(B, M4, Kp)
     ok = True
-    for bi in range(B):
+    for bi in (range(B) if wins is None else wins):
         ref_out, rq, rsa, rza = O.pw_s8(x[bi], pk, act=act, ldo=ldo, ow=W_ if opad else 0, opad=opad,
                                         res=None if rs is None else rs[bi], ldr=Np if res else 0,
                                         rpad=rpad, rw=W_ if rpad else 0, gate=None if gt is None else gt[bi])
@@ -215,6 +216,15 @@ def test_pw_s8_perch_shapes(hip, act):
 
 def test_pw_s8_config0_shape(hip):
     assert pw_case(hip, 2, 24, 64, 1152, 256, 1, seed=5)
+
+
+def test_pw_s8_large_k_tile_kernel(hip):
+    """Kp >= 256 with rows for 1024+ tiles: the LDS-staged tile GEMM (k_s8n_gemm_lds). 128 x 256 tiles at config 0's
+    1152 -> 256 (86 windows); 256 x 128 tiles with a residual from a zero-haloed buffer into a haloed output
+    (N = 100); ldo odd (values stored one by one) with a gate; windows at both ends and the middle checked"""
+    assert pw_case(hip, 86, 24, 64, 1152, 256, 1, seed=41, wins=(0, 43, 85))
+    assert pw_case(hip, 128, 32, 64, 320, 100, 2, opad=1, res=True, rpad=1, seed=42, wins=(0, 77, 127))
+    assert pw_case(hip, 86, 24, 64, 256, 200, 0, seed=43, gate=True, ldo_extra=1, wins=(0, 85))
 
 
 def test_pw_s8_residual_halo_gate(hip):
