@@ -852,15 +852,18 @@ def host_buffers_leg(L, path, pcm, a):
                                 status.ctypes.data_as(binding._IP))
         if r != 0:
             raise RuntimeError(f"bnn_infer_batch returned {r}")
-    for _ in range(3):
+    for _ in range(5):   # the context settles its stream split on its first five batches
         once()
     n = max(5, a.steps // 2)
-    t0 = time.perf_counter()
+    times = []
     for _ in range(n):
+        t0 = time.perf_counter()
         once()
-    dt = (time.perf_counter() - t0) / n
+        times.append(time.perf_counter() - t0)
+    dt = sum(times) / n
     m.close()
     return {"value": round(B / dt, 1), "unit": "windows/s", "ms_per_batch": round(dt * 1e3, 3), "batches": n,
+            "ms_per_batch_min_max": [round(min(times) * 1e3, 3), round(max(times) * 1e3, 3)],
             "note": "bnn_infer_batch from pageable host buffers (copies in and out included, host clock around "
                     "each call); the line's value is the device-resident rate"}
 

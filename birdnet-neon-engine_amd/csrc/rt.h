@@ -92,6 +92,16 @@ struct rt_ctx {
   hipEvent_t sub_fork[RT_MAXSUB], sub_join[RT_MAXSUB];
   int n_sub;             // sub-batch streams created, including the context's own
   int one_stream;        // never split a batch over two streams
+  // Whether batches run as two sub-batches or on the context's stream alone is measured on the context's first
+  // batches of one size (64 windows or more): split_choice -1 while undecided, then 0 (two) or 1 (one stream)
+  int split_choice;
+  int tune_seen;         // batches of tune_B windows finished while undecided
+  int tune_B;
+  double tune_best[2];   // per mode (0 two sub-batches, 1 one stream): the least wall seconds per window measured
+  int tune_n[2];
+  int batch_open;        // a batch's first range has been launched and the batch has not finished
+  int batch_mode;        // the mode that batch runs in
+  double batch_t0;
   int f16_mfma;          // fp16 PW ops on fp16 MFMA (fp32 accumulation) instead of the reference's exact fp16 chains
   size_t *slot_bytes;    // per slot: bytes of one window's copy (64-aligned, >= 64 bytes of zero slack)
   int *slot_users;       // per slot: the number of buffers placed in it
@@ -141,6 +151,10 @@ int rt_reserve(rt_ctx *c, int windows, char *err, size_t errlen);
 // run every op over windows [0, B) whose input already sits in buffer in_buf; fills status[B] (0 = scored, else
 // 1 + the failing op index) and returns the number of failed windows, or -1 on a device error (err set)
 int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen);
+// the same in two halves, for windows [W0, W0 + B) of the arena: the launches on the context's stream (after whatever
+// it holds), then the wait and the windows' status (the number of failed windows, or -1)
+int rt_launch_range(rt_ctx *c, int W0, int B, char *err, size_t errlen);
+int rt_finish_range(rt_ctx *c, int W0, int B, int *status, char *err, size_t errlen);
 int rt_op_src(const rt_ctx *c, int i, char *buf, size_t n);
 const char *rt_op_name(const rt_ctx *c, int i);
 const char *rt_dtype_name(uint32_t dt);

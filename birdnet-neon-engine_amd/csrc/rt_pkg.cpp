@@ -410,8 +410,11 @@ rt_ctx *rt_ctx_new(rt_pkg *p, int pi, char *err, size_t errlen, int *kind) {
   }
   const char *fe = getenv("BNH_FUSE");  // BNH_FUSE=0 runs every op as the package lists it
   if (!fe || atoi(fe) != 0) fuse_ops(c);
-  const char *se = getenv("BNH_SPLIT");  // BNH_SPLIT=0 runs every batch on one stream
+  // BNH_SPLIT=0 runs every batch on one stream, BNH_SPLIT=1 splits every batch of 64 windows or more; unset, the
+  // context measures both on its first batches and keeps the faster
+  const char *se = getenv("BNH_SPLIT");
   c->one_stream = se && atoi(se) == 0;
+  c->split_choice = se ? (atoi(se) == 0 ? 1 : 0) : -1;
   const char *fm = getenv("BNH_F16_MFMA");  // BNH_F16_MFMA=1: fp16 PW ops accumulate in fp32 on the matrix cores
   c->f16_mfma = fm && atoi(fm) == 1;
   const char *pe = getenv("BNN_PROF");
@@ -425,6 +428,30 @@ static double now_s(void) {
   struct timespec t;
   clock_gettime(CLOCK_MONOTONIC, &t);
   return t.tv_sec + t.tv_nsec * 1e-9;
+}
+
+// Two sub-batches on two streams run 8 % faster than one stream on the Perch-shaped net when the HIP runtime maps
+// the two streams to different hardware queues; when it maps them to the same queue (it multiplexes a process's
+// streams over a few queues, and which ones share depends on what the process created and destroyed before),
+// measured on the MI355X: 1.4x slower than one stream. The library cannot see the mapping, so each context times
+// its first batches of one size (64 windows or more): one untimed, two split, two on one stream, and keeps one
+// stream only when it was at least 10 % faster.
+static int tune_mode(const rt_ctx *c) {
+  return c->tune_seen >= 3 ? 1 : 0;  // batches 0 (untimed), 1, 2 split; 3, 4 one stream
+}
+
+static void tune_note(rt_ctx *c, int B, double secs) {
+  if (B < 64) return;
+  if (c->tune_seen == 0) c->tune_B = B;
+  if (B != c->tune_B) return;
+  const int mode = c->batch_mode;
+  if (c->tune_seen > 0) {
+    const double per = secs / B;
+    if (!c->tune_n[mode] || per < c->tune_best[mode]) c->tune_best[mode] = per;
+    c->tune_n[mode]++;
+  }
+  c->tune_seen++;
+  if (c->tune_n[0] >= 2 && c->tune_n[1] >= 2) c->split_choice = c->tune_best[1] < 0.9 * c->tune_best[0] ? 1 : 0;
 }
 
 // the streams and fork / join events of sub-batches 1 .. n - 1, created once (fewer when the runtime refuses them)
@@ -450,10 +477,18 @@ static int ensure_subs(rt_ctx *c, int n) {
 }
 
 int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
-  if (B > c->bcap) { snprintf(err, errlen, "rt_run_batch: %d windows but the arena holds %d", B, c->bcap); return -1; }
-  if (hipMemsetAsync(c->win_fail, 0, sizeof(int) * (size_t)B, c->stream) != hipSuccess) {
+  if (rt_launch_range(c, 0, B, err, errlen)) return -1;
+  return rt_finish_range(c, 0, B, status, err, errlen);
+}
+
+int rt_launch_range(rt_ctx *c, int W0, int B, char *err, size_t errlen) {
+  if (W0 < 0 || B < 1 || W0 + B > c->bcap) {
+    snprintf(err, errlen, "rt_run_batch: windows %d..%d but the arena holds %d", W0, W0 + B - 1, c->bcap);
+    return c->batch_open = 0, -1;
+  }
+  if (hipMemsetAsync(c->win_fail + W0, 0, sizeof(int) * (size_t)B, c->stream) != hipSuccess) {
     snprintf(err, errlen, "device error clearing the window flags");
-    return -1;
+    return c->batch_open = 0, -1;
   }
   // Sub-batches on their own streams, their launches interleaved op by op: the windows are independent, so the GPU
   // may run one sub-batch's kernel beside another's (a VALU-bound kernel beside a memory-bound one). Sub-batch h
@@ -462,8 +497,13 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
   // stream waits for every sub-batch at the end.
   // two sub-batches (measured: three or four, on as many streams, are 15-25 % slower on both nets; one op of skew is
   // 1.5-1.7 % faster than none, four or more slower)
+  if (!c->batch_open) {
+    c->batch_open = 1;
+    c->batch_t0 = now_s();
+    c->batch_mode = c->split_choice >= 0 ? c->split_choice : tune_mode(c);
+  }
   int ns = 2;
-  if (c->prof || c->one_stream || B < 64) ns = 1;
+  if (c->prof || c->one_stream || B < 64 || c->batch_mode == 1) ns = 1;
   if (ns > RT_MAXSUB) ns = RT_MAXSUB;
   while (ns > 1 && B / ns < 32) ns--;  // sub-batches of at least 32 windows
   if (ns > 1) ns = ensure_subs(c, ns);
@@ -484,10 +524,10 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
       if (h && i == 0 && hipStreamWaitEvent(c->sub_stream[h], c->sub_fork[h], 0) != hipSuccess) {
         drain();
         snprintf(err, errlen, "device error starting sub-batch %d", h);
-        return -1;
+        return c->batch_open = 0, -1;
       }
       c->fail_op = i;  // ops read it to tag the windows they fail
-      c->w0 = first(h);
+      c->w0 = W0 + first(h);
       c->nwin = first(h + 1) - first(h);
       c->stream = strm(h);
       int r = op->k->run(c, op);
@@ -502,7 +542,7 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
         const char *why = bnh_last_error();
         snprintf(err, errlen, "op %d %s%s%s%s: launch failed (%s)", i, op->k->name, src[0] ? " (ONNX node " : "", src,
                  src[0] ? ")" : "", why && why[0] ? why : hipGetErrorString(hipGetLastError()));
-        return -1;
+        return c->batch_open = 0, -1;
       }
       if (c->prof) {
         hipStreamSynchronize(c->stream);
@@ -517,12 +557,19 @@ int rt_run_batch(rt_ctx *c, int B, int *status, char *err, size_t errlen) {
         hipStreamWaitEvent(s1, c->sub_join[h], 0) != hipSuccess) {
       drain();
       snprintf(err, errlen, "device error joining sub-batch %d", h);
-      return -1;
+      return c->batch_open = 0, -1;
     }
   c->fail_op = -1;
-  hipError_t e = hipMemcpyAsync(status, c->win_fail, sizeof(int) * (size_t)B, hipMemcpyDeviceToHost, c->stream);
+  return 0;
+}
+
+int rt_finish_range(rt_ctx *c, int W0, int B, int *status, char *err, size_t errlen) {
+  hipError_t e = hipMemcpyAsync(status, c->win_fail + W0, sizeof(int) * (size_t)B, hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  const bool opened = c->batch_open;
+  c->batch_open = 0;
   if (e != hipSuccess) { snprintf(err, errlen, "device error after the op list: %s", hipGetErrorString(e)); return -1; }
+  if (opened && c->split_choice < 0) tune_note(c, B, now_s() - c->batch_t0);
   c->nprof += B;
   int nf = 0;
   for (int w = 0; w < B; w++) nf += status[w] != 0;

@@ -239,3 +239,47 @@ def test_pw_s8_into_depthwise(hip, tmp_path, form, k, s):
             ro, rc = O.dw3_f32(xp, H, W, N, s, wd, bd, Ho, Wo)
         assert same(out[i], ro.reshape(-1)), i
         assert same(emb[i], rc), i
+
+
+def test_host_batch_staged_chunks(hip, tmp_path):
+    """300 windows from host buffers run in pinned chunks of 128 (the last one partial), each uploaded while the
+    previous one runs: the same bits as calls of 37 windows (one chunk each) and as the oracle; a window of extreme
+    input in the second chunk fails alone, with its status and the message"""
+    spec = Spec(3)
+    path = spec.package(str(tmp_path / "net.bnpk"))
+    rng = np.random.default_rng(8)
+    n = 300
+    pcm = (rng.standard_normal((n, spec.M * spec.K0)) * 0.5).astype(np.float32)
+    pcm[170] = np.where(np.arange(pcm.shape[1]) % 2, -1.5e38, 1.5e38)   # overflows to non-finite logits
+    say("runtime staged host batch", n)
+    with binding.Model(path) as m:
+        out, _, status = m.infer_batch(pcm, check=False)
+        assert [w for w in range(n) if status[w]] == [170] and status[170] == 3
+        with pytest.raises(binding.BnnError) as e:
+            m.infer_batch(pcm)
+        assert e.value.kind == "window" and "window 170 of 300" in str(e.value)
+        small = np.concatenate([m.infer_batch(pcm[i:i + 37], check=False)[0] for i in range(0, n, 37)])
+    ok = [w for w in range(n) if w != 170]
+    assert same(out[ok], small[ok])
+    for w in (0, 127, 128, 255, 256, 299):
+        rc, ref = spec.oracle(pcm[w])
+        assert rc == 0 and same(out[w], ref), w
+
+
+def test_stream_split_choice_keeps_bits(hip, tmp_path):
+    """A context times its first batches of one size split over two streams and on one stream, then keeps the faster:
+    seven calls of the same 130 windows from host buffers (the first five in the measuring order: one untimed and two
+    split, then two on one stream) give bit-identical logits, equal to the oracle's"""
+    spec = Spec(3)
+    path = spec.package(str(tmp_path / "net.bnpk"))
+    rng = np.random.default_rng(9)
+    n = 130
+    pcm = (rng.standard_normal((n, spec.M * spec.K0)) * 0.5).astype(np.float32)
+    say("runtime split choice", n)
+    with binding.Model(path) as m:
+        outs = [m.infer_batch(pcm)[0] for _ in range(7)]
+    for o in outs[1:]:
+        assert same(o, outs[0])
+    for w in (0, 64, 129):
+        rc, ref = spec.oracle(pcm[w])
+        assert rc == 0 and same(outs[0][w], ref), w
