@@ -1119,6 +1119,233 @@ __global__ __launch_bounds__(256) void k_dw_s8(const int8_t *__restrict__ x, lon
   }
 }
 
+// ------------------------------------------------------------------ int8 depthwise, stride 1, row-streamed
+// A block computes 32 channels x 64 output columns of one window over a segment of output rows, 4 rows a step, with
+// the input rows it needs in an LDS ring of 8 row slots (blocks numbered channel group fastest, then column tile,
+// segment and window, XCD-contiguous, so that the blocks reading the same pixels' other channels share an L2). In
+// the ring each input row is held as planes of one channel, a word holding 4 consecutive columns, written from
+// 16-byte loads (4 columns x 16 channels) transposed 4 x 4 in registers; pixels outside the image (and channels
+// past C) hold the zero point, so that w (x - zx) vanishes there and acc = bias - zx sum_t w[t] + sum_t w[t] x[t]
+// (mod 2^32) holds for every output, as in k_dw_s8. A thread owns one channel and 8 consecutive output columns: per
+// tap row it reads the 3 words covering its 8 + K - 1 input columns, and output column 4h + r of its 8 takes its K
+// taps as v_dot4 of words h and h + 1 with the row's weights shifted by r bytes (prepared once per thread for the
+// four shifts), so no byte realignment is done per tap. While a step computes, the loads of the next step's 4 input
+// rows are in flight in registers; they go into the ring slots of the 4 rows the step no longer needs after it.
+// The requantised bytes go through LDS planes, are transposed back to 4-channel words and stored as 16 bytes.
+constexpr int kDwtStep = 4, kDwtSeg = 12;
+template <int K, int CT, int TW>
+struct DwtShape {
+  static constexpr int NG = CT / 16;                    // 16-channel groups
+  static constexpr int NR = kDwtStep + K - 1;           // input rows a step reads
+  static constexpr int IW = (TW + K - 1 + 3) / 4;       // input words per row and channel
+  static constexpr int PI = (8 * IW) | 1;               // words per channel plane of the 8-slot ring (odd: the 32
+                                                        // channels' reads of one word fall in 32 banks)
+  static constexpr int OW = TW / 4;                     // output words per row
+  static constexpr int PO = (kDwtStep * OW) | 1;
+  static_assert(NR <= 8, "a step's input rows fit the ring");
+};
+
+template <int K, int CT, int TW, bool LUT>
+__global__ __launch_bounds__(256) void k_dw_s8_t(const int8_t *__restrict__ x, long long x_ws, unsigned x_len, int H,
+                                                 int W, int C, int pt, int pl, const int8_t *__restrict__ w,
+                                                 const int32_t *__restrict__ bias, const int32_t *__restrict__ mult,
+                                                 const int32_t *__restrict__ shift, int zx, int zy, int lo, int hi,
+                                                 const int8_t *__restrict__ lut, int8_t *__restrict__ out,
+                                                 long long o_ws, unsigned o_len, int Ho, int Wo, int ncg, int ntx,
+                                                 int nseg) {
+  using S = DwtShape<K, CT, TW>;
+  static_assert(CT * TW / 8 == 256, "a thread per channel and 8 columns");
+  __shared__ uint32_t s_in[CT * S::PI];
+  __shared__ uint32_t s_out[CT * S::PO];
+  __shared__ int8_t s_lut[256];
+  const int tid = threadIdx.x;
+  if (LUT) s_lut[tid] = lut[tid];
+  unsigned L = bnh_xcd_block(blockIdx.x, gridDim.x);
+  const int cg = (int)(L % (unsigned)ncg);
+  L /= (unsigned)ncg;
+  const int tx = (int)(L % (unsigned)ntx);
+  L /= (unsigned)ntx;
+  const int sg = (int)(L % (unsigned)nseg);
+  const int win = (int)(L / (unsigned)nseg);
+  const int c0 = cg * CT, ox0 = tx * TW, oy0 = sg * kDwtSeg, ix0 = ox0 - pl, iy0 = oy0 - pt;
+  const int nstep = (min(kDwtSeg, Ho - oy0) + kDwtStep - 1) / kDwtStep;
+  const uint32_t zxw = (uint32_t)(uint8_t)zx * 0x01010101u;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)x, 0, (int)x_len, 0x00020000);
+  const int xw = (int)(win * x_ws);
+  // unit u of a set of input rows = (row of the set, word wd, 16-channel group g), g fastest: 4 columns x 16
+  // channels as four 16-byte loads (the zero point outside the image and for channels past C)
+  auto load_unit = [&](int u, int r0, v4i (&v)[4]) {
+    const int g = u % S::NG, p = u / S::NG, rr = p / S::IW, wd = p - rr * S::IW;
+    const int iy = iy0 + r0 + rr, ixb = ix0 + 4 * wd, c = c0 + 16 * g;
+    const bool rok = (unsigned)iy < (unsigned)H;
+    const int ro = xw + iy * W * C + c;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int ix = ixb + i;
+      if (rok && (unsigned)ix < (unsigned)W) {
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, ro + ix * C, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          if (c + 4 * j >= C) v[i][j] = (int)zxw;
+      } else {
+        v[i] = v4i{(int)zxw, (int)zxw, (int)zxw, (int)zxw};
+      }
+    }
+  };
+  // ... and its four 4 x 4 transposes into the ring: word wd of row r0 + rr's slot in planes 16g .. 16g + 15
+  auto put_unit = [&](int u, int r0, const v4i (&v)[4]) {
+    const int g = u % S::NG, p = u / S::NG, rr = p / S::IW, wd = p - rr * S::IW;
+    const int at = ((r0 + rr) & 7) * S::IW + wd;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint32_t t[4];
+      transpose4x4((uint32_t)v[0][j], (uint32_t)v[1][j], (uint32_t)v[2][j], (uint32_t)v[3][j], t);  // t[i]: channel
+#pragma unroll                                                                                     // c + 4j + i
+      for (int i = 0; i < 4; i++) s_in[(16 * g + 4 * j + i) * S::PI + at] = t[i];
+    }
+  };
+  // the first step's input rows
+  for (int u = tid; u < S::NR * S::IW * S::NG; u += 256) {
+    v4i v[4];
+    load_unit(u, 0, v);
+    put_unit(u, 0, v);
+  }
+  // the thread's channel, its weights per tap row and shift, and its requantisation
+  const int ch = tid % CT, sub = tid / CT, c = c0 + ch;
+  const bool cok = c < C;
+  // ws[ky][r][h]: byte p = w[ky][4h + p - r] (0 where that tap index is outside 0..K-1), from the row's taps packed
+  // into two words (w0..w3, w4..w7 with zeros past K): word 0 is the first shifted up by r bytes, word 1 the pair
+  // shifted by r bytes across the word boundary
+  uint32_t ws[K][4][2];
+  uint32_t wsum = 0;
+#pragma unroll
+  for (int ky = 0; ky < K; ky++) {
+    uint32_t W0 = 0, W1 = 0;
+#pragma unroll
+    for (int kx = 0; kx < K; kx++) {
+      const int32_t v = cok ? (int32_t)w[(ky * K + kx) * C + c] : 0;
+      wsum += (uint32_t)v;
+      if (kx < 4) W0 |= ((uint32_t)v & 0xffu) << (8 * kx);
+      else W1 |= ((uint32_t)v & 0xffu) << (8 * (kx - 4));
+    }
+    ws[ky][0][0] = W0;
+    ws[ky][0][1] = W1;
+#pragma unroll
+    for (int r = 1; r < 4; r++) {
+      ws[ky][r][0] = W0 << (8 * r);
+      ws[ky][r][1] = __builtin_amdgcn_alignbyte(W1, W0, 4 - r);
+    }
+  }
+  const int32_t a0 = cok ? (int32_t)((uint32_t)bias[c] - (uint32_t)zx * wsum) : 0;
+  const int32_t m = cok ? mult[c] : 0, e = cok ? shift[c] : 1;
+  const bool nowrap = (a0 < 0 ? -(long long)a0 : (long long)a0) + (long long)K * K * 16384 < (1LL << 31);
+  // the short requantisation of k_dw_s8 (shift in 1..31, sums that cannot wrap, zy <= lo) when the whole wave
+  // qualifies, else the general one
+  const bool fast = __all(e >= 1 && e <= 31 && nowrap && zy <= lo);
+  const long long rnd = (1LL << 30) + (1LL << (30 + (fast ? e : 1)));
+  const int e1 = fast ? e - 1 : 0, lz = lo - zy, hz = hi - zy, zy128 = zy + 128;
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc((void *)out, 0, (int)o_len, 0x00020000);
+  const int ow = (int)(win * o_ws);
+  __syncthreads();
+  // one step: output rows oy0 + 4 st .. + 3 from ring rows 4 st .. 4 st + NR - 1; FAST picks the requantisation,
+  // B = (4 st) & 7 the ring slot of the step's first input row
+  auto step = [&]<bool FAST, int B>(int st) {
+    auto requant = [&](int32_t a) -> uint32_t {
+      int32_t y;
+      if (FAST) {
+        const int32_t v = (int32_t)(((long long)a * m + rnd) >> 32) >> e1;
+        asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y) : "v"(v), "v"(lz), "v"(hz));
+        if (LUT) return (uint32_t)(uint8_t)s_lut[y + zy128];  // the table at y + zy
+        y += zy;
+      } else {
+        y = bnh_requant(a, m, e, zy, lo, hi);
+        if (LUT) y = s_lut[y + 128];
+      }
+      return (uint32_t)y & 0xffu;
+    };
+    // the next step's 4 new input rows (ring rows 4 st + NR ..), in flight while this step computes
+    const bool more = st + 1 < nstep;
+    constexpr int NPF = kDwtStep * S::IW * S::NG, PFI = (NPF + 255) / 256;  // units of the 4 rows, per thread
+    const int r_next = 4 * st + S::NR;
+    v4i pv[PFI][4];
+#pragma unroll
+    for (int i = 0; i < PFI; i++)
+      if (more && tid + 256 * i < NPF) load_unit(tid + 256 * i, r_next, pv[i]);
+    uint32_t res[kDwtStep][2];
+    const uint32_t *plane = s_in + ch * S::PI + 2 * sub;
+#pragma unroll
+    for (int oy = 0; oy < kDwtStep; oy++) {
+      int32_t acc[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) acc[q] = a0;
+#pragma unroll
+      for (int ky = 0; ky < K; ky++) {
+        const uint32_t *row = plane + ((B + oy + ky) & 7) * S::IW;
+        const uint32_t A[3] = {row[0], row[1], row[2]};
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const int h = q >> 2, r = q & 3;
+          acc[q] = __builtin_amdgcn_sdot4((int)A[h], (int)ws[ky][r][0], acc[q], false);
+          if (r >= 5 - K) acc[q] = __builtin_amdgcn_sdot4((int)A[h + 1], (int)ws[ky][r][1], acc[q], false);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+        res[oy][h] = requant(acc[4 * h]) | requant(acc[4 * h + 1]) << 8 | requant(acc[4 * h + 2]) << 16 |
+                     requant(acc[4 * h + 3]) << 24;
+    }
+    __syncthreads();  // the step's reads of the ring and the previous step's reads of s_out are done
+#pragma unroll
+    for (int oy = 0; oy < kDwtStep; oy++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) s_out[ch * S::PO + oy * S::OW + 2 * sub + h] = res[oy][h];
+#pragma unroll
+    for (int i = 0; i < PFI; i++)
+      if (more && tid + 256 * i < NPF) put_unit(tid + 256 * i, r_next, pv[i]);
+    __syncthreads();
+    // store: unit = (output row, word wd, 16-channel group g), g fastest: sixteen plane words, four transposes back,
+    // four 16-byte stores (word by word for a group that reaches past C)
+    for (int u = tid; u < kDwtStep * S::OW * S::NG; u += 256) {
+      const int g = u % S::NG, p = u / S::NG, oy = p / S::OW, wd = p - oy * S::OW;
+      const int y = oy0 + 4 * st + oy, cq = c0 + 16 * g;
+      if (y < Ho && cq < C) {
+        v4i v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          uint32_t t[4], o4[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) t[i] = s_out[(16 * g + 4 * j + i) * S::PO + p];
+          transpose4x4(t[0], t[1], t[2], t[3], o4);  // o4[col]: the column's channels cq + 4j .. + 3
+#pragma unroll
+          for (int col = 0; col < 4; col++) v[col][j] = (int)o4[col];
+        }
+        const int o = ow + (y * Wo + ox0 + 4 * wd) * C + cq;
+        const bool whole = cq + 16 <= C;
+#pragma unroll
+        for (int col = 0; col < 4; col++) {
+          if (ox0 + 4 * wd + col >= Wo) break;
+          if (whole) {
+            __builtin_amdgcn_raw_buffer_store_b128(v[col], orr, o + col * C, 0, 0);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+              if (cq + 4 * j < C) __builtin_amdgcn_raw_buffer_store_b32(v[col][j], orr, o + col * C + 4 * j, 0, 0);
+          }
+        }
+      }
+    }
+  };
+  for (int st = 0; st < nstep; st++) {
+    if (fast) {
+      if (st & 1) step.template operator()<true, 4>(st);
+      else step.template operator()<true, 0>(st);
+    } else {
+      if (st & 1) step.template operator()<false, 4>(st);
+      else step.template operator()<false, 0>(st);
+    }
+  }
+}
+
 // ================================================================== host side
 template <typename T, typename L>
 static void dispatch_ks(int k, int s, L &&launch) {
@@ -1410,6 +1637,19 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
   return 0;
 }
 
+}  // extern "C"
+
+// BNH_DW_S8=strip runs stride-1 3x3 / 5x5 int8 depthwise convs on the strip kernel (k_dw_s8) instead of the
+// row-streamed one (k_dw_s8_t), for comparison; results are the same bytes
+static bool dw_s8_tiled() {
+  static const bool tiled = [] {
+    const char *e = getenv("BNH_DW_S8");
+    return !(e && strcmp(e, "strip") == 0);
+  }();
+  return tiled;
+}
+
+extern "C" {
 int bnh_dw_s8(const int8_t *x, long long x_ws, int H, int W, int C, int k, int s, int pt, int pl, const int8_t *w,
               const int32_t *bias, const int32_t *mult, const int32_t *shift, int zx, int zy, int lo, int hi,
               const int8_t *lut, int8_t *out, long long o_ws, int Ho, int Wo, int B, void *stream) {
@@ -1423,11 +1663,34 @@ int bnh_dw_s8(const int8_t *x, long long x_ws, int H, int W, int C, int k, int s
   const long long x_len = (long long)(B - 1) * x_ws + (long long)H * W * C;
   const long long o_len = (long long)(B - 1) * o_ws + (long long)Ho * Wo * C;
   BNH_REQ(x_len < (1LL << 31) && o_len < (1LL << 31) && (long long)k * k * C < (1LL << 31));
+  hipStream_t st = bnh_stream(stream);
+  // stride 1 with 3 x 3 or 5 x 5 taps: the LDS-tiled kernel
+  if (s == 1 && (k == 3 || k == 5) && dw_s8_tiled()) {
+    // 32 channels x 64 columns a block (64 or 128 channels with 32 or 16 columns measured the same or slower)
+    auto launch = [&]<int K, int CT>() {
+      constexpr int TW = 2048 / CT;
+      const int ncg = (int)bnh_ceil_div(C, CT), ntx = (int)bnh_ceil_div(Wo, TW);
+      const int nseg = (int)bnh_ceil_div(Ho, kDwtSeg);
+      const long long nblk = (long long)ncg * ntx * nseg * B;
+      if (nblk >= (1LL << 31)) return;
+      if (lut)
+        hipLaunchKernelGGL((k_dw_s8_t<K, CT, TW, true>), dim3((unsigned)nblk), dim3(256), 0, st, x, x_ws,
+                           (unsigned)x_len, H, W, C, pt, pl, w, bias, mult, shift, zx, zy, lo, hi, lut, out, o_ws,
+                           (unsigned)o_len, Ho, Wo, ncg, ntx, nseg);
+      else
+        hipLaunchKernelGGL((k_dw_s8_t<K, CT, TW, false>), dim3((unsigned)nblk), dim3(256), 0, st, x, x_ws,
+                           (unsigned)x_len, H, W, C, pt, pl, w, bias, mult, shift, zx, zy, lo, hi, lut, out, o_ws,
+                           (unsigned)o_len, Ho, Wo, ncg, ntx, nseg);
+    };
+    if (k == 3) launch.template operator()<3, 32>();
+    else launch.template operator()<5, 32>();
+    BNH_HIP(hipGetLastError());
+    return 0;
+  }
   unsigned nb;
   long long total;
   DwGrid g;
   if (dw_grid(Wo, dw_s8_np(s), C / 4, Ho, B, &nb, &total, &g)) return -1;
-  hipStream_t st = bnh_stream(stream);
   dispatch_ks<int8_t>(k, s, [&]<int K, int S>() {
     if (lut)
       hipLaunchKernelGGL((k_dw_s8<K, S, true>), dim3(nb), dim3(256), 0, st, x, x_ws, (unsigned)x_len, H, W, C, pt, pl, w,

@@ -257,3 +257,42 @@ def test_dw_s8_short_requant(hip, k, s):
                                   lut if use_lut else None, Ho, Wo)
                     assert np.array_equal(out[i], ref), ("window", i, "zy", zy, "over", over, "lut", use_lut,
                                                          np.argwhere(out[i] != ref)[:4])
+
+
+@pytest.mark.parametrize("k", [3, 5])
+def test_dw_s8_tiled_ragged(hip, k):
+    """The stride-1 tiled int8 kernel on shapes that leave partial tiles: channel counts that are not a multiple of
+    32 (the last channel group partly empty), widths past one 64-column tile and not a multiple of it, heights that
+    are not a multiple of the 8-row tile, every top / left padding, outputs smaller than the input (valid-style) and
+    larger (reading past the bottom and right edges, which hold the zero point); the strip kernel's results are the
+    same bytes (BNH_DW_S8=strip is read once per process, so the oracle is the check here)"""
+    rng = np.random.default_rng(70 + k)
+    for H, W, C, pt, pl, Ho, Wo in ((5, 7, 36, 0, k - 1, 5, 7), (13, 70, 100, k // 2, 1, 13, 70),
+                                    (9, 130, 44, k - 1, 0, 7, 126), (3, 64, 8, 1, k // 2, 6, 66),
+                                    (17, 1, 4, k // 2, k // 2, 17, 1)):
+        B = 2
+        x = rng.integers(-128, 128, (B, H, W, C)).astype(np.int8)
+        w = rng.integers(-128, 128, (k * k, C)).astype(np.int8)
+        bias = rng.integers(-20000, 20000, C).astype(np.int32)
+        mult = rng.integers(2 ** 30, 2 ** 31 - 1, C).astype(np.int32)
+        shift = rng.integers(1, 12, C).astype(np.int32)
+        lut = rng.integers(-128, 128, 256).astype(np.int8)
+        xs, x_ws = with_slack(x, 64)
+        o_ws = Ho * Wo * C + 64
+        dx, dwt = hip.DeviceArray.from_host(xs), hip.DeviceArray.from_host(w)
+        dbias, dm = hip.DeviceArray.from_host(bias), hip.DeviceArray.from_host(mult)
+        dsh, dl = hip.DeviceArray.from_host(shift), hip.DeviceArray.from_host(lut)
+        for zx, zy, lo, hi, use_lut in ((-128, -128, -128, 127, True), (9, 4, -90, 110, False)):
+            say("dw_s8 tiled k", k, "shape", H, W, C, "pads", pt, pl, "out", Ho, Wo, "lut", use_lut)
+            do = hip.DeviceArray.zeros((B, o_ws), np.int8)
+            hip.check(hip.lib().bnh_dw_s8(dx.ptr, x_ws, H, W, C, k, 1, pt, pl, dwt.ptr, dbias.ptr, dm.ptr, dsh.ptr,
+                                          zx, zy, lo, hi, dl.ptr if use_lut else None, do.ptr, o_ws, Ho, Wo, B,
+                                          None), "dw_s8")
+            hip.sync()
+            raw = do.numpy()
+            assert not raw[:, Ho * Wo * C:].any(), "wrote past the window's outputs"
+            out = raw[:, :Ho * Wo * C].reshape(B, Ho, Wo, C)
+            for i in range(B):
+                ref = O.dw_s8(x[i], k, 1, pt, pl, w, bias, mult, shift, zx, zy, lo, hi, lut if use_lut else None,
+                              Ho, Wo)
+                assert np.array_equal(out[i], ref), ("window", i, np.argwhere(out[i] != ref)[:4])
