@@ -497,9 +497,10 @@ __global__ __launch_bounds__(256) void k_dw_f16p(const h16 *__restrict__ xp, lon
   }
 }
 
-// The same on channel quads (C % 4 == 0, 8-byte aligned data): a thread owns 4 channels (two packed pairs) of a strip
-// of NP output pixels (whole items) in a band of up to R output rows. It loads each input row of the band's strip
-// once (8-byte buffer loads: the lane's row in the vector offset, the column step in the scalar one; the input is
+// The same on channel quads (C % 4 == 0, 8-byte aligned data): a thread owns CP packed pairs (the fp16 DWK launch
+// takes one, the fp16 DW3 launch two) of a strip of NP output pixels (whole items) in a band of up to R output rows.
+// It loads each input row of the band's strip once (4- or 8-byte buffer loads: the lane's row in the vector offset,
+// the column step in the scalar one; the input is
 // haloed, so no checks: a strip past the row's end reads the next row or, at the batch's end, the buffer's
 // out-of-range zeros, and stores nothing there) and keeps the rows in registers while the band's output rows that
 // share them are computed. Each pixel runs its chains row by row in the reference's tap order: the two chains of a
@@ -512,34 +513,40 @@ BNH_DEV h2 h2_bits(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __host__ __device__ constexpr int dw_f16v_np(int k, int s) { return k == 3 && s == 1 ? 8 : 4; }
 __host__ __device__ constexpr int dw_f16v_rows(int k, int s) { return s == 1 ? 4 : 2; }
 
-template <int K, int S, int FORM, int NP, int R, bool ALL>
+template <int K, int S, int FORM, int NP, int R, int CP, bool ALL>
 BNH_DEV void dw_f16v_band(__amdgpu_buffer_rsrc_t xr, int xo, int rstep, int cstep, int px0, int g4, int nrows,
-                          const h2 (&wv)[K * K][2], const h2 (&bias)[2], bool silu, const uint32_t *t01,
+                          const h2 (&wv)[K * K][CP], const h2 (&bias)[CP], bool silu, const uint32_t *t01,
                           const uint16_t *t2, __amdgpu_buffer_rsrc_t orr, int oo, int ostep, int Wo) {
   constexpr int NCOL = (NP - 1) * S + K, NIN = (R - 1) * S + K;
   // every row of a full band: the rows a short last band does not use are read (from the next window, or as the
   // buffer's out-of-range zeros) and dropped
-  h2 xin[NIN][NCOL][2];
+  h2 xin[NIN][NCOL][CP];
 #pragma unroll
   for (int i = 0; i < NIN; i++)
 #pragma unroll
     for (int col = 0; col < NCOL; col++) {
       // a strip past the row's end (not ALL) keeps its whole offset in the vector operand, the range-checked one
-      const u32x2 v = ALL ? __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep, col * cstep, 0)
-                          : __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep + col * cstep, 0, 0);
-      xin[i][col][0] = h2_bits(v[0]);
-      xin[i][col][1] = h2_bits(v[1]);
+      if (CP == 2) {
+        const u32x2 v = ALL ? __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep, col * cstep, 0)
+                            : __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep + col * cstep, 0, 0);
+        xin[i][col][0] = h2_bits(v[0]);
+        xin[i][col][CP - 1] = h2_bits(v[1]);
+      } else {
+        const uint32_t v = ALL ? __builtin_amdgcn_raw_buffer_load_b32(xr, xo + i * rstep, col * cstep, 0)
+                               : __builtin_amdgcn_raw_buffer_load_b32(xr, xo + i * rstep + col * cstep, 0, 0);
+        xin[i][col][0] = h2_bits(v);
+      }
     }
   const h2 z = (h2){(h16)0.0f, (h16)0.0f};
 #pragma unroll
   for (int r = 0; r < R; r++) {
     if (r >= nrows) break;
-    h2 a[NP][2], e[NP][2];
+    h2 a[NP][CP], e[NP][CP];
 #pragma unroll
     for (int q = 0; q < NP; q++) {
       const bool split = FORM == 2 || ALL || px0 + q < g4;
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
+      for (int j = 0; j < CP; j++) {
         a[q][j] = bias[j];
         e[q][j] = z;
       }
@@ -549,7 +556,7 @@ BNH_DEV void dw_f16v_band(__amdgpu_buffer_rsrc_t xr, int xo, int rstep, int cste
         for (int kx = 0; kx < K; kx++) {
           const int t = ky * K + kx;
 #pragma unroll
-          for (int j = 0; j < 2; j++) {
+          for (int j = 0; j < CP; j++) {
             const h2 x = xin[r * S + ky][q * S + kx][j];
             if (FORM == 2 && t == 1) e[q][j] = x * wv[t][j];
             else if (split && (t & 1)) e[q][j] = __builtin_elementwise_fma(x, wv[t][j], e[q][j]);
@@ -557,7 +564,7 @@ BNH_DEV void dw_f16v_band(__amdgpu_buffer_rsrc_t xr, int xo, int rstep, int cste
           }
         }
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
+      for (int j = 0; j < CP; j++) {
         h2 y = split ? a[q][j] + e[q][j] : a[q][j];
         if (silu) y = silu2_lut(y, t01, t2);
         a[q][j] = y;
@@ -566,13 +573,17 @@ BNH_DEV void dw_f16v_band(__amdgpu_buffer_rsrc_t xr, int xo, int rstep, int cste
 #pragma unroll
     for (int q = 0; q < NP; q++) {
       if (px0 + q >= Wo) break;
-      const u32x2 v = {__builtin_bit_cast(uint32_t, a[q][0]), __builtin_bit_cast(uint32_t, a[q][1])};
-      __builtin_amdgcn_raw_buffer_store_b64(v, orr, oo + r * ostep, q * cstep, 0);
+      if (CP == 2) {
+        const u32x2 v = {__builtin_bit_cast(uint32_t, a[q][0]), __builtin_bit_cast(uint32_t, a[q][CP - 1])};
+        __builtin_amdgcn_raw_buffer_store_b64(v, orr, oo + r * ostep, q * cstep, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, a[q][0]), orr, oo + r * ostep, q * cstep, 0);
+      }
     }
   }
 }
 
-template <int K, int S, int FORM, int NP, int R>
+template <int K, int S, int FORM, int NP, int R, int CP>
 __global__ __launch_bounds__(256) void k_dw_f16v(const h16 *__restrict__ xp, long long x_ws, unsigned x_len, int Wp,
                                                  int C, int pt, int pl, const h16 *__restrict__ w,
                                                  const h16 *__restrict__ b, int act, h16 *__restrict__ out,
@@ -586,24 +597,30 @@ __global__ __launch_bounds__(256) void k_dw_f16v(const h16 *__restrict__ xp, lon
   }
   __syncthreads();
   const int nband = (Ho + R - 1) / R;
-  const DwPos ps = dw_pos(C / 4, nband, total, g);
+  const DwPos ps = dw_pos(C / (2 * CP), nband, total, g);
   if (!ps.ok) return;
-  const int c = 4 * ps.c, oy0 = ps.oy * R, px0 = ps.it0, nrows = Ho - oy0 < R ? Ho - oy0 : R;
+  const int c = 2 * CP * ps.c, oy0 = ps.oy * R, px0 = ps.it0, nrows = Ho - oy0 < R ? Ho - oy0 : R;
   constexpr int HH = (K - 1) / 2;
   const int iy0 = FORM == 2 ? oy0 * S - pt + 1 : oy0 * S - pt + HH;
   const int ix0 = FORM == 2 ? px0 * S - pl + 1 : px0 * S - pl + HH;
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void *)w, 0, K * K * C * 2, 0x00020000);
-  h2 wv[K * K][2], bias[2];
+  h2 wv[K * K][CP], bias[CP];
 #pragma unroll
   for (int t = 0; t < K * K; t++) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(wr, 2 * c, t * C * 2, 0);
-    wv[t][0] = h2_bits(v[0]);
-    wv[t][1] = h2_bits(v[1]);
+    if (CP == 2) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(wr, 2 * c, t * C * 2, 0);
+      wv[t][0] = h2_bits(v[0]);
+      wv[t][CP - 1] = h2_bits(v[1]);
+    } else {
+      wv[t][0] = h2_bits(__builtin_amdgcn_raw_buffer_load_b32(wr, 2 * c, t * C * 2, 0));
+    }
   }
-  {
+  if (CP == 2) {
     const uint2 v = *(const uint2 *)(b + c);
     bias[0] = __builtin_bit_cast(h2, v.x);
-    bias[1] = __builtin_bit_cast(h2, v.y);
+    bias[CP - 1] = __builtin_bit_cast(h2, v.y);
+  } else {
+    bias[0] = __builtin_bit_cast(h2, *(const uint32_t *)(b + c));
   }
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)xp, 0, (int)x_len, 0x00020000);
   const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc((void *)out, 0, (int)o_len, 0x00020000);
@@ -612,10 +629,10 @@ __global__ __launch_bounds__(256) void k_dw_f16v(const h16 *__restrict__ xp, lon
   const int g4 = FORM == 2 ? Wo : Wo & ~3;
   const bool silu = FORM == 2 || act == 1;
   if (px0 + NP <= g4)
-    dw_f16v_band<K, S, FORM, NP, R, true>(xr, xo, 2 * Wp * C, 2 * C, px0, g4, nrows, wv, bias, silu, s_t01, s_t2, orr,
+    dw_f16v_band<K, S, FORM, NP, R, CP, true>(xr, xo, 2 * Wp * C, 2 * C, px0, g4, nrows, wv, bias, silu, s_t01, s_t2, orr,
                                           oo, 2 * Wo * C, Wo);
   else
-    dw_f16v_band<K, S, FORM, NP, R, false>(xr, xo, 2 * Wp * C, 2 * C, px0, g4, nrows, wv, bias, silu, s_t01, s_t2, orr,
+    dw_f16v_band<K, S, FORM, NP, R, CP, false>(xr, xo, 2 * Wp * C, 2 * C, px0, g4, nrows, wv, bias, silu, s_t01, s_t2, orr,
                                            oo, 2 * Wo * C, Wo);
 }
 
@@ -1561,11 +1578,12 @@ int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, 
     const unsigned x_len = (unsigned)(2 * ((long long)(B - 1) * x_ws + (long long)(H + k - 1) * Wp * C));
     const unsigned o_len = (unsigned)(2 * ((long long)(B - 1) * o_ws + (long long)Ho * Wo * C));
     const int R = dw_f16v_rows(k, s);
-    if (dw_grid(Wo, dw_f16v_np(k, s), C / 4, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
+    // one channel pair a thread (5 x 5: 103 VGPRs, 4 waves per SIMD; two pairs held 193 and ran 9 % slower)
+    if (dw_grid(Wo, dw_f16v_np(k, s), C / 2, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
     dispatch_ks<h16>(k, s, [&]<int K, int S>() {
       constexpr int NP = dw_f16v_np(K, S), RR = dw_f16v_rows(K, S);
-      hipLaunchKernelGGL((k_dw_f16v<K, S, 1, NP, RR>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, x_len, Wp, C, pt,
-                         pl, (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, o_len, Ho, Wo, total, g);
+      hipLaunchKernelGGL((k_dw_f16v<K, S, 1, NP, RR, 1>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, x_len, Wp, C,
+                         pt, pl, (const h16 *)w, (const h16 *)b, act, (h16 *)out, o_ws, o_len, Ho, Wo, total, g);
     });
     BNH_HIP(hipGetLastError());
     if (chsum) {
@@ -1609,7 +1627,7 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
     if (dw_grid(Wo, dw_f16v_np(3, s), C / 4, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
     auto launch = [&]<int S>() {
       constexpr int NP = dw_f16v_np(3, S), RR = dw_f16v_rows(3, S);
-      hipLaunchKernelGGL((k_dw_f16v<3, S, 2, NP, RR>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, x_len, W + 2, C,
+      hipLaunchKernelGGL((k_dw_f16v<3, S, 2, NP, RR, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, x_len, W + 2, C,
                          pt, pl, (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, o_len, Ho, Wo, total, g);
     };
     if (s == 1) launch.template operator()<1>();
