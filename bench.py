@@ -885,15 +885,17 @@ def config_legs(a, H, rng, stream):
     the oracle: config 1 (the depthwise convs at 5x5 stride 1, fp16 and int8, batch 64), config 2 (the fp16
     Winograd conv, batch 64), config 3 (the v2.4-shaped fp16 net, batch 256)."""
     legs = {}
+    # each leg follows host work (input generation, the previous leg's oracle check) during which the GPU's clocks
+    # fall; a few hundred untimed launches (~30 ms of load) bring them back up before the timed ones
     for kind in ("f16", "s8"):
         b = argparse.Namespace(**vars(a))
-        b.workload, b.k, b.s, b.no_cpu, b.steps, b.warmup = "dw_" + kind, 5, 1, True, max(50, a.steps), 10
+        b.workload, b.k, b.s, b.no_cpu, b.steps, b.warmup = "dw_" + kind, 5, 1, True, max(200, a.steps), 400
         legs[f"config1_dw_{kind}"] = compact_leg(run_dw(b, H, rng, 64, stream, emit=False))
     b = argparse.Namespace(**vars(a))
-    b.workload, b.no_cpu, b.steps, b.warmup = "wino_f16", True, max(50, a.steps), 10
+    b.workload, b.no_cpu, b.steps, b.warmup = "wino_f16", True, max(200, a.steps), 200
     legs["config2_wino_f16"] = compact_leg(run_wino(b, H, rng, 64, stream, emit=False))
     b = argparse.Namespace(**vars(a))
-    b.workload, b.no_cpu, b.steps, b.warmup = "v24_f16", True, max(20, a.steps), 5
+    b.workload, b.no_cpu, b.steps, b.warmup = "v24_f16", True, max(20, a.steps), 10
     legs["config3_v24_f16"] = compact_leg(run_v24(b, H, rng, 256, stream, emit=False))
     return legs
 

@@ -26,6 +26,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "bnh_internal.h"
 #include "bnh_num.h"
 #include "bnh_f16.h"
@@ -34,6 +36,7 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 struct bnh_wino16 {
   int C, K, Cp, Kp;  // Cp = C rounded up to 32 (the MFMA k step), Kp = K rounded up to 16
@@ -260,6 +263,234 @@ __global__ __launch_bounds__(128 * NCO) void k_wino_f16(const uint16_t *__restri
   }
 }
 
+// Version 2 (position-row waves; channel counts that are multiples of 8, 4-channel aligned outputs). The block is
+// 4 waves and owns the same strip of 16 tiles as above; wave i owns row i of the 16 Winograd positions
+// (p = 4 i + j) for every output channel, and computes the V operands of its row itself, in registers, straight from
+// the ring of input rows: row i of B^T d combines two input rows (d0 - d2, d1 + d2, d2 - d1, d1 - d3), then the four
+// column combinations give V[i][0..3] in the order of the form above (same fp16 adds, same bits). So V is never
+// written to LDS or read back once per consumer wave; the wave's U fragments (its 4 positions x every channel pair,
+// 128 VGPRs at 64 x 64) stay in registers for the strip. Each 16-channel block's four position products are summed
+// over the columns in registers (M A: two values per tile row) and exchanged through LDS as S[i][tile][jx][co]; after
+// a barrier every thread takes a tile and 4 output channels and finishes A^T (M A) over the rows, + b, activation,
+// fp16, residual, with 8-byte stores. Two barriers per step (S written / S read); 66.5 KB of LDS at 64 x 64, so two
+// blocks share a CU and one block's epilogue runs beside the other's products. The fp32 output transform sums the
+// columns first (the form above sums the rows first): the same bound, other fp32 roundings.
+// wino_silu with the DX9 multiply (v_mul_legacy_f32: 0 x anything = +0), so that y = -inf, whose reciprocal factor
+// is 0, gives +0 without a compare and select; every other input gives wino_silu's value (NaN stays NaN). The
+// reciprocal and the multiply are one asm block with the wait state a VALU read of a transcendental result needs
+// (the compiler inserts none for registers an asm statement reads).
+BNH_DEV float wino_silu_l(float y) {
+  const float a = 1.0f + __builtin_amdgcn_exp2f(-1.44269504f * y);
+  float d, r;
+  asm("v_rcp_f32 %1, %3\n\ts_nop 0\n\tv_mul_legacy_f32 %0, %2, %1" : "=v"(d), "=&v"(r) : "v"(y), "v"(a));
+  return d;
+}
+
+// Eight fp16 channels as four pairs. The transforms below run on the pairs so that every add and subtract is one
+// v_pk_add_f16 (the compiler turns 8-wide fp16 subtractions into scalar v_sub_f16 pairs and repacks them, 3
+// instructions per pair).
+struct H8 {
+  h2 h[4];
+};
+BNH_DEV H8 h8_ld(const _Float16 *p) {
+  H8 r;
+  __builtin_memcpy(&r, p, 16);
+  return r;
+}
+BNH_DEV H8 h8_add(H8 a, H8 b) {
+  H8 r;
+#pragma unroll
+  for (int k = 0; k < 4; k++) r.h[k] = a.h[k] + b.h[k];
+  return r;
+}
+BNH_DEV H8 h8_sub(H8 a, H8 b) {
+  H8 r;
+#pragma unroll
+  for (int k = 0; k < 4; k++) r.h[k] = a.h[k] - b.h[k];
+  return r;
+}
+BNH_DEV v8h h8_v(H8 a) {
+  v8h o;
+  __builtin_memcpy(&o, &a, 16);
+  return o;
+}
+
+template <int NCH, int NCB, int ACT>  // NCH = Cp / 32 MFMA k steps, NCB = Kp / 16 output channel blocks
+__global__ __launch_bounds__(256, 2) void k_wino_f16r(const uint16_t *__restrict__ x, long long x_ws, int H, int W,
+                                                      int C, int ldx, const uint16_t *__restrict__ U,
+                                                      const float *__restrict__ bias, int K,
+                                                      uint16_t *__restrict__ out, long long o_ws, int ldo, int opad,
+                                                      const uint16_t *__restrict__ res, long long r_ws, int ldr,
+                                                      int rpad, int strips) {
+  constexpr int CP = 32 * NCH, KP = 16 * NCB, RING = 6;
+  constexpr int XS = CP + 8;                 // ring pixel stride (halves)
+  constexpr int XR = WT_COLS * XS;           // ring row stride (halves)
+  constexpr int SS = 2 * KP + 4;             // S tile stride (floats): a write's 4 tile groups in distinct banks
+  constexpr int NQ = CP / 8;                 // 16-byte chunks of a pixel
+  constexpr int NLD = 2 * WT_COLS * NQ;      // chunks of two ring rows
+  constexpr int PRE = (NLD + 255) / 256;     // prefetch slots per thread
+  __shared__ __attribute__((aligned(16))) _Float16 Xs[RING * XR];
+  __shared__ __attribute__((aligned(16))) float Ss[4 * WT_TILES * SS];
+  __shared__ __attribute__((aligned(16))) float Bs[KP];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wi = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's row of positions
+  const int win = blockIdx.x / strips, strip = blockIdx.x % strips;
+  const int T = W / 2, tx0 = strip * WT_TILES, Wp = W + 2, NS = H / 2, c8 = C / 8;
+  const int ntl = T - tx0 < WT_TILES ? T - tx0 : WT_TILES;  // tiles of this strip that are stored
+  // the window's haloed input as one buffer (columns past the image read the next row or zeros; tiles past T are
+  // never stored)
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(x + win * x_ws), 0, (int)((long long)(H + 2) * Wp * ldx * 2), 0x00020000);
+  const int rowb = Wp * ldx * 2;
+  // prefetch slot j: chunk q of pixel px of ring row r (0 / 1 of the pair); -1 past the pair or past C
+  int pgo[PRE], plo[PRE], prr[PRE];
+#pragma unroll
+  for (int j = 0; j < PRE; j++) {
+    const int it = tid + 256 * j, r = it / (WT_COLS * NQ), rem = it - r * (WT_COLS * NQ), px = rem / NQ,
+              q = rem - px * NQ;
+    const bool ok = it < NLD && q < c8;
+    prr[j] = ok ? r : -1;
+    pgo[j] = ((r * Wp + 2 * tx0 + px) * ldx + 8 * q) * 2;
+    plo[j] = (r * XR + px * XS + 8 * q) * 2;  // bytes from the pair's first ring row
+  }
+  v4i pre[PRE];
+  auto fetch = [&](int r0) {
+#pragma unroll
+    for (int j = 0; j < PRE; j++)
+      pre[j] = prr[j] >= 0 ? __builtin_amdgcn_raw_buffer_load_b128(xr, pgo[j] + r0 * rowb, 0, 0) : (v4i){0, 0, 0, 0};
+  };
+  auto commit = [&](int slot0) {  // the pair into ring rows slot0, slot0 + 1 (slot0 even, so never wrapping)
+    char *xb = (char *)(Xs + slot0 * XR);
+#pragma unroll
+    for (int j = 0; j < PRE; j++)
+      if (prr[j] >= 0) *(v4i *)(xb + plo[j]) = pre[j];
+  };
+  // this wave's U fragments: position p = 4 wi + j, k step c, channel block cb -> output channel
+  // 16 cb + (lane & 15), input channels 32 c + 8 (lane >> 4) .. + 7
+  v8h u[4][NCH][NCB];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+#pragma unroll
+      for (int cb = 0; cb < NCB; cb++)
+        u[j][c][cb] = *(const v8h *)(U + ((long long)((4 * wi + j) * KP + 16 * cb + (lane & 15))) * CP + 32 * c +
+                                     8 * (lane >> 4));
+  if (c8 < NQ)  // channels past C read as zeros: no load ever writes them
+    for (int i = tid; i < RING * XR / 8; i += 256) ((v4i *)Xs)[i] = (v4i){0, 0, 0, 0};
+  for (int i = tid; i < KP; i += 256) Bs[i] = i < K ? bias[i] : 0.f;
+  __syncthreads();
+  fetch(0);
+  commit(0);
+  fetch(2);
+  commit(2);
+  if (NS > 1) fetch(4);
+  // the output and residual of the window as buffers: 32-bit byte offsets, a lane part and a scalar row part
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(out + win * o_ws), 0, (int)((long long)(H + 2 * opad) * (W + 2 * opad) * ldo * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rrr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(res ? res + win * r_ws : out), 0, res ? (int)((long long)(H + 2 * rpad) * (W + 2 * rpad) * ldr * 2) : 0,
+      0x00020000);
+  __syncthreads();
+  // row i of B^T d: d[ra] - d[rb] (i = 0, 2, 3) or d[ra] + d[rb] (i = 1)
+  const int ra = wi == 0 ? 0 : wi == 2 ? 2 : 1, rb = wi == 0 ? 2 : wi == 3 ? 3 : wi == 1 ? 2 : 1;
+  const int xl = (2 * (lane & 15)) * XS + 8 * (lane >> 4);  // this lane's tile's first column, its channel group
+  // epilogue item: tile et, output channels 4 eq .. 4 eq + 3
+  const int et = tid >> 4, eq = tid & 15;
+  const bool eon = et < ntl && 4 * eq < K;
+  const int orow = (W + 2 * opad) * ldo * 2, rrow = (W + 2 * rpad) * ldr * 2;  // bytes per row
+  const int ol = ((opad * (W + 2 * opad) + 2 * (tx0 + et) + opad) * ldo + 4 * eq) * 2;
+  const int rl = ((rpad * (W + 2 * rpad) + 2 * (tx0 + et) + rpad) * ldr + 4 * eq) * 2;
+  // the step loop, compiled once for row 1 (an add of the two input rows) and once for the others (a subtraction),
+  // so that no wave branches per instruction on its row
+  auto steps = [&](auto add_rows) {
+  constexpr bool ADD = decltype(add_rows)::value;
+  int base = 0;  // ring row of the step's first input row
+  for (int s = 0; s < NS; s++) {
+    // the rows of step s + 1 (loaded during step s - 1) into the ring slots step s - 1 read last
+    if (s + 1 < NS) commit(base == 0 ? 4 : base - 2);
+    if (s + 2 < NS) fetch(2 * s + 6);
+    // ---- V operands of row wi for the 16 tiles, every k step
+    v8h vv[4][NCH];
+    const _Float16 *xa = Xs + ((base + ra) % RING) * XR + xl, *xb = Xs + ((base + rb) % RING) * XR + xl;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      H8 tt[4];
+#pragma unroll
+      for (int cc = 0; cc < 4; cc++) {
+        const H8 da = h8_ld(xa + cc * XS + 32 * c), db = h8_ld(xb + cc * XS + 32 * c);
+        tt[cc] = ADD ? h8_add(da, db) : h8_sub(da, db);
+      }
+      vv[0][c] = h8_v(h8_sub(tt[0], tt[2]));
+      vv[1][c] = h8_v(h8_add(tt[1], tt[2]));
+      vv[2][c] = h8_v(h8_sub(tt[2], tt[1]));
+      vv[3][c] = h8_v(h8_sub(tt[1], tt[3]));
+      __builtin_amdgcn_sched_barrier(0);  // one k step's input chunks live at a time (VGPRs: U holds 128)
+    }
+    // ---- per channel block: the four position products, then M A over the columns into S
+    float *sw = Ss + wi * WT_TILES * SS + (lane & 15);
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) {
+      v4f m[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        m[j] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCH; c++) m[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv[j][c], u[j][c][cb], m[j], 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int tile = 4 * (lane >> 4) + r;
+        float *d = sw + tile * SS + 16 * cb;
+        d[0] = (m[0][r] + m[1][r]) + m[2][r];
+        d[KP] = (m[1][r] - m[2][r]) - m[3][r];
+      }
+    }
+    __syncthreads();
+    // ---- y = A^T (M A) + b, activation, fp16, residual: tile et, channels 4 eq .. + 3, both output rows and columns
+    if (eon) {
+      float4 sv[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int jx = 0; jx < 2; jx++) sv[i][jx] = *(const float4 *)(Ss + (i * WT_TILES + et) * SS + jx * KP + 4 * eq);
+      const float4 bq = *(const float4 *)(Bs + 4 * eq);
+      auto epi = [&](float y, float b) {
+        y = y + b;
+        if (ACT == 1) y = wino_silu_l(y);
+        else if (ACT == 2) y = bnh_relu_f32(y);
+        return f2h(y);
+      };
+#pragma unroll
+      for (int iy = 0; iy < 2; iy++)
+#pragma unroll
+        for (int jx = 0; jx < 2; jx++) {
+          const float4 a = sv[0][jx], b = sv[1][jx], c = sv[2][jx], e = sv[3][jx];
+          float4 y;
+          if (iy == 0) y = make_float4((a.x + b.x) + c.x, (a.y + b.y) + c.y, (a.z + b.z) + c.z, (a.w + b.w) + c.w);
+          else y = make_float4((b.x - c.x) - e.x, (b.y - c.y) - e.y, (b.z - c.z) - e.z, (b.w - c.w) - e.w);
+          h2 lo = (h2){epi(y.x, bq.x), epi(y.y, bq.y)}, hi = (h2){epi(y.z, bq.z), epi(y.w, bq.w)};
+          if (res) {
+            const v2u rv = __builtin_amdgcn_raw_buffer_load_b64(rrr, rl, (2 * s + iy) * rrow + jx * ldr * 2, 0);
+            // the words as scalars first: hipcc miscompiles __builtin_bit_cast of an ext_vector element (it reads
+            // element 0 for every index)
+            const uint32_t r0 = rv.x, r1 = rv.y;
+            lo = lo + __builtin_bit_cast(h2, r0);
+            hi = hi + __builtin_bit_cast(h2, r1);
+          }
+          __builtin_amdgcn_raw_buffer_store_b64(
+              (v2u){__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)}, orr, ol,
+              (2 * s + iy) * orow + jx * ldo * 2, 0);
+        }
+    }
+    __syncthreads();
+    base = base + 2 == RING ? 0 : base + 2;
+  }
+  };
+  if (wi == 1) steps(std::true_type{});
+  else steps(std::false_type{});
+}
+
 __global__ void k_zero_halo16(uint16_t *__restrict__ out, long long ws, int H, int W, int C, int h, long long total) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
@@ -339,6 +570,35 @@ int bnh_wino_f16(const uint16_t *x, long long x_ws, int H, int W, int ldx, const
   const int strips = (int)bnh_ceil_div(W / 2, WT_TILES);
   const dim3 grid((unsigned)((long long)strips * B));
   const int nco = P->Kp / 16, nch = P->Cp / 32;
+  // version 2 (position-row waves) when 16-byte input chunks and 8-byte output quads are aligned;
+  // BNH_WINO_FORM=1 keeps version 1, for comparison
+  static const bool v1 = [] {
+    const char *e = getenv("BNH_WINO_FORM");
+    return e && e[0] == '1';
+  }();
+  const bool r_ok = P->C % 8 == 0 && ldx % 8 == 0 && ((uintptr_t)x & 15) == 0 && (B == 1 || x_ws % 8 == 0) &&
+                    P->K % 4 == 0 && ldo % 4 == 0 && ((uintptr_t)out & 7) == 0 && (B == 1 || o_ws % 4 == 0) &&
+                    (!res || (ldr % 4 == 0 && ((uintptr_t)res & 7) == 0 && (B == 1 || r_ws % 4 == 0)));
+  if (r_ok && !v1) {
+#define WINOR_A(NCH, NCB, ACT)                                                                                         \
+  hipLaunchKernelGGL((k_wino_f16r<NCH, NCB, ACT>), grid, dim3(256), 0, st, x, x_ws, H, W, P->C, ldx, P->U, P->b, P->K, \
+                     out, o_ws, ldo, opad, res, r_ws, ldr, rpad, strips)
+#define WINOR(NCH, NCB)                                                                                                \
+  do {                                                                                                                 \
+    if (act == 1) WINOR_A(NCH, NCB, 1);                                                                                \
+    else if (act == 2) WINOR_A(NCH, NCB, 2);                                                                           \
+    else WINOR_A(NCH, NCB, 0);                                                                                         \
+  } while (0)
+    if (nch == 1) {
+      if (nco == 1) WINOR(1, 1); else if (nco == 2) WINOR(1, 2); else if (nco == 3) WINOR(1, 3); else WINOR(1, 4);
+    } else {
+      if (nco == 1) WINOR(2, 1); else if (nco == 2) WINOR(2, 2); else if (nco == 3) WINOR(2, 3); else WINOR(2, 4);
+    }
+#undef WINOR
+#undef WINOR_A
+    BNH_HIP(hipGetLastError());
+    return 0;
+  }
   // a window's input is one buffer resource; per-window element offsets of the output and residual fit 32 bits
   BNH_REQ((long long)(H + 2) * (W + 2) * ldx * 2 < (1LL << 31));
   BNH_REQ((long long)(H + 2 * opad) * (W + 2 * opad) * ldo < (1LL << 31));
