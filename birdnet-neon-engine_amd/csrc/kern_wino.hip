@@ -270,11 +270,13 @@ __global__ __launch_bounds__(128 * NCO) void k_wino_f16(const uint16_t *__restri
 // column combinations give V[i][0..3] in the order of the form above (same fp16 adds, same bits). So V is never
 // written to LDS or read back once per consumer wave; the wave's U fragments (its 4 positions x every channel pair,
 // 128 VGPRs at 64 x 64) stay in registers for the strip. Each 16-channel block's four position products are summed
-// over the columns in registers (M A: two values per tile row) and exchanged through LDS as S[i][tile][jx][co]; after
-// a barrier every thread takes a tile and 4 output channels and finishes A^T (M A) over the rows, + b, activation,
-// fp16, residual, with 8-byte stores. Two barriers per step (S written / S read); 66.5 KB of LDS at 64 x 64, so two
-// blocks share a CU and one block's epilogue runs beside the other's products. The fp32 output transform sums the
-// columns first (the form above sums the rows first): the same bound, other fp32 roundings.
+// over the columns in registers (M A: two values per tile row; row 1's position-1 product starts from the bias, which
+// every output takes exactly once through row 1) and exchanged through LDS as S[i][tile][jx][co]; after a barrier
+// every thread takes a tile and 4 output channels and finishes A^T (M A) over the rows, the activation, fp16 and the
+// residual, with 8-byte stores. Two barriers per step (S written / S read); 62 KB of LDS at 64 x 64, so two blocks
+// share a CU and one block's epilogue runs beside the other's products. The fp32 output transform sums the columns
+// first (the form above sums the rows first) and carries the bias inside it: the same bound, other fp32 roundings.
+
 // wino_silu with the DX9 multiply (v_mul_legacy_f32: 0 x anything = +0), so that y = -inf, whose reciprocal factor
 // is 0, gives +0 without a compare and select; every other input gives wino_silu's value (NaN stays NaN). The
 // reciprocal and the multiply are one asm block with the wait state a VALU read of a transcendental result needs
@@ -401,6 +403,9 @@ __global__ __launch_bounds__(256, 2) void k_wino_f16r(const uint16_t *__restrict
   const int orow = (W + 2 * opad) * ldo * 2, rrow = (W + 2 * rpad) * ldr * 2;  // bytes per row
   const int ol = ((opad * (W + 2 * opad) + 2 * (tx0 + et) + opad) * ldo + 4 * eq) * 2;
   const int rl = ((rpad * (W + 2 * rpad) + 2 * (tx0 + et) + rpad) * ldr + 4 * eq) * 2;
+  float binit[NCB];  // row 1's position-1 sums start from the bias of the lane's output channel in each block
+#pragma unroll
+  for (int cb = 0; cb < NCB; cb++) binit[cb] = wi == 1 ? Bs[16 * cb + (lane & 15)] : 0.f;
   // the step loop, compiled once for row 1 (an add of the two input rows) and once for the others (a subtraction),
   // so that no wave branches per instruction on its row
   auto steps = [&](auto add_rows) {
@@ -427,14 +432,15 @@ __global__ __launch_bounds__(256, 2) void k_wino_f16r(const uint16_t *__restrict
       vv[3][c] = h8_v(h8_sub(tt[1], tt[3]));
       __builtin_amdgcn_sched_barrier(0);  // one k step's input chunks live at a time (VGPRs: U holds 128)
     }
-    // ---- per channel block: the four position products, then M A over the columns into S
+    // ---- per channel block: the four position products (row 1's position 1 starts from the bias, which every
+    // output takes once through it), then M A over the columns into S
     float *sw = Ss + wi * WT_TILES * SS + (lane & 15);
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
       v4f m[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        m[j] = (v4f){0.f, 0.f, 0.f, 0.f};
+        m[j] = j == 1 ? (v4f){binit[cb], binit[cb], binit[cb], binit[cb]} : (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < NCH; c++) m[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv[j][c], u[j][c][cb], m[j], 0, 0, 0);
       }
@@ -454,9 +460,7 @@ __global__ __launch_bounds__(256, 2) void k_wino_f16r(const uint16_t *__restrict
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int jx = 0; jx < 2; jx++) sv[i][jx] = *(const float4 *)(Ss + (i * WT_TILES + et) * SS + jx * KP + 4 * eq);
-      const float4 bq = *(const float4 *)(Bs + 4 * eq);
-      auto epi = [&](float y, float b) {
-        y = y + b;
+      auto epi = [&](float y) {  // the bias is in S[1]
         if (ACT == 1) y = wino_silu_l(y);
         else if (ACT == 2) y = bnh_relu_f32(y);
         return f2h(y);
@@ -469,7 +473,7 @@ __global__ __launch_bounds__(256, 2) void k_wino_f16r(const uint16_t *__restrict
           float4 y;
           if (iy == 0) y = make_float4((a.x + b.x) + c.x, (a.y + b.y) + c.y, (a.z + b.z) + c.z, (a.w + b.w) + c.w);
           else y = make_float4((b.x - c.x) - e.x, (b.y - c.y) - e.y, (b.z - c.z) - e.z, (b.w - c.w) - e.w);
-          h2 lo = (h2){epi(y.x, bq.x), epi(y.y, bq.y)}, hi = (h2){epi(y.z, bq.z), epi(y.w, bq.w)};
+          h2 lo = (h2){epi(y.x), epi(y.y)}, hi = (h2){epi(y.z), epi(y.w)};
           if (res) {
             const v2u rv = __builtin_amdgcn_raw_buffer_load_b64(rrr, rl, (2 * s + iy) * rrow + jx * ldr * 2, 0);
             // the words as scalars first: hipcc miscompiles __builtin_bit_cast of an ext_vector element (it reads
