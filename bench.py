@@ -769,6 +769,44 @@ def cpu_baseline_perch(pn, pcms, n_one=6):
     return base, outs
 
 
+def cpu_baseline_reference(pn, pcms, n_one=2):
+    """The reference's own scalar fp32 Perch v2 oracle (src/perch_ref.c, built from the reference checkout into
+    oracle/_ref) on the bench net's float weights, written as a .bnp2 file: len(pcms) windows one per thread on
+    cpu_threads() threads, then n_one on one thread. Returns (baseline dict, its embeddings of pcms), or None where
+    the library was not built."""
+    sys.path[:0] = [os.path.join(ROOT, "oracle"), os.path.join(ROOT, "oracle", "ref")]
+    import perchref
+    if not perchref.available():
+        return None
+    import tempfile
+    T = cpu_threads()
+    tmp = tempfile.mkdtemp(prefix="bnn_ref_")
+    path = os.path.join(tmp, "bench_net.bnp2")
+    perchref.write_bnp2(path, pn)
+    m = perchref.Model(path)
+    try:
+        t0 = time.perf_counter()
+        with concurrent.futures.ThreadPoolExecutor(T) as ex:
+            embs = list(ex.map(lambda p: m.infer(p)[1], pcms))
+        dt = time.perf_counter() - t0
+        t1 = time.perf_counter()
+        for p in pcms[:n_one]:
+            m.infer(p)
+        dt1 = time.perf_counter() - t1
+    finally:
+        m.close()
+        os.unlink(path)
+        os.rmdir(tmp)
+    base = {"value": round(len(pcms) / dt, 3), "unit": "windows/s", "cores": T, "kind": "reference",
+            "sample": f"{len(pcms)} windows through the reference's own scalar fp32 Perch v2 oracle (src/perch_ref.c "
+                      f"pc_ref_infer, clang -O2 -ffp-contract=off) on the bench net's float weights: exact FFT "
+                      f"front end, stem, 26 blocks, head conv and embedding, a one-prototype head in place of the "
+                      f"linear one (1.8 % of the net's MACs); one window per thread ({T} threads), {dt:.2f} s wall",
+            "one_thread": {"value": round(n_one / dt1, 3), "unit": "windows/s", "cores": 1,
+                           "sample": f"{n_one} of those windows on one thread; {dt1:.2f} s wall"}}
+    return base, embs
+
+
 def run_perch(a, H, rng, B, stream):
     import tempfile
     from bnneon import binding, perchnet
@@ -828,10 +866,23 @@ def run_perch(a, H, rng, B, stream):
     if not a.no_legs:
         line.update(config_legs(a, H, rng, stream))
     if not a.no_cpu:
-        line["cpu_baseline"], ref = cpu_baseline_perch(pn, pcms)
+        port, ref = cpu_baseline_perch(pn, pcms)
         same = [bool(np.array_equal(logits[w].view(np.uint32), ref[w % n_distinct][:nc].view(np.uint32)))
                 for w in range(B)]
         line["parity_windows"] = f"{sum(same)}/{B} windows' logits bit-identical to the oracle's"
+        rb = cpu_baseline_reference(pn, pcms[:2 * cpu_threads()])
+        if rb is None:
+            line["cpu_baseline"] = port
+        else:
+            base, embs = rb
+            host = port.pop("host")
+            line["cpu_baseline"] = dict(base, port=port, host=host)
+            gemb = demb.numpy()
+            rel = [float(np.linalg.norm(gemb[w] - e) / np.linalg.norm(e)) for w, e in enumerate(embs)]
+            line["vs_reference_fp32"] = {
+                "windows": len(embs), "emb_rel_l2_max": round(max(rel), 5),
+                "note": "the GPU's int8 embeddings against the reference's fp32 oracle on the same float weights: the "
+                        "int8 quantisation of every 1x1 conv (tests/test_ref_perch.py states the bounds)"}
     print(json.dumps(line), flush=True)
 
 

@@ -30,10 +30,10 @@ STAGES = [(1, 3, 1, 24, 2), (6, 3, 2, 32, 3), (6, 5, 2, 48, 3), (6, 3, 2, 96, 5)
 STEM_C = 40
 
 
-def blocks():
-    """(cin, cexp, k, stride, cout) of the 26 blocks."""
+def blocks(stages=None):
+    """(cin, cexp, k, stride, cout) of the 26 blocks (or of the given stages)."""
     out, cin = [], STEM_C
-    for e, k, s, co, n in STAGES:
+    for e, k, s, co, n in (STAGES if stages is None else stages):
         for i in range(n):
             out.append((cin, cin * e, k, s if i == 0 else 1, co))
             cin = co
@@ -76,47 +76,90 @@ def signal(rng, n=NSAMP, sr=SR):
 
 
 class PerchNet:
-    """The package and the float weights it was built from."""
+    """The package and the float weights it was built from.
 
-    def __init__(self, seed=0, n_classes=N_CLASSES, n_blocks=None):
+    kind "int8": the 1x1 convs on PW_S8 (the neon-int8 path, the benched net); "f32": the same graph with every 1x1
+    conv an fp32 PW op (the neon-fp32 path). head "gemv": the linear classifier (GEMV_S8 for int8, GEMV for f32);
+    "proto": Perch v2's ProtoPNet head (PROTO_S8 for int8, fp32 PROTO for f32) over ppc prototypes per class. The
+    float weights are kept in `fw` under the reference's .bnp2 tensor names, with the block table in `blocks_table`,
+    so the same net can be written for the reference's own fp32 oracle (src/perch_ref.c)."""
+
+    def __init__(self, seed=0, n_classes=N_CLASSES, n_blocks=None, kind="int8", head="gemv", ppc=1, eps=1e-5,
+                 bias_scale=0.1, pj_gain=0.5, se_open=False, stages=None):
+        """bias_scale, pj_gain, se_open (SE gates near 1: the second FC's weights x 0.1, its biases 4) keep the same
+        random draws; with small biases, unit-gain projections and open gates the embedding depends strongly on the
+        input (the defaults, the benched net, let a deep random stack wash most of the input out). stages: the
+        (expand ratio, k, stride, out channels, repeats) list in place of EfficientNet-B3's."""
+        assert kind in ("int8", "f32") and head in ("gemv", "proto")
         rng = np.random.default_rng(seed)
-        self.n_classes = n_classes
+        self.n_classes, self.kind, self.head, self.ppc, self.eps = n_classes, kind, head, ppc, eps
         pkg = pkgfmt.Package()
         net = netbuild.Net(pkg)
         self.pkg, self.net = pkg, net
+        self.fw, self.blocks_table = [], []
         nw = lambda shape, fan, g=1.0: (rng.standard_normal(shape) * g * np.sqrt(2.0 / fan)).astype(np.float32)
-        bias = lambda n: (rng.standard_normal(n) * 0.1).astype(np.float32)
+        bias = lambda n: (rng.standard_normal(n) * bias_scale).astype(np.float32)
+        pw = net.pw_s8 if kind == "int8" else net.pw
+
+        def keep(name, a):
+            self.fw.append((name, a))
+            return a
         ib = net.buf(netbuild.F32, 1, NSAMP, 1)
-        window = (0.5 - 0.5 * np.cos(2 * np.pi * np.arange(FRAME) / FRAME)).astype(np.float32)
-        spec = net.logmel(ib, NSAMP, FRAME, HOP, PAD, NFFT, window, mel_bank(), 1e-3, 1.0)
-        x = net.stem(spec, nw((STEM_C, 9), 9), bias(STEM_C), 3, 2, act="silu", opad=1, ldo=STEM_C)
+        window = keep("fe.window", (0.5 - 0.5 * np.cos(2 * np.pi * np.arange(FRAME) / FRAME)).astype(np.float32))
+        mel = keep("fe.mel", mel_bank())
+        self.log_floor, self.log_scale = 1e-3, 1.0
+        spec = net.logmel(ib, NSAMP, FRAME, HOP, PAD, NFFT, window, mel, self.log_floor, self.log_scale)
+        x = net.stem(spec, keep("stem.w", nw((STEM_C, 9), 9)), keep("stem.b", bias(STEM_C)), 3, 2, act="silu", opad=1,
+                     ldo=STEM_C)
         H, W = net.bufs[x][1], net.bufs[x][2]
-        bl = blocks() if n_blocks is None else blocks()[:n_blocks]
+        bl = blocks(stages) if n_blocks is None else blocks(stages)[:n_blocks]
         for i, (cin, ce, k, s, co) in enumerate(bl):
             res = x if (s == 1 and cin == co) else -1
             h = (k - 1) // 2
             if ce != cin:   # expand 1x1 + SiLU straight into the depthwise conv's zero-haloed input
-                d = net.pw_s8(x, nw((ce, cin), cin), bias(ce), act="silu", opad=h)
+                d = pw(x, keep(f"m{i}.ex.w", nw((ce, cin), cin)), keep(f"m{i}.ex.b", bias(ce)), act="silu", opad=h)
             elif net.bufs[x][5] == h and net.bufs[x][4] == cin:
                 d = x
             else:
                 d = net.pad(x, h)
             Ho, Wo, pt, pl = same_pads(H, W, k, s)
-            wdw = nw((k * k, ce), k * k)
+            wdw = keep(f"m{i}.dw.w", nw((k * k, ce), k * k))
+            bdw = keep(f"m{i}.dw.b", bias(ce))
             if k == 3 and pt == 1 and pl == 1:
-                y, cs = net.dw3(d, wdw, bias(ce), s=s)
+                y, cs = net.dw3(d, wdw, bdw, s=s)
             else:
-                y, cs = net.dwk(d, wdw, bias(ce), k, s, pt, pl)
+                y, cs = net.dwk(d, wdw, bdw, k, s, pt, pl)
             rd = max(1, cin // 4)
-            g = net.se_gate(cs, Ho * Wo, nw((rd, ce), ce), bias(rd), nw((ce, rd), rd), bias(ce))
-            x = net.pw_s8(y, nw((co, ce), ce, 0.5), bias(co), gate=g, res=res)
+            w1, b1, w2, b2 = nw((rd, ce), ce), bias(rd), nw((ce, rd), rd), bias(ce)
+            if se_open:
+                w2, b2 = w2 * np.float32(0.1), np.full(ce, 4.0, np.float32)
+            g = net.se_gate(cs, Ho * Wo, keep(f"m{i}.se1.w", w1), keep(f"m{i}.se1.b", b1), keep(f"m{i}.se2.w", w2),
+                            keep(f"m{i}.se2.b", b2))
+            x = pw(y, keep(f"m{i}.pj.w", nw((co, ce), ce, pj_gain)), keep(f"m{i}.pj.b", bias(co)), gate=g, res=res)
+            pb, pr = max((Ho - 1) * s + k - H, 0) - pt, max((Wo - 1) * s + k - W, 0) - pl
+            self.blocks_table.append((k, s, cin, ce if ce != cin else 0, co, rd, int(res >= 0),
+                                      pt | pl << 8 | pb << 16 | pr << 24))
             H, W = Ho, Wo
-        top = net.pw_s8(x, nw((EMB, net.bufs[x][3]), net.bufs[x][3]), bias(EMB), act="silu")
+        c_top = net.bufs[x][3]
+        top = pw(x, keep("top.w", nw((EMB, c_top), c_top)), keep("top.b", bias(EMB)), act="silu")
         emb = net.mean(top)
         self.emb_buf = emb
-        net.gemv_s8(emb, nw((n_classes, EMB), EMB, 0.5), bias(n_classes))
+        if head == "gemv":
+            wl, bl_ = nw((n_classes, EMB), EMB, 0.5), bias(n_classes)
+            if kind == "int8":
+                net.gemv_s8(emb, wl, bl_)
+            else:
+                net.gemv(emb, wl, bl_)
+        else:
+            protos = keep("proto", nw((n_classes * ppc, EMB), EMB))
+            clsw = keep("cls.w", (rng.standard_normal((n_classes, ppc)) * 0.5).astype(np.float32))
+            clsb = keep("cls.b", bias(n_classes))
+            if kind == "int8":
+                net.proto_s8(top, protos, clsw, clsb, eps=eps)
+            else:
+                net.proto_fp(top, protos, clsw, clsb, eps=eps, kind="f32")
         self.H, self.W = H, W
-        net.add_to("neon-int8", 0, in_buf=ib, emb_buf=emb)
+        net.add_to("neon-int8" if kind == "int8" else "neon-fp32", 0, in_buf=ib, emb_buf=emb)
         netbuild.standard_meta(pkg, NSAMP, n_classes, sample_rate=SR, model_id="perch_v2_shaped_synthetic",
                                emb_dim=EMB)
 
