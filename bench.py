@@ -554,7 +554,7 @@ def run_wino(a, H, rng, B, stream, emit=True):
                    "parallelism": "1 GPU, windows batched per launch", "wall_s_timed_region": round(wall, 4)},
         "direct_equivalent_tflops": round(flops_direct / (ms * 1e-3) / 1e12, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_wino_f16",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_wino_f16r",
                      "algorithmic_bytes_per_launch": bytes_per_launch},
     }
     got = dout.numpy().reshape(B, Hh, W, K).astype(np.float64)
