@@ -45,14 +45,20 @@ __global__ void k_zero_halo(T *__restrict__ out, long long ws, int H, int W, int
 // thread per (window, output pixel, 4 channels); w panels [Np/8][Kp][8]. H16: the fp16-path form, channels < N
 // rounded to fp16 (pc_cvt_pad_f16, src/pc_kern_f16.c:104-113) and stored as fp16
 // KK: the kernel size when it is 3 or 5 (the taps unrolled), 0 for any k. A thread owns 4 output channels of one
-// pixel; windows on grid.y; 32-bit index arithmetic; 16-byte stores when the output rows allow them (VEC).
+// pixel; windows on grid.y; 32-bit index arithmetic; 16-byte stores when the output rows allow them (VEC). The
+// weight panels and the bias are copied into LDS once per block (dynamic LDS, Np Kp + Np floats): every thread reads
+// Kp 16-byte weight rows, the same for every pixel, which through the vector memory path bound the kernel on its
+// address units.
 template <int KK, bool H16, bool VEC>
 __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img, long long i_ws, int W, int k, int s,
                                                   int Ho, int Wo, const float *__restrict__ w,
                                                   const float *__restrict__ bias, int Kp, int Np, int act,
                                                   void *__restrict__ outv, long long o_ws, int ldo, int opad, int N) {
   __shared__ uint32_t tbl[256];
+  extern __shared__ __attribute__((aligned(16))) float s_wb[];  // [Np Kp] panels, then [Np] bias
   bnh_silu_table(tbl);
+  for (int i = threadIdx.x; i < Np * Kp / 4; i += blockDim.x) ((float4 *)s_wb)[i] = ((const float4 *)w)[i];
+  for (int i = threadIdx.x; i < Np; i += blockDim.x) s_wb[Np * Kp + i] = bias[i];
   __syncthreads();
   const int ng = Np / 4;
   const int i = blockIdx.x * blockDim.x + threadIdx.x, per = Ho * Wo * ng;
@@ -60,7 +66,7 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
   if (i >= per) return;
   const int m = i / ng, g = i - m * ng, oy = m / Wo, ox = m - oy * Wo, n0 = 4 * g;
   const float *x = img + win * i_ws + (oy * s) * W + ox * s;
-  const float *wp = w + (n0 / 8) * Kp * 8 + n0 % 8;
+  const float *wp = s_wb + (n0 / 8) * Kp * 8 + n0 % 8;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   auto tap = [&](int q, float a) {
     const float4 wv = *(const float4 *)(wp + q * 8);
@@ -82,7 +88,7 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
   float y[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    y[j] = acc[j] + bias[n0 + j];
+    y[j] = acc[j] + s_wb[Np * Kp + n0 + j];
     if (act == 1) y[j] = bnh_silu_f32_t(y[j], tbl);
     else if (act == 2) y[j] = bnh_relu_f32(y[j]);
   }
@@ -112,8 +118,9 @@ template <bool H16>
 static void stem_launch(dim3 grid, hipStream_t st, bool vec, const float *img, long long i_ws, int W, int k, int s,
                         int Ho, int Wo, const float *w, const float *bias, int Kp, int Np, int act, void *out,
                         long long o_ws, int ldo, int opad, int N) {
+  const size_t lds = sizeof(float) * ((size_t)Np * Kp + Np);
 #define STEM_L(KK, V)                                                                                                  \
-  hipLaunchKernelGGL((k_stem_f32<KK, H16, V>), grid, dim3(256), 0, st, img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np,   \
+  hipLaunchKernelGGL((k_stem_f32<KK, H16, V>), grid, dim3(256), lds, st, img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, \
                      act, out, o_ws, ldo, opad, N)
   if (k == 3 && Kp == 12) { if (vec) STEM_L(3, true); else STEM_L(3, false); }
   else if (k == 5 && Kp == 28) { if (vec) STEM_L(5, true); else STEM_L(5, false); }
@@ -585,6 +592,7 @@ int bnh_stem_f32_body(const float *img, long long i_ws, int H, int W, int k, int
   BNH_REQ((Ho - 1) * s + k <= H && (Wo - 1) * s + k <= W && Kp >= k * k && Kp % 4 == 0 && Np % 8 == 0);
   BNH_REQ(ldo >= Np && opad >= 0 && opad <= 3 && act >= 0 && act <= 2 && ldo % 4 == 0);
   BNH_REQ(((uintptr_t)w & 15) == 0 && ((uintptr_t)out & 3) == 0);
+  BNH_REQ((long long)Np * (Kp + 1) * 4 <= 48 * 1024);  // the panels and the bias in LDS
   BNH_REQ(B == 1 || (i_ws >= (long long)H * W && o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo));
   const long long per = (long long)Ho * Wo * (Np / 4);
   BNH_REQ(per < (1LL << 31) && (long long)H * W < (1LL << 31));
@@ -602,6 +610,7 @@ int bnh_stem_f32to16_body(const float *img, long long i_ws, int H, int W, int k,
   BNH_REQ((Ho - 1) * s + k <= H && (Wo - 1) * s + k <= W && Kp >= k * k && Kp % 4 == 0 && Np % 8 == 0);
   BNH_REQ(ldo >= N && opad >= 0 && opad <= 3 && act >= 0 && act <= 2);
   BNH_REQ(((uintptr_t)w & 15) == 0);
+  BNH_REQ((long long)Np * (Kp + 1) * 4 <= 48 * 1024);  // the panels and the bias in LDS
   BNH_REQ(B == 1 || (i_ws >= (long long)H * W && o_ws >= (long long)(Ho + 2 * opad) * (Wo + 2 * opad) * ldo));
   const long long per = (long long)Ho * Wo * (Np / 4);
   BNH_REQ(per < (1LL << 31) && (long long)H * W < (1LL << 31));
