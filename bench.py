@@ -1141,8 +1141,8 @@ FP16_VALU_PEAK_TFLOPS = 157.3
 def v24_roofline(H, vn, B, stream, a):
     """The net's largest fp16 1x1 conv (by FLOPs) replayed through bnh_gemm_f16 with the net's own weights and
     shape on `stream`, timed with events. The exact GEMM keeps the reference's fp16 accumulation, so it runs on
-    packed fp16 VALU FMAs, not MFMA: the roofline is priced against the fp16 MFMA peak as the contract asks, and
-    against the packed-fp16 VALU peak that actually bounds it."""
+    packed fp16 VALU FMAs, not MFMA: the roofline is priced against the packed-fp16 VALU peak that bounds it, with
+    the fp16 MFMA pricing beside it (the MFMA form, --f16-mfma, is priced against MFMA)."""
     import ctypes
     _, big = v24_counts(vn.net)
     code, b, t, p = big
@@ -1177,8 +1177,10 @@ def v24_roofline(H, vn, B, stream, a):
          "ms_per_launch": round(ms, 4), "algorithmic_flops_per_launch": 2 * M * N * K * B,
          "algorithmic_bytes_per_launch": hbm_bytes, "hbm_GBps": round(gbps, 1), "hbm_frac": round(gbps / 8000.0, 4)}
     if not a.f16_mfma:
-        r["valu_peak"] = FP16_VALU_PEAK_TFLOPS
-        r["valu_frac"] = round(tf / FP16_VALU_PEAK_TFLOPS, 4)
+        # the exact GEMM's binding resource is the packed fp16 VALU (the matrix cores cannot keep fp16 sums):
+        # the roofline is priced against it, with the MFMA pricing beside it
+        r.update({"bound": "valu", "peak": FP16_VALU_PEAK_TFLOPS, "frac": round(tf / FP16_VALU_PEAK_TFLOPS, 4),
+                  "mfma": {"peak": FP16_MFMA_PEAK_TFLOPS, "frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4)}})
     return r
 
 
