@@ -511,7 +511,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 BNH_DEV h2 h2_bits(uint32_t u) { return __builtin_bit_cast(h2, u); }
 // output rows per band: input rows shared by more outputs against registers and the number of waves
 __host__ __device__ constexpr int dw_f16v_np(int k, int s) { return k == 3 && s == 1 ? 8 : 4; }
-__host__ __device__ constexpr int dw_f16v_rows(int k, int s) { return s == 1 ? 4 : 2; }
+// (5 x 5 stride 1: 6 rows, 3.3 input loads per output pair where 4-row bands take 4; the 24 x 64 C = 672 launch of 64
+// windows 0.0914 -> 0.0856 ms; 8 rows the same, 10 and more spill)
+__host__ __device__ constexpr int dw_f16v_rows(int k, int s) { return k == 5 && s == 1 ? 6 : s == 1 ? 4 : 2; }
 
 template <int K, int S, int FORM, int NP, int R, int CP, bool ALL>
 BNH_DEV void dw_f16v_band(__amdgpu_buffer_rsrc_t xr, int xo, int rstep, int cstep, int px0, int g4, int nrows,
@@ -1578,7 +1580,8 @@ int bnh_dwk_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int k, 
     const unsigned x_len = (unsigned)(2 * ((long long)(B - 1) * x_ws + (long long)(H + k - 1) * Wp * C));
     const unsigned o_len = (unsigned)(2 * ((long long)(B - 1) * o_ws + (long long)Ho * Wo * C));
     const int R = dw_f16v_rows(k, s);
-    // one channel pair a thread (5 x 5: 103 VGPRs, 4 waves per SIMD; two pairs held 193 and ran 9 % slower)
+    // one channel pair a thread (5 x 5: 119 VGPRs with 6-row bands, 4 waves per SIMD; two pairs held 193 and ran 9 %
+    // slower)
     if (dw_grid(Wo, dw_f16v_np(k, s), C / 2, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
     dispatch_ks<h16>(k, s, [&]<int K, int S>() {
       constexpr int NP = dw_f16v_np(K, S), RR = dw_f16v_rows(K, S);
