@@ -192,7 +192,9 @@ __global__ __launch_bounds__(256) void k_gemm_f16(const uint16_t *__restrict__ A
 
 // GATE: A's columns are multiplied by the window's fp16 gates gh [K] as they are staged (the fp16 SE's in-place
 // scaling of A, src/rt_ops_f32.c:256-327, done in the A-load: the same fp16 products, no pass over A)
-template <bool VEC, bool RES, bool GATE>
+// MB: the fp32 sums of several K blocks (false when the launch has one K block, or one K block per block: the 32
+// registers of those sums then stay free, 4 -> 5 waves per SIMD)
+template <bool VEC, bool RES, bool GATE, bool MB>
 __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ A, long long a_ws, int lda, int M,
                                                    double rM, long long rows, const uint16_t *__restrict__ wk, int Ntp,
                                                    const float *__restrict__ b32, const uint16_t *__restrict__ b16,
@@ -274,13 +276,16 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
     }
   };
   h2 acc[4][4];
-  float fb[4][8];
+  float fb[MB ? 4 : 1][MB ? 8 : 1];
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
+  for (int r = 0; r < 4; r++)
 #pragma unroll
     for (int p = 0; p < 4; p++) acc[r][p] = (h2){(h16)0.0f, (h16)0.0f};
+  if constexpr (MB) {
 #pragma unroll
-    for (int c = 0; c < 8; c++) fb[r][c] = 0.f;
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int c = 0; c < 8; c++) fb[r][c] = 0.f;
   }
   const int nblk = (Kp + bs - 1) / bs;
   int kb = kbeg, k0 = kbeg;
@@ -320,15 +325,17 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
           for (int p = 0; p < 4; p++) acc[r][p] = __builtin_elementwise_fma(wb[p], hi, acc[r][p]);
         }
       }
-      if (k0 + kn >= ke && nblk > 1 && !part) {  // a K block ends: its fp16 results into the fp32 sums
+      if constexpr (MB) {
+        if (k0 + kn >= ke && nblk > 1 && !part) {  // a K block ends: its fp16 results into the fp32 sums
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+          for (int r = 0; r < 4; r++)
 #pragma unroll
-          for (int p = 0; p < 4; p++) {
-            fb[r][2 * p] = fb[r][2 * p] + (float)acc[r][p].x;
-            fb[r][2 * p + 1] = fb[r][2 * p + 1] + (float)acc[r][p].y;
-            acc[r][p] = (h2){(h16)0.0f, (h16)0.0f};
-          }
+            for (int p = 0; p < 4; p++) {
+              fb[r][2 * p] = fb[r][2 * p] + (float)acc[r][p].x;
+              fb[r][2 * p + 1] = fb[r][2 * p + 1] + (float)acc[r][p].y;
+              acc[r][p] = (h2){(h16)0.0f, (h16)0.0f};
+            }
+        }
       }
     }
     if (!nkn) break;
@@ -375,8 +382,9 @@ __global__ __launch_bounds__(256) void k_gemm_f16e(const uint16_t *__restrict__ 
     h2 v[4];
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-      if (nblk > 1) {
-        v[p] = (h2){f2h(fb[r][2 * p] + bias32[2 * p]), f2h(fb[r][2 * p + 1] + bias32[2 * p + 1])};
+      if (MB && nblk > 1) {
+        v[p] = (h2){f2h(fb[MB ? r : 0][MB ? 2 * p : 0] + bias32[2 * p]),
+                    f2h(fb[MB ? r : 0][MB ? 2 * p + 1 : 0] + bias32[2 * p + 1])};
       } else {
         v[p] = acc[r][p] + (h2){hfrom(bias16[2 * p]), hfrom(bias16[2 * p + 1])};
       }
@@ -570,9 +578,15 @@ static int gemm_f16e_run(const uint16_t *A, long long a_ws, int lda, int M, int 
   BNH_REQ(nb * nsplit < (1LL << 31) && rows * np8 < (1LL << 40));
   const dim3 grid((unsigned)(nb * nsplit));
   hipStream_t st = bnh_stream(stream);
+  const bool mb = nblk > 1 && !split;  // a block sums several K blocks
+#define GEMM_F16E_(V_, R_, G_, M_)                                                                                     \
+  hipLaunchKernelGGL((k_gemm_f16e<V_, R_, G_, M_>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk,     \
+                     W->Nt, W->b, W->b16, W->Kp, W->Np, bs, tc, d, gh, gh_ws, part, nsplit)
 #define GEMM_F16E(V_, R_, G_)                                                                                          \
-  hipLaunchKernelGGL((k_gemm_f16e<V_, R_, G_>), grid, dim3(256), 0, st, A, a_ws, lda, M, 1.0 / M, rows, W->wk, W->Nt,  \
-                     W->b, W->b16, W->Kp, W->Np, bs, tc, d, gh, gh_ws, part, nsplit)
+  do {                                                                                                                 \
+    if (mb) GEMM_F16E_(V_, R_, G_, true);                                                                              \
+    else GEMM_F16E_(V_, R_, G_, false);                                                                                \
+  } while (0)
   if (gh) {
     if (vec && e->res && !split) GEMM_F16E(true, true, true);
     else if (vec) GEMM_F16E(true, false, true);
@@ -583,6 +597,7 @@ static int gemm_f16e_run(const uint16_t *A, long long a_ws, int lda, int M, int 
     else GEMM_F16E(false, false, false);
   }
 #undef GEMM_F16E
+#undef GEMM_F16E_
   BNH_HIP(hipGetLastError());
   if (split) {
     const dim3 g2((unsigned)bnh_ceil_div(rows * np8, 256));
