@@ -256,9 +256,11 @@ __global__ __launch_bounds__(256) void k_s8n_quant_v(const float *__restrict__ x
 // reference's epilogue. A wave writing every channel of its rows, one group after the other, hands whole output rows
 // to its L2, where their cache lines complete before they are written back (rows split between blocks leave partial
 // lines, which cost HBM write rate). Blocks split the channel groups only when there are too few rows to fill the
-// chip (gsplit blocks per row block, consecutive after the XCD remap so that they share an L2).
+// chip (gsplit blocks per row block, consecutive after the XCD remap so that they share an L2). Four waves per SIMD
+// at least (112 VGPRs, no spill, where the compiler's own choice took 151 and three): the K loop waits on its
+// fragment loads, and more waves hide that (the Perch-shaped net 11.68 -> 11.60 ms per 256 windows).
 template <bool RES>
-__global__ __launch_bounds__(256) void k_s8n_gemm(const int8_t *__restrict__ q, long long q_ws,
+__global__ __launch_bounds__(256, 4) void k_s8n_gemm(const int8_t *__restrict__ q, long long q_ws,
                                                   const float *__restrict__ sa, long long sa_ws,
                                                   const int32_t *__restrict__ za, long long za_ws, int M, double rM,
                                                   long long rows, const int8_t *__restrict__ wt,
