@@ -1134,7 +1134,7 @@ def v24_parity(vn, pcm, logits, nc, wins, f16_mfma):
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 # HBM bytes per launch of the replayed fp16 GEMM (72 -> 864 channels, 384 px, 256 windows): FETCH_SIZE x 2 +
 # WRITE_SIZE from rocprofv3 --pmc runs of this bench (profiles/k_gemm_f16e_pw_f16_72to864_24x16_b256.md)
-V24_GEMM_TRAFFIC = 185384640
+V24_GEMM_TRAFFIC = 185333824
 FP16_VALU_PEAK_TFLOPS = 157.3
 
 
