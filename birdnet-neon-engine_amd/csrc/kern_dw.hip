@@ -513,6 +513,9 @@ BNH_DEV h2 h2_bits(uint32_t u) { return __builtin_bit_cast(h2, u); }
 __host__ __device__ constexpr int dw_f16v_np(int k, int s) { return k == 3 && s == 1 ? 8 : 4; }
 // (5 x 5 stride 1: 6 rows, 3.3 input loads per output pair where 4-row bands take 4; the 24 x 64 C = 672 launch of 64
 // windows 0.0914 -> 0.0856 ms; 8 rows the same, 10 and more spill)
+// the DW3 form on channel quads (two pairs a thread): 4-pixel strips at either stride (3x3 s1 with 8-pixel strips held
+// 141 VGPRs and 3 waves per SIMD, with 4 it holds 95 and 5: the v2.4-shaped net 3.815 -> 3.764 ms on one stream)
+__host__ __device__ constexpr int dw3_f16v_np(int s) { return 4; }
 __host__ __device__ constexpr int dw_f16v_rows(int k, int s) { return k == 5 && s == 1 ? 6 : s == 1 ? 4 : 2; }
 
 template <int K, int S, int FORM, int NP, int R, int CP, bool ALL>
@@ -1627,9 +1630,9 @@ int bnh_dw3_f16(const uint16_t *xp, long long x_ws, int H, int W, int C, int s, 
     const unsigned x_len = (unsigned)(2 * ((long long)(B - 1) * x_ws + (long long)(H + 2) * (W + 2) * C));
     const unsigned o_len = (unsigned)(2 * ((long long)(B - 1) * o_ws + (long long)Ho * Wo * C));
     const int R = dw_f16v_rows(3, s);
-    if (dw_grid(Wo, dw_f16v_np(3, s), C / 4, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
+    if (dw_grid(Wo, dw3_f16v_np(s), C / 4, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
     auto launch = [&]<int S>() {
-      constexpr int NP = dw_f16v_np(3, S), RR = dw_f16v_rows(3, S);
+      constexpr int NP = dw3_f16v_np(S), RR = dw_f16v_rows(3, S);
       hipLaunchKernelGGL((k_dw_f16v<3, S, 2, NP, RR, 2>), dim3(nb), dim3(256), 0, st, (const h16 *)xp, x_ws, x_len, W + 2, C,
                          pt, pl, (const h16 *)w, (const h16 *)b, 1, (h16 *)out, o_ws, o_len, Ho, Wo, total, g);
     };
