@@ -47,12 +47,18 @@ __device__ __forceinline__ void fe_cmul(float br, float bi, float wr, float wi, 
   ti = __builtin_fmaf(bi, wr, br * wi);
 }
 
-// grid (ceil(nfr / FPB), B); dynamic LDS: re, im [FPB][M] and mag [FPB][bins]
+// grid (ceil(nfr / FPB), B); dynamic LDS: re, im [FPB][M], mag [FPB][bins] and the twiddles (cos, sin [M / 2]: read
+// by every frame and pass, staged once per block)
 __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, long long p_ws, float *__restrict__ spec,
                                                 long long s_ws, bnh_logmel F) {
   extern __shared__ float lds[];
   const int M = F.M, bins = M + 1, tid = threadIdx.x;
   float *re = lds, *im = lds + FE_FPB * M, *mag = lds + 2 * FE_FPB * M;
+  float *twr = mag + FE_FPB * bins, *twi = twr + M / 2;
+  for (int i = tid; i < M / 2; i += 256) {
+    twr[i] = F.twr[i];
+    twi[i] = F.twi[i];
+  }
   const int t0 = blockIdx.x * FE_FPB, win = blockIdx.y;
   const float *x = pcm + win * p_ws;
   const int nz = (F.frame + 1) / 2;
@@ -92,7 +98,7 @@ __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, l
     const int h = len / 2, st1 = M / len, st2 = M / (2 * len);
     for (int it = tid; it < FE_FPB * (M / 4); it += 256) {
       const int f = it >> (lg - 2), g = it & (M / 4 - 1), j = g & (h - 1), i = (g >> (lgl - 1)) << (lgl + 1);
-      const float w1r = F.twr[j * st1], w1i = F.twi[j * st1], w2r = F.twr[j * st2], w2i = F.twi[j * st2];
+      const float w1r = twr[j * st1], w1i = twi[j * st1], w2r = twr[j * st2], w2i = twi[j * st2];
       float *pr = re + f * M + i + j, *pi = im + f * M + i + j;
       const float ar = pr[0], ai = pi[0], br = pr[h], bi = pi[h], cr = pr[2 * h], ci = pi[2 * h], dr = pr[3 * h],
                   di = pi[3 * h];
@@ -115,7 +121,7 @@ __global__ __launch_bounds__(256) void k_logmel(const float *__restrict__ pcm, l
     const int half = len / 2, step = M / len;
     for (int it = tid; it < FE_FPB * (M / 2); it += 256) {
       const int f = it >> (lg - 1), g = it & (M / 2 - 1), j = g & (half - 1), i = (g >> (lgl - 1)) << lgl;
-      const float wr = F.twr[j * step], wi = F.twi[j * step];
+      const float wr = twr[j * step], wi = twi[j * step];
       float *pr = re + f * M + i + j, *pi = im + f * M + i + j;
       float vr, vi;
       fe_cmul(pr[half], pi[half], wr, wi, vr, vi);
@@ -238,8 +244,8 @@ int bnh_logmel_run(const bnh_logmel *F, const float *pcm, long long p_ws, float 
                void *stream) {
   BNH_REQ(F && pcm && spec && B > 0);
   BNH_REQ(B == 1 || (p_ws >= F->nsamp && s_ws >= (long long)F->nfr * F->nmel));
-  const size_t lds = sizeof(float) * FE_FPB * (2 * (size_t)F->M + F->M + 1);
-  BNH_REQ(lds <= 64 * 1024);  // nfft <= 2048: at most 49 KB
+  const size_t lds = sizeof(float) * (FE_FPB * (2 * (size_t)F->M + F->M + 1) + F->M);
+  BNH_REQ(lds <= 64 * 1024);  // nfft <= 2048: at most 53 KB
   hipLaunchKernelGGL(k_logmel, dim3((unsigned)bnh_ceil_div(F->nfr, FE_FPB), (unsigned)B), dim3(256), lds,
                      bnh_stream(stream), pcm, p_ws, spec, s_ws, *F);
   BNH_HIP(hipGetLastError());
