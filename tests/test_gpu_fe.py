@@ -320,8 +320,10 @@ def test_mean_f16_and_gemv(hip):
     m = do.numpy()[:, :C]
     for i in range(B):
         assert same_bits(m[i], O.mean_f16(x[i], C))
-    # GEMV, fp16 and fp32 weights, K with 8-lane, 4-lane and scalar remainders, ReLU
-    for K, N, w16, act in ((1024, 6522, 1, 0), (1027, 300, 1, 2), (1536, 1000, 0, 0), (13, 33, 0, 2), (6, 17, 1, 0)):
+    # GEMV, fp16 and fp32 weights, K with 8-lane, 4-lane and scalar remainders, ReLU; 8, 4 and 2 windows a block (K up
+    # to 2048, 4096 and 8192: their inputs fill at most 64 KB of LDS)
+    for K, N, w16, act in ((1024, 6522, 1, 0), (1027, 300, 1, 2), (1536, 1000, 0, 0), (13, 33, 0, 2), (6, 17, 1, 0),
+                           (3001, 70, 1, 0), (5003, 40, 0, 2)):
         w = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16 if w16 else np.float32)
         b = (rng.standard_normal(N) * 0.1).astype(np.float32)
         xv = rng.standard_normal((B, K)).astype(np.float32)
@@ -337,3 +339,16 @@ def test_mean_f16_and_gemv(hip):
         assert (y[:, N:] == 9.0).all()
         for i in range(B):
             assert same_bits(y[i, :N], O.gemv(w, b, xv[i], act)), (K, N, w16, i)
+    # 20 windows: two full groups of 8 and a partial one
+    K, N, B2 = 1024, 500, 20
+    w = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    xv = rng.standard_normal((B2, K)).astype(np.float32)
+    dxv, dwt, dbt = H.DeviceArray.from_host(xv), H.DeviceArray.from_host(w), H.DeviceArray.from_host(b)
+    dy = H.DeviceArray.from_host(np.zeros((B2, N), np.float32))
+    say("gemv 20 windows")
+    H.check(H.lib().bnh_gemv(dwt.ptr, 1, dbt.ptr, N, K, dxv.ptr, K, 0, dy.ptr, N, B2, None), "gemv")
+    H.sync()
+    y = dy.numpy()
+    for i in (0, 15, 16, 19):
+        assert same_bits(y[i], O.gemv(w, b, xv[i], 0)), i
