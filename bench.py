@@ -934,7 +934,8 @@ def compact_leg(line):
 def config_legs(a, H, rng, stream):
     """The other configurations, each timed on its own, with its roofline fraction and its parity windows against
     the oracle: config 1 (the depthwise convs at 5x5 stride 1, fp16 and int8, batch 64), config 2 (the fp16
-    Winograd conv, batch 64), config 3 (the v2.4-shaped fp16 net, batch 256)."""
+    Winograd conv, batch 64), config 3 (the v2.4-shaped fp16 net, batch 256: its exact fp16 path, and its fp16
+    1x1 convs on fp16 MFMA within the stated tolerance)."""
     legs = {}
     # each leg follows host work (input generation, the previous leg's oracle check) during which the GPU's clocks
     # fall; a few hundred untimed launches (~30 ms of load) bring them back up before the timed ones
@@ -948,6 +949,14 @@ def config_legs(a, H, rng, stream):
     b = argparse.Namespace(**vars(a))
     b.workload, b.no_cpu, b.steps, b.warmup = "v24_f16", True, max(20, a.steps), 10
     legs["config3_v24_f16"] = compact_leg(run_v24(b, H, rng, 256, stream, emit=False))
+    # the same net with its fp16 1x1 convs on fp16 MFMA (fp32 accumulation): within the configuration's stated
+    # fp16 tolerance against the exact path, not bit-identical; priced against the fp16 MFMA peak
+    b = argparse.Namespace(**vars(a))
+    b.workload, b.no_cpu, b.steps, b.warmup, b.f16_mfma = "v24_f16", True, max(20, a.steps), 10, True
+    try:
+        legs["config3_v24_f16_mfma"] = compact_leg(run_v24(b, H, rng, 256, stream, emit=False))
+    finally:
+        os.environ.pop("BNH_F16_MFMA", None)   # read by bnn_init: the exact path for any later context
     return legs
 
 
