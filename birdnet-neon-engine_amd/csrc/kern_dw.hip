@@ -164,13 +164,20 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
     const int ix0 = FORM == 2 ? item.px * S : item.px * S - pl + H;
     const float *x0 = xw + (long long)ix0 * C;
     // the item's whole input window first (columns past its last pixel's taps stay unread), so that its loads are
-    // in flight together
+    // in flight together; a 4-pixel item (all but a row's last) reads all NC columns without a guard per load
     const int ncol = (item.n - 1) * S + K;
     float xv[K][NC];
+    if (item.n == 4) {
 #pragma unroll
-    for (int ky = 0; ky < K; ky++)
+      for (int ky = 0; ky < K; ky++)
 #pragma unroll
-      for (int kx = 0; kx < NC; kx++) xv[ky][kx] = kx < ncol ? x0[ky * rs + (long long)kx * C] : 0.f;
+        for (int kx = 0; kx < NC; kx++) xv[ky][kx] = x0[ky * rs + (long long)kx * C];
+    } else {
+#pragma unroll
+      for (int ky = 0; ky < K; ky++)
+#pragma unroll
+        for (int kx = 0; kx < NC; kx++) xv[ky][kx] = kx < ncol ? x0[ky * rs + (long long)kx * C] : 0.f;
+    }
     float v[4];
     dw_chains_f32<K, S, FORM>(xv, wv, bias, item.split, v);
     if (FORM == 2 || act == 1) {
@@ -335,14 +342,16 @@ __global__ __launch_bounds__(256) void k_pwdw_f32(const int8_t *__restrict__ q, 
     for (int pos = threadIdx.x / CG; pos < npos; pos += 256 / CG) {
       const int it = (int)(((float)pos + 0.5f) * rth), row = pos - it * THb;
       const Item item = item_of(it, Wo, FORM);
-      const int ncol = (item.n - 1) * S + K;
       const float *x0 = xs + row * S * RS + item.px * S * PS + c;
       float pa[4], pe[4], pd[4], v[4];
 #pragma unroll
       for (int ky = 0; ky < K; ky++) {  // one input row at a time
+        // all NC columns, unguarded: those past the item's (item.n - 1) S + K feed only its outputs q >= item.n, which
+        // are dropped, and read at most 3 S cells past the row's WL, within the allocation (the next row, or the
+        // discard cells and per-pixel arrays after the last row: 60 S - 5 floats past RIN RS at most, < 64 + 12 + 16)
         float xr_[NC];
 #pragma unroll
-        for (int kx = 0; kx < NC; kx++) xr_[kx] = kx < ncol ? x0[ky * RS + kx * PS] : 0.f;
+        for (int kx = 0; kx < NC; kx++) xr_[kx] = x0[ky * RS + kx * PS];
         dw_row_f32<K, S, FORM>(ky, xr_, wv, bias, item.split, pa, pe, pd);
       }
       dw_finish_f32<K, S, FORM>(item.split, pa, pe, pd, v);
