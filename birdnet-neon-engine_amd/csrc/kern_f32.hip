@@ -173,11 +173,20 @@ __global__ __launch_bounds__(256) void k_se_fc1(const float *__restrict__ chsum,
     float a[WB];
 #pragma unroll
     for (int wg = 0; wg < WB; wg++) a[wg] = 0.f;
-#pragma unroll 4
-    for (int c = l; c < C8; c += 8) {
-      const float wv = w[c];
+    // sixteen of the chain's weights loaded at once, then their FMAs in order (one memory round trip per sixteen
+    // steps of the chain, not per step)
+    for (int cb = l; cb < C8; cb += 8 * 16) {
+      float wv[16];
 #pragma unroll
-      for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv, mean[wg * C + c], a[wg]);
+      for (int u = 0; u < 16; u++) wv[u] = cb + 8 * u < C8 ? w[cb + 8 * u] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 16; u++) {
+        const int c = cb + 8 * u;
+        if (c < C8) {
+#pragma unroll
+          for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv[u], mean[wg * C + c], a[wg]);
+        }
+      }
     }
     if (l < 4 && C8 + l < C) {
       const float wv = w[C8 + l];
@@ -214,11 +223,16 @@ __global__ __launch_bounds__(256) void k_se_fc2(const float *__restrict__ s1, in
   const float b = b2[c];
 #pragma unroll
   for (int wg = 0; wg < WB; wg++) a[wg] = b;
-#pragma unroll 4
-  for (int r = 0; r < rd; r++) {
-    const float wv = w2t[(long long)r * C + c];
+  for (int rb = 0; rb < rd; rb += 16) {  // sixteen rows' weights loaded at once, then their FMAs in order
+    float wv[16];
 #pragma unroll
-    for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv, ss[wg * rd + r], a[wg]);
+    for (int u = 0; u < 16; u++) wv[u] = rb + u < rd ? w2t[(long long)(rb + u) * C + c] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 16; u++)
+      if (rb + u < rd) {
+#pragma unroll
+        for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv[u], ss[wg * rd + rb + u], a[wg]);
+      }
   }
 #pragma unroll
   for (int wg = 0; wg < WB; wg++)
