@@ -191,6 +191,80 @@ __global__ __launch_bounds__(256) void k_dw_f32(const float *__restrict__ xp, lo
   }
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// fp32 DW3 (halo-1 input, SiLU) on bands of R output rows: a thread owns a channel pair (8-byte loads) of a strip of
+// 4 output pixels in a band of up to R rows. It loads each input row of the band's strip once and keeps the rows in
+// registers while the band's output rows that share them are computed (k_dw_f32 loads the three input rows of every
+// output row), and runs every output's chains through dw_row_f32, in its order. Loads are range-checked buffer loads
+// on the haloed input: a strip past the row's end reads the next row (or, past the batch's last row, the buffer's
+// out-of-range zeros) and stores nothing there; rows past a short last band are read and dropped.
+template <int S, int R>
+__global__ __launch_bounds__(256) void k_dw3_f32v(const float *__restrict__ xp, long long x_ws, unsigned x_len, int Wp,
+                                                  int C, const float *__restrict__ w, const float *__restrict__ b,
+                                                  float *__restrict__ out, long long o_ws, unsigned o_len, int Ho,
+                                                  int Wo, long long total, DwGrid g) {
+  __shared__ uint32_t tbl[256];
+  bnh_silu_table(tbl);
+  __syncthreads();
+  const int nband = (Ho + R - 1) / R;
+  const DwPos ps = dw_pos(C / 2, nband, total, g);
+  if (!ps.ok) return;
+  constexpr int NC = 3 * S + 3, NIN = (R - 1) * S + 3;  // input columns of the 4-pixel strip, input rows of a band
+  const int c = 2 * ps.c, oy0 = ps.oy * R, px0 = ps.it0, nrows = Ho - oy0 < R ? Ho - oy0 : R;
+  float wv[2][9], bias[2];
+#pragma unroll
+  for (int t = 0; t < 9; t++) {
+    const float2 v = *(const float2 *)(w + (long long)t * C + c);
+    wv[0][t] = v.x;
+    wv[1][t] = v.y;
+  }
+  {
+    const float2 v = *(const float2 *)(b + c);
+    bias[0] = v.x;
+    bias[1] = v.y;
+  }
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *)xp, 0, (int)x_len, 0x00020000);
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc((void *)out, 0, (int)o_len, 0x00020000);
+  // input row oy S + ky, column px S + kx of the halo-1 input (k_dw_f32's form 2)
+  const int xo = 4 * ((int)(ps.win * x_ws) + (oy0 * S * Wp + px0 * S) * C + c);
+  const int oo = 4 * ((int)(ps.win * o_ws) + (oy0 * Wo + px0) * C + c);
+  const int rstep = 4 * Wp * C, cstep = 4 * C;
+  float xin[NIN][NC][2];
+#pragma unroll
+  for (int i = 0; i < NIN; i++)
+#pragma unroll
+    for (int col = 0; col < NC; col++) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(xr, xo + i * rstep + col * cstep, 0, 0);
+      xin[i][col][0] = bnh_float(v[0]);  // by value (a bit cast of an ext_vector element reads element 0)
+      xin[i][col][1] = bnh_float(v[1]);
+    }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    if (r >= nrows) break;
+    float v[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      float pa[4], pe[4], pd[4];
+#pragma unroll
+      for (int ky = 0; ky < 3; ky++) {
+        float row[NC];
+#pragma unroll
+        for (int col = 0; col < NC; col++) row[col] = xin[r * S + ky][col][j];
+        dw_row_f32<3, S, 2>(ky, row, wv[j], bias[j], false, pa, pe, pd);
+      }
+      dw_finish_f32<3, S, 2>(false, pa, pe, pd, v[j]);
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[j][q] = bnh_silu_f32_t(v[j][q], tbl);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      if (px0 + q >= Wo) break;
+      const u32x2 st = {__builtin_bit_cast(uint32_t, v[0][q]), __builtin_bit_cast(uint32_t, v[1][q])};
+      __builtin_amdgcn_raw_buffer_store_b64(st, orr, oo + r * 4 * Wo * C, q * cstep, 0);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ PW_S8 expansion fused into the fp32 depthwise
 // An int8 1x1 expansion (PW_S8: the int8 GEMM over rows that are already quantized, its fp32 dequant epilogue and
 // activation, src/gemm_s8n.c:105-135) whose output only this depthwise conv reads. A block recomputes the expanded
@@ -1509,7 +1583,17 @@ int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, con
   DwGrid g;
   if (dw_grid(nit, dw_ni(3), C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
-  if (s == 1)
+  // stride 1 on channel pairs (8-byte aligned, 32-bit buffer offsets): bands of 4 output rows
+  const long long x_len = 4 * ((long long)(B - 1) * x_ws + (long long)(H + 2) * (W + 2) * C);
+  const long long o_len = 4 * ((long long)(B - 1) * o_ws + (long long)Ho * Wo * C);
+  if (s == 1 && C % 2 == 0 && ((uintptr_t)xp & 7) == 0 && ((uintptr_t)w & 7) == 0 && ((uintptr_t)b & 7) == 0 &&
+      ((uintptr_t)out & 7) == 0 && (B == 1 || (x_ws % 2 == 0 && o_ws % 2 == 0)) &&
+      x_len + 4LL * 6 * (W + 2) * C < (1LL << 31) && o_len + 4LL * 4 * Wo * C < (1LL << 31)) {
+    constexpr int R = 4;
+    if (dw_grid(Wo, 4, C / 2, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
+    hipLaunchKernelGGL((k_dw3_f32v<1, R>), dim3(nb), dim3(256), 0, st, xp, x_ws, (unsigned)x_len, W + 2, C, w, b, out,
+                       o_ws, (unsigned)o_len, Ho, Wo, total, g);
+  } else if (s == 1)
     hipLaunchKernelGGL((k_dw_f32<3, 1, 2>), dim3(nb), dim3(256), 0, st, xp, x_ws, W + 2, C, 1, 1, w, b, 1, out, o_ws,
                        Ho, Wo, nit, total, g);
   else

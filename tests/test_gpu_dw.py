@@ -149,7 +149,9 @@ def test_dwk_k7_and_odd_channels(hip, dtype):
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
 @pytest.mark.parametrize("s", [1, 2])
 def test_dw3(hip, dtype, s):
-    for H, W, C in ((24, 64, 144), (5, 7, 24), (6, 2, 8), (7, 9, 18)):
+    # 249 x 63 x 40: the Perch-shaped net's first block; C = 5: odd channel counts (single channels); heights 24, 5,
+    # 6, 7: every band tail of the 4-row fp32 stride-1 kernel
+    for H, W, C in ((24, 64, 144), (5, 7, 24), (6, 2, 8), (7, 9, 18), (249, 63, 40), (4, 6, 5)):
         _, pt = same_pads(H, 3, s)
         _, pl = same_pads(W, 3, s)
         check_case(hip, "dw3", dtype, 2, H, W, C, 3, s, pt, pl, 1, seed=H + W + s)
