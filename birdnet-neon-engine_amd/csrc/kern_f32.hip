@@ -49,7 +49,10 @@ __global__ void k_zero_halo(T *__restrict__ out, long long ws, int H, int W, int
 // weight panels and the bias are copied into LDS once per block (dynamic LDS, Np Kp + Np floats): every thread reads
 // Kp 16-byte weight rows, the same for every pixel, which through the vector memory path bound the kernel on its
 // address units.
-template <int KK, bool H16, bool VEC>
+// NPX > 1 (3 x 3 taps): a thread owns 4 output channels of NPX pixels m, m + MQ, ... (MQ = ceil(Ho Wo / NPX)),
+// with the channels' 12 weight rows read from LDS into registers once (not once per pixel) and the block's set-up
+// (the SiLU table, the panels in LDS) spread over NPX times the pixels.
+template <int KK, bool H16, bool VEC, int NPX>
 __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img, long long i_ws, int W, int k, int s,
                                                   int Ho, int Wo, const float *__restrict__ w,
                                                   const float *__restrict__ bias, int Kp, int Np, int act,
@@ -60,55 +63,66 @@ __global__ __launch_bounds__(256) void k_stem_f32(const float *__restrict__ img,
   for (int i = threadIdx.x; i < Np * Kp / 4; i += blockDim.x) ((float4 *)s_wb)[i] = ((const float4 *)w)[i];
   for (int i = threadIdx.x; i < Np; i += blockDim.x) s_wb[Np * Kp + i] = bias[i];
   __syncthreads();
-  const int ng = Np / 4;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x, per = Ho * Wo * ng;
+  const int ng = Np / 4, npx = Ho * Wo, MQ = (npx + NPX - 1) / NPX;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
   const long long win = blockIdx.y;
-  if (i >= per) return;
-  const int m = i / ng, g = i - m * ng, oy = m / Wo, ox = m - oy * Wo, n0 = 4 * g;
-  const float *x = img + win * i_ws + (oy * s) * W + ox * s;
+  if (i >= MQ * ng) return;
+  const int mq = i / ng, g = i - mq * ng, n0 = 4 * g;
   const float *wp = s_wb + (n0 / 8) * Kp * 8 + n0 % 8;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  auto tap = [&](int q, float a) {
-    const float4 wv = *(const float4 *)(wp + q * 8);
-    acc[0] = __builtin_fmaf(wv.x, a, acc[0]);
-    acc[1] = __builtin_fmaf(wv.y, a, acc[1]);
-    acc[2] = __builtin_fmaf(wv.z, a, acc[2]);
-    acc[3] = __builtin_fmaf(wv.w, a, acc[3]);
-  };
-  if constexpr (KK > 0) {
-    constexpr int KP = (KK * KK + 3) / 4 * 4;
-    float a[KP];
+  constexpr int KP = KK > 0 ? (KK * KK + 3) / 4 * 4 : 1;
+  float4 wr[NPX > 1 ? KP : 1];
+  if constexpr (NPX > 1) {
 #pragma unroll
-    for (int q = 0; q < KP; q++) a[q] = q < KK * KK ? x[(q / KK) * W + q % KK] : 0.f;
-#pragma unroll
-    for (int q = 0; q < KP; q++) tap(q, a[q]);
-  } else {
-    for (int q = 0; q < Kp; q++) tap(q, q < k * k ? x[(q / k) * W + q % k] : 0.f);
+    for (int q = 0; q < KP; q++) wr[q] = *(const float4 *)(wp + q * 8);
   }
-  float y[4];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    y[j] = acc[j] + s_wb[Np * Kp + n0 + j];
-    if (act == 1) y[j] = bnh_silu_f32_t(y[j], tbl);
-    else if (act == 2) y[j] = bnh_relu_f32(y[j]);
-  }
-  const long long orow = opad ? (long long)(oy + opad) * (Wo + 2 * opad) + ox + opad : m;
-  if (H16) {
-    uint16_t *o = (uint16_t *)outv + win * o_ws + orow * ldo + n0;
-    if (VEC && n0 + 4 <= N) {
-      *(uint2 *)o = make_uint2((uint32_t)hbits(f2h(y[0])) | ((uint32_t)hbits(f2h(y[1])) << 16),
-                               (uint32_t)hbits(f2h(y[2])) | ((uint32_t)hbits(f2h(y[3])) << 16));
+  for (int j = 0; j < NPX; j++) {
+    const int m = mq + j * MQ;
+    if (m >= npx) break;
+    const int oy = m / Wo, ox = m - oy * Wo;
+    const float *x = img + win * i_ws + (oy * s) * W + ox * s;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    auto tap = [&](int q, float a) {
+      const float4 wv = NPX > 1 ? wr[NPX > 1 ? q : 0] : *(const float4 *)(wp + q * 8);
+      acc[0] = __builtin_fmaf(wv.x, a, acc[0]);
+      acc[1] = __builtin_fmaf(wv.y, a, acc[1]);
+      acc[2] = __builtin_fmaf(wv.z, a, acc[2]);
+      acc[3] = __builtin_fmaf(wv.w, a, acc[3]);
+    };
+    if constexpr (KK > 0) {
+      float a[KP];
+#pragma unroll
+      for (int q = 0; q < KP; q++) a[q] = q < KK * KK ? x[(q / KK) * W + q % KK] : 0.f;
+#pragma unroll
+      for (int q = 0; q < KP; q++) tap(q, a[q]);
     } else {
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        if (n0 + j < N) o[j] = hbits(f2h(y[j]));  // one rounding to nearest even (no fused mix forms)
+      for (int q = 0; q < Kp; q++) tap(q, q < k * k ? x[(q / k) * W + q % k] : 0.f);
     }
-  } else {
-    float *o = (float *)outv + win * o_ws + orow * ldo + n0;
-    if (VEC) {
-      *(float4 *)o = make_float4(y[0], y[1], y[2], y[3]);
+    float y[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      y[u] = acc[u] + s_wb[Np * Kp + n0 + u];
+      if (act == 1) y[u] = bnh_silu_f32_t(y[u], tbl);
+      else if (act == 2) y[u] = bnh_relu_f32(y[u]);
+    }
+    const long long orow = opad ? (long long)(oy + opad) * (Wo + 2 * opad) + ox + opad : m;
+    if (H16) {
+      uint16_t *o = (uint16_t *)outv + win * o_ws + orow * ldo + n0;
+      if (VEC && n0 + 4 <= N) {
+        *(uint2 *)o = make_uint2((uint32_t)hbits(f2h(y[0])) | ((uint32_t)hbits(f2h(y[1])) << 16),
+                                 (uint32_t)hbits(f2h(y[2])) | ((uint32_t)hbits(f2h(y[3])) << 16));
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+          if (n0 + u < N) o[u] = hbits(f2h(y[u]));  // one rounding to nearest even (no fused mix forms)
+      }
     } else {
-      o[0] = y[0]; o[1] = y[1]; o[2] = y[2]; o[3] = y[3];
+      float *o = (float *)outv + win * o_ws + orow * ldo + n0;
+      if (VEC) {
+        *(float4 *)o = make_float4(y[0], y[1], y[2], y[3]);
+      } else {
+        o[0] = y[0]; o[1] = y[1]; o[2] = y[2]; o[3] = y[3];
+      }
     }
   }
 }
@@ -119,12 +133,14 @@ static void stem_launch(dim3 grid, hipStream_t st, bool vec, const float *img, l
                         int Ho, int Wo, const float *w, const float *bias, int Kp, int Np, int act, void *out,
                         long long o_ws, int ldo, int opad, int N) {
   const size_t lds = sizeof(float) * ((size_t)Np * Kp + Np);
-#define STEM_L(KK, V)                                                                                                  \
-  hipLaunchKernelGGL((k_stem_f32<KK, H16, V>), grid, dim3(256), lds, st, img, i_ws, W, k, s, Ho, Wo, w, bias, Kp, Np, \
-                     act, out, o_ws, ldo, opad, N)
-  if (k == 3 && Kp == 12) { if (vec) STEM_L(3, true); else STEM_L(3, false); }
-  else if (k == 5 && Kp == 28) { if (vec) STEM_L(5, true); else STEM_L(5, false); }
-  else { if (vec) STEM_L(0, true); else STEM_L(0, false); }
+  const long long ng = Np / 4, npx = (long long)Ho * Wo;
+  auto g = [&](int npxt) { return dim3((unsigned)bnh_ceil_div(bnh_ceil_div(npx, npxt) * ng, 256), grid.y); };
+#define STEM_L(KK, V, P)                                                                                               \
+  hipLaunchKernelGGL((k_stem_f32<KK, H16, V, P>), g(P), dim3(256), lds, st, img, i_ws, W, k, s, Ho, Wo, w, bias, Kp,  \
+                     Np, act, out, o_ws, ldo, opad, N)
+  if (k == 3 && Kp == 12) { if (vec) STEM_L(3, true, 4); else STEM_L(3, false, 4); }
+  else if (k == 5 && Kp == 28) { if (vec) STEM_L(5, true, 1); else STEM_L(5, false, 1); }
+  else { if (vec) STEM_L(0, true, 1); else STEM_L(0, false, 1); }
 #undef STEM_L
 }
 

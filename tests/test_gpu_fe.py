@@ -126,7 +126,8 @@ def test_logmel_geometries(hip, nsamp, frame, hop, pad, nfft, nmel):
 
 
 @pytest.mark.parametrize("Hh,W,k,s,co,act,opad", [(500, 128, 3, 2, 40, 1, 1), (33, 20, 5, 1, 12, 2, 0),
-                                                   (17, 19, 1, 1, 8, 0, 2), (40, 30, 7, 3, 16, 1, 0)])
+                                                   (17, 19, 1, 1, 8, 0, 2), (40, 30, 7, 3, 16, 1, 0),
+                                                   (33, 20, 3, 1, 24, 1, 0)])
 def test_stem(hip, Hh, W, k, s, co, act, opad):
     H = hip
     rng = np.random.default_rng(Hh + k)
