@@ -966,8 +966,8 @@ def config_legs(a, H, rng, stream):
 # launch. The VALU issue share is computed in the run from the instruction count and this run's launch time: a wave64
 # VALU instruction occupies a 16-lane SIMD for 4 cycles; the chip has 1,024 SIMDs at 2.4 GHz.
 PERCH_PWDW_PROFILE = "profiles/k_pwdw_f32_24to144_dw3s2_249x63_b256.md"
-PERCH_PWDW_TRAFFIC = 774989248
-PERCH_PWDW_VALU_INSTS = 508447744
+PERCH_PWDW_TRAFFIC = 775128064
+PERCH_PWDW_VALU_INSTS = 486559744
 SIMDS, SCLK_HZ = 1024, 2.4e9
 
 
