@@ -189,18 +189,22 @@ __global__ __launch_bounds__(256) void k_se_fc1(const float *__restrict__ chsum,
     float a[WB];
 #pragma unroll
     for (int wg = 0; wg < WB; wg++) a[wg] = 0.f;
-    // sixteen of the chain's weights loaded at once, then their FMAs in order (one memory round trip per sixteen
-    // steps of the chain, not per step)
-    for (int cb = l; cb < C8; cb += 8 * 16) {
-      float wv[16];
+    // 32 of the chain's weights loaded at once, then their FMAs in order (one memory round trip per 32 steps of the
+    // chain, not per step; the launch has few waves, so the registers cost no occupancy that matters)
+    for (int cb = l; cb < C8; cb += 8 * 32) {
+      float wv[32];
 #pragma unroll
-      for (int u = 0; u < 16; u++) wv[u] = cb + 8 * u < C8 ? w[cb + 8 * u] : 0.f;
+      for (int u = 0; u < 32; u++) wv[u] = cb + 8 * u < C8 ? w[cb + 8 * u] : 0.f;
+      float mv[32][WB];  // the means they multiply, read from LDS ahead of the chain too
 #pragma unroll
-      for (int u = 0; u < 16; u++) {
-        const int c = cb + 8 * u;
-        if (c < C8) {
+      for (int u = 0; u < 32; u++)
 #pragma unroll
-          for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv[u], mean[wg * C + c], a[wg]);
+        for (int wg = 0; wg < WB; wg++) mv[u][wg] = cb + 8 * u < C8 ? mean[wg * C + cb + 8 * u] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 32; u++) {
+        if (cb + 8 * u < C8) {
+#pragma unroll
+          for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv[u], mv[u][wg], a[wg]);
         }
       }
     }
@@ -239,12 +243,12 @@ __global__ __launch_bounds__(256) void k_se_fc2(const float *__restrict__ s1, in
   const float b = b2[c];
 #pragma unroll
   for (int wg = 0; wg < WB; wg++) a[wg] = b;
-  for (int rb = 0; rb < rd; rb += 16) {  // sixteen rows' weights loaded at once, then their FMAs in order
-    float wv[16];
+  for (int rb = 0; rb < rd; rb += 32) {  // 32 rows' weights loaded at once, then their FMAs in order
+    float wv[32];
 #pragma unroll
-    for (int u = 0; u < 16; u++) wv[u] = rb + u < rd ? w2t[(long long)(rb + u) * C + c] : 0.f;
+    for (int u = 0; u < 32; u++) wv[u] = rb + u < rd ? w2t[(long long)(rb + u) * C + c] : 0.f;
 #pragma unroll
-    for (int u = 0; u < 16; u++)
+    for (int u = 0; u < 32; u++)
       if (rb + u < rd) {
 #pragma unroll
         for (int wg = 0; wg < WB; wg++) a[wg] = __builtin_fmaf(wv[u], ss[wg * rd + rb + u], a[wg]);
