@@ -1583,13 +1583,13 @@ int bnh_dw3_f32(const float *xp, long long x_ws, int H, int W, int C, int s, con
   DwGrid g;
   if (dw_grid(nit, dw_ni(3), C, Ho, B, &nb, &total, &g)) return -1;
   hipStream_t st = bnh_stream(stream);
-  // stride 1 on channel pairs (8-byte aligned, 32-bit buffer offsets): bands of 4 output rows
+  // stride 1 on channel pairs (8-byte aligned, 32-bit buffer offsets): bands of R output rows
+  constexpr int R = 6;
   const long long x_len = 4 * ((long long)(B - 1) * x_ws + (long long)(H + 2) * (W + 2) * C);
   const long long o_len = 4 * ((long long)(B - 1) * o_ws + (long long)Ho * Wo * C);
   if (s == 1 && C % 2 == 0 && ((uintptr_t)xp & 7) == 0 && ((uintptr_t)w & 7) == 0 && ((uintptr_t)b & 7) == 0 &&
       ((uintptr_t)out & 7) == 0 && (B == 1 || (x_ws % 2 == 0 && o_ws % 2 == 0)) &&
-      x_len + 4LL * 6 * (W + 2) * C < (1LL << 31) && o_len + 4LL * 4 * Wo * C < (1LL << 31)) {
-    constexpr int R = 4;
+      x_len + 4LL * (R + 2) * (W + 2) * C < (1LL << 31) && o_len + 4LL * R * Wo * C < (1LL << 31)) {
     if (dw_grid(Wo, 4, C / 2, (Ho + R - 1) / R, B, &nb, &total, &g)) return -1;
     hipLaunchKernelGGL((k_dw3_f32v<1, R>), dim3(nb), dim3(256), 0, st, xp, x_ws, (unsigned)x_len, W + 2, C, w, b, out,
                        o_ws, (unsigned)o_len, Ho, Wo, total, g);
